@@ -1,0 +1,285 @@
+"""Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce]
+                    [--no-cpu-baseline] [--components]
+
+One step is one launch of the workload's fused kernel on one batch of synthetic
+input already resident in HBM (inputs are generated on the device with a
+seeded generator before the timed region). The timed region is K back-to-back
+steps on the current stream, bracketed by torch.cuda.synchronize() and timed
+with HIP events on that stream; ``value`` is the workload's throughput and
+``roofline`` compares it to MI355X's published peak (fp32 MFMA 157.3 TFLOP/s,
+HBM 8 TB/s). ``cpu_baseline`` times the CPU oracle (the op-for-op restatement
+of the reference's general path) on a bounded sample of the same workload on
+this host. Rank 0 prints one JSON line.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "ms & TFLOP/s per degree-K Taylor attention fwd; GB/s norm/CE; % roofline"
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, dense
+PEAK_FP64_MFMA = 78.6    # TFLOP/s, dense
+PEAK_HBM = 8000.0        # GB/s
+
+
+def _gen(seed, device):
+    import torch
+
+    return torch.Generator(device=device).manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------
+# Workloads: each returns a dict with the step closure and its algorithmic work.
+
+def wl_attention(device, dense_orders=False):
+    """B=4 H=16 L=2048 d=128, K=4, fp32, causal, scale 1/sqrt(128)."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(2, device)
+
+    def series():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        rest = [torch.randn(B * H, L, d, generator=g, device=device) * 0.5 ** k if dense_orders
+                else torch.zeros(B * H, L, d, device=device) for k in range(2, K + 1)]
+        return [base, direction, *rest]
+
+    q, k, v = series(), series(), series()
+    scale = 1 / math.sqrt(d)
+
+    def step():
+        return _ops.taylor_attention_fwd(q, k, v, None, True, scale, K)
+
+    pairs = (K + 1) * (K + 2) // 2
+    flops = 2 * pairs * 2 * d * B * H * L * (L + 1) / 2    # dense-series count, causal
+    nbytes = 4 * (K + 1) * B * H * L * d * 4                 # q, k, v read + out written (fp32)
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_FP32_MFMA,
+                bytes=nbytes, kernel="taylor_attention", dtype="fp32",
+                workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} fp32 causal"
+                         + (" dense orders" if dense_orders else " line inputs (orders 2..4 zero)"),
+                cpu=lambda: cpu_attention(L, d, K))
+
+
+def wl_matmul(device):
+    """A, B [5, 4096, 4096] fp32 (K=4), coefficient k scaled by 0.5^k."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, n = 4, 4096
+    g = _gen(1, device)
+    a = [torch.randn(1, n, n, generator=g, device=device) * 0.5 ** k for k in range(K + 1)]
+    b = [torch.randn(1, n, n, generator=g, device=device) * 0.5 ** k for k in range(K + 1)]
+
+    def step():
+        return _ops.cauchy_matmul(a, b, K, False)
+
+    pairs = (K + 1) * (K + 2) // 2
+    return dict(step=step, work=2 * pairs * n ** 3, unit="TFLOP/s", bound="mfma", peak=PEAK_FP32_MFMA,
+                bytes=3 * (K + 1) * n * n * 4, kernel="cauchy_matmul", dtype="fp32",
+                workload=f"cauchy_matmul [{K + 1},{n},{n}] x [{K + 1},{n},{n}] fp32",
+                cpu=lambda: cpu_matmul(n, K))
+
+
+def wl_norm(device):
+    """BASELINE config 4a: RMSNorm series x [5, 8192, 4096] bf16, eps 1e-6, weight 1+0.02 N(0,1)."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, rows, n = 4, 8192, 4096
+    g = _gen(3, device)
+    x = [(torch.randn(rows, n, generator=g, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    w = (1 + 0.02 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+
+    def step():
+        return _ops.norm_series(x, [w], [], n, 1e-6, False)
+
+    nbytes = 2 * (K + 1) * rows * n * 2 + n * 2
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+                kernel="norm_series", dtype="bf16",
+                workload=f"rms_norm_series [{K + 1},{rows},{n}] bf16 weight eps=1e-6",
+                cpu=lambda: cpu_norm(rows, n, K))
+
+
+def wl_ce(device):
+    """BASELINE config 4b: logits [5, 8192, 32000] fp32, base N(0,2^2), order k N(0,1) 0.5^k, mean."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, rows, classes = 4, 8192, 32000
+    g = _gen(4, device)
+    z = [torch.randn(rows, classes, generator=g, device=device) * (2.0 if k == 0 else 0.5 ** k)
+         for k in range(K + 1)]
+    y = torch.randint(0, classes, (rows,), generator=g, device=device)
+
+    def step():
+        return _ops.cross_entropy_series(z, y, -100, 1)
+
+    nbytes = (K + 1) * rows * classes * 4 + rows * 8 + (K + 1) * rows * 4
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+                kernel="cross_entropy_series", dtype="fp32",
+                workload=f"cross_entropy_series [{K + 1},{rows},{classes}] fp32 mean",
+                cpu=lambda: cpu_ce(rows, classes, K))
+
+
+WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (the reference's general path restated op for op) on a bounded sample.
+
+def _cpu_time(fn, reps=3):
+    fn()   # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_attention(L, d, K):
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(2)
+    q, k, v = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(3))
+    t = _cpu_time(lambda: oracle.attention(q, k, v, is_causal=True), reps=1)
+    flops = 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
+    return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"1 of 64 (b,h) heads, L={L} d={d} K={K} fp32 causal",
+                seconds=t)
+
+
+def cpu_matmul(n, K):
+    import torch
+    import oracle
+
+    rows = n // 8
+    g = torch.Generator().manual_seed(1)
+    a = [torch.randn(rows, n, generator=g) * 0.5 ** k for k in range(K + 1)]
+    b = [torch.randn(n, n, generator=g) * 0.5 ** k for k in range(K + 1)]
+    t = _cpu_time(lambda: oracle.matmul(a, b), reps=1)
+    flops = 2 * ((K + 1) * (K + 2) // 2) * rows * n * n
+    return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"{rows} of {n} rows of A, K={K} fp32", seconds=t)
+
+
+def cpu_norm(rows, n, K):
+    import torch
+    import oracle
+
+    rows = rows // 16
+    g = torch.Generator().manual_seed(3)
+    x = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    w = [(1 + 0.02 * torch.randn(n, generator=g)).to(torch.bfloat16)]
+    t = _cpu_time(lambda: oracle.rms_norm(x, (n,), weight=w, eps=1e-6))
+    nbytes = 2 * (K + 1) * rows * n * 2
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"{rows} of 8192 rows, n={n} K={K} bf16", seconds=t)
+
+
+def cpu_ce(rows, classes, K):
+    import torch
+    import oracle
+
+    rows = rows // 32
+    g = torch.Generator().manual_seed(4)
+    z = [torch.randn(rows, classes, generator=g) * (2.0 if k == 0 else 0.5 ** k) for k in range(K + 1)]
+    y = torch.randint(0, classes, (rows,), generator=g)
+    t = _cpu_time(lambda: oracle.cross_entropy(z, y))
+    nbytes = (K + 1) * rows * classes * 4
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"{rows} of 8192 rows, C={classes} K={K} fp32", seconds=t)
+
+
+# ---------------------------------------------------------------------------
+
+def time_steps(step, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def measure(name, device, steps, warmup):
+    w = WORKLOADS[name](device)
+    ms = time_steps(w["step"], steps, warmup)
+    achieved = w["work"] / (ms * 1e-3) / (1e12 if w["unit"] == "TFLOP/s" else 1e9)
+    w.update(ms=ms, achieved=achieved)
+    return w
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--workload", default="attention", choices=sorted(WORKLOADS))
+    parser.add_argument("--components", action="store_true", help="also time the other three kernels")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the Taylor kernels are single-GPU "
+              "in this build; multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    device = torch.device("cuda:0")
+    w = measure(args.workload, device, args.steps, args.warmup)
+    line = {
+        "metric": METRIC,
+        "value": round(w["achieved"], 3),
+        "unit": w["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(w["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w["dtype"],
+        "data": "synthetic (seeded torch.randn on device)",
+        "config": {"workload": w["workload"], "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": w["bound"], "achieved": round(w["achieved"], 3), "peak": w["peak"],
+                     "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4), "traffic": None},
+    }
+    if args.components:
+        comps = {}
+        for name in sorted(WORKLOADS):
+            if name == args.workload:
+                continue
+            c = measure(name, device, max(3, args.steps // 2), 2)
+            comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "achieved": round(c["achieved"], 3),
+                           "unit": c["unit"], "frac": round(c["achieved"] / c["peak"], 4)}
+            del c
+            torch.cuda.empty_cache()
+        line["components"] = comps
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        cpu = w["cpu"]()
+        line["cpu_baseline"] = {"value": round(cpu["value"], 6), "unit": cpu["unit"], "cores": torch.get_num_threads(),
+                                "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,182 @@
+/*
+ * polytaylor.h — C ABI of the MI355X (gfx950) truncated-Taylor kernels.
+ *
+ * A degree-K series tensor is passed the way the reference stores it: as K+1
+ * coefficient buffers, one device pointer per order (the reference keeps a
+ * tuple of K+1 tensors, /root/reference/src/polytensors/_tensor.py:147).
+ * Every pointer array is a HOST array of device pointers; each coefficient
+ * buffer is dense row-major with the shape stated per entry point. An
+ * operand given with fewer orders (`*_orders` < K+1) has zero higher orders:
+ * a plain tensor is passed with one order, as the reference's lift pads it
+ * with zeros (/root/reference/src/polytensors/_range_ops.py:37-45).
+ *
+ * dtype codes: PT_FLOAT32, PT_FLOAT64, PT_BFLOAT16, PT_FLOAT16. Arithmetic is
+ * float32 for the 32/16-bit types and float64 for PT_FLOAT64.
+ *
+ * All entry points are asynchronous on `stream` (a hipStream_t; NULL is the
+ * null stream), allocate nothing, never synchronise the host, and return a
+ * pt_status. On failure pt_last_error() gives a message (thread-local).
+ * Outputs never alias inputs.
+ */
+#ifndef POLYTAYLOR_H
+#define POLYTAYLOR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PT_ABI_VERSION 1
+#define PT_MAX_DEGREE 8
+
+typedef enum pt_dtype {
+  PT_FLOAT32 = 0,
+  PT_FLOAT64 = 1,
+  PT_BFLOAT16 = 2,
+  PT_FLOAT16 = 3
+} pt_dtype;
+
+typedef enum pt_status {
+  PT_OK = 0,
+  PT_INVALID_ARGUMENT = 1, /* shapes, pointers or sizes inconsistent */
+  PT_UNSUPPORTED = 2,      /* valid call outside what the kernels implement */
+  PT_DEVICE_ERROR = 3      /* the HIP runtime reported an error */
+} pt_status;
+
+typedef enum pt_reduction {
+  PT_REDUCTION_NONE = 0,
+  PT_REDUCTION_MEAN = 1,
+  PT_REDUCTION_SUM = 2
+} pt_reduction;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pt_last_error(void);
+
+/* PT_ABI_VERSION of the built library. */
+int pt_abi_version(void);
+
+/* Largest supported degree K (PT_MAX_DEGREE). */
+int pt_max_degree(void);
+
+/*
+ * RMSNorm of a degree-K series over the last `n` elements of each of `rows`
+ * rows:  y(t) = x(t) * rsqrt(mean(x(t)^2) + eps) [* w(t)].
+ * x, y: K+1 pointers, each [rows, n] of `dtype`.
+ * weight: NULL, or `weight_orders` pointers (1 = plain weight, K+1 = series),
+ *         each [n] of `dtype`.
+ * Replaces the fused degree-1 RMSNorm of the reference
+ *   /root/reference/src/polytensors/_fused_norm.py:24-40 (_run) and
+ *   /root/reference/src/polytensors/_norm_kernels.py:7-19 (_forward),
+ * generalised to degree K with the series of the reference's general rule
+ *   /root/reference/src/polytensors/_decompositions.py:14-22 (_rms_norm) and
+ *   /root/reference/src/polytensors/_series.py:83-96 (poly_rsqrt);
+ * the weight multiply is the reference's separate `result * weight`
+ *   (/root/reference/src/polytensors/_fused_norm.py:69), fused here.
+ */
+int pt_rms_norm_series_fwd(int dtype, int degree, const void* const* x,
+                           const void* const* weight, int weight_orders,
+                           void* const* y, int64_t rows, int64_t n, double eps,
+                           void* stream);
+
+/*
+ * LayerNorm of a degree-K series over the last `n` elements of each row:
+ *   c(t) = x(t) - mean(x(t)),
+ *   y(t) = c(t) * rsqrt(mean(c(t)^2) + eps) [* w(t)] [+ b(t)].
+ * Shapes as pt_rms_norm_series_fwd; bias like weight.
+ * The reference has no layer-norm rule (native layer norm is listed as
+ * missing, /root/reference/docs/notes.md:33-35); this is the series of the
+ * composite built from its mean/mul/rsqrt rules
+ *   (/root/reference/src/polytensors/_range_ops.py:133-149,178-193,
+ *    /root/reference/src/polytensors/_series.py:83-96).
+ */
+int pt_layer_norm_series_fwd(int dtype, int degree, const void* const* x,
+                             const void* const* weight, int weight_orders,
+                             const void* const* bias, int bias_orders,
+                             void* const* y, int64_t rows, int64_t n,
+                             double eps, void* stream);
+
+/*
+ * Cross entropy of a degree-K series of logits z(t) with integer targets.
+ * logits: K+1 pointers, each `rows` rows of `classes` values, row i at
+ *         element offset i * row_stride (row_stride >= classes).
+ * target: [rows] int64 device array; rows whose target == ignore_index get
+ *         zero loss and are excluded from the mean's count.
+ * reduction PT_REDUCTION_NONE: loss = K+1 pointers, each [rows] of the
+ *           arithmetic type (float32, or float64 for PT_FLOAT64).
+ *           PT_REDUCTION_MEAN / _SUM: loss = K+1 pointers, each one scalar of
+ *           the arithmetic type; `workspace` must hold
+ *           pt_cross_entropy_series_workspace_size(...) bytes (else unused).
+ * lse: NULL, or K+1 pointers, each [rows] of the arithmetic type (float32, or
+ *      float64 for PT_FLOAT64): the log-sum-exp series of each row.
+ * loss_0 = lse_0 - z_0[y]; loss_k = lse_k - z_k[y] for k >= 1.
+ * Replaces the fused degree-1 forward of the reference
+ *   /root/reference/src/polytensors/_fused_cross_entropy.py:161-170 (forward),
+ *   /root/reference/src/polytensors/_cross_entropy_kernels.py:20-55 (_forward)
+ * and its reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:257-277),
+ * generalised to degree K with the log-softmax series of the general rule
+ *   /root/reference/src/polytensors/_plain.py:262-273 (plain_softmax_family)
+ *   and per-order NLL /root/reference/src/polytensors/_dispatch.py:537-543.
+ */
+int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits,
+                                int64_t rows, int64_t classes, int64_t row_stride,
+                                const int64_t* target, int64_t ignore_index,
+                                int reduction, void* const* loss,
+                                void* const* lse, void* workspace, void* stream);
+
+/* Bytes of device workspace pt_cross_entropy_series_fwd needs for a
+ * reduction (0 for PT_REDUCTION_NONE). */
+size_t pt_cross_entropy_series_workspace_size(int dtype, int degree,
+                                              int64_t rows, int reduction);
+
+/*
+ * Cauchy-product (truncated series) matrix product
+ *   C_k = sum_{i+j=k} A_i @ B_j,   k = 0..K,
+ * the i-sum in increasing i as the reference's plain_polynomial_product
+ *   (/root/reference/src/polytensors/_plain.py:118-128), reached from the
+ *   mm/bmm/matmul/linear rules (/root/reference/src/polytensors/_range_ops.py:78-84,160-176).
+ * a: a_orders pointers (1 or K+1), each [batch, m, k] (batch stride
+ *    a_batch_stride elements; 0 broadcasts one matrix over the batch).
+ * b: b_orders pointers (1 or K+1), each [batch, k, n], or [batch, n, k] if
+ *    trans_b (then B_j is used transposed), batch stride b_batch_stride.
+ * c: K+1 pointers, each [batch, m, n] contiguous.
+ * dtype: PT_FLOAT32 (fp32 MFMA) or PT_FLOAT64 (fp64 MFMA).
+ */
+int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
+                     const void* const* b, int b_orders, void* const* c,
+                     int64_t batch, int64_t m, int64_t n, int64_t k,
+                     int64_t a_batch_stride, int64_t b_batch_stride,
+                     int trans_b, void* stream);
+
+/*
+ * Flash-style attention forward of degree-K series:
+ *   S(t) = scale * Q(t) K(t)^T (masked), P(t) = softmax(S(t)), O(t) = P(t) V(t).
+ * q: q_orders pointers (1 or K+1), each [bh, lq, d];
+ * k, v: k_orders / v_orders pointers, each [bh, lk, d];
+ * out: K+1 pointers, each [bh, lq, d] of `dtype`.
+ * lse: NULL, or K+1 pointers, each [bh, lq] of the arithmetic type: the
+ *      log-sum-exp series of each score row (+inf, 0, ... for a row with no
+ *      admissible key, whose output is zero, as the reference's fused kernel
+ *      /root/reference/src/polytensors/_attention_kernels.py:70-76).
+ * causal: key j admissible for query i iff j <= i.
+ * mask: NULL, or [lq, lk] uint8 (nonzero = admissible); not with causal.
+ * Replaces the degree-1 fused forward
+ *   /root/reference/src/polytensors/_fused_attention.py:126-141 (forward),
+ *   /root/reference/src/polytensors/_attention_kernels.py:27-82 (_forward),
+ * generalised to degree K; the series follow the general decomposition
+ *   /root/reference/src/polytensors/_decompositions.py:28-43 (_attention).
+ * dtype: PT_FLOAT32 or PT_FLOAT64.
+ */
+int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
+                            int q_orders, const void* const* k, int k_orders,
+                            const void* const* v, int v_orders,
+                            void* const* out, void* const* lse, int64_t bh,
+                            int64_t lq, int64_t lk, int64_t d, int causal,
+                            const uint8_t* mask, double scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POLYTAYLOR_H */

@@ -1,0 +1,123 @@
+"""The four hot-path operations of the oracle (test infrastructure only; see oracle/__init__.py).
+
+Each restates the reference's plain-range general path, operation for
+operation, on lists of K+1 CPU coefficient tensors. An ordinary operand is a
+list of one tensor; ``lift`` pads it with zero orders as the reference does
+(/root/reference/src/polytensors/_range_ops.py:37-45).
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from .series import cauchy, rsqrt_series, softmax_family
+
+
+def lift(x, degree):
+    x = list(x)
+    return x + [torch.zeros_like(x[0]) for _ in range(degree + 1 - len(x))]
+
+
+def _mean(X, dims):
+    # sum then divide by the element count: /root/reference/src/polytensors/_range_ops.py:178-193
+    divisor = 1
+    for d in dims:
+        divisor *= X[0].shape[d]
+    return [c.sum(dim=dims, keepdim=True) / divisor for c in X]
+
+
+def _add_to_order0(X, value):
+    # constant operand: only order 0 changes, /root/reference/src/polytensors/_range_ops.py:122-132
+    return [X[0] + value] + [c.clone() for c in X[1:]]
+
+
+def _affine(out, weight, bias):
+    if weight is not None:
+        out = [c * weight[0] for c in out] if len(weight) == 1 else cauchy(out, lift(weight, len(out) - 1))
+    if bias is not None:
+        out = _add_to_order0(out, bias[0]) if len(bias) == 1 else [c + b for c, b in zip(out, bias)]
+    return out
+
+
+def rms_norm(X, normalized_shape, weight=None, eps=None):
+    """Series of ``input * rsqrt(mean(input*input) + eps) [* weight]``.
+
+    /root/reference/src/polytensors/_decompositions.py:14-22 (_rms_norm); eps
+    defaults to finfo(dtype).eps (:16-17); input*input and input*r are Cauchy
+    products (_range_ops.py:143-144); rsqrt is _series.py:83-96. ``weight`` is a
+    list of 1 (ordinary) or K+1 coefficients.
+    """
+    dims = tuple(range(-len(normalized_shape), 0))
+    eps = torch.finfo(X[0].dtype).eps if eps is None else eps
+    s = _add_to_order0(_mean(cauchy(X, X), dims), eps)
+    out = cauchy(X, rsqrt_series(s))
+    return _affine(out, weight, None)
+
+
+def layer_norm(X, normalized_shape, weight=None, bias=None, eps=1e-5):
+    """Series of ``(x - mean x) * rsqrt(mean((x - mean x)^2) + eps) [* w] [+ b]``.
+
+    The reference has no layer-norm rule (/root/reference/docs/notes.md:33-35);
+    this is the composite of its rules: mean (_range_ops.py:178-193), series
+    subtraction (:140-142), Cauchy products (:143-144) and rsqrt (_series.py:83-96).
+    """
+    dims = tuple(range(-len(normalized_shape), 0))
+    mu = _mean(X, dims)
+    C = [x - m for x, m in zip(X, mu)]
+    s = _add_to_order0(_mean(cauchy(C, C), dims), eps)
+    out = cauchy(C, rsqrt_series(s))
+    return _affine(out, weight, bias)
+
+
+def attention(Q, K, V, attn_mask=None, is_causal=False, scale=None):
+    """Series of ``softmax((Q*scale) @ K^T masked) @ V``.
+
+    /root/reference/src/polytensors/_decompositions.py:28-43 (_attention):
+    scale defaults to 1/sqrt(d); a masked score becomes (-inf, 0, ..., 0)
+    (masked_fill of the lifted -inf, _range_ops.py:271-277 with _plain.py:70-75);
+    a float mask is added to order 0; softmax is _plain.py:262-273; both
+    products are Cauchy matmuls (_plain.py:118-128). A row with no admissible
+    key is NaN here, as in the reference's general rule.
+    """
+    degree = max(len(Q), len(K), len(V)) - 1
+    Q, K, V = lift(Q, degree), lift(K, degree), lift(V, degree)
+    L, S = Q[0].shape[-2], K[0].shape[-2]
+    scale = 1 / math.sqrt(Q[0].shape[-1]) if scale is None else scale
+    scores = cauchy([q * scale for q in Q], [k.transpose(-2, -1) for k in K], matmul=True)
+
+    def masked_fill(series, excluded):
+        return [torch.where(excluded, torch.full((), float("-inf") if k == 0 else 0.0, dtype=c.dtype), c)
+                for k, c in enumerate(series)]
+
+    if is_causal:
+        keep = torch.ones(L, S, dtype=torch.bool).tril(diagonal=0)
+        scores = masked_fill(scores, ~keep)
+    if attn_mask is not None:
+        if attn_mask.dtype == torch.bool:
+            scores = masked_fill(scores, ~attn_mask)
+        else:
+            scores = _add_to_order0(scores, attn_mask)
+    probabilities = softmax_family(scores, -1)[0]
+    return cauchy(probabilities, V, matmul=True)
+
+
+def cross_entropy(Z, target, ignore_index=-100, reduction="mean"):
+    """Per-order loss series of ``F.cross_entropy(z, target)`` on (N, C) logits.
+
+    The log-softmax series (/root/reference/src/polytensors/_plain.py:262-273)
+    followed by native NLL on every order (/root/reference/src/polytensors/_dispatch.py:537-543).
+    """
+    _, log_softmax, _ = softmax_family(Z, 1)
+    return [F.nll_loss(lp, target, ignore_index=ignore_index, reduction=reduction) for lp in log_softmax]
+
+
+def logsumexp(Z, dim=-1):
+    """Log-sum-exp series along ``dim`` (keepdim squeezed), /root/reference/src/polytensors/_plain.py:262-273."""
+    return [c.squeeze(dim) for c in softmax_family(Z, dim)[2]]
+
+
+def matmul(A, B):
+    """Cauchy-product matmul, /root/reference/src/polytensors/_plain.py:118-128."""
+    degree = max(len(A), len(B)) - 1
+    return cauchy(lift(A, degree), lift(B, degree), matmul=True)

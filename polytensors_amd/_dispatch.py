@@ -1,0 +1,178 @@
+"""aten-level rules of ``PolyTensor`` (the ``__torch_dispatch__`` hook).
+
+Only the rules the hot path needs exist here:
+  * shape, view, copy and conversion operations, applied to every coefficient
+    (as /root/reference/src/polytensors/_range_ops.py:224-257);
+  * linear arithmetic: series +/- series, and +, -, *, / with an ordinary
+    operand (the constant-operand fast path, _range_ops.py:109-132), sum and
+    mean (_range_ops.py:178-193);
+  * the matrix products mm/bmm/addmm/mv/dot, which run the Cauchy-product
+    kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84).
+Every other operation raises NotImplementedError (as the reference does for
+operations without a rule, /root/reference/src/polytensors/_dispatch.py:852):
+nonlinear series arithmetic outside the four fused operations is not part of
+this package.
+"""
+
+import torch
+from torch.utils._python_dispatch import return_and_correct_aliasing
+
+aten = torch.ops.aten
+
+_VIEW_OPS = {
+    aten.t.default, aten.transpose.int, aten.permute.default, aten.view.default,
+    aten._unsafe_view.default, aten.reshape.default, aten.flatten.using_ints, aten.slice.Tensor,
+    aten.select.int, aten.unsqueeze.default, aten.squeeze.dim, aten.squeeze.dims, aten.squeeze.default,
+    aten.expand.default, aten.alias.default, aten.unbind.int, aten.split.Tensor, aten.chunk.default,
+    aten.narrow.default, aten.unfold.default, aten.diagonal.default, aten.as_strided.default,
+    aten.view_as_real.default, aten.view_as_complex.default,
+}
+_COPY_OPS = {
+    aten.clone.default, aten.detach.default, aten._to_copy.default, aten.contiguous.default,
+    aten.index_select.default, aten.gather.default, aten.index.Tensor, aten.flip.default,
+    aten.roll.default, aten.repeat.default,
+}
+_ADD = {aten.add.Tensor, aten.add.Scalar}
+_SUB = {aten.sub.Tensor, aten.sub.Scalar}
+_MUL = {aten.mul.Tensor, aten.mul.Scalar}
+_DIV = {aten.div.Tensor, aten.div.Scalar}
+_MATMUL = {aten.mm.default, aten.bmm.default, aten.mv.default, aten.dot.default, aten.matmul.default}
+
+
+def _is_poly(x):
+    from ._tensor import PolyTensor
+
+    return type(x) is PolyTensor
+
+
+def _collect(x, out):
+    if _is_poly(x):
+        out.append(x)
+    elif isinstance(x, (tuple, list)):
+        for y in x:
+            _collect(y, out)
+    elif isinstance(x, dict):
+        for y in x.values():
+            _collect(y, out)
+
+
+def _wrap(coeffs):
+    from ._tensor import PolyTensor
+
+    return PolyTensor(tuple(coeffs), requires_grad=False)
+
+
+def _per_order(args, k):
+    """The k-th coefficient of every PolyTensor in a nested argument structure."""
+    if _is_poly(args):
+        return args.coeffs[k]
+    if isinstance(args, tuple):
+        return tuple(_per_order(a, k) for a in args)
+    if isinstance(args, list):
+        return [_per_order(a, k) for a in args]
+    if isinstance(args, dict):
+        return {key: _per_order(v, k) for key, v in args.items()}
+    return args
+
+
+def _to_copy_kwargs(coefficient, kwargs):
+    dtype = kwargs.get("dtype")
+    if dtype is None or not coefficient.is_complex() or dtype.is_complex:
+        return kwargs
+    complex_dtype = {torch.float16: torch.complex32, torch.float32: torch.complex64,
+                     torch.float64: torch.complex128}.get(dtype)
+    if complex_dtype is None:
+        raise TypeError(f"{dtype} cannot hold complex PolyTensor directions")
+    return {**kwargs, "dtype": complex_dtype}
+
+
+def dispatch(func, types, args=(), kwargs=None):
+    kwargs = {} if kwargs is None else kwargs
+    polys = []
+    _collect(args, polys)
+    _collect(kwargs, polys)
+    if not polys:
+        return func(*args, **kwargs)
+    for p in polys:
+        if not hasattr(p, "coeffs"):
+            raise RuntimeError("PolyTensor wrapper reached dispatch without coefficient storage; "
+                               "keep PolyTensor wrappers alive (PolyTensor.retain_wrappers())")
+    degree = polys[0].degree
+    if any(p.degree != degree for p in polys[1:]):
+        raise ValueError("PolyTensor operands must have the same degree")
+    count = degree + 1
+    schema = getattr(func, "_schema", None)
+    mutable = bool(getattr(schema, "is_mutable", False))
+    if mutable and args and not _is_poly(args[0]):
+        raise RuntimeError(f"cannot update a regular Tensor in-place with a PolyTensor ({func})")
+
+    if func in _VIEW_OPS:
+        source = args[0]
+        results = [func(*_per_order(args, k), **_per_order(kwargs, k)) for k in range(count)]
+        if isinstance(results[0], (tuple, list)):
+            out = type(results[0])(_wrap(r[i] for r in results) for i in range(len(results[0])))
+        else:
+            out = _wrap(results)
+        del source
+        return return_and_correct_aliasing(func, args, kwargs, out)
+
+    if func in _COPY_OPS:
+        if func is aten._to_copy.default:
+            results = [func(c, **_to_copy_kwargs(c, kwargs)) for c in args[0].coeffs]
+        else:
+            results = [func(*_per_order(args, k), **_per_order(kwargs, k)) for k in range(count)]
+        return _wrap(results)
+
+    if func in (aten.copy_.default,):
+        target, source = args[0], args[1]
+        sources = source.coeffs if _is_poly(source) else (source,) + (None,) * degree
+        for dest, src in zip(target.coeffs, sources):
+            if src is None:
+                dest.zero_()
+            else:
+                if src.is_complex() and not dest.is_complex():
+                    raise RuntimeError("cannot copy complex PolyTensor coefficients into real storage")
+                dest.copy_(src)
+        return target
+    if func is aten.zero_.default:
+        for c in args[0].coeffs:
+            c.zero_()
+        return args[0]
+
+    if func is aten.neg.default:
+        return _wrap(-c for c in args[0].coeffs)
+
+    if func in _ADD or func in _SUB:
+        a, b = args[0], args[1]
+        alpha = kwargs.get("alpha", 1)
+        sign = alpha if func in _ADD else -alpha
+        if _is_poly(a) and _is_poly(b):
+            return _wrap(torch.add(x, y, alpha=sign) for x, y in zip(a.coeffs, b.coeffs))
+        if _is_poly(a):
+            return _wrap((torch.add(a.coeffs[0], b, alpha=sign), *(c.clone() for c in a.coeffs[1:])))
+        return _wrap((torch.add(a, b.coeffs[0], alpha=sign), *(sign * c for c in b.coeffs[1:])))
+
+    if func in _MUL or func in _DIV:
+        a, b = args[0], args[1]
+        if _is_poly(a) and _is_poly(b):
+            raise NotImplementedError(
+                f"{func}: elementwise series products are not part of polytensors_amd (only the fused "
+                "matmul, attention, norm and cross-entropy kernels are)")
+        if func in _DIV and not _is_poly(a):
+            raise NotImplementedError(f"{func}: division by a series is not part of polytensors_amd")
+        if _is_poly(a):
+            return _wrap((c * b if func in _MUL else c / b) for c in a.coeffs)
+        return _wrap(a * c for c in b.coeffs)
+
+    if func in (aten.sum.default, aten.sum.dim_IntList, aten.mean.default, aten.mean.dim):
+        return _wrap(func(*_per_order(args, k), **kwargs) for k in range(count))
+
+    if func in _MATMUL or func is aten.addmm.default:
+        from . import _fused_matmul
+
+        return _fused_matmul.from_dispatch(func, args, kwargs)
+
+    raise NotImplementedError(
+        f"PolyTensor has no rule for {func}: polytensors_amd implements the fused Taylor hot path "
+        "(matmul, scaled_dot_product_attention, rms_norm/layer_norm, cross_entropy) and linear "
+        "shape/arithmetic operations only")

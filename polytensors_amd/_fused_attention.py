@@ -1,0 +1,106 @@
+"""Fused flash-style attention of degree-K series on gfx950.
+
+For query, key and value series Q(t), K(t), V(t):
+    S(t) = scale * Q(t) K(t)^T  (masked),  P(t) = softmax(S(t)),  O(t) = P(t) V(t),
+the series of the reference's plain-range decomposition
+/root/reference/src/polytensors/_decompositions.py:28-43, computed block by block
+without forming the L x S score series: the online max and rescale use the
+constant-order scores only, the exponential series of the higher orders is
+formed from ``k E_k = sum_j j S_j E_{k-j}`` (/root/reference/src/polytensors/_plain.py:153-159),
+and the output is the series quotient of the accumulated numerator and row sum.
+Eligibility and conventions follow the degree-1 kernel of the reference
+(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or a
+boolean (L, S) mask (not both), no dropout or GQA, default scale 1/sqrt(d), and
+a query row with no admissible key gets output zero.
+"""
+
+import contextvars
+import math
+
+import torch
+
+from . import _gate, _ops
+
+_enabled = contextvars.ContextVar("polytensors_amd_fused_attention", default=True)
+_HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128)}
+
+
+def default_scale(head_dim):
+    return 1 / math.sqrt(head_dim)
+
+
+def _square_mask(attn_mask, L, S):
+    """A boolean mask as an (L, S) tensor, None if absent, NotImplemented if batch-dependent or additive."""
+    if attn_mask is None:
+        return None
+    if attn_mask.dtype != torch.bool or tuple(attn_mask.shape[-2:]) != (L, S):
+        return NotImplemented
+    if any(size != 1 for size in attn_mask.shape[:-2]):
+        return NotImplemented
+    return attn_mask.reshape(L, S)
+
+
+def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa):
+    from ._tensor import PolyTensor
+
+    if not _enabled.get():
+        return ("the fused attention kernel is disabled (PolyTensor.fused_attention(False)) and "
+                "polytensors_amd has no general series rules")
+    if dropout_p != 0.0:
+        return "dropout is not supported"
+    if enable_gqa:
+        return "GQA is not supported"
+    tensors = (query, key, value)
+    if not all(isinstance(x, torch.Tensor) for x in tensors):
+        return "query, key and value must be tensors"
+    if isinstance(attn_mask, PolyTensor):
+        return "the mask must be an ordinary tensor"
+    reason = _gate.common_reason(tensors)
+    if reason is not None:
+        return reason
+    dtype = query.dtype
+    coeffs = [c for x in tensors for c in _gate.coefficients(x, 0)]
+    if any(c.dtype != dtype for c in coeffs):
+        return "query, key and value coefficients must share one dtype"
+    if dtype not in _HEAD_DIMS:
+        return f"dtype {dtype} is not supported (float32 or float64)"
+    if query.ndim < 3 or key.shape != value.shape or query.shape[:-2] != key.shape[:-2]:
+        return "shapes must be (..., L, d) and (..., S, d) with equal batch dimensions"
+    if query.shape[-1] != key.shape[-1] or query.shape[-1] not in _HEAD_DIMS[dtype]:
+        return f"head dim {query.shape[-1]} not in {_HEAD_DIMS[dtype]}"
+    if is_causal and attn_mask is not None:
+        return "is_causal and attn_mask are exclusive"
+    if _square_mask(attn_mask, query.shape[-2], key.shape[-2]) is NotImplemented:
+        return "only a boolean (L, S) mask is supported"
+    return None
+
+
+def eligible(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, enable_gqa=False):
+    return why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa) is None
+
+
+def require_eligible(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, enable_gqa=False):
+    reason = why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa)
+    if reason is not None:
+        raise NotImplementedError(f"scaled_dot_product_attention: {reason}")
+
+
+def _flat(coeffs, shape):
+    """[bh, T, d] contiguous coefficients (no copy when already contiguous)."""
+    return [c.expand(shape).reshape(-1, shape[-2], shape[-1]).contiguous() for c in coeffs]
+
+
+def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
+    """Fused degree-K attention of an eligible call (see ``eligible``)."""
+    from ._tensor import PolyTensor
+
+    require_eligible(query, key, value, attn_mask, 0.0, is_causal, False)
+    degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
+    L, S = query.shape[-2], key.shape[-2]
+    mask = _square_mask(attn_mask, L, S)
+    scale = default_scale(query.shape[-1]) if scale is None else scale
+    q = _flat(_gate.coefficients(query, degree), query.shape)
+    k = _flat(_gate.coefficients(key, degree), key.shape)
+    v = _flat(_gate.coefficients(value, degree), value.shape)
+    out, _ = _ops.taylor_attention_fwd(q, k, v, mask, bool(is_causal), float(scale), degree)
+    return PolyTensor.from_stacked(out.view(degree + 1, *query.shape))

@@ -1,0 +1,95 @@
+"""Fused cross entropy of degree-K series of (N, C) logits on gfx950.
+
+For logits ``z(t) = sum_k z_k t^k`` and integer targets ``y``, one streaming
+pass per row computes the log-sum-exp series ``lse(t)`` of the row, and the
+loss series is ``lse_k - z_k[y]`` (the log-softmax series of
+/root/reference/src/polytensors/_plain.py:262-273 read at the target, the
+per-order NLL of /root/reference/src/polytensors/_dispatch.py:537-543). Rows
+whose target is ``ignore_index`` have zero loss; ``mean`` divides by the
+number of other rows, as ``torch.nn.functional.cross_entropy`` and the
+reference's reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:257-277).
+Arithmetic is float32 (float64 for float64 logits).
+"""
+
+import contextvars
+
+import torch
+
+from . import _gate, _lib, _ops
+
+_enabled = contextvars.ContextVar("polytensors_amd_fused_cross_entropy", default=True)
+_DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
+
+
+def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, softcap=None):
+    from ._tensor import PolyTensor
+
+    if not _enabled.get():
+        return ("the fused cross-entropy kernel is disabled (PolyTensor.fused_cross_entropy(False)) and "
+                "polytensors_amd has no general series rules")
+    if not isinstance(input, PolyTensor):
+        return "logits must be a PolyTensor"
+    reason = _gate.common_reason((input,))
+    if reason is not None:
+        return reason
+    if input.ndim != 2:
+        return "logits must be (N, C)"
+    if input.dtype not in _DTYPES or any(c.dtype != input.dtype for c in input.coeffs):
+        return "logits must be float16/bfloat16/float32/float64 in every order"
+    if isinstance(target, PolyTensor) or not isinstance(target, torch.Tensor) or target.dtype != torch.int64:
+        return "targets must be an ordinary int64 tensor (class indices)"
+    if target.shape != input.shape[:1] or target.device != input.device:
+        return "targets must be (N,) on the logits' device"
+    if weight is not None:
+        return "class weights are not implemented"
+    if label_smoothing != 0.0:
+        return "label smoothing is not implemented"
+    if reduction not in _lib.REDUCTIONS:
+        return f"unknown reduction {reduction!r}"
+    if softcap is not None:
+        return "softcap is not implemented for series logits"
+    return None
+
+
+def eligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, softcap=None):
+    return why_ineligible(input, target, weight, reduction, label_smoothing, softcap) is None
+
+
+def _rows(coeffs):
+    """Coefficients whose rows are unit-stride with one common row stride (a padded slice is fine)."""
+    first = coeffs[0]
+    if first.stride(-1) == 1 and all(c.stride() == first.stride() for c in coeffs):
+        return list(coeffs)
+    return [c.contiguous() for c in coeffs]
+
+
+def fused(input, target, ignore_index=-100, reduction="mean"):
+    """Loss series (a PolyTensor in float32, or float64 for float64 logits)."""
+    from ._tensor import PolyTensor
+
+    z = _rows(input.coeffs)
+    loss, _ = _ops.cross_entropy_series(z, target.contiguous(), int(ignore_index), _lib.REDUCTIONS[reduction])
+    return PolyTensor.from_stacked(loss)
+
+
+def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mean", label_smoothing=0.0):
+    reason = why_ineligible(input, target, weight, reduction, label_smoothing)
+    if reason is not None:
+        raise NotImplementedError(f"cross_entropy: {reason}")
+    return fused(input, target, ignore_index=ignore_index, reduction=reduction)
+
+
+def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="mean"):
+    """``PolyTensor.cross_entropy``: series logits use the fused kernel (at least float32 out);
+    ordinary tensors use the composite, as /root/reference/src/polytensors/_fused_cross_entropy.py:280-294."""
+    from ._tensor import PolyTensor
+
+    if isinstance(logits, PolyTensor):
+        reason = why_ineligible(logits, target, None, reduction, 0.0, softcap)
+        if reason is not None:
+            raise NotImplementedError(f"cross_entropy: {reason}")
+        return fused(logits, target, ignore_index=ignore_index, reduction=reduction)
+    logits = logits.to(torch.promote_types(logits.dtype, torch.float32))
+    if softcap is not None:
+        logits = softcap * torch.tanh(logits / softcap)
+    return torch.nn.functional.cross_entropy(logits, target, ignore_index=ignore_index, reduction=reduction)

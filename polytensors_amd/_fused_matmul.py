@@ -1,0 +1,114 @@
+"""Cauchy-product matrix products of degree-K series on gfx950.
+
+``C_k = sum_{i+j=k} A_i @ B_j`` for all k in one kernel launch: the reference
+computes the same product as (K+1)(K+2)/2 separate matmuls
+(/root/reference/src/polytensors/_plain.py:118-128, reached from the
+mm/bmm/matmul/linear/addmm rules of /root/reference/src/polytensors/_range_ops.py:160-176).
+An ordinary-tensor operand is a series with one order (the reference lifts it
+with zero orders, _range_ops.py:37-45), so only K+1 products are formed.
+Batch dimensions broadcast as in torch.matmul; float32 and float64.
+"""
+
+import torch
+
+from . import _gate, _ops
+
+_DTYPES = (torch.float32, torch.float64)
+
+
+def why_ineligible(a, b):
+    reason = _gate.common_reason((a, b))
+    if reason is not None:
+        return reason
+    coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
+    dtype = coeffs[0].dtype
+    if dtype not in _DTYPES or any(c.dtype != dtype for c in coeffs):
+        return "operands must share one dtype, float32 or float64"
+    if a.ndim == 0 or b.ndim == 0:
+        return "matmul of a 0-d tensor"
+    return None
+
+
+def eligible(a, b):
+    return why_ineligible(a, b) is None
+
+
+def _degree(*xs):
+    from ._tensor import PolyTensor
+
+    return next(x.degree for x in xs if isinstance(x, PolyTensor))
+
+
+def matmul(a, b):
+    """Series of ``torch.matmul(a, b)``."""
+    from ._tensor import PolyTensor
+
+    reason = why_ineligible(a, b)
+    if reason is not None:
+        raise NotImplementedError(f"matmul: {reason}")
+    degree = _degree(a, b)
+    A = list(_gate.coefficients(a, degree))
+    B = list(_gate.coefficients(b, degree))
+    squeeze_m = A[0].ndim == 1
+    squeeze_n = B[0].ndim == 1
+    if squeeze_m:
+        A = [c.unsqueeze(0) for c in A]
+    if squeeze_n:
+        B = [c.unsqueeze(-1) for c in B]
+    m, kd = A[0].shape[-2:]
+    kb, n = B[0].shape[-2:]
+    if kd != kb:
+        raise RuntimeError(f"matmul: inner dimensions differ ({kd} vs {kb})")
+    batch = torch.broadcast_shapes(A[0].shape[:-2], B[0].shape[:-2])
+
+    def flat(coeffs, rows, cols):
+        own = coeffs[0].shape[:-2]
+        if len(own) == 0 or (tuple(own) != tuple(batch) and all(s == 1 for s in own)):
+            return [c.reshape(1, rows, cols).contiguous() for c in coeffs]
+        return [c.expand(*batch, rows, cols).reshape(-1, rows, cols).contiguous() for c in coeffs]
+
+    out = _ops.cauchy_matmul(flat(A, m, kd), flat(B, kd, n), degree, False)
+    out = out.view(degree + 1, *batch, m, n)
+    if squeeze_m:
+        out = out.squeeze(-2)
+    if squeeze_n:
+        out = out.squeeze(-1)
+    return PolyTensor.from_stacked(out)
+
+
+def linear(x, weight, bias=None):
+    """Series of ``torch.nn.functional.linear``: x @ weight^T (+ bias)."""
+    from ._tensor import PolyTensor
+
+    reason = why_ineligible(x, weight)
+    if reason is not None:
+        raise NotImplementedError(f"linear: {reason}")
+    degree = _degree(x, weight, *([bias] if isinstance(bias, PolyTensor) else []))
+    X = list(_gate.coefficients(x, degree))
+    W = list(_gate.coefficients(weight, degree))
+    if W[0].ndim != 2:
+        raise RuntimeError("linear: weight must be 2-D")
+    out_features, in_features = W[0].shape
+    lead = X[0].shape[:-1]
+    X = [c.reshape(1, -1, in_features).contiguous() for c in X]
+    W = [c.reshape(1, out_features, in_features).contiguous() for c in W]
+    out = _ops.cauchy_matmul(X, W, degree, True)
+    result = PolyTensor.from_stacked(out.view(degree + 1, *lead, out_features))
+    if bias is not None:
+        result = result + bias
+    return result
+
+
+def from_dispatch(func, args, kwargs):
+    """mm/bmm/mv/dot/matmul/addmm reaching ``__torch_dispatch__``."""
+    aten = torch.ops.aten
+    if func is aten.addmm.default:
+        bias, a, b = args[:3]
+        beta, alpha = kwargs.get("beta", 1), kwargs.get("alpha", 1)
+        product = matmul(a, b)
+        if alpha != 1:
+            product = product * alpha
+        if beta == 0:
+            return product
+        return product + (bias * beta if beta != 1 else bias)
+    return matmul(args[0], args[1])

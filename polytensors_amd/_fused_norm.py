@@ -1,0 +1,100 @@
+"""Fused RMSNorm / LayerNorm series (any degree up to 8) on gfx950.
+
+``rms_norm`` mirrors /root/reference/src/polytensors/_fused_norm.py:63-69: the
+normalisation runs in one kernel pass and ``eps`` defaults to
+``finfo(dtype).eps`` (:64). The reference then multiplies by the weight as a
+separate PolyTensor operation (:69); here an ordinary or series weight of the
+normalised shape and input dtype is applied inside the kernel, and any other
+weight falls back to that separate multiply. Half and bfloat16 inputs compute in
+float32, float64 in float64 (as the reference's kernel, _norm_kernels.py:12-13).
+
+``layer_norm`` has no reference counterpart (native layer norm has no rule
+there, /root/reference/docs/notes.md:33-35); it is the series of
+``(x - mean(x)) * rsqrt(mean((x - mean(x))**2) + eps) * w + b``.
+"""
+
+import math
+
+import torch
+
+from . import _gate, _ops
+
+_DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
+
+
+def why_ineligible(input, normalized_shape, weight=None, bias=None):
+    from ._tensor import PolyTensor
+
+    reason = _gate.common_reason((input, weight, bias))
+    if reason is not None:
+        return reason
+    if not isinstance(input, torch.Tensor) or input.dtype not in _DTYPES:
+        return "input must be a float16/bfloat16/float32/float64 tensor"
+    polys = [x for x in (input, weight, bias) if isinstance(x, PolyTensor)]
+    if any(c.dtype != input.dtype for p in polys for c in p.coeffs):
+        return "all series coefficients must have the input's dtype"
+    shape = tuple(normalized_shape)
+    if not shape or tuple(input.shape[-len(shape):]) != shape:
+        return "normalized_shape must match the input's trailing dimensions"
+    if math.prod(shape) == 0 or input.numel() == 0:
+        return "empty normalisation"
+    return None
+
+
+def eligible(input, normalized_shape, weight=None, bias=None):
+    return why_ineligible(input, normalized_shape, weight, bias) is None
+
+
+def _series_coeffs(x, degree):
+    from ._tensor import PolyTensor
+
+    if isinstance(x, PolyTensor):
+        return [c.contiguous() for c in x.coeffs]
+    return [x.contiguous()] + [torch.zeros_like(x, memory_format=torch.contiguous_format)
+                               for _ in range(degree)]
+
+
+def _affine_coeffs(a, input, shape):
+    """Kernel-side coefficients of a weight/bias, or None if it must be applied separately."""
+    from ._tensor import PolyTensor
+
+    if a is None:
+        return []
+    coeffs = a.coeffs if isinstance(a, PolyTensor) else (a,)
+    if any(c.dtype != input.dtype or tuple(c.shape) != shape or c.device != input.device for c in coeffs):
+        return None
+    return [c.contiguous().reshape(-1) for c in coeffs]
+
+
+def _run(input, normalized_shape, weight, bias, eps, layer):
+    from ._tensor import PolyTensor
+
+    shape = tuple(normalized_shape)
+    reason = why_ineligible(input, shape, weight, bias)
+    if reason is not None:
+        raise NotImplementedError(f"{'layer_norm' if layer else 'rms_norm'}: {reason}")
+    degree = next(x.degree for x in (input, weight, bias) if isinstance(x, PolyTensor))
+    x = _series_coeffs(input, degree)
+    w = _affine_coeffs(weight, input, shape)
+    b = _affine_coeffs(bias, input, shape) if layer else []
+    fused_affine = w is not None and b is not None
+    out = _ops.norm_series(x, w if fused_affine else [], b if fused_affine else [], math.prod(shape),
+                           float(eps), layer)
+    result = PolyTensor.from_stacked(out)
+    if not fused_affine:
+        if weight is not None:
+            result = result * weight
+        if layer and bias is not None:
+            result = result + bias
+    return result
+
+
+def rms_norm(input, normalized_shape, weight=None, eps=None):
+    """Degree-K series of ``torch.nn.functional.rms_norm``."""
+    eps = torch.finfo(input.dtype).eps if eps is None else eps
+    return _run(input, normalized_shape, weight, None, eps, layer=False)
+
+
+def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
+    """Degree-K series of ``torch.nn.functional.layer_norm``."""
+    return _run(input, normalized_shape, weight, bias, eps, layer=True)

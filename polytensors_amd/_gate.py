@@ -1,0 +1,57 @@
+"""Conditions every fused entry point shares, as reason strings.
+
+A ``None`` reason means the call can run on the gfx950 kernels. The reference's
+``eligible`` functions (/root/reference/src/polytensors/_fused_attention.py:227-256,
+_fused_norm.py:11-21, _fused_cross_entropy.py:238-254) return False and let the
+caller use the general rules; this package has no general rules, so callers
+turn a reason into NotImplementedError. A missing kernel library on a HIP
+device is never a reason: it raises LibraryMissingError.
+"""
+
+import torch
+
+from . import _lib
+from ._plain import plain_range_enabled
+
+MAX_DEGREE = 8
+
+
+def coefficients(x, degree):
+    """The coefficient tuple of a PolyTensor, or (x,) for an ordinary tensor (a plain operand)."""
+    from ._tensor import PolyTensor
+
+    if isinstance(x, PolyTensor):
+        return tuple(x.coeffs)
+    return (x,)
+
+
+def common_reason(values, *, allow_plain_grad=False):
+    """Shared conditions over the tensor operands of one fused call."""
+    from ._tensor import PolyTensor, _coefficient_autograd_enabled
+
+    tensors = [v for v in values if isinstance(v, torch.Tensor)]
+    polys = [v for v in tensors if isinstance(v, PolyTensor)]
+    if not polys:
+        return "no PolyTensor operand"
+    if not plain_range_enabled():
+        return ("extended-range (default) mode is not implemented by polytensors_amd; "
+                "run the series inside PolyTensor.plain_range()")
+    degree = polys[0].degree
+    if any(p.degree != degree for p in polys):
+        return "PolyTensor operands must have the same degree"
+    if degree > MAX_DEGREE:
+        return f"degree {degree} exceeds the kernels' maximum {MAX_DEGREE}"
+    if _coefficient_autograd_enabled.get():
+        return "coefficient_autograd needs series backward kernels, which polytensors_amd does not implement"
+    if torch.is_grad_enabled():
+        grads = any(t.requires_grad for t in tensors) or any(
+            c.requires_grad for p in polys for c in p.coeffs)
+        if grads and not allow_plain_grad:
+            return "series backward is not implemented (forward-only kernels); use torch.no_grad()"
+    coeffs = [c for t in tensors for c in coefficients(t, degree)]
+    if any(c.is_complex() for c in coeffs):
+        return "complex directions are not implemented by the fused kernels"
+    if any(c.device.type != "cuda" for c in coeffs):
+        return "polytensors_amd runs on HIP (cuda) devices only"
+    _lib.load()   # loud failure if the kernels are not built
+    return None

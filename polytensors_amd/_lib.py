@@ -1,0 +1,114 @@
+"""ctypes binding of ``libpolytaylor.so`` (the C ABI declared in ``include/polytaylor.h``).
+
+The library is loaded after torch, so its HIP runtime dependency resolves to the
+runtime torch already loaded (one HIP runtime per process: the stream handles
+torch hands out are valid in the library). There is no fallback: a missing or
+stale library raises ``LibraryMissingError``.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
+ABI_VERSION = 1
+
+PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
+REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
+
+DTYPE_CODES = {
+    torch.float32: 0,
+    torch.float64: 1,
+    torch.bfloat16: 2,
+    torch.float16: 3,
+}
+
+_c_int, _c_i64, _c_dbl, _c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_double, ctypes.c_void_p
+_c_vpp = ctypes.POINTER(ctypes.c_void_p)
+
+# name -> (restype, argtypes); mirrors include/polytaylor.h.
+SIGNATURES = {
+    "pt_last_error": (ctypes.c_char_p, []),
+    "pt_abi_version": (_c_int, []),
+    "pt_max_degree": (_c_int, []),
+    "pt_rms_norm_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_int, _c_vpp,
+                                        _c_i64, _c_i64, _c_dbl, _c_vp]),
+    "pt_layer_norm_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_int, _c_vpp, _c_int,
+                                          _c_vpp, _c_i64, _c_i64, _c_dbl, _c_vp]),
+    "pt_cross_entropy_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
+                                             _c_i64, _c_int, _c_vpp, _c_vpp, _c_vp, _c_vp]),
+    "pt_cross_entropy_series_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_int]),
+    "pt_cauchy_matmul": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp,
+                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp]),
+    "pt_taylor_attention_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp, _c_int,
+                                         _c_vpp, _c_vpp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp,
+                                         _c_dbl, _c_vp]),
+}
+
+
+class LibraryMissingError(RuntimeError):
+    """The HIP kernels were not built (run ``python -m polytensors_amd.build``)."""
+
+
+class KernelError(RuntimeError):
+    """A pt_* entry point returned an error status."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Load and bind the library (once); raises LibraryMissingError if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissingError(
+                f"{LIB_PATH} is missing: build the gfx950 kernels with `python -m polytensors_amd.build`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if lib.pt_abi_version() != ABI_VERSION:
+            raise LibraryMissingError(f"{LIB_PATH} has ABI {lib.pt_abi_version()}, expected {ABI_VERSION}: rebuild it")
+        _lib = lib
+    return _lib
+
+
+def available():
+    try:
+        load()
+    except (LibraryMissingError, OSError):
+        return False
+    return True
+
+
+def max_degree():
+    return load().pt_max_degree()
+
+
+def ptr_array(tensors):
+    """A host array of device pointers (keeps no reference to the tensors)."""
+    arr = (ctypes.c_void_p * max(1, len(tensors)))()
+    for i, t in enumerate(tensors):
+        arr[i] = t.data_ptr()
+    return arr
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(status, what):
+    if status != PT_OK:
+        message = load().pt_last_error().decode(errors="replace")
+        kind = {PT_INVALID_ARGUMENT: "invalid argument", PT_UNSUPPORTED: "unsupported",
+                PT_DEVICE_ERROR: "device error"}.get(status, f"status {status}")
+        raise KernelError(f"{what}: {kind}: {message}")

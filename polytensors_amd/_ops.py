@@ -1,0 +1,217 @@
+"""``torch.library`` custom ops of the gfx950 Taylor kernels.
+
+Each op takes the K+1 coefficient tensors of a series as a ``Tensor[]`` (the
+reference's tuple storage, passed without stacking copies), launches the C-ABI
+entry point of ``libpolytaylor.so`` on the current HIP stream, and returns the
+result as one coefficient-stacked tensor ``[K+1, ...]``. The ops are registered
+for the CUDA (HIP) device only, with fake implementations for shape
+propagation; on any other device the dispatcher raises. Outputs never alias
+inputs.
+"""
+
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+NAMESPACE = "polytensors_amd"
+
+
+def _acc_dtype(dtype):
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+def _require(cond, message):
+    if not cond:
+        raise ValueError(message)
+
+
+def _check_series(name, coeffs, dtype=None):
+    _require(len(coeffs) >= 1, f"{name}: at least one coefficient is required")
+    first = coeffs[0]
+    dtype = first.dtype if dtype is None else dtype
+    for c in coeffs:
+        _require(c.dtype == dtype, f"{name}: coefficient dtypes differ ({c.dtype} vs {dtype})")
+        _require(c.device == first.device, f"{name}: coefficients on different devices")
+        _require(c.shape == first.shape, f"{name}: coefficient shapes differ")
+        _require(c.is_contiguous(), f"{name}: coefficients must be contiguous")
+    _require(dtype in _lib.DTYPE_CODES, f"{name}: unsupported dtype {dtype}")
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm / LayerNorm series
+
+@torch.library.custom_op(f"{NAMESPACE}::norm_series", mutates_args=(), device_types="cuda")
+def norm_series(x: List[torch.Tensor], weight: List[torch.Tensor], bias: List[torch.Tensor],
+                n: int, eps: float, layer: bool) -> torch.Tensor:
+    """y = (Layer|RMS)Norm series over the last ``n`` elements of each coefficient."""
+    _check_series("norm_series", x)
+    degree = len(x) - 1
+    numel = x[0].numel()
+    _require(n >= 1 and numel % n == 0, "norm_series: n must divide the element count")
+    for name, aff in (("weight", weight), ("bias", bias)):
+        _require(len(aff) in (0, 1, degree + 1), f"norm_series: {name} needs 0, 1 or degree+1 coefficients")
+        for c in aff:
+            _require(c.dtype == x[0].dtype and c.device == x[0].device and c.numel() == n
+                     and c.is_contiguous(), f"norm_series: {name} coefficients must be contiguous [n] of the input dtype")
+    _require(layer or not bias, "norm_series: bias is a LayerNorm argument")
+    out = torch.empty((degree + 1, *x[0].shape), dtype=x[0].dtype, device=x[0].device)
+    lib = _lib.load()
+    ys = list(out.unbind(0))
+    args = (_lib.DTYPE_CODES[x[0].dtype], degree, _lib.ptr_array(x),
+            _lib.ptr_array(weight) if weight else None, len(weight))
+    if layer:
+        status = lib.pt_layer_norm_series_fwd(*args, _lib.ptr_array(bias) if bias else None, len(bias),
+                                              _lib.ptr_array(ys), numel // n, n, float(eps),
+                                              _lib.stream_of(x[0].device))
+    else:
+        status = lib.pt_rms_norm_series_fwd(*args, _lib.ptr_array(ys), numel // n, n, float(eps),
+                                            _lib.stream_of(x[0].device))
+    _lib.check(status, "layer_norm_series" if layer else "rms_norm_series")
+    return out
+
+
+@norm_series.register_fake
+def _(x, weight, bias, n, eps, layer):
+    return x[0].new_empty((len(x), *x[0].shape))
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy series
+
+@torch.library.custom_op(f"{NAMESPACE}::cross_entropy_series", mutates_args=(), device_types="cuda")
+def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_index: int,
+                         reduction: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-order cross entropy of (N, C) logit series; returns (loss, lse).
+
+    loss: [K+1, N] (reduction none) or [K+1] (mean/sum), and lse: [K+1, N], both in
+    float32 (float64 for float64 logits).
+    """
+    _require(len(z) >= 1, "cross_entropy_series: at least one coefficient is required")
+    first = z[0]
+    _require(first.dim() == 2, "cross_entropy_series: logits must be (N, C)")
+    _require(first.dtype in _lib.DTYPE_CODES, f"cross_entropy_series: unsupported dtype {first.dtype}")
+    for c in z:
+        _require(c.dtype == first.dtype and c.device == first.device and c.shape == first.shape,
+                 "cross_entropy_series: coefficients must share dtype, device and shape")
+        _require(c.stride() == first.stride() and c.stride(1) == 1,
+                 "cross_entropy_series: coefficient rows must be contiguous with one common row stride")
+    _require(target.dtype == torch.int64 and target.shape == first.shape[:1] and target.is_contiguous()
+             and target.device == first.device, "cross_entropy_series: target must be contiguous int64 [N]")
+    _require(reduction in (0, 1, 2), "cross_entropy_series: reduction must be 0, 1 or 2")
+    degree = len(z) - 1
+    rows, classes = first.shape
+    dtype = first.dtype
+    lse = torch.empty((degree + 1, rows), dtype=_acc_dtype(dtype), device=first.device)
+    loss = torch.empty((degree + 1, rows) if reduction == 0 else (degree + 1,), dtype=_acc_dtype(dtype),
+                       device=first.device)
+    lib = _lib.load()
+    code = _lib.DTYPE_CODES[dtype]
+    wbytes = lib.pt_cross_entropy_series_workspace_size(code, degree, rows, reduction)
+    workspace = torch.empty((max(1, wbytes),), dtype=torch.uint8, device=first.device)
+    status = lib.pt_cross_entropy_series_fwd(
+        code, degree, _lib.ptr_array(z), rows, classes, first.stride(0) if rows else classes,
+        target.data_ptr(), ignore_index, reduction, _lib.ptr_array(list(loss.unbind(0))),
+        _lib.ptr_array(list(lse.unbind(0))), workspace.data_ptr(), _lib.stream_of(first.device))
+    _lib.check(status, "cross_entropy_series")
+    return loss, lse
+
+
+@cross_entropy_series.register_fake
+def _(z, target, ignore_index, reduction):
+    rows = z[0].shape[0]
+    loss = z[0].new_empty((len(z), rows) if reduction == 0 else (len(z),), dtype=_acc_dtype(z[0].dtype))
+    lse = z[0].new_empty((len(z), rows), dtype=_acc_dtype(z[0].dtype))
+    return loss, lse
+
+
+# ---------------------------------------------------------------------------
+# Cauchy-product matmul
+
+@torch.library.custom_op(f"{NAMESPACE}::cauchy_matmul", mutates_args=(), device_types="cuda")
+def cauchy_matmul(a: List[torch.Tensor], b: List[torch.Tensor], degree: int, trans_b: bool) -> torch.Tensor:
+    """C_k = sum_{i+j=k} A_i @ B_j for [batch, m, k] x [batch, k, n] (or [batch, n, k] if trans_b).
+
+    ``a`` and ``b`` hold 1 (plain operand) or degree+1 coefficients; a batch
+    dimension of size 1 broadcasts. Returns [degree+1, batch, m, n].
+    """
+    for name, s in (("a", a), ("b", b)):
+        _require(len(s) in (1, degree + 1), f"cauchy_matmul: {name} needs 1 or degree+1 coefficients")
+        _check_series(f"cauchy_matmul {name}", s)
+        _require(s[0].dim() == 3, f"cauchy_matmul: {name} must be 3-D [batch, rows, cols]")
+    dtype = a[0].dtype
+    _require(b[0].dtype == dtype and b[0].device == a[0].device, "cauchy_matmul: operand dtype/device differ")
+    _require(dtype in (torch.float32, torch.float64), "cauchy_matmul: float32 or float64 only")
+    ba, m, kd = a[0].shape
+    if trans_b:
+        bb, n, kb = b[0].shape
+    else:
+        bb, kb, n = b[0].shape
+    _require(kb == kd, "cauchy_matmul: inner dimensions differ")
+    _require(ba == bb or ba == 1 or bb == 1, "cauchy_matmul: batch dimensions do not broadcast")
+    batch = max(ba, bb)
+    out = torch.empty((degree + 1, batch, m, n), dtype=dtype, device=a[0].device)
+    lib = _lib.load()
+    status = lib.pt_cauchy_matmul(
+        _lib.DTYPE_CODES[dtype], degree, _lib.ptr_array(a), len(a), _lib.ptr_array(b), len(b),
+        _lib.ptr_array(list(out.unbind(0))), batch, m, n, kd,
+        0 if ba == 1 else m * kd, 0 if bb == 1 else n * kd, int(trans_b), _lib.stream_of(a[0].device))
+    _lib.check(status, "cauchy_matmul")
+    return out
+
+
+@cauchy_matmul.register_fake
+def _(a, b, degree, trans_b):
+    ba, m, _ = a[0].shape
+    bb = b[0].shape[0]
+    n = b[0].shape[1] if trans_b else b[0].shape[2]
+    return a[0].new_empty((degree + 1, max(ba, bb), m, n))
+
+
+# ---------------------------------------------------------------------------
+# Taylor flash attention forward
+
+@torch.library.custom_op(f"{NAMESPACE}::taylor_attention_fwd", mutates_args=(), device_types="cuda")
+def taylor_attention_fwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[torch.Tensor],
+                         mask: Optional[torch.Tensor], causal: bool, scale: float,
+                         degree: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Degree-K attention of [bh, L, d] query and [bh, S, d] key/value series.
+
+    Each of q, k, v holds 1 (plain operand) or degree+1 coefficients. ``mask``
+    is an optional (L, S) bool tensor (True = admissible). Returns
+    (out [degree+1, bh, L, d], lse [degree+1, bh, L]).
+    """
+    for name, s in (("q", q), ("k", k), ("v", v)):
+        _require(len(s) in (1, degree + 1), f"taylor_attention: {name} needs 1 or degree+1 coefficients")
+        _check_series(f"taylor_attention {name}", s)
+        _require(s[0].dim() == 3, f"taylor_attention: {name} must be [bh, length, d]")
+    dtype = q[0].dtype
+    _require(dtype in (torch.float32, torch.float64), "taylor_attention: float32 or float64 only")
+    bh, lq, d = q[0].shape
+    _require(k[0].shape == v[0].shape and k[0].shape[0] == bh and k[0].shape[2] == d,
+             "taylor_attention: key/value shapes must be [bh, S, d] matching the query")
+    _require(k[0].dtype == dtype and v[0].dtype == dtype, "taylor_attention: dtypes differ")
+    lk = k[0].shape[1]
+    if mask is not None:
+        _require(mask.dtype == torch.bool and mask.shape == (lq, lk) and mask.device == q[0].device,
+                 "taylor_attention: mask must be a bool (L, S) tensor on the query's device")
+        _require(not causal, "taylor_attention: mask and causal are exclusive")
+        mask = mask.contiguous()
+    out = torch.empty((degree + 1, bh, lq, d), dtype=dtype, device=q[0].device)
+    lse = torch.empty((degree + 1, bh, lq), dtype=_acc_dtype(dtype), device=q[0].device)
+    lib = _lib.load()
+    status = lib.pt_taylor_attention_fwd(
+        _lib.DTYPE_CODES[dtype], degree, _lib.ptr_array(q), len(q), _lib.ptr_array(k), len(k),
+        _lib.ptr_array(v), len(v), _lib.ptr_array(list(out.unbind(0))), _lib.ptr_array(list(lse.unbind(0))),
+        bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(), float(scale),
+        _lib.stream_of(q[0].device))
+    _lib.check(status, "taylor_attention_fwd")
+    return out, lse
+
+
+@taylor_attention_fwd.register_fake
+def _(q, k, v, mask, causal, scale, degree):
+    bh, lq, d = q[0].shape
+    return (q[0].new_empty((degree + 1, bh, lq, d)),
+            q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))

@@ -1,0 +1,7 @@
+// Instantiates the norm-series kernels for one storage type.
+#include "norm_series.inl"
+
+namespace pt {
+template int launch_norm<_Float16, false>(const NormArgs&);
+template int launch_norm<_Float16, true>(const NormArgs&);
+}  // namespace pt

@@ -1,0 +1,28 @@
+// Entry points whose kernels are not built yet: they report PT_UNSUPPORTED.
+#include "pt_common.h"
+
+extern "C" {
+
+int pt_cross_entropy_series_fwd(int, int, const void* const*, int64_t, int64_t, int64_t,
+                                const int64_t*, int64_t, int, void* const*, void* const*, void*,
+                                void*) {
+  pt_host::set_error("cross-entropy series kernel not built");
+  return PT_UNSUPPORTED;
+}
+
+size_t pt_cross_entropy_series_workspace_size(int, int, int64_t, int) { return 0; }
+
+int pt_cauchy_matmul(int, int, const void* const*, int, const void* const*, int, void* const*,
+                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, void*) {
+  pt_host::set_error("Cauchy matmul kernel not built");
+  return PT_UNSUPPORTED;
+}
+
+int pt_taylor_attention_fwd(int, int, const void* const*, int, const void* const*, int,
+                            const void* const*, int, void* const*, void* const*, int64_t, int64_t,
+                            int64_t, int64_t, int, const uint8_t*, double, void*) {
+  pt_host::set_error("Taylor attention kernel not built");
+  return PT_UNSUPPORTED;
+}
+
+}  // extern "C"

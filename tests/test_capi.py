@@ -1,0 +1,65 @@
+"""The C-ABI library loads and exports everything include/polytaylor.h declares (CPU only).
+
+No kernel is launched: the calls below return at argument validation, before
+any device work.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from polytensors_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "polytaylor.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert os.path.exists(_lib.LIB_PATH), "build the kernels: python -m polytensors_amd.build"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    names = declared_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_version_queries():
+    lib = _lib.load()
+    assert lib.pt_abi_version() == _lib.ABI_VERSION
+    assert lib.pt_max_degree() == 8
+
+
+def _vpp(n):
+    return (ctypes.c_void_p * n)(*([1 << 20] * n))
+
+
+@pytest.mark.parametrize("entry,args,status,needle", [
+    ("pt_rms_norm_series_fwd", lambda: (0, 9, _vpp(10), None, 0, _vpp(10), 4, 8, 1e-5, None), 2, "degree"),
+    ("pt_rms_norm_series_fwd", lambda: (7, 1, _vpp(2), None, 0, _vpp(2), 4, 8, 1e-5, None), 2, "dtype"),
+    ("pt_rms_norm_series_fwd", lambda: (0, 1, None, None, 0, _vpp(2), 4, 8, 1e-5, None), 1, "required"),
+    ("pt_rms_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 3, _vpp(2), 4, 8, 1e-5, None), 1, "weight_orders"),
+    ("pt_layer_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 0, None, 1, _vpp(2), 4, 8, 1e-5, None), 1, "bias"),
+    ("pt_rms_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 0, _vpp(2), 4, 0, 1e-5, None), 1, "n >= 1"),
+])
+def test_argument_errors_return_before_launch(entry, args, status, needle):
+    lib = _lib.load()
+    got = getattr(lib, entry)(*args())
+    assert got == status
+    assert needle in lib.pt_last_error().decode()
+
+
+def test_empty_rows_is_a_no_op():
+    lib = _lib.load()
+    assert lib.pt_rms_norm_series_fwd(0, 2, _vpp(3), None, 0, _vpp(3), 0, 16, 1e-5, None) == 0
+    assert lib.pt_last_error().decode() == ""
