@@ -1,0 +1,26 @@
+// Launch interface of the cross-entropy series kernels (definitions in cross_entropy_series.inl).
+#pragma once
+
+#include "pt_common.h"
+
+namespace pt {
+
+struct CeArgs {
+  int degree;
+  const void* const* z;
+  int64_t rows;
+  int64_t classes;
+  int64_t row_stride;
+  const int64_t* target;
+  int64_t ignore_index;
+  int reduction;
+  void* const* loss;
+  void* const* lse;
+  void* workspace;
+  hipStream_t stream;
+};
+
+template <typename T>
+int launch_ce(const CeArgs& a);
+
+}  // namespace pt

@@ -1,0 +1,6 @@
+// Instantiates the cross-entropy series kernels for one storage type.
+#include "cross_entropy_series.inl"
+
+namespace pt {
+template int launch_ce<double>(const CeArgs&);
+}  // namespace pt

@@ -311,7 +311,9 @@ static int launch_norm_k(const NormArgs& a) {
       }
     }
     if (chunks > 0) {
-      const int tpr = static_cast<int>(((vecs + chunks - 1) / chunks + kWave - 1) / kWave * kWave);
+      int tpr = static_cast<int>(((vecs + chunks - 1) / chunks + kWave - 1) / kWave * kWave);
+      // Several rows share a 256-thread block only when tpr divides it.
+      if (tpr > kWave && tpr < 256) tpr = tpr <= 128 ? 128 : 256;
       const int threads = tpr >= 256 ? tpr : 256;
       const int64_t rows_per_block = threads / tpr;
       const int64_t grid = (a.rows + rows_per_block - 1) / rows_per_block;

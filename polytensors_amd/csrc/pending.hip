@@ -3,15 +3,6 @@
 
 extern "C" {
 
-int pt_cross_entropy_series_fwd(int, int, const void* const*, int64_t, int64_t, int64_t,
-                                const int64_t*, int64_t, int, void* const*, void* const*, void*,
-                                void*) {
-  pt_host::set_error("cross-entropy series kernel not built");
-  return PT_UNSUPPORTED;
-}
-
-size_t pt_cross_entropy_series_workspace_size(int, int, int64_t, int) { return 0; }
-
 int pt_cauchy_matmul(int, int, const void* const*, int, const void* const*, int, void* const*,
                      int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, void*) {
   pt_host::set_error("Cauchy matmul kernel not built");

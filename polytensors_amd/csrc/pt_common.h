@@ -144,3 +144,10 @@ inline bool aligned16(const void* p) {
       return PT_DEVICE_ERROR;                                               \
     }                                                                       \
   } while (0)
+
+namespace pt {
+// exp on the hardware exp2 unit for float (relative error of a few ulp plus
+// |x| * 2^-24 from rounding x * log2(e)); the accurate routine for double.
+__device__ __forceinline__ float exp_fast(float x) { return __expf(x); }
+__device__ __forceinline__ double exp_fast(double x) { return exp(x); }
+}  // namespace pt

@@ -1,0 +1,130 @@
+"""Cross-entropy series kernel vs the CPU oracle (GPU).
+
+Mirrors the reference's fused cross-entropy tests
+(/root/reference/tests/test_fused_kernels.py:142-181): N=300, C=5000 logits with
+every 7th target ignored, all three reductions, F.cross_entropy inside
+plain_range() taking the fused path. The oracle (log-softmax series + per-order
+NLL) runs in float64 on the same (upcast) inputs. Per-order tolerance
+max|got - want| / max|want|: 1e-10 float64, 1e-4 float32, 2e-2 bfloat16/float16.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from oracle import paths
+from polytensors_amd import PolyTensor, _fused_cross_entropy, _ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-10, torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _logits(N, C, degree, seed, dtype, base_scale=3.0, pad=0):
+    g = torch.Generator().manual_seed(seed)
+    full = [(torch.randn(N, C + pad, generator=g, dtype=torch.float64) * (base_scale if k == 0 else 0.5 ** k))
+            .to(dtype) for k in range(degree + 1)]
+    target = torch.randint(0, C, (N,), generator=g)
+    return full, target
+
+
+def _check(got, want, dtype, inputs=None):
+    # max |got - want| / max |want|. A loss coefficient is lse_k - z_k[y]; when it vanishes
+    # identically (one class) both results are the rounding of cancelling O(|z_k|) terms, so the
+    # scale is floored at the order's input scale max |z_k| when the inputs are given.
+    for k, (a, b) in enumerate(zip(got, want)):
+        a, b = a.cpu().double(), b.double()
+        scale = b.abs().max().item()
+        if inputs is not None:
+            scale = max(scale, inputs[k].double().abs().max().item())
+        err = (a - b).abs().max().item() / scale
+        assert err <= TOL[dtype], f"order {k}: {err:.3e}"
+
+
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("degree", [1, 4])
+def test_matches_oracle_with_ignored_rows(monkeypatch, reduction, degree):
+    calls = []
+    original = _ops.cross_entropy_series
+    monkeypatch.setattr(_ops, "cross_entropy_series", lambda *a, **k: calls.append(1) or original(*a, **k))
+    Z, y = _logits(300, 5000, degree, seed=0, dtype=torch.float32)
+    y[::7] = -1
+    logits = PolyTensor(tuple(c.cuda() for c in Z))
+    with torch.no_grad(), PolyTensor.plain_range():
+        assert _fused_cross_entropy.eligible(logits, y.cuda(), None, reduction, 0.0)
+        loss = F.cross_entropy(logits, y.cuda(), ignore_index=-1, reduction=reduction)
+    assert calls == [1]
+    assert loss.dtype == torch.float32 and loss.degree == degree
+    want = oracle.cross_entropy([c.double() for c in Z], y, ignore_index=-1, reduction=reduction)
+    _check(loss.coeffs, want, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("degree", [0, 2, 3, 5, 8])
+def test_dtypes_and_degrees(dtype, degree):
+    Z, y = _logits(64, 1000, degree, seed=1, dtype=dtype)
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = PolyTensor.cross_entropy(PolyTensor(tuple(c.cuda() for c in Z)), y.cuda(), reduction="none")
+    assert loss.dtype == torch.promote_types(dtype, torch.float32)   # PolyTensor.cross_entropy: at least float32
+    want = oracle.cross_entropy([c.double() for c in Z], y, reduction="none")
+    _check(loss.coeffs, want, dtype)
+
+
+@pytest.mark.parametrize("C,pad", [(3000, 64), (777, 0), (5, 3), (1, 0), (257, 1), (40000, 0)])
+def test_row_strides_and_class_counts(C, pad):
+    # a sliced (padded) row stride stays a zero-copy view; odd strides take the scalar path
+    degree = 3
+    full, y = _logits(50, C, degree, seed=2, dtype=torch.float32, pad=pad)
+    dev = [c.cuda() for c in full]
+    logits = PolyTensor(tuple(c[:, :C] for c in dev))
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = F.cross_entropy(logits, y.cuda(), reduction="none")
+    want = oracle.cross_entropy([c[:, :C].double() for c in full], y, reduction="none")
+    _check(loss.coeffs, want, torch.float32, inputs=[c[:, :C] for c in full])
+
+
+def test_lse_series_output():
+    degree = 4
+    Z, y = _logits(40, 2000, degree, seed=3, dtype=torch.float32)
+    _, lse = _ops.cross_entropy_series([c.cuda() for c in Z], y.cuda(), -100, 0)
+    want = paths.logsumexp([c.double() for c in Z], 1)
+    _check(list(lse.unbind(0)), want, torch.float32)
+
+
+def test_all_ignored_mean_is_nan_like_torch():
+    Z, y = _logits(8, 100, 2, seed=4, dtype=torch.float32)
+    y[:] = -100
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = F.cross_entropy(PolyTensor(tuple(c.cuda() for c in Z)), y.cuda())
+    native = F.cross_entropy(Z[0], y)
+    assert math.isnan(native.item())
+    assert all(torch.isnan(c).item() for c in loss.coeffs)
+
+
+def test_large_common_offset_keeps_higher_orders_exact():
+    # /root/reference/tests/test_series.py:113-120 through the kernel: logits 1e20 + t.
+    base = torch.full((3, 2), 1e20, dtype=torch.float32)
+    coeffs = (base, torch.ones_like(base), *(torch.zeros_like(base) for _ in range(3)))
+    _, lse = _ops.cross_entropy_series([c.cuda() for c in coeffs], torch.zeros(3, dtype=torch.int64).cuda(), -100, 0)
+    lse = lse.cpu()
+    assert torch.equal(lse[1], torch.ones(3))
+    assert torch.equal(lse[2:], torch.zeros(3, 3))
+
+
+def test_full_size_config_rows_sample():
+    # BASELINE config 4b: [5, 8192, 32000] fp32, base N(0, 2^2), order k N(0,1) 0.5^k; the mean must
+    # equal the mean of the per-row losses, and a seeded sample of rows must match the oracle.
+    degree, N, C = 4, 8192, 32000
+    g = torch.Generator(device="cuda").manual_seed(4)
+    Z = [torch.randn(N, C, generator=g, device="cuda") * (2.0 if k == 0 else 0.5 ** k) for k in range(degree + 1)]
+    y = torch.randint(0, C, (N,), generator=g, device="cuda")
+    rows, _ = _ops.cross_entropy_series(Z, y, -100, 0)
+    mean, _ = _ops.cross_entropy_series(Z, y, -100, 1)
+    for k in range(degree + 1):
+        assert abs(mean[k].item() - rows[k].double().mean().item()) <= 1e-5 * max(1.0, abs(mean[k].item()))
+    pick = torch.randperm(N, generator=torch.Generator().manual_seed(5))[:32].cuda()
+    want = oracle.cross_entropy([c[pick].cpu().double() for c in Z], y[pick].cpu(), reduction="none")
+    _check([r[pick] for r in rows], want, torch.float32)
