@@ -3,12 +3,6 @@
 
 extern "C" {
 
-int pt_cauchy_matmul(int, int, const void* const*, int, const void* const*, int, void* const*,
-                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, void*) {
-  pt_host::set_error("Cauchy matmul kernel not built");
-  return PT_UNSUPPORTED;
-}
-
 int pt_taylor_attention_fwd(int, int, const void* const*, int, const void* const*, int,
                             const void* const*, int, void* const*, void* const*, int64_t, int64_t,
                             int64_t, int64_t, int, const uint8_t*, double, void*) {
