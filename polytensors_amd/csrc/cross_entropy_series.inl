@@ -31,7 +31,7 @@ __device__ __forceinline__ void accumulate_element(A x0, const A (&xk)[K + 1], A
     A s = A(0);
 #pragma unroll
     for (int i = 1; i <= k; ++i) s += (A(i) * xk[i]) * e[k - i];
-    e[k] = s / A(k);
+    e[k] = s * (A(1) / A(k));   // a compile-time reciprocal, not a division
   }
   S[0] += p;
 #pragma unroll

@@ -1,0 +1,380 @@
+// Flash-style attention forward of degree-K series on MFMA (gfx950).
+//
+// Per query row, with score series S(t) = scale Q(t) K(t)^T:
+//   exp(S(t)) = exp(S_0) e(t),  e_0 = 1,  e_k = sum_{j=1..k} (j/k) S_j e_{k-j}
+// (the exponential-series recurrence of /root/reference/src/polytensors/_plain.py:153-159),
+//   l_k = sum_keys exp(S_0 - m) e_k,   N_k = sum_keys sum_{a+b=k} exp(S_0 - m) e_a V_b,
+//   O(t) = N(t) / l(t):  O_0 = N_0 / l_0,  O_k = (N_k - sum_{j=1..k} l_j O_{k-j}) / l_0,
+// which equals softmax(S(t)) V(t) of the reference's decomposition
+// (/root/reference/src/polytensors/_decompositions.py:28-43) since the softmax
+// series is exp(S(t)) divided by its row sum. The running maximum m uses the
+// constant order only and is raised lazily (only when a block's maximum
+// exceeds it by more than kRescaleSlack), rescaling l and N by exp(m_old - m_new).
+//
+// Work decomposition: a workgroup of 4 waves owns 64 query rows of one (batch,
+// head); each wave owns 16 queries. Key blocks of 16 keys of every order of K
+// and V are staged in LDS. Scores are formed transposed, S^T = K Q^T, with
+// 16x16x4 MFMAs (keys on the M side, queries on the N side, head dim
+// contracted): the accumulator then holds, per lane, one query column and four
+// keys, which is exactly the B operand layout of the value product
+// O^T = V^T P^T. So the exponential series is computed in place in the score
+// accumulators and fed straight to the PV MFMAs: P never leaves registers.
+// Query operands are read from global memory (L2-resident) per 16-wide
+// head-dim chunk; within a chunk the head-dim index is permuted so that a lane
+// reads its 4 operand values with one 16-byte load (same permutation on K).
+// The output accumulators O^T_k (16 head-dim rows x 16 queries per MFMA block)
+// stay in registers for the whole key loop.
+#pragma once
+
+#include "mfma.h"
+#include "taylor_attention.h"
+
+namespace pt {
+
+// 16x16x4 MFMA for float (fp32) and double (fp64): same shape, different accumulator layouts.
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<float> {
+  using acc_t = floatx4;
+  __device__ __forceinline__ static acc_t zero() { return acc_t{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ static acc_t mma(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  // accumulator register r of lane l: row 4 (l/16) + r, column l % 16
+  __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * h + r; }
+};
+
+template <>
+struct Mfma16<double> {
+  using acc_t = doublex4;
+  __device__ __forceinline__ static acc_t zero() { return acc_t{0.0, 0.0, 0.0, 0.0}; }
+  __device__ __forceinline__ static acc_t mma(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  // accumulator register r of lane l: row 4 r + l/16, column l % 16
+  __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * r + h; }
+};
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnQPerWave = 16;
+constexpr int kAttnBM = kAttnWaves * kAttnQPerWave;   // query rows per workgroup
+constexpr int kAttnBN = 16;                           // keys per block
+
+template <typename T>
+struct AttnRescale {
+  static constexpr float value = 8.0f;   // lazy-rescale slack (natural-log units): p <= e^8
+};
+
+template <typename T, int K, int D>
+struct AttnShape {
+  // Row stride of the staged K/V tiles: D + 4 values. For floats that is 4 mod 64
+  // banks, so the 16 key rows of a 16-byte K-operand read and the 4 key rows of
+  // a V-operand read fall on distinct banks; for doubles it keeps rows 32-byte aligned.
+  static constexpr int LD = D + 4;
+  static constexpr size_t LDS = 2ull * (K + 1) * kAttnBN * LD * sizeof(T);
+  static constexpr bool fits = LDS <= 160 * 1024;
+};
+
+template <typename T, int K, int D>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
+    CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
+    MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask, int causal,
+    typename AccOf<T>::type scale) {
+  using A = typename AccOf<T>::type;
+  using MF = Mfma16<T>;
+  using acc_t = typename MF::acc_t;
+  using Shape = AttnShape<T, K, D>;
+  constexpr int LD = Shape::LD;
+  constexpr int DB = D / 16;                  // 16-wide head-dim chunks / output blocks
+  constexpr int V = 16 / sizeof(T);           // values per 16-byte load
+  constexpr int QV = 4;                       // operand values per lane per 16-wide chunk
+  constexpr A kNegInf = -__builtin_huge_val();
+  constexpr A kSlack = AttnRescale<T>::value;
+  static_assert(Shape::fits, "K/V tiles exceed LDS");
+
+  __shared__ T Ks[K + 1][kAttnBN][LD];
+  __shared__ T Vs[K + 1][kAttnBN][LD];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;        // query column of this lane (and key row for K operands)
+  const int h = lane / 16;        // lane group
+  const int64_t head = blockIdx.y;
+  const int q_block = blockIdx.x * kAttnBM;
+  const int q0 = q_block + wave * kAttnQPerWave;
+  const int my_q = q0 + c;
+  const bool q_ok = my_q < L;
+
+  // Every pair (a, b) runs unconditionally: an operand with fewer orders reads
+  // zeros for the missing ones (selected after a load from a valid address), so
+  // no branch splits the MFMA sequence.
+  const T* qrow[K + 1];
+  bool q_live[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    q_live[o] = q_ok && o < q_orders;
+    qrow[o] = Q.p[o < q_orders ? o : 0] + (head * L + (q_ok ? my_q : 0)) * D;
+  }
+
+  acc_t acc_o[K + 1][DB];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[o][db] = MF::zero();
+  A m_used = kNegInf;
+  A lsum[K + 1];   // per-lane partial row sums (this lane's keys only)
+#pragma unroll
+  for (int o = 0; o <= K; ++o) lsum[o] = A(0);
+
+  int hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+
+  for (int kb0 = 0; kb0 < hi; kb0 += kAttnBN) {
+    __syncthreads();
+    // ---- stage K and V rows kb0 .. kb0+15 of every order (zero past S) ----
+    {
+      constexpr int VPR = D / V;   // 16-byte vectors per row
+      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
+        const int o = idx / (kAttnBN * VPR);
+        const int rem = idx % (kAttnBN * VPR);
+        const int r = rem / VPR, cv = (rem % VPR) * V;
+        const int key = kb0 + r;
+        Vec<T, V> kx, vx;
+        const bool kin = key < S && o < k_orders;
+        const bool vin = key < S && o < v_orders;
+        if (kin) {
+          kx = load_vec<T, V>(Kp.p[o] + (head * S + key) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) kx.v[e] = T(0);
+        }
+        if (vin) {
+          vx = load_vec<T, V>(Vp.p[o] + (head * S + key) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) vx.v[e] = T(0);
+        }
+        store_vec<T, V>(&Ks[o][r][cv], kx);
+        store_vec<T, V>(&Vs[o][r][cv], vx);
+      }
+    }
+    __syncthreads();
+
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T (keys x queries) ----
+    acc_t sc[K + 1];
+#pragma unroll
+    for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
+    // Not unrolled: no register array is indexed by dc, and a rolled loop keeps
+    // the code (and compile time) of the high-degree instantiations small.
+#pragma unroll 1
+    for (int dc = 0; dc < DB; ++dc) {
+      // lane operands: K[key = c][d = 16 dc + 4 h + s], Q[my_q][same d], s = 0..3
+      Vec<T, QV> qa[K + 1], kb[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(qrow[o] + dc * 16 + 4 * h);
+#pragma unroll
+        for (int e = 0; e < QV; ++e) qa[o].v[e] = q_live[o] ? qa[o].v[e] : T(0);
+        kb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Ks[o][c][dc * 16 + 4 * h]);
+      }
+#pragma unroll
+      for (int s = 0; s < QV; ++s) {
+#pragma unroll
+        for (int k = 0; k <= K; ++k) {
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MF::mma(kb[k - a].v[s], qa[a].v[s], sc[k]);
+        }
+      }
+    }
+
+    // ---- mask, online maximum of the constant order, exponential series ----
+    bool valid[4];
+    A s0[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kb0 + MF::acc_row(h, r);
+      bool ok = q_ok && key < S;
+      if (causal) ok = ok && key <= my_q;
+      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+      valid[r] = ok;
+      s0[r] = ok ? static_cast<A>(sc[0][r]) * scale : kNegInf;
+    }
+    A bmax = fmax(fmax(s0[0], s0[1]), fmax(s0[2], s0[3]));
+    bmax = fmax(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmax(bmax, __shfl_xor(bmax, 32, kWave));
+    const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
+    if (__any(raise)) {
+      const A m_new = raise ? bmax : m_used;
+      const A alpha = (raise && m_used != kNegInf) ? exp_fast(m_used - m_new) : (raise ? A(0) : A(1));
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        lsum[o] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+      }
+      m_used = m_new;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const A p = valid[r] ? exp_fast(s0[r] - m_used) : A(0);
+      A sk[K + 1], e[K + 1];
+#pragma unroll
+      for (int o = 1; o <= K; ++o) sk[o] = static_cast<A>(sc[o][r]) * scale;
+      e[0] = A(1);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A t = A(0);
+#pragma unroll
+        for (int j = 1; j <= k; ++j) t += (A(j) * sk[j]) * e[k - j];
+        e[k] = t * (A(1) / A(k));   // a compile-time reciprocal, not a division
+      }
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const A w = p * e[o];
+        lsum[o] += w;
+        sc[o][r] = static_cast<T>(w);
+      }
+    }
+
+    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T (head dim x queries) ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key_row = MF::acc_row(h, s);   // key held in score register s by this lane group
+        T vb[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) vb[o] = Vs[o][key_row][db * 16 + c];
+#pragma unroll
+        for (int k = 0; k <= K; ++k) {
+#pragma unroll
+          for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: full row sums, series quotient O = N / l, lse series ----
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  }
+  if (!q_ok) return;
+  const bool empty = !(lsum[0] > A(0));
+  const A inv_l0 = empty ? A(0) : A(1) / lsum[0];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    A out[4][K + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+        A t = static_cast<A>(acc_o[k][db][r]);
+#pragma unroll
+        for (int j = 1; j <= k; ++j) t -= lsum[j] * out[r][k - j];
+        out[r][k] = t * inv_l0;
+      }
+    }
+    T* orow = nullptr;
+#pragma unroll
+    for (int k = 0; k <= K; ++k) {
+      orow = O.p[k] + (head * L + my_q) * D + db * 16;
+      if constexpr (sizeof(T) == 4) {
+        // fp32 layout: registers r = 0..3 hold head-dim columns 4h + r: one 16-byte store
+        Vec<T, 4> w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w.v[r] = static_cast<T>(out[r][k]);
+        store_vec<T, 4>(orow + 4 * h, w);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) orow[MF::acc_row(h, r)] = static_cast<T>(out[r][k]);
+      }
+    }
+  }
+  if (LSE.p[0] != nullptr && h == 0) {
+    const int64_t at = head * L + my_q;
+    if (empty) {
+      LSE.p[0][at] = __builtin_huge_val();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][at] = A(0);
+    } else {
+      A lse[K + 1], nrm[K + 1];
+      lse[0] = m_used + log_acc(lsum[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A t = nrm[k];
+#pragma unroll
+        for (int j = 1; j < k; ++j) t -= (A(j) / A(k)) * lse[j] * nrm[k - j];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+    }
+  }
+}
+
+template <typename T, int K, int D>
+static int launch_attention_kd(const AttnArgs& a) {
+  using A = typename AccOf<T>::type;
+  if constexpr (!AttnShape<T, K, D>::fits) {
+    pt_host::set_error("Taylor attention: degree and head dim exceed the LDS budget for this dtype");
+    return PT_UNSUPPORTED;
+  } else {
+    CPtrs<T> q{}, k{}, v{};
+    MPtrs<T> o{};
+    MPtrs<A> lse{};
+    for (int i = 0; i < a.q_orders; ++i) q.p[i] = static_cast<const T*>(a.q[i]);
+    for (int i = 0; i < a.k_orders; ++i) k.p[i] = static_cast<const T*>(a.k[i]);
+    for (int i = 0; i < a.v_orders; ++i) v.p[i] = static_cast<const T*>(a.v[i]);
+    for (int i = 0; i <= K; ++i) {
+      o.p[i] = static_cast<T*>(a.out[i]);
+      if (a.lse != nullptr) lse.p[i] = static_cast<A*>(a.lse[i]);
+    }
+    const dim3 grid((a.lq + kAttnBM - 1) / kAttnBM, a.bh);
+    taylor_attention_fwd_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+        q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
+        static_cast<int>(a.lk), a.mask, a.causal ? 1 : 0, static_cast<A>(a.scale));
+    PT_LAUNCH_CHECK();
+    return PT_OK;
+  }
+}
+
+template <typename T, int K>
+static int launch_attention_k(const AttnArgs& a) {
+  switch (a.d) {
+    case 16: return launch_attention_kd<T, K, 16>(a);
+    case 32: return launch_attention_kd<T, K, 32>(a);
+    case 64: return launch_attention_kd<T, K, 64>(a);
+    case 128: return launch_attention_kd<T, K, 128>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention: head dim must be 16, 32, 64 or 128");
+  return PT_UNSUPPORTED;
+}
+
+template <typename T>
+int launch_attention(const AttnArgs& a) {
+  switch (a.degree) {
+    case 0: return launch_attention_k<T, 0>(a);
+    case 1: return launch_attention_k<T, 1>(a);
+    case 2: return launch_attention_k<T, 2>(a);
+    case 3: return launch_attention_k<T, 3>(a);
+    case 4: return launch_attention_k<T, 4>(a);
+    case 5: return launch_attention_k<T, 5>(a);
+    case 6: return launch_attention_k<T, 6>(a);
+    case 7: return launch_attention_k<T, 7>(a);
+    case 8: return launch_attention_k<T, 8>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention: degree outside 0..PT_MAX_DEGREE");
+  return PT_UNSUPPORTED;
+}
+
+}  // namespace pt

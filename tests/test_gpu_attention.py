@@ -1,0 +1,186 @@
+"""Taylor flash-attention kernel vs the CPU oracle (GPU).
+
+Mirrors the reference's fused-attention tests (/root/reference/tests/test_fused_kernels.py:48-134):
+shape (2, 3, 150, 64), causal, a window-37 boolean mask and unmasked, explicit
+scale, plain operands, F.scaled_dot_product_attention inside plain_range()
+taking the fused path, here at degrees up to 8. The oracle is the reference's
+plain-range decomposition (softmax series of the masked Cauchy-product scores,
+then the Cauchy product with V) in float64 on the same (upcast) inputs.
+Per-order tolerance max|got - want| / max|want|: 1e-10 float64, 1e-4 float32.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from oracle import paths, series
+from polytensors_amd import PolyTensor, _fused_attention, _ops
+from tests.jets import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-10, torch.float32: 1e-4}
+
+
+def _series(shape, degree, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(shape, generator=g, dtype=torch.float64) * scale * 0.5 ** k).to(dtype)
+            for k in range(degree + 1)]
+
+
+def _poly(cs):
+    return PolyTensor(tuple(c.cuda() for c in cs))
+
+
+def _window_mask(L, window):
+    i = torch.arange(L)
+    return (i[:, None] >= i[None, :]) & (i[:, None] - i[None, :] <= window)
+
+
+def _check(got, want, dtype):
+    for k, (a, b) in enumerate(zip(got, want)):
+        err = rel_err(a.cpu(), b)
+        assert err <= TOL[dtype], f"order {k}: {err:.3e}"
+
+
+def _run(q, k, v, **kwargs):
+    with torch.no_grad(), PolyTensor.plain_range():
+        return F.scaled_dot_product_attention(q, k, v, **kwargs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("causal,window", [(True, None), (False, 37), (False, None)])
+@pytest.mark.parametrize("degree", [1, 4])
+def test_matches_oracle(monkeypatch, dtype, causal, window, degree):
+    calls = []
+    original = _ops.taylor_attention_fwd
+    monkeypatch.setattr(_ops, "taylor_attention_fwd", lambda *a, **k: calls.append(1) or original(*a, **k))
+    shape = (2, 3, 150, 64)
+    Q, K, V = (_series(shape, degree, 10 + i, dtype) for i in range(3))
+    mask = None if window is None else _window_mask(150, window)
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=None if mask is None else mask.cuda(), is_causal=causal)
+    assert calls == [1] and out.degree == degree and out.dtype == dtype
+    want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                            attn_mask=mask, is_causal=causal)
+    _check(out.coeffs, want, dtype)
+
+
+@pytest.mark.parametrize("degree", [0, 2, 3, 5, 6, 7, 8])
+@pytest.mark.parametrize("d", [16, 32, 128])
+def test_every_degree_and_head_dim(degree, d):
+    shape = (1, 2, 70, d)
+    Q, K, V = (_series(shape, degree, 20 + i, torch.float32) for i in range(3))
+    out = _run(_poly(Q), _poly(K), _poly(V), is_causal=True)
+    want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V], is_causal=True)
+    _check(out.coeffs, want, torch.float32)
+
+
+def test_scale_argument_and_default():
+    shape = (1, 2, 40, 64)
+    Q, K, V = (_series(shape, 3, 30 + i, torch.float64) for i in range(3))
+    out = _run(_poly(Q), _poly(K), _poly(V), is_causal=True, scale=0.3)
+    want = oracle.attention([c for c in Q], [c for c in K], [c for c in V], is_causal=True, scale=0.3)
+    _check(out.coeffs, want, torch.float64)
+    assert math.isclose(_fused_attention.default_scale(64), 0.125)
+
+
+def test_plain_operands():
+    # /root/reference/tests/test_fused_kernels.py:112-122: an ordinary key tensor has a zero tangent
+    shape = (2, 2, 64, 32)
+    Q, V = _series(shape, 2, 40, torch.float64), _series(shape, 2, 41, torch.float64)
+    k = torch.randn(shape, generator=torch.Generator().manual_seed(42), dtype=torch.float64)
+    out = _run(_poly(Q), k.cuda(), _poly(V), is_causal=True)
+    want = oracle.attention(Q, [k], V, is_causal=True)
+    _check(out.coeffs, want, torch.float64)
+
+
+def test_cross_attention_lengths():
+    Q = _series((1, 2, 50, 64), 3, 43, torch.float32)
+    K, V = _series((1, 2, 90, 64), 3, 44, torch.float32), _series((1, 2, 90, 64), 3, 45, torch.float32)
+    for causal in (False, True):
+        out = _run(_poly(Q), _poly(K), _poly(V), is_causal=causal)
+        want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                                is_causal=causal)
+        _check(out.coeffs, want, torch.float32)
+
+
+def test_fully_masked_row_is_zero_with_infinite_lse():
+    # The reference's fused kernel convention (/root/reference/src/polytensors/_attention_kernels.py:70-76):
+    # a row with no admissible key gets output zero and lse = +inf.
+    L = 24
+    Q, K, V = (_series((1, 1, L, 32), 2, 50 + i, torch.float64) for i in range(3))
+    mask = _window_mask(L, 3)
+    mask[5, :] = False
+    out, lse = _ops.taylor_attention_fwd([c.cuda().reshape(1, L, 32) for c in Q],
+                                         [c.cuda().reshape(1, L, 32) for c in K],
+                                         [c.cuda().reshape(1, L, 32) for c in V], mask.cuda(), False, 0.2, 2)
+    assert torch.equal(out[:, 0, 5].cpu(), torch.zeros(3, 32, dtype=torch.float64))
+    assert lse[0, 0, 5].item() == math.inf and lse[1:, 0, 5].abs().max().item() == 0
+    keep = torch.ones(L, dtype=torch.bool)
+    keep[5] = False
+    want = oracle.attention(Q, K, V, attn_mask=mask, scale=0.2)
+    _check([o[0][keep] for o in out], [w[0, 0][keep] for w in want], torch.float64)
+
+
+def test_lse_series_output():
+    L, d, degree = 48, 64, 3
+    Q, K, V = (_series((1, 1, L, d), degree, 60 + i, torch.float64) for i in range(3))
+    _, lse = _ops.taylor_attention_fwd([c.cuda().reshape(1, L, d) for c in Q], [c.cuda().reshape(1, L, d) for c in K],
+                                       [c.cuda().reshape(1, L, d) for c in V], None, True, 0.125, degree)
+    scores = series.cauchy([q * 0.125 for q in Q], [k.transpose(-2, -1) for k in K], matmul=True)
+    excluded = ~torch.ones(L, L, dtype=torch.bool).tril()
+    scores = [torch.where(excluded, torch.tensor(-math.inf if o == 0 else 0.0, dtype=torch.float64), s)
+              for o, s in enumerate(scores)]
+    want = paths.logsumexp(scores, -1)
+    _check([x.reshape(1, 1, L) for x in lse.unbind(0)], want, torch.float64)
+
+
+def test_config1_fp64_attention_and_projected_cross_entropy():
+    # K=3, fp64, Q/K/V [1,1,128,64] = x + t v with x, v ~ N(0,1)/8 (seed 0), causal;
+    # logits = out.view(128, 64) @ W with W ~ N(0,1)/8 [64, 256], integer targets in [0, 256), mean CE.
+    g = torch.Generator().manual_seed(0)
+    shape = (1, 1, 128, 64)
+    lines = [(torch.randn(shape, generator=g, dtype=torch.float64) / 8,
+              torch.randn(shape, generator=g, dtype=torch.float64) / 8) for _ in range(3)]
+    W = torch.randn(64, 256, generator=g, dtype=torch.float64) / 8
+    y = torch.randint(0, 256, (128,), generator=g)
+    q, k, v = (PolyTensor((x.cuda(), d.cuda()), degree=3) for x, d in lines)
+    with torch.no_grad(), PolyTensor.plain_range():
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        logits = out.reshape(128, 64) @ W.cuda()
+        loss = F.cross_entropy(logits, y.cuda())
+    Qs, Ks, Vs = (paths.lift([x, d], 3) for x, d in lines)
+    want = oracle.attention(Qs, Ks, Vs, is_causal=True)
+    _check(out.coeffs, want, torch.float64)
+    want_logits = oracle.matmul([w.reshape(128, 64) for w in want], [W])
+    _check(logits.coeffs, want_logits, torch.float64)
+    want_loss = oracle.cross_entropy(want_logits, y)
+    for k_, (a, b) in enumerate(zip(loss.coeffs, want_loss)):
+        assert abs(a.item() - b.item()) <= 1e-10 * max(1.0, abs(b.item())), k_
+
+
+def test_full_size_config3_one_head():
+    # B=4 H=16 L=2048 d=128, K=4, fp32, causal; line inputs (x + t v). One (b, h) of
+    # the full launch is checked against the oracle; every head's order-0 output is checked against
+    # torch's own fp32 attention (the ordinary softmax attention that order 0 equals).
+    B, H, L, d, degree = 4, 16, 2048, 128, 4
+    g = torch.Generator(device="cuda").manual_seed(2)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device="cuda") / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device="cuda")
+        return [base, direction] + [torch.zeros_like(base) for _ in range(degree - 1)]
+
+    q, k, v = line(), line(), line()
+    out, _ = _ops.taylor_attention_fwd(q, k, v, None, True, 1 / math.sqrt(d), degree)
+    head = 37
+    want = oracle.attention([c[head].cpu().double() for c in q], [c[head].cpu().double() for c in k],
+                            [c[head].cpu().double() for c in v], is_causal=True)
+    _check([o[head] for o in out], want, torch.float32)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref0 = torch.softmax((q[0] @ k[0].transpose(-1, -2).contiguous() / math.sqrt(d)).masked_fill(
+        ~torch.ones(L, L, dtype=torch.bool, device="cuda").tril(), -math.inf), -1) @ v[0]
+    assert rel_err(out[0].cpu(), ref0.cpu()) <= 1e-4
