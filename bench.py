@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce]
-                    [--no-cpu-baseline] [--components]
+                    [--no-cpu-baseline] [--no-components] [--copy-calibration]
 
 One step is one launch of the workload's fused kernel on one batch of synthetic
 input already resident in HBM (inputs are generated on the device with a
@@ -149,16 +149,21 @@ def _cpu_time(fn, reps=3):
     return times[len(times) // 2]
 
 
-def cpu_attention(L, d, K):
+def cpu_attention(L, d, K, heads=64):
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(2)
     q, k, v = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(3))
-    t = _cpu_time(lambda: oracle.attention(q, k, v, is_causal=True), reps=1)
-    flops = 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
-    return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"1 of 64 (b,h) heads, L={L} d={d} K={K} fp32 causal",
-                seconds=t)
+
+    def all_heads():   # one head at a time (the L x L series of all heads would not fit in host memory)
+        for _ in range(heads):
+            oracle.attention(q, k, v, is_causal=True)
+
+    t = _cpu_time(all_heads, reps=1)
+    flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
+    return dict(value=flops / t / 1e12, unit="TFLOP/s",
+                sample=f"all {heads} (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
 
 
 def cpu_matmul(n, K):
@@ -202,6 +207,18 @@ def cpu_ce(rows, classes, K):
 
 # ---------------------------------------------------------------------------
 
+def profiled_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this workload, if any."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_bench.txt")
+    try:
+        for line in open(path):
+            if line.startswith("HBM traffic per launch"):
+                return float(line.rsplit("=", 1)[1].split()[0]) * 1e6
+    except OSError:
+        pass
+    return None
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -231,8 +248,10 @@ def main():
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="attention", choices=sorted(WORKLOADS))
-    parser.add_argument("--components", action="store_true", help="also time the other three kernels")
+    parser.add_argument("--no-components", action="store_true", help="skip timing the other three kernels")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a plain 1 GiB device copy (scales rocprof FETCH_SIZE/WRITE_SIZE)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the Taylor kernels are single-GPU "
@@ -243,6 +262,13 @@ def main():
 
     torch.backends.cuda.matmul.allow_tf32 = False
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, device=device)          # 1 GiB of float32
+        dst = torch.empty_like(src)
+        ms = time_steps(lambda: dst.copy_(src), max(1, args.steps), args.warmup)
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "ms": round(ms, 4),
+                          "GB/s": round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
     w = measure(args.workload, device, args.steps, args.warmup)
     line = {
         "metric": METRIC,
@@ -259,9 +285,10 @@ def main():
         "data": "synthetic (seeded torch.randn on device)",
         "config": {"workload": w["workload"], "parallelism": "none (1 GPU)"},
         "roofline": {"bound": w["bound"], "achieved": round(w["achieved"], 3), "peak": w["peak"],
-                     "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4), "traffic": None},
+                     "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4),
+                     "traffic": profiled_traffic(w["kernel"])},
     }
-    if args.components:
+    if not args.no_components:
         comps = {}
         for name in sorted(WORKLOADS):
             if name == args.workload:

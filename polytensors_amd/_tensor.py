@@ -27,6 +27,30 @@ _coefficient_autograd_enabled = contextvars.ContextVar("polytensors_amd_coeffici
 _COMPLEX_OF = {torch.float16: torch.complex32, torch.float32: torch.complex64, torch.float64: torch.complex128}
 
 
+def _extent(t):
+    """[start, end) byte range of a strided tensor within its storage (conservative for gaps)."""
+    if t.numel() == 0:
+        return 0, 0
+    span = 1 + sum((n - 1) * abs(st) for n, st in zip(t.shape, t.stride()))
+    start = t.storage_offset() - sum((n - 1) * abs(st) for n, st in zip(t.shape, t.stride()) if st < 0)
+    size = t.element_size()
+    return start * size, (start + span) * size
+
+
+def _overlaps(a, b):
+    """Whether two coefficients may share memory.
+
+    ``torch._C._overlaps`` (which the reference uses, _tensor.py:93,124) reports any two views of
+    one storage as overlapping, so it would clone every order of a coefficient-stacked buffer.
+    This compares byte ranges instead: exact for the disjoint slices of a stacked [K+1, ...]
+    buffer, conservative for interleaved strided views.
+    """
+    if a.device != b.device or a.untyped_storage().data_ptr() != b.untyped_storage().data_ptr():
+        return False
+    (s0, e0), (s1, e1) = _extent(a), _extent(b)
+    return s0 < e1 and s1 < e0
+
+
 def _as_coefficient(value, like):
     if isinstance(value, torch.Tensor):
         return value
@@ -82,7 +106,7 @@ def _coerce_coeffs(coeffs, degree=None):
     # otherwise change another.
     kept = []
     for c in coeffs:
-        if any(torch._C._overlaps(c, other) for other in kept):
+        if any(_overlaps(c, other) for other in kept):
             c = c.clone()
         kept.append(c)
     return tuple(kept)
@@ -111,7 +135,7 @@ def _well_formed(coeffs):
             return False
     for i in range(1, len(coeffs)):
         for j in range(i):
-            if torch._C._overlaps(coeffs[i], coeffs[j]):
+            if _overlaps(coeffs[i], coeffs[j]):
                 return False
     return True
 
