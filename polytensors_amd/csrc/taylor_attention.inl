@@ -77,6 +77,92 @@ struct AttnShape {
   static constexpr bool fits = LDS <= 160 * 1024;
 };
 
+// Shared epilogue: row sums across the 4 lane groups, series quotient
+// O_k = (N_k - sum_{j=1..k} l_j O_{k-j}) / l_0, and the lse series.
+// Work item of a workgroup in a one-dimensional grid of (query blocks) x (heads).
+// Causal work grows with the query block, so the heaviest blocks are issued
+// first; consecutive workgroup ids go to consecutive XCDs, and taking the head
+// as the fast index gives every XCD an equal share of each query-block level
+// (the same eight-head residue class on each XCD, which also keeps its K/V
+// rows in that XCD's L2).
+__device__ __forceinline__ void attn_work_item(int L, int64_t& head, int& q_block) {
+  const int nqb = (L + kAttnBM - 1) / kAttnBM;
+  const int64_t bh = gridDim.x / nqb;
+  const int64_t t = blockIdx.x;
+  head = t % bh;
+  q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
+}
+
+template <typename T, int K, int D, typename AccT>
+__device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
+                                                   typename AccOf<T>::type (&lsum)[K + 1],
+                                                   typename AccOf<T>::type m_used, MPtrs<T>& O,
+                                                   MPtrs<typename AccOf<T>::type>& LSE, int64_t head,
+                                                   int L, int my_q, bool q_ok, int h) {
+  using A = typename AccOf<T>::type;
+  using MF = Mfma16<T>;
+  constexpr int DB = D / 16;
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  }
+  if (!q_ok) return;
+  const bool empty = !(lsum[0] > A(0));
+  const A inv_l0 = empty ? A(0) : A(1) / lsum[0];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    A out[4][K + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+        A t = static_cast<A>(acc_o[k][db][r]);
+#pragma unroll
+        for (int j = 1; j <= k; ++j) t -= lsum[j] * out[r][k - j];
+        out[r][k] = t * inv_l0;
+      }
+    }
+    T* orow = nullptr;
+#pragma unroll
+    for (int k = 0; k <= K; ++k) {
+      orow = O.p[k] + (head * L + my_q) * D + db * 16;
+      if constexpr (sizeof(T) == 4) {
+        // fp32 layout: registers r = 0..3 hold head-dim columns 4h + r: one 16-byte store
+        Vec<T, 4> w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w.v[r] = static_cast<T>(out[r][k]);
+        store_vec<T, 4>(orow + 4 * h, w);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) orow[MF::acc_row(h, r)] = static_cast<T>(out[r][k]);
+      }
+    }
+  }
+  if (LSE.p[0] != nullptr && h == 0) {
+    const int64_t at = head * L + my_q;
+    if (empty) {
+      LSE.p[0][at] = __builtin_huge_val();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][at] = A(0);
+    } else {
+      A lse[K + 1], nrm[K + 1];
+      lse[0] = m_used + log_acc(lsum[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A t = nrm[k];
+#pragma unroll
+        for (int j = 1; j < k; ++j) t -= (A(j) / A(k)) * lse[j] * nrm[k - j];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+    }
+  }
+}
+
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
@@ -101,8 +187,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
   const int wave = threadIdx.x / kWave;
   const int c = lane % 16;        // query column of this lane (and key row for K operands)
   const int h = lane / 16;        // lane group
-  const int64_t head = blockIdx.y;
-  const int q_block = blockIdx.x * kAttnBM;
+  int64_t head;
+  int q_block;
+  attn_work_item(L, head, q_block);
   const int q0 = q_block + wave * kAttnQPerWave;
   const int my_q = q0 + c;
   const bool q_ok = my_q < L;
@@ -258,66 +345,267 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     }
   }
 
-  // ---- epilogue: full row sums, series quotient O = N / l, lse series ----
+  attention_epilogue<T, K, D>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined fp32 kernel for full-order operands (every operand has K+1 orders),
+// key length a multiple of 16, and two K/V tiles within LDS:
+// * the K and V tiles of key block j+1 are fetched by LDS DMA
+//   (global_load_lds_dwordx4) into the second LDS buffer while block j's PV
+//   products run, so staging costs no registers and its latency hides behind
+//   MFMAs; one barrier per key block;
+// * tiles are stored unpadded with the 16-byte chunks of a key row XOR-swizzled
+//   by the row index (physical chunk = chunk ^ (row mod min(16, chunks))), which
+//   keeps both the 16-byte K-operand reads and the 4-byte V-operand reads free
+//   of bank conflicts;
+// * query and key operands of head-dim chunk dc+1 are loaded while chunk dc's
+//   MFMAs run;
+// * masks are evaluated only on key blocks that cross the causal diagonal (or
+//   with an explicit mask); interior blocks skip the per-element tests.
+template <int K, int D>
+struct AttnPipeShape {
+  static constexpr int CH = D / 4;                        // 16-byte chunks per key row
+  static constexpr int SWZ = CH < 16 ? CH : 16;           // swizzle period (power of two)
+  static constexpr int RPS = 1024 / (D * 4);              // key rows per 1 KB DMA segment
+  static constexpr int SEGS = kAttnBN / RPS;              // segments per order tile
+  static constexpr size_t LDS = 2ull * 2 * (K + 1) * kAttnBN * D * sizeof(float);
+  static constexpr bool fits = LDS <= 160 * 1024;
+};
+
+// LDS DMA of the K and V tiles of the key block starting at kb0 into one
+// buffer (tiles[kv][order][row][d]): 1 KB segments; lane l writes physical
+// chunk l % CH of row l / CH of its segment, loading the logical chunk that the
+// row swizzle maps there.
+template <int K, int D>
+__device__ __forceinline__ void attn_issue_tile(float (&buf)[2][K + 1][kAttnBN][D], const CPtrs<float>& Kp,
+                                                const CPtrs<float>& Vp, int64_t head, int S, int kb0, int lane,
+                                                int wave) {
+  using Shape = AttnPipeShape<K, D>;
+  constexpr int CH = Shape::CH, SWZ = Shape::SWZ, RPS = Shape::RPS, SEGS = Shape::SEGS;
+  const int r_in = lane / CH, pch = lane % CH;
+  // kv and the order are compile-time (static pointer indices); waves split the segments.
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+#pragma unroll
+      for (int it = 0; it < (SEGS + kAttnWaves - 1) / kAttnWaves; ++it) {
+        const int seg = it * kAttnWaves + wave;
+        if (SEGS % kAttnWaves != 0 && seg >= SEGS) break;
+        const int r = seg * RPS + r_in;
+        const int lch = pch ^ (r % SWZ);
+        const float* src = (kv ? Vp.p[o] : Kp.p[o]) + (head * S + kb0 + r) * D + lch * 4;
+        __builtin_amdgcn_global_load_lds(src, &buf[kv][o][seg * RPS][0], 16, 0, 0);
+      }
+    }
+  }
+}
+
+// Operands of head-dim chunk dc: Q[my row][16 dc + 4 h .. +3] from global memory,
+// K[key c][same d] from the swizzled LDS tile.
+template <int K, int D>
+__device__ __forceinline__ void attn_load_chunk(Vec<float, 4> (&qn)[K + 1], Vec<float, 4> (&kn)[K + 1],
+                                                const float* const (&qrow)[K + 1],
+                                                const float (&ktile)[K + 1][kAttnBN][D], int dc, int c, int h) {
+  constexpr int SWZ = AttnPipeShape<K, D>::SWZ;
+  const int pchk = (dc * 4 + h) ^ (c % SWZ);
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
-    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+    qn[o] = *reinterpret_cast<const Vec<float, 4>*>(qrow[o] + dc * 16 + 4 * h);
+    kn[o] = *reinterpret_cast<const Vec<float, 4>*>(&ktile[o][c][pchk * 4]);
   }
-  if (!q_ok) return;
-  const bool empty = !(lsum[0] > A(0));
-  const A inv_l0 = empty ? A(0) : A(1) / lsum[0];
+}
+
+template <int K, int D>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_kernel(
+    CPtrs<float> Q, CPtrs<float> Kp, CPtrs<float> Vp, MPtrs<float> O, MPtrs<float> LSE, int L, int S,
+    const uint8_t* __restrict__ mask, int causal, float scale) {
+  using A = float;
+  using MF = Mfma16<float>;
+  using acc_t = MF::acc_t;
+  using Shape = AttnPipeShape<K, D>;
+  constexpr int DB = D / 16;
+  constexpr int CH = Shape::CH, SWZ = Shape::SWZ, RPS = Shape::RPS, SEGS = Shape::SEGS;
+  constexpr A kNegInf = -__builtin_huge_valf();
+  static_assert(Shape::fits, "two K/V tiles exceed LDS");
+
+  // [buffer][0 = K, 1 = V][order][key row][head dim], rows unpadded and chunk-swizzled
+  __shared__ __attribute__((aligned(16))) float tiles[2][2][K + 1][kAttnBN][D];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;
+  const int h = lane / 16;
+  int64_t head;
+  int q_block;
+  attn_work_item(L, head, q_block);
+  const int q0_wave = q_block + wave * kAttnQPerWave;
+  const int my_q = q0_wave + c;
+  const bool q_ok = my_q < L;
+  const int q_row = q_ok ? my_q : L - 1;   // rows past L read a valid row; their results are dropped
+
+  const float* qrow[K + 1];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    A out[4][K + 1];
+  for (int o = 0; o <= K; ++o) qrow[o] = Q.p[o] + (head * L + q_row) * D;
+
+  int hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  const int nblocks = (hi + kAttnBN - 1) / kAttnBN;
+
+  // ---- pass 1: the exact row maximum of the order-0 scores. With it fixed up
+  // front the output accumulators are never rescaled, so they are touched by
+  // MFMAs only (one extra product per key block against (K+1)(K+2) in pass 2).
+  if (nblocks > 0) attn_issue_tile<K, D>(tiles[0], Kp, Vp, head, S, 0, lane, wave);
+  A m_row = kNegInf;
+  {
+    // key operands are fetched two blocks ahead (global/L2 latency exceeds one block's 32 MFMAs)
+    Vec<float, 4> q0[DB], kc[DB], kn[DB], kx[DB];
+#pragma unroll
+    for (int dc = 0; dc < DB; ++dc) q0[dc] = load_vec<float, 4>(qrow[0] + dc * 16 + 4 * h);
+    const float* k0 = Kp.p[0] + (head * S + c) * D + 4 * h;
+#pragma unroll
+    for (int dc = 0; dc < DB; ++dc) kc[dc] = load_vec<float, 4>(k0 + dc * 16);
+    if (nblocks > 1) {
+#pragma unroll
+      for (int dc = 0; dc < DB; ++dc) kn[dc] = load_vec<float, 4>(k0 + kAttnBN * D + dc * 16);
+    }
+    for (int j = 0; j < nblocks; ++j) {
+      const int kb0 = j * kAttnBN;
+      if (j + 2 < nblocks) {
+#pragma unroll
+        for (int dc = 0; dc < DB; ++dc) kx[dc] = load_vec<float, 4>(k0 + (kb0 + 2 * kAttnBN) * D + dc * 16);
+      }
+      acc_t s0 = MF::zero();
+#pragma unroll
+      for (int dc = 0; dc < DB; ++dc)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) s0 = MF::mma(kc[dc].v[s], q0[dc].v[s], s0);
+      const bool interior = mask == nullptr && (!causal || kb0 + kAttnBN - 1 <= q0_wave);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bool ok = true;
+        if (!interior) {
+          const int key = kb0 + MF::acc_row(h, r);
+          ok = q_ok;
+          if (causal) ok = ok && key <= my_q;
+          if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+        }
+        if (ok) m_row = fmaxf(m_row, s0[r] * scale);
+      }
+#pragma unroll
+      for (int dc = 0; dc < DB; ++dc) {
+        kc[dc] = kn[dc];
+        kn[dc] = kx[dc];
+      }
+    }
+    m_row = fmaxf(m_row, __shfl_xor(m_row, 16, kWave));
+    m_row = fmaxf(m_row, __shfl_xor(m_row, 32, kWave));
+  }
+  // a row with no visible key keeps p = 0 everywhere; any finite shift will do
+  const A m_used = m_row == kNegInf ? A(0) : m_row;
+
+  acc_t acc_o[K + 1][DB];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[o][db] = MF::zero();
+  A lsum[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) lsum[o] = A(0);
+
+  for (int j = 0; j < nblocks; ++j) {
+    const int buf = j & 1;
+    const int kb0 = j * kAttnBN;
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed
+    __syncthreads();                 // ... and every wave's; block j-1's buffer is free
+
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, operands of chunk dc+1 loaded during chunk dc ----
+    acc_t sc[K + 1];
+#pragma unroll
+    for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
+    Vec<float, 4> qn[K + 1], kn[K + 1];
+    attn_load_chunk<K, D>(qn, kn, qrow, tiles[buf][0], 0, c, h);
+#pragma unroll 1
+    for (int dc = 0; dc < DB; ++dc) {
+      Vec<float, 4> qa[K + 1], kb[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        qa[o] = qn[o];
+        kb[o] = kn[o];
+      }
+      if (dc + 1 < DB) attn_load_chunk<K, D>(qn, kn, qrow, tiles[buf][0], dc + 1, c, h);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int k = 0; k <= K; ++k) {
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MF::mma(kb[k - a].v[s], qa[a].v[s], sc[k]);
+        }
+      }
+    }
+
+    // ---- prefetch the next key block into the other buffer (it lands during the PV products) ----
+    if (j + 1 < nblocks) attn_issue_tile<K, D>(tiles[buf ^ 1], Kp, Vp, head, S, (j + 1) * kAttnBN, lane, wave);
+
+    // ---- mask (diagonal / masked blocks only) and exponential series against the fixed row maximum ----
+    const bool interior = mask == nullptr && (!causal || kb0 + kAttnBN - 1 <= q0_wave);
+    bool valid[4];
+    A s0[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int k = 0; k <= K; ++k) {
-        A t = static_cast<A>(acc_o[k][db][r]);
-#pragma unroll
-        for (int j = 1; j <= k; ++j) t -= lsum[j] * out[r][k - j];
-        out[r][k] = t * inv_l0;
+      bool ok = true;
+      if (!interior) {
+        const int key = kb0 + MF::acc_row(h, r);
+        ok = q_ok;
+        if (causal) ok = ok && key <= my_q;
+        if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
       }
+      valid[r] = ok;
+      s0[r] = ok ? sc[0][r] * scale : kNegInf;
     }
-    T* orow = nullptr;
 #pragma unroll
-    for (int k = 0; k <= K; ++k) {
-      orow = O.p[k] + (head * L + my_q) * D + db * 16;
-      if constexpr (sizeof(T) == 4) {
-        // fp32 layout: registers r = 0..3 hold head-dim columns 4h + r: one 16-byte store
-        Vec<T, 4> w;
+    for (int r = 0; r < 4; ++r) {
+      const A p = valid[r] ? exp_fast(s0[r] - m_used) : A(0);
+      A sk[K + 1], e[K + 1];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w.v[r] = static_cast<T>(out[r][k]);
-        store_vec<T, 4>(orow + 4 * h, w);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) orow[MF::acc_row(h, r)] = static_cast<T>(out[r][k]);
-      }
-    }
-  }
-  if (LSE.p[0] != nullptr && h == 0) {
-    const int64_t at = head * L + my_q;
-    if (empty) {
-      LSE.p[0][at] = __builtin_huge_val();
-#pragma unroll
-      for (int k = 1; k <= K; ++k) LSE.p[k][at] = A(0);
-    } else {
-      A lse[K + 1], nrm[K + 1];
-      lse[0] = m_used + log_acc(lsum[0]);
-#pragma unroll
-      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+      for (int o = 1; o <= K; ++o) sk[o] = sc[o][r] * scale;
+      e[0] = A(1);
 #pragma unroll
       for (int k = 1; k <= K; ++k) {
-        A t = nrm[k];
+        A t = A(0);
 #pragma unroll
-        for (int j = 1; j < k; ++j) t -= (A(j) / A(k)) * lse[j] * nrm[k - j];
-        lse[k] = t;
+        for (int i = 1; i <= k; ++i) t += (A(i) * sk[i]) * e[k - i];
+        e[k] = t * (A(1) / A(k));
       }
 #pragma unroll
-      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+      for (int o = 0; o <= K; ++o) {
+        const A w = p * e[o];
+        lsum[o] += w;
+        sc[o][r] = w;
+      }
+    }
+
+    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key_row = MF::acc_row(h, s);
+        const int pchv = (db * 4 + (c >> 2)) ^ (key_row % SWZ);
+        float vb[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) vb[o] = tiles[buf][1][o][key_row][pchv * 4 + (c & 3)];
+#pragma unroll
+        for (int k = 0; k <= K; ++k) {
+#pragma unroll
+          for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
+        }
+      }
     }
   }
+
+  attention_epilogue<float, K, D>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
 }
 
 template <typename T, int K, int D>
@@ -337,7 +625,19 @@ static int launch_attention_kd(const AttnArgs& a) {
       o.p[i] = static_cast<T*>(a.out[i]);
       if (a.lse != nullptr) lse.p[i] = static_cast<A*>(a.lse[i]);
     }
-    const dim3 grid((a.lq + kAttnBM - 1) / kAttnBM, a.bh);
+    const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
+    if constexpr (sizeof(T) == 4 && AttnPipeShape<K, D>::fits) {
+      bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk % kAttnBN == 0;
+      for (int i = 0; i <= K && pipe; ++i)
+        pipe = pt_host::aligned16(a.q[i]) && pt_host::aligned16(a.k[i]) && pt_host::aligned16(a.v[i]);
+      if (pipe) {
+        taylor_attention_fwd_pipe_kernel<K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.causal ? 1 : 0,
+            static_cast<A>(a.scale));
+        PT_LAUNCH_CHECK();
+        return PT_OK;
+      }
+    }
     taylor_attention_fwd_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
         q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
         static_cast<int>(a.lk), a.mask, a.causal ? 1 : 0, static_cast<A>(a.scale));

@@ -22,8 +22,8 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
              "Taylor attention: head dim must be 16, 32, 64 or 128");
   PT_REQUIRE(!(causal && mask != nullptr), PT_INVALID_ARGUMENT,
              "Taylor attention: causal and mask are exclusive");
-  PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && bh <= 65535, PT_UNSUPPORTED,
-             "Taylor attention: sizes beyond the launch grid");
+  PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && (lq + 63) / 64 * bh <= (int64_t{1} << 24), PT_UNSUPPORTED,
+             "Taylor attention: sizes beyond the launch grid (query blocks x heads > 2^24)");
   for (int o = 0; o < q_orders; ++o) PT_REQUIRE(q[o] != nullptr, PT_INVALID_ARGUMENT, "null q");
   for (int o = 0; o < k_orders; ++o) PT_REQUIRE(k[o] != nullptr, PT_INVALID_ARGUMENT, "null k");
   for (int o = 0; o < v_orders; ++o) PT_REQUIRE(v[o] != nullptr, PT_INVALID_ARGUMENT, "null v");

@@ -184,3 +184,28 @@ def test_full_size_config3_one_head():
     ref0 = torch.softmax((q[0] @ k[0].transpose(-1, -2).contiguous() / math.sqrt(d)).masked_fill(
         ~torch.ones(L, L, dtype=torch.bool, device="cuda").tril(), -math.inf), -1) @ v[0]
     assert rel_err(out[0].cpu(), ref0.cpu()) <= 1e-4
+
+
+# The pipelined fp32 kernel runs for full-order operands with a key length that is a multiple of 16
+# (and two K/V tiles within LDS); these shapes exercise it.
+@pytest.mark.parametrize("d,degree", [(16, 1), (16, 8), (32, 4), (64, 4), (64, 8), (128, 1), (128, 4)])
+@pytest.mark.parametrize("causal,window", [(True, None), (False, 21), (False, None)])
+def test_pipelined_kernel_shapes(d, degree, causal, window):
+    shape = (2, 3, 144, d)
+    Q, K, V = (_series(shape, degree, 70 + i, torch.float32) for i in range(3))
+    mask = None if window is None else _window_mask(144, window)
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=None if mask is None else mask.cuda(), is_causal=causal)
+    want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                            attn_mask=mask, is_causal=causal)
+    _check(out.coeffs, want, torch.float32)
+
+
+@pytest.mark.parametrize("L,S", [(50, 96), (100, 32), (16, 16), (1, 64)])
+def test_pipelined_kernel_cross_lengths(L, S):
+    Q = _series((1, 2, L, 128), 4, 80, torch.float32)
+    K, V = _series((1, 2, S, 128), 4, 81, torch.float32), _series((1, 2, S, 128), 4, 82, torch.float32)
+    for causal in (False, True):
+        out = _run(_poly(Q), _poly(K), _poly(V), is_causal=causal)
+        want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                                is_causal=causal)
+        _check(out.coeffs, want, torch.float32)
