@@ -404,17 +404,50 @@ __device__ __forceinline__ void attn_issue_tile(float (&buf)[2][K + 1][kAttnBN][
 
 // Operands of head-dim chunk dc: Q[my row][16 dc + 4 h .. +3] from global memory,
 // K[key c][same d] from the swizzled LDS tile.
+// Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format, no swizzle).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ Vec<float, 4> attn_buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
+  return __builtin_bit_cast(Vec<float, 4>, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
+// Whether key kb0 + 4h + r (score register r of lane group h in the 16x16x4
+// accumulator layout) is admissible for query my_q; mword holds the mask bytes
+// of keys kb0 + 4h .. kb0 + 4h + 3.
+// Branch-free (bitwise operators): a branch in the loops that call this splits
+// their bodies and makes the compiler's memory-counter waits conservative.
+__device__ __forceinline__ bool attn_key_ok(uint32_t mword, int kb0, int r, int h, int my_q, bool q_ok, int causal,
+                                            bool has_mask) {
+  const bool causal_ok = (kb0 + 4 * h + r <= my_q) | (causal == 0);
+  const bool mask_ok = (((mword >> (8 * r)) & 0xffu) != 0u) | !has_mask;
+  return q_ok & causal_ok & mask_ok;
+}
+
+template <int K>
+__device__ __forceinline__ void attn_load_q_chunk(Vec<float, 4> (&qn)[K + 1], const float* const (&qrow)[K + 1],
+                                                  int dc, int h) {
+#pragma unroll
+  for (int o = 0; o <= K; ++o) qn[o] = *reinterpret_cast<const Vec<float, 4>*>(qrow[o] + dc * 16 + 4 * h);
+}
+
 template <int K, int D>
-__device__ __forceinline__ void attn_load_chunk(Vec<float, 4> (&qn)[K + 1], Vec<float, 4> (&kn)[K + 1],
-                                                const float* const (&qrow)[K + 1],
-                                                const float (&ktile)[K + 1][kAttnBN][D], int dc, int c, int h) {
+__device__ __forceinline__ void attn_load_k_chunk(Vec<float, 4> (&kn)[K + 1], const float (&ktile)[K + 1][kAttnBN][D],
+                                                  int dc, int c, int h) {
   constexpr int SWZ = AttnPipeShape<K, D>::SWZ;
   const int pchk = (dc * 4 + h) ^ (c % SWZ);
 #pragma unroll
-  for (int o = 0; o <= K; ++o) {
-    qn[o] = *reinterpret_cast<const Vec<float, 4>*>(qrow[o] + dc * 16 + 4 * h);
-    kn[o] = *reinterpret_cast<const Vec<float, 4>*>(&ktile[o][c][pchk * 4]);
-  }
+  for (int o = 0; o <= K; ++o) kn[o] = *reinterpret_cast<const Vec<float, 4>*>(&ktile[o][c][pchk * 4]);
+}
+
+// V-operand values of PV step (db, s): head-dim column db*16 + c of key row acc_row(h, s)
+template <int K, int D>
+__device__ __forceinline__ void attn_load_v_step(float (&vb)[K + 1], const float (&vtile)[K + 1][kAttnBN][D],
+                                                 int db, int s, int c, int h) {
+  constexpr int SWZ = AttnPipeShape<K, D>::SWZ;
+  const int key_row = Mfma16<float>::acc_row(h, s);
+  const int pchv = (db * 4 + (c >> 2)) ^ (key_row % SWZ);
+#pragma unroll
+  for (int o = 0; o <= K; ++o) vb[o] = vtile[o][key_row][pchv * 4 + (c & 3)];
 }
 
 template <int K, int D>
@@ -451,52 +484,73 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 
   int hi = S;
   if (causal) hi = min(S, q_block + kAttnBM);
-  const int nblocks = (hi + kAttnBN - 1) / kAttnBN;
+  const int nblocks = (hi + kAttnBN - 1) / kAttnBN;   // >= 1: the launcher requires S >= 16
+
+  // Mask bits of this lane's keys 4h .. 4h+3 of a key block (the rows of its
+  // score registers r = 0..3) are one aligned 32-bit read of the mask row; it
+  // is unconditional and branch-free (without a mask it re-reads a valid dummy
+  // word), so no load sits behind a branch and the compiler's memory-counter
+  // waits stay exact for the prefetches around it.
+  const uint8_t* mrow = mask != nullptr ? mask + static_cast<int64_t>(q_row) * S + 4 * h
+                                        : reinterpret_cast<const uint8_t*>(Q.p[0]);
+  const int mstep = mask != nullptr ? 1 : 0;
 
   // ---- pass 1: the exact row maximum of the order-0 scores. With it fixed up
   // front the output accumulators are never rescaled, so they are touched by
   // MFMAs only (one extra product per key block against (K+1)(K+2) in pass 2).
-  if (nblocks > 0) attn_issue_tile<K, D>(tiles[0], Kp, Vp, head, S, 0, lane, wave);
   A m_row = kNegInf;
   {
-    // key operands are fetched two blocks ahead (global/L2 latency exceeds one block's 32 MFMAs)
-    Vec<float, 4> q0[DB], kc[DB], kn[DB], kx[DB];
+    // Key operands and mask words are fetched two blocks ahead (global/L2
+    // latency exceeds one block's 32 MFMAs) with the block index clamped to the
+    // last block, so every load is unconditional. They are buffer loads: LLVM
+    // folds a loop-carried rotation of plain loads back into a load at the use,
+    // which would undo the prefetch.
+    Vec<float, 4> q0[DB], kb[3][DB];
+    uint32_t mb[3];
 #pragma unroll
     for (int dc = 0; dc < DB; ++dc) q0[dc] = load_vec<float, 4>(qrow[0] + dc * 16 + 4 * h);
-    const float* k0 = Kp.p[0] + (head * S + c) * D + 4 * h;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(Kp.p[0] + head * S * D), static_cast<short>(0), S * D * 4, kBufferRsrcWord3);
+    // (a buffer resource must be wave-uniform: the mask's is the whole (L, S)
+    // mask, with this lane's row in the offset; without a mask, a 4-byte dummy)
+    const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+        mask != nullptr ? static_cast<void*>(const_cast<uint8_t*>(mask)) : static_cast<void*>(const_cast<float*>(Q.p[0])),
+        static_cast<short>(0), mask != nullptr ? L * S : 4, kBufferRsrcWord3);
+    const uint32_t mofs = mask != nullptr ? static_cast<uint32_t>(q_row * S + 4 * h) : 0u;
+    const uint32_t kofs = static_cast<uint32_t>((c * D + 4 * h) * 4);
+    const int last = (nblocks - 1) * kAttnBN;
+    // block b's operands go to buffer b % 3; the loop is unrolled by three so the
+    // buffers rotate statically (a register copy would wait for its load), and
+    // runs a multiple of three blocks, the surplus ones re-reading the last
+    // block and excluded from the maximum
 #pragma unroll
-    for (int dc = 0; dc < DB; ++dc) kc[dc] = load_vec<float, 4>(k0 + dc * 16);
-    if (nblocks > 1) {
+    for (int b = 0; b < 2; ++b) {
+      const int rb = min(b * kAttnBN, last);
 #pragma unroll
-      for (int dc = 0; dc < DB; ++dc) kn[dc] = load_vec<float, 4>(k0 + kAttnBN * D + dc * 16);
+      for (int dc = 0; dc < DB; ++dc) kb[b][dc] = attn_buffer_load4(krs, kofs + (rb * D + dc * 16) * 4);
+      mb[b] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs + mstep * rb, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);   // keep block 0's loads ahead of block 1's
     }
-    for (int j = 0; j < nblocks; ++j) {
-      const int kb0 = j * kAttnBN;
-      if (j + 2 < nblocks) {
+    for (int j0 = 0; j0 < nblocks; j0 += 3) {
 #pragma unroll
-        for (int dc = 0; dc < DB; ++dc) kx[dc] = load_vec<float, 4>(k0 + (kb0 + 2 * kAttnBN) * D + dc * 16);
-      }
-      acc_t s0 = MF::zero();
+      for (int u = 0; u < 3; ++u) {
+        const int kb0 = (j0 + u) * kAttnBN;
+        const int ra = min(kb0 + 2 * kAttnBN, last);
 #pragma unroll
-      for (int dc = 0; dc < DB; ++dc)
+        for (int dc = 0; dc < DB; ++dc) kb[(u + 2) % 3][dc] = attn_buffer_load4(krs, kofs + (ra * D + dc * 16) * 4);
+        mb[(u + 2) % 3] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs + mstep * ra, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        acc_t s0 = MF::zero();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) s0 = MF::mma(kc[dc].v[s], q0[dc].v[s], s0);
-      const bool interior = mask == nullptr && (!causal || kb0 + kAttnBN - 1 <= q0_wave);
+        for (int dc = 0; dc < DB; ++dc)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bool ok = true;
-        if (!interior) {
-          const int key = kb0 + MF::acc_row(h, r);
-          ok = q_ok;
-          if (causal) ok = ok && key <= my_q;
-          if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+          for (int s = 0; s < 4; ++s) s0 = MF::mma(kb[u][dc].v[s], q0[dc].v[s], s0);
+        const bool real = kb0 <= last;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = real & attn_key_ok(mb[u], kb0, r, h, my_q, q_ok, causal, mask != nullptr);
+          m_row = fmaxf(m_row, ok ? s0[r] * scale : kNegInf);
         }
-        if (ok) m_row = fmaxf(m_row, s0[r] * scale);
-      }
-#pragma unroll
-      for (int dc = 0; dc < DB; ++dc) {
-        kc[dc] = kn[dc];
-        kn[dc] = kx[dc];
       }
     }
     m_row = fmaxf(m_row, __shfl_xor(m_row, 16, kWave));
@@ -504,6 +558,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
   }
   // a row with no visible key keeps p = 0 everywhere; any finite shift will do
   const A m_used = m_row == kNegInf ? A(0) : m_row;
+
+  // the first key block's DMA is issued only now: LDS-DMA loads pending beside
+  // ordinary loads make the compiler wait for every load in flight
+  attn_issue_tile<K, D>(tiles[0], Kp, Vp, head, S, 0, lane, wave);
 
   acc_t acc_o[K + 1][DB];
 #pragma unroll
@@ -514,27 +572,40 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 #pragma unroll
   for (int o = 0; o <= K; ++o) lsum[o] = A(0);
 
+  // Query chunks live in a ring of NQ register slots (chunk dc in slot dc % NQ).
+  // With NQ == DB the whole query tile stays resident; otherwise chunk dc+NQ-1
+  // (cyclically: every key block reads the same chunks) is fetched while chunk
+  // dc's MFMAs run, NQ-1 chunks ahead of its use.
+  constexpr int NQ = DB < 4 ? DB : 4;
+  Vec<float, 4> qs[NQ][K + 1];
+#pragma unroll
+  for (int dc = 0; dc < (NQ == DB ? DB : NQ - 1); ++dc) attn_load_q_chunk<K>(qs[dc], qrow, dc, h);
+
   for (int j = 0; j < nblocks; ++j) {
     const int buf = j & 1;
     const int kb0 = j * kAttnBN;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
+    const uint32_t mword = *reinterpret_cast<const uint32_t*>(mrow + mstep * kb0);   // used after the scores
 
-    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, operands of chunk dc+1 loaded during chunk dc ----
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T; key chunk dc+1 read from LDS during chunk dc ----
+    // (scheduling barriers keep each chunk's prefetches ahead of its MFMAs; left
+    // alone the scheduler sinks them next to their uses)
     acc_t sc[K + 1];
 #pragma unroll
     for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
-    Vec<float, 4> qn[K + 1], kn[K + 1];
-    attn_load_chunk<K, D>(qn, kn, qrow, tiles[buf][0], 0, c, h);
-#pragma unroll 1
-    for (int dc = 0; dc < DB; ++dc) {
-      Vec<float, 4> qa[K + 1], kb[K + 1];
+    Vec<float, 4> kq[2][K + 1];
+    attn_load_k_chunk<K, D>(kq[0], tiles[buf][0], 0, c, h);
 #pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        qa[o] = qn[o];
-        kb[o] = kn[o];
+    for (int dc = 0; dc < DB; ++dc) {
+      if constexpr (NQ < DB) {
+        const int ahead = (dc + NQ - 1) % DB;
+        attn_load_q_chunk<K>(qs[ahead % NQ], qrow, ahead, h);
       }
-      if (dc + 1 < DB) attn_load_chunk<K, D>(qn, kn, qrow, tiles[buf][0], dc + 1, c, h);
+      if (dc + 1 < DB) attn_load_k_chunk<K, D>(kq[(dc + 1) & 1], tiles[buf][0], dc + 1, c, h);
+      __builtin_amdgcn_sched_barrier(0);
+      const Vec<float, 4>(&qa)[K + 1] = qs[dc % NQ];
+      const Vec<float, 4>(&kb)[K + 1] = kq[dc & 1];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -545,28 +616,19 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
       }
     }
 
+    // admissibility is settled before the DMA below is issued, so waiting for
+    // the mask word never waits for the DMA
+    bool valid[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) valid[r] = attn_key_ok(mword, kb0, r, h, my_q, q_ok, causal, mask != nullptr);
+
     // ---- prefetch the next key block into the other buffer (it lands during the PV products) ----
     if (j + 1 < nblocks) attn_issue_tile<K, D>(tiles[buf ^ 1], Kp, Vp, head, S, (j + 1) * kAttnBN, lane, wave);
 
-    // ---- mask (diagonal / masked blocks only) and exponential series against the fixed row maximum ----
-    const bool interior = mask == nullptr && (!causal || kb0 + kAttnBN - 1 <= q0_wave);
-    bool valid[4];
-    A s0[4];
+    // ---- exponential series against the fixed row maximum ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      bool ok = true;
-      if (!interior) {
-        const int key = kb0 + MF::acc_row(h, r);
-        ok = q_ok;
-        if (causal) ok = ok && key <= my_q;
-        if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
-      }
-      valid[r] = ok;
-      s0[r] = ok ? sc[0][r] * scale : kNegInf;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const A p = valid[r] ? exp_fast(s0[r] - m_used) : A(0);
+      const A p = valid[r] ? exp_fast(sc[0][r] * scale - m_used) : A(0);
       A sk[K + 1], e[K + 1];
 #pragma unroll
       for (int o = 1; o <= K; ++o) sk[o] = sc[o][r] * scale;
@@ -586,21 +648,19 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
       }
     }
 
-    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T ----
+    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T, V values of step t+1 read during step t ----
+    float vq[2][K + 1];
+    attn_load_v_step<K, D>(vq[0], tiles[buf][1], 0, 0, c, h);
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int t = 0; t < DB * 4; ++t) {
+      const int db = t / 4, s = t % 4;
+      if (t + 1 < DB * 4) attn_load_v_step<K, D>(vq[(t + 1) & 1], tiles[buf][1], (t + 1) / 4, (t + 1) % 4, c, h);
+      __builtin_amdgcn_sched_barrier(0);
+      const float(&vb)[K + 1] = vq[t & 1];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int key_row = MF::acc_row(h, s);
-        const int pchv = (db * 4 + (c >> 2)) ^ (key_row % SWZ);
-        float vb[K + 1];
+      for (int k = 0; k <= K; ++k) {
 #pragma unroll
-        for (int o = 0; o <= K; ++o) vb[o] = tiles[buf][1][o][key_row][pchv * 4 + (c & 3)];
-#pragma unroll
-        for (int k = 0; k <= K; ++k) {
-#pragma unroll
-          for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
-        }
+        for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
       }
     }
   }
@@ -627,7 +687,11 @@ static int launch_attention_kd(const AttnArgs& a) {
     }
     const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
     if constexpr (sizeof(T) == 4 && AttnPipeShape<K, D>::fits) {
-      bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk % kAttnBN == 0;
+      // the pipelined kernel reads each lane's four mask bytes as one 32-bit word
+      bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= kAttnBN &&
+                  a.lk % kAttnBN == 0 && reinterpret_cast<uintptr_t>(a.mask) % 4 == 0 &&
+                  a.lk * D * sizeof(float) < (size_t{1} << 31) &&   // 32-bit buffer offsets: per-head keys,
+                  (a.mask == nullptr || a.lq * a.lk < (int64_t{1} << 31));   // ... and the whole mask
       for (int i = 0; i <= K && pipe; ++i)
         pipe = pt_host::aligned16(a.q[i]) && pt_host::aligned16(a.k[i]) && pt_host::aligned16(a.v[i]);
       if (pipe) {

@@ -25,8 +25,9 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
   PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && (lq + 63) / 64 * bh <= (int64_t{1} << 24), PT_UNSUPPORTED,
              "Taylor attention: sizes beyond the launch grid (query blocks x heads > 2^24)");
   for (int o = 0; o < q_orders; ++o) PT_REQUIRE(q[o] != nullptr, PT_INVALID_ARGUMENT, "null q");
-  for (int o = 0; o < k_orders; ++o) PT_REQUIRE(k[o] != nullptr, PT_INVALID_ARGUMENT, "null k");
-  for (int o = 0; o < v_orders; ++o) PT_REQUIRE(v[o] != nullptr, PT_INVALID_ARGUMENT, "null v");
+  // an empty key sequence may come with null key/value buffers (nothing is read)
+  for (int o = 0; o < k_orders; ++o) PT_REQUIRE(k[o] != nullptr || lk == 0, PT_INVALID_ARGUMENT, "null k");
+  for (int o = 0; o < v_orders; ++o) PT_REQUIRE(v[o] != nullptr || lk == 0, PT_INVALID_ARGUMENT, "null v");
   for (int o = 0; o <= degree; ++o) {
     PT_REQUIRE(out[o] != nullptr, PT_INVALID_ARGUMENT, "null out");
     PT_REQUIRE(lse == nullptr || lse[o] != nullptr, PT_INVALID_ARGUMENT, "null lse entry");

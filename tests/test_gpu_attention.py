@@ -209,3 +209,14 @@ def test_pipelined_kernel_cross_lengths(L, S):
         want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
                                 is_causal=causal)
         _check(out.coeffs, want, torch.float32)
+
+
+def test_empty_key_length_gives_empty_rows():
+    # zero keys: every row is empty (zero output, +inf order-0 log-sum-exp) on both fp32 paths' dispatch
+    for dtype in (torch.float32, torch.float64):
+        q = [torch.randn(2, 5, 32, dtype=dtype, device="cuda") for _ in range(5)]
+        kv = [torch.empty(2, 0, 32, dtype=dtype, device="cuda") for _ in range(5)]
+        for causal in (False, True):
+            out, lse = _ops.taylor_attention_fwd(q, kv, kv, None, causal, 0.1, 4)
+            assert torch.equal(out, torch.zeros_like(out))
+            assert torch.isinf(lse[0]).all() and (lse[1:] == 0).all()
