@@ -377,33 +377,40 @@ struct AttnPipeShape {
 // buffer (tiles[kv][order][row][d]): 1 KB segments; lane l writes physical
 // chunk l % CH of row l / CH of its segment, loading the logical chunk that the
 // row swizzle maps there.
+// LDS-DMA operations one wave issues per key block: (K, V) x orders x its share
+// of the 1 KB segments of an order tile.
+template <int K, int D>
+struct AttnDma {
+  static constexpr int IT = (AttnPipeShape<K, D>::SEGS + kAttnWaves - 1) / kAttnWaves;
+  static constexpr int OPS = 2 * (K + 1) * IT;
+};
+
+// Operation i of this wave's share of key block kb0's DMA. Callers pass an i that
+// is a constant once their loops are unrolled, so the K/V pointer and the order
+// are static indices.
+template <int K, int D>
+__device__ __forceinline__ void attn_issue_op(float (&buf)[2][K + 1][kAttnBN][D], const CPtrs<float>& Kp,
+                                              const CPtrs<float>& Vp, int64_t head, int S, int kb0, int lane,
+                                              int wave, int i) {
+  using Shape = AttnPipeShape<K, D>;
+  constexpr int CH = Shape::CH, SWZ = Shape::SWZ, RPS = Shape::RPS, SEGS = Shape::SEGS, IT = AttnDma<K, D>::IT;
+  const int kv = i / ((K + 1) * IT), o = (i / IT) % (K + 1), it = i % IT;
+  const int seg = it * kAttnWaves + wave;
+  if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
+  const int r = seg * RPS + lane / CH;
+  const int lch = (lane % CH) ^ (r % SWZ);
+  const float* src = (kv ? Vp.p[o] : Kp.p[o]) + (head * S + kb0 + r) * D + lch * 4;
+  __builtin_amdgcn_global_load_lds(src, &buf[kv][o][seg * RPS][0], 16, 0, 0);
+}
+
 template <int K, int D>
 __device__ __forceinline__ void attn_issue_tile(float (&buf)[2][K + 1][kAttnBN][D], const CPtrs<float>& Kp,
                                                 const CPtrs<float>& Vp, int64_t head, int S, int kb0, int lane,
                                                 int wave) {
-  using Shape = AttnPipeShape<K, D>;
-  constexpr int CH = Shape::CH, SWZ = Shape::SWZ, RPS = Shape::RPS, SEGS = Shape::SEGS;
-  const int r_in = lane / CH, pch = lane % CH;
-  // kv and the order are compile-time (static pointer indices); waves split the segments.
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-#pragma unroll
-    for (int o = 0; o <= K; ++o) {
-#pragma unroll
-      for (int it = 0; it < (SEGS + kAttnWaves - 1) / kAttnWaves; ++it) {
-        const int seg = it * kAttnWaves + wave;
-        if (SEGS % kAttnWaves != 0 && seg >= SEGS) break;
-        const int r = seg * RPS + r_in;
-        const int lch = pch ^ (r % SWZ);
-        const float* src = (kv ? Vp.p[o] : Kp.p[o]) + (head * S + kb0 + r) * D + lch * 4;
-        __builtin_amdgcn_global_load_lds(src, &buf[kv][o][seg * RPS][0], 16, 0, 0);
-      }
-    }
-  }
+  for (int i = 0; i < AttnDma<K, D>::OPS; ++i) attn_issue_op<K, D>(buf, Kp, Vp, head, S, kb0, lane, wave, i);
 }
 
-// Operands of head-dim chunk dc: Q[my row][16 dc + 4 h .. +3] from global memory,
-// K[key c][same d] from the swizzled LDS tile.
 // Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format, no swizzle).
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
@@ -423,6 +430,8 @@ __device__ __forceinline__ bool attn_key_ok(uint32_t mword, int kb0, int r, int 
   return q_ok & causal_ok & mask_ok;
 }
 
+// Operands of head-dim chunk dc: Q[my row][16 dc + 4 h .. +3] from global memory,
+// K[key c][same d] from the swizzled LDS tile.
 template <int K>
 __device__ __forceinline__ void attn_load_q_chunk(Vec<float, 4> (&qn)[K + 1], const float* const (&qrow)[K + 1],
                                                   int dc, int h) {
@@ -622,8 +631,6 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 #pragma unroll
     for (int r = 0; r < 4; ++r) valid[r] = attn_key_ok(mword, kb0, r, h, my_q, q_ok, causal, mask != nullptr);
 
-    // ---- prefetch the next key block into the other buffer (it lands during the PV products) ----
-    if (j + 1 < nblocks) attn_issue_tile<K, D>(tiles[buf ^ 1], Kp, Vp, head, S, (j + 1) * kAttnBN, lane, wave);
 
     // ---- exponential series against the fixed row maximum ----
 #pragma unroll
@@ -649,22 +656,40 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
     }
 
     // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T, V values of step t+1 read during step t ----
+    // The next key block's DMA into the other buffer is spread over the steps so
+    // its issue hides behind MFMAs (the last block re-loads itself: no branch).
+    // While it is in flight the compiler waits for every outstanding LDS read
+    // before using any, so step t+1's reads are issued in the middle of step t
+    // (after orders 0..K/2), early enough to have landed by the end of it.
+    constexpr int STEPS = DB * 4, OPS = AttnDma<K, D>::OPS;
+    const int next_kb0 = min(kb0 + kAttnBN, (nblocks - 1) * kAttnBN);
     float vq[2][K + 1];
     attn_load_v_step<K, D>(vq[0], tiles[buf][1], 0, 0, c, h);
 #pragma unroll
     for (int t = 0; t < DB * 4; ++t) {
       const int db = t / 4, s = t % 4;
-      if (t + 1 < DB * 4) attn_load_v_step<K, D>(vq[(t + 1) & 1], tiles[buf][1], (t + 1) / 4, (t + 1) % 4, c, h);
-      __builtin_amdgcn_sched_barrier(0);
       const float(&vb)[K + 1] = vq[t & 1];
 #pragma unroll
-      for (int k = 0; k <= K; ++k) {
+      for (int k = 0; k <= K / 2; ++k) {
 #pragma unroll
         for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < DB * 4) attn_load_v_step<K, D>(vq[(t + 1) & 1], tiles[buf][1], (t + 1) / 4, (t + 1) % 4, c, h);
+#pragma unroll
+      for (int i = t * OPS / STEPS; i < (t + 1) * OPS / STEPS; ++i)
+        attn_issue_op<K, D>(tiles[buf ^ 1], Kp, Vp, head, S, next_kb0, lane, wave, i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = K / 2 + 1; k <= K; ++k) {
+#pragma unroll
+        for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
+  __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMA has landed before the workgroup ends
   attention_epilogue<float, K, D>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
 }
 
