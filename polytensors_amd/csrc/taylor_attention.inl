@@ -93,7 +93,10 @@ __device__ __forceinline__ void attn_work_item(int L, int64_t& head, int& q_bloc
   q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
 }
 
-template <typename T, int K, int D, typename AccT>
+// E is the head-dim interleave of the output accumulators: accumulator
+// g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
+// (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).
+template <typename T, int K, int D, typename AccT, int E = 1>
 __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
                                                    typename AccOf<T>::type (&lsum)[K + 1],
                                                    typename AccOf<T>::type m_used, MPtrs<T>& O,
@@ -110,8 +113,35 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
   if (!q_ok) return;
   const bool empty = !(lsum[0] > A(0));
   const A inv_l0 = empty ? A(0) : A(1) / lsum[0];
+  if constexpr (E > 1) {
+    static_assert(sizeof(T) == 4, "interleaved accumulators are an fp32 layout");
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+    for (int g = 0; g < DB / E; ++g) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        A out[E][K + 1];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+#pragma unroll
+          for (int k = 0; k <= K; ++k) {
+            A t = static_cast<A>(acc_o[k][g * E + e][r]);
+#pragma unroll
+            for (int j = 1; j <= k; ++j) t -= lsum[j] * out[e][k - j];
+            out[e][k] = t * inv_l0;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k <= K; ++k) {
+          Vec<T, E> w;
+#pragma unroll
+          for (int e = 0; e < E; ++e) w.v[e] = static_cast<T>(out[e][k]);
+          store_vec<T, E>(O.p[k] + (head * L + my_q) * D + g * 16 * E + E * (4 * h + r), w);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int db = 0; db < (E == 1 ? DB : 0); ++db) {
     A out[4][K + 1];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -448,15 +478,26 @@ __device__ __forceinline__ void attn_load_k_chunk(Vec<float, 4> (&kn)[K + 1], co
   for (int o = 0; o <= K; ++o) kn[o] = *reinterpret_cast<const Vec<float, 4>*>(&ktile[o][c][pchk * 4]);
 }
 
-// V-operand values of PV step (db, s): head-dim column db*16 + c of key row acc_row(h, s)
+// Head-dim columns per lane in a PV operand read of the pipelined kernel: one
+// 16-byte read serves four MFMAs when 16 lanes x 4 columns fit the head dim.
+template <int D>
+struct AttnPvE {
+  static constexpr int value = D >= 64 ? 4 : D / 16;
+};
+
+// V operands of PV step (g, s): key row acc_row(h, s), head-dim columns
+// g*16E + E*c .. +E-1 of every order (E consecutive floats: one LDS read).
 template <int K, int D>
-__device__ __forceinline__ void attn_load_v_step(float (&vb)[K + 1], const float (&vtile)[K + 1][kAttnBN][D],
-                                                 int db, int s, int c, int h) {
-  constexpr int SWZ = AttnPipeShape<K, D>::SWZ;
+__device__ __forceinline__ void attn_load_v_step(Vec<float, AttnPvE<D>::value> (&vb)[K + 1],
+                                                 const float (&vtile)[K + 1][kAttnBN][D], int g, int s, int c,
+                                                 int h) {
+  constexpr int E = AttnPvE<D>::value, SWZ = AttnPipeShape<K, D>::SWZ;
   const int key_row = Mfma16<float>::acc_row(h, s);
-  const int pchv = (db * 4 + (c >> 2)) ^ (key_row % SWZ);
+  const int col = g * 16 * E + E * c;
+  const int pch = (col / 4) ^ (key_row % SWZ);
 #pragma unroll
-  for (int o = 0; o <= K; ++o) vb[o] = vtile[o][key_row][pchv * 4 + (c & 3)];
+  for (int o = 0; o <= K; ++o)
+    vb[o] = *reinterpret_cast<const Vec<float, E>*>(&vtile[o][key_row][pch * 4 + col % 4]);
 }
 
 template <int K, int D>
@@ -655,42 +696,46 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
       }
     }
 
-    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T, V values of step t+1 read during step t ----
-    // The next key block's DMA into the other buffer is spread over the steps so
-    // its issue hides behind MFMAs (the last block re-loads itself: no branch).
-    // While it is in flight the compiler waits for every outstanding LDS read
-    // before using any, so step t+1's reads are issued in the middle of step t
-    // (after orders 0..K/2), early enough to have landed by the end of it.
-    constexpr int STEPS = DB * 4, OPS = AttnDma<K, D>::OPS;
+    // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T ----
+    // Step t = (g, s) reads E consecutive head-dim columns of key row 4h+s per
+    // lane and order; element e feeds the MFMAs of accumulator g*E + e, whose
+    // rows are the columns g*16E + E*m + e. Step t+1's reads (and a share of the
+    // next key block's DMA into the other buffer; the last block re-loads
+    // itself, so there is no branch) are issued right after step t's first
+    // MFMA: with an LDS DMA in flight the compiler waits for every outstanding
+    // LDS read before using any, and the rest of step t covers their latency.
+    constexpr int PE = AttnPvE<D>::value, STEPS = DB / PE * 4, OPS = AttnDma<K, D>::OPS;
     const int next_kb0 = min(kb0 + kAttnBN, (nblocks - 1) * kAttnBN);
-    float vq[2][K + 1];
+    Vec<float, PE> vq[2][K + 1];
     attn_load_v_step<K, D>(vq[0], tiles[buf][1], 0, 0, c, h);
 #pragma unroll
-    for (int t = 0; t < DB * 4; ++t) {
-      const int db = t / 4, s = t % 4;
-      const float(&vb)[K + 1] = vq[t & 1];
-#pragma unroll
-      for (int k = 0; k <= K / 2; ++k) {
-#pragma unroll
-        for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
-      }
+    for (int t = 0; t < STEPS; ++t) {
+      const int g = t / 4, s = t % 4;
+      const Vec<float, PE>(&vb)[K + 1] = vq[t & 1];
+      acc_o[0][g * PE] = MF::mma(vb[0].v[0], sc[0][s], acc_o[0][g * PE]);
       __builtin_amdgcn_sched_barrier(0);
-      if (t + 1 < DB * 4) attn_load_v_step<K, D>(vq[(t + 1) & 1], tiles[buf][1], (t + 1) / 4, (t + 1) % 4, c, h);
+      if (t + 1 < STEPS) attn_load_v_step<K, D>(vq[(t + 1) & 1], tiles[buf][1], (t + 1) / 4, (t + 1) % 4, c, h);
 #pragma unroll
       for (int i = t * OPS / STEPS; i < (t + 1) * OPS / STEPS; ++i)
         attn_issue_op<K, D>(tiles[buf ^ 1], Kp, Vp, head, S, next_kb0, lane, wave, i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = K / 2 + 1; k <= K; ++k) {
+      for (int e = 0; e < PE; ++e) {
 #pragma unroll
-        for (int a = 0; a <= k; ++a) acc_o[k][db] = MF::mma(vb[k - a], sc[a][s], acc_o[k][db]);
+        for (int k = 0; k <= K; ++k) {
+#pragma unroll
+          for (int a = 0; a <= k; ++a) {
+            if (e == 0 && k == 0) continue;   // issued above
+            acc_o[k][g * PE + e] = MF::mma(vb[k - a].v[e], sc[a][s], acc_o[k][g * PE + e]);
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
   __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMA has landed before the workgroup ends
-  attention_epilogue<float, K, D>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
+  attention_epilogue<float, K, D, acc_t, AttnPvE<D>::value>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
 }
 
 template <typename T, int K, int D>
