@@ -626,7 +626,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
   // With NQ == DB the whole query tile stays resident; otherwise chunk dc+NQ-1
   // (cyclically: every key block reads the same chunks) is fetched while chunk
   // dc's MFMAs run, NQ-1 chunks ahead of its use.
-  constexpr int NQ = DB < 4 ? DB : 4;
+  constexpr int NQ = DB;
   Vec<float, 4> qs[NQ][K + 1];
 #pragma unroll
   for (int dc = 0; dc < (NQ == DB ? DB : NQ - 1); ++dc) attn_load_q_chunk<K>(qs[dc], qrow, dc, h);
