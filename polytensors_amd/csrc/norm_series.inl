@@ -11,9 +11,9 @@
 //   z_k = sum_{i+j=k} c_i r_j,  then y = z (*) w (+ b)  (Cauchy products).
 //
 // Register path: every coefficient of a row is loaded once into VGPRs with
-// 16-byte loads, the K+1 row sums are reduced with wavefront shuffles (and
-// LDS across the 4 waves of a block), and y is written once: one HBM read
-// and one HBM write of the series. Streaming path (rows too long for
+// 16-byte loads, the K+1 row sums are reduced with DPP and lane exchanges
+// within each wave (and LDS across the row's waves), and y is written once:
+// one HBM read and one HBM write of the series. Streaming path (rows too long for
 // registers, or unaligned rows): the same math re-reading x per pass.
 #pragma once
 
@@ -30,9 +30,10 @@ __device__ __forceinline__ void rsqrt_series(const A (&sums)[K + 1], A inv_n, A 
                                              A (&r)[K + 1]) {
   const A s0 = sums[0] * inv_n + eps;
   r[0] = rsqrt_acc(s0);
+  const A inv_s0 = A(1) / s0;
   A u[K + 1];
 #pragma unroll
-  for (int k = 1; k <= K; ++k) u[k] = (sums[k] * inv_n) / s0;
+  for (int k = 1; k <= K; ++k) u[k] = (sums[k] * inv_n) * inv_s0;
 #pragma unroll
   for (int k = 1; k <= K; ++k) {
     A acc = A(0);
@@ -109,9 +110,15 @@ __device__ __forceinline__ void apply_affine(A (&z)[K + 1], const A (&w)[K + 1],
 // Register-resident kernel. `tpr` threads share a row (a multiple of 64; a
 // block holds blockDim.x / tpr rows), each thread owns CHUNKS 16-byte vectors
 // of every order, kept in their storage type (a bf16 row costs half the
-// VGPRs of its float values) and converted where used. The launcher sizes tpr
-// so that CHUNKS is 1 wherever a row fits 1024 threads: few VGPRs per thread,
-// many rows in flight per CU. Affine terms here are ordinary (one order).
+// VGPRs of its float values) and unpacked where used. The arithmetic is kept
+// lean so that the kernel stays HBM-bound: the squared series takes one FMA
+// per element and order pair (the products c_i c_j with i < j are summed once
+// and doubled once per thread), the weight is folded into the coefficients
+// before the output Cauchy product, bf16 results are packed two per
+// instruction, and the row's rsqrt series costs one division. The series is
+// read and written with non-temporal 16-byte accesses: each byte is touched
+// once, and streaming it past the caches lifts a read+write stream from about
+// 5.4 to 5.8 TB/s on MI355X. Affine terms here are ordinary (one order).
 template <typename T, int K, int CHUNKS, bool LAYER>
 __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
     CPtrs<T> x, const T* __restrict__ w, const T* __restrict__ b, MPtrs<T> y, int64_t rows, int n,
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
 #pragma unroll
     for (int k = 0; k <= K; ++k) {
       if (in) {
-        raw[ch][k] = load_vec<T, V>(x.p[k] + base + col);
+        raw[ch][k] = load_vec_nt<T, V>(x.p[k] + base + col);
       } else {
 #pragma unroll
         for (int e = 0; e < V; ++e) raw[ch][k].v[e] = from_acc<T>(A(0));
@@ -149,30 +156,44 @@ __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
 #pragma unroll
     for (int ch = 0; ch < CHUNKS; ++ch)
 #pragma unroll
-      for (int e = 0; e < V; ++e)
+      for (int k = 0; k <= K; ++k) {
+        A f[V];
+        unpack_vec(raw[ch][k], f);
 #pragma unroll
-        for (int k = 0; k <= K; ++k) mean[k] += to_acc(raw[ch][k].v[e]);
+        for (int e = 0; e < V; ++e) mean[k] += f[e];
+      }
     row_sums<A, K>(mean, &red[0][0][0], tpr);
 #pragma unroll
     for (int k = 0; k <= K; ++k) mean[k] *= inv_n;
   }
 
-  A sums[K + 1];
+  // cross[k] = sum over i < k - i of c_i c_{k-i};  sq[k] = c_{k/2}^2 (k even).
+  A cross[K + 1], sq[K + 1];
 #pragma unroll
-  for (int k = 0; k <= K; ++k) sums[k] = A(0);
+  for (int k = 0; k <= K; ++k) cross[k] = sq[k] = A(0);
 #pragma unroll
   for (int ch = 0; ch < CHUNKS; ++ch) {
     const int col = (ch * tpr + tid) * V;
     if (!(active && col < n)) continue;
+    A f[K + 1][V];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) unpack_vec(raw[ch][k], f[k]);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       A c[K + 1];
 #pragma unroll
-      for (int k = 0; k <= K; ++k) c[k] = to_acc(raw[ch][k].v[e]) - mean[k];
+      for (int k = 0; k <= K; ++k) c[k] = LAYER ? f[k][e] - mean[k] : f[k][e];
 #pragma unroll
-      for (int k = 0; k <= K; ++k) sums[k] += cauchy_square<A, K>(c, k);
+      for (int k = 0; k <= K; ++k) {
+#pragma unroll
+        for (int i = 0; 2 * i < k; ++i) cross[k] = fma(c[i], c[k - i], cross[k]);
+        if (k % 2 == 0) sq[k] = fma(c[k / 2], c[k / 2], sq[k]);
+      }
     }
   }
+  A sums[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) sums[k] = A(2) * cross[k] + sq[k];
   row_sums<A, K>(sums, &red[1][0][0], tpr);
 
   A r[K + 1];
@@ -183,28 +204,41 @@ __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
   for (int ch = 0; ch < CHUNKS; ++ch) {
     const int col = (ch * tpr + tid) * V;
     if (col >= n) continue;
-    Vec<T, V> wv, bv;
-    if (w != nullptr) wv = load_vec<T, V>(w + col);
-    if (b != nullptr) bv = load_vec<T, V>(b + col);
+    A wf[V], bf[V];
+    if (w != nullptr) {
+      unpack_vec(load_vec<T, V>(w + col), wf);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) wf[e] = A(1);
+    }
+    if (b != nullptr) {
+      unpack_vec(load_vec<T, V>(b + col), bf);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) bf[e] = A(0);
+    }
+    A f[K + 1][V];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) unpack_vec(raw[ch][k], f[k]);
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       A c[K + 1];
 #pragma unroll
-      for (int k = 0; k <= K; ++k) c[k] = to_acc(raw[ch][k].v[e]) - mean[k];
-      const A we = (w != nullptr) ? to_acc(wv.v[e]) : A(1);
-      // The result overwrites the consumed input vector in place.
+      for (int k = 0; k <= K; ++k) c[k] = (LAYER ? f[k][e] - mean[k] : f[k][e]) * wf[e];
+      // y_k = sum_i (w c_i) r_{k-i}, written over the consumed inputs.
 #pragma unroll
-      for (int k = 0; k <= K; ++k) {
+      for (int k = K; k >= 0; --k) {
         A s = c[0] * r[k];
 #pragma unroll
-        for (int i = 1; i <= k; ++i) s += c[i] * r[k - i];
-        s *= we;
-        if (k == 0 && b != nullptr) s += to_acc(bv.v[e]);
-        raw[ch][k].v[e] = from_acc<T>(s);
+        for (int i = 1; i <= k; ++i) s = fma(c[i], r[k - i], s);
+        f[k][e] = (k == 0) ? s + bf[e] : s;
       }
     }
 #pragma unroll
-    for (int k = 0; k <= K; ++k) store_vec<T, V>(y.p[k] + base + col, raw[ch][k]);
+    for (int k = 0; k <= K; ++k) {
+      pack_vec(f[k], raw[ch][k]);
+      store_vec_nt<T, V>(y.p[k] + base + col, raw[ch][k]);
+    }
   }
 }
 

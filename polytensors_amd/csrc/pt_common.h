@@ -56,17 +56,20 @@ template <>
 __device__ __forceinline__ _Float16 from_acc<_Float16>(float x) {
   return static_cast<_Float16>(x);
 }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to two bfloat16 in one 32-bit word (a in the low half) with
+// gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const floatx2_t f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
 template <>
 __device__ __forceinline__ bf16 from_acc<bf16>(float x) {
-  // Round to nearest, ties to even; NaN stays a quiet NaN.
-  uint32_t u = __float_as_uint(x);
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x0040u);
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = static_cast<uint16_t>(pack_bf16x2(x, 0.0f));
   return r;
 }
 
@@ -90,11 +93,71 @@ __device__ __forceinline__ void store_vec(T* p, const Vec<T, V>& v) {
   *reinterpret_cast<Vec<T, V>*>(p) = v;
 }
 
+// Streaming (non-temporal) 16-byte accesses, for data touched exactly once.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+template <typename T, int V>
+__device__ __forceinline__ Vec<T, V> load_vec_nt(const T* p) {
+  static_assert(sizeof(Vec<T, V>) == 16, "16-byte vectors only");
+  return __builtin_bit_cast(Vec<T, V>, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+}
+template <typename T, int V>
+__device__ __forceinline__ void store_vec_nt(T* p, const Vec<T, V>& v) {
+  static_assert(sizeof(Vec<T, V>) == 16, "16-byte vectors only");
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
+}
+
+// Storage vector <-> arithmetic values. bfloat16 pairs are unpacked from
+// 32-bit words with one shift or mask each and packed with one conversion
+// instruction per pair.
+template <typename T, int V>
+__device__ __forceinline__ void unpack_vec(const Vec<T, V>& v, typename AccOf<T>::type (&f)[V]) {
+#pragma unroll
+  for (int e = 0; e < V; ++e) f[e] = to_acc(v.v[e]);
+}
+template <int V>
+__device__ __forceinline__ void unpack_vec(const Vec<bf16, V>& v, float (&f)[V]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&v);
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void pack_vec(const typename AccOf<T>::type (&f)[V], Vec<T, V>& v) {
+#pragma unroll
+  for (int e = 0; e < V; ++e) v.v[e] = from_acc<T>(f[e]);
+}
+template <int V>
+__device__ __forceinline__ void pack_vec(const float (&f)[V], Vec<bf16, V>& v) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+  for (int i = 0; i < V / 2; ++i) w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+}
+
 // ---- wave and block reductions (fixed order: deterministic) ---------------
 template <typename A>
 __device__ __forceinline__ A wave_sum(A x) {
 #pragma unroll
   for (int off = kWave / 2; off >= 1; off >>= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+// float: DPP moves within each row of 16 lanes (quad swaps, half-row and row
+// mirrors), then two lane exchanges across rows. Each step adds a lane's
+// value to its partner's, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_mov<0xB1>(x);    // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);    // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);   // row_half_mirror
+  x += dpp_mov<0x140>(x);   // row_mirror
+  x += __shfl_xor(x, 16, kWave);
+  x += __shfl_xor(x, 32, kWave);
   return x;
 }
 
