@@ -9,6 +9,13 @@
 // i + j <= K into K+1 accumulators, so each staged operand is reused by all
 // pairs of its k-diagonals.
 //
+// The operands' order counts (1 for an ordinary tensor, K+1 for a series) are
+// template parameters: the pair set is fixed at compile time, so the MFMA
+// sequence has no branches and issues back to back. The next chunk's global
+// loads are issued into registers before the current chunk's MFMAs, so their
+// latency hides behind the matrix work; the registers are committed to LDS
+// between two barriers.
+//
 // LDS layout: As[order][row][k], Bs[order][col][k], k contiguous with a
 // 16-byte pad per row. Within a chunk the contraction index is permuted: MFMA
 // step s uses k = (lane / M) * RUN + s, so each lane reads its RUN operand
@@ -17,15 +24,18 @@
 // bank-conflict-free.
 #pragma once
 
+#include <algorithm>
+
 #include "cauchy_matmul.h"
 #include "mfma.h"
 
 namespace pt {
 
-template <typename T, int K, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool TRANS_B, bool VEC>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kernel(
-    CPtrs<T> A, int a_orders, CPtrs<T> B, int b_orders, MPtrs<T> C, int M, int N, int Kd,
-    int64_t a_bs, int64_t b_bs) {
+template <typename T, int K, int AO, int BO, int BM, int BN, int BK, int WAVES_M, int WAVES_N,
+          int MIN_WAVES, bool TRANS_B, bool VEC>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) __attribute__((amdgpu_waves_per_eu(MIN_WAVES)))
+void cauchy_matmul_kernel(
+    CPtrs<T> A, CPtrs<T> B, MPtrs<T> C, int M, int N, int Kd, int64_t a_bs, int64_t b_bs) {
   using MF = Mfma<T>;
   using acc_t = typename MF::acc_t;
   constexpr int THREADS = WAVES_M * WAVES_N * kWave;
@@ -35,12 +45,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kerne
   constexpr int QV = 16 / sizeof(T);          // values per 16-byte LDS read
   constexpr int V = 16 / sizeof(T);           // values per 16-byte global load
   constexpr int LDK = BK + 16 / sizeof(T);    // padded row length
+  constexpr int NA = BM * BK / V / THREADS;   // A vectors per thread and order
+  constexpr int NB = BN * BK / V / THREADS;   // B vectors per thread and order
   static_assert(FM * MF::M == WM && FN * MF::N == WN, "wave tile must be whole MFMA blocks");
   static_assert(RUN % QV == 0, "chunk must give whole 16-byte runs");
-  static_assert((BM * BK / V) % THREADS == 0 && (BN * BK / V) % THREADS == 0, "whole loads per thread");
+  static_assert(NA * V * THREADS == BM * BK && NB * V * THREADS == BN * BK, "whole vectors per thread");
+  static_assert((AO == 1 || AO == K + 1) && (BO == 1 || BO == K + 1), "operand orders are 1 or K+1");
 
-  __shared__ T As[K + 1][BM][LDK];
-  __shared__ T Bs[K + 1][BN][LDK];
+  __shared__ T As[AO][BM][LDK];
+  __shared__ T Bs[BO][BN][LDK];
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -48,13 +61,94 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kerne
   const int tile_m = blockIdx.y * BM, tile_n = blockIdx.x * BN;
   const int64_t batch = blockIdx.z;
 
-  const T* a_base[K + 1];
-  const T* b_base[K + 1];
+  const T* a_base[AO];
+  const T* b_base[BO];
 #pragma unroll
-  for (int o = 0; o <= K; ++o) {
-    a_base[o] = (o < a_orders) ? A.p[o] + batch * a_bs : nullptr;
-    b_base[o] = (o < b_orders) ? B.p[o] + batch * b_bs : nullptr;
-  }
+  for (int o = 0; o < AO; ++o) a_base[o] = A.p[o] + batch * a_bs;
+#pragma unroll
+  for (int o = 0; o < BO; ++o) b_base[o] = B.p[o] + batch * b_bs;
+
+  // ---- global -> registers (one chunk), zero outside the matrices ----
+  Vec<T, V> ra[AO][NA], rb[BO][NB];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int o = 0; o < AO; ++o)
+#pragma unroll
+      for (int it = 0; it < NA; ++it) {
+        const int v = it * THREADS + threadIdx.x;
+        const int gr = tile_m + v / (BK / V), gk = k0 + (v % (BK / V)) * V;
+        const T* p = a_base[o] + static_cast<int64_t>(gr) * Kd + gk;
+        if constexpr (VEC) {   // Kd % V == 0: a vector is wholly inside or outside
+          if (gr < M && gk < Kd) {
+            ra[o][it] = load_vec<T, V>(p);
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) ra[o][it].v[e] = T(0);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) ra[o][it].v[e] = (gr < M && gk + e < Kd) ? p[e] : T(0);
+        }
+      }
+#pragma unroll
+    for (int o = 0; o < BO; ++o)
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        const int v = it * THREADS + threadIdx.x;
+        if constexpr (TRANS_B) {   // B stored [N][Kd]
+          const int gn = tile_n + v / (BK / V), gk = k0 + (v % (BK / V)) * V;
+          const T* p = b_base[o] + static_cast<int64_t>(gn) * Kd + gk;
+          if constexpr (VEC) {
+            if (gn < N && gk < Kd) {
+              rb[o][it] = load_vec<T, V>(p);
+            } else {
+#pragma unroll
+              for (int e = 0; e < V; ++e) rb[o][it].v[e] = T(0);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) rb[o][it].v[e] = (gn < N && gk + e < Kd) ? p[e] : T(0);
+          }
+        } else {                   // B stored [Kd][N]: a vector runs along n
+          const int gk = k0 + v / (BN / V), gn = tile_n + (v % (BN / V)) * V;
+          const T* p = b_base[o] + static_cast<int64_t>(gk) * N + gn;
+          if constexpr (VEC) {     // N % V == 0
+            if (gk < Kd && gn < N) {
+              rb[o][it] = load_vec<T, V>(p);
+            } else {
+#pragma unroll
+              for (int e = 0; e < V; ++e) rb[o][it].v[e] = T(0);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) rb[o][it].v[e] = (gk < Kd && gn + e < N) ? p[e] : T(0);
+          }
+        }
+      }
+  };
+  // ---- registers -> LDS (B transposed to [n][k] when stored [Kd][N]) ----
+  auto commit = [&]() {
+#pragma unroll
+    for (int o = 0; o < AO; ++o)
+#pragma unroll
+      for (int it = 0; it < NA; ++it) {
+        const int v = it * THREADS + threadIdx.x;
+        store_vec<T, V>(&As[o][v / (BK / V)][(v % (BK / V)) * V], ra[o][it]);
+      }
+#pragma unroll
+    for (int o = 0; o < BO; ++o)
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        const int v = it * THREADS + threadIdx.x;
+        if constexpr (TRANS_B) {
+          store_vec<T, V>(&Bs[o][v / (BK / V)][(v % (BK / V)) * V], rb[o][it]);
+        } else {
+          const int kk = v / (BN / V), nv = (v % (BN / V)) * V;
+#pragma unroll
+          for (int e = 0; e < V; ++e) Bs[o][nv + e][kk] = rb[o][it].v[e];
+        }
+      }
+  };
 
   acc_t acc[K + 1][FM][FN];
 #pragma unroll
@@ -64,110 +158,30 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kerne
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) acc[o][fm][fn] = MF::zero();
 
-  for (int k0 = 0; k0 < Kd; k0 += BK) {
-    __syncthreads();   // the previous chunk's operands are consumed
-    // ---- stage A (row-major [M][Kd]) into As[o][r][k] ----
-#pragma unroll
-    for (int o = 0; o <= K; ++o) {
-      if (o >= a_orders) break;
-      if constexpr (VEC) {
-#pragma unroll
-        for (int it = 0; it < BM * BK / V / THREADS; ++it) {
-          const int v = it * THREADS + threadIdx.x;
-          const int r = v / (BK / V), kv = (v % (BK / V)) * V;
-          const int gr = tile_m + r, gk = k0 + kv;
-          Vec<T, V> x;
-          if (gr < M && gk < Kd) {
-            x = load_vec<T, V>(a_base[o] + static_cast<int64_t>(gr) * Kd + gk);
-          } else {
-#pragma unroll
-            for (int e = 0; e < V; ++e) x.v[e] = T(0);
-          }
-          store_vec<T, V>(&As[o][r][kv], x);
-        }
-      } else {
-        for (int idx = threadIdx.x; idx < BM * BK; idx += THREADS) {
-          const int r = idx / BK, kk = idx % BK;
-          const int gr = tile_m + r, gk = k0 + kk;
-          As[o][r][kk] = (gr < M && gk < Kd) ? a_base[o][static_cast<int64_t>(gr) * Kd + gk] : T(0);
-        }
-      }
-    }
-    // ---- stage B into Bs[o][n][k] ----
-#pragma unroll
-    for (int o = 0; o <= K; ++o) {
-      if (o >= b_orders) break;
-      if constexpr (TRANS_B) {   // B stored [N][Kd]
-        if constexpr (VEC) {
-#pragma unroll
-          for (int it = 0; it < BN * BK / V / THREADS; ++it) {
-            const int v = it * THREADS + threadIdx.x;
-            const int n = v / (BK / V), kv = (v % (BK / V)) * V;
-            const int gn = tile_n + n, gk = k0 + kv;
-            Vec<T, V> x;
-            if (gn < N && gk < Kd) {
-              x = load_vec<T, V>(b_base[o] + static_cast<int64_t>(gn) * Kd + gk);
-            } else {
-#pragma unroll
-              for (int e = 0; e < V; ++e) x.v[e] = T(0);
-            }
-            store_vec<T, V>(&Bs[o][n][kv], x);
-          }
-        } else {
-          for (int idx = threadIdx.x; idx < BN * BK; idx += THREADS) {
-            const int n = idx / BK, kk = idx % BK;
-            const int gn = tile_n + n, gk = k0 + kk;
-            Bs[o][n][kk] = (gn < N && gk < Kd) ? b_base[o][static_cast<int64_t>(gn) * Kd + gk] : T(0);
-          }
-        }
-      } else {                   // B stored [Kd][N]: transpose while staging
-        if constexpr (VEC) {
-#pragma unroll
-          for (int it = 0; it < BN * BK / V / THREADS; ++it) {
-            const int v = it * THREADS + threadIdx.x;
-            const int kk = v / (BN / V), nv = (v % (BN / V)) * V;
-            const int gk = k0 + kk, gn = tile_n + nv;
-            Vec<T, V> x;
-            if (gk < Kd && gn < N) {
-              x = load_vec<T, V>(b_base[o] + static_cast<int64_t>(gk) * N + gn);
-            } else {
-#pragma unroll
-              for (int e = 0; e < V; ++e) x.v[e] = T(0);
-            }
-#pragma unroll
-            for (int e = 0; e < V; ++e) Bs[o][nv + e][kk] = x.v[e];
-          }
-        } else {
-          for (int idx = threadIdx.x; idx < BN * BK; idx += THREADS) {
-            const int kk = idx / BN, n = idx % BN;
-            const int gk = k0 + kk, gn = tile_n + n;
-            Bs[o][n][kk] = (gk < Kd && gn < N) ? b_base[o][static_cast<int64_t>(gk) * N + gn] : T(0);
-          }
-        }
-      }
-    }
+  const int row_a = wm * WM + lane % MF::M;
+  const int col_b = wn * WN + lane % MF::N;
+  const int kbase = (lane / MF::M) * RUN;
+  const int chunks = (Kd + BK - 1) / BK;
+  fetch(0);
+  for (int c = 0; c < chunks; ++c) {
+    __syncthreads();   // every wave is done reading the previous chunk
+    commit();
     __syncthreads();
+    if (c + 1 < chunks) fetch((c + 1) * BK);   // in flight during this chunk's MFMAs
 
-    // ---- MFMAs of every (i, j) pair with i + j <= K ----
-    const int row_a = wm * WM + lane % MF::M;
-    const int col_b = wn * WN + lane % MF::N;
-    const int kbase = (lane / MF::M) * RUN;
 #pragma unroll
     for (int q = 0; q < RUN / QV; ++q) {
-      Vec<T, QV> av[K + 1][FM], bv[K + 1][FN];
+      Vec<T, QV> av[AO][FM], bv[BO][FN];
 #pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        if (o < a_orders) {
+      for (int o = 0; o < AO; ++o)
 #pragma unroll
-          for (int fm = 0; fm < FM; ++fm)
-            av[o][fm] = *reinterpret_cast<const Vec<T, QV>*>(&As[o][row_a + fm * MF::M][kbase + q * QV]);
-        }
-        if (o < b_orders) {
+        for (int fm = 0; fm < FM; ++fm)
+          av[o][fm] = *reinterpret_cast<const Vec<T, QV>*>(&As[o][row_a + fm * MF::M][kbase + q * QV]);
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-            bv[o][fn] = *reinterpret_cast<const Vec<T, QV>*>(&Bs[o][col_b + fn * MF::N][kbase + q * QV]);
-        }
-      }
+      for (int o = 0; o < BO; ++o)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          bv[o][fn] = *reinterpret_cast<const Vec<T, QV>*>(&Bs[o][col_b + fn * MF::N][kbase + q * QV]);
 #pragma unroll
       for (int ss = 0; ss < QV; ++ss) {
 #pragma unroll
@@ -175,7 +189,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kerne
 #pragma unroll
           for (int i = 0; i <= k; ++i) {
             const int j = k - i;
-            if (i < a_orders && j < b_orders) {
+            if (i < AO && j < BO) {   // compile-time after unrolling
 #pragma unroll
               for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -206,20 +220,61 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void cauchy_matmul_kerne
   }
 }
 
-// Tile shapes: 64x64 output tiles, 4 waves of 32x32 each (one 32x32x2 fp32
-// MFMA block, or 2x2 16x16x4 fp64 blocks), contraction chunk 16 -- 8 for fp64
-// at degree 8, whose 9 staged orders of A and B would otherwise pass the
-// 160 KB of LDS a workgroup can hold.
-template <typename T, int K>
+// Zero orders 1..degree of C (both operands ordinary: only C_0 is a product).
+template <typename T>
+__global__ __launch_bounds__(256) void cauchy_zero_orders_kernel(MPtrs<T> C, int degree, int64_t count) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int o = 1; o <= degree; ++o)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride)
+      C.p[o][i] = T(0);
+}
+
+// Tile shapes: 4 waves in a 2x2 grid. fp32: 64x64 output tiles, one 32x32x2
+// MFMA block per wave. fp64: 64x64 tiles (2x2 16x16x4 blocks per wave) up to
+// degree 3, and 32x32 tiles (one block per wave) from degree 4, where K+1
+// accumulator sets of 2x2 blocks would no longer fit the register file.
+// Contraction chunk 16: at most 9 orders of both operands, 92 KB of LDS.
+// MIN_WAVES asks the register allocator for two
+// waves per SIMD (at most 256 registers per lane) where the accumulators, the
+// prefetched chunk and the MFMA operands fit without spilling, and otherwise
+// lets a wave use the whole register file.
+template <typename T, int K, int AO, int BO>
 struct CauchyTile {
-  static constexpr int BM = 64, BN = 64, WAVES_M = 2, WAVES_N = 2;
-  static constexpr int BK = (sizeof(T) == 8 && K >= 8) ? 8 : 16;
-  static_assert((K + 1) * (BM + BN) * (BK + 16 / sizeof(T)) * sizeof(T) <= 160 * 1024, "LDS budget");
+  static constexpr bool kSmallTile = sizeof(T) == 8 && K >= 4;
+  static constexpr int BM = kSmallTile ? 32 : 64, BN = BM, WAVES_M = 2, WAVES_N = 2;
+  static constexpr int BK = 16;
+  static constexpr bool kOneSeries = (AO == 1) || (BO == 1);
+  static constexpr int kMaxDegreeTwoWaves =
+      sizeof(T) == 4 ? (kOneSeries ? 7 : 5) : (kSmallTile ? (kOneSeries ? 8 : 6) : (kOneSeries ? 3 : 2));
+  static constexpr int MIN_WAVES = K <= kMaxDegreeTwoWaves ? 2 : 1;
+  static_assert(AO * BM * (BK + 16 / sizeof(T)) * sizeof(T) + BO * BN * (BK + 16 / sizeof(T)) * sizeof(T) <=
+                    160 * 1024, "LDS budget");
 };
+
+template <typename T, int K, int AO, int BO>
+static int launch_cauchy_orders(const CauchyArgs& a, const CPtrs<T>& A, const CPtrs<T>& B,
+                                const MPtrs<T>& C, bool vec) {
+  using Tile = CauchyTile<T, K, AO, BO>;
+  const dim3 grid((a.n + Tile::BN - 1) / Tile::BN, (a.m + Tile::BM - 1) / Tile::BM, a.batch);
+  const dim3 block(Tile::WAVES_M * Tile::WAVES_N * kWave);
+  const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), Kd = static_cast<int>(a.k);
+#define PT_CAUCHY_LAUNCH(TB, VV)                                                                   \
+  cauchy_matmul_kernel<T, K, AO, BO, Tile::BM, Tile::BN, Tile::BK, Tile::WAVES_M, Tile::WAVES_N, \
+                       Tile::MIN_WAVES, TB, VV><<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs)
+  if (a.trans_b) {
+    if (vec) PT_CAUCHY_LAUNCH(true, true);
+    else PT_CAUCHY_LAUNCH(true, false);
+  } else {
+    if (vec) PT_CAUCHY_LAUNCH(false, true);
+    else PT_CAUCHY_LAUNCH(false, false);
+  }
+#undef PT_CAUCHY_LAUNCH
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
 
 template <typename T, int K>
 static int launch_cauchy_k(const CauchyArgs& a) {
-  using Tile = CauchyTile<T, K>;
   constexpr int V = 16 / sizeof(T);
   CPtrs<T> A{}, B{};
   MPtrs<T> C{};
@@ -234,22 +289,22 @@ static int launch_cauchy_k(const CauchyArgs& a) {
   }
   for (int o = 0; o <= K; ++o) C.p[o] = static_cast<T*>(a.c[o]);
   vec = vec && a.k % V == 0 && a.a_bs % V == 0 && a.b_bs % V == 0 && (a.trans_b || a.n % V == 0);
-  const dim3 grid((a.n + Tile::BN - 1) / Tile::BN, (a.m + Tile::BM - 1) / Tile::BM, a.batch);
-  const dim3 block(Tile::WAVES_M * Tile::WAVES_N * kWave);
-  const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), Kd = static_cast<int>(a.k);
-#define PT_CAUCHY_LAUNCH(TB, VV)                                                                  \
-  cauchy_matmul_kernel<T, K, Tile::BM, Tile::BN, Tile::BK, Tile::WAVES_M, Tile::WAVES_N, TB, VV> \
-      <<<grid, block, 0, a.stream>>>(A, a.a_orders, B, a.b_orders, C, M, N, Kd, a.a_bs, a.b_bs)
-  if (a.trans_b) {
-    if (vec) PT_CAUCHY_LAUNCH(true, true);
-    else PT_CAUCHY_LAUNCH(true, false);
+  const bool a_series = a.a_orders > 1, b_series = a.b_orders > 1;
+  if constexpr (K == 0) {
+    return launch_cauchy_orders<T, 0, 1, 1>(a, A, B, C, vec);
   } else {
-    if (vec) PT_CAUCHY_LAUNCH(false, true);
-    else PT_CAUCHY_LAUNCH(false, false);
+    if (a_series && b_series) return launch_cauchy_orders<T, K, K + 1, K + 1>(a, A, B, C, vec);
+    if (a_series) return launch_cauchy_orders<T, K, K + 1, 1>(a, A, B, C, vec);
+    if (b_series) return launch_cauchy_orders<T, K, 1, K + 1>(a, A, B, C, vec);
+    // Two ordinary operands: C_0 = A_0 B_0 and zero higher orders.
+    int st = launch_cauchy_orders<T, 0, 1, 1>(a, A, B, C, vec);
+    if (st != PT_OK) return st;
+    const int64_t count = a.batch * a.m * a.n;
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 4096);
+    cauchy_zero_orders_kernel<T><<<dim3(blocks), dim3(256), 0, a.stream>>>(C, K, count);
+    PT_LAUNCH_CHECK();
+    return PT_OK;
   }
-#undef PT_CAUCHY_LAUNCH
-  PT_LAUNCH_CHECK();
-  return PT_OK;
 }
 
 template <typename T>

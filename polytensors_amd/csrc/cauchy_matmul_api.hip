@@ -23,7 +23,7 @@ int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
   PT_REQUIRE(a_batch_stride >= 0 && b_batch_stride >= 0, PT_INVALID_ARGUMENT,
              "Cauchy matmul: negative batch stride");
   PT_REQUIRE(m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX && batch <= 65535 &&
-                 (m + 63) / 64 <= 65535,
+                 (m + 31) / 32 <= 65535,
              PT_UNSUPPORTED, "Cauchy matmul: sizes beyond the launch grid");
   for (int o = 0; o < a_orders; ++o)
     PT_REQUIRE(a[o] != nullptr, PT_INVALID_ARGUMENT, "Cauchy matmul: null A coefficient");
