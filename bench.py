@@ -1,7 +1,8 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce]
-                    [--no-cpu-baseline] [--no-components] [--copy-calibration]
+                    [--no-cpu-baseline] [--no-components] [--component-seconds S]
+                    [--copy-calibration]
 
 One step is one launch of the workload's fused kernel on one batch of synthetic
 input already resident in HBM (inputs are generated on the device with a
@@ -234,9 +235,15 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def measure(name, device, steps, warmup):
+def measure(name, device, steps, warmup, min_seconds=0.0):
+    """Time ``steps`` steps (raised so the timed region lasts at least ``min_seconds``)."""
     w = WORKLOADS[name](device)
+    if min_seconds > 0:
+        estimate = time_steps(w["step"], 3, warmup)
+        steps = max(steps, math.ceil(min_seconds * 1e3 / max(estimate, 1e-3)))
+        warmup = 1
     ms = time_steps(w["step"], steps, warmup)
+    w["steps"] = steps
     achieved = w["work"] / (ms * 1e-3) / (1e12 if w["unit"] == "TFLOP/s" else 1e9)
     w.update(ms=ms, achieved=achieved)
     return w
@@ -250,6 +257,8 @@ def main():
     parser.add_argument("--workload", default="attention", choices=sorted(WORKLOADS))
     parser.add_argument("--no-components", action="store_true", help="skip timing the other three kernels")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--component-seconds", type=float, default=0.2,
+                        help="minimum timed duration of each component kernel (0: steps/2 steps)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain 1 GiB device copy (scales rocprof FETCH_SIZE/WRITE_SIZE)")
     args = parser.parse_args()
@@ -293,9 +302,10 @@ def main():
         for name in sorted(WORKLOADS):
             if name == args.workload:
                 continue
-            c = measure(name, device, max(3, args.steps // 2), 2)
-            comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "achieved": round(c["achieved"], 3),
-                           "unit": c["unit"], "frac": round(c["achieved"] / c["peak"], 4)}
+            c = measure(name, device, max(3, args.steps // 2), 2, min_seconds=args.component_seconds)
+            comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "steps": c["steps"],
+                           "achieved": round(c["achieved"], 3), "unit": c["unit"],
+                           "frac": round(c["achieved"] / c["peak"], 4)}
             del c
             torch.cuda.empty_cache()
         line["components"] = comps
