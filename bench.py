@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce|activation]
                     [--no-cpu-baseline] [--no-components] [--component-seconds S]
                     [--copy-calibration]
 
@@ -133,7 +133,27 @@ def wl_ce(device):
                 cpu=lambda: cpu_ce(rows, classes, K))
 
 
-WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce}
+def wl_activation(device):
+    """Activation series: GELU (erf form) of a degree-4 bf16 [8192, 4096] series (config 4a's shape)."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, rows, n = 4, 8192, 4096
+    g = _gen(5, device)
+    x = [(torch.randn(rows, n, generator=g, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+
+    def step():
+        return _ops.activation_series(x, "gelu")
+
+    nbytes = 2 * (K + 1) * rows * n * 2
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+                kernel="activation_series", dtype="bf16",
+                workload=f"gelu_series [{K + 1},{rows},{n}] bf16",
+                cpu=lambda: cpu_activation(rows, n, K))
+
+
+WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
+             "activation": wl_activation}
 
 
 # ---------------------------------------------------------------------------
@@ -171,7 +191,7 @@ def cpu_matmul(n, K):
     import torch
     import oracle
 
-    rows = n // 8
+    rows = n // 4
     g = torch.Generator().manual_seed(1)
     a = [torch.randn(rows, n, generator=g) * 0.5 ** k for k in range(K + 1)]
     b = [torch.randn(n, n, generator=g) * 0.5 ** k for k in range(K + 1)]
@@ -184,26 +204,36 @@ def cpu_norm(rows, n, K):
     import torch
     import oracle
 
-    rows = rows // 16
     g = torch.Generator().manual_seed(3)
     x = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
     w = [(1 + 0.02 * torch.randn(n, generator=g)).to(torch.bfloat16)]
     t = _cpu_time(lambda: oracle.rms_norm(x, (n,), weight=w, eps=1e-6))
     nbytes = 2 * (K + 1) * rows * n * 2
-    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"{rows} of 8192 rows, n={n} K={K} bf16", seconds=t)
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"all {rows} rows, n={n} K={K} bf16", seconds=t)
 
 
 def cpu_ce(rows, classes, K):
     import torch
     import oracle
 
-    rows = rows // 32
+    rows = rows // 8
     g = torch.Generator().manual_seed(4)
     z = [torch.randn(rows, classes, generator=g) * (2.0 if k == 0 else 0.5 ** k) for k in range(K + 1)]
     y = torch.randint(0, classes, (rows,), generator=g)
     t = _cpu_time(lambda: oracle.cross_entropy(z, y))
     nbytes = (K + 1) * rows * classes * 4
     return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"{rows} of 8192 rows, C={classes} K={K} fp32", seconds=t)
+
+
+def cpu_activation(rows, n, K):
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(5)
+    x = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    t = _cpu_time(lambda: oracle.activation(x, "gelu"))
+    nbytes = 2 * (K + 1) * rows * n * 2
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"all {rows} rows, n={n} K={K} bf16", seconds=t)
 
 
 # ---------------------------------------------------------------------------
@@ -297,6 +327,7 @@ def main():
                      "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4),
                      "traffic": profiled_traffic(w["kernel"])},
     }
+    cpu_samplers = {}
     if not args.no_components:
         comps = {}
         for name in sorted(WORKLOADS):
@@ -305,16 +336,23 @@ def main():
             c = measure(name, device, max(3, args.steps // 2), 2, min_seconds=args.component_seconds)
             comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "steps": c["steps"],
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
-                           "frac": round(c["achieved"] / c["peak"], 4)}
+                           "frac": round(c["achieved"] / c["peak"], 4), "traffic": profiled_traffic(c["kernel"])}
+            cpu_samplers[name] = c["cpu"]
             del c
             torch.cuda.empty_cache()
         line["components"] = comps
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
-        cpu = w["cpu"]()
-        line["cpu_baseline"] = {"value": round(cpu["value"], 6), "unit": cpu["unit"], "cores": torch.get_num_threads(),
-                                "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3)}
+
+        def cpu_entry(sampler):
+            cpu = sampler()
+            return {"value": round(cpu["value"], 6), "unit": cpu["unit"], "cores": torch.get_num_threads(),
+                    "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3)}
+
+        line["cpu_baseline"] = cpu_entry(w["cpu"])
+        for name, sampler in cpu_samplers.items():   # the reference's CPU path beside each component
+            line["components"][name]["cpu_baseline"] = cpu_entry(sampler)
     print(json.dumps(line), flush=True)
 
 

@@ -175,6 +175,56 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
                             int64_t lq, int64_t lk, int64_t d, int causal,
                             const uint8_t* mask, double scale, void* stream);
 
+/* Activation kinds of pt_activation_series_fwd / _bwd. */
+typedef enum pt_activation {
+  PT_ACT_GELU = 0,      /* x * Phi(x) (erf form, torch approximate='none') */
+  PT_ACT_GELU_TANH = 1, /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) */
+  PT_ACT_TANH = 2,
+  PT_ACT_SIGMOID = 3,
+  PT_ACT_SILU = 4,      /* x * sigmoid(x) */
+  PT_ACT_EXP = 5,       /* forward only */
+  PT_ACT_LOG = 6        /* forward only */
+} pt_activation;
+
+/*
+ * Elementwise activation of a degree-K series: y(t) = f(x(t)).
+ * x, y: K+1 pointers, each `numel` elements of `dtype` (any shape, dense).
+ * Arithmetic float32 (float64 for PT_FLOAT64); order 0 is f(x_0).
+ * Replaces the fused degree-1 activation of the reference
+ *   /root/reference/src/polytensors/_fused_activation.py:5-24 (maybe_activation),
+ *   /root/reference/src/polytensors/_activation_kernels.py:8-38 (_activation),
+ * generalised to degree K with the series of its plain-range rules
+ *   /root/reference/src/polytensors/_plain.py:153-171 (plain_exp, plain_log),
+ *   /root/reference/src/polytensors/_plain.py:174-259 (plain_activation: gelu,
+ *   tanh, sigmoid by Faa di Bruno composition), dispatched from
+ *   /root/reference/src/polytensors/_plain.py:276-355 (plain_rule),
+ * and for silu / gelu_tanh the jets of
+ *   /root/reference/src/polytensors/_activations.py:89-115 (_scalar_taylor),
+ *   dispatched from /root/reference/src/polytensors/_dispatch.py:460-473.
+ */
+int pt_activation_series_fwd(int dtype, int degree, int kind,
+                             const void* const* x, void* const* y,
+                             int64_t numel, void* stream);
+
+/*
+ * Gradient series of the native activation backward operations:
+ *   dx(t) = g(t) * f'(x(t)), Cauchy product truncated at K.
+ * saved: for PT_ACT_GELU, PT_ACT_GELU_TANH and PT_ACT_SILU the forward INPUT
+ *        series x; for PT_ACT_TANH and PT_ACT_SIGMOID the forward OUTPUT
+ *        series y (as aten.tanh_backward / aten.sigmoid_backward take it).
+ * g, saved, dx: K+1 pointers, each `numel` elements of `dtype`.
+ * PT_ACT_EXP and PT_ACT_LOG return PT_UNSUPPORTED.
+ * Replaces the BACKWARD mode of
+ *   /root/reference/src/polytensors/_activation_kernels.py:8-38 (degree 1),
+ * generalised with the reference's gradient-series rules
+ *   /root/reference/src/polytensors/_plain.py:333-348 (gelu_backward,
+ *   tanh_backward, sigmoid_backward) and
+ *   /root/reference/src/polytensors/_dispatch.py:629-630 (silu_backward).
+ */
+int pt_activation_series_bwd(int dtype, int degree, int kind,
+                             const void* const* g, const void* const* saved,
+                             void* const* dx, int64_t numel, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,7 +2,8 @@
 
 A restatement, in plain PyTorch on the CPU, of the reference's plain-range
 general series rules for the four fused operations (Cauchy-product matmul,
-scaled-dot-product attention, RMSNorm/LayerNorm, cross entropy). Each function
+scaled-dot-product attention, RMSNorm/LayerNorm, cross entropy) and of the
+elementwise activation series (oracle/activations.py). Each function
 cites the reference file:line it follows.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
@@ -17,3 +18,4 @@ values the reference's own tests hold, and against brute-force sums.
 
 from .series import cauchy, exp_series, log_series, rsqrt_series, softmax_family  # noqa: F401
 from .paths import attention, cross_entropy, layer_norm, matmul, rms_norm  # noqa: F401
+from .activations import activation, activation_backward  # noqa: F401

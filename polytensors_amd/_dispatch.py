@@ -7,11 +7,16 @@ Only the rules the hot path needs exist here:
     operand (the constant-operand fast path, _range_ops.py:109-132), sum and
     mean (_range_ops.py:178-193);
   * the matrix products mm/bmm/addmm/mv/dot, which run the Cauchy-product
-    kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84).
+    kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84);
+  * the elementwise activations gelu (erf and tanh forms), tanh, sigmoid,
+    silu, exp, log and the gelu/tanh/sigmoid/silu backward operations, which
+    run the activation-series kernel (the reference's rules,
+    /root/reference/src/polytensors/_plain.py:276-355 and
+    /root/reference/src/polytensors/_dispatch.py:460-473,612-638).
 Every other operation raises NotImplementedError (as the reference does for
 operations without a rule, /root/reference/src/polytensors/_dispatch.py:852):
-nonlinear series arithmetic outside the four fused operations is not part of
-this package.
+nonlinear series arithmetic outside the fused operations is not part of this
+package.
 """
 
 import torch
@@ -37,6 +42,17 @@ _SUB = {aten.sub.Tensor, aten.sub.Scalar}
 _MUL = {aten.mul.Tensor, aten.mul.Scalar}
 _DIV = {aten.div.Tensor, aten.div.Scalar}
 _MATMUL = {aten.mm.default, aten.bmm.default, aten.mv.default, aten.dot.default, aten.matmul.default}
+_ACTIVATION = {aten.tanh.default: "tanh", aten.sigmoid.default: "sigmoid", aten.silu.default: "silu",
+               aten.exp.default: "exp", aten.log.default: "log"}
+# (grad_output, output) for tanh/sigmoid, (grad_output, self) for silu
+_ACTIVATION_BACKWARD = {aten.tanh_backward.default: "tanh", aten.sigmoid_backward.default: "sigmoid",
+                        aten.silu_backward.default: "silu"}
+
+
+def _gelu_kind(approximate):
+    if approximate not in ("none", "tanh"):
+        raise ValueError("GELU approximate must be 'none' or 'tanh'")
+    return "gelu" if approximate == "none" else "gelu_tanh"
 
 
 def _is_poly(x):
@@ -172,7 +188,25 @@ def dispatch(func, types, args=(), kwargs=None):
 
         return _fused_matmul.from_dispatch(func, args, kwargs)
 
+    if func in _ACTIVATION or func is aten.gelu.default:
+        from . import _fused_activation
+
+        if func is aten.gelu.default:
+            kind = _gelu_kind(args[1] if len(args) > 1 else kwargs.get("approximate", "none"))
+        else:
+            kind = _ACTIVATION[func]
+        return _fused_activation.activation(args[0], kind)
+
+    if func in _ACTIVATION_BACKWARD or func is aten.gelu_backward.default:
+        from . import _fused_activation
+
+        if func is aten.gelu_backward.default:
+            kind = _gelu_kind(args[2] if len(args) > 2 else kwargs.get("approximate", "none"))
+        else:
+            kind = _ACTIVATION_BACKWARD[func]
+        return _fused_activation.backward(args[0], args[1], kind)
+
     raise NotImplementedError(
         f"PolyTensor has no rule for {func}: polytensors_amd implements the fused Taylor hot path "
-        "(matmul, scaled_dot_product_attention, rms_norm/layer_norm, cross_entropy) and linear "
-        "shape/arithmetic operations only")
+        "(matmul, scaled_dot_product_attention, rms_norm/layer_norm, cross_entropy, elementwise "
+        "activations) and linear shape/arithmetic operations only")

@@ -17,6 +17,8 @@ ABI_VERSION = 1
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
+# pt_activation codes of include/polytaylor.h
+ACTIVATIONS = {"gelu": 0, "gelu_tanh": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "exp": 5, "log": 6}
 
 DTYPE_CODES = {
     torch.float32: 0,
@@ -45,6 +47,8 @@ SIGNATURES = {
     "pt_taylor_attention_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp, _c_int,
                                          _c_vpp, _c_vpp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp,
                                          _c_dbl, _c_vp]),
+    "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),
+    "pt_activation_series_bwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
 }
 
 

@@ -215,3 +215,52 @@ def _(q, k, v, mask, causal, scale, degree):
     bh, lq, d = q[0].shape
     return (q[0].new_empty((degree + 1, bh, lq, d)),
             q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))
+
+
+# ---------------------------------------------------------------------------
+# Elementwise activation series
+
+@torch.library.custom_op(f"{NAMESPACE}::activation_series", mutates_args=(), device_types="cuda")
+def activation_series(x: List[torch.Tensor], kind: str) -> torch.Tensor:
+    """f(x(t)) for f in _lib.ACTIVATIONS; returns [K+1, *x.shape]."""
+    _check_series("activation_series", x)
+    _require(kind in _lib.ACTIVATIONS, f"activation_series: unknown kind {kind!r}")
+    degree = len(x) - 1
+    out = torch.empty((degree + 1, *x[0].shape), dtype=x[0].dtype, device=x[0].device)
+    lib = _lib.load()
+    status = lib.pt_activation_series_fwd(_lib.DTYPE_CODES[x[0].dtype], degree, _lib.ACTIVATIONS[kind],
+                                          _lib.ptr_array(x), _lib.ptr_array(list(out.unbind(0))),
+                                          x[0].numel(), _lib.stream_of(x[0].device))
+    _lib.check(status, f"activation_series({kind})")
+    return out
+
+
+@activation_series.register_fake
+def _(x, kind):
+    return x[0].new_empty((len(x), *x[0].shape))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::activation_series_backward", mutates_args=(), device_types="cuda")
+def activation_series_backward(grad: List[torch.Tensor], saved: List[torch.Tensor], kind: str) -> torch.Tensor:
+    """grad(t) * f'(x(t)); ``saved`` is the forward input (gelu, gelu_tanh, silu) or output (tanh, sigmoid)."""
+    _check_series("activation_series_backward grad", grad)
+    _check_series("activation_series_backward saved", saved)
+    _require(len(grad) == len(saved) and grad[0].shape == saved[0].shape and grad[0].dtype == saved[0].dtype
+             and grad[0].device == saved[0].device,
+             "activation_series_backward: grad and saved series must match in degree, shape, dtype and device")
+    _require(kind in ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu"),
+             f"activation_series_backward: no backward for kind {kind!r}")
+    degree = len(grad) - 1
+    out = torch.empty((degree + 1, *grad[0].shape), dtype=grad[0].dtype, device=grad[0].device)
+    lib = _lib.load()
+    status = lib.pt_activation_series_bwd(_lib.DTYPE_CODES[grad[0].dtype], degree, _lib.ACTIVATIONS[kind],
+                                          _lib.ptr_array(grad), _lib.ptr_array(saved),
+                                          _lib.ptr_array(list(out.unbind(0))), grad[0].numel(),
+                                          _lib.stream_of(grad[0].device))
+    _lib.check(status, f"activation_series_backward({kind})")
+    return out
+
+
+@activation_series_backward.register_fake
+def _(grad, saved, kind):
+    return grad[0].new_empty((len(grad), *grad[0].shape))

@@ -1,0 +1,6 @@
+// Instantiates the activation-series kernels for one storage type.
+#include "activation_series.inl"
+
+namespace pt {
+template int launch_activation<bf16>(const ActArgs&);
+}  // namespace pt
