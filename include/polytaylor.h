@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 1
+#define PT_ABI_VERSION 2
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -110,11 +110,16 @@ int pt_layer_norm_series_fwd(int dtype, int degree, const void* const* x,
  *           pt_cross_entropy_series_workspace_size(...) bytes (else unused).
  * lse: NULL, or K+1 pointers, each [rows] of the arithmetic type (float32, or
  *      float64 for PT_FLOAT64): the log-sum-exp series of each row.
+ * softcap: 0 for none; else every logit series is first capped as
+ *          softcap * tanh(z(t) / softcap) (the series of the cap), on the fly,
+ *          as the reference's fused kernel caps its degree-1 logits
+ *          (/root/reference/src/polytensors/_cross_entropy_kernels.py:7-17,
+ *          _fused_cross_entropy.py:173-187); lse and loss refer to the capped logits.
  * loss_0 = lse_0 - z_0[y]; loss_k = lse_k - z_k[y] for k >= 1.
  * Replaces the fused degree-1 forward of the reference
- *   /root/reference/src/polytensors/_fused_cross_entropy.py:161-170 (forward),
+ *   /root/reference/src/polytensors/_fused_cross_entropy.py:54-63 (forward),
  *   /root/reference/src/polytensors/_cross_entropy_kernels.py:20-55 (_forward)
- * and its reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:257-277),
+ * and its reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:163-170),
  * generalised to degree K with the log-softmax series of the general rule
  *   /root/reference/src/polytensors/_plain.py:262-273 (plain_softmax_family)
  *   and per-order NLL /root/reference/src/polytensors/_dispatch.py:537-543.
@@ -122,7 +127,7 @@ int pt_layer_norm_series_fwd(int dtype, int degree, const void* const* x,
 int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits,
                                 int64_t rows, int64_t classes, int64_t row_stride,
                                 const int64_t* target, int64_t ignore_index,
-                                int reduction, void* const* loss,
+                                double softcap, int reduction, void* const* loss,
                                 void* const* lse, void* workspace, void* stream);
 
 /* Bytes of device workspace pt_cross_entropy_series_fwd needs for a
@@ -217,7 +222,7 @@ int pt_activation_series_fwd(int dtype, int degree, int kind,
  * Replaces the BACKWARD mode of
  *   /root/reference/src/polytensors/_activation_kernels.py:8-38 (degree 1),
  * generalised with the reference's gradient-series rules
- *   /root/reference/src/polytensors/_plain.py:333-348 (gelu_backward,
+ *   /root/reference/src/polytensors/_plain.py:310-325 (gelu_backward,
  *   tanh_backward, sigmoid_backward) and
  *   /root/reference/src/polytensors/_dispatch.py:629-630 (silu_backward).
  */

@@ -3,12 +3,12 @@
 gelu, tanh and sigmoid follow the reference's plain-range rule: the
 derivatives of the activation at the constant term, composed with the
 series' higher orders by Faa di Bruno
-(/root/reference/src/polytensors/_plain.py:174-262). silu and gelu_tanh have
+(/root/reference/src/polytensors/_plain.py:174-259). silu and gelu_tanh have
 no plain-range rule in the reference; they follow its default-mode jets
 (/root/reference/src/polytensors/_activations.py:89-115): normalized
 derivatives of x*sigmoid(x) and x*sigmoid(2c(x + 0.044715 x^3)) at the
 constant term, composed the same way. exp and log are plain_exp/plain_log
-(_plain.py:153-171). Backward rules are _plain.py:333-348 (gelu, tanh,
+(_plain.py:153-171). Backward rules are _plain.py:310-325 (gelu, tanh,
 sigmoid) and the derivative jets of the same functions (silu, gelu_tanh).
 """
 
@@ -67,7 +67,7 @@ def _gelu_derivatives(x, count, offset=0):
 def _output_polynomial_derivatives(y, count, offset, g):
     """Derivatives P_n(y) of a function with f' = g(f): P_0 = y, P_{n+1} = P_n'(y) g(y).
 
-    /root/reference/src/polytensors/_plain.py:222-245; ``g`` lists polynomial
+    /root/reference/src/polytensors/_plain.py:221-244; ``g`` lists polynomial
     coefficients in increasing powers.
     """
     polynomial = [0.0, 1.0]
@@ -90,7 +90,7 @@ def _output_polynomial_derivatives(y, count, offset, g):
 
 
 def derivatives(kind, x, count, offset=0):
-    """f^(n)(x) for n = offset..offset+count-1, /root/reference/src/polytensors/_plain.py:248-255."""
+    """f^(n)(x) for n = offset..offset+count-1, /root/reference/src/polytensors/_plain.py:246-253."""
     if kind == "gelu":
         return _gelu_derivatives(x, count, offset)
     if kind == "tanh":
@@ -177,9 +177,9 @@ def activation_backward(G, S, kind):
 
     ``S`` is the forward input X for gelu, gelu_tanh, silu, and the forward
     output Y for tanh and sigmoid (as aten.tanh_backward takes it):
-      gelu     G (*) f'(X) with f' composed from derivatives at offset 1 (_plain.py:333-338);
-      tanh     G (*) (1 - Y (*) Y)                                        (_plain.py:339-343);
-      sigmoid  G (*) (Y (*) (1 - Y))                                      (_plain.py:344-348);
+      gelu     G (*) f'(X) with f' composed from derivatives at offset 1 (_plain.py:310-315);
+      tanh     G (*) (1 - Y (*) Y)                                        (_plain.py:316-320);
+      sigmoid  G (*) (Y (*) (1 - Y))                                      (_plain.py:321-325);
       silu, gelu_tanh: G (*) f'(X), f' from the same derivative jets.
     """
     degree = len(S) - 1

@@ -102,12 +102,20 @@ def attention(Q, K, V, attn_mask=None, is_causal=False, scale=None):
     return cauchy(probabilities, V, matmul=True)
 
 
-def cross_entropy(Z, target, ignore_index=-100, reduction="mean"):
+def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
     """Per-order loss series of ``F.cross_entropy(z, target)`` on (N, C) logits.
 
     The log-softmax series (/root/reference/src/polytensors/_plain.py:262-273)
     followed by native NLL on every order (/root/reference/src/polytensors/_dispatch.py:537-543).
+    With ``softcap`` the logits are first ``softcap * tanh(z / softcap)``, the
+    composite of /root/reference/src/polytensors/_fused_cross_entropy.py:184-187:
+    per-coefficient scalar division and product around the plain-range tanh
+    rule (_plain.py:256-259, 303-304).
     """
+    if softcap is not None:
+        from .activations import activation
+
+        Z = [softcap * t for t in activation([z / softcap for z in Z], "tanh")]
     _, log_softmax, _ = softmax_family(Z, 1)
     return [F.nll_loss(lp, target, ignore_index=ignore_index, reduction=reduction) for lp in log_softmax]
 

@@ -7,7 +7,7 @@ loss series is ``lse_k - z_k[y]`` (the log-softmax series of
 per-order NLL of /root/reference/src/polytensors/_dispatch.py:537-543). Rows
 whose target is ``ignore_index`` have zero loss; ``mean`` divides by the
 number of other rows, as ``torch.nn.functional.cross_entropy`` and the
-reference's reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:257-277).
+reference's reductions (/root/reference/src/polytensors/_fused_cross_entropy.py:163-170).
 Arithmetic is float32 (float64 for float64 logits).
 """
 
@@ -46,8 +46,8 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
         return "label smoothing is not implemented"
     if reduction not in _lib.REDUCTIONS:
         return f"unknown reduction {reduction!r}"
-    if softcap is not None:
-        return "softcap is not implemented for series logits"
+    if softcap is not None and not (isinstance(softcap, (int, float)) and 0 < softcap < float("inf")):
+        return "softcap must be a positive finite number"
     return None
 
 
@@ -63,12 +63,18 @@ def _rows(coeffs):
     return [c.contiguous() for c in coeffs]
 
 
-def fused(input, target, ignore_index=-100, reduction="mean"):
-    """Loss series (a PolyTensor in float32, or float64 for float64 logits)."""
+def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
+    """Loss series (a PolyTensor in float32, or float64 for float64 logits).
+
+    ``softcap`` caps the logit series as ``softcap * tanh(z / softcap)`` inside the
+    kernel, as the reference's fused pass does at degree 1
+    (/root/reference/src/polytensors/_cross_entropy_kernels.py:7-17).
+    """
     from ._tensor import PolyTensor
 
     z = _rows(input.coeffs)
-    loss, _ = _ops.cross_entropy_series(z, target.contiguous(), int(ignore_index), _lib.REDUCTIONS[reduction])
+    loss, _ = _ops.cross_entropy_series(z, target.contiguous(), int(ignore_index), _lib.REDUCTIONS[reduction],
+                                        float(softcap) if softcap is not None else 0.0)
     return PolyTensor.from_stacked(loss)
 
 
@@ -81,14 +87,14 @@ def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mea
 
 def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="mean"):
     """``PolyTensor.cross_entropy``: series logits use the fused kernel (at least float32 out);
-    ordinary tensors use the composite, as /root/reference/src/polytensors/_fused_cross_entropy.py:280-294."""
+    ordinary tensors use the composite, as /root/reference/src/polytensors/_fused_cross_entropy.py:173-187."""
     from ._tensor import PolyTensor
 
     if isinstance(logits, PolyTensor):
         reason = why_ineligible(logits, target, None, reduction, 0.0, softcap)
         if reason is not None:
             raise NotImplementedError(f"cross_entropy: {reason}")
-        return fused(logits, target, ignore_index=ignore_index, reduction=reduction)
+        return fused(logits, target, ignore_index=ignore_index, reduction=reduction, softcap=softcap)
     logits = logits.to(torch.promote_types(logits.dtype, torch.float32))
     if softcap is not None:
         logits = softcap * torch.tanh(logits / softcap)

@@ -2,7 +2,7 @@
 
 A ``None`` reason means the call can run on the gfx950 kernels. The reference's
 ``eligible`` functions (/root/reference/src/polytensors/_fused_attention.py:227-256,
-_fused_norm.py:11-21, _fused_cross_entropy.py:238-254) return False and let the
+_fused_norm.py:11-21, _fused_cross_entropy.py:131-147) return False and let the
 caller use the general rules; this package has no general rules, so callers
 turn a reason into NotImplementedError. A missing kernel library on a HIP
 device is never a reason: it raises LibraryMissingError.

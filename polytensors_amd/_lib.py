@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -40,7 +40,7 @@ SIGNATURES = {
     "pt_layer_norm_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_int, _c_vpp, _c_int,
                                           _c_vpp, _c_i64, _c_i64, _c_dbl, _c_vp]),
     "pt_cross_entropy_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
-                                             _c_i64, _c_int, _c_vpp, _c_vpp, _c_vp, _c_vp]),
+                                             _c_i64, _c_dbl, _c_int, _c_vpp, _c_vpp, _c_vp, _c_vp]),
     "pt_cross_entropy_series_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_int]),
     "pt_cauchy_matmul": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp,
                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp]),

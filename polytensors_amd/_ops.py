@@ -82,11 +82,12 @@ def _(x, weight, bias, n, eps, layer):
 
 @torch.library.custom_op(f"{NAMESPACE}::cross_entropy_series", mutates_args=(), device_types="cuda")
 def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_index: int,
-                         reduction: int) -> Tuple[torch.Tensor, torch.Tensor]:
+                         reduction: int, softcap: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-order cross entropy of (N, C) logit series; returns (loss, lse).
 
     loss: [K+1, N] (reduction none) or [K+1] (mean/sum), and lse: [K+1, N], both in
-    float32 (float64 for float64 logits).
+    float32 (float64 for float64 logits). ``softcap`` > 0 caps the logit series as
+    softcap * tanh(z / softcap) first.
     """
     _require(len(z) >= 1, "cross_entropy_series: at least one coefficient is required")
     first = z[0]
@@ -100,6 +101,7 @@ def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_ind
     _require(target.dtype == torch.int64 and target.shape == first.shape[:1] and target.is_contiguous()
              and target.device == first.device, "cross_entropy_series: target must be contiguous int64 [N]")
     _require(reduction in (0, 1, 2), "cross_entropy_series: reduction must be 0, 1 or 2")
+    _require(softcap >= 0.0 and softcap != float("inf"), "cross_entropy_series: softcap must be 0 or a positive cap")
     degree = len(z) - 1
     rows, classes = first.shape
     dtype = first.dtype
@@ -112,14 +114,14 @@ def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_ind
     workspace = torch.empty((max(1, wbytes),), dtype=torch.uint8, device=first.device)
     status = lib.pt_cross_entropy_series_fwd(
         code, degree, _lib.ptr_array(z), rows, classes, first.stride(0) if rows else classes,
-        target.data_ptr(), ignore_index, reduction, _lib.ptr_array(list(loss.unbind(0))),
+        target.data_ptr(), ignore_index, float(softcap), reduction, _lib.ptr_array(list(loss.unbind(0))),
         _lib.ptr_array(list(lse.unbind(0))), workspace.data_ptr(), _lib.stream_of(first.device))
     _lib.check(status, "cross_entropy_series")
     return loss, lse
 
 
 @cross_entropy_series.register_fake
-def _(z, target, ignore_index, reduction):
+def _(z, target, ignore_index, reduction, softcap=0.0):
     rows = z[0].shape[0]
     loss = z[0].new_empty((len(z), rows) if reduction == 0 else (len(z),), dtype=_acc_dtype(z[0].dtype))
     lse = z[0].new_empty((len(z), rows), dtype=_acc_dtype(z[0].dtype))

@@ -255,7 +255,7 @@ class PolyTensor(torch.Tensor):
     @staticmethod
     def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="mean"):
         """Cross entropy of (N, C) logits; returns at least float32 (as the reference's
-        /root/reference/src/polytensors/_fused_cross_entropy.py:280-294)."""
+        /root/reference/src/polytensors/_fused_cross_entropy.py:173-187)."""
         from ._fused_cross_entropy import cross_entropy
 
         return cross_entropy(logits, target, softcap=softcap, ignore_index=ignore_index, reduction=reduction)

@@ -13,6 +13,7 @@ struct CeArgs {
   int64_t row_stride;
   const int64_t* target;
   int64_t ignore_index;
+  double softcap;   // 0: none
   int reduction;
   void* const* loss;
   void* const* lse;

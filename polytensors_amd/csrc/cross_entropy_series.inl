@@ -16,6 +16,7 @@
 #pragma once
 
 #include "cross_entropy_series.h"
+#include "series_math.h"
 
 namespace pt {
 
@@ -51,12 +52,13 @@ __device__ __forceinline__ void rescale(A& m, A new_m, A (&S)[K + 1]) {
 // One block of THREADS threads per row. Logits are read with non-temporal
 // 16-byte loads (each byte is read once; streaming them past the caches lifts
 // the kernel from about 74% to 86% of HBM peak on MI355X), two vectors per
-// order in flight per thread and iteration.
-template <typename T, int K, int THREADS>
+// order in flight per thread and iteration. With CAP every logit series is
+// first replaced by its softcap cap * tanh(z / cap) (series_math.h), on the fly.
+template <typename T, int K, int THREADS, bool CAP>
 __global__ __launch_bounds__(THREADS) void cross_entropy_series_row_kernel(
     CPtrs<T> z, int64_t rows, int64_t classes, int64_t row_stride, bool vec_ok,
     const int64_t* __restrict__ target, int64_t ignore_index, MPtrs<typename AccOf<T>::type> loss,
-    MPtrs<typename AccOf<T>::type> lse) {
+    MPtrs<typename AccOf<T>::type> lse, typename AccOf<T>::type cap, typename AccOf<T>::type inv_cap) {
   using A = typename AccOf<T>::type;
   constexpr int V = VecWidth<T>::value;
   constexpr A kNegInf = -__builtin_huge_val();
@@ -80,44 +82,43 @@ __global__ __launch_bounds__(THREADS) void cross_entropy_series_row_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int k = 0; k <= K; ++k) {
-          const T* p = z.p[k] + base + (j + u * THREADS) * V;
-          a[u][k] = load_vec_nt<T, V>(p);
-        }
+        for (int k = 0; k <= K; ++k) a[u][k] = load_vec_nt<T, V>(z.p[k] + base + (j + u * THREADS) * V);
+      A x[U][V][K + 1];
       A hi = kNegInf;
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int e = 0; e < V; ++e) hi = fmax(hi, to_acc(a[u][0].v[e]));
+        for (int e = 0; e < V; ++e) {
+#pragma unroll
+          for (int k = 0; k <= K; ++k) x[u][e][k] = to_acc(a[u][k].v[e]);
+          if constexpr (CAP) softcap_series<A, K>(x[u][e], cap, inv_cap);
+          hi = fmax(hi, x[u][e][0]);
+        }
       rescale<A, K>(m, hi, S);
       if (m != kNegInf) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int e = 0; e < V; ++e) {
-            A xa[K + 1];
-#pragma unroll
-            for (int k = 0; k <= K; ++k) xa[k] = to_acc(a[u][k].v[e]);
-            accumulate_element<A, K>(xa[0], xa, m, S);
-          }
+          for (int e = 0; e < V; ++e) accumulate_element<A, K>(x[u][e][0], x[u][e], m, S);
       }
     }
     for (; j < nvec; j += THREADS) {
       Vec<T, V> a[K + 1];
 #pragma unroll
       for (int k = 0; k <= K; ++k) a[k] = load_vec_nt<T, V>(z.p[k] + base + j * V);
+      A x[V][K + 1];
       A hi = kNegInf;
 #pragma unroll
-      for (int e = 0; e < V; ++e) hi = fmax(hi, to_acc(a[0].v[e]));
+      for (int e = 0; e < V; ++e) {
+#pragma unroll
+        for (int k = 0; k <= K; ++k) x[e][k] = to_acc(a[k].v[e]);
+        if constexpr (CAP) softcap_series<A, K>(x[e], cap, inv_cap);
+        hi = fmax(hi, x[e][0]);
+      }
       rescale<A, K>(m, hi, S);
       if (m != kNegInf) {
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          A xa[K + 1];
-#pragma unroll
-          for (int k = 0; k <= K; ++k) xa[k] = to_acc(a[k].v[e]);
-          accumulate_element<A, K>(xa[0], xa, m, S);
-        }
+        for (int e = 0; e < V; ++e) accumulate_element<A, K>(x[e][0], x[e], m, S);
       }
     }
     scalar_from = nvec * V;
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(THREADS) void cross_entropy_series_row_kernel(
     A x[K + 1];
 #pragma unroll
     for (int k = 0; k <= K; ++k) x[k] = to_acc(z.p[k][base + col]);
+    if constexpr (CAP) softcap_series<A, K>(x, cap, inv_cap);
     rescale<A, K>(m, x[0], S);
     if (m != kNegInf) accumulate_element<A, K>(x[0], x, m, S);
   }
@@ -177,6 +179,10 @@ __global__ __launch_bounds__(THREADS) void cross_entropy_series_row_kernel(
   const int64_t y = target[row];
   const bool ignored = (y == ignore_index);
   const bool in_range = (y >= 0 && y < classes);
+  A zy[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) zy[k] = in_range ? to_acc(z.p[k][base + y]) : A(0);
+  if constexpr (CAP) softcap_series<A, K>(zy, cap, inv_cap);
 #pragma unroll
   for (int k = 0; k <= K; ++k) {
     A v;
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(THREADS) void cross_entropy_series_row_kernel(
     } else if (!in_range) {
       v = __builtin_nan("");   // an out-of-range class index poisons the loss instead of reading past the row
     } else {
-      v = L[k] - to_acc(z.p[k][base + y]);
+      v = L[k] - zy[k];
     }
     loss.p[k][row] = v;
   }
@@ -239,13 +245,20 @@ static int launch_ce_k(const CeArgs& a) {
   for (int k = 0; k <= K; ++k)
     loss.p[k] = a.reduction == PT_REDUCTION_NONE ? static_cast<A*>(a.loss[k]) : per_row + k * a.rows;
   // Long rows (>= 16 vectors per thread at 256 threads) take 512-thread blocks.
+  const bool cap = a.softcap > 0.0;
+  const A capv = cap ? static_cast<A>(a.softcap) : A(1);
+  const A inv_cap = A(1) / capv;
+#define PT_CE_LAUNCH(TH, CP)                                                                   \
+  cross_entropy_series_row_kernel<T, K, TH, CP><<<dim3(a.rows), dim3(TH), 0, a.stream>>>(     \
+      z, a.rows, a.classes, a.row_stride, vec_ok, a.target, a.ignore_index, loss, lse, capv, inv_cap)
   if (a.classes >= 4096 * static_cast<int64_t>(V)) {
-    cross_entropy_series_row_kernel<T, K, 512><<<dim3(a.rows), dim3(512), 0, a.stream>>>(
-        z, a.rows, a.classes, a.row_stride, vec_ok, a.target, a.ignore_index, loss, lse);
+    if (cap) PT_CE_LAUNCH(512, true);
+    else PT_CE_LAUNCH(512, false);
   } else {
-    cross_entropy_series_row_kernel<T, K, kCeThreads><<<dim3(a.rows), dim3(kCeThreads), 0, a.stream>>>(
-        z, a.rows, a.classes, a.row_stride, vec_ok, a.target, a.ignore_index, loss, lse);
+    if (cap) PT_CE_LAUNCH(kCeThreads, true);
+    else PT_CE_LAUNCH(kCeThreads, false);
   }
+#undef PT_CE_LAUNCH
   PT_LAUNCH_CHECK();
   if (a.reduction != PT_REDUCTION_NONE) {
     MPtrs<A> out{};

@@ -16,7 +16,7 @@ size_t pt_cross_entropy_series_workspace_size(int dtype, int degree, int64_t row
 
 int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits, int64_t rows,
                                 int64_t classes, int64_t row_stride, const int64_t* target,
-                                int64_t ignore_index, int reduction, void* const* loss,
+                                int64_t ignore_index, double softcap, int reduction, void* const* loss,
                                 void* const* lse, void* workspace, void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
@@ -30,6 +30,8 @@ int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits
   PT_REQUIRE(rows >= 0 && classes >= 1 && row_stride >= classes, PT_INVALID_ARGUMENT,
              "cross-entropy series: need rows >= 0, classes >= 1, row_stride >= classes");
   PT_REQUIRE(rows <= INT32_MAX, PT_UNSUPPORTED, "cross-entropy series: rows beyond 2^31-1");
+  PT_REQUIRE(softcap >= 0.0 && softcap <= 1e300, PT_INVALID_ARGUMENT,
+             "cross-entropy series: softcap must be 0 (none) or a positive finite cap");
   PT_REQUIRE(rows == 0 || target != nullptr, PT_INVALID_ARGUMENT,
              "cross-entropy series: target is required");
   PT_REQUIRE(reduction == PT_REDUCTION_NONE || rows == 0 || workspace != nullptr,
@@ -43,7 +45,7 @@ int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits
   PT_REQUIRE(rows > 0 || reduction == PT_REDUCTION_NONE, PT_UNSUPPORTED,
              "cross-entropy series: a reduction over zero rows");
   if (rows == 0) return PT_OK;
-  pt::CeArgs a{degree, logits, rows, classes, row_stride, target, ignore_index, reduction,
+  pt::CeArgs a{degree, logits, rows, classes, row_stride, target, ignore_index, softcap, reduction,
                loss, lse, workspace, static_cast<hipStream_t>(stream)};
   switch (dtype) {
     case PT_FLOAT32: return pt::launch_ce<float>(a);

@@ -5,7 +5,7 @@ order-k coefficient of ``f(x(t))`` at t = 0 is ``g^(k)(0) / k!`` with
 ``g(t) = f(x(t))``; ``taylor`` computes it with k nested ``torch.func.jvp``
 calls on the scalar t, exactly as the reference's tests derive their expected
 values (/root/reference/tests/test_attention.py:33-46,
-/root/reference/tests/test_plain_range.py:432-445). It shares no code with the
+/root/reference/tests/test_plain_range.py:103-115). It shares no code with the
 series recurrences it checks.
 """
 

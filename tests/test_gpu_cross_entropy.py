@@ -128,3 +128,47 @@ def test_full_size_config_rows_sample():
     pick = torch.randperm(N, generator=torch.Generator().manual_seed(5))[:32].cuda()
     want = oracle.cross_entropy([c[pick].cpu().double() for c in Z], y[pick].cpu(), reduction="none")
     _check([r[pick] for r in rows], want, torch.float32)
+
+
+@pytest.mark.parametrize("strided", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("degree", [1, 4])
+def test_softcap_matches_oracle(monkeypatch, degree, dtype, strided):
+    # /root/reference/tests/test_fused_kernels.py:186-211: N=200, C=3000 logits of scale 40, cap 15,
+    # every 5th target ignored, optionally a padded (strided) row slice; the kernel caps on the fly.
+    calls = []
+    original = _ops.cross_entropy_series
+    monkeypatch.setattr(_ops, "cross_entropy_series", lambda *a, **k: calls.append(1) or original(*a, **k))
+    N, C, pad, cap = 200, 3000, 64 if strided else 0, 15.0
+    g = torch.Generator().manual_seed(1)
+    full = [(torch.randn(N, C + pad, generator=g, dtype=torch.float64) * 40 * 0.5 ** k).to(dtype)
+            for k in range(degree + 1)]
+    y = torch.randint(0, C, (N,), generator=g)
+    y[::5] = -1
+    logits = PolyTensor(tuple(c.cuda() for c in full))
+    with torch.no_grad(), PolyTensor.plain_range():
+        sliced = logits[:, :C]
+        loss = PolyTensor.cross_entropy(sliced, y.cuda(), softcap=cap, ignore_index=-1, reduction="none")
+    assert calls == [1] and loss.degree == degree
+    Z = [c[:, :C].double() for c in full]
+    want = oracle.cross_entropy(Z, y, ignore_index=-1, reduction="none", softcap=cap)
+    capped = [cap * t for t in oracle.activation([z / cap for z in Z], "tanh")]
+    _check(loss.coeffs, want, dtype, inputs=capped)
+
+
+def test_softcap_mean_and_lse_at_degree_eight():
+    N, C, cap = 64, 1000, 7.5
+    Z, y = _logits(N, C, 8, seed=9, dtype=torch.float64, base_scale=10.0)
+    out, lse = _ops.cross_entropy_series([c.cuda() for c in Z], y.cuda(), -100, 1, cap)
+    want = oracle.cross_entropy(Z, y, reduction="mean", softcap=cap)
+    _check(list(out), want, torch.float64)
+    capped = [cap * t for t in oracle.activation([z / cap for z in Z], "tanh")]
+    want_lse = paths.logsumexp(capped, dim=1)
+    _check(list(lse), want_lse, torch.float64)
+
+
+def test_softcap_must_be_positive():
+    Z, y = _logits(4, 16, 1, seed=10, dtype=torch.float32)
+    with torch.no_grad(), PolyTensor.plain_range():
+        with pytest.raises(NotImplementedError, match="softcap"):
+            PolyTensor.cross_entropy(PolyTensor(tuple(c.cuda() for c in Z)), y.cuda(), softcap=-1.0)

@@ -2,7 +2,7 @@
 
 ``oracle.activation`` restates the reference's plain-range activation rule
 (derivatives at the constant term composed by Faa di Bruno,
-/root/reference/src/polytensors/_plain.py:174-262) and its default-mode silu /
+/root/reference/src/polytensors/_plain.py:174-259) and its default-mode silu /
 gelu_tanh jets (/root/reference/src/polytensors/_activations.py:89-115). The
 checks here fix the answer independently of those rules: nested forward-mode
 derivatives of torch's own activation along the curve (tests/jets.py), and,

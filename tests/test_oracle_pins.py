@@ -153,7 +153,7 @@ def _check(got, want, tol):
 
 
 def test_rms_norm_line_matches_higher_derivatives():
-    # /root/reference/tests/test_plain_range.py:432-445 (shape (4,), eps 1e-5, degree 4)
+    # /root/reference/tests/test_plain_range.py:103-115 (shape (4,), eps 1e-5, degree 4)
     g = torch.Generator().manual_seed(7)
     base, direction = torch.randn(4, generator=g, dtype=torch.float64), torch.randn(4, generator=g, dtype=torch.float64)
     got = oracle.rms_norm(paths.lift([base, direction], 4), (4,), eps=1e-5)
@@ -251,6 +251,19 @@ def test_cross_entropy_general_series(reduction):
     y[::5] = -1
     got = oracle.cross_entropy(Z, y, ignore_index=-1, reduction=reduction)
     want = taylor(lambda z: F.cross_entropy(z, y, ignore_index=-1, reduction=reduction), [Z], 4)
+    _check(got, want, 1e-12)
+
+
+@pytest.mark.parametrize("reduction", ("none", "mean"))
+def test_cross_entropy_softcap_general_series(reduction):
+    # the composite of /root/reference/src/polytensors/_fused_cross_entropy.py:184-187
+    Z = _series((12, 37), 4, seed=42, scale=20.0)
+    y = torch.randint(0, 37, (12,), generator=torch.Generator().manual_seed(43))
+    y[::4] = -1
+    cap = 15.0
+    got = oracle.cross_entropy(Z, y, ignore_index=-1, reduction=reduction, softcap=cap)
+    want = taylor(lambda z: F.cross_entropy(cap * torch.tanh(z / cap), y, ignore_index=-1, reduction=reduction),
+                  [Z], 4)
     _check(got, want, 1e-12)
 
 
