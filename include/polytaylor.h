@@ -230,6 +230,26 @@ int pt_activation_series_bwd(int dtype, int degree, int kind,
                              const void* const* g, const void* const* saved,
                              void* const* dx, int64_t numel, void* stream);
 
+/* Operations of pt_series_binary. */
+typedef enum pt_binary {
+  PT_BINARY_MUL = 0,
+  PT_BINARY_DIV = 1
+} pt_binary;
+
+/*
+ * Elementwise product or quotient of two degree-K series of one shape:
+ *   PT_BINARY_MUL  y_k = sum_{i+j=k} a_i b_j,
+ *   PT_BINARY_DIV  y_k = (a_k - sum_{i=1..k} b_i y_{k-i}) / b_0.
+ * a, b, y: K+1 pointers, each `numel` elements of `dtype`.
+ * Replaces the reference's general rules for a series times / over a series
+ *   /root/reference/src/polytensors/_range_ops.py:133-149 (mul -> convolution,
+ *   _plain.py:118-128; div -> quotient, _range_ops.py:86-93); an ordinary
+ *   operand takes the constant-operand path there (:109-132) and needs no kernel.
+ */
+int pt_series_binary(int dtype, int degree, int op, const void* const* a,
+                     const void* const* b, void* const* y, int64_t numel,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,6 @@ function along the curve, in float64), against closed forms and known-answer
 values the reference's own tests hold, and against brute-force sums.
 """
 
-from .series import cauchy, exp_series, log_series, rsqrt_series, softmax_family  # noqa: F401
+from .series import cauchy, exp_series, log_series, quotient, rsqrt_series, softmax_family  # noqa: F401
 from .paths import attention, cross_entropy, layer_norm, matmul, rms_norm  # noqa: F401
 from .activations import activation, activation_backward  # noqa: F401

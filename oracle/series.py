@@ -29,6 +29,20 @@ def cauchy(left, right, matmul=False):
     return out
 
 
+def quotient(A, B):
+    """Elementwise series quotient: Q_k = (A_k - sum_{i=1..k} B_i Q_{k-i}) / B_0.
+
+    /root/reference/src/polytensors/_range_ops.py:86-93 (quotient).
+    """
+    out = []
+    for k in range(len(A)):
+        remainder = A[k]
+        for i in range(1, k + 1):
+            remainder = remainder - B[i] * out[k - i]
+        out.append(remainder / B[0])
+    return out
+
+
 def exp_series(X):
     """exp along a series: Y_0 = exp(X_0), Y_k = sum_{i=1..k} (i/k) X_i Y_{k-i}.
 

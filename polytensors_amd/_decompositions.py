@@ -30,6 +30,13 @@ def _has_poly(values):
     return any(isinstance(v, PolyTensor) for v in values)
 
 
+def _needs_grad(args, kwargs):
+    if not torch.is_grad_enabled():
+        return False
+    values = list(args) + list(kwargs.values())
+    return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+
+
 def maybe_decompose(function, args, kwargs):
     """The fused result, or NotImplemented to continue with ordinary dispatch."""
     if function in _RMS_NORM or function in _LAYER_NORM:
@@ -83,6 +90,10 @@ def maybe_decompose(function, args, kwargs):
     if function in _MATMUL:
         from . import _fused_matmul
 
+        if _needs_grad(args, kwargs):
+            # Let autograd record mm/bmm/addmm; they reach the kernel through __torch_dispatch__,
+            # and so do the products of their backward.
+            return NotImplemented
         if function is F.linear:
             names = ("input", "weight", "bias")
             bound = dict(zip(names, args))

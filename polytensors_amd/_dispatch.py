@@ -2,10 +2,13 @@
 
 Only the rules the hot path needs exist here:
   * shape, view, copy and conversion operations, applied to every coefficient
-    (as /root/reference/src/polytensors/_range_ops.py:224-257);
+    (as /root/reference/src/polytensors/_range_ops.py:224-257), and the
+    factories autograd uses (_dispatch.py:769-790);
   * linear arithmetic: series +/- series, and +, -, *, / with an ordinary
     operand (the constant-operand fast path, _range_ops.py:109-132), sum and
     mean (_range_ops.py:178-193);
+  * series (*) series and series / series (and ordinary / series), the
+    elementwise Cauchy product and quotient kernel (_range_ops.py:133-149);
   * the matrix products mm/bmm/addmm/mv/dot, which run the Cauchy-product
     kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84);
   * the elementwise activations gelu (erf and tanh forms), tanh, sigmoid,
@@ -37,6 +40,12 @@ _COPY_OPS = {
     aten.index_select.default, aten.gather.default, aten.index.Tensor, aten.flip.default,
     aten.roll.default, aten.repeat.default,
 }
+# In-place arithmetic: the out-of-place rule, written into the target's coefficients
+# (/root/reference/src/polytensors/_range_ops.py:95-103, write).
+_IN_PLACE = {aten.add_.Tensor: aten.add.Tensor, aten.add_.Scalar: aten.add.Scalar,
+             aten.sub_.Tensor: aten.sub.Tensor, aten.sub_.Scalar: aten.sub.Scalar,
+             aten.mul_.Tensor: aten.mul.Tensor, aten.mul_.Scalar: aten.mul.Scalar,
+             aten.div_.Tensor: aten.div.Tensor, aten.div_.Scalar: aten.div.Scalar}
 _ADD = {aten.add.Tensor, aten.add.Scalar}
 _SUB = {aten.sub.Tensor, aten.sub.Scalar}
 _MUL = {aten.mul.Tensor, aten.mul.Scalar}
@@ -109,6 +118,18 @@ def dispatch(func, types, args=(), kwargs=None):
     _collect(kwargs, polys)
     if not polys:
         return func(*args, **kwargs)
+    from ._plain import _plain_range, in_backward, plain_range_enabled
+
+    if not plain_range_enabled() and in_backward() and any(getattr(p, "_plain", False) for p in polys):
+        token = _plain_range.set(True)
+        try:
+            return _dispatch(func, types, args, kwargs, polys)
+        finally:
+            _plain_range.reset(token)
+    return _dispatch(func, types, args, kwargs, polys)
+
+
+def _dispatch(func, types, args, kwargs, polys):
     for p in polys:
         if not hasattr(p, "coeffs"):
             raise RuntimeError("PolyTensor wrapper reached dispatch without coefficient storage; "
@@ -121,6 +142,15 @@ def dispatch(func, types, args=(), kwargs=None):
     mutable = bool(getattr(schema, "is_mutable", False))
     if mutable and args and not _is_poly(args[0]):
         raise RuntimeError(f"cannot update a regular Tensor in-place with a PolyTensor ({func})")
+
+    if func in _IN_PLACE:
+        target = args[0]
+        result = dispatch(_IN_PLACE[func], types, args, kwargs)
+        for dest, src in zip(target.coeffs, result.coeffs):
+            if src.is_complex() and not dest.is_complex():
+                raise RuntimeError("cannot write complex PolyTensor coefficients into real storage")
+            dest.copy_(src)
+        return target
 
     if func in _VIEW_OPS:
         source = args[0]
@@ -155,8 +185,35 @@ def dispatch(func, types, args=(), kwargs=None):
             c.zero_()
         return args[0]
 
+    # Autograd and optimizer plumbing (/root/reference/src/polytensors/_dispatch.py:769-790): a
+    # constant fill is a constant series; empty/zero factories act on every coefficient.
+    if func in (aten.ones_like.default, aten.full_like.default, aten.new_ones.default, aten.new_full.default):
+        head = func(args[0].coeffs[0], *args[1:], **kwargs)
+        return _wrap((head, *(torch.zeros_like(head) for _ in range(degree))))
+    if func in (aten.zeros_like.default, aten.empty_like.default, aten.new_empty_strided.default,
+                aten.new_empty.default, aten.new_zeros.default):
+        return _wrap(func(c, *args[1:], **kwargs) for c in args[0].coeffs)
+    if func is aten.fill_.Scalar:
+        args[0].coeffs[0].fill_(args[1])
+        for c in args[0].coeffs[1:]:
+            c.zero_()
+        return args[0]
+    if func is aten.detach_.default:
+        args[0]._set_coeffs(tuple(c.detach() for c in args[0].coeffs))
+        return args[0]
+
     if func is aten.neg.default:
         return _wrap(-c for c in args[0].coeffs)
+    if func is aten.rsub.Scalar:
+        # other - alpha * x (/root/reference/src/polytensors/_range_ops.py:151-155)
+        x, other = args[0], args[1]
+        alpha = kwargs.get("alpha", 1)
+        return _wrap((other - alpha * x.coeffs[0], *(-alpha * c for c in x.coeffs[1:])))
+    if func is aten.reciprocal.default:
+        # quotient(1, x) (/root/reference/src/polytensors/_range_ops.py:86-93,157-158)
+        from . import _fused_elementwise
+
+        return _fused_elementwise.binary(torch.ones_like(args[0].coeffs[0]), args[0], "div")
 
     if func in _ADD or func in _SUB:
         a, b = args[0], args[1]
@@ -170,12 +227,14 @@ def dispatch(func, types, args=(), kwargs=None):
 
     if func in _MUL or func in _DIV:
         a, b = args[0], args[1]
-        if _is_poly(a) and _is_poly(b):
-            raise NotImplementedError(
-                f"{func}: elementwise series products are not part of polytensors_amd (only the fused "
-                "matmul, attention, norm and cross-entropy kernels are)")
-        if func in _DIV and not _is_poly(a):
-            raise NotImplementedError(f"{func}: division by a series is not part of polytensors_amd")
+        if func in _DIV and kwargs.get("rounding_mode") is not None:
+            raise NotImplementedError("PolyTensor does not implement rounded division")
+        if (_is_poly(a) and _is_poly(b)) or (func in _DIV and _is_poly(b)):
+            from . import _fused_elementwise
+
+            if not isinstance(a, torch.Tensor):
+                a = torch.as_tensor(a, dtype=b.dtype, device=b.device)
+            return _fused_elementwise.binary(a, b, "mul" if func in _MUL else "div")
         if _is_poly(a):
             return _wrap((c * b if func in _MUL else c / b) for c in a.coeffs)
         return _wrap(a * c for c in b.coeffs)

@@ -22,7 +22,9 @@ BACKWARD_KINDS = ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu")
 def why_ineligible(*operands):
     from ._tensor import PolyTensor
 
-    reason = _gate.common_reason(operands)
+    # Reached from __torch_dispatch__ only: autograd above has recorded the native
+    # backward operation (gelu_backward, tanh_backward, ...), which routes here too.
+    reason = _gate.common_reason(operands, below_autograd=True)
     if reason is not None:
         return reason
     polys = [x for x in operands if isinstance(x, PolyTensor)]

@@ -16,8 +16,8 @@ from . import _gate, _ops
 _DTYPES = (torch.float32, torch.float64)
 
 
-def why_ineligible(a, b):
-    reason = _gate.common_reason((a, b))
+def why_ineligible(a, b, below_autograd=False):
+    reason = _gate.common_reason((a, b), below_autograd=below_autograd)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
@@ -39,11 +39,11 @@ def _degree(*xs):
     return next(x.degree for x in xs if isinstance(x, PolyTensor))
 
 
-def matmul(a, b):
+def matmul(a, b, below_autograd=False):
     """Series of ``torch.matmul(a, b)``."""
     from ._tensor import PolyTensor
 
-    reason = why_ineligible(a, b)
+    reason = why_ineligible(a, b, below_autograd)
     if reason is not None:
         raise NotImplementedError(f"matmul: {reason}")
     degree = _degree(a, b)
@@ -100,15 +100,16 @@ def linear(x, weight, bias=None):
 
 
 def from_dispatch(func, args, kwargs):
-    """mm/bmm/mv/dot/matmul/addmm reaching ``__torch_dispatch__``."""
+    """mm/bmm/mv/dot/matmul/addmm reaching ``__torch_dispatch__`` (under autograd, whose
+    recorded backward runs these same products on the cotangent series)."""
     aten = torch.ops.aten
     if func is aten.addmm.default:
         bias, a, b = args[:3]
         beta, alpha = kwargs.get("beta", 1), kwargs.get("alpha", 1)
-        product = matmul(a, b)
+        product = matmul(a, b, below_autograd=True)
         if alpha != 1:
             product = product * alpha
         if beta == 0:
             return product
         return product + (bias * beta if beta != 1 else bias)
-    return matmul(args[0], args[1])
+    return matmul(args[0], args[1], below_autograd=True)

@@ -25,8 +25,13 @@ def coefficients(x, degree):
     return (x,)
 
 
-def common_reason(values, *, allow_plain_grad=False):
-    """Shared conditions over the tensor operands of one fused call."""
+def common_reason(values, *, allow_plain_grad=False, below_autograd=False):
+    """Shared conditions over the tensor operands of one fused call.
+
+    ``below_autograd``: the call comes from ``__torch_dispatch__``, under the
+    autograd layer, which has already recorded the operation's native backward;
+    operands requiring grad are then fine (the backward operations have rules too).
+    """
     from ._tensor import PolyTensor, _coefficient_autograd_enabled
 
     tensors = [v for v in values if isinstance(v, torch.Tensor)]
@@ -43,11 +48,11 @@ def common_reason(values, *, allow_plain_grad=False):
         return f"degree {degree} exceeds the kernels' maximum {MAX_DEGREE}"
     if _coefficient_autograd_enabled.get():
         return "coefficient_autograd needs series backward kernels, which polytensors_amd does not implement"
-    if torch.is_grad_enabled():
+    if torch.is_grad_enabled() and not below_autograd:
         grads = any(t.requires_grad for t in tensors) or any(
             c.requires_grad for p in polys for c in p.coeffs)
         if grads and not allow_plain_grad:
-            return "series backward is not implemented (forward-only kernels); use torch.no_grad()"
+            return "this fused operation has no series backward kernel; use torch.no_grad()"
     coeffs = [c for t in tensors for c in coefficients(t, degree)]
     if any(c.is_complex() for c in coeffs):
         return "complex directions are not implemented by the fused kernels"

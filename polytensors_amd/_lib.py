@@ -18,6 +18,7 @@ ABI_VERSION = 2
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
 # pt_activation codes of include/polytaylor.h
+BINARY_OPS = {"mul": 0, "div": 1}
 ACTIVATIONS = {"gelu": 0, "gelu_tanh": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "exp": 5, "log": 6}
 
 DTYPE_CODES = {
@@ -49,6 +50,7 @@ SIGNATURES = {
                                          _c_dbl, _c_vp]),
     "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_bwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
+    "pt_series_binary": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
 }
 
 

@@ -266,3 +266,29 @@ def activation_series_backward(grad: List[torch.Tensor], saved: List[torch.Tenso
 @activation_series_backward.register_fake
 def _(grad, saved, kind):
     return grad[0].new_empty((len(grad), *grad[0].shape))
+
+
+# ---------------------------------------------------------------------------
+# Elementwise series product / quotient
+
+@torch.library.custom_op(f"{NAMESPACE}::series_binary", mutates_args=(), device_types="cuda")
+def series_binary(a: List[torch.Tensor], b: List[torch.Tensor], op: str) -> torch.Tensor:
+    """a (*) b or a / b of two series of one shape; returns [K+1, *shape]."""
+    _check_series("series_binary a", a)
+    _check_series("series_binary b", b)
+    _require(len(a) == len(b) and a[0].shape == b[0].shape and a[0].dtype == b[0].dtype
+             and a[0].device == b[0].device, "series_binary: operands must match in degree, shape, dtype and device")
+    _require(op in _lib.BINARY_OPS, f"series_binary: unknown operation {op!r}")
+    degree = len(a) - 1
+    out = torch.empty((degree + 1, *a[0].shape), dtype=a[0].dtype, device=a[0].device)
+    lib = _lib.load()
+    status = lib.pt_series_binary(_lib.DTYPE_CODES[a[0].dtype], degree, _lib.BINARY_OPS[op], _lib.ptr_array(a),
+                                  _lib.ptr_array(b), _lib.ptr_array(list(out.unbind(0))), a[0].numel(),
+                                  _lib.stream_of(a[0].device))
+    _lib.check(status, f"series_binary({op})")
+    return out
+
+
+@series_binary.register_fake
+def _(a, b, op):
+    return a[0].new_empty((len(a), *a[0].shape))

@@ -11,3 +11,17 @@ _plain_range = contextvars.ContextVar("polytensors_amd_plain_range", default=Fal
 
 def plain_range_enabled():
     return _plain_range.get()
+
+
+def in_backward():
+    """Whether the calling thread is running an autograd graph task.
+
+    The engine runs a CUDA graph's backward on its own device thread, where the
+    caller's ``plain_range()`` context variable is not set. The reference's rules
+    then fall back to its default mode; this package has no other mode, so a
+    backward operation whose operands were created in plain range runs in plain
+    range (``_dispatch.dispatch``), as if the context had travelled with the graph.
+    """
+    import torch
+
+    return torch._C._current_graph_task_id() != -1

@@ -22,6 +22,8 @@ import operator
 
 import torch
 
+from ._plain import plain_range_enabled
+
 _retention_scopes = contextvars.ContextVar("polytensors_amd_retention_scopes", default=())
 _coefficient_autograd_enabled = contextvars.ContextVar("polytensors_amd_coefficient_autograd", default=False)
 _COMPLEX_OF = {torch.float16: torch.complex32, torch.float32: torch.complex64, torch.float64: torch.complex128}
@@ -157,6 +159,7 @@ class PolyTensor(torch.Tensor):
             dtype=head.dtype, layout=head.layout, device=head.device, requires_grad=requires_grad)
         out.coeffs = coeffs
         out.degree = len(coeffs) - 1
+        out._plain = plain_range_enabled()
         for scope in _retention_scopes.get():
             scope.append(out)
         return out
@@ -261,8 +264,22 @@ class PolyTensor(torch.Tensor):
         return cross_entropy(logits, target, softcap=softcap, ignore_index=ignore_index, reduction=reduction)
 
     def backward(self, gradient=None, retain_graph=None, create_graph=False, inputs=None):
-        raise NotImplementedError(
-            "polytensors_amd implements the forward Taylor kernels only; series backward is not available")
+        """Reverse mode through the series (/root/reference/src/polytensors/_tensor.py:325-338).
+
+        A scalar output seeds the cotangent series (1, 0, ..., 0); an ordinary
+        ``gradient`` is lifted to a constant series. Gradients of the fused
+        operations are their degree-K backward kernels.
+        """
+        if gradient is None:
+            if self.numel() != 1:
+                raise RuntimeError("grad can be implicitly created only for scalar outputs")
+            if self.is_complex():
+                raise RuntimeError("an explicit gradient is required for a complex output")
+            gradient = PolyTensor.constant(torch.ones_like(self.value), self.degree)
+        elif not isinstance(gradient, PolyTensor):
+            gradient = PolyTensor.constant(gradient, self.degree)
+        torch.autograd.backward(self, gradient, retain_graph=retain_graph, create_graph=create_graph,
+                                inputs=inputs)
 
     def __repr__(self):
         if not hasattr(self, "coeffs"):

@@ -1,0 +1,6 @@
+// Instantiates the elementwise series product / quotient kernels for one storage type.
+#include "series_binary.inl"
+
+namespace pt {
+template int launch_binary<_Float16>(const BinaryArgs&);
+}  // namespace pt

@@ -267,6 +267,15 @@ def test_cross_entropy_softcap_general_series(reduction):
     _check(got, want, 1e-12)
 
 
+def test_elementwise_product_and_quotient_series():
+    # /root/reference/src/polytensors/_range_ops.py:86-93,143-144
+    A = _series((4, 9), 5, seed=52)
+    B = _series((4, 9), 5, seed=53)
+    B[0] = B[0].abs() + 0.5
+    _check(series.cauchy(A, B), taylor(lambda a, b: a * b, [A, B], 5), 1e-13)
+    _check(oracle.quotient(A, B), taylor(lambda a, b: a / b, [A, B], 5), 1e-12)
+
+
 def test_matmul_general_series():
     A = _series((3, 6, 5), 4, seed=50)
     B = _series((5, 7), 4, seed=51)

@@ -139,10 +139,30 @@ def test_eligibility_reasons():
         assert "exceeds" in _fused_norm.why_ineligible(deep, (4,))
 
 
-def test_backward_is_not_available():
-    x = PolyTensor((torch.ones(()), torch.ones(())))
-    with pytest.raises(NotImplementedError):
-        x.backward()
+def test_backward_seeds_the_constant_series_and_accumulates():
+    # /root/reference/src/polytensors/_tensor.py:325-338: a scalar output seeds (1, 0, ..., 0).
+    x = PolyTensor((torch.ones(3, dtype=torch.float64), torch.full((3,), 2.0, dtype=torch.float64)),
+                   requires_grad=True)
+    with PolyTensor.retain_wrappers():
+        y = (x * 3.0 + 1.0).sum()
+        y.backward()
+        assert isinstance(x.grad, PolyTensor) and x.grad.degree == 1
+        assert [c.tolist() for c in x.grad.coeffs] == [[3.0] * 3, [0.0] * 3]
+        (x * 2.0).sum().backward()          # a second pass accumulates
+        assert [c.tolist() for c in x.grad.coeffs] == [[5.0] * 3, [0.0] * 3]
+
+
+def test_backward_with_an_ordinary_gradient_lifts_it():
+    x = PolyTensor((torch.ones(2, dtype=torch.float64), torch.ones(2, dtype=torch.float64)), requires_grad=True)
+    with PolyTensor.retain_wrappers():
+        (x * 4.0).backward(torch.tensor([1.0, 2.0], dtype=torch.float64))
+        assert [c.tolist() for c in x.grad.coeffs] == [[4.0, 8.0], [0.0, 0.0]]
+
+
+def test_backward_needs_a_scalar_or_a_gradient():
+    x = PolyTensor((torch.ones(3), torch.ones(3)), requires_grad=True)
+    with PolyTensor.retain_wrappers(), pytest.raises(RuntimeError, match="scalar"):
+        (x * 2.0).backward()
 
 
 def test_plain_tensor_cross_entropy_with_softcap_matches_composite():
