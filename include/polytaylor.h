@@ -98,6 +98,24 @@ int pt_layer_norm_series_fwd(int dtype, int degree, const void* const* x,
                              double eps, void* stream);
 
 /*
+ * Gradient series of the RMSNorm / LayerNorm normalization (no affine terms):
+ *   dx(t) = J(x(t))^T g(t), the reverse-mode series of the output cotangent g.
+ * RMSNorm:   dx = r (*) g - (1/n) r^3 (*) c (*) x,   c = sum_row g (*) x;
+ * LayerNorm: with d = x - mean(x), the same for d and g - mean(g).
+ * x, g, dx: K+1 pointers, each [rows, n] of `dtype`; eps as the forward.
+ * Replaces the degree-1 backward of the reference
+ *   /root/reference/src/polytensors/_norm_kernels.py:22-38 (_backward) and
+ *   /root/reference/src/polytensors/_fused_norm.py:43-60 (_SeriesNorm, whose
+ *   general formula :52-56 this evaluates in series arithmetic), at degree K.
+ */
+int pt_rms_norm_series_bwd(int dtype, int degree, const void* const* x,
+                           const void* const* g, void* const* dx, int64_t rows,
+                           int64_t n, double eps, void* stream);
+int pt_layer_norm_series_bwd(int dtype, int degree, const void* const* x,
+                             const void* const* g, void* const* dx,
+                             int64_t rows, int64_t n, double eps, void* stream);
+
+/*
  * Cross entropy of a degree-K series of logits z(t) with integer targets.
  * logits: K+1 pointers, each `rows` rows of `classes` values, row i at
  *         element offset i * row_stride (row_stride >= classes).

@@ -70,6 +70,35 @@ def layer_norm(X, normalized_shape, weight=None, bias=None, eps=1e-5):
     return _affine(out, weight, bias)
 
 
+def rms_norm_backward(X, G, normalized_shape, eps=None):
+    """Gradient series of the RMSNorm normalization (no weight): the series of
+    ``g * r - x * r**3 * mean(x * g)``, r = rsqrt(mean(x*x) + eps), every product a
+    Cauchy product -- the reference's backward formula
+    /root/reference/src/polytensors/_fused_norm.py:52-56 evaluated on series.
+    """
+    dims = tuple(range(-len(normalized_shape), 0))
+    eps = torch.finfo(X[0].dtype).eps if eps is None else eps
+    r = rsqrt_series(_add_to_order0(_mean(cauchy(X, X), dims), eps))
+    r3 = cauchy(cauchy(r, r), r)
+    dot = _mean(cauchy(X, G), dims)
+    return [a - b for a, b in zip(cauchy(G, r), cauchy(X, cauchy(r3, dot)))]
+
+
+def layer_norm_backward(X, G, normalized_shape, eps=1e-5):
+    """Gradient series of the LayerNorm normalization (no affine terms): with
+    d = x - mean(x) and r = rsqrt(mean(d*d) + eps), the series of
+    ``r * (g - mean(g)) - d * r**3 * mean(d * g)`` (Cauchy products), the composite
+    rules' VJP (the reference has no layer-norm rule, docs/notes.md:33-35).
+    """
+    dims = tuple(range(-len(normalized_shape), 0))
+    D = [x - m for x, m in zip(X, _mean(X, dims))]
+    r = rsqrt_series(_add_to_order0(_mean(cauchy(D, D), dims), eps))
+    r3 = cauchy(cauchy(r, r), r)
+    Gc = [g - m for g, m in zip(G, _mean(G, dims))]
+    dot = _mean(cauchy(D, G), dims)
+    return [a - b for a, b in zip(cauchy(r, Gc), cauchy(D, cauchy(r3, dot)))]
+
+
 def attention(Q, K, V, attn_mask=None, is_causal=False, scale=None):
     """Series of ``softmax((Q*scale) @ K^T masked) @ V``.
 

@@ -22,10 +22,10 @@ from . import _gate, _ops
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
-def why_ineligible(input, normalized_shape, weight=None, bias=None):
+def why_ineligible(input, normalized_shape, weight=None, bias=None, allow_grad=False):
     from ._tensor import PolyTensor
 
-    reason = _gate.common_reason((input, weight, bias))
+    reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad)
     if reason is not None:
         return reason
     if not isinstance(input, torch.Tensor) or input.dtype not in _DTYPES:
@@ -66,13 +66,66 @@ def _affine_coeffs(a, input, shape):
     return [c.contiguous().reshape(-1) for c in coeffs]
 
 
+def _needs_grad(*values):
+    return torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+
+
+class _SeriesNorm(torch.autograd.Function):
+    """The normalization (no affine terms) with its degree-K gradient series.
+
+    As /root/reference/src/polytensors/_fused_norm.py:43-60 (_SeriesNorm): the
+    forward kernel, and a backward kernel computing J(x(t))^T g(t); the weight
+    and bias are separate operations under autograd, so their gradients follow
+    from the elementwise rules.
+    """
+
+    @staticmethod
+    def forward(ctx, input, shape, eps, layer):
+        ctx.save_for_backward(input)
+        ctx.shape, ctx.eps, ctx.layer = shape, eps, layer
+        x = _series_coeffs(input, input.degree)
+        return _from_stacked(_ops.norm_series(x, [], [], math.prod(shape), eps, layer))
+
+    @staticmethod
+    def backward(ctx, gradient):
+        from ._plain import _plain_range
+
+        if torch.is_grad_enabled():
+            raise NotImplementedError("second-order reverse mode through the fused norm is not implemented")
+        (input,) = ctx.saved_tensors
+        token = _plain_range.set(True)   # the engine's thread does not see the caller's context
+        try:
+            x = _series_coeffs(input, input.degree)
+            g = _series_coeffs(gradient, input.degree)
+            dx = _from_stacked(_ops.norm_series_backward(x, g, math.prod(ctx.shape), ctx.eps, ctx.layer))
+        finally:
+            _plain_range.reset(token)
+        return dx, None, None, None
+
+
+def _from_stacked(stacked):
+    from ._tensor import PolyTensor
+
+    return PolyTensor.from_stacked(stacked)
+
+
 def _run(input, normalized_shape, weight, bias, eps, layer):
     from ._tensor import PolyTensor
 
     shape = tuple(normalized_shape)
-    reason = why_ineligible(input, shape, weight, bias)
+    grads = _needs_grad(input, weight, bias)
+    reason = why_ineligible(input, shape, weight, bias, allow_grad=grads)
     if reason is not None:
         raise NotImplementedError(f"{'layer_norm' if layer else 'rms_norm'}: {reason}")
+    if grads:
+        if not isinstance(input, PolyTensor):
+            raise NotImplementedError("reverse mode through the fused norm needs a PolyTensor input")
+        result = _SeriesNorm.apply(input, shape, float(eps), layer)
+        if weight is not None:
+            result = result * weight
+        if layer and bias is not None:
+            result = result + bias
+        return result
     degree = next(x.degree for x in (input, weight, bias) if isinstance(x, PolyTensor))
     x = _series_coeffs(input, degree)
     w = _affine_coeffs(weight, input, shape)

@@ -51,6 +51,8 @@ SIGNATURES = {
     "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_bwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
     "pt_series_binary": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
+    "pt_rms_norm_series_bwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_i64, _c_dbl, _c_vp]),
+    "pt_layer_norm_series_bwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_i64, _c_dbl, _c_vp]),
 }
 
 

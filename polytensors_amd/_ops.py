@@ -292,3 +292,28 @@ def series_binary(a: List[torch.Tensor], b: List[torch.Tensor], op: str) -> torc
 @series_binary.register_fake
 def _(a, b, op):
     return a[0].new_empty((len(a), *a[0].shape))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::norm_series_backward", mutates_args=(), device_types="cuda")
+def norm_series_backward(x: List[torch.Tensor], grad: List[torch.Tensor], n: int, eps: float,
+                         layer: bool) -> torch.Tensor:
+    """Gradient series of the (Layer|RMS)Norm normalization over the last ``n`` elements."""
+    _check_series("norm_series_backward x", x)
+    _check_series("norm_series_backward grad", grad)
+    _require(len(x) == len(grad) and x[0].shape == grad[0].shape and x[0].dtype == grad[0].dtype
+             and x[0].device == grad[0].device, "norm_series_backward: x and grad series must match")
+    degree = len(x) - 1
+    numel = x[0].numel()
+    _require(n >= 1 and numel % n == 0, "norm_series_backward: n must divide the element count")
+    out = torch.empty((degree + 1, *x[0].shape), dtype=x[0].dtype, device=x[0].device)
+    lib = _lib.load()
+    entry = lib.pt_layer_norm_series_bwd if layer else lib.pt_rms_norm_series_bwd
+    status = entry(_lib.DTYPE_CODES[x[0].dtype], degree, _lib.ptr_array(x), _lib.ptr_array(grad),
+                   _lib.ptr_array(list(out.unbind(0))), numel // n, n, float(eps), _lib.stream_of(x[0].device))
+    _lib.check(status, "layer_norm_series_bwd" if layer else "rms_norm_series_bwd")
+    return out
+
+
+@norm_series_backward.register_fake
+def _(x, grad, n, eps, layer):
+    return x[0].new_empty((len(x), *x[0].shape))

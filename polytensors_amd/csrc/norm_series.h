@@ -22,4 +22,19 @@ struct NormArgs {
 template <typename T, bool LAYER>
 int launch_norm(const NormArgs& a);
 
+// Gradient series of the normalization (no affine terms): dx = J(x(t))^T g(t).
+struct NormBwdArgs {
+  int degree;
+  const void* const* x;
+  const void* const* g;
+  void* const* dx;
+  int64_t rows;
+  int64_t n;
+  double eps;
+  hipStream_t stream;
+};
+
+template <typename T, bool LAYER>
+int launch_norm_bwd(const NormBwdArgs& a);
+
 }  // namespace pt

@@ -47,6 +47,40 @@ int dispatch_norm(int dtype, bool layer, const pt::NormArgs& a) {
   return PT_UNSUPPORTED;
 }
 
+int check_norm_bwd(int dtype, int degree, const void* const* x, const void* const* g, void* const* dx,
+                   int64_t rows, int64_t n, double eps) {
+  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
+             "norm series backward: degree must be in 0..8");
+  PT_REQUIRE(dtype >= PT_FLOAT32 && dtype <= PT_FLOAT16, PT_UNSUPPORTED,
+             "norm series backward: unknown dtype code");
+  PT_REQUIRE(x != nullptr && g != nullptr && dx != nullptr, PT_INVALID_ARGUMENT,
+             "norm series backward: x, g and dx pointer arrays are required");
+  PT_REQUIRE(rows >= 0 && n >= 1, PT_INVALID_ARGUMENT, "norm series backward: rows must be >= 0 and n >= 1");
+  PT_REQUIRE(rows <= INT32_MAX, PT_UNSUPPORTED, "norm series backward: rows beyond 2^31-1");
+  PT_REQUIRE(eps >= 0.0, PT_INVALID_ARGUMENT, "norm series backward: eps must be >= 0");
+  for (int k = 0; k <= degree; ++k)
+    PT_REQUIRE(x[k] != nullptr && g[k] != nullptr && dx[k] != nullptr, PT_INVALID_ARGUMENT,
+               "norm series backward: null coefficient pointer");
+  return PT_OK;
+}
+
+int dispatch_norm_bwd(int dtype, bool layer, const pt::NormBwdArgs& a) {
+  switch (dtype) {
+    case PT_FLOAT32:
+      return layer ? pt::launch_norm_bwd<float, true>(a) : pt::launch_norm_bwd<float, false>(a);
+    case PT_FLOAT64:
+      return layer ? pt::launch_norm_bwd<double, true>(a) : pt::launch_norm_bwd<double, false>(a);
+    case PT_BFLOAT16:
+      return layer ? pt::launch_norm_bwd<pt::bf16, true>(a) : pt::launch_norm_bwd<pt::bf16, false>(a);
+    case PT_FLOAT16:
+      return layer ? pt::launch_norm_bwd<_Float16, true>(a) : pt::launch_norm_bwd<_Float16, false>(a);
+    default:
+      break;
+  }
+  pt_host::set_error("norm series backward: unknown dtype code");
+  return PT_UNSUPPORTED;
+}
+
 }  // namespace
 
 extern "C" {
@@ -75,6 +109,26 @@ int pt_layer_norm_series_fwd(int dtype, int degree, const void* const* x,
   pt::NormArgs a{degree, x, weight, weight_orders, bias, bias_orders, y, rows, n, eps,
                  static_cast<hipStream_t>(stream)};
   return dispatch_norm(dtype, true, a);
+}
+
+int pt_rms_norm_series_bwd(int dtype, int degree, const void* const* x, const void* const* g,
+                           void* const* dx, int64_t rows, int64_t n, double eps, void* stream) {
+  pt_host::clear_error();
+  int st = check_norm_bwd(dtype, degree, x, g, dx, rows, n, eps);
+  if (st != PT_OK) return st;
+  if (rows == 0) return PT_OK;
+  pt::NormBwdArgs a{degree, x, g, dx, rows, n, eps, static_cast<hipStream_t>(stream)};
+  return dispatch_norm_bwd(dtype, false, a);
+}
+
+int pt_layer_norm_series_bwd(int dtype, int degree, const void* const* x, const void* const* g,
+                             void* const* dx, int64_t rows, int64_t n, double eps, void* stream) {
+  pt_host::clear_error();
+  int st = check_norm_bwd(dtype, degree, x, g, dx, rows, n, eps);
+  if (st != PT_OK) return st;
+  if (rows == 0) return PT_OK;
+  pt::NormBwdArgs a{degree, x, g, dx, rows, n, eps, static_cast<hipStream_t>(stream)};
+  return dispatch_norm_bwd(dtype, true, a);
 }
 
 }  // extern "C"

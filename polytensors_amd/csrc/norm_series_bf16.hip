@@ -4,4 +4,6 @@
 namespace pt {
 template int launch_norm<bf16, false>(const NormArgs&);
 template int launch_norm<bf16, true>(const NormArgs&);
+template int launch_norm_bwd<bf16, false>(const NormBwdArgs&);
+template int launch_norm_bwd<bf16, true>(const NormBwdArgs&);
 }  // namespace pt

@@ -4,4 +4,6 @@
 namespace pt {
 template int launch_norm<float, false>(const NormArgs&);
 template int launch_norm<float, true>(const NormArgs&);
+template int launch_norm_bwd<float, false>(const NormBwdArgs&);
+template int launch_norm_bwd<float, true>(const NormBwdArgs&);
 }  // namespace pt

@@ -124,6 +124,28 @@ __device__ __forceinline__ void unpack_vec(const Vec<bf16, V>& v, float (&f)[V])
   }
 }
 
+// Element e of a storage vector in the arithmetic type, and a pair (e, e+1)
+// written back (one conversion instruction per bfloat16 pair).
+template <typename T, int V>
+__device__ __forceinline__ typename AccOf<T>::type vec_get(const Vec<T, V>& v, int e) {
+  return to_acc(v.v[e]);
+}
+template <int V>
+__device__ __forceinline__ float vec_get(const Vec<bf16, V>& v, int e) {
+  const uint32_t w = reinterpret_cast<const uint32_t*>(&v)[e / 2];
+  return __uint_as_float((e % 2 == 0) ? (w << 16) : (w & 0xffff0000u));
+}
+template <typename T, int V>
+__device__ __forceinline__ void vec_put2(Vec<T, V>& v, int e, typename AccOf<T>::type a,
+                                         typename AccOf<T>::type b) {
+  v.v[e] = from_acc<T>(a);
+  v.v[e + 1] = from_acc<T>(b);
+}
+template <int V>
+__device__ __forceinline__ void vec_put2(Vec<bf16, V>& v, int e, float a, float b) {
+  reinterpret_cast<uint32_t*>(&v)[e / 2] = pack_bf16x2(a, b);
+}
+
 template <typename T, int V>
 __device__ __forceinline__ void pack_vec(const typename AccOf<T>::type (&f)[V], Vec<T, V>& v) {
 #pragma unroll

@@ -126,3 +126,43 @@ def test_mlp_gradient_series_matches_jets_of_grad():
         grad = x.grad
     _check(loss_gpu.coeffs, taylor(loss, [X], degree), torch.float64)
     _check(grad.coeffs, taylor(lambda z: torch.func.grad(loss)(z), [X], degree), torch.float64)
+
+
+@pytest.mark.parametrize("n", [64, 4096, 999])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("degree", [1, 4, 8])
+@pytest.mark.parametrize("layer", [False, True])
+def test_norm_gradient_series(layer, degree, dtype, n):
+    # RMSNorm / LayerNorm value and gradient series (register paths for n = 64, 4096; the
+    # streaming path for n = 999), as /root/reference/tests/test_fused_norm.py:14-35 at degree K.
+    X = [c.to(dtype).double() for c in _series((6, n), degree, seed=27, scale=2.0)]
+    G = [c.to(dtype).double() for c in _series((6, n), degree, seed=28)]
+    x = _poly(X, dtype, requires_grad=True)
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        y = F.layer_norm(x, (n,), eps=1e-5) if layer else F.rms_norm(x, (n,), eps=1e-5)
+        (dx,) = torch.autograd.grad(y, x, _poly(G, dtype))
+    if layer:
+        want_y, want_dx = oracle.layer_norm(X, (n,), eps=1e-5), oracle.layer_norm_backward(X, G, (n,), eps=1e-5)
+    else:
+        want_y, want_dx = oracle.rms_norm(X, (n,), eps=1e-5), oracle.rms_norm_backward(X, G, (n,), eps=1e-5)
+    _check(y.coeffs, want_y, dtype)
+    _check(dx.coeffs, want_dx, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_norm_with_series_weight_gradients(dtype):
+    # The weight multiplies as a separate series product (as the reference's
+    # /root/reference/src/polytensors/_fused_norm.py:69), so its gradient is sum_rows g (*) normalized.
+    degree, n = 3, 256
+    X = _series((8, n), degree, seed=29, scale=2.0)
+    W = _series((n,), degree, seed=30)
+    W[0] = W[0] + 1.0
+    G = _series((8, n), degree, seed=31)
+    x, w = _poly(X, dtype, True), _poly(W, dtype, True)
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        y = F.rms_norm(x, (n,), weight=w, eps=1e-6)
+        dx, dw = torch.autograd.grad(y, (x, w), _poly(G, dtype))
+    normalized = oracle.rms_norm(X, (n,), eps=1e-6)
+    _check(y.coeffs, oracle.cauchy(normalized, W), dtype)
+    _check(dx.coeffs, oracle.rms_norm_backward(X, oracle.cauchy(G, W), (n,), eps=1e-6), dtype)
+    _check(dw.coeffs, [c.sum(0) for c in oracle.cauchy(G, normalized)], dtype)

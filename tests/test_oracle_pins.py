@@ -267,6 +267,32 @@ def test_cross_entropy_softcap_general_series(reduction):
     _check(got, want, 1e-12)
 
 
+@pytest.mark.parametrize("degree", (1, 4))
+def test_rms_norm_backward_series_matches_jets_of_vjp(degree):
+    X = _series((5, 16), degree, seed=54)
+    G = _series((5, 16), degree, seed=55)
+
+    def vjp(x, g):
+        return torch.func.vjp(lambda z: F.rms_norm(z, (16,), eps=1e-5), x)[1](g)[0]
+
+    _check(oracle.rms_norm_backward(X, G, (16,), eps=1e-5), taylor(vjp, [X, G], degree), 1e-12)
+
+
+@pytest.mark.parametrize("degree", (1, 4))
+def test_layer_norm_backward_series_matches_jets_of_vjp(degree):
+    X = _series((5, 16), degree, seed=56)
+    G = _series((5, 16), degree, seed=57)
+
+    def layer_norm(z):   # the explicit composite (torch's native layer_norm has wrong higher jets)
+        d = z - z.mean(-1, keepdim=True)
+        return d * torch.rsqrt((d * d).mean(-1, keepdim=True) + 1e-5)
+
+    def vjp(x, g):
+        return torch.func.vjp(layer_norm, x)[1](g)[0]
+
+    _check(oracle.layer_norm_backward(X, G, (16,), eps=1e-5), taylor(vjp, [X, G], degree), 1e-12)
+
+
 def test_elementwise_product_and_quotient_series():
     # /root/reference/src/polytensors/_range_ops.py:86-93,143-144
     A = _series((4, 9), 5, seed=52)
