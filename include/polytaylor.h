@@ -148,6 +148,25 @@ int pt_cross_entropy_series_fwd(int dtype, int degree, const void* const* logits
                                 double softcap, int reduction, void* const* loss,
                                 void* const* lse, void* workspace, void* stream);
 
+/*
+ * Gradient series of the per-row cross-entropy losses:
+ *   dz(t) = c(t) (*) (softmax(z(t)) - e_y)  per row (times the series of
+ *   1 - tanh(z / softcap)^2 with a softcap), c the row's cotangent series.
+ * logits, rows, classes, row_stride, target, ignore_index, softcap: as the
+ *   forward; lse: the forward's lse output (K+1 pointers [rows], arithmetic
+ *   type); cot: K+1 pointers [rows] of the arithmetic type; dz: K+1 pointers,
+ *   each [rows, classes] contiguous of `dtype`. Ignored rows get zero.
+ * Replaces the degree-1 backward of the reference
+ *   /root/reference/src/polytensors/_cross_entropy_kernels.py:58-85 (_backward),
+ *   /root/reference/src/polytensors/_fused_cross_entropy.py:101-128 (_SeriesCrossEntropy),
+ * at degree K.
+ */
+int pt_cross_entropy_series_bwd(int dtype, int degree, const void* const* logits,
+                                int64_t rows, int64_t classes, int64_t row_stride,
+                                const int64_t* target, int64_t ignore_index,
+                                double softcap, const void* const* lse,
+                                const void* const* cot, void* const* dz, void* stream);
+
 /* Bytes of device workspace pt_cross_entropy_series_fwd needs for a
  * reduction (0 for PT_REDUCTION_NONE). */
 size_t pt_cross_entropy_series_workspace_size(int dtype, int degree,

@@ -149,6 +149,31 @@ def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
     return [F.nll_loss(lp, target, ignore_index=ignore_index, reduction=reduction) for lp in log_softmax]
 
 
+def cross_entropy_backward(Z, target, C, ignore_index=-100, softcap=None):
+    """Gradient series of the per-row losses w.r.t. (N, C) logits for per-row cotangents C:
+    c (*) (softmax(z) - e_y) per kept row, zero for ignored rows, times the series of
+    1 - tanh(z / cap)^2 with a softcap -- the reference's degree-1 backward
+    (/root/reference/src/polytensors/_cross_entropy_kernels.py:58-85) in series arithmetic,
+    with the softmax series of _plain.py:262-273.
+    """
+    from .activations import activation
+
+    if softcap is not None:
+        T = activation([z / softcap for z in Z], "tanh")
+        Zc = [softcap * t for t in T]
+        dT = [(1 if k == 0 else 0) - s for k, s in enumerate(cauchy(T, T))]
+    else:
+        Zc = Z
+    p = softmax_family(Zc, 1)[0]
+    onehot = torch.zeros_like(p[0])
+    keep = target != ignore_index
+    onehot[keep.nonzero().squeeze(1), target[keep]] = 1
+    p = [p[0] - onehot] + p[1:]
+    Cr = [torch.where(keep, c, torch.zeros_like(c)).unsqueeze(1) for c in C]
+    dz = cauchy(Cr, p)
+    return cauchy(dz, dT) if softcap is not None else dz
+
+
 def logsumexp(Z, dim=-1):
     """Log-sum-exp series along ``dim`` (keepdim squeezed), /root/reference/src/polytensors/_plain.py:262-273."""
     return [c.squeeze(dim) for c in softmax_family(Z, dim)[2]]

@@ -39,6 +39,9 @@ _COPY_OPS = {
     aten.clone.default, aten.detach.default, aten._to_copy.default, aten.contiguous.default,
     aten.index_select.default, aten.gather.default, aten.index.Tensor, aten.flip.default,
     aten.roll.default, aten.repeat.default,
+    # the (linear) backward operations of views and gathers, per coefficient
+    aten.slice_backward.default, aten.select_backward.default, aten.diagonal_backward.default,
+    aten.index_add.default, aten.scatter_add.default, aten.unfold_backward.default,
 }
 # In-place arithmetic: the out-of-place rule, written into the target's coefficients
 # (/root/reference/src/polytensors/_range_ops.py:95-103, write).

@@ -21,7 +21,8 @@ _enabled = contextvars.ContextVar("polytensors_amd_fused_cross_entropy", default
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
-def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, softcap=None):
+def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, softcap=None,
+                   allow_grad=False):
     from ._tensor import PolyTensor
 
     if not _enabled.get():
@@ -29,7 +30,7 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
                 "polytensors_amd has no general series rules")
     if not isinstance(input, PolyTensor):
         return "logits must be a PolyTensor"
-    reason = _gate.common_reason((input,))
+    reason = _gate.common_reason((input,), allow_plain_grad=allow_grad)
     if reason is not None:
         return reason
     if input.ndim != 2:
@@ -63,15 +64,69 @@ def _rows(coeffs):
     return [c.contiguous() for c in coeffs]
 
 
+class _SeriesCrossEntropy(torch.autograd.Function):
+    """Per-row loss series with their degree-K gradient series.
+
+    As /root/reference/src/polytensors/_fused_cross_entropy.py:101-128
+    (_SeriesCrossEntropy): the forward kernel gives the per-row losses (and the
+    lse series, saved); the backward kernel computes J(z(t))^T c(t) per row.
+    Reductions are ordinary series operations on the per-row losses.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, target, ignore_index, softcap):
+        from ._tensor import PolyTensor
+
+        z = _rows(logits.coeffs)
+        target = target.contiguous()
+        loss, lse = _ops.cross_entropy_series(z, target, int(ignore_index), 0, float(softcap or 0.0))
+        ctx.save_for_backward(logits, target, lse)
+        ctx.ignore_index, ctx.softcap = int(ignore_index), float(softcap or 0.0)
+        return PolyTensor.from_stacked(loss)
+
+    @staticmethod
+    def backward(ctx, gradient):
+        from ._plain import _plain_range
+        from ._tensor import PolyTensor
+
+        if torch.is_grad_enabled():
+            raise NotImplementedError("second-order reverse mode through the fused cross entropy is not implemented")
+        logits, target, lse = ctx.saved_tensors
+        degree = logits.degree
+        coeffs = gradient.coeffs if isinstance(gradient, PolyTensor) else (gradient,)
+        cot = [c.to(lse.dtype).expand(lse.shape[1:]).contiguous() for c in coeffs]
+        cot += [torch.zeros_like(cot[0]) for _ in range(degree + 1 - len(cot))]
+        token = _plain_range.set(True)   # the engine's thread does not see the caller's context
+        try:
+            dz = _ops.cross_entropy_series_backward(_rows(logits.coeffs), target, ctx.ignore_index, ctx.softcap,
+                                                    lse, cot)
+            dz = PolyTensor.from_stacked(dz)
+        finally:
+            _plain_range.reset(token)
+        return dz, None, None, None
+
+
 def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     """Loss series (a PolyTensor in float32, or float64 for float64 logits).
 
     ``softcap`` caps the logit series as ``softcap * tanh(z / softcap)`` inside the
     kernel, as the reference's fused pass does at degree 1
-    (/root/reference/src/polytensors/_cross_entropy_kernels.py:7-17).
+    (/root/reference/src/polytensors/_cross_entropy_kernels.py:7-17). Under grad the
+    per-row losses come from ``_SeriesCrossEntropy`` and the reduction is a series
+    sum (and division by the count of kept rows), as the reference's
+    /root/reference/src/polytensors/_fused_cross_entropy.py:163-170.
     """
     from ._tensor import PolyTensor
 
+    if torch.is_grad_enabled() and input.requires_grad:
+        losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
+        if reduction == "none":
+            return losses
+        total = losses.sum()
+        if reduction == "sum":
+            return total
+        count = (target != ignore_index).sum().to(losses.dtype)
+        return total / count
     z = _rows(input.coeffs)
     loss, _ = _ops.cross_entropy_series(z, target.contiguous(), int(ignore_index), _lib.REDUCTIONS[reduction],
                                         float(softcap) if softcap is not None else 0.0)
@@ -79,7 +134,8 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
 
 
 def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mean", label_smoothing=0.0):
-    reason = why_ineligible(input, target, weight, reduction, label_smoothing)
+    reason = why_ineligible(input, target, weight, reduction, label_smoothing,
+                            allow_grad=torch.is_grad_enabled() and input.requires_grad)
     if reason is not None:
         raise NotImplementedError(f"cross_entropy: {reason}")
     return fused(input, target, ignore_index=ignore_index, reduction=reduction)
@@ -91,7 +147,8 @@ def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="me
     from ._tensor import PolyTensor
 
     if isinstance(logits, PolyTensor):
-        reason = why_ineligible(logits, target, None, reduction, 0.0, softcap)
+        reason = why_ineligible(logits, target, None, reduction, 0.0, softcap,
+                                allow_grad=torch.is_grad_enabled() and logits.requires_grad)
         if reason is not None:
             raise NotImplementedError(f"cross_entropy: {reason}")
         return fused(logits, target, ignore_index=ignore_index, reduction=reduction, softcap=softcap)

@@ -42,6 +42,8 @@ SIGNATURES = {
                                           _c_vpp, _c_i64, _c_i64, _c_dbl, _c_vp]),
     "pt_cross_entropy_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
                                              _c_i64, _c_dbl, _c_int, _c_vpp, _c_vpp, _c_vp, _c_vp]),
+    "pt_cross_entropy_series_bwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
+                                             _c_i64, _c_dbl, _c_vpp, _c_vpp, _c_vpp, _c_vp]),
     "pt_cross_entropy_series_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_int]),
     "pt_cauchy_matmul": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp,
                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp]),

@@ -317,3 +317,41 @@ def norm_series_backward(x: List[torch.Tensor], grad: List[torch.Tensor], n: int
 @norm_series_backward.register_fake
 def _(x, grad, n, eps, layer):
     return x[0].new_empty((len(x), *x[0].shape))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::cross_entropy_series_backward", mutates_args=(), device_types="cuda")
+def cross_entropy_series_backward(z: List[torch.Tensor], target: torch.Tensor, ignore_index: int, softcap: float,
+                                  lse: torch.Tensor, cot: List[torch.Tensor]) -> torch.Tensor:
+    """Gradient series of the per-row losses w.r.t. (N, C) logits; ``lse`` [K+1, N] from the
+    forward, ``cot`` the K+1 per-row cotangents. Returns [K+1, N, C] in the logits' dtype."""
+    _require(len(z) >= 1 and len(cot) == len(z) and lse.shape[0] == len(z),
+             "cross_entropy_series_backward: z, lse and cot need the same number of orders")
+    first = z[0]
+    for c in z:
+        _require(c.dtype == first.dtype and c.device == first.device and c.shape == first.shape
+                 and c.stride() == first.stride() and c.stride(1) == 1,
+                 "cross_entropy_series_backward: logit rows must be unit-stride with one common row stride")
+    rows, classes = first.shape
+    acc = _acc_dtype(first.dtype)
+    _require(lse.dtype == acc and lse.is_contiguous() and tuple(lse.shape[1:]) == (rows,),
+             "cross_entropy_series_backward: lse must be contiguous [K+1, N] of the arithmetic type")
+    for c in cot:
+        _require(c.dtype == acc and c.is_contiguous() and tuple(c.shape) == (rows,),
+                 "cross_entropy_series_backward: cotangents must be contiguous [N] of the arithmetic type")
+    _require(target.dtype == torch.int64 and target.is_contiguous() and tuple(target.shape) == (rows,),
+             "cross_entropy_series_backward: target must be contiguous int64 [N]")
+    degree = len(z) - 1
+    out = torch.empty((degree + 1, rows, classes), dtype=first.dtype, device=first.device)
+    lib = _lib.load()
+    status = lib.pt_cross_entropy_series_bwd(
+        _lib.DTYPE_CODES[first.dtype], degree, _lib.ptr_array(z), rows, classes,
+        first.stride(0) if rows else classes, target.data_ptr(), ignore_index, float(softcap),
+        _lib.ptr_array(list(lse.unbind(0))), _lib.ptr_array(cot), _lib.ptr_array(list(out.unbind(0))),
+        _lib.stream_of(first.device))
+    _lib.check(status, "cross_entropy_series_bwd")
+    return out
+
+
+@cross_entropy_series_backward.register_fake
+def _(z, target, ignore_index, softcap, lse, cot):
+    return z[0].new_empty((len(z), *z[0].shape))

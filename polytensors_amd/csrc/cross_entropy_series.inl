@@ -270,6 +270,155 @@ static int launch_ce_k(const CeArgs& a) {
   return PT_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Backward: the gradient series of the per-row losses, dz(t) = J(z(t))^T c(t)
+// = c (*) (p - e_y), with p = exp series of (z - lse) the softmax series of the
+// row (lse saved by the forward) and c the row's cotangent series; with a
+// softcap, dz is further multiplied by the series of 1 - tanh(z / cap)^2.
+// Generalises the reference's degree-1 kernel
+// /root/reference/src/polytensors/_cross_entropy_kernels.py:58-85 to degree K.
+// Ignored rows get zero. One block per row streams z once and writes dz once.
+template <typename A, int K, bool CAP>
+__device__ __forceinline__ void ce_bwd_element(const A (&x)[K + 1], bool is_target, const A (&lse)[K + 1],
+                                               const A (&c)[K + 1], A cap, A inv_cap, A (&dz)[K + 1]) {
+  A z[K + 1], dt[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) z[k] = x[k];
+  if constexpr (CAP) softcap_series<A, K>(z, cap, inv_cap, dt);
+  A ju[K + 1], p[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) ju[k] = A(k) * (z[k] - lse[k]);
+  p[0] = exp_acc(z[0] - lse[0]);
+#pragma unroll
+  for (int k = 1; k <= K; ++k) {
+    A s = A(0);
+#pragma unroll
+    for (int j = 1; j <= k; ++j) s = fma(ju[j], p[k - j], s);
+    p[k] = s * (A(1) / A(k));
+  }
+  if (is_target) p[0] -= A(1);
+#pragma unroll
+  for (int k = K; k >= 0; --k) {
+    A s = c[0] * p[k];
+#pragma unroll
+    for (int i = 1; i <= k; ++i) s = fma(c[i], p[k - i], s);
+    dz[k] = s;
+  }
+  if constexpr (CAP) {
+#pragma unroll
+    for (int k = K; k >= 0; --k) {
+      A s = dz[0] * dt[k];
+#pragma unroll
+      for (int i = 1; i <= k; ++i) s = fma(dz[i], dt[k - i], s);
+      dz[k] = s;
+    }
+  }
+}
+
+template <typename T, int K, int THREADS, bool CAP>
+__global__ __launch_bounds__(THREADS) void cross_entropy_series_bwd_kernel(
+    CPtrs<T> z, int64_t classes, int64_t row_stride, bool vec_ok, const int64_t* __restrict__ target,
+    int64_t ignore_index, CPtrs<typename AccOf<T>::type> lse_p, CPtrs<typename AccOf<T>::type> cot_p,
+    MPtrs<T> dz, typename AccOf<T>::type cap, typename AccOf<T>::type inv_cap) {
+  using A = typename AccOf<T>::type;
+  constexpr int V = VecWidth<T>::value;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * row_stride, out = row * classes;
+  const int64_t y = target[row];
+  const bool ignored = (y == ignore_index);
+  A lse[K + 1], c[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+    lse[k] = lse_p.p[k][row];
+    c[k] = ignored ? A(0) : cot_p.p[k][row];
+  }
+  int64_t scalar_from = 0;
+  if (vec_ok) {
+    const int64_t nvec = classes / V;
+    for (int64_t j = threadIdx.x; j < nvec; j += THREADS) {
+      Vec<T, V> a[K + 1];
+#pragma unroll
+      for (int k = 0; k <= K; ++k) a[k] = load_vec_nt<T, V>(z.p[k] + base + j * V);
+#pragma unroll
+      for (int e = 0; e < V; e += 2) {
+        A r[2][K + 1];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          A x[K + 1];
+#pragma unroll
+          for (int k = 0; k <= K; ++k) x[k] = vec_get(a[k], e + h);
+          ce_bwd_element<A, K, CAP>(x, j * V + e + h == y, lse, c, cap, inv_cap, r[h]);
+        }
+#pragma unroll
+        for (int k = 0; k <= K; ++k) vec_put2(a[k], e, r[0][k], r[1][k]);
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) store_vec_nt<T, V>(dz.p[k] + out + j * V, a[k]);
+    }
+    scalar_from = nvec * V;
+  }
+  for (int64_t col = scalar_from + threadIdx.x; col < classes; col += THREADS) {
+    A x[K + 1], r[K + 1];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) x[k] = to_acc(z.p[k][base + col]);
+    ce_bwd_element<A, K, CAP>(x, col == y, lse, c, cap, inv_cap, r);
+#pragma unroll
+    for (int k = 0; k <= K; ++k) dz.p[k][out + col] = from_acc<T>(r[k]);
+  }
+}
+
+template <typename T, int K>
+static int launch_ce_bwd_k(const CeBwdArgs& a) {
+  using A = typename AccOf<T>::type;
+  constexpr int V = VecWidth<T>::value;
+  CPtrs<T> z{};
+  CPtrs<A> lse{}, cot{};
+  MPtrs<T> dz{};
+  bool vec_ok = (a.row_stride * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+                (a.classes * static_cast<int64_t>(sizeof(T))) % 16 == 0;
+  for (int k = 0; k <= K; ++k) {
+    z.p[k] = static_cast<const T*>(a.z[k]);
+    lse.p[k] = static_cast<const A*>(a.lse[k]);
+    cot.p[k] = static_cast<const A*>(a.cot[k]);
+    dz.p[k] = static_cast<T*>(a.dz[k]);
+    vec_ok = vec_ok && pt_host::aligned16(a.z[k]) && pt_host::aligned16(a.dz[k]);
+  }
+  const bool cap = a.softcap > 0.0;
+  const A capv = cap ? static_cast<A>(a.softcap) : A(1);
+  const A inv_cap = A(1) / capv;
+#define PT_CE_BWD_LAUNCH(TH, CP)                                                                     \
+  cross_entropy_series_bwd_kernel<T, K, TH, CP><<<dim3(a.rows), dim3(TH), 0, a.stream>>>(           \
+      z, a.classes, a.row_stride, vec_ok, a.target, a.ignore_index, lse, cot, dz, capv, inv_cap)
+  if (a.classes >= 4096 * static_cast<int64_t>(V)) {
+    if (cap) PT_CE_BWD_LAUNCH(512, true);
+    else PT_CE_BWD_LAUNCH(512, false);
+  } else {
+    if (cap) PT_CE_BWD_LAUNCH(kCeThreads, true);
+    else PT_CE_BWD_LAUNCH(kCeThreads, false);
+  }
+#undef PT_CE_BWD_LAUNCH
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
+
+template <typename T>
+int launch_ce_bwd(const CeBwdArgs& a) {
+  switch (a.degree) {
+    case 0: return launch_ce_bwd_k<T, 0>(a);
+    case 1: return launch_ce_bwd_k<T, 1>(a);
+    case 2: return launch_ce_bwd_k<T, 2>(a);
+    case 3: return launch_ce_bwd_k<T, 3>(a);
+    case 4: return launch_ce_bwd_k<T, 4>(a);
+    case 5: return launch_ce_bwd_k<T, 5>(a);
+    case 6: return launch_ce_bwd_k<T, 6>(a);
+    case 7: return launch_ce_bwd_k<T, 7>(a);
+    case 8: return launch_ce_bwd_k<T, 8>(a);
+    default: break;
+  }
+  pt_host::set_error("cross-entropy series backward: degree outside 0..PT_MAX_DEGREE");
+  return PT_UNSUPPORTED;
+}
+
 template <typename T>
 int launch_ce(const CeArgs& a) {
   switch (a.degree) {

@@ -3,4 +3,5 @@
 
 namespace pt {
 template int launch_ce<bf16>(const CeArgs&);
+template int launch_ce_bwd<bf16>(const CeBwdArgs&);
 }  // namespace pt

@@ -3,4 +3,5 @@
 
 namespace pt {
 template int launch_ce<_Float16>(const CeArgs&);
+template int launch_ce_bwd<_Float16>(const CeBwdArgs&);
 }  // namespace pt

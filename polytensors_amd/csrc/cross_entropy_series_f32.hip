@@ -3,4 +3,5 @@
 
 namespace pt {
 template int launch_ce<float>(const CeArgs&);
+template int launch_ce_bwd<float>(const CeBwdArgs&);
 }  // namespace pt

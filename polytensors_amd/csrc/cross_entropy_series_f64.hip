@@ -3,4 +3,5 @@
 
 namespace pt {
 template int launch_ce<double>(const CeArgs&);
+template int launch_ce_bwd<double>(const CeBwdArgs&);
 }  // namespace pt

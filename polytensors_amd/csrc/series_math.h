@@ -91,15 +91,21 @@ __device__ __forceinline__ void tanh_pair(double v, double& t, double& dt) {
 // Softcap of a series in place: z(t) <- cap tanh(z(t) / cap), by the tanh series
 // of w = z / cap (the capped logits of the reference's fused cross entropy,
 // /root/reference/src/polytensors/_cross_entropy_kernels.py:7-17, at degree K).
+// dt receives the series of the cap's derivative 1 - tanh(z / cap)^2.
 template <typename A, int K>
-__device__ __forceinline__ void softcap_series(A (&z)[K + 1], A cap, A inv_cap) {
-  A jw[K + 1], t[K + 1], dt[K + 1];
+__device__ __forceinline__ void softcap_series(A (&z)[K + 1], A cap, A inv_cap, A (&dt)[K + 1]) {
+  A jw[K + 1], t[K + 1];
 #pragma unroll
   for (int k = 0; k <= K; ++k) jw[k] = A(k) * (z[k] * inv_cap);
   tanh_pair(z[0] * inv_cap, t[0], dt[0]);
   output_ode<A, K, false>(jw, t, dt);
 #pragma unroll
   for (int k = 0; k <= K; ++k) z[k] = cap * t[k];
+}
+template <typename A, int K>
+__device__ __forceinline__ void softcap_series(A (&z)[K + 1], A cap, A inv_cap) {
+  A dt[K + 1];
+  softcap_series<A, K>(z, cap, inv_cap, dt);
 }
 
 }  // namespace pt

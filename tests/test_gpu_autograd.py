@@ -166,3 +166,34 @@ def test_norm_with_series_weight_gradients(dtype):
     _check(y.coeffs, oracle.cauchy(normalized, W), dtype)
     _check(dx.coeffs, oracle.rms_norm_backward(X, oracle.cauchy(G, W), (n,), eps=1e-6), dtype)
     _check(dw.coeffs, [c.sum(0) for c in oracle.cauchy(G, normalized)], dtype)
+
+
+@pytest.mark.parametrize("softcap,strided", [(None, False), (15.0, True)])
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("degree", [1, 4])
+def test_cross_entropy_gradient_series(degree, dtype, reduction, softcap, strided):
+    # /root/reference/tests/test_fused_kernels.py:142-164,186-211 (ignored targets, all reductions,
+    # softcap on a padded row slice) with value and gradient series at degree K.
+    N, C, pad = 150, 3000, 64 if strided else 0
+    full = [c.to(dtype).double() for c in _series((N, C + pad), degree, seed=32, scale=40.0 if softcap else 3.0)]
+    g = torch.Generator().manual_seed(33)
+    y = torch.randint(0, C, (N,), generator=g)
+    y[::7] = -1
+    logits = _poly(full, dtype, requires_grad=True)
+    gshape = (N,) if reduction == "none" else ()
+    Gs = [c.double() for c in _series(gshape, degree, seed=34)]
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        z = logits[:, :C] if strided else logits
+        loss = PolyTensor.cross_entropy(z, y.cuda(), softcap=softcap, ignore_index=-1, reduction=reduction)
+        (dz,) = torch.autograd.grad(loss, logits, _poly(Gs, acc))
+    Z = [c[:, :C] for c in full]
+    _check(loss.coeffs, oracle.cross_entropy(Z, y, ignore_index=-1, reduction=reduction, softcap=softcap), dtype)
+    count = (y != -1).sum().double()
+    rows = [c if reduction == "none" else (c / count if reduction == "mean" else c).expand(N) for c in Gs]
+    want = oracle.cross_entropy_backward(Z, y, rows, ignore_index=-1, softcap=softcap)
+    got = [c[:, :C] for c in dz.coeffs]
+    if strided:
+        assert all(float(c[:, C:].abs().max()) == 0 for c in dz.coeffs)
+    _check(got, want, dtype)

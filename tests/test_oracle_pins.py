@@ -293,6 +293,26 @@ def test_layer_norm_backward_series_matches_jets_of_vjp(degree):
     _check(oracle.layer_norm_backward(X, G, (16,), eps=1e-5), taylor(vjp, [X, G], degree), 1e-12)
 
 
+@pytest.mark.parametrize("softcap", (None, 3.0))
+def test_cross_entropy_backward_series_matches_jets_of_vjp(softcap):
+    degree = 4
+    Z = _series((6, 11), degree, seed=58, scale=2.0)
+    C = _series((6,), degree, seed=59)
+    y = torch.randint(0, 11, (6,), generator=torch.Generator().manual_seed(60))
+    y[2] = -1
+
+    def per_row(z):
+        if softcap is not None:
+            z = softcap * torch.tanh(z / softcap)
+        return F.cross_entropy(z, y, ignore_index=-1, reduction="none")
+
+    def vjp(z, c):
+        return torch.func.vjp(per_row, z)[1](c)[0]
+
+    got = oracle.cross_entropy_backward(Z, y, C, ignore_index=-1, softcap=softcap)
+    _check(got, taylor(vjp, [Z, C], degree), 1e-12)
+
+
 def test_elementwise_product_and_quotient_series():
     # /root/reference/src/polytensors/_range_ops.py:86-93,143-144
     A = _series((4, 9), 5, seed=52)
