@@ -1,6 +1,7 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload attention|matmul|norm|ce|activation]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload attention|matmul|norm|ce|activation|norm_bwd|ce_bwd]
                     [--no-cpu-baseline] [--no-components] [--component-seconds S]
                     [--copy-calibration]
 
@@ -152,8 +153,51 @@ def wl_activation(device):
                 cpu=lambda: cpu_activation(rows, n, K))
 
 
+def wl_norm_bwd(device):
+    """RMSNorm gradient series on config 4a's shape: x, g [5, 8192, 4096] bf16, eps 1e-6."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, rows, n = 4, 8192, 4096
+    gen = _gen(6, device)
+    x = [(torch.randn(rows, n, generator=gen, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    g = [(torch.randn(rows, n, generator=gen, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+
+    def step():
+        return _ops.norm_series_backward(x, g, n, 1e-6, False)
+
+    nbytes = 3 * (K + 1) * rows * n * 2
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+                kernel="norm_series_bwd", dtype="bf16",
+                workload=f"rms_norm_series_backward [{K + 1},{rows},{n}] bf16",
+                cpu=lambda: cpu_norm_bwd(rows, n, K))
+
+
+def wl_ce_bwd(device):
+    """Cross-entropy gradient series on config 4b's shape: logits [5, 8192, 32000] fp32, per-row cotangents."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, rows, classes = 4, 8192, 32000
+    gen = _gen(7, device)
+    z = [torch.randn(rows, classes, generator=gen, device=device) * (2.0 if k == 0 else 0.5 ** k)
+         for k in range(K + 1)]
+    y = torch.randint(0, classes, (rows,), generator=gen, device=device)
+    _, lse = _ops.cross_entropy_series(z, y, -100, 0, 0.0)
+    cot = [torch.randn(rows, generator=gen, device=device) * 0.5 ** k for k in range(K + 1)]
+
+    def step():
+        return _ops.cross_entropy_series_backward(z, y, -100, 0.0, lse, cot)
+
+    nbytes = 2 * (K + 1) * rows * classes * 4 + rows * 8 + 2 * (K + 1) * rows * 4
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+                kernel="cross_entropy_series_bwd", dtype="fp32",
+                workload=f"cross_entropy_series_backward [{K + 1},{rows},{classes}] fp32",
+                cpu=lambda: cpu_ce_bwd(rows, classes, K))
+
+
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
-             "activation": wl_activation}
+             "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd}
 
 
 # ---------------------------------------------------------------------------
@@ -234,6 +278,32 @@ def cpu_activation(rows, n, K):
     t = _cpu_time(lambda: oracle.activation(x, "gelu"))
     nbytes = 2 * (K + 1) * rows * n * 2
     return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"all {rows} rows, n={n} K={K} bf16", seconds=t)
+
+
+def cpu_norm_bwd(rows, n, K):
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(6)
+    x = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    gr = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    t = _cpu_time(lambda: oracle.rms_norm_backward(x, gr, (n,), eps=1e-6))
+    nbytes = 3 * (K + 1) * rows * n * 2
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"all {rows} rows, n={n} K={K} bf16", seconds=t)
+
+
+def cpu_ce_bwd(rows, classes, K):
+    import torch
+    import oracle
+
+    rows = rows // 8
+    g = torch.Generator().manual_seed(7)
+    z = [torch.randn(rows, classes, generator=g) * (2.0 if k == 0 else 0.5 ** k) for k in range(K + 1)]
+    y = torch.randint(0, classes, (rows,), generator=g)
+    cot = [torch.randn(rows, generator=g) * 0.5 ** k for k in range(K + 1)]
+    t = _cpu_time(lambda: oracle.cross_entropy_backward(z, y, cot))
+    nbytes = 2 * (K + 1) * rows * classes * 4
+    return dict(value=nbytes / t / 1e9, unit="GB/s", sample=f"{rows} of 8192 rows, C={classes} K={K} fp32", seconds=t)
 
 
 # ---------------------------------------------------------------------------
