@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 2
+#define PT_ABI_VERSION 3
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -216,6 +216,38 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
                             void* const* out, void* const* lse, int64_t bh,
                             int64_t lq, int64_t lk, int64_t d, int causal,
                             const uint8_t* mask, double scale, void* stream);
+
+/*
+ * Gradient series of pt_taylor_attention_fwd for an output cotangent series G:
+ * coefficient j of dQ, dK, dV is sum_{k<=j} J_{j-k}^T G_k, i.e. the VJP
+ *   P = exp(scale Q K^T - lse), dV = P^T G, dP = G V^T,
+ *   dS = P (dP - rowsum(G O)), dQ = scale dS K, dK = scale dS^T Q
+ * in truncated series arithmetic (products are Cauchy products of orders).
+ * q, k, v, out, grad: K+1 pointers each (a plain operand or cotangent passes
+ *   zeros for orders 1..K); shapes as in pt_taylor_attention_fwd; out and lse
+ *   are that call's outputs for the same q, k, v, mask and scale.
+ * dq ([bh, lq, d]), dk, dv ([bh, lk, d]): K+1 pointers each, or NULL when that
+ *   gradient is not wanted.
+ * workspace: pt_taylor_attention_bwd_workspace_size(...) bytes of device memory.
+ * Pointers must be 16-byte aligned. Deterministic (no atomics).
+ * Replaces the degree-1 fused backward
+ *   /root/reference/src/polytensors/_fused_attention.py:144-163 (backward),
+ *   /root/reference/src/polytensors/_fused_attention.py:267-295 (_SeriesAttention.backward),
+ *   /root/reference/src/polytensors/_attention_kernels.py:85-201 (_block_terms,
+ *   _backward_kv, _backward_q), generalised to degree K.
+ */
+int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
+                            const void* const* k, const void* const* v,
+                            const void* const* out, const void* const* lse,
+                            const void* const* grad, void* const* dq,
+                            void* const* dk, void* const* dv, void* workspace,
+                            int64_t bh, int64_t lq, int64_t lk, int64_t d,
+                            int causal, const uint8_t* mask, double scale,
+                            void* stream);
+
+/* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row
+ * rowsum(G O) series in the arithmetic type). */
+size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq);
 
 /* Activation kinds of pt_activation_series_fwd / _bwd. */
 typedef enum pt_activation {

@@ -131,6 +131,41 @@ def attention(Q, K, V, attn_mask=None, is_causal=False, scale=None):
     return cauchy(probabilities, V, matmul=True)
 
 
+def attention_backward(Q, K, V, G, attn_mask=None, is_causal=False, scale=None):
+    """Gradient series (dQ, dK, dV) of ``attention`` for the output cotangent series ``G``.
+
+    The vector-Jacobian product of softmax(scale Q K^T) V evaluated on series,
+    every product a Cauchy product: P = softmax series of the masked scores
+    (_plain.py:262-273), dV = P^T G, dP = G V^T, dS = P (dP - rowsum(P dP)),
+    dQ = scale dS K, dK = scale dS^T Q -- the reference's degree-1 backward
+    (/root/reference/src/polytensors/_attention_kernels.py:85-201) at degree K.
+    Boolean masks only. A query row with no admissible key has P = 0, as in the
+    fused kernels (lse = +inf, _attention_kernels.py:80-81).
+    """
+    degree = max(len(Q), len(K), len(V), len(G)) - 1
+    Q, K, V, G = (lift(x, degree) for x in (Q, K, V, G))
+    L, S = Q[0].shape[-2], K[0].shape[-2]
+    scale = 1 / math.sqrt(Q[0].shape[-1]) if scale is None else scale
+    scores = cauchy([q * scale for q in Q], [k.transpose(-2, -1) for k in K], matmul=True)
+    keep = torch.ones(L, S, dtype=torch.bool)
+    if is_causal:
+        keep = keep.tril(diagonal=0)
+    if attn_mask is not None:
+        keep = keep & attn_mask
+    scores = [torch.where(keep, c, torch.full((), float("-inf") if k == 0 else 0.0, dtype=c.dtype))
+              for k, c in enumerate(scores)]
+    empty = ~keep.any(-1, keepdim=True)
+    P = [torch.where(empty, torch.zeros((), dtype=p.dtype), p) for p in softmax_family(scores, -1)[0]]
+    Pt = [p.transpose(-2, -1) for p in P]
+    dV = cauchy(Pt, G, matmul=True)
+    dP = cauchy(G, [v.transpose(-2, -1) for v in V], matmul=True)
+    row = [x.sum(-1, keepdim=True) for x in cauchy(P, dP)]
+    dS = cauchy(P, [a - b for a, b in zip(dP, row)])
+    dQ = [scale * x for x in cauchy(dS, K, matmul=True)]
+    dK = [scale * x for x in cauchy([d.transpose(-2, -1) for d in dS], Q, matmul=True)]
+    return dQ, dK, dV
+
+
 def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
     """Per-order loss series of ``F.cross_entropy(z, target)`` on (N, C) logits.
 

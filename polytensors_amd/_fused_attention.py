@@ -12,6 +12,10 @@ Eligibility and conventions follow the degree-1 kernel of the reference
 (/root/reference/src/polytensors/_fused_attention.py:188-316): causal or a
 boolean (L, S) mask (not both), no dropout or GQA, default scale 1/sqrt(d), and
 a query row with no admissible key gets output zero.
+
+Under autograd (a PolyTensor operand requiring grad) the call records
+``_SeriesAttention``, whose backward is the degree-K gradient series kernel
+(the reference's _SeriesAttention, _fused_attention.py:259-295, at any degree).
 """
 
 import contextvars
@@ -40,6 +44,10 @@ def _square_mask(attn_mask, L, S):
     return attn_mask.reshape(L, S)
 
 
+def _needs_grad(*values):
+    return torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+
+
 def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa):
     from ._tensor import PolyTensor
 
@@ -55,9 +63,14 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
         return "query, key and value must be tensors"
     if isinstance(attn_mask, PolyTensor):
         return "the mask must be an ordinary tensor"
-    reason = _gate.common_reason(tensors)
+    grads = _needs_grad(*tensors)
+    reason = _gate.common_reason(tensors, allow_plain_grad=grads)
     if reason is not None:
         return reason
+    if grads and any(not isinstance(x, PolyTensor) and x.requires_grad for x in tensors):
+        # as the reference's gate (_fused_attention.py:242-243): the gradient of an
+        # ordinary operand would be a series, which autograd cannot hand to it
+        return "an ordinary (non-PolyTensor) operand requires grad"
     dtype = query.dtype
     coeffs = [c for x in tensors for c in _gate.coefficients(x, 0)]
     if any(c.dtype != dtype for c in coeffs):
@@ -90,6 +103,63 @@ def _flat(coeffs, shape):
     return [c.expand(shape).reshape(-1, shape[-2], shape[-1]).contiguous() for c in coeffs]
 
 
+def _full(x, degree, shape):
+    """K+1 flattened [bh, T, d] coefficients; an ordinary tensor gets zero higher orders."""
+    from ._tensor import PolyTensor
+
+    if isinstance(x, PolyTensor):
+        return _flat(x.coeffs, shape)
+    base = _flat([x], shape)[0]
+    return [base] + [torch.zeros_like(base) for _ in range(degree)]
+
+
+class _SeriesAttention(torch.autograd.Function):
+    """Degree-K attention with its gradient series.
+
+    As /root/reference/src/polytensors/_fused_attention.py:259-295 (_SeriesAttention):
+    the forward kernel saves the log-sum-exp series, and the backward computes
+    the gradient series of query, key and value (coefficient j = sum_{k<=j}
+    J_{j-k}^T G_k) with the degree-K backward kernels. Ordinary operands get no
+    gradient.
+    """
+
+    @staticmethod
+    def forward(ctx, query, key, value, mask, causal, scale):
+        from ._tensor import PolyTensor
+
+        degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
+        q = _full(query, degree, query.shape)
+        k = _full(key, degree, key.shape)
+        v = _full(value, degree, value.shape)
+        out, lse = _ops.taylor_attention_fwd(q, k, v, mask, causal, scale, degree)
+        ctx.save_for_backward(*q, *k, *v, out, lse)
+        ctx.meta = (degree, mask, causal, scale, query.shape, key.shape)
+        ctx.poly = tuple(isinstance(x, PolyTensor) for x in (query, key, value))
+        return PolyTensor.from_stacked(out.view(degree + 1, *query.shape))
+
+    @staticmethod
+    def backward(ctx, gradient):
+        from ._plain import _plain_range
+        from ._tensor import PolyTensor
+
+        if torch.is_grad_enabled():
+            raise NotImplementedError("second-order reverse mode through the fused attention is not implemented")
+        degree, mask, causal, scale, shape_q, shape_k = ctx.meta
+        saved = ctx.saved_tensors
+        n = degree + 1
+        q, k, v = list(saved[:n]), list(saved[n:2 * n]), list(saved[2 * n:3 * n])
+        out, lse = saved[3 * n], saved[3 * n + 1]
+        token = _plain_range.set(True)   # the engine's thread does not see the caller's context
+        try:
+            g = _full(gradient, degree, shape_q)
+            dq, dk, dv = _ops.taylor_attention_bwd(q, k, v, out, lse, g, mask, causal, scale)
+            grads = (PolyTensor.from_stacked(dq.view(n, *shape_q)), PolyTensor.from_stacked(dk.view(n, *shape_k)),
+                     PolyTensor.from_stacked(dv.view(n, *shape_k)))
+        finally:
+            _plain_range.reset(token)
+        return (*(gr if is_poly else None for gr, is_poly in zip(grads, ctx.poly)), None, None, None)
+
+
 def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
     """Fused degree-K attention of an eligible call (see ``eligible``)."""
     from ._tensor import PolyTensor
@@ -99,6 +169,8 @@ def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
     L, S = query.shape[-2], key.shape[-2]
     mask = _square_mask(attn_mask, L, S)
     scale = default_scale(query.shape[-1]) if scale is None else scale
+    if _needs_grad(query, key, value):
+        return _SeriesAttention.apply(query, key, value, mask, bool(is_causal), float(scale))
     q = _flat(_gate.coefficients(query, degree), query.shape)
     k = _flat(_gate.coefficients(key, degree), key.shape)
     v = _flat(_gate.coefficients(value, degree), value.shape)

@@ -219,6 +219,62 @@ def _(q, k, v, mask, causal, scale, degree):
             q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))
 
 
+@torch.library.custom_op(f"{NAMESPACE}::taylor_attention_bwd", mutates_args=(), device_types="cuda")
+def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[torch.Tensor], out: torch.Tensor,
+                         lse: torch.Tensor, grad: List[torch.Tensor], mask: Optional[torch.Tensor], causal: bool,
+                         scale: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradient series (dq, dk, dv) of ``taylor_attention_fwd`` for the cotangent series ``grad``.
+
+    q, k, v and grad hold degree+1 coefficients each ([bh, L, d] and [bh, S, d]);
+    ``out`` [degree+1, bh, L, d] and ``lse`` [degree+1, bh, L] are the forward's
+    outputs. Returns three [degree+1, ...] tensors in the operands' dtype.
+    """
+    degree = len(q) - 1
+    for name, s in (("q", q), ("k", k), ("v", v), ("grad", grad)):
+        _require(len(s) == degree + 1, f"taylor_attention_bwd: {name} needs degree+1 coefficients")
+        _check_series(f"taylor_attention_bwd {name}", s)
+        _require(s[0].dim() == 3, f"taylor_attention_bwd: {name} must be [bh, length, d]")
+    dtype = q[0].dtype
+    _require(dtype in (torch.float32, torch.float64), "taylor_attention_bwd: float32 or float64 only")
+    bh, lq, d = q[0].shape
+    _require(k[0].shape == v[0].shape and k[0].shape[0] == bh and k[0].shape[2] == d,
+             "taylor_attention_bwd: key/value shapes must be [bh, S, d] matching the query")
+    _require(grad[0].shape == q[0].shape, "taylor_attention_bwd: grad must have the query's shape")
+    _require(all(s[0].dtype == dtype for s in (k, v, grad)), "taylor_attention_bwd: dtypes differ")
+    _require(out.dtype == dtype and out.is_contiguous() and tuple(out.shape) == (degree + 1, bh, lq, d),
+             "taylor_attention_bwd: out must be the forward's contiguous [K+1, bh, L, d] output")
+    _require(lse.dtype == _acc_dtype(dtype) and lse.is_contiguous() and tuple(lse.shape) == (degree + 1, bh, lq),
+             "taylor_attention_bwd: lse must be the forward's contiguous [K+1, bh, L] output")
+    lk = k[0].shape[1]
+    if mask is not None:
+        _require(mask.dtype == torch.bool and mask.shape == (lq, lk) and mask.device == q[0].device,
+                 "taylor_attention_bwd: mask must be a bool (L, S) tensor on the query's device")
+        _require(not causal, "taylor_attention_bwd: mask and causal are exclusive")
+        mask = mask.contiguous()
+    device = q[0].device
+    dq = torch.empty((degree + 1, bh, lq, d), dtype=dtype, device=device)
+    dk = torch.empty((degree + 1, bh, lk, d), dtype=dtype, device=device)
+    dv = torch.empty_like(dk)
+    lib = _lib.load()
+    code = _lib.DTYPE_CODES[dtype]
+    workspace = torch.empty(max(lib.pt_taylor_attention_bwd_workspace_size(code, degree, bh, lq), 1),
+                            dtype=torch.uint8, device=device)
+    status = lib.pt_taylor_attention_bwd(
+        code, degree, _lib.ptr_array(q), _lib.ptr_array(k), _lib.ptr_array(v),
+        _lib.ptr_array(list(out.unbind(0))), _lib.ptr_array(list(lse.unbind(0))), _lib.ptr_array(grad),
+        _lib.ptr_array(list(dq.unbind(0))), _lib.ptr_array(list(dk.unbind(0))), _lib.ptr_array(list(dv.unbind(0))),
+        workspace.data_ptr(), bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(), float(scale),
+        _lib.stream_of(device))
+    _lib.check(status, "taylor_attention_bwd")
+    return dq, dk, dv
+
+
+@taylor_attention_bwd.register_fake
+def _(q, k, v, out, lse, grad, mask, causal, scale):
+    return (q[0].new_empty((len(q), *q[0].shape)), k[0].new_empty((len(k), *k[0].shape)),
+            k[0].new_empty((len(k), *k[0].shape)))
+
+
 # ---------------------------------------------------------------------------
 # Elementwise activation series
 

@@ -25,4 +25,28 @@ struct AttnArgs {
 template <typename T>
 int launch_attention(const AttnArgs& a);
 
+// Backward: every series has degree+1 orders; dq/dk/dv may be null (not
+// computed). workspace holds (degree+1) * bh * lq accumulator-type values.
+struct AttnBwdArgs {
+  int degree;
+  const void* const* q;
+  const void* const* k;
+  const void* const* v;
+  const void* const* out;
+  const void* const* lse;
+  const void* const* grad;
+  void* const* dq;
+  void* const* dk;
+  void* const* dv;
+  void* workspace;
+  int64_t bh, lq, lk, d;
+  bool causal;
+  const uint8_t* mask;
+  double scale;
+  hipStream_t stream;
+};
+
+template <typename T>
+int launch_attention_bwd(const AttnBwdArgs& a);
+
 }  // namespace pt

@@ -24,18 +24,74 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
              "Taylor attention: causal and mask are exclusive");
   PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && (lq + 63) / 64 * bh <= (int64_t{1} << 24), PT_UNSUPPORTED,
              "Taylor attention: sizes beyond the launch grid (query blocks x heads > 2^24)");
-  for (int o = 0; o < q_orders; ++o) PT_REQUIRE(q[o] != nullptr, PT_INVALID_ARGUMENT, "null q");
-  // an empty key sequence may come with null key/value buffers (nothing is read)
+  // empty sequences may come with null buffers (nothing is read or written)
+  const bool no_rows = bh == 0 || lq == 0;
+  for (int o = 0; o < q_orders; ++o) PT_REQUIRE(q[o] != nullptr || no_rows, PT_INVALID_ARGUMENT, "null q");
   for (int o = 0; o < k_orders; ++o) PT_REQUIRE(k[o] != nullptr || lk == 0, PT_INVALID_ARGUMENT, "null k");
   for (int o = 0; o < v_orders; ++o) PT_REQUIRE(v[o] != nullptr || lk == 0, PT_INVALID_ARGUMENT, "null v");
   for (int o = 0; o <= degree; ++o) {
-    PT_REQUIRE(out[o] != nullptr, PT_INVALID_ARGUMENT, "null out");
-    PT_REQUIRE(lse == nullptr || lse[o] != nullptr, PT_INVALID_ARGUMENT, "null lse entry");
+    PT_REQUIRE(out[o] != nullptr || no_rows, PT_INVALID_ARGUMENT, "null out");
+    PT_REQUIRE(lse == nullptr || lse[o] != nullptr || no_rows, PT_INVALID_ARGUMENT, "null lse entry");
   }
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
                  causal != 0, mask, scale, static_cast<hipStream_t>(stream)};
   return dtype == PT_FLOAT32 ? pt::launch_attention<float>(a) : pt::launch_attention<double>(a);
+}
+
+size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq) {
+  if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0) return 0;
+  const size_t acc = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);
+  return static_cast<size_t>(degree + 1) * static_cast<size_t>(bh) * static_cast<size_t>(lq) * acc;
+}
+
+int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const void* const* k,
+                            const void* const* v, const void* const* out, const void* const* lse,
+                            const void* const* grad, void* const* dq, void* const* dk, void* const* dv,
+                            void* workspace, int64_t bh, int64_t lq, int64_t lk, int64_t d, int causal,
+                            const uint8_t* mask, double scale, void* stream) {
+  pt_host::clear_error();
+  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
+             "Taylor attention backward: degree must be in 0..8");
+  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
+             "Taylor attention backward: float32 and float64 only");
+  PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr && lse != nullptr &&
+                 grad != nullptr,
+             PT_INVALID_ARGUMENT, "Taylor attention backward: q, k, v, out, lse and grad are required");
+  PT_REQUIRE(bh >= 0 && lq >= 0 && lk >= 0, PT_INVALID_ARGUMENT, "Taylor attention backward: negative size");
+  PT_REQUIRE(d == 16 || d == 32 || d == 64 || d == 128, PT_UNSUPPORTED,
+             "Taylor attention backward: head dim must be 16, 32, 64 or 128");
+  PT_REQUIRE(!(causal && mask != nullptr), PT_INVALID_ARGUMENT,
+             "Taylor attention backward: causal and mask are exclusive");
+  // grids: (query blocks x heads x slices) and (key blocks x heads x slices), at most 8 slices
+  PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && (lq + 63) / 64 * bh <= (int64_t{1} << 24) &&
+                 (lk + 63) / 64 * bh <= (int64_t{1} << 24),
+             PT_UNSUPPORTED, "Taylor attention backward: sizes beyond the launch grid (blocks x heads > 2^24)");
+  PT_REQUIRE(bh * lq == 0 || workspace != nullptr, PT_INVALID_ARGUMENT,
+             "Taylor attention backward: the workspace is required");
+  PT_REQUIRE(pt_host::aligned16(workspace), PT_INVALID_ARGUMENT,
+             "Taylor attention backward: workspace must be 16-byte aligned");
+  const bool need_q = bh * lq > 0, need_k = bh * lk > 0;
+  for (int o = 0; o <= degree; ++o) {
+    PT_REQUIRE((q[o] != nullptr || !need_q) && (out[o] != nullptr || !need_q) &&
+                   (grad[o] != nullptr || !need_q) && (lse[o] != nullptr || !need_q),
+               PT_INVALID_ARGUMENT, "Taylor attention backward: null q/out/grad/lse entry");
+    PT_REQUIRE((k[o] != nullptr && v[o] != nullptr) || !need_k, PT_INVALID_ARGUMENT,
+               "Taylor attention backward: null k/v entry");
+    PT_REQUIRE(pt_host::aligned16(q[o]) && pt_host::aligned16(k[o]) && pt_host::aligned16(v[o]) &&
+                   pt_host::aligned16(out[o]) && pt_host::aligned16(grad[o]),
+               PT_INVALID_ARGUMENT, "Taylor attention backward: operands must be 16-byte aligned");
+    PT_REQUIRE(dq == nullptr || dq[o] != nullptr || !need_q, PT_INVALID_ARGUMENT, "null dq entry");
+    PT_REQUIRE(dk == nullptr || dk[o] != nullptr || !need_k, PT_INVALID_ARGUMENT, "null dk entry");
+    PT_REQUIRE(dv == nullptr || dv[o] != nullptr || !need_k, PT_INVALID_ARGUMENT, "null dv entry");
+    PT_REQUIRE((dq == nullptr || pt_host::aligned16(dq[o])) && (dk == nullptr || pt_host::aligned16(dk[o])) &&
+                   (dv == nullptr || pt_host::aligned16(dv[o])),
+               PT_INVALID_ARGUMENT, "Taylor attention backward: outputs must be 16-byte aligned");
+  }
+  if (bh == 0) return PT_OK;
+  pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
+                    causal != 0, mask, scale, static_cast<hipStream_t>(stream)};
+  return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
 }
 
 }  // extern "C"

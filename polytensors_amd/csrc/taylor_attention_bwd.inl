@@ -1,0 +1,590 @@
+// Flash-style attention backward of degree-K series on MFMA (gfx950).
+//
+// The gradient series of attention for an output cotangent series G(t)
+// (coefficient j = sum_{k<=j} J_{j-k}^T G_k) is the vector-Jacobian product of
+// O = softmax(scale Q K^T) V evaluated in truncated series arithmetic, every
+// product a Cauchy product (*) of the orders:
+//   P = exp(scale Q (*) K^T - lse)     lse: the forward's log-sum-exp series,
+//   dV = P^T (*) G,   dP = G (*) V^T,   Delta = rowsum(G (*) O),
+//   dS = P (*) (dP - Delta),   dQ = scale dS (*) K,   dK = scale dS^T (*) Q.
+// At degree 1 this is the reference's backward
+// (/root/reference/src/polytensors/_attention_kernels.py:85-201 with the
+// cotangent swap of _fused_attention.py:267-295), here at any degree. The
+// exponential series is P_0 = exp(x_0), P_k = (1/k) sum_{i=1..k} i x_i P_{k-i}
+// with x = scale Q (*) K^T - lse (/root/reference/src/polytensors/_plain.py:153-159).
+// An inadmissible (query, key) pair and a query row with no admissible key
+// (lse_0 = +inf) have P = 0 in every order.
+//
+// Three kernels, deterministic (no atomics):
+// * attn_bwd_delta_kernel: the Delta series of every query row (16 lanes per row).
+// * taylor_attention_bwd_q_kernel: the forward's decomposition (64 queries per
+//   workgroup, 16 per wave, key blocks of 16 of every order of K and V staged
+//   in LDS). Scores and dP are formed transposed (keys x queries) so that dS^T
+//   sits in the accumulator registers in the B-operand layout of
+//   dQ^T += K^T dS^T; lse and Delta of the lane's query are per-lane constants.
+// * taylor_attention_bwd_kv_kernel: the mirror image (64 keys per workgroup, 16
+//   per wave, query blocks of 16 with their Q, G, lse and Delta staged in LDS).
+//   Scores are queries x keys, so that P and dS are the B operands of
+//   dV^T += G^T P and dK^T += Q^T dS.
+// Output accumulators beyond a register budget are split into head-dim slices
+// (a grid dimension; each slice recomputes its scores), and dK and dV get one
+// pass each when both do not fit.
+#pragma once
+
+#include "taylor_attention.inl"
+
+namespace pt {
+
+// Head-dim chunks per slice: the most (a power-of-two divisor of db) whose
+// accumulators stay within `budget` 32-bit registers per lane.
+constexpr int attn_bwd_chunks(int orders, int acc_regs, int outputs, int db, int budget) {
+  int n = db;
+  while (n > 1 && orders * n * acc_regs * outputs > budget) n /= 2;
+  return n;
+}
+
+// Launch plan of the backward kernels: accumulator budget of 160 registers per lane.
+template <typename T, int K, int D>
+struct AttnBwdPlan {
+  using A = typename AccOf<T>::type;
+  static constexpr int DB = D / 16;
+  static constexpr int kAccRegs = 4 * static_cast<int>(sizeof(A) / 4);   // registers per 16x16 accumulator
+  static constexpr int kBudget = 160;
+  static constexpr bool kv_fused = (K + 1) * DB * kAccRegs * 2 <= kBudget;   // dK and dV in one pass
+  static constexpr int NS_KV = attn_bwd_chunks(K + 1, kAccRegs, kv_fused ? 2 : 1, DB, kBudget);
+  static constexpr int NS_Q = attn_bwd_chunks(K + 1, kAccRegs, 1, DB, kBudget);
+  static constexpr size_t kv_lds = AttnShape<T, K, D>::LDS + 2ull * (K + 1) * 16 * sizeof(A);
+  static constexpr bool fits = AttnShape<T, K, D>::fits && kv_lds <= 160 * 1024;
+};
+
+// N consecutive values at p (16-byte loads when the run is a whole number of them).
+template <typename T, int N>
+__device__ __forceinline__ void load_run(const T* p, typename AccOf<T>::type (&out)[N]) {
+  constexpr int V = 16 / sizeof(T);
+  if constexpr (N % V == 0) {
+#pragma unroll
+    for (int i = 0; i < N / V; ++i) {
+      const Vec<T, V> x = load_vec<T, V>(p + i * V);
+#pragma unroll
+      for (int e = 0; e < V; ++e) out[i * V + e] = to_acc(x.v[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = to_acc(p[e]);
+  }
+}
+
+// Delta_k = sum_{a+b=k} rowsum(G_a * O_b) for every query row; 16 lanes per row.
+template <typename T, int K, int D>
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(CPtrs<T> G, CPtrs<T> O,
+                                                             MPtrs<typename AccOf<T>::type> Delta,
+                                                             int64_t rows) {
+  using A = typename AccOf<T>::type;
+  constexpr int EPL = D / 16;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + threadIdx.x / 16;
+  const int j = threadIdx.x % 16;
+  A acc[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) acc[k] = A(0);
+  if (row < rows) {
+    A g[K + 1][EPL], o[K + 1][EPL];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) {
+      load_run<T, EPL>(G.p[k] + row * D + j * EPL, g[k]);
+      load_run<T, EPL>(O.p[k] + row * D + j * EPL, o[k]);
+    }
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+#pragma unroll
+      for (int a = 0; a <= k; ++a)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[k] += g[a][e] * o[k - a][e];
+  }
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc[k] += __shfl_xor(acc[k], off, kWave);
+  }
+  if (row < rows && j == 0) {
+#pragma unroll
+    for (int k = 0; k <= K; ++k) Delta.p[k][row] = acc[k];
+  }
+}
+
+// Probability series of one score element from its raw score accumulators
+// (unscaled), the row's lse series and admissibility.
+template <typename A, int K, typename AccT>
+__device__ __forceinline__ void attn_prob_series(const AccT (&sc)[K + 1], int r, const A (&lse)[K + 1],
+                                                 bool valid, A scale, A (&p)[K + 1]) {
+  p[0] = valid ? exp_fast(static_cast<A>(sc[0][r]) * scale - lse[0]) : A(0);
+  A x[K + 1];
+#pragma unroll
+  for (int i = 1; i <= K; ++i) x[i] = static_cast<A>(sc[i][r]) * scale - lse[i];
+#pragma unroll
+  for (int k = 1; k <= K; ++k) {
+    A t = A(0);
+#pragma unroll
+    for (int i = 1; i <= k; ++i) t += (A(i) * x[i]) * p[k - i];
+    p[k] = t * (A(1) / A(k));
+  }
+}
+
+// dS_k = sum_{a+b=k} P_a (dP_b - Delta_b).
+template <typename A, int K, typename AccT>
+__device__ __forceinline__ void attn_ds_series(const A (&p)[K + 1], const AccT (&dp)[K + 1], int r,
+                                               const A (&delta)[K + 1], A (&ds)[K + 1]) {
+  A u[K + 1];
+#pragma unroll
+  for (int b = 0; b <= K; ++b) u[b] = static_cast<A>(dp[b][r]) - delta[b];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+    A t = A(0);
+#pragma unroll
+    for (int a = 0; a <= k; ++a) t += p[a] * u[k - a];
+    ds[k] = t;
+  }
+}
+
+// Stores the accumulators of one 16-row tile of a [rows, D] output (accumulator
+// n of the slice covers head-dim chunk chunk0 + n; register r of lane group h
+// holds column 16 (chunk0 + n) + acc_row(h, r) of row `row`).
+template <typename T, int K, int NS, typename AccT>
+__device__ __forceinline__ void attn_bwd_store(const AccT (&acc)[K + 1][NS], MPtrs<T>& out, int64_t row,
+                                               int chunk0, int h, typename AccOf<T>::type factor) {
+  using MF = Mfma16<T>;
+  constexpr int D16 = 16;
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      T* dst = out.p[k] + row + (chunk0 + n) * D16;
+      if constexpr (sizeof(T) == 4) {
+        Vec<T, 4> w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w.v[r] = static_cast<T>(acc[k][n][r] * factor);
+        store_vec<T, 4>(dst + 4 * h, w);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[MF::acc_row(h, r)] = static_cast<T>(acc[k][n][r] * factor);
+      }
+    }
+  }
+}
+
+template <typename T, int K, int D, int NS>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
+    CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, int L, int S, const uint8_t* __restrict__ mask,
+    int causal, typename AccOf<T>::type scale) {
+  using A = typename AccOf<T>::type;
+  using MF = Mfma16<T>;
+  using acc_t = typename MF::acc_t;
+  constexpr int LD = AttnShape<T, K, D>::LD;
+  constexpr int DB = D / 16;
+  constexpr int SLICES = DB / NS;
+  constexpr int V = 16 / sizeof(T);
+  constexpr int QV = 4;
+
+  __shared__ T Ks[K + 1][kAttnBN][LD];
+  __shared__ T Vs[K + 1][kAttnBN][LD];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;
+  const int h = lane / 16;
+  // work item: head fastest (consecutive workgroups on consecutive XCDs), then
+  // head-dim slice, then query block, heaviest (last) query block first
+  const int nqb = (L + kAttnBM - 1) / kAttnBM;
+  const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SLICES);
+  const int64_t t = blockIdx.x;
+  const int64_t head = t % bh;
+  const int slice = static_cast<int>((t / bh) % SLICES);
+  const int q_block = (nqb - 1 - static_cast<int>(t / (bh * SLICES))) * kAttnBM;
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qoff = (head * L + (q_ok ? my_q : 0)) * D;
+
+  A lse[K + 1], delta[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lse[o] = q_ok ? LSE.p[o][head * L + my_q] : (o == 0 ? A(__builtin_huge_val()) : A(0));
+    delta[o] = q_ok ? DELTA.p[o][head * L + my_q] : A(0);
+  }
+
+  acc_t acc[K + 1][NS];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int n = 0; n < NS; ++n) acc[o][n] = MF::zero();
+
+  const int hi = causal ? min(S, q_block + kAttnBM) : S;
+  for (int kb0 = 0; kb0 < hi; kb0 += kAttnBN) {
+    __syncthreads();
+    {
+      constexpr int VPR = D / V;
+      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
+        const int o = idx / (kAttnBN * VPR);
+        const int rem = idx % (kAttnBN * VPR);
+        const int r = rem / VPR, cv = (rem % VPR) * V;
+        const int key = kb0 + r;
+        Vec<T, V> kx, vx;
+        if (key < S) {
+          kx = load_vec<T, V>(Kp.p[o] + (head * S + key) * D + cv);
+          vx = load_vec<T, V>(Vp.p[o] + (head * S + key) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) kx.v[e] = vx.v[e] = T(0);
+        }
+        store_vec<T, V>(&Ks[o][r][cv], kx);
+        store_vec<T, V>(&Vs[o][r][cv], vx);
+      }
+    }
+    __syncthreads();
+
+    // S^T_k = sum_{a+b=k} K_b Q_a^T and dP^T_k = sum_{a+b=k} V_b G_a^T (keys x queries)
+    acc_t sc[K + 1], dp[K + 1];
+#pragma unroll
+    for (int o = 0; o <= K; ++o) sc[o] = dp[o] = MF::zero();
+#pragma unroll 1
+    for (int dc = 0; dc < DB; ++dc) {
+      Vec<T, QV> qa[K + 1], kb[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(Q.p[o] + qoff + dc * 16 + 4 * h);
+        kb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Ks[o][c][dc * 16 + 4 * h]);
+      }
+#pragma unroll
+      for (int s = 0; s < QV; ++s)
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MF::mma(kb[k - a].v[s], qa[a].v[s], sc[k]);
+    }
+#pragma unroll 1
+    for (int dc = 0; dc < DB; ++dc) {
+      Vec<T, QV> ga[K + 1], vb[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        ga[o] = *reinterpret_cast<const Vec<T, QV>*>(G.p[o] + qoff + dc * 16 + 4 * h);
+        vb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Vs[o][c][dc * 16 + 4 * h]);
+      }
+#pragma unroll
+      for (int s = 0; s < QV; ++s)
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) dp[k] = MF::mma(vb[k - a].v[s], ga[a].v[s], dp[k]);
+    }
+
+    // dS^T in place of the scores
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kb0 + MF::acc_row(h, r);
+      bool ok = q_ok && key < S;
+      if (causal) ok = ok && key <= my_q;
+      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+      A p[K + 1], ds[K + 1];
+      attn_prob_series<A, K>(sc, r, lse, ok, scale, p);
+      attn_ds_series<A, K>(p, dp, r, delta, ds);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(ds[o]);
+    }
+
+    // dQ^T_k += sum_{a+b=k} K_b^T dS^T_a (head dim x queries)
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const int col = (slice * NS + n) * 16 + c;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int key_row = MF::acc_row(h, s);
+        T kv[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) kv[o] = Ks[o][key_row][col];
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) acc[k][n] = MF::mma(kv[k - a], sc[a][s], acc[k][n]);
+      }
+    }
+  }
+
+  if (q_ok) attn_bwd_store<T, K, NS>(acc, DQ, (head * L + my_q) * D, slice * NS, h, scale);
+}
+
+// WHAT: 1 = dV, 2 = dK, 3 = both.
+template <typename T, int K, int D, int NS, int WHAT>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
+    CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
+    const uint8_t* __restrict__ mask, int causal, typename AccOf<T>::type scale) {
+  using A = typename AccOf<T>::type;
+  using MF = Mfma16<T>;
+  using acc_t = typename MF::acc_t;
+  constexpr int LD = AttnShape<T, K, D>::LD;
+  constexpr int DB = D / 16;
+  constexpr int SLICES = DB / NS;
+  constexpr int V = 16 / sizeof(T);
+  constexpr int QV = 4;
+  constexpr int kBM = 16;                       // queries per block
+  constexpr int kBK = kAttnWaves * 16;          // keys per workgroup
+  constexpr bool DO_V = (WHAT & 1) != 0;
+  constexpr bool DO_K = (WHAT & 2) != 0;
+
+  __shared__ T Qs[K + 1][kBM][LD];
+  __shared__ T Gs[K + 1][kBM][LD];
+  __shared__ A Ls[K + 1][kBM];
+  __shared__ A Ds[K + 1][kBM];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;
+  const int h = lane / 16;
+  // work item: head fastest, then slice, then key block, lightest causal work
+  // (the last key block) last
+  const int nkb = (S + kBK - 1) / kBK;
+  const int64_t bh = gridDim.x / (static_cast<int64_t>(nkb) * SLICES);
+  const int64_t t = blockIdx.x;
+  const int64_t head = t % bh;
+  const int slice = static_cast<int>((t / bh) % SLICES);
+  const int kv_block = static_cast<int>(t / (bh * SLICES)) * kBK;
+  const int my_k = kv_block + wave * 16 + c;
+  const bool k_ok = my_k < S;
+  const int64_t koff = (head * S + (k_ok ? my_k : 0)) * D;
+
+  acc_t acc_v[DO_V ? K + 1 : 1][NS], acc_k[DO_K ? K + 1 : 1][NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+#pragma unroll
+    for (int o = 0; o < (DO_V ? K + 1 : 1); ++o) acc_v[o][n] = MF::zero();
+#pragma unroll
+    for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) acc_k[o][n] = MF::zero();
+  }
+
+  const int lo = causal ? kv_block : 0;
+  for (int qb0 = lo; qb0 < L; qb0 += kBM) {
+    __syncthreads();
+    {
+      constexpr int VPR = D / V;
+      for (int idx = threadIdx.x; idx < (K + 1) * kBM * VPR; idx += kAttnWaves * kWave) {
+        const int o = idx / (kBM * VPR);
+        const int rem = idx % (kBM * VPR);
+        const int r = rem / VPR, cv = (rem % VPR) * V;
+        const int q = qb0 + r;
+        Vec<T, V> qx, gx;
+        if (q < L) {
+          qx = load_vec<T, V>(Q.p[o] + (head * L + q) * D + cv);
+          gx = load_vec<T, V>(G.p[o] + (head * L + q) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) qx.v[e] = gx.v[e] = T(0);
+        }
+        store_vec<T, V>(&Qs[o][r][cv], qx);
+        store_vec<T, V>(&Gs[o][r][cv], gx);
+      }
+      for (int idx = threadIdx.x; idx < (K + 1) * kBM; idx += kAttnWaves * kWave) {
+        const int o = idx / kBM, r = idx % kBM;
+        const int q = qb0 + r;
+        Ls[o][r] = q < L ? LSE.p[o][head * L + q] : (o == 0 ? A(__builtin_huge_val()) : A(0));
+        Ds[o][r] = q < L ? DELTA.p[o][head * L + q] : A(0);
+      }
+    }
+    __syncthreads();
+
+    // S_k = sum_{a+b=k} Q_a K_b^T and dP_k = sum_{a+b=k} G_a V_b^T (queries x keys)
+    acc_t sc[K + 1], dp[DO_K ? K + 1 : 1];
+#pragma unroll
+    for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
+#pragma unroll
+    for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) dp[o] = MF::zero();
+#pragma unroll 1
+    for (int dc = 0; dc < DB; ++dc) {
+      Vec<T, QV> qa[K + 1], kb[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(&Qs[o][c][dc * 16 + 4 * h]);
+        kb[o] = *reinterpret_cast<const Vec<T, QV>*>(Kp.p[o] + koff + dc * 16 + 4 * h);
+      }
+#pragma unroll
+      for (int s = 0; s < QV; ++s)
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MF::mma(qa[a].v[s], kb[k - a].v[s], sc[k]);
+    }
+    if constexpr (DO_K) {
+#pragma unroll 1
+      for (int dc = 0; dc < DB; ++dc) {
+        Vec<T, QV> ga[K + 1], vb[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          ga[o] = *reinterpret_cast<const Vec<T, QV>*>(&Gs[o][c][dc * 16 + 4 * h]);
+          vb[o] = *reinterpret_cast<const Vec<T, QV>*>(Vp.p[o] + koff + dc * 16 + 4 * h);
+        }
+#pragma unroll
+        for (int s = 0; s < QV; ++s)
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) dp[k] = MF::mma(ga[a].v[s], vb[k - a].v[s], dp[k]);
+      }
+    }
+
+    // P in place of the scores (dV), dS in place of dP (dK)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qr = MF::acc_row(h, r);
+      const int q = qb0 + qr;
+      bool ok = k_ok && q < L;
+      if (causal) ok = ok && my_k <= q;
+      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(q) * S + my_k] != 0;
+      A lse[K + 1], p[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) lse[o] = Ls[o][qr];
+      attn_prob_series<A, K>(sc, r, lse, ok, scale, p);
+      if constexpr (DO_K) {
+        A delta[K + 1], ds[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) delta[o] = Ds[o][qr];
+        attn_ds_series<A, K>(p, dp, r, delta, ds);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) dp[o][r] = static_cast<T>(ds[o]);
+      }
+      if constexpr (DO_V) {
+#pragma unroll
+        for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(p[o]);
+      }
+    }
+
+    // dV^T_k += sum_{a+b=k} G_b^T P_a and dK^T_k += sum_{a+b=k} Q_b^T dS_a (head dim x keys)
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const int col = (slice * NS + n) * 16 + c;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int qr = MF::acc_row(h, s);
+        if constexpr (DO_V) {
+          T gv[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) gv[o] = Gs[o][qr][col];
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc_v[k][n] = MF::mma(gv[k - a], sc[a][s], acc_v[k][n]);
+        }
+        if constexpr (DO_K) {
+          T qv[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) qv[o] = Qs[o][qr][col];
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc_k[k][n] = MF::mma(qv[k - a], dp[a][s], acc_k[k][n]);
+        }
+      }
+    }
+  }
+
+  if (!k_ok) return;
+  const int64_t row = (head * S + my_k) * D;
+  if constexpr (DO_V) attn_bwd_store<T, K, NS>(acc_v, DV, row, slice * NS, h, A(1));
+  if constexpr (DO_K) attn_bwd_store<T, K, NS>(acc_k, DK, row, slice * NS, h, scale);
+}
+
+template <typename T, int K, int D>
+static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
+  using A = typename AccOf<T>::type;
+  using Plan = AttnBwdPlan<T, K, D>;
+  if constexpr (!Plan::fits) {
+    pt_host::set_error("Taylor attention backward: degree and head dim exceed the LDS budget for this dtype");
+    return PT_UNSUPPORTED;
+  } else {
+    CPtrs<T> q{}, k{}, v{}, o{}, g{};
+    CPtrs<A> lse{}, delta_in{};
+    MPtrs<A> delta{};
+    MPtrs<T> dq{}, dk{}, dv{};
+    const int64_t rows = a.bh * a.lq;
+    for (int i = 0; i <= K; ++i) {
+      q.p[i] = static_cast<const T*>(a.q[i]);
+      k.p[i] = static_cast<const T*>(a.k[i]);
+      v.p[i] = static_cast<const T*>(a.v[i]);
+      o.p[i] = static_cast<const T*>(a.out[i]);
+      g.p[i] = static_cast<const T*>(a.grad[i]);
+      lse.p[i] = static_cast<const A*>(a.lse[i]);
+      delta.p[i] = static_cast<A*>(a.workspace) + i * rows;
+      delta_in.p[i] = delta.p[i];
+      if (a.dq != nullptr) dq.p[i] = static_cast<T*>(a.dq[i]);
+      if (a.dk != nullptr) dk.p[i] = static_cast<T*>(a.dk[i]);
+      if (a.dv != nullptr) dv.p[i] = static_cast<T*>(a.dv[i]);
+    }
+    const int L = static_cast<int>(a.lq), S = static_cast<int>(a.lk);
+    const A scale = static_cast<A>(a.scale);
+    const int causal = a.causal ? 1 : 0;
+    if (rows > 0) {
+      attn_bwd_delta_kernel<T, K, D><<<dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0, a.stream>>>(
+          g, o, delta, rows);
+      PT_LAUNCH_CHECK();
+    }
+    if (a.dq != nullptr && rows > 0) {
+      constexpr int SL = Plan::DB / Plan::NS_Q;
+      const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
+      taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+          q, k, v, g, lse, delta_in, dq, L, S, a.mask, causal, scale);
+      PT_LAUNCH_CHECK();
+    }
+    if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
+      constexpr int SL = Plan::DB / Plan::NS_KV;
+      const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+      const dim3 block(kAttnWaves * kWave);
+      if constexpr (Plan::kv_fused) {
+        taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 3><<<grid, block, 0, a.stream>>>(
+            q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+        PT_LAUNCH_CHECK();
+      } else {
+        if (a.dv != nullptr) {
+          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 1><<<grid, block, 0, a.stream>>>(
+              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+          PT_LAUNCH_CHECK();
+        }
+        if (a.dk != nullptr) {
+          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 2><<<grid, block, 0, a.stream>>>(
+              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+          PT_LAUNCH_CHECK();
+        }
+      }
+    }
+    return PT_OK;
+  }
+}
+
+template <typename T, int K>
+static int launch_attention_bwd_k(const AttnBwdArgs& a) {
+  switch (a.d) {
+    case 16: return launch_attention_bwd_kd<T, K, 16>(a);
+    case 32: return launch_attention_bwd_kd<T, K, 32>(a);
+    case 64: return launch_attention_bwd_kd<T, K, 64>(a);
+    case 128: return launch_attention_bwd_kd<T, K, 128>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention backward: head dim must be 16, 32, 64 or 128");
+  return PT_UNSUPPORTED;
+}
+
+template <typename T>
+int launch_attention_bwd(const AttnBwdArgs& a) {
+  switch (a.degree) {
+    case 0: return launch_attention_bwd_k<T, 0>(a);
+    case 1: return launch_attention_bwd_k<T, 1>(a);
+    case 2: return launch_attention_bwd_k<T, 2>(a);
+    case 3: return launch_attention_bwd_k<T, 3>(a);
+    case 4: return launch_attention_bwd_k<T, 4>(a);
+    case 5: return launch_attention_bwd_k<T, 5>(a);
+    case 6: return launch_attention_bwd_k<T, 6>(a);
+    case 7: return launch_attention_bwd_k<T, 7>(a);
+    case 8: return launch_attention_bwd_k<T, 8>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention backward: degree outside 0..PT_MAX_DEGREE");
+  return PT_UNSUPPORTED;
+}
+
+}  // namespace pt

@@ -313,6 +313,34 @@ def test_cross_entropy_backward_series_matches_jets_of_vjp(softcap):
     _check(got, taylor(vjp, [Z, C], degree), 1e-12)
 
 
+@pytest.mark.parametrize("mode,degree", (("causal", 1), ("causal", 3), ("window", 2), ("none", 3)))
+def test_attention_backward_series_matches_jets_of_vjp(mode, degree):
+    L, S, d = 7, 9, 4
+    Q = _series((2, L, d), degree, seed=61)
+    K, V = (_series((2, S, d), degree, seed=62 + i) for i in range(2))
+    G = _series((2, L, d), degree, seed=64)
+    i, j = torch.arange(L)[:, None], torch.arange(S)[None, :]
+    window = (i + 2 >= j) & (i + 2 - j <= 3)
+    window[3] = False                                      # a query row with no admissible key
+    mask = {"causal": None, "window": window, "none": None}[mode]
+    excluded = {"causal": ~torch.ones(L, S, dtype=torch.bool).tril(), "window": ~window}.get(mode)
+
+    def vjp(q, k, v, g):
+        def f(a, b, c):
+            s = 0.4 * (a @ b.transpose(-2, -1))
+            if excluded is None:
+                return torch.softmax(s, -1) @ c
+            empty = excluded.all(-1, keepdim=True)          # such a row: zero output, no gradient
+            p = torch.softmax(s.masked_fill(excluded & ~empty, float("-inf")), -1)
+            return torch.where(empty, torch.zeros((), dtype=p.dtype), p) @ c
+        return torch.func.vjp(f, q, k, v)[1](g)
+
+    got = oracle.attention_backward(Q, K, V, G, attn_mask=mask, is_causal=mode == "causal", scale=0.4)
+    want = taylor(vjp, [Q, K, V, G], degree)
+    for which in range(3):
+        _check(got[which], [w[which] for w in want], 1e-12)
+
+
 def test_elementwise_product_and_quotient_series():
     # /root/reference/src/polytensors/_range_ops.py:86-93,143-144
     A = _series((4, 9), 5, seed=52)
