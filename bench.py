@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|matmul|norm|ce|activation|norm_bwd|ce_bwd]
+                    [--workload attention|matmul|norm|ce|activation|norm_bwd|ce_bwd|attention_bwd]
                     [--no-cpu-baseline] [--no-components] [--component-seconds S]
                     [--copy-calibration]
 
@@ -71,6 +71,38 @@ def wl_attention(device, dense_orders=False):
                 workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} fp32 causal"
                          + (" dense orders" if dense_orders else " line inputs (orders 2..4 zero)"),
                 cpu=lambda: cpu_attention(L, d, K))
+
+
+def wl_attention_bwd(device):
+    """Attention gradient series on config 3's shape (B=4 H=16 L=2048 d=128, K=4, fp32, causal, line
+    inputs) for a random cotangent series G_k ~ N(0,1) 0.5^k: the dQ, dK and dV series."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(8, device)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [base, direction] + [torch.zeros(B * H, L, d, device=device) for _ in range(2, K + 1)]
+
+    q, k, v = line(), line(), line()
+    cot = [torch.randn(B * H, L, d, generator=g, device=device) * 0.5 ** o for o in range(K + 1)]
+    scale = 1 / math.sqrt(d)
+    out, lse = _ops.taylor_attention_fwd(q, k, v, None, True, scale, K)
+
+    def step():
+        return _ops.taylor_attention_bwd(q, k, v, out, lse, cot, None, True, scale)
+
+    pairs = (K + 1) * (K + 2) // 2
+    # five series products over the causal pairs: S (recomputed), dP, dV, dK, dQ
+    flops = 5 * pairs * 2 * d * B * H * L * (L + 1) / 2
+    nbytes = 8 * (K + 1) * B * H * L * d * 4               # q, k, v, out, G read; dq, dk, dv written
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_FP32_MFMA,
+                bytes=nbytes, kernel="taylor_attention_bwd", dtype="fp32",
+                workload=f"taylor_attention_bwd B={B} H={H} L={L} d={d} K={K} fp32 causal line inputs",
+                cpu=lambda: cpu_attention_bwd(L, d, K))
 
 
 def wl_matmul(device):
@@ -197,7 +229,8 @@ def wl_ce_bwd(device):
 
 
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
-             "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd}
+             "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
+             "attention_bwd": wl_attention_bwd}
 
 
 # ---------------------------------------------------------------------------
@@ -229,6 +262,23 @@ def cpu_attention(L, d, K, heads=64):
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"all {heads} (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
+
+
+def cpu_attention_bwd(L, d, K, heads=16):
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(8)
+    q, k, v, cot = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(4))
+
+    def some_heads():
+        for _ in range(heads):
+            oracle.attention_backward(q, k, v, cot, is_causal=True)
+
+    t = _cpu_time(some_heads, reps=1)
+    flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
+    return dict(value=flops / t / 1e12, unit="TFLOP/s",
+                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
 
 
 def cpu_matmul(n, K):
