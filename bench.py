@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|matmul|norm|ce|activation|norm_bwd|ce_bwd|attention_bwd]
+                    [--workload attention|attention_window|attention_bwd|matmul|norm|ce|activation|norm_bwd|ce_bwd]
                     [--no-cpu-baseline] [--no-components] [--component-seconds S]
                     [--copy-calibration]
 
@@ -71,6 +71,39 @@ def wl_attention(device, dense_orders=False):
                 workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} fp32 causal"
                          + (" dense orders" if dense_orders else " line inputs (orders 2..4 zero)"),
                 cpu=lambda: cpu_attention(L, d, K))
+
+
+def wl_attention_window(device):
+    """Config 3's shape with a boolean sliding-window mask (key j admissible for query i iff
+    0 <= i - j < 256) instead of causal: the kernel visits only the key blocks in each query
+    block's mask range. Work is the dense-series count over the admissible pairs."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K, W = 4, 16, 2048, 128, 4, 256
+    g = _gen(9, device)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [base, direction] + [torch.zeros(B * H, L, d, device=device) for _ in range(2, K + 1)]
+
+    q, k, v = line(), line(), line()
+    i = torch.arange(L, device=device)
+    mask = ((i[:, None] - i[None, :]) >= 0) & ((i[:, None] - i[None, :]) < W)
+    scale = 1 / math.sqrt(d)
+
+    def step():
+        return _ops.taylor_attention_fwd(q, k, v, mask, False, scale, K)
+
+    pairs = (K + 1) * (K + 2) // 2
+    admissible = W * (W + 1) // 2 + (L - W) * W
+    flops = 2 * pairs * 2 * d * B * H * admissible
+    nbytes = 4 * (K + 1) * B * H * L * d * 4 + L * L
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_FP32_MFMA,
+                bytes=nbytes, kernel="taylor_attention_window", dtype="fp32",
+                workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} fp32 sliding window {W} (bool mask)",
+                cpu=lambda: cpu_attention_window(L, d, K, W))
 
 
 def wl_attention_bwd(device):
@@ -230,7 +263,7 @@ def wl_ce_bwd(device):
 
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
-             "attention_bwd": wl_attention_bwd}
+             "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window}
 
 
 # ---------------------------------------------------------------------------
@@ -262,6 +295,25 @@ def cpu_attention(L, d, K, heads=64):
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"all {heads} (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
+
+
+def cpu_attention_window(L, d, K, W, heads=16):
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(9)
+    q, k, v = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(3))
+    i = torch.arange(L)
+    mask = ((i[:, None] - i[None, :]) >= 0) & ((i[:, None] - i[None, :]) < W)
+
+    def some_heads():
+        for _ in range(heads):
+            oracle.attention(q, k, v, attn_mask=mask)
+
+    t = _cpu_time(some_heads, reps=1)
+    flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * (W * (W + 1) // 2 + (L - W) * W)
+    return dict(value=flops / t / 1e12, unit="TFLOP/s",
+                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 window {W}", seconds=t)
 
 
 def cpu_attention_bwd(L, d, K, heads=16):

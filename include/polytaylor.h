@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 3
+#define PT_ABI_VERSION 4
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -203,6 +203,8 @@ int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
  *      /root/reference/src/polytensors/_attention_kernels.py:70-76).
  * causal: key j admissible for query i iff j <= i.
  * mask: NULL, or [lq, lk] uint8 (nonzero = admissible); not with causal.
+ * mask_ranges: NULL, or pt_attention_mask_ranges(mask, ...) of this mask: key
+ *   blocks outside each query block's admissible range are then skipped.
  * Replaces the degree-1 fused forward
  *   /root/reference/src/polytensors/_fused_attention.py:126-141 (forward),
  *   /root/reference/src/polytensors/_attention_kernels.py:27-82 (_forward),
@@ -215,7 +217,22 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
                             const void* const* v, int v_orders,
                             void* const* out, void* const* lse, int64_t bh,
                             int64_t lq, int64_t lk, int64_t d, int causal,
-                            const uint8_t* mask, double scale, void* stream);
+                            const uint8_t* mask, const int32_t* mask_ranges,
+                            double scale, void* stream);
+
+/*
+ * Block ranges of a boolean [lq, lk] attention mask (nonzero = admissible),
+ * the reference's _mask_ranges
+ *   /root/reference/src/polytensors/_fused_attention.py:81-99:
+ * for each 64-row query block the first and one-past-last admissible key,
+ * then for each 64-key block the first and one-past-last query admitting one of
+ * its keys ((0, 0) when none). ranges: pt_attention_mask_ranges_count(lq, lk)
+ * int32 of device memory. Computed once per mask, reused by any number of
+ * forward and backward calls with that mask.
+ */
+int64_t pt_attention_mask_ranges_count(int64_t lq, int64_t lk);
+int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk,
+                             int32_t* ranges, void* stream);
 
 /*
  * Gradient series of pt_taylor_attention_fwd for an output cotangent series G:
@@ -229,6 +246,7 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
  * dq ([bh, lq, d]), dk, dv ([bh, lk, d]): K+1 pointers each, or NULL when that
  *   gradient is not wanted.
  * workspace: pt_taylor_attention_bwd_workspace_size(...) bytes of device memory.
+ * mask, mask_ranges: as in pt_taylor_attention_fwd.
  * Pointers must be 16-byte aligned. Deterministic (no atomics).
  * Replaces the degree-1 fused backward
  *   /root/reference/src/polytensors/_fused_attention.py:144-163 (backward),
@@ -242,7 +260,8 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
                             const void* const* grad, void* const* dq,
                             void* const* dk, void* const* dv, void* workspace,
                             int64_t bh, int64_t lq, int64_t lk, int64_t d,
-                            int causal, const uint8_t* mask, double scale,
+                            int causal, const uint8_t* mask,
+                            const int32_t* mask_ranges, double scale,
                             void* stream);
 
 /* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row

@@ -174,6 +174,17 @@ def _(a, b, degree, trans_b):
 # ---------------------------------------------------------------------------
 # Taylor flash attention forward
 
+def _mask_ranges(mask, lq, lk):
+    """Block ranges of a bool (L, S) mask on its device (skipped key/query blocks), or None."""
+    if mask is None:
+        return None
+    lib = _lib.load()
+    ranges = torch.empty(max(lib.pt_attention_mask_ranges_count(lq, lk), 1), dtype=torch.int32, device=mask.device)
+    _lib.check(lib.pt_attention_mask_ranges(mask.data_ptr(), lq, lk, ranges.data_ptr(), _lib.stream_of(mask.device)),
+               "attention_mask_ranges")
+    return ranges
+
+
 @torch.library.custom_op(f"{NAMESPACE}::taylor_attention_fwd", mutates_args=(), device_types="cuda")
 def taylor_attention_fwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[torch.Tensor],
                          mask: Optional[torch.Tensor], causal: bool, scale: float,
@@ -202,11 +213,13 @@ def taylor_attention_fwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
         mask = mask.contiguous()
     out = torch.empty((degree + 1, bh, lq, d), dtype=dtype, device=q[0].device)
     lse = torch.empty((degree + 1, bh, lq), dtype=_acc_dtype(dtype), device=q[0].device)
+    ranges = _mask_ranges(mask, lq, lk)
     lib = _lib.load()
     status = lib.pt_taylor_attention_fwd(
         _lib.DTYPE_CODES[dtype], degree, _lib.ptr_array(q), len(q), _lib.ptr_array(k), len(k),
         _lib.ptr_array(v), len(v), _lib.ptr_array(list(out.unbind(0))), _lib.ptr_array(list(lse.unbind(0))),
-        bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(), float(scale),
+        bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(),
+        None if ranges is None else ranges.data_ptr(), float(scale),
         _lib.stream_of(q[0].device))
     _lib.check(status, "taylor_attention_fwd")
     return out, lse
@@ -255,6 +268,7 @@ def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
     dq = torch.empty((degree + 1, bh, lq, d), dtype=dtype, device=device)
     dk = torch.empty((degree + 1, bh, lk, d), dtype=dtype, device=device)
     dv = torch.empty_like(dk)
+    ranges = _mask_ranges(mask, lq, lk)
     lib = _lib.load()
     code = _lib.DTYPE_CODES[dtype]
     workspace = torch.empty(max(lib.pt_taylor_attention_bwd_workspace_size(code, degree, bh, lq), 1),
@@ -263,7 +277,8 @@ def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
         code, degree, _lib.ptr_array(q), _lib.ptr_array(k), _lib.ptr_array(v),
         _lib.ptr_array(list(out.unbind(0))), _lib.ptr_array(list(lse.unbind(0))), _lib.ptr_array(grad),
         _lib.ptr_array(list(dq.unbind(0))), _lib.ptr_array(list(dk.unbind(0))), _lib.ptr_array(list(dv.unbind(0))),
-        workspace.data_ptr(), bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(), float(scale),
+        workspace.data_ptr(), bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(),
+        None if ranges is None else ranges.data_ptr(), float(scale),
         _lib.stream_of(device))
     _lib.check(status, "taylor_attention_bwd")
     return dq, dk, dv

@@ -18,12 +18,17 @@ struct AttnArgs {
   int64_t bh, lq, lk, d;
   bool causal;
   const uint8_t* mask;
+  const int32_t* mask_ranges;   // null, or the block ranges of mask (launch_attention_mask_ranges)
   double scale;
   hipStream_t stream;
 };
 
 template <typename T>
 int launch_attention(const AttnArgs& a);
+
+// Block ranges of a boolean (L, S) mask into ranges[attention_mask_ranges_count(L, S)].
+int64_t attention_mask_ranges_count(int64_t lq, int64_t lk);
+int launch_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, hipStream_t stream);
 
 // Backward: every series has degree+1 orders; dq/dk/dv may be null (not
 // computed). workspace holds (degree+1) * bh * lq accumulator-type values.
@@ -42,6 +47,7 @@ struct AttnBwdArgs {
   int64_t bh, lq, lk, d;
   bool causal;
   const uint8_t* mask;
+  const int32_t* mask_ranges;
   double scale;
   hipStream_t stream;
 };

@@ -93,6 +93,83 @@ __device__ __forceinline__ void attn_work_item(int L, int64_t& head, int& q_bloc
   q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
 }
 
+// Block ranges of a boolean (L, S) mask, the reference's _mask_ranges
+// (/root/reference/src/polytensors/_fused_attention.py:81-99) at this build's
+// block sizes: for each 64-row query block the first and one-past-last key
+// admissible for any of its rows, then for each 64-key block the first and
+// one-past-last query admitting any of its keys; (0, 0) for a block with none.
+// The attention kernels skip the key (query) blocks outside these ranges.
+// One workgroup per block; the mask is read once per block set.
+constexpr int kAttnRangeBlock = 64;
+
+template <int Unused = 0>   // a template: this header is included by several translation units
+__global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __restrict__ mask, int L, int S,
+                                                               int32_t* __restrict__ ranges) {
+  __shared__ int lo_s, hi_s;
+  const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
+  const int b = blockIdx.x;
+  if (threadIdx.x == 0) {
+    lo_s = INT32_MAX;
+    hi_s = -1;
+  }
+  __syncthreads();
+  int lo = INT32_MAX, hi = -1;
+  if (b < nqb) {
+    const int r0 = b * kAttnRangeBlock, nr = min(kAttnRangeBlock, L - r0);
+    for (int r = 0; r < nr; ++r) {
+      const uint8_t* row = mask + static_cast<int64_t>(r0 + r) * S;
+#pragma unroll 8
+      for (int col = threadIdx.x; col < S; col += 256) {
+        if (row[col] != 0) {
+          lo = min(lo, col);
+          hi = max(hi, col);
+        }
+      }
+    }
+  } else {
+    const int c0 = (b - nqb) * kAttnRangeBlock, nc = min(kAttnRangeBlock, S - c0);
+    const int col = threadIdx.x % kAttnRangeBlock;
+    if (col < nc) {
+#pragma unroll 8
+      for (int r = threadIdx.x / kAttnRangeBlock; r < L; r += 256 / kAttnRangeBlock) {
+        if (mask[static_cast<int64_t>(r) * S + c0 + col] != 0) {
+          lo = min(lo, r);
+          hi = max(hi, r);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) {
+    lo = min(lo, __shfl_xor(lo, off, kWave));
+    hi = max(hi, __shfl_xor(hi, off, kWave));
+  }
+  if (threadIdx.x % kWave == 0) {
+    atomicMin(&lo_s, lo);   // LDS atomics
+    atomicMax(&hi_s, hi);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool any = hi_s >= 0;
+    ranges[2 * b] = any ? lo_s : 0;
+    ranges[2 * b + 1] = any ? hi_s + 1 : 0;
+  }
+}
+
+// Key range [lo, hi) a query workgroup visits: causal and mask-range bounds,
+// lo rounded down to a key block.
+__device__ __forceinline__ void attn_key_range(int S, int q_block, int causal, const int32_t* ranges, int& lo,
+                                               int& hi) {
+  lo = 0;
+  hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / kAttnBN * kAttnBN;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+  }
+}
+
 // E is the head-dim interleave of the output accumulators: accumulator
 // g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
 // (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).
@@ -196,8 +273,8 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
-    MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask, int causal,
-    typename AccOf<T>::type scale) {
+    MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask,
+    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -245,10 +322,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 #pragma unroll
   for (int o = 0; o <= K; ++o) lsum[o] = A(0);
 
-  int hi = S;
-  if (causal) hi = min(S, q_block + kAttnBM);
+  int lo, hi;
+  attn_key_range(S, q_block, causal, ranges, lo, hi);
 
-  for (int kb0 = 0; kb0 < hi; kb0 += kAttnBN) {
+  for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
     __syncthreads();
     // ---- stage K and V rows kb0 .. kb0+15 of every order (zero past S) ----
     {
@@ -503,7 +580,7 @@ __device__ __forceinline__ void attn_load_v_step(Vec<float, AttnPvE<D>::value> (
 template <int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_kernel(
     CPtrs<float> Q, CPtrs<float> Kp, CPtrs<float> Vp, MPtrs<float> O, MPtrs<float> LSE, int L, int S,
-    const uint8_t* __restrict__ mask, int causal, float scale) {
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
   using A = float;
   using MF = Mfma16<float>;
   using acc_t = MF::acc_t;
@@ -532,9 +609,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 #pragma unroll
   for (int o = 0; o <= K; ++o) qrow[o] = Q.p[o] + (head * L + q_row) * D;
 
-  int hi = S;
-  if (causal) hi = min(S, q_block + kAttnBM);
-  const int nblocks = (hi + kAttnBN - 1) / kAttnBN;   // >= 1: the launcher requires S >= 16
+  int lo, hi;
+  attn_key_range(S, q_block, causal, ranges, lo, hi);
+  // a workgroup whose rows admit no key keeps one (fully masked) block, so the
+  // pipeline below always has a first block (the launcher requires S >= 16)
+  if (hi <= lo) {
+    lo = 0;
+    hi = kAttnBN;
+  }
+  const int nblocks = (hi - lo + kAttnBN - 1) / kAttnBN;
 
   // Mask bits of this lane's keys 4h .. 4h+3 of a key block (the rows of its
   // score registers r = 0..3) are one aligned 32-bit read of the mask row; it
@@ -568,14 +651,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
         static_cast<short>(0), mask != nullptr ? L * S : 4, kBufferRsrcWord3);
     const uint32_t mofs = mask != nullptr ? static_cast<uint32_t>(q_row * S + 4 * h) : 0u;
     const uint32_t kofs = static_cast<uint32_t>((c * D + 4 * h) * 4);
-    const int last = (nblocks - 1) * kAttnBN;
+    const int last = lo + (nblocks - 1) * kAttnBN;
     // block b's operands go to buffer b % 3; the loop is unrolled by three so the
     // buffers rotate statically (a register copy would wait for its load), and
     // runs a multiple of three blocks, the surplus ones re-reading the last
     // block and excluded from the maximum
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int rb = min(b * kAttnBN, last);
+      const int rb = min(lo + b * kAttnBN, last);
 #pragma unroll
       for (int dc = 0; dc < DB; ++dc) kb[b][dc] = attn_buffer_load4(krs, kofs + (rb * D + dc * 16) * 4);
       mb[b] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs + mstep * rb, 0, 0);
@@ -584,7 +667,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
     for (int j0 = 0; j0 < nblocks; j0 += 3) {
 #pragma unroll
       for (int u = 0; u < 3; ++u) {
-        const int kb0 = (j0 + u) * kAttnBN;
+        const int kb0 = lo + (j0 + u) * kAttnBN;
         const int ra = min(kb0 + 2 * kAttnBN, last);
 #pragma unroll
         for (int dc = 0; dc < DB; ++dc) kb[(u + 2) % 3][dc] = attn_buffer_load4(krs, kofs + (ra * D + dc * 16) * 4);
@@ -611,7 +694,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 
   // the first key block's DMA is issued only now: LDS-DMA loads pending beside
   // ordinary loads make the compiler wait for every load in flight
-  attn_issue_tile<K, D>(tiles[0], Kp, Vp, head, S, 0, lane, wave);
+  attn_issue_tile<K, D>(tiles[0], Kp, Vp, head, S, lo, lane, wave);
 
   acc_t acc_o[K + 1][DB];
 #pragma unroll
@@ -633,7 +716,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
 
   for (int j = 0; j < nblocks; ++j) {
     const int buf = j & 1;
-    const int kb0 = j * kAttnBN;
+    const int kb0 = lo + j * kAttnBN;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
     const uint32_t mword = *reinterpret_cast<const uint32_t*>(mrow + mstep * kb0);   // used after the scores
@@ -705,7 +788,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
     // MFMA: with an LDS DMA in flight the compiler waits for every outstanding
     // LDS read before using any, and the rest of step t covers their latency.
     constexpr int PE = AttnPvE<D>::value, STEPS = DB / PE * 4, OPS = AttnDma<K, D>::OPS;
-    const int next_kb0 = min(kb0 + kAttnBN, (nblocks - 1) * kAttnBN);
+    const int next_kb0 = min(kb0 + kAttnBN, lo + (nblocks - 1) * kAttnBN);
     Vec<float, PE> vq[2][K + 1];
     attn_load_v_step<K, D>(vq[0], tiles[buf][1], 0, 0, c, h);
 #pragma unroll
@@ -766,15 +849,15 @@ static int launch_attention_kd(const AttnArgs& a) {
         pipe = pt_host::aligned16(a.q[i]) && pt_host::aligned16(a.k[i]) && pt_host::aligned16(a.v[i]);
       if (pipe) {
         taylor_attention_fwd_pipe_kernel<K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.causal ? 1 : 0,
-            static_cast<A>(a.scale));
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_ranges,
+            a.causal ? 1 : 0, static_cast<A>(a.scale));
         PT_LAUNCH_CHECK();
         return PT_OK;
       }
     }
     taylor_attention_fwd_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
         q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
-        static_cast<int>(a.lk), a.mask, a.causal ? 1 : 0, static_cast<A>(a.scale));
+        static_cast<int>(a.lk), a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale));
     PT_LAUNCH_CHECK();
     return PT_OK;
   }

@@ -6,10 +6,13 @@ extern "C" {
 int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_orders,
                             const void* const* k, int k_orders, const void* const* v, int v_orders,
                             void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
-                            int64_t d, int causal, const uint8_t* mask, double scale, void* stream) {
+                            int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
+                            void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention: degree must be in 0..8");
+  PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
+             "Taylor attention: mask_ranges without a mask");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
              "Taylor attention: float32 and float64 only");
   PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr, PT_INVALID_ARGUMENT,
@@ -35,8 +38,22 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
   }
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
-                 causal != 0, mask, scale, static_cast<hipStream_t>(stream)};
+                 causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream)};
   return dtype == PT_FLOAT32 ? pt::launch_attention<float>(a) : pt::launch_attention<double>(a);
+}
+
+int64_t pt_attention_mask_ranges_count(int64_t lq, int64_t lk) {
+  if (lq < 0 || lk < 0) return 0;
+  return pt::attention_mask_ranges_count(lq, lk);
+}
+
+int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, void* stream) {
+  pt_host::clear_error();
+  PT_REQUIRE(lq >= 0 && lk >= 0 && lq <= INT32_MAX && lk <= INT32_MAX, PT_INVALID_ARGUMENT,
+             "attention mask ranges: sizes out of range");
+  PT_REQUIRE((mask != nullptr || lq * lk == 0) && (ranges != nullptr || lq + lk == 0), PT_INVALID_ARGUMENT,
+             "attention mask ranges: mask and ranges are required");
+  return pt::launch_attention_mask_ranges(mask, lq, lk, ranges, static_cast<hipStream_t>(stream));
 }
 
 size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq) {
@@ -49,8 +66,10 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
                             const void* const* v, const void* const* out, const void* const* lse,
                             const void* const* grad, void* const* dq, void* const* dk, void* const* dv,
                             void* workspace, int64_t bh, int64_t lq, int64_t lk, int64_t d, int causal,
-                            const uint8_t* mask, double scale, void* stream) {
+                            const uint8_t* mask, const int32_t* mask_ranges, double scale, void* stream) {
   pt_host::clear_error();
+  PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
+             "Taylor attention backward: mask_ranges without a mask");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention backward: degree must be in 0..8");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
@@ -90,7 +109,7 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   }
   if (bh == 0) return PT_OK;
   pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
-                    causal != 0, mask, scale, static_cast<hipStream_t>(stream)};
+                    causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream)};
   return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
 }
 

@@ -175,7 +175,7 @@ template <typename T, int K, int D, int NS>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, int L, int S, const uint8_t* __restrict__ mask,
-    int causal, typename AccOf<T>::type scale) {
+    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -217,8 +217,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 #pragma unroll
     for (int n = 0; n < NS; ++n) acc[o][n] = MF::zero();
 
-  const int hi = causal ? min(S, q_block + kAttnBM) : S;
-  for (int kb0 = 0; kb0 < hi; kb0 += kAttnBN) {
+  int lo, hi;
+  attn_key_range(S, q_block, causal, ranges, lo, hi);
+  for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
     __syncthreads();
     {
       constexpr int VPR = D / V;
@@ -316,7 +317,8 @@ template <typename T, int K, int D, int NS, int WHAT>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
-    const uint8_t* __restrict__ mask, int causal, typename AccOf<T>::type scale) {
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
+    typename AccOf<T>::type scale) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -327,6 +329,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   constexpr int QV = 4;
   constexpr int kBM = 16;                       // queries per block
   constexpr int kBK = kAttnWaves * 16;          // keys per workgroup
+  static_assert(kBK == kAttnRangeBlock, "key blocks are the mask-range blocks");
   constexpr bool DO_V = (WHAT & 1) != 0;
   constexpr bool DO_K = (WHAT & 2) != 0;
 
@@ -360,8 +363,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
     for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) acc_k[o][n] = MF::zero();
   }
 
-  const int lo = causal ? kv_block : 0;
-  for (int qb0 = lo; qb0 < L; qb0 += kBM) {
+  // query range: causal (queries from the block's first key on) and mask-range bounds
+  int lo = causal ? kv_block : 0, hi = L;
+  if (ranges != nullptr) {
+    const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
+    const int kb = nqb + kv_block / kAttnRangeBlock;
+    lo = max(lo, static_cast<int>(ranges[2 * kb]) / kBM * kBM);
+    hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
+  }
+  for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
     __syncthreads();
     {
       constexpr int VPR = D / V;
@@ -528,7 +538,7 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
       constexpr int SL = Plan::DB / Plan::NS_Q;
       const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
       taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-          q, k, v, g, lse, delta_in, dq, L, S, a.mask, causal, scale);
+          q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_ranges, causal, scale);
       PT_LAUNCH_CHECK();
     }
     if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
@@ -537,17 +547,17 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
       const dim3 block(kAttnWaves * kWave);
       if constexpr (Plan::kv_fused) {
         taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 3><<<grid, block, 0, a.stream>>>(
-            q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+            q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
         PT_LAUNCH_CHECK();
       } else {
         if (a.dv != nullptr) {
           taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 1><<<grid, block, 0, a.stream>>>(
-              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
           PT_LAUNCH_CHECK();
         }
         if (a.dk != nullptr) {
           taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 2><<<grid, block, 0, a.stream>>>(
-              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, causal, scale);
+              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
           PT_LAUNCH_CHECK();
         }
       }

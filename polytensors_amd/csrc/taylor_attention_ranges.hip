@@ -1,0 +1,19 @@
+// Block ranges of boolean attention masks (launcher of attn_mask_ranges_kernel).
+#include "taylor_attention.inl"
+
+namespace pt {
+
+int64_t attention_mask_ranges_count(int64_t lq, int64_t lk) {
+  return 2 * ((lq + kAttnRangeBlock - 1) / kAttnRangeBlock + (lk + kAttnRangeBlock - 1) / kAttnRangeBlock);
+}
+
+int launch_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, hipStream_t stream) {
+  const int64_t blocks = attention_mask_ranges_count(lq, lk) / 2;
+  if (blocks == 0) return PT_OK;
+  attn_mask_ranges_kernel<><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream>>>(
+      mask, static_cast<int>(lq), static_cast<int>(lk), ranges);
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
+
+}  // namespace pt

@@ -220,3 +220,49 @@ def test_empty_key_length_gives_empty_rows():
             out, lse = _ops.taylor_attention_fwd(q, kv, kv, None, causal, 0.1, 4)
             assert torch.equal(out, torch.zeros_like(out))
             assert torch.isinf(lse[0]).all() and (lse[1:] == 0).all()
+
+
+def _ranges_reference(mask, block=64):
+    # per query block / key block, first and one-past-last admissible index (0, 0 if none), the
+    # definition of /root/reference/src/polytensors/_fused_attention.py:81-99 at block 64
+    L, S = mask.shape
+    out = []
+    for r0 in range(0, L, block):
+        cols = mask[r0:r0 + block].any(0).nonzero().flatten()
+        out += [int(cols[0]), int(cols[-1]) + 1] if len(cols) else [0, 0]
+    for c0 in range(0, S, block):
+        rows = mask[:, c0:c0 + block].any(1).nonzero().flatten()
+        out += [int(rows[0]), int(rows[-1]) + 1] if len(rows) else [0, 0]
+    return out
+
+
+@pytest.mark.parametrize("L,S", [(150, 150), (64, 200), (300, 37), (1, 1)])
+def test_mask_ranges_kernel(L, S):
+    g = torch.Generator().manual_seed(L + S)
+    mask = _window_mask(max(L, S), 23)[:L, :S] & (torch.rand(L, S, generator=g) > 0.3)
+    if L > 70:
+        mask[64:128] = False          # a query block with no admissible key
+    if S > 70:
+        mask[:, 64:128] = False       # a key block no query admits
+    got = _ops._mask_ranges(mask.cuda(), L, S)
+    assert got.cpu().tolist()[:len(_ranges_reference(mask))] == _ranges_reference(mask)
+
+
+# Sliding windows much narrower than the sequence: the kernels skip the key blocks outside each
+# query block's range (and, in the pipelined kernel, keep one fully masked block for a query block
+# with no admissible key).
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sliding_window_skips_blocks(dtype):
+    L, d, degree = 704, 64, 2
+    mask = _window_mask(L, 60)
+    mask[256:320] = False
+    Q, K, V = (_series((1, 2, L, d), degree, 90 + i, dtype) for i in range(3))
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=mask.cuda())
+    want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                            attn_mask=mask)
+    for k, (a, b) in enumerate(zip(out.coeffs, want)):
+        a = a.cpu()
+        assert torch.equal(a[..., 256:320, :], torch.zeros_like(a[..., 256:320, :]))
+        keep = torch.ones(L, dtype=torch.bool)
+        keep[256:320] = False
+        assert rel_err(a[..., keep, :], b[..., keep, :]) <= TOL[dtype], k

@@ -203,3 +203,15 @@ def test_full_size_config3_backward():
         for o in range(degree + 1):
             err = rel_err((a[o] + b[o]).cpu(), ab[o].cpu())
             assert err <= TOL[torch.float32], f"{name} order {o}: linearity {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sliding_window_skips_blocks(dtype):
+    # narrow window: whole key blocks (dQ) and query blocks (dK, dV) lie outside the mask ranges,
+    # plus a query block with no admissible key and a key block that no query admits
+    L, d, degree = 640, 32, 2
+    mask = _window_mask(L, L, 50)
+    mask[192:256] = False
+    mask[:, 448:512] = False
+    Q, K, V, G = (_series((2, L, d), degree, 160 + i) for i in range(4))
+    _compare(Q, K, V, G, dtype, mask=mask)
