@@ -15,7 +15,7 @@ a query row with no admissible key gets output zero.
 
 Under autograd (a PolyTensor operand requiring grad) the call records
 ``_SeriesAttention``, whose backward is the degree-K gradient series kernel
-(the reference's _SeriesAttention, _fused_attention.py:259-295, at any degree).
+(the reference's _SeriesAttention, _fused_attention.py:267-295, at any degree).
 """
 
 import contextvars
@@ -116,7 +116,7 @@ def _full(x, degree, shape):
 class _SeriesAttention(torch.autograd.Function):
     """Degree-K attention with its gradient series.
 
-    As /root/reference/src/polytensors/_fused_attention.py:259-295 (_SeriesAttention):
+    As /root/reference/src/polytensors/_fused_attention.py:267-295 (_SeriesAttention):
     the forward kernel saves the log-sum-exp series, and the backward computes
     the gradient series of query, key and value (coefficient j = sum_{k<=j}
     J_{j-k}^T G_k) with the degree-K backward kernels. Ordinary operands get no

@@ -2,7 +2,7 @@
 
 The backward kernels compute, for an output cotangent series G(t), the series
 of the vector-Jacobian product J(x(t))^T G(t) for query, key and value
-(/root/reference/src/polytensors/_fused_attention.py:259-295 at degree 1,
+(/root/reference/src/polytensors/_fused_attention.py:267-295 at degree 1,
 /root/reference/tests/test_fused_kernels.py:136-160 for its gradient check).
 The oracle is ``oracle.attention_backward`` (pinned against jets of
 torch.func.vjp in tests/test_oracle_pins.py) in float64 on the same (upcast)
