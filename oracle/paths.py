@@ -181,7 +181,16 @@ def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
 
         Z = [softcap * t for t in activation([z / softcap for z in Z], "tanh")]
     _, log_softmax, _ = softmax_family(Z, 1)
-    return [F.nll_loss(lp, target, ignore_index=ignore_index, reduction=reduction) for lp in log_softmax]
+    return [_nll(lp, target, ignore_index, reduction) for lp in log_softmax]
+
+
+def _nll(lp, target, ignore_index, reduction):
+    """Native NLL of one order; a complex order is split into its real and imaginary parts (NLL is
+    linear), as /root/reference/src/polytensors/_dispatch.py:12-26,537-543."""
+    if lp.is_complex():
+        return torch.complex(F.nll_loss(lp.real, target, ignore_index=ignore_index, reduction=reduction),
+                             F.nll_loss(lp.imag, target, ignore_index=ignore_index, reduction=reduction))
+    return F.nll_loss(lp, target, ignore_index=ignore_index, reduction=reduction)
 
 
 def cross_entropy_backward(Z, target, C, ignore_index=-100, softcap=None):

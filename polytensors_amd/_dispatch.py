@@ -39,6 +39,8 @@ _COPY_OPS = {
     aten.clone.default, aten.detach.default, aten._to_copy.default, aten.contiguous.default,
     aten.index_select.default, aten.gather.default, aten.index.Tensor, aten.flip.default,
     aten.roll.default, aten.repeat.default,
+    # embedding of a series weight, per order (/root/reference/src/polytensors/_dispatch.py:530-532)
+    aten.embedding.default,
     # the (linear) backward operations of views and gathers, per coefficient
     aten.slice_backward.default, aten.select_backward.default, aten.diagonal_backward.default,
     aten.index_add.default, aten.scatter_add.default, aten.unfold_backward.default,

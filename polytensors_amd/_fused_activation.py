@@ -13,23 +13,23 @@ Half and bfloat16 compute in float32, float64 in float64.
 
 import torch
 
-from . import _gate, _ops
+from . import _complex, _gate, _ops
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 BACKWARD_KINDS = ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu")
 
 
-def why_ineligible(*operands):
+def why_ineligible(*operands, complex_ok=False):
     from ._tensor import PolyTensor
 
     # Reached from __torch_dispatch__ only: autograd above has recorded the native
     # backward operation (gelu_backward, tanh_backward, ...), which routes here too.
-    reason = _gate.common_reason(operands, below_autograd=True)
+    reason = _gate.common_reason(operands, below_autograd=True, complex_ok=complex_ok)
     if reason is not None:
         return reason
     polys = [x for x in operands if isinstance(x, PolyTensor)]
     dtype = polys[0].dtype
-    if dtype not in _DTYPES or any(c.dtype != dtype for p in polys for c in p.coeffs):
+    if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for p in polys for c in p.coeffs):
         return "activation series need float16/bfloat16/float32/float64 in every order"
     if any(not isinstance(x, PolyTensor) and (x.dtype != dtype) for x in operands if isinstance(x, torch.Tensor)):
         return "an ordinary operand must have the series' dtype"
@@ -52,9 +52,11 @@ def activation(x, kind):
     """Series of ``f(x)`` for ``kind`` in gelu, gelu_tanh, tanh, sigmoid, silu, exp, log."""
     from ._tensor import PolyTensor
 
-    reason = why_ineligible(x)
+    reason = why_ineligible(x, complex_ok=True)
     if reason is not None:
         raise NotImplementedError(f"{kind}: {reason}")
+    if _complex.has_complex(x):
+        return _complex.at_real_nodes(activation, kind, x, kind)
     out = _ops.activation_series(_coeffs(x, x.degree), kind)
     return PolyTensor.from_stacked(out)
 

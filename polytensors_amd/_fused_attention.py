@@ -23,7 +23,7 @@ import math
 
 import torch
 
-from . import _gate, _ops
+from . import _complex, _gate, _ops
 
 _enabled = contextvars.ContextVar("polytensors_amd_fused_attention", default=True)
 _HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128)}
@@ -64,7 +64,7 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if isinstance(attn_mask, PolyTensor):
         return "the mask must be an ordinary tensor"
     grads = _needs_grad(*tensors)
-    reason = _gate.common_reason(tensors, allow_plain_grad=grads)
+    reason = _gate.common_reason(tensors, allow_plain_grad=grads, complex_ok=True)
     if reason is not None:
         return reason
     if grads and any(not isinstance(x, PolyTensor) and x.requires_grad for x in tensors):
@@ -73,7 +73,7 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
         return "an ordinary (non-PolyTensor) operand requires grad"
     dtype = query.dtype
     coeffs = [c for x in tensors for c in _gate.coefficients(x, 0)]
-    if any(c.dtype != dtype for c in coeffs):
+    if any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "query, key and value coefficients must share one dtype"
     if dtype not in _HEAD_DIMS:
         return f"dtype {dtype} is not supported (float32 or float64)"
@@ -165,6 +165,9 @@ def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
     from ._tensor import PolyTensor
 
     require_eligible(query, key, value, attn_mask, 0.0, is_causal, False)
+    if _complex.has_complex(query, key, value):
+        return _complex.at_real_nodes(attention, "scaled_dot_product_attention", query, key, value,
+                                      attn_mask=attn_mask, is_causal=is_causal, scale=scale)
     degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
     L, S = query.shape[-2], key.shape[-2]
     mask = _square_mask(attn_mask, L, S)

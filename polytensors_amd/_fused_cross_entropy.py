@@ -15,7 +15,7 @@ import contextvars
 
 import torch
 
-from . import _gate, _lib, _ops
+from . import _complex, _gate, _lib, _ops
 
 _enabled = contextvars.ContextVar("polytensors_amd_fused_cross_entropy", default=True)
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
@@ -30,12 +30,12 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
                 "polytensors_amd has no general series rules")
     if not isinstance(input, PolyTensor):
         return "logits must be a PolyTensor"
-    reason = _gate.common_reason((input,), allow_plain_grad=allow_grad)
+    reason = _gate.common_reason((input,), allow_plain_grad=allow_grad, complex_ok=True)
     if reason is not None:
         return reason
     if input.ndim != 2:
         return "logits must be (N, C)"
-    if input.dtype not in _DTYPES or any(c.dtype != input.dtype for c in input.coeffs):
+    if input.dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != input.dtype for c in input.coeffs):
         return "logits must be float16/bfloat16/float32/float64 in every order"
     if isinstance(target, PolyTensor) or not isinstance(target, torch.Tensor) or target.dtype != torch.int64:
         return "targets must be an ordinary int64 tensor (class indices)"
@@ -118,6 +118,9 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     """
     from ._tensor import PolyTensor
 
+    if _complex.has_complex(input):
+        return _complex.at_real_nodes(fused, "cross_entropy", input, target, ignore_index=ignore_index,
+                                      reduction=reduction, softcap=softcap)
     if torch.is_grad_enabled() and input.requires_grad:
         losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
         if reduction == "none":

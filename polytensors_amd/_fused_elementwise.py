@@ -11,7 +11,7 @@ when their shapes differ). Reached from ``__torch_dispatch__``, under autograd.
 
 import torch
 
-from . import _gate, _ops
+from . import _complex, _gate, _ops
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
@@ -19,12 +19,12 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 def why_ineligible(a, b):
     from ._tensor import PolyTensor
 
-    reason = _gate.common_reason((a, b), below_autograd=True)
+    reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
     dtype = coeffs[0].dtype
-    if dtype not in _DTYPES or any(c.dtype != dtype for c in coeffs):
+    if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "series operands must share one float16/bfloat16/float32/float64 dtype"
     return None
 
@@ -36,6 +36,10 @@ def binary(a, b, op):
     reason = why_ineligible(a, b)
     if reason is not None:
         raise NotImplementedError(f"series {op}: {reason}")
+    if _complex.has_complex(a, b):
+        if op == "mul":
+            return _complex.bilinear(binary, "series mul", a, b, op)
+        return _complex.at_real_nodes(binary, "series div", a, b, op)
     degree = next(x.degree for x in (a, b) if isinstance(x, PolyTensor))
     shape = torch.broadcast_shapes(a.shape, b.shape)
 

@@ -11,18 +11,18 @@ Batch dimensions broadcast as in torch.matmul; float32 and float64.
 
 import torch
 
-from . import _gate, _ops
+from . import _complex, _gate, _ops
 
 _DTYPES = (torch.float32, torch.float64)
 
 
 def why_ineligible(a, b, below_autograd=False):
-    reason = _gate.common_reason((a, b), below_autograd=below_autograd)
+    reason = _gate.common_reason((a, b), below_autograd=below_autograd, complex_ok=True)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
     dtype = coeffs[0].dtype
-    if dtype not in _DTYPES or any(c.dtype != dtype for c in coeffs):
+    if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "operands must share one dtype, float32 or float64"
     if a.ndim == 0 or b.ndim == 0:
         return "matmul of a 0-d tensor"
@@ -46,6 +46,8 @@ def matmul(a, b, below_autograd=False):
     reason = why_ineligible(a, b, below_autograd)
     if reason is not None:
         raise NotImplementedError(f"matmul: {reason}")
+    if _complex.has_complex(a, b):
+        return _complex.bilinear(matmul, "matmul", a, b, below_autograd=below_autograd)
     degree = _degree(a, b)
     A = list(_gate.coefficients(a, degree))
     B = list(_gate.coefficients(b, degree))
@@ -83,6 +85,9 @@ def linear(x, weight, bias=None):
     reason = why_ineligible(x, weight)
     if reason is not None:
         raise NotImplementedError(f"linear: {reason}")
+    if _complex.has_complex(x, weight):
+        result = _complex.bilinear(linear, "linear", x, weight)
+        return result if bias is None else result + bias
     degree = _degree(x, weight, *([bias] if isinstance(bias, PolyTensor) else []))
     X = list(_gate.coefficients(x, degree))
     W = list(_gate.coefficients(weight, degree))

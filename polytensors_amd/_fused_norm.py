@@ -17,7 +17,7 @@ import math
 
 import torch
 
-from . import _gate, _ops
+from . import _complex, _gate, _ops
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
@@ -25,13 +25,13 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 def why_ineligible(input, normalized_shape, weight=None, bias=None, allow_grad=False):
     from ._tensor import PolyTensor
 
-    reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad)
+    reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad, complex_ok=True)
     if reason is not None:
         return reason
     if not isinstance(input, torch.Tensor) or input.dtype not in _DTYPES:
         return "input must be a float16/bfloat16/float32/float64 tensor"
     polys = [x for x in (input, weight, bias) if isinstance(x, PolyTensor)]
-    if any(c.dtype != input.dtype for p in polys for c in p.coeffs):
+    if any(_gate.real_dtype(c.dtype) != input.dtype for p in polys for c in p.coeffs):
         return "all series coefficients must have the input's dtype"
     shape = tuple(normalized_shape)
     if not shape or tuple(input.shape[-len(shape):]) != shape:
@@ -117,6 +117,9 @@ def _run(input, normalized_shape, weight, bias, eps, layer):
     reason = why_ineligible(input, shape, weight, bias, allow_grad=grads)
     if reason is not None:
         raise NotImplementedError(f"{'layer_norm' if layer else 'rms_norm'}: {reason}")
+    if _complex.has_complex(input, weight, bias):
+        return _complex.at_real_nodes(_run, "layer_norm" if layer else "rms_norm", input, normalized_shape,
+                                      weight, bias, eps, layer)
     if grads:
         if not isinstance(input, PolyTensor):
             raise NotImplementedError("reverse mode through the fused norm needs a PolyTensor input")

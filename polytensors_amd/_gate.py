@@ -14,6 +14,12 @@ from . import _lib
 from ._plain import plain_range_enabled
 
 MAX_DEGREE = 8
+_REAL_OF = {torch.complex32: torch.float16, torch.complex64: torch.float32, torch.complex128: torch.float64}
+
+
+def real_dtype(dtype):
+    """The real dtype of a (possibly complex) coefficient dtype."""
+    return _REAL_OF.get(dtype, dtype)
 
 
 def coefficients(x, degree):
@@ -25,12 +31,14 @@ def coefficients(x, degree):
     return (x,)
 
 
-def common_reason(values, *, allow_plain_grad=False, below_autograd=False):
+def common_reason(values, *, allow_plain_grad=False, below_autograd=False, complex_ok=False):
     """Shared conditions over the tensor operands of one fused call.
 
     ``below_autograd``: the call comes from ``__torch_dispatch__``, under the
     autograd layer, which has already recorded the operation's native backward;
     operands requiring grad are then fine (the backward operations have rules too).
+    ``complex_ok``: the entry point runs complex directions through its real kernel
+    (polytensors_amd._complex); a complex constant coefficient is still refused.
     """
     from ._tensor import PolyTensor, _coefficient_autograd_enabled
 
@@ -54,8 +62,11 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False):
         if grads and not allow_plain_grad:
             return "this fused operation has no series backward kernel; use torch.no_grad()"
     coeffs = [c for t in tensors for c in coefficients(t, degree)]
-    if any(c.is_complex() for c in coeffs):
-        return "complex directions are not implemented by the fused kernels"
+    if any(t.is_complex() for t in tensors if not isinstance(t, PolyTensor)) or any(
+            p.coeffs[0].is_complex() for p in polys):
+        return "a complex constant term (complex base) is not implemented; complex directions need a real base"
+    if not complex_ok and any(c.is_complex() for c in coeffs):
+        return "complex directions are not implemented for this operation"
     if any(c.device.type != "cuda" for c in coeffs):
         return "polytensors_amd runs on HIP (cuda) devices only"
     _lib.load()   # loud failure if the kernels are not built

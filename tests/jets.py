@@ -44,10 +44,43 @@ def taylor(f, series, degree, dtype=torch.float64):
     return out
 
 
+def taylor_complex(f, bases, reals, imags, degree, dtype=torch.float64):
+    """Coefficients 0..degree of f along x_j + t (u_j + i w_j), a complex direction over a real base.
+
+    By multilinearity (/root/reference/docs/notes.md:59-76) coefficient k is
+    sum_b C(k, b) i^b d_s^{k-b} d_t^b g(0, 0) / k! with g(s, t) = f(x + s u + t w), a
+    real function; its mixed partials are nested torch.func.jvp calls on s and t.
+    """
+    s0 = torch.zeros((), dtype=dtype)
+
+    def g(s, t):
+        return f(*(x + s * u + t * w for x, u, w in zip(bases, reals, imags)))
+
+    def mixed(a, b):
+        fn = g
+        for _ in range(a):
+            def fn(s, t, prev=fn):
+                return torch.func.jvp(lambda s_: prev(s_, t), (s,), (torch.ones_like(s),))[1]
+        for _ in range(b):
+            def fn(s, t, prev=fn):
+                return torch.func.jvp(lambda t_: prev(s, t_), (t,), (torch.ones_like(t),))[1]
+        return fn(s0, s0)
+
+    out = []
+    for k in range(degree + 1):
+        total = None
+        for b in range(k + 1):
+            term = mixed(k - b, b) * (math.comb(k, b) * (1j ** b))
+            total = term if total is None else total + term
+        out.append(total / math.factorial(k) if k else total.real)
+    return out
+
+
 def rel_err(got, want):
-    """max |got - want| / max |want| (the per-order tolerance metric)."""
-    got = got.to(torch.float64)
-    want = want.to(torch.float64)
+    """max |got - want| / max |want| (the per-order tolerance metric); complex values compare whole."""
+    dtype = torch.complex128 if (got.is_complex() or want.is_complex()) else torch.float64
+    got = got.to(dtype)
+    want = want.to(dtype)
     scale = want.abs().max().item()
     err = (got - want).abs().max().item()
     return err / scale if scale > 0 else err
@@ -55,6 +88,7 @@ def rel_err(got, want):
 
 def norm_rel_err(got, want):
     """||got - want|| / ||want|| (the reference's _relative, tests/test_fused_kernels.py:44-45)."""
-    got = got.to(torch.float64)
-    want = want.to(torch.float64)
+    dtype = torch.complex128 if (got.is_complex() or want.is_complex()) else torch.float64
+    got = got.to(dtype)
+    want = want.to(dtype)
     return ((got - want).norm() / want.norm()).item()

@@ -414,3 +414,83 @@ def test_planted_mistakes_are_caught(monkeypatch, target, mutant):
         except AssertionError:
             failures += 1
     assert failures >= 1, f"no pin caught the planted mistake in {target}"
+
+
+# --- complex directions over a real base (config 5) ------------------------------------------------
+
+def _complex_line(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(shape, generator=g, dtype=torch.float64) for _ in range(3))
+
+
+def _line_series(x, u, w, degree):
+    return [x, torch.complex(u, w)] + [torch.zeros(x.shape, dtype=torch.complex128) for _ in range(degree - 1)]
+
+
+def _check_complex(got, want, tol):
+    assert len(got) == len(want)
+    for k, (a, b) in enumerate(zip(got, want)):
+        err = (a - b).abs().max().item() / max(b.abs().max().item(), 1e-300)
+        assert err <= tol, (k, err)
+
+
+def _composite_layer_norm(z, shape, weight=None, bias=None, eps=1e-5):
+    # torch's native layer_norm has wrong higher-order forward-mode jets; the explicit composite
+    d = z - z.mean(-1, keepdim=True)
+    out = d * torch.rsqrt((d * d).mean(-1, keepdim=True) + eps)
+    return out * weight + bias if weight is not None else out
+
+
+def test_complex_direction_attention_norm_activation_ce():
+    # the oracle's recurrences in complex arithmetic vs mixed real partials (tests/jets.py)
+    from tests.jets import taylor_complex
+
+    degree = 3
+    q, k, v = (_complex_line((1, 2, 6, 4), 70 + i) for i in range(3))
+    got = oracle.attention(*(_line_series(*t, degree) for t in (q, k, v)), is_causal=True)
+    excluded = ~torch.ones(6, 6, dtype=torch.bool).tril()
+    want = taylor_complex(lambda a, b, c: _math_attention(a, b, c, excluded=excluded),
+                          [q[0], k[0], v[0]], [q[1], k[1], v[1]], [q[2], k[2], v[2]], degree)
+    _check_complex(got, want, 1e-12)
+
+    x, u, w = _complex_line((5, 16), 73)
+    weight, bias = torch.randn(16, dtype=torch.float64), torch.randn(16, dtype=torch.float64)
+    got = oracle.layer_norm(_line_series(x, u, w, degree), (16,), weight=[weight], bias=[bias])
+    want = taylor_complex(lambda z: _composite_layer_norm(z, (16,), weight, bias), [x], [u], [w], degree)
+    _check_complex(got, want, 1e-12)
+
+    got = oracle.activation(_line_series(x, u, w, degree), "gelu_tanh")
+    want = taylor_complex(lambda z: F.gelu(z, approximate="tanh"), [x], [u], [w], degree)
+    _check_complex(got, want, 1e-12)
+
+    y = torch.randint(0, 16, (5,), generator=torch.Generator().manual_seed(74))
+    y[1] = -100
+    got = oracle.cross_entropy(_line_series(x, u, w, degree), y)
+    want = taylor_complex(lambda z: F.cross_entropy(z, y), [x], [u], [w], degree)
+    _check_complex(got, want, 1e-12)
+
+
+def test_decoder_oracle_matches_complex_jets(monkeypatch):
+    # the config-5 network (tests/gpt_decoder.py) at toy size: the oracle composite with a complex
+    # embedding direction vs mixed real partials of the same network (math attention)
+    from tests import gpt_decoder
+    from tests.jets import taylor_complex
+
+    degree, d, heads, vocab, seq = 3, 16, 2, 11, 5
+    params = gpt_decoder.init_params(2, d, vocab, seq, seed=3, dtype=torch.float64)
+    params["blocks"][0]["ln1_w"] = params["blocks"][0]["ln1_w"] + 0.1   # non-trivial affine terms
+    g = torch.Generator().manual_seed(4)
+    tokens = torch.randint(0, vocab, (1, seq), generator=g)
+    targets = torch.randint(0, vocab, (1, seq), generator=g)
+    base = gpt_decoder.embed(params, tokens)
+    u, w = (torch.randn(base.shape, generator=g, dtype=torch.float64) for _ in range(2))
+
+    def math_sdpa(q, k, v, is_causal):
+        L = q.shape[-2]
+        return _math_attention(q, k, v, excluded=~torch.ones(L, L, dtype=torch.bool).tril())
+
+    monkeypatch.setattr(F, "layer_norm", _composite_layer_norm)
+    got = gpt_decoder.oracle_forward(params, _line_series(base, u, w, degree), targets, heads)
+    want = taylor_complex(lambda x: gpt_decoder.forward(params, x, targets, heads, attention=math_sdpa),
+                          [base], [u], [w], degree)
+    _check_complex(got, want, 1e-10)
