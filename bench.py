@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|attention_window|attention_bwd|matmul|norm|ce|activation|norm_bwd|ce_bwd]
+                    [--workload attention|attention_window|attention_bwd|matmul|norm|ce|activation|norm_bwd|ce_bwd|decoder]
                     [--no-cpu-baseline] [--no-components] [--component-seconds S]
                     [--copy-calibration]
 
@@ -138,6 +138,35 @@ def wl_attention_bwd(device):
                 cpu=lambda: cpu_attention_bwd(L, d, K))
 
 
+def wl_decoder(device):
+    """GPT-style decoder forward plus mean cross entropy in Taylor mode. 12 layers,
+    d_model 768, 12 heads, seq 1024, batch 8, vocab 32000, K=3; weights N(0, 0.02) (ordinary tensors:
+    zero higher coefficients); a complex64 direction N(0,1) + i N(0,1) on the token embeddings."""
+    import torch
+    from polytensors_amd import PolyTensor
+    from tests import gpt_decoder
+
+    layers, d, heads, vocab, batch, seq, K = 12, 768, 12, 32000, 8, 1024, 3
+    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=10, device=device)
+    g = _gen(11, device)
+    tokens = torch.randint(0, vocab, (batch, seq), generator=g, device=device)
+    targets = torch.randint(0, vocab, (batch, seq), generator=g, device=device)
+    base = gpt_decoder.embed(params, tokens)
+    direction = torch.complex(torch.randn(batch, seq, d, generator=g, device=device),
+                              torch.randn(batch, seq, d, generator=g, device=device))
+
+    def step():
+        with torch.no_grad(), PolyTensor.plain_range():
+            x = PolyTensor((base, direction), degree=K)
+            return gpt_decoder.forward(params, x, targets, heads)
+
+    return dict(step=step, work=batch * seq, unit="tokens/s", bound=None, peak=None, bytes=None,
+                kernel="gpt_decoder", dtype="fp32 (complex64 directions)",
+                workload=f"gpt_decoder_taylor layers={layers} d={d} heads={heads} seq={seq} batch={batch} "
+                         f"vocab={vocab} K={K} complex64 directions, forward + mean CE",
+                cpu=lambda: cpu_decoder(layers, d, heads, vocab, K))
+
+
 def wl_matmul(device):
     """A, B [5, 4096, 4096] fp32 (K=4), coefficient k scaled by 0.5^k."""
     import torch
@@ -263,7 +292,8 @@ def wl_ce_bwd(device):
 
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
-             "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window}
+             "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
+             "decoder": wl_decoder}
 
 
 # ---------------------------------------------------------------------------
@@ -331,6 +361,22 @@ def cpu_attention_bwd(L, d, K, heads=16):
     flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
+
+
+def cpu_decoder(layers, d, heads, vocab, K, seq=64):
+    import torch
+    from tests import gpt_decoder
+
+    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=10)
+    g = torch.Generator().manual_seed(11)
+    tokens = torch.randint(0, vocab, (1, seq), generator=g)
+    targets = torch.randint(0, vocab, (1, seq), generator=g)
+    base = gpt_decoder.embed(params, tokens)
+    direction = torch.complex(torch.randn(1, seq, d, generator=g), torch.randn(1, seq, d, generator=g))
+    X = [base, direction] + [torch.zeros(1, seq, d, dtype=torch.complex64) for _ in range(K - 1)]
+    t = _cpu_time(lambda: gpt_decoder.oracle_forward(params, X, targets, heads), reps=1)
+    return dict(value=seq / t, unit="tokens/s", seconds=t,
+                sample=f"one sequence of {seq} tokens (attention cost grows with seq), full width, K={K} complex64")
 
 
 def cpu_matmul(n, K):
@@ -446,7 +492,8 @@ def measure(name, device, steps, warmup, min_seconds=0.0):
         warmup = 1
     ms = time_steps(w["step"], steps, warmup)
     w["steps"] = steps
-    achieved = w["work"] / (ms * 1e-3) / (1e12 if w["unit"] == "TFLOP/s" else 1e9)
+    scale = {"TFLOP/s": 1e12, "GB/s": 1e9}.get(w["unit"], 1.0)
+    achieved = w["work"] / (ms * 1e-3) / scale
     w.update(ms=ms, achieved=achieved)
     return w
 
@@ -496,8 +543,8 @@ def main():
         "data": "synthetic (seeded torch.randn on device)",
         "config": {"workload": w["workload"], "parallelism": "none (1 GPU)"},
         "roofline": {"bound": w["bound"], "achieved": round(w["achieved"], 3), "peak": w["peak"],
-                     "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4),
-                     "traffic": profiled_traffic(w["kernel"])},
+                     "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4) if w["peak"] else None,
+                     "traffic": profiled_traffic(w["kernel"]) if w["peak"] else None},
     }
     cpu_samplers = {}
     if not args.no_components:
@@ -508,7 +555,8 @@ def main():
             c = measure(name, device, max(3, args.steps // 2), 2, min_seconds=args.component_seconds)
             comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "steps": c["steps"],
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
-                           "frac": round(c["achieved"] / c["peak"], 4), "traffic": profiled_traffic(c["kernel"])}
+                           "frac": round(c["achieved"] / c["peak"], 4) if c["peak"] else None,
+                           "traffic": profiled_traffic(c["kernel"]) if c["peak"] else None}
             cpu_samplers[name] = c["cpu"]
             del c
             torch.cuda.empty_cache()
