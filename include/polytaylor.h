@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 4
+#define PT_ABI_VERSION 5
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -267,6 +267,29 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
 /* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row
  * rowsum(G O) series in the arithmetic type). */
 size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq);
+
+/*
+ * Complex directions through the real kernels. A series with a real constant
+ * term and complex higher coefficients is run as real-direction variants and
+ * recombined (the result is the multilinear extension of the real derivatives,
+ *   /root/reference/docs/notes.md:59-76, and linear operations on complex
+ * coefficients split into real and imaginary parts as the reference's
+ *   /root/reference/src/polytensors/_dispatch.py:12-26 (_linear_complex_split)).
+ * pt_complex_to_real: src holds `orders` complex planes of `numel` values
+ *   (interleaved re, im); writes dst[v * orders + o] = alpha[v] Re(src[o]) +
+ *   beta[v] Im(src[o]) for v < variants (real nodes: (1, lam_v); a real /
+ *   imaginary split: (1, 0), (0, 1)).
+ * pt_real_to_complex: writes dst[o] = sum_v (wre[v] + i wim[v]) src[v * orders + o].
+ * orders <= 8, variants <= 9; PT_FLOAT32 (complex64) or PT_FLOAT64
+ * (complex128); alpha/beta/wre/wim are host arrays. 16-byte aligned planes take
+ * 16-byte accesses, others a scalar path.
+ */
+int pt_complex_to_real(int dtype, int orders, const void* const* src, int variants,
+                       const double* alpha, const double* beta, void* const* dst,
+                       int64_t numel, void* stream);
+int pt_real_to_complex(int dtype, int orders, int variants, const void* const* src,
+                       const double* wre, const double* wim, void* const* dst,
+                       int64_t numel, void* stream);
 
 /* Activation kinds of pt_activation_series_fwd / _bwd. */
 typedef enum pt_activation {

@@ -29,6 +29,8 @@ import functools
 
 import torch
 
+from . import _ops
+
 _NODE_RADIUS = {1: 1.0, 2: 1.5, 3: 1.5}
 
 
@@ -91,19 +93,26 @@ def _flatten(values):
     return out
 
 
-def _real_part(x, lam):
-    """The real-direction series Re c_j + lam Im c_j (orders >= 1); other values unchanged."""
+def _planes(x):
+    """The contiguous complex planes (orders 1..K) of a complex-direction series."""
+    return [c.contiguous() for c in x.coeffs[1:]]
+
+
+def _variants(x, alpha, beta):
+    """Real-direction series alpha_v Re + beta_v Im of x's higher orders (order 0 shared), one per v."""
     from ._tensor import PolyTensor
 
+    planes = _ops.complex_to_real(_planes(x), list(alpha), list(beta))
+    return [PolyTensor((x.coeffs[0],) + tuple(v.unbind(0))) for v in planes.unbind(0)]
+
+
+def _substitute(x, table):
+    """x with every complex-direction series replaced by its variant from ``table``."""
     if isinstance(x, (list, tuple)):
-        return type(x)(_real_part(v, lam) for v in x)
+        return type(x)(_substitute(v, table) for v in x)
     if isinstance(x, dict):
-        return {k: _real_part(v, lam) for k, v in x.items()}
-    if not _is_complex_series(x):
-        return x
-    head = x.coeffs[0]
-    return PolyTensor((head,) + tuple(torch.add(c.real, c.imag, alpha=lam) if c.is_complex() else c
-                                      for c in x.coeffs[1:]))
+        return {k: _substitute(v, table) for k, v in x.items()}
+    return table.get(id(x), x)
 
 
 def _combine(outputs, weights):
@@ -111,22 +120,19 @@ def _combine(outputs, weights):
     from ._tensor import PolyTensor
 
     first = outputs[0]
-    coeffs = [first.coeffs[0]]
-    for k in range(1, first.degree + 1):
-        re = im = None
-        for w, y in zip(weights, outputs):
-            c = y.coeffs[k]
-            re = c * w.real if re is None else re.add_(c, alpha=w.real)
-            im = c * w.imag if im is None else im.add_(c, alpha=w.imag)
-        coeffs.append(torch.complex(re, im))
-    return PolyTensor(tuple(coeffs))
+    orders = first.degree
+    if orders == 0:
+        return first
+    src = [y.coeffs[k].contiguous() for y in outputs for k in range(1, orders + 1)]
+    planes = _ops.real_to_complex(src, orders, [w.real for w in weights], [w.imag for w in weights])
+    return PolyTensor((first.coeffs[0],) + tuple(planes.unbind(0)))
 
 
 def at_real_nodes(fn, what, *args, **kwargs):
     """``fn(*args, **kwargs)`` for complex-direction series from K+1 runs on real directions.
 
-    ``fn`` returns one PolyTensor; its real runs are made one at a time (the
-    working set is one real variant of the operands).
+    ``fn`` returns one PolyTensor. The real variants of every complex-direction
+    operand are formed in one pass per operand (all nodes at once).
     """
     from ._tensor import PolyTensor
 
@@ -134,36 +140,49 @@ def at_real_nodes(fn, what, *args, **kwargs):
     _check(values, what)
     degree = next(v.degree for v in values if isinstance(v, PolyTensor))
     nodes, weights = nodes_and_weights(degree)
+    ones = [1.0] * len(nodes)
+    variants = {id(v): _variants(v, ones, nodes) for v in values if _is_complex_series(v)}
     outputs = []
-    for lam in nodes:
-        out = fn(*_real_part(list(args), lam), **_real_part(kwargs, lam))
+    for m in range(len(nodes)):
+        table = {key: vs[m] for key, vs in variants.items()}
+        out = fn(*_substitute(list(args), table), **_substitute(kwargs, table))
         if not isinstance(out, PolyTensor):
             raise TypeError(f"{what}: a series operation returned {type(out).__name__}")
         outputs.append(out)
+    del variants
     return _combine(outputs, weights)
 
 
-def _parts(x):
-    """(real part, imaginary part or None) of a series operand: A_R = [A_0, Re A_1, ...],
-    A_I = [0, Im A_1, ...]; ordinary tensors are real."""
-    from ._tensor import PolyTensor
-
-    if not _is_complex_series(x):
-        return x, None
-    head = x.coeffs[0]
-    real = PolyTensor((head,) + tuple(c.real.contiguous() if c.is_complex() else c for c in x.coeffs[1:]))
-    imag = PolyTensor((torch.zeros_like(head),) + tuple(c.imag.contiguous() if c.is_complex() else torch.zeros_like(c)
-                                                       for c in x.coeffs[1:]))
-    return real, imag
-
-
 def bilinear(fn, what, a, b, *rest, **kwargs):
-    """``fn(a, b, ...)`` for an operation bilinear in the series a, b (Cauchy products)."""
+    """``fn(a, b, ...)`` for an operation bilinear in the series a, b (Cauchy products).
+
+    With one complex-direction series and one ordinary tensor, the imaginary run
+    takes the imaginary planes as a series of degree K-1 (orders shifted down by
+    one: an ordinary operand does not mix orders), so it forms K products, not
+    K+1. Two series operands use the four real runs of the complex product.
+    """
     from ._tensor import PolyTensor
 
     _check([a, b], what)
-    ar, ai = _parts(a)
-    br, bi = _parts(b)
+    ac, bc = _is_complex_series(a), _is_complex_series(b)
+    if ac != bc and not isinstance(b if ac else a, PolyTensor):
+        x = a if ac else b
+        real, imag = _ops.complex_to_real(_planes(x), [1.0, 0.0], [0.0, 1.0]).unbind(0)
+        xr = PolyTensor((x.coeffs[0],) + tuple(real.unbind(0)))
+        xi = PolyTensor(tuple(imag.unbind(0)))
+        yr = fn(xr, b, *rest, **kwargs) if ac else fn(a, xr, *rest, **kwargs)
+        yi = fn(xi, b, *rest, **kwargs) if ac else fn(a, xi, *rest, **kwargs)
+        # orders 1..K of the result: real from yr's orders 1..K, imaginary from yi's orders 0..K-1
+        return _combine_parts(yr, list(yi.coeffs))
+    def parts(x):
+        if not _is_complex_series(x):
+            return x, None
+        r, i = _ops.complex_to_real(_planes(x), [1.0, 0.0], [0.0, 1.0]).unbind(0)
+        return (PolyTensor((x.coeffs[0],) + tuple(r.unbind(0))),
+                PolyTensor((torch.zeros_like(x.coeffs[0]),) + tuple(i.unbind(0))))
+
+    ar, ai = parts(a)
+    br, bi = parts(b)
     real = fn(ar, br, *rest, **kwargs)
     imag = None
     if ai is not None:
@@ -174,5 +193,16 @@ def bilinear(fn, what, a, b, *rest, **kwargs):
         if ai is not None:
             t = fn(ai, bi, *rest, **kwargs)
             real = PolyTensor(tuple(x - y for x, y in zip(real.coeffs, t.coeffs)))
-    coeffs = [real.coeffs[0]] + [torch.complex(r, i) for r, i in zip(real.coeffs[1:], imag.coeffs[1:])]
-    return PolyTensor(tuple(coeffs))
+    return _combine_parts(real, list(imag.coeffs[1:]))
+
+
+def _combine_parts(real, imag_orders):
+    """Series with order 0 of ``real`` and orders k >= 1 = real_k + i imag_orders[k-1]."""
+    from ._tensor import PolyTensor
+
+    orders = real.degree
+    if orders == 0:
+        return real
+    src = [c.contiguous() for c in real.coeffs[1:]] + [c.contiguous() for c in imag_orders[:orders]]
+    planes = _ops.real_to_complex(src, orders, [1.0, 0.0], [0.0, 1.0])
+    return PolyTensor((real.coeffs[0],) + tuple(planes.unbind(0)))

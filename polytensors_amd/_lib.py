@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -30,6 +30,7 @@ DTYPE_CODES = {
 
 _c_int, _c_i64, _c_dbl, _c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_double, ctypes.c_void_p
 _c_vpp = ctypes.POINTER(ctypes.c_void_p)
+_c_dblp = ctypes.POINTER(ctypes.c_double)
 
 # name -> (restype, argtypes); mirrors include/polytaylor.h.
 SIGNATURES = {
@@ -56,6 +57,8 @@ SIGNATURES = {
                                          _c_vpp, _c_vpp, _c_vpp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_int, _c_vp, _c_vp, _c_dbl, _c_vp]),
     "pt_taylor_attention_bwd_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_i64]),
+    "pt_complex_to_real": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
+    "pt_real_to_complex": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_bwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
     "pt_series_binary": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_i64, _c_vp]),
@@ -108,6 +111,11 @@ def available():
 
 def max_degree():
     return load().pt_max_degree()
+
+
+def double_array(values):
+    """A host array of doubles."""
+    return (ctypes.c_double * max(1, len(values)))(*values)
 
 
 def ptr_array(tensors):

@@ -291,6 +291,64 @@ def _(q, k, v, out, lse, grad, mask, causal, scale):
 
 
 # ---------------------------------------------------------------------------
+# Complex directions: real variants and their recombination
+
+_REAL_OF = {torch.complex64: torch.float32, torch.complex128: torch.float64}
+
+
+@torch.library.custom_op(f"{NAMESPACE}::complex_to_real", mutates_args=(), device_types="cuda")
+def complex_to_real(src: List[torch.Tensor], alpha: List[float], beta: List[float]) -> torch.Tensor:
+    """[len(alpha), len(src), *shape] real planes alpha[v] Re(src[o]) + beta[v] Im(src[o])."""
+    _require(len(src) >= 1 and len(alpha) == len(beta) >= 1, "complex_to_real: planes and variants required")
+    first = src[0]
+    _require(first.dtype in _REAL_OF, "complex_to_real: complex64 or complex128 planes")
+    for c in src:
+        _require(c.dtype == first.dtype and c.shape == first.shape and c.device == first.device and c.is_contiguous(),
+                 "complex_to_real: planes must share dtype, shape and device and be contiguous")
+    real = _REAL_OF[first.dtype]
+    out = torch.empty((len(alpha), len(src), *first.shape), dtype=real, device=first.device)
+    lib = _lib.load()
+    dst = [p for v in out.unbind(0) for p in v.unbind(0)]
+    status = lib.pt_complex_to_real(_lib.DTYPE_CODES[real], len(src), _lib.ptr_array(src), len(alpha),
+                                    _lib.double_array(alpha), _lib.double_array(beta), _lib.ptr_array(dst),
+                                    first.numel(), _lib.stream_of(first.device))
+    _lib.check(status, "complex_to_real")
+    return out
+
+
+@complex_to_real.register_fake
+def _(src, alpha, beta):
+    return src[0].new_empty((len(alpha), len(src), *src[0].shape), dtype=_REAL_OF[src[0].dtype])
+
+
+@torch.library.custom_op(f"{NAMESPACE}::real_to_complex", mutates_args=(), device_types="cuda")
+def real_to_complex(src: List[torch.Tensor], orders: int, wre: List[float], wim: List[float]) -> torch.Tensor:
+    """[orders, *shape] complex planes sum_v (wre[v] + i wim[v]) src[v * orders + o]."""
+    variants = len(wre)
+    _require(variants >= 1 and len(wim) == variants and len(src) == variants * orders and orders >= 1,
+             "real_to_complex: src must hold variants x orders planes")
+    first = src[0]
+    _require(first.dtype in (torch.float32, torch.float64), "real_to_complex: float32 or float64 planes")
+    for c in src:
+        _require(c.dtype == first.dtype and c.shape == first.shape and c.device == first.device and c.is_contiguous(),
+                 "real_to_complex: planes must share dtype, shape and device and be contiguous")
+    cplx = torch.complex64 if first.dtype == torch.float32 else torch.complex128
+    out = torch.empty((orders, *first.shape), dtype=cplx, device=first.device)
+    lib = _lib.load()
+    status = lib.pt_real_to_complex(_lib.DTYPE_CODES[first.dtype], orders, variants, _lib.ptr_array(src),
+                                    _lib.double_array(wre), _lib.double_array(wim),
+                                    _lib.ptr_array(list(out.unbind(0))), first.numel(), _lib.stream_of(first.device))
+    _lib.check(status, "real_to_complex")
+    return out
+
+
+@real_to_complex.register_fake
+def _(src, orders, wre, wim):
+    cplx = torch.complex64 if src[0].dtype == torch.float32 else torch.complex128
+    return src[0].new_empty((orders, *src[0].shape), dtype=cplx)
+
+
+# ---------------------------------------------------------------------------
 # Elementwise activation series
 
 @torch.library.custom_op(f"{NAMESPACE}::activation_series", mutates_args=(), device_types="cuda")

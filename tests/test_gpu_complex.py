@@ -63,6 +63,29 @@ def _check(got, want, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("numel", [1, 6, 4099])
+def test_plane_kernels_round_trip(dtype, numel):
+    # real variants at every node, recombined with the interpolation weights, give back the complex
+    # planes (the identity map is a polynomial of degree 1 in lam); a real/imaginary split likewise
+    from polytensors_amd import _complex, _ops
+
+    cdt = torch.complex64 if dtype == torch.float32 else torch.complex128
+    planes = [torch.randn(numel, dtype=cdt, device="cuda") for _ in range(3)]
+    nodes, weights = _complex.nodes_and_weights(3)
+    var = _ops.complex_to_real(planes, [1.0] * 4, list(nodes))
+    for v, lam in enumerate(nodes):
+        for o in range(3):
+            want = planes[o].real + lam * planes[o].imag
+            assert torch.allclose(var[v, o], want, rtol=1e-6 if dtype == torch.float32 else 1e-14, atol=1e-6)
+    back = _ops.real_to_complex([p for v in var.unbind(0) for p in v.unbind(0)], 3,
+                                [w.real for w in weights], [w.imag for w in weights])
+    for o in range(3):
+        assert (back[o] - planes[o]).abs().max() <= (1e-5 if dtype == torch.float32 else 1e-13)
+    split = _ops.complex_to_real(planes, [1.0, 0.0], [0.0, 1.0])
+    assert torch.equal(split[0, 1], planes[1].real) and torch.equal(split[1, 2], planes[2].imag)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("both", [False, True])
 def test_matmul_and_linear(dtype, both):
     degree = 3
