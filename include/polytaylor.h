@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 5
+#define PT_ABI_VERSION 6
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -246,6 +246,11 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk,
  * dq ([bh, lq, d]), dk, dv ([bh, lk, d]): K+1 pointers each, or NULL when that
  *   gradient is not wanted.
  * workspace: pt_taylor_attention_bwd_workspace_size(...) bytes of device memory.
+ * materialize: nonzero stores the P and dS series of every visited 16 x 16
+ *   tile in the workspace (2 (K+1) bh lq lk values): five series products per
+ *   admissible pair instead of eight (S and dP are then not recomputed for dK
+ *   and dV), at the cost of that workspace. PT_FLOAT32 only (PT_UNSUPPORTED
+ *   for PT_FLOAT64).
  * mask, mask_ranges: as in pt_taylor_attention_fwd.
  * Pointers must be 16-byte aligned. Deterministic (no atomics).
  * Replaces the degree-1 fused backward
@@ -259,14 +264,16 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
                             const void* const* out, const void* const* lse,
                             const void* const* grad, void* const* dq,
                             void* const* dk, void* const* dv, void* workspace,
-                            int64_t bh, int64_t lq, int64_t lk, int64_t d,
+                            int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
                             int causal, const uint8_t* mask,
                             const int32_t* mask_ranges, double scale,
                             void* stream);
 
 /* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row
- * rowsum(G O) series in the arithmetic type). */
-size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq);
+ * rowsum(G O) series in the arithmetic type, and with materialize the P and
+ * dS tiles). */
+size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq,
+                                              int64_t lk, int materialize);
 
 /*
  * Complex directions through the real kernels. A series with a real constant

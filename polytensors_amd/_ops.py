@@ -235,12 +235,16 @@ def _(q, k, v, mask, causal, scale, degree):
 @torch.library.custom_op(f"{NAMESPACE}::taylor_attention_bwd", mutates_args=(), device_types="cuda")
 def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[torch.Tensor], out: torch.Tensor,
                          lse: torch.Tensor, grad: List[torch.Tensor], mask: Optional[torch.Tensor], causal: bool,
-                         scale: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                         scale: float, materialize: int = -1) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradient series (dq, dk, dv) of ``taylor_attention_fwd`` for the cotangent series ``grad``.
 
     q, k, v and grad hold degree+1 coefficients each ([bh, L, d] and [bh, S, d]);
     ``out`` [degree+1, bh, L, d] and ``lse`` [degree+1, bh, L] are the forward's
     outputs. Returns three [degree+1, ...] tensors in the operands' dtype.
+    ``materialize``: 1 stores the P and dS tiles (5 series products per pair;
+    float32 only), 0 recomputes them (8 products, no L x S workspace), -1
+    chooses 1 for float32 when that workspace is at most a quarter of the
+    device's memory.
     """
     degree = len(q) - 1
     for name, s in (("q", q), ("k", k), ("v", v), ("grad", grad)):
@@ -271,13 +275,18 @@ def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
     ranges = _mask_ranges(mask, lq, lk)
     lib = _lib.load()
     code = _lib.DTYPE_CODES[dtype]
-    workspace = torch.empty(max(lib.pt_taylor_attention_bwd_workspace_size(code, degree, bh, lq), 1),
+    if materialize < 0:   # float32 only: the library refuses the stored-tile path for float64
+        size = lib.pt_taylor_attention_bwd_workspace_size(code, degree, bh, lq, lk, 1)
+        materialize = int(dtype == torch.float32 and
+                          size <= torch.cuda.get_device_properties(device).total_memory // 4)
+    workspace = torch.empty(max(lib.pt_taylor_attention_bwd_workspace_size(code, degree, bh, lq, lk,
+                                                                           int(materialize)), 1),
                             dtype=torch.uint8, device=device)
     status = lib.pt_taylor_attention_bwd(
         code, degree, _lib.ptr_array(q), _lib.ptr_array(k), _lib.ptr_array(v),
         _lib.ptr_array(list(out.unbind(0))), _lib.ptr_array(list(lse.unbind(0))), _lib.ptr_array(grad),
         _lib.ptr_array(list(dq.unbind(0))), _lib.ptr_array(list(dk.unbind(0))), _lib.ptr_array(list(dv.unbind(0))),
-        workspace.data_ptr(), bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(),
+        workspace.data_ptr(), int(materialize), bh, lq, lk, d, int(causal), None if mask is None else mask.data_ptr(),
         None if ranges is None else ranges.data_ptr(), float(scale),
         _lib.stream_of(device))
     _lib.check(status, "taylor_attention_bwd")
@@ -285,7 +294,7 @@ def taylor_attention_bwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
 
 
 @taylor_attention_bwd.register_fake
-def _(q, k, v, out, lse, grad, mask, causal, scale):
+def _(q, k, v, out, lse, grad, mask, causal, scale, materialize=-1):
     return (q[0].new_empty((len(q), *q[0].shape)), k[0].new_empty((len(k), *k[0].shape)),
             k[0].new_empty((len(k), *k[0].shape)))
 

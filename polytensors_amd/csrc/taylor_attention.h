@@ -49,10 +49,29 @@ struct AttnBwdArgs {
   const uint8_t* mask;
   const int32_t* mask_ranges;
   double scale;
+  bool materialize;   // store P and dS tiles in the workspace (5 products per pair instead of 8)
   hipStream_t stream;
 };
 
 template <typename T>
 int launch_attention_bwd(const AttnBwdArgs& a);
+
+// Workspace of the backward: the rowsum(G O) series ((K+1) bh lq accumulator
+// values), then, when materializing, the P and dS tiles of every order
+// ((K+1) x 2 buffers of bh x ceil(lq/16) x ceil(lk/16) tiles of 256 values).
+struct AttnBwdLayout {
+  size_t delta_bytes, tiles_offset, tile_bytes, total;
+};
+
+inline AttnBwdLayout attention_bwd_layout(size_t acc_size, size_t elem_size, int degree, int64_t bh, int64_t lq,
+                                          int64_t lk, bool materialize = true) {
+  AttnBwdLayout l{};
+  l.delta_bytes = static_cast<size_t>(degree + 1) * static_cast<size_t>(bh) * static_cast<size_t>(lq) * acc_size;
+  l.tiles_offset = (l.delta_bytes + 255) / 256 * 256;
+  const size_t tiles = static_cast<size_t>(bh) * static_cast<size_t>((lq + 15) / 16) * static_cast<size_t>((lk + 15) / 16);
+  l.tile_bytes = (tiles * 256 * elem_size + 255) / 256 * 256;
+  l.total = materialize ? l.tiles_offset + 2 * static_cast<size_t>(degree + 1) * l.tile_bytes : l.delta_bytes;
+  return l;
+}
 
 }  // namespace pt

@@ -44,6 +44,9 @@ struct Mfma16<float> {
   }
   // accumulator register r of lane l: row 4 (l/16) + r, column l % 16
   __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * h + r; }
+  // the lane group and register holding row i
+  __device__ __forceinline__ static int row_group(int i) { return i / 4; }
+  __device__ __forceinline__ static int row_reg(int i) { return i % 4; }
 };
 
 template <>
@@ -55,6 +58,8 @@ struct Mfma16<double> {
   }
   // accumulator register r of lane l: row 4 r + l/16, column l % 16
   __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * r + h; }
+  __device__ __forceinline__ static int row_group(int i) { return i % 4; }
+  __device__ __forceinline__ static int row_reg(int i) { return i / 4; }
 };
 
 constexpr int kAttnWaves = 4;

@@ -56,20 +56,26 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_
   return pt::launch_attention_mask_ranges(mask, lq, lk, ranges, static_cast<hipStream_t>(stream));
 }
 
-size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq) {
-  if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0) return 0;
-  const size_t acc = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);
-  return static_cast<size_t>(degree + 1) * static_cast<size_t>(bh) * static_cast<size_t>(lq) * acc;
+size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq, int64_t lk,
+                                              int materialize) {
+  if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0 || lk < 0) return 0;
+  const size_t size = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);   // accumulator = element type
+  return pt::attention_bwd_layout(size, size, degree, bh, lq, lk, materialize != 0).total;
 }
 
 int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const void* const* k,
                             const void* const* v, const void* const* out, const void* const* lse,
                             const void* const* grad, void* const* dq, void* const* dk, void* const* dv,
-                            void* workspace, int64_t bh, int64_t lq, int64_t lk, int64_t d, int causal,
-                            const uint8_t* mask, const int32_t* mask_ranges, double scale, void* stream) {
+                            void* workspace, int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
+                            int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
+                            void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention backward: mask_ranges without a mask");
+  // The stored-tile path is float32 only: a float64 run of it (degree 8, head dim 64) took a GPU
+  // memory fault whose cause is not established, so float64 always recomputes.
+  PT_REQUIRE(!(materialize && dtype == PT_FLOAT64), PT_UNSUPPORTED,
+             "Taylor attention backward: materialize is float32 only");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention backward: degree must be in 0..8");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
@@ -86,7 +92,7 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   PT_REQUIRE(lq <= INT32_MAX && lk <= INT32_MAX && (lq + 63) / 64 * bh <= (int64_t{1} << 24) &&
                  (lk + 63) / 64 * bh <= (int64_t{1} << 24),
              PT_UNSUPPORTED, "Taylor attention backward: sizes beyond the launch grid (blocks x heads > 2^24)");
-  PT_REQUIRE(bh * lq == 0 || workspace != nullptr, PT_INVALID_ARGUMENT,
+  PT_REQUIRE((bh * lq == 0 && !materialize) || workspace != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention backward: the workspace is required");
   PT_REQUIRE(pt_host::aligned16(workspace), PT_INVALID_ARGUMENT,
              "Taylor attention backward: workspace must be 16-byte aligned");
@@ -109,7 +115,7 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   }
   if (bh == 0) return PT_OK;
   pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
-                    causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream)};
+                    causal != 0, mask, mask_ranges, scale, materialize != 0, static_cast<hipStream_t>(stream)};
   return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
 }
 

@@ -53,6 +53,10 @@ struct AttnBwdPlan {
   static constexpr bool kv_fused = (K + 1) * DB * kAccRegs * 2 <= kBudget;   // dK and dV in one pass
   static constexpr int NS_KV = attn_bwd_chunks(K + 1, kAccRegs, kv_fused ? 2 : 1, DB, kBudget);
   static constexpr int NS_Q = attn_bwd_chunks(K + 1, kAccRegs, 1, DB, kBudget);
+  // the dK/dV kernel on stored P and dS tiles holds no score series: a larger budget
+  static constexpr int kMatBudget = 192;
+  static constexpr bool km_fused = (K + 1) * DB * kAccRegs * 2 <= kMatBudget;
+  static constexpr int NS_KM = attn_bwd_chunks(K + 1, kAccRegs, km_fused ? 2 : 1, DB, kMatBudget);
   static constexpr size_t kv_lds = AttnShape<T, K, D>::LDS + 2ull * (K + 1) * 16 * sizeof(A);
   static constexpr bool fits = AttnShape<T, K, D>::fits && kv_lds <= 160 * 1024;
 };
@@ -171,11 +175,70 @@ __device__ __forceinline__ void attn_bwd_store(const AccT (&acc)[K + 1][NS], MPt
   }
 }
 
-template <typename T, int K, int D, int NS>
+// Offset of element (query qi, key ki) of 16 x 16 tile (qt, kt) of one head in
+// the P / dS tile buffers: tiles are [head][query tile][key tile], and within a
+// tile the element sits where the consumer's (queries x keys) accumulator
+// layout holds it: lane (row_group(qi), ki), register row_reg(qi). A consumer
+// lane reads its four values with one load.
+template <typename MF>
+__device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt, int nqt, int nkt, int qi,
+                                                    int ki) {
+  const int64_t tile = (head * nqt + qt) * nkt + kt;
+  return tile * 256 + (MF::row_group(qi) * 16 + ki) * 4 + MF::row_reg(qi);
+}
+
+// The two head-dim contractions of one block, S (chunks 0..DB-1 of the global
+// operand) then dP (chunks DB..2DB-1), with the global operand read one chunk
+// ahead: chunk c+1 is loaded into the other half of the register ring while
+// chunk c's MFMAs run, and the last step loads chunk 0 again for the next
+// block. Chunks are taken in pairs so that the ring halves are static
+// registers. ring[0] holds chunk 0 on entry and on exit. PHASES = 1 runs the S
+// contraction only (chunks 0..DB-1).
+template <typename T, int K, int DB, int PHASES = 2, typename Load, typename StepS, typename StepP>
+__device__ __forceinline__ void attn_bwd_contract(Vec<T, 4> (&ring)[2][K + 1], Load& load, StepS& s_step,
+                                                  StepP& p_step) {
+  constexpr int NC = PHASES * DB;   // chunks per block
+  if constexpr (NC == 1) {
+    s_step(0, ring[0]);
+  } else if constexpr (DB == 1) {   // PHASES == 2: one chunk per phase
+    load(ring[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    s_step(0, ring[0]);
+    load(ring[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    p_step(0, ring[1]);
+  } else {
+#pragma unroll 1
+    for (int dc = 0; dc < DB; dc += 2) {
+      load(ring[1], dc + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      s_step(dc, ring[0]);
+      load(ring[0], (dc + 2) % NC);
+      __builtin_amdgcn_sched_barrier(0);
+      s_step(dc + 1, ring[1]);
+    }
+    if constexpr (PHASES == 2) {
+#pragma unroll 1
+      for (int dc = 0; dc < DB; dc += 2) {
+        load(ring[1], DB + dc + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        p_step(dc, ring[0]);
+        load(ring[0], (DB + dc + 2) % NC);
+        __builtin_amdgcn_sched_barrier(0);
+        p_step(dc + 1, ring[1]);
+      }
+    }
+  }
+}
+
+// STORE: also write the P and dS series of every visited 16 x 16 (query, key)
+// tile to PT / DST (attn_tile_offset layout) for taylor_attention_bwd_kv_mat_kernel.
+template <typename T, int K, int D, int NS, bool STORE>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
-    CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, int L, int S, const uint8_t* __restrict__ mask,
-    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+    CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, MPtrs<T> PT, MPtrs<T> DST, int L, int S,
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
+    typename AccOf<T>::type scale) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -217,6 +280,18 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 #pragma unroll
     for (int n = 0; n < NS; ++n) acc[o][n] = MF::zero();
 
+  // Global operand chunks c = 0 .. 2 DB - 1: Q[my row] for c < DB, then G[my row]; chunk c
+  // covers head dims 16 (c mod DB) + 4h .. +3 of every order.
+  auto load_glob = [&](Vec<T, QV>(&buf)[K + 1], int cg) {
+    const bool second = cg >= DB;
+    const int dc = second ? cg - DB : cg;
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+      buf[o] = *reinterpret_cast<const Vec<T, QV>*>((second ? G.p[o] : Q.p[o]) + qoff + dc * 16 + 4 * h);
+  };
+  Vec<T, QV> gq[2][K + 1];
+  load_glob(gq[0], 0);
+
   int lo, hi;
   attn_key_range(S, q_block, causal, ranges, lo, hi);
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
@@ -246,36 +321,29 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
     acc_t sc[K + 1], dp[K + 1];
 #pragma unroll
     for (int o = 0; o <= K; ++o) sc[o] = dp[o] = MF::zero();
-#pragma unroll 1
-    for (int dc = 0; dc < DB; ++dc) {
-      Vec<T, QV> qa[K + 1], kb[K + 1];
+    auto s_step = [&](int dc, const Vec<T, QV>(&qa)[K + 1]) {
+      Vec<T, QV> kb[K + 1];
 #pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(Q.p[o] + qoff + dc * 16 + 4 * h);
-        kb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Ks[o][c][dc * 16 + 4 * h]);
-      }
+      for (int o = 0; o <= K; ++o) kb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Ks[o][c][dc * 16 + 4 * h]);
 #pragma unroll
       for (int s = 0; s < QV; ++s)
 #pragma unroll
         for (int k = 0; k <= K; ++k)
 #pragma unroll
           for (int a = 0; a <= k; ++a) sc[k] = MF::mma(kb[k - a].v[s], qa[a].v[s], sc[k]);
-    }
-#pragma unroll 1
-    for (int dc = 0; dc < DB; ++dc) {
-      Vec<T, QV> ga[K + 1], vb[K + 1];
+    };
+    auto p_step = [&](int dc, const Vec<T, QV>(&ga)[K + 1]) {
+      Vec<T, QV> vb[K + 1];
 #pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        ga[o] = *reinterpret_cast<const Vec<T, QV>*>(G.p[o] + qoff + dc * 16 + 4 * h);
-        vb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Vs[o][c][dc * 16 + 4 * h]);
-      }
+      for (int o = 0; o <= K; ++o) vb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Vs[o][c][dc * 16 + 4 * h]);
 #pragma unroll
       for (int s = 0; s < QV; ++s)
 #pragma unroll
         for (int k = 0; k <= K; ++k)
 #pragma unroll
           for (int a = 0; a <= k; ++a) dp[k] = MF::mma(vb[k - a].v[s], ga[a].v[s], dp[k]);
-    }
+    };
+    attn_bwd_contract<T, K, DB>(gq, load_glob, s_step, p_step);
 
     // dS^T in place of the scores
 #pragma unroll
@@ -289,6 +357,19 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       attn_ds_series<A, K>(p, dp, r, delta, ds);
 #pragma unroll
       for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(ds[o]);
+      if constexpr (STORE) {
+        // (a wave whose 16 queries all lie past L owns no tile)
+        if (slice == 0 && q_block + wave * kAttnQPerWave < L) {
+          // element (query c, key acc_row(h, r)) of the wave's tile
+          const int64_t at = attn_tile_offset<MF>(head, q_block / 16 + wave, kb0 / 16, (L + 15) / 16,
+                                                  (S + 15) / 16, c, MF::acc_row(h, r));
+#pragma unroll
+          for (int o = 0; o <= K; ++o) {
+            PT.p[o][at] = static_cast<T>(p[o]);
+            DST.p[o][at] = static_cast<T>(ds[o]);
+          }
+        }
+      }
     }
 
     // dQ^T_k += sum_{a+b=k} K_b^T dS^T_a (head dim x queries)
@@ -309,7 +390,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
     }
   }
 
-  if (q_ok) attn_bwd_store<T, K, NS>(acc, DQ, (head * L + my_q) * D, slice * NS, h, scale);
+  if (q_ok && DQ.p[0] != nullptr) attn_bwd_store<T, K, NS>(acc, DQ, (head * L + my_q) * D, slice * NS, h, scale);
 }
 
 // WHAT: 1 = dV, 2 = dK, 3 = both.
@@ -363,6 +444,17 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
     for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) acc_k[o][n] = MF::zero();
   }
 
+  // Global operand chunks c: K[my key] for c < DB, then V[my key] (dK passes).
+  auto load_glob = [&](Vec<T, QV>(&buf)[K + 1], int cg) {
+    const bool second = cg >= DB;
+    const int dc = second ? cg - DB : cg;
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+      buf[o] = *reinterpret_cast<const Vec<T, QV>*>((second ? Vp.p[o] : Kp.p[o]) + koff + dc * 16 + 4 * h);
+  };
+  Vec<T, QV> gk[2][K + 1];
+  load_glob(gk[0], 0);
+
   // query range: causal (queries from the block's first key on) and mask-range bounds
   int lo = causal ? kv_block : 0, hi = L;
   if (ranges != nullptr) {
@@ -406,30 +498,22 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
     for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
 #pragma unroll
     for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) dp[o] = MF::zero();
-#pragma unroll 1
-    for (int dc = 0; dc < DB; ++dc) {
-      Vec<T, QV> qa[K + 1], kb[K + 1];
+    auto s_step = [&](int dc, const Vec<T, QV>(&kb)[K + 1]) {
+      Vec<T, QV> qa[K + 1];
 #pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(&Qs[o][c][dc * 16 + 4 * h]);
-        kb[o] = *reinterpret_cast<const Vec<T, QV>*>(Kp.p[o] + koff + dc * 16 + 4 * h);
-      }
+      for (int o = 0; o <= K; ++o) qa[o] = *reinterpret_cast<const Vec<T, QV>*>(&Qs[o][c][dc * 16 + 4 * h]);
 #pragma unroll
       for (int s = 0; s < QV; ++s)
 #pragma unroll
         for (int k = 0; k <= K; ++k)
 #pragma unroll
           for (int a = 0; a <= k; ++a) sc[k] = MF::mma(qa[a].v[s], kb[k - a].v[s], sc[k]);
-    }
-    if constexpr (DO_K) {
-#pragma unroll 1
-      for (int dc = 0; dc < DB; ++dc) {
-        Vec<T, QV> ga[K + 1], vb[K + 1];
+    };
+    auto p_step = [&](int dc, const Vec<T, QV>(&vb)[K + 1]) {
+      if constexpr (DO_K) {
+        Vec<T, QV> ga[K + 1];
 #pragma unroll
-        for (int o = 0; o <= K; ++o) {
-          ga[o] = *reinterpret_cast<const Vec<T, QV>*>(&Gs[o][c][dc * 16 + 4 * h]);
-          vb[o] = *reinterpret_cast<const Vec<T, QV>*>(Vp.p[o] + koff + dc * 16 + 4 * h);
-        }
+        for (int o = 0; o <= K; ++o) ga[o] = *reinterpret_cast<const Vec<T, QV>*>(&Gs[o][c][dc * 16 + 4 * h]);
 #pragma unroll
         for (int s = 0; s < QV; ++s)
 #pragma unroll
@@ -437,7 +521,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
 #pragma unroll
             for (int a = 0; a <= k; ++a) dp[k] = MF::mma(ga[a].v[s], vb[k - a].v[s], dp[k]);
       }
-    }
+    };
+    attn_bwd_contract<T, K, DB, DO_K ? 2 : 1>(gk, load_glob, s_step, p_step);
 
     // P in place of the scores (dV), dS in place of dP (dK)
 #pragma unroll
@@ -500,6 +585,142 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   if constexpr (DO_K) attn_bwd_store<T, K, NS>(acc_k, DK, row, slice * NS, h, scale);
 }
 
+// dK / dV from the P and dS tiles written by the dQ kernel: per 64-key
+// workgroup (16 keys per wave) and query block of 16, dV^T += G^T P and
+// dK^T += Q^T dS with G and Q staged in LDS and the tile series read straight
+// into the B-operand registers (masked by admissibility: tiles the dQ kernel
+// did not visit hold no admissible pair). Two products per pair instead of the
+// four of the recomputing kernel. WHAT: 1 = dV, 2 = dK, 3 = both.
+template <typename T, int K, int D, int NS, int WHAT>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_mat_kernel(
+    CPtrs<T> Q, CPtrs<T> G, CPtrs<T> PT, CPtrs<T> DST, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
+    typename AccOf<T>::type scale) {
+  using A = typename AccOf<T>::type;
+  using MF = Mfma16<T>;
+  using acc_t = typename MF::acc_t;
+  constexpr int LD = AttnShape<T, K, D>::LD;
+  constexpr int DB = D / 16;
+  constexpr int SLICES = DB / NS;
+  constexpr int V = 16 / sizeof(T);
+  constexpr int kBM = 16;
+  constexpr int kBK = kAttnWaves * 16;
+  static_assert(kBK == kAttnRangeBlock, "key blocks are the mask-range blocks");
+  constexpr bool DO_V = (WHAT & 1) != 0;
+  constexpr bool DO_K = (WHAT & 2) != 0;
+
+  __shared__ T Gs[DO_V ? K + 1 : 1][kBM][LD];
+  __shared__ T Qs[DO_K ? K + 1 : 1][kBM][LD];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;
+  const int h = lane / 16;
+  const int nkb = (S + kBK - 1) / kBK;
+  const int64_t bh = gridDim.x / (static_cast<int64_t>(nkb) * SLICES);
+  const int64_t t = blockIdx.x;
+  const int64_t head = t % bh;
+  const int slice = static_cast<int>((t / bh) % SLICES);
+  const int kv_block = static_cast<int>(t / (bh * SLICES)) * kBK;
+  const int my_k = kv_block + wave * 16 + c;
+  const bool k_ok = my_k < S;
+  const int nqt = (L + 15) / 16, nkt = (S + 15) / 16;
+  const int kt = min(kv_block / 16 + wave, nkt - 1);   // a wave past S reads a valid tile, all masked
+
+  acc_t acc_v[DO_V ? K + 1 : 1][NS], acc_k[DO_K ? K + 1 : 1][NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+#pragma unroll
+    for (int o = 0; o < (DO_V ? K + 1 : 1); ++o) acc_v[o][n] = MF::zero();
+#pragma unroll
+    for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) acc_k[o][n] = MF::zero();
+  }
+
+  int lo = causal ? kv_block : 0, hi = L;
+  if (ranges != nullptr) {
+    const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
+    const int kb = nqb + kv_block / kAttnRangeBlock;
+    lo = max(lo, static_cast<int>(ranges[2 * kb]) / kBM * kBM);
+    hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
+  }
+  for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
+    // this lane's four tile values of every order (loaded before the staging barrier)
+    const int64_t at = (((head * nqt + qb0 / 16) * nkt + kt) * 256) + lane * 4;
+    Vec<T, 4> pv[DO_V ? K + 1 : 1], sv[DO_K ? K + 1 : 1];
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) pv[o] = *reinterpret_cast<const Vec<T, 4>*>(PT.p[o] + at);
+      if constexpr (DO_K) sv[o] = *reinterpret_cast<const Vec<T, 4>*>(DST.p[o] + at);
+    }
+    __syncthreads();
+    {
+      constexpr int VPR = D / V;
+      for (int idx = threadIdx.x; idx < (K + 1) * kBM * VPR; idx += kAttnWaves * kWave) {
+        const int o = idx / (kBM * VPR);
+        const int rem = idx % (kBM * VPR);
+        const int r = rem / VPR, cv = (rem % VPR) * V;
+        const int q = qb0 + r;
+        Vec<T, V> gx, qx;
+        if (q < L) {
+          if constexpr (DO_V) gx = load_vec<T, V>(G.p[o] + (head * L + q) * D + cv);
+          if constexpr (DO_K) qx = load_vec<T, V>(Q.p[o] + (head * L + q) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) gx.v[e] = qx.v[e] = T(0);
+        }
+        if constexpr (DO_V) store_vec<T, V>(&Gs[o][r][cv], gx);
+        if constexpr (DO_K) store_vec<T, V>(&Qs[o][r][cv], qx);
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int sidx = 0; sidx < 4; ++sidx) {
+      const int q = qb0 + MF::acc_row(h, sidx);
+      bool ok = k_ok && q < L;
+      if (causal) ok = ok && my_k <= q;
+      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(q) * S + my_k] != 0;
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        if constexpr (DO_V) pv[o].v[sidx] = ok ? pv[o].v[sidx] : T(0);
+        if constexpr (DO_K) sv[o].v[sidx] = ok ? sv[o].v[sidx] : T(0);
+      }
+    }
+
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const int col = (slice * NS + n) * 16 + c;
+#pragma unroll
+      for (int sidx = 0; sidx < 4; ++sidx) {
+        const int qr = MF::acc_row(h, sidx);
+        if constexpr (DO_V) {
+          T gv[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) gv[o] = Gs[o][qr][col];
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc_v[k][n] = MF::mma(gv[k - a], pv[a].v[sidx], acc_v[k][n]);
+        }
+        if constexpr (DO_K) {
+          T qv[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) qv[o] = Qs[o][qr][col];
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc_k[k][n] = MF::mma(qv[k - a], sv[a].v[sidx], acc_k[k][n]);
+        }
+      }
+    }
+  }
+
+  if (!k_ok) return;
+  const int64_t row = (head * S + my_k) * D;
+  if constexpr (DO_V) attn_bwd_store<T, K, NS>(acc_v, DV, row, slice * NS, h, A(1));
+  if constexpr (DO_K) attn_bwd_store<T, K, NS>(acc_k, DK, row, slice * NS, h, scale);
+}
+
 template <typename T, int K, int D>
 static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
   using A = typename AccOf<T>::type;
@@ -529,36 +750,84 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
     const int L = static_cast<int>(a.lq), S = static_cast<int>(a.lk);
     const A scale = static_cast<A>(a.scale);
     const int causal = a.causal ? 1 : 0;
+    // the stored-tile path is built for float32 only (the C ABI refuses it for float64)
+    constexpr bool kCanStore = sizeof(T) == 4;
+    if (!kCanStore && a.materialize) {
+      pt_host::set_error("Taylor attention backward: materialize is float32 only");
+      return PT_UNSUPPORTED;
+    }
+    MPtrs<T> pt{}, dst{};
+    CPtrs<T> pt_in{}, dst_in{};
+    if (a.materialize) {
+      const AttnBwdLayout lay = attention_bwd_layout(sizeof(A), sizeof(T), K, a.bh, a.lq, a.lk);
+      for (int i = 0; i <= K; ++i) {
+        pt.p[i] = reinterpret_cast<T*>(static_cast<char*>(a.workspace) + lay.tiles_offset + i * lay.tile_bytes);
+        dst.p[i] = reinterpret_cast<T*>(static_cast<char*>(a.workspace) + lay.tiles_offset +
+                                        (K + 1 + i) * lay.tile_bytes);
+        pt_in.p[i] = pt.p[i];
+        dst_in.p[i] = dst.p[i];
+      }
+    }
     if (rows > 0) {
       attn_bwd_delta_kernel<T, K, D><<<dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0, a.stream>>>(
           g, o, delta, rows);
       PT_LAUNCH_CHECK();
     }
-    if (a.dq != nullptr && rows > 0) {
+    const bool need_q = a.dq != nullptr || a.materialize;
+    if (need_q && rows > 0) {
       constexpr int SL = Plan::DB / Plan::NS_Q;
       const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
-      taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-          q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_ranges, causal, scale);
+      if constexpr (kCanStore) {
+        if (a.materialize)   // (without a dq output the kernel still writes the P and dS tiles)
+          taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, true><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+              q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale);
+      }
+      if (!a.materialize)
+        taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, false><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+            q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale);
       PT_LAUNCH_CHECK();
     }
     if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
-      constexpr int SL = Plan::DB / Plan::NS_KV;
-      const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
       const dim3 block(kAttnWaves * kWave);
-      if constexpr (Plan::kv_fused) {
-        taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 3><<<grid, block, 0, a.stream>>>(
-            q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
-        PT_LAUNCH_CHECK();
-      } else {
-        if (a.dv != nullptr) {
-          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 1><<<grid, block, 0, a.stream>>>(
-              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+      if (a.materialize) {
+       if constexpr (kCanStore) {
+        constexpr int SL = Plan::DB / Plan::NS_KM;
+        const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+        if constexpr (Plan::km_fused) {
+          taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 3><<<grid, block, 0, a.stream>>>(
+              q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
           PT_LAUNCH_CHECK();
+        } else {
+          if (a.dv != nullptr) {
+            taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 1><<<grid, block, 0, a.stream>>>(
+                q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_LAUNCH_CHECK();
+          }
+          if (a.dk != nullptr) {
+            taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 2><<<grid, block, 0, a.stream>>>(
+                q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_LAUNCH_CHECK();
+          }
         }
-        if (a.dk != nullptr) {
-          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 2><<<grid, block, 0, a.stream>>>(
+       }
+      } else {
+        constexpr int SL = Plan::DB / Plan::NS_KV;
+        const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+        if constexpr (Plan::kv_fused) {
+          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 3><<<grid, block, 0, a.stream>>>(
               q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
           PT_LAUNCH_CHECK();
+        } else {
+          if (a.dv != nullptr) {
+            taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 1><<<grid, block, 0, a.stream>>>(
+                q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_LAUNCH_CHECK();
+          }
+          if (a.dk != nullptr) {
+            taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 2><<<grid, block, 0, a.stream>>>(
+                q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_LAUNCH_CHECK();
+          }
         }
       }
     }

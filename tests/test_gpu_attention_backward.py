@@ -48,14 +48,14 @@ def _check(got, want, dtype, what="", floor=0.0):
         assert err <= TOL[dtype], f"{what} order {k}: {err:.3e} > {TOL[dtype]:.0e}"
 
 
-def _kernel(Q, K, V, G, dtype, mask=None, causal=False, scale=None):
+def _kernel(Q, K, V, G, dtype, mask=None, causal=False, scale=None, materialize=-1):
     """Forward then backward kernels on [bh, T, d] series; returns (dq, dk, dv) as lists."""
     q, k, v, g = ([c.to(dtype).cuda().contiguous() for c in s] for s in (Q, K, V, G))
     degree = len(q) - 1
     scale = 1 / math.sqrt(q[0].shape[-1]) if scale is None else scale
     m = None if mask is None else mask.cuda()
     out, lse = _ops.taylor_attention_fwd(q, k, v, m, causal, scale, degree)
-    dq, dk, dv = _ops.taylor_attention_bwd(q, k, v, out, lse, g, m, causal, scale)
+    dq, dk, dv = _ops.taylor_attention_bwd(q, k, v, out, lse, g, m, causal, scale, materialize)
     return list(dq.unbind(0)), list(dk.unbind(0)), list(dv.unbind(0))
 
 
@@ -64,8 +64,15 @@ def _oracle(Q, K, V, G, dtype, **kwargs):
     return oracle.attention_backward(*up, **kwargs)
 
 
-def _compare(Q, K, V, G, dtype, mask=None, causal=False, scale=None):
-    got = _kernel(Q, K, V, G, dtype, mask=mask, causal=causal, scale=scale)
+# The stored-tile path (materialize=1) is float32 only: a float64 run of it (degree 8, head dim 64)
+# took a GPU memory fault whose cause is not established, and the library refuses it for float64.
+FP64_MATERIALIZE = "the stored-tile backward is float32 only (float64 fault, cause not established)"
+
+
+def _compare(Q, K, V, G, dtype, mask=None, causal=False, scale=None, materialize=-1):
+    if dtype == torch.float64 and materialize == 1:
+        pytest.skip(FP64_MATERIALIZE)
+    got = _kernel(Q, K, V, G, dtype, mask=mask, causal=causal, scale=scale, materialize=materialize)
     want = _oracle(Q, K, V, G, dtype, attn_mask=mask, is_causal=causal, scale=scale)
     # with a single admissible key per row the softmax is 1 and dQ is exactly zero: scale by the
     # (order-one) inputs instead
@@ -74,26 +81,29 @@ def _compare(Q, K, V, G, dtype, mask=None, causal=False, scale=None):
         _check(a, b, dtype, name, floor=floor)
 
 
+# materialize 1: P and dS tiles stored by the dQ kernel and read by the dK/dV kernel; 0: recomputed
+@pytest.mark.parametrize("materialize", [1, 0])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("causal,window", [(True, None), (False, 21), (False, None)])
 @pytest.mark.parametrize("degree", [0, 1, 2, 4])
-def test_matches_oracle(dtype, causal, window, degree):
+def test_matches_oracle(dtype, causal, window, degree, materialize):
     bh, L, d = 3, 150, 64
     Q, K, V, G = (_series((bh, L, d), degree, 100 + i) for i in range(4))
     mask = None if window is None else _window_mask(L, L, window)
-    _compare(Q, K, V, G, dtype, mask=mask, causal=causal)
+    _compare(Q, K, V, G, dtype, mask=mask, causal=causal, materialize=materialize)
 
 
 # Every degree and head dim, including the head-dim slices and separate dK/dV passes of the
 # high-degree launches (float64 with d=128 fits LDS up to degree 3).
+@pytest.mark.parametrize("materialize", [1, 0])
 @pytest.mark.parametrize("degree", [3, 5, 6, 7, 8])
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_every_degree_and_head_dim(dtype, d, degree):
+def test_every_degree_and_head_dim(dtype, d, degree, materialize):
     if dtype == torch.float64 and d == 128 and degree > 3:
         pytest.skip("float64 K/V tiles of d=128 exceed LDS above degree 3 (the forward's limit too)")
     Q, K, V, G = (_series((2, 83, d), degree, 110 + i) for i in range(4))
-    _compare(Q, K, V, G, dtype, causal=True)
+    _compare(Q, K, V, G, dtype, causal=True, materialize=materialize)
 
 
 @pytest.mark.parametrize("L,S", [(50, 96), (100, 32), (1, 64), (64, 1), (17, 130)])
@@ -103,7 +113,8 @@ def test_cross_lengths(dtype, L, S):
     Q, G = _series((2, L, 32), degree, 120), _series((2, L, 32), degree, 121)
     K, V = _series((2, S, 32), degree, 122), _series((2, S, 32), degree, 123)
     for causal in (False, True):
-        _compare(Q, K, V, G, dtype, causal=causal, scale=0.3)
+        for materialize in ((1, 0) if dtype == torch.float32 else (0,)):
+            _compare(Q, K, V, G, dtype, causal=causal, scale=0.3, materialize=materialize)
 
 
 def test_rows_and_columns_without_admissible_pairs():
@@ -116,26 +127,30 @@ def test_rows_and_columns_without_admissible_pairs():
     Q, G = _series((2, L, 16), degree, 130), _series((2, L, 16), degree, 131)
     K, V = _series((2, S, 16), degree, 132), _series((2, S, 16), degree, 133)
     for dtype in (torch.float32, torch.float64):
-        dq, dk, dv = _kernel(Q, K, V, G, dtype, mask=mask)
+        dq, dk, dv = _kernel(Q, K, V, G, dtype, mask=mask, materialize=int(dtype == torch.float32))
         for c in dq:
             assert torch.equal(c[:, [3, 40]].cpu(), torch.zeros_like(c[:, [3, 40]].cpu()))
         for c in dk + dv:
             assert torch.equal(c[:, 10:12].cpu(), torch.zeros_like(c[:, 10:12].cpu()))
-        _compare(Q, K, V, G, dtype, mask=mask)
+        if dtype == torch.float32:
+            _compare(Q, K, V, G, dtype, mask=mask, materialize=1)
+        _compare(Q, K, V, G, dtype, mask=mask, materialize=0)
 
 
 def test_empty_sequences():
-    for dtype in (torch.float32, torch.float64):
+    for dtype in (torch.float32, torch.float64):  # materialize=1 for float32 only (see FP64_MATERIALIZE)
         q = [torch.randn(2, 5, 32, dtype=dtype, device="cuda") for _ in range(3)]
         kv = [torch.empty(2, 0, 32, dtype=dtype, device="cuda") for _ in range(3)]
         out, lse = _ops.taylor_attention_fwd(q, kv, kv, None, False, 0.1, 2)
-        dq, dk, dv = _ops.taylor_attention_bwd(q, kv, kv, out, lse, q, None, False, 0.1)
-        assert torch.equal(dq, torch.zeros_like(dq)) and dk.numel() == 0 and dv.numel() == 0
+        for materialize in ((1, 0) if dtype == torch.float32 else (0,)):
+            dq, dk, dv = _ops.taylor_attention_bwd(q, kv, kv, out, lse, q, None, False, 0.1, materialize)
+            assert torch.equal(dq, torch.zeros_like(dq)) and dk.numel() == 0 and dv.numel() == 0
         # no queries: key and value gradients are zero
         qe = [torch.empty(2, 0, 32, dtype=dtype, device="cuda") for _ in range(3)]
         out, lse = _ops.taylor_attention_fwd(qe, q, q, None, False, 0.1, 2)
-        dq, dk, dv = _ops.taylor_attention_bwd(qe, q, q, out, lse, qe, None, False, 0.1)
-        assert dq.numel() == 0 and torch.equal(dk, torch.zeros_like(dk)) and torch.equal(dv, torch.zeros_like(dv))
+        for materialize in ((1, 0) if dtype == torch.float32 else (0,)):
+            dq, dk, dv = _ops.taylor_attention_bwd(qe, q, q, out, lse, qe, None, False, 0.1, materialize)
+            assert dq.numel() == 0 and torch.equal(dk, torch.zeros_like(dk)) and torch.equal(dv, torch.zeros_like(dv))
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -171,6 +186,13 @@ def test_autograd_with_an_ordinary_key():
     want = oracle.attention_backward(*flat, is_causal=True)
     _check([c.reshape(2, 40, 16) for c in dq.coeffs], want[0], torch.float64, "dq")
     _check([c.reshape(2, 40, 16) for c in dv.coeffs], want[2], torch.float64, "dv")
+
+
+def test_float64_materialize_is_refused():
+    q = [torch.randn(1, 16, 16, dtype=torch.float64, device="cuda") for _ in range(2)]
+    out, lse = _ops.taylor_attention_fwd(q, q, q, None, True, 0.25, 1)
+    with pytest.raises(Exception, match="float32 only"):
+        _ops.taylor_attention_bwd(q, q, q, out, lse, q, None, True, 0.25, 1)
 
 
 def test_full_size_config3_backward():
@@ -214,4 +236,6 @@ def test_sliding_window_skips_blocks(dtype):
     mask[192:256] = False
     mask[:, 448:512] = False
     Q, K, V, G = (_series((2, L, d), degree, 160 + i) for i in range(4))
-    _compare(Q, K, V, G, dtype, mask=mask)
+    if dtype == torch.float32:
+        _compare(Q, K, V, G, dtype, mask=mask, materialize=1)
+    _compare(Q, K, V, G, dtype, mask=mask, materialize=0)
