@@ -55,7 +55,8 @@ struct AttnBwdPlan {
   static constexpr int NS_Q = attn_bwd_chunks(K + 1, kAccRegs, 1, DB, kBudget);
   // the dK/dV kernel on stored P and dS tiles holds no score series: a larger budget
   static constexpr int kMatBudget = 192;
-  static constexpr bool km_fused = (K + 1) * DB * kAccRegs * 2 <= kMatBudget;
+  // fused dK and dV also hold both tile series twice (current and prefetched block)
+  static constexpr bool km_fused = (K + 1) * DB * kAccRegs * 2 + 4 * (K + 1) * kAccRegs <= kMatBudget;
   static constexpr int NS_KM = attn_bwd_chunks(K + 1, kAccRegs, km_fused ? 2 : 1, DB, kMatBudget);
   static constexpr size_t kv_lds = AttnShape<T, K, D>::LDS + 2ull * (K + 1) * 16 * sizeof(A);
   static constexpr bool fits = AttnShape<T, K, D>::fits && kv_lds <= 160 * 1024;
@@ -187,6 +188,48 @@ __device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt
   return tile * 256 + (MF::row_group(qi) * 16 + ki) * 4 + MF::row_reg(qi);
 }
 
+// Register-staged copy of ROWS rows (from row `first`, zero past `limit`) of the
+// K+1 orders of a [*, D] series into an LDS tile [K+1][ROWS][LD]: fetch issues
+// the global loads into registers (early, so they are in flight during the
+// previous block's MFMAs) and commit writes them to LDS after the barrier.
+template <typename T, int K, int D, int ROWS>
+struct RowStager {
+  static constexpr int V = 16 / sizeof(T);
+  static constexpr int VPR = D / V;   // 16-byte vectors per row
+  static constexpr int TOTAL = (K + 1) * ROWS * VPR;
+  static constexpr int THREADS = kAttnWaves * kWave;
+  static constexpr int ITERS = (TOTAL + THREADS - 1) / THREADS;
+  Vec<T, V> r[ITERS];
+
+  __device__ __forceinline__ void fetch(const CPtrs<T>& src, int64_t row_base, int first, int limit) {
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const int idx = threadIdx.x + THREADS * i;
+      if (TOTAL % THREADS == 0 || idx < TOTAL) {
+        const int o = idx / (ROWS * VPR), rem = idx % (ROWS * VPR);
+        const int row = first + rem / VPR, cv = (rem % VPR) * V;
+        if (row < limit) {
+          r[i] = load_vec<T, V>(src.p[o] + (row_base + row) * D + cv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) r[i].v[e] = T(0);
+        }
+      }
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void commit(T (&tile)[K + 1][ROWS][LD]) const {
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const int idx = threadIdx.x + THREADS * i;
+      if (TOTAL % THREADS == 0 || idx < TOTAL) {
+        const int o = idx / (ROWS * VPR), rem = idx % (ROWS * VPR);
+        store_vec<T, V>(&tile[o][rem / VPR][(rem % VPR) * V], r[i]);
+      }
+    }
+  }
+};
+
 // The two head-dim contractions of one block, S (chunks 0..DB-1 of the global
 // operand) then dP (chunks DB..2DB-1), with the global operand read one chunk
 // ahead: chunk c+1 is loaded into the other half of the register ring while
@@ -294,9 +337,22 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 
   int lo, hi;
   attn_key_range(S, q_block, causal, ranges, lo, hi);
+  // Key block kb0+16's K and V rows are fetched into registers while block kb0's
+  // MFMAs run, where the registers allow (otherwise staged when needed).
+  constexpr bool kPrefetchStage = (K + 1) * D * static_cast<int>(sizeof(T)) <= 640 * 4;
+  RowStager<T, K, D, kAttnBN> stage_k, stage_v;
+  if constexpr (kPrefetchStage) {
+    if (lo < hi) {
+      stage_k.fetch(Kp, head * S, lo, S);
+      stage_v.fetch(Vp, head * S, lo, S);
+    }
+  }
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
-    __syncthreads();
-    {
+    __syncthreads();   // the previous block's MFMAs are done with the tiles
+    if constexpr (kPrefetchStage) {
+      stage_k.commit(Ks);
+      stage_v.commit(Vs);
+    } else {
       constexpr int VPR = D / V;
       for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
         const int o = idx / (kAttnBN * VPR);
@@ -316,6 +372,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       }
     }
     __syncthreads();
+    if constexpr (kPrefetchStage) {
+      if (kb0 + kAttnBN < hi) {
+        stage_k.fetch(Kp, head * S, kb0 + kAttnBN, S);
+        stage_v.fetch(Vp, head * S, kb0 + kAttnBN, S);
+      }
+      __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of this block's MFMAs
+    }
 
     // S^T_k = sum_{a+b=k} K_b Q_a^T and dP^T_k = sum_{a+b=k} V_b G_a^T (keys x queries)
     acc_t sc[K + 1], dp[K + 1];
@@ -643,36 +706,34 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
     lo = max(lo, static_cast<int>(ranges[2 * kb]) / kBM * kBM);
     hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
   }
+  // Block qb0+16's rows and tile values are fetched into registers while block
+  // qb0's MFMAs run (register double buffering of the staging).
+  RowStager<T, K, D, kBM> stage_g, stage_q;
+  Vec<T, 4> pn[DO_V ? K + 1 : 1], sn[DO_K ? K + 1 : 1];   // next block's tile values
+  auto fetch = [&](int qb) {
+    const int64_t at = (((head * nqt + qb / 16) * nkt + kt) * 256) + lane * 4;
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) pn[o] = *reinterpret_cast<const Vec<T, 4>*>(PT.p[o] + at);
+      if constexpr (DO_K) sn[o] = *reinterpret_cast<const Vec<T, 4>*>(DST.p[o] + at);
+    }
+    if constexpr (DO_V) stage_g.fetch(G, head * L, qb, L);
+    if constexpr (DO_K) stage_q.fetch(Q, head * L, qb, L);
+  };
+  if (lo < hi) fetch(lo);
   for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
-    // this lane's four tile values of every order (loaded before the staging barrier)
-    const int64_t at = (((head * nqt + qb0 / 16) * nkt + kt) * 256) + lane * 4;
     Vec<T, 4> pv[DO_V ? K + 1 : 1], sv[DO_K ? K + 1 : 1];
 #pragma unroll
     for (int o = 0; o <= K; ++o) {
-      if constexpr (DO_V) pv[o] = *reinterpret_cast<const Vec<T, 4>*>(PT.p[o] + at);
-      if constexpr (DO_K) sv[o] = *reinterpret_cast<const Vec<T, 4>*>(DST.p[o] + at);
+      if constexpr (DO_V) pv[o] = pn[o];
+      if constexpr (DO_K) sv[o] = sn[o];
     }
+    __syncthreads();   // the previous block's MFMAs are done with the tiles
+    if constexpr (DO_V) stage_g.commit(Gs);
+    if constexpr (DO_K) stage_q.commit(Qs);
     __syncthreads();
-    {
-      constexpr int VPR = D / V;
-      for (int idx = threadIdx.x; idx < (K + 1) * kBM * VPR; idx += kAttnWaves * kWave) {
-        const int o = idx / (kBM * VPR);
-        const int rem = idx % (kBM * VPR);
-        const int r = rem / VPR, cv = (rem % VPR) * V;
-        const int q = qb0 + r;
-        Vec<T, V> gx, qx;
-        if (q < L) {
-          if constexpr (DO_V) gx = load_vec<T, V>(G.p[o] + (head * L + q) * D + cv);
-          if constexpr (DO_K) qx = load_vec<T, V>(Q.p[o] + (head * L + q) * D + cv);
-        } else {
-#pragma unroll
-          for (int e = 0; e < V; ++e) gx.v[e] = qx.v[e] = T(0);
-        }
-        if constexpr (DO_V) store_vec<T, V>(&Gs[o][r][cv], gx);
-        if constexpr (DO_K) store_vec<T, V>(&Qs[o][r][cv], qx);
-      }
-    }
-    __syncthreads();
+    if (qb0 + kBM < hi) fetch(qb0 + kBM);
+    __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of this block's MFMAs
 
 #pragma unroll
     for (int sidx = 0; sidx < 4; ++sidx) {
