@@ -230,6 +230,36 @@ struct RowStager {
   }
 };
 
+// acc[k][n] += sum_{a+b=k} tile[b][row(s)][col(n)] * bop(a, s) for the NS
+// head-dim chunks n and the 4 steps s of a 16x16x4 product (A operands from an
+// LDS tile [K+1][16][LD]: row acc_row(h, s), column 16 (chunk0 + n) + c; B
+// operands bop(a, s) from registers). Step t+1's LDS operands are read while
+// step t's MFMAs run.
+template <typename T, int K, int NS, int LD, typename AccT, typename BOp>
+__device__ __forceinline__ void attn_lds_products(AccT (&acc)[K + 1][NS], const T (&tile)[K + 1][16][LD],
+                                                  int chunk0, int c, int h, const BOp& bop) {
+  using MF = Mfma16<T>;
+  constexpr int STEPS = NS * 4;
+  T ring[2][K + 1];
+  auto load = [&](T (&dst)[K + 1], int t) {
+    const int row = MF::acc_row(h, t % 4), col = (chunk0 + t / 4) * 16 + c;
+#pragma unroll
+    for (int o = 0; o <= K; ++o) dst[o] = tile[o][row][col];
+  };
+  load(ring[0], 0);
+#pragma unroll
+  for (int t = 0; t < STEPS; ++t) {
+    if (t + 1 < STEPS) load(ring[(t + 1) & 1], t + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = t / 4, sidx = t % 4;
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+#pragma unroll
+      for (int a = 0; a <= k; ++a) acc[k][n] = MF::mma(ring[t & 1][k - a], bop(a, sidx), acc[k][n]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // The two head-dim contractions of one block, S (chunks 0..DB-1 of the global
 // operand) then dP (chunks DB..2DB-1), with the global operand read one chunk
 // ahead: chunk c+1 is loaded into the other half of the register ring while
@@ -436,21 +466,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
     }
 
     // dQ^T_k += sum_{a+b=k} K_b^T dS^T_a (head dim x queries)
-#pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      const int col = (slice * NS + n) * 16 + c;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int key_row = MF::acc_row(h, s);
-        T kv[K + 1];
-#pragma unroll
-        for (int o = 0; o <= K; ++o) kv[o] = Ks[o][key_row][col];
-#pragma unroll
-        for (int k = 0; k <= K; ++k)
-#pragma unroll
-          for (int a = 0; a <= k; ++a) acc[k][n] = MF::mma(kv[k - a], sc[a][s], acc[k][n]);
-      }
-    }
+    attn_lds_products<T, K, NS>(acc, Ks, slice * NS, c, h, [&](int a, int sidx) { return sc[a][sidx]; });
   }
 
   if (q_ok && DQ.p[0] != nullptr) attn_bwd_store<T, K, NS>(acc, DQ, (head * L + my_q) * D, slice * NS, h, scale);
@@ -748,32 +764,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
       }
     }
 
-#pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      const int col = (slice * NS + n) * 16 + c;
-#pragma unroll
-      for (int sidx = 0; sidx < 4; ++sidx) {
-        const int qr = MF::acc_row(h, sidx);
-        if constexpr (DO_V) {
-          T gv[K + 1];
-#pragma unroll
-          for (int o = 0; o <= K; ++o) gv[o] = Gs[o][qr][col];
-#pragma unroll
-          for (int k = 0; k <= K; ++k)
-#pragma unroll
-            for (int a = 0; a <= k; ++a) acc_v[k][n] = MF::mma(gv[k - a], pv[a].v[sidx], acc_v[k][n]);
-        }
-        if constexpr (DO_K) {
-          T qv[K + 1];
-#pragma unroll
-          for (int o = 0; o <= K; ++o) qv[o] = Qs[o][qr][col];
-#pragma unroll
-          for (int k = 0; k <= K; ++k)
-#pragma unroll
-            for (int a = 0; a <= k; ++a) acc_k[k][n] = MF::mma(qv[k - a], sv[a].v[sidx], acc_k[k][n]);
-        }
-      }
-    }
+    if constexpr (DO_V)
+      attn_lds_products<T, K, NS>(acc_v, Gs, slice * NS, c, h, [&](int a, int sidx) { return pv[a].v[sidx]; });
+    if constexpr (DO_K)
+      attn_lds_products<T, K, NS>(acc_k, Qs, slice * NS, c, h, [&](int a, int sidx) { return sv[a].v[sidx]; });
   }
 
   if (!k_ok) return;
