@@ -275,6 +275,17 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
   }
 }
 
+// The order-o pointer of a series for a per-lane o: selected among the kernel
+// arguments (scalar registers) instead of indexing the argument array, which
+// would load the pointer from memory and wait for it before the data load.
+template <int K, typename T>
+__device__ __forceinline__ const T* order_ptr(const CPtrs<T>& s, int o) {
+  const T* p = s.p[0];
+#pragma unroll
+  for (int i = 1; i <= K; ++i) p = (o == i) ? s.p[i] : p;
+  return p;
+}
+
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
@@ -344,13 +355,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
         const bool kin = key < S && o < k_orders;
         const bool vin = key < S && o < v_orders;
         if (kin) {
-          kx = load_vec<T, V>(Kp.p[o] + (head * S + key) * D + cv);
+          kx = load_vec<T, V>(order_ptr<K>(Kp, o) + (head * S + key) * D + cv);
         } else {
 #pragma unroll
           for (int e = 0; e < V; ++e) kx.v[e] = T(0);
         }
         if (vin) {
-          vx = load_vec<T, V>(Vp.p[o] + (head * S + key) * D + cv);
+          vx = load_vec<T, V>(order_ptr<K>(Vp, o) + (head * S + key) * D + cv);
         } else {
 #pragma unroll
           for (int e = 0; e < V; ++e) vx.v[e] = T(0);

@@ -195,36 +195,49 @@ __device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt
 template <typename T, int K, int D, int ROWS>
 struct RowStager {
   static constexpr int V = 16 / sizeof(T);
-  static constexpr int VPR = D / V;   // 16-byte vectors per row
-  static constexpr int TOTAL = (K + 1) * ROWS * VPR;
+  static constexpr int VPR = D / V;                // 16-byte vectors per row
+  static constexpr int PER_ORDER = ROWS * VPR;     // vectors per order
   static constexpr int THREADS = kAttnWaves * kWave;
-  static constexpr int ITERS = (TOTAL + THREADS - 1) / THREADS;
+  static constexpr int IPO = (PER_ORDER + THREADS - 1) / THREADS;   // per thread and order
+  static constexpr int ITERS = (K + 1) * IPO;
+  static_assert(ITERS <= 64, "validity bits");
   Vec<T, V> r[ITERS];
+  uint64_t valid = 0;   // bit i: vector i is real (in range and below the row limit)
 
+  // Every step handles one order for all lanes (its pointer is a scalar kernel
+  // argument), and every lane loads: rows past `limit` (>= 1) and lanes past the
+  // order's vectors load a valid duplicate and are dropped at commit. A load
+  // under a per-lane branch would be waited for at the branch's end.
   __device__ __forceinline__ void fetch(const CPtrs<T>& src, int64_t row_base, int first, int limit) {
+    valid = 0;
 #pragma unroll
-    for (int i = 0; i < ITERS; ++i) {
-      const int idx = threadIdx.x + THREADS * i;
-      if (TOTAL % THREADS == 0 || idx < TOTAL) {
-        const int o = idx / (ROWS * VPR), rem = idx % (ROWS * VPR);
-        const int row = first + rem / VPR, cv = (rem % VPR) * V;
-        if (row < limit) {
-          r[i] = load_vec<T, V>(src.p[o] + (row_base + row) * D + cv);
-        } else {
+    for (int o = 0; o <= K; ++o) {
 #pragma unroll
-          for (int e = 0; e < V; ++e) r[i].v[e] = T(0);
-        }
+      for (int j = 0; j < IPO; ++j) {
+        const int i = o * IPO + j;
+        const int idx = static_cast<int>(threadIdx.x) + THREADS * j;
+        const int e = min(idx, PER_ORDER - 1);
+        const int row = first + e / VPR, cv = (e % VPR) * V;
+        r[i] = load_vec<T, V>(src.p[o] + (row_base + min(row, limit - 1)) * D + cv);
+        valid |= static_cast<uint64_t>(row < limit) << i;
       }
     }
   }
   template <int LD>
   __device__ __forceinline__ void commit(T (&tile)[K + 1][ROWS][LD]) const {
 #pragma unroll
-    for (int i = 0; i < ITERS; ++i) {
-      const int idx = threadIdx.x + THREADS * i;
-      if (TOTAL % THREADS == 0 || idx < TOTAL) {
-        const int o = idx / (ROWS * VPR), rem = idx % (ROWS * VPR);
-        store_vec<T, V>(&tile[o][rem / VPR][(rem % VPR) * V], r[i]);
+    for (int o = 0; o <= K; ++o) {
+#pragma unroll
+      for (int j = 0; j < IPO; ++j) {
+        const int i = o * IPO + j;
+        const int idx = static_cast<int>(threadIdx.x) + THREADS * j;
+        if (PER_ORDER % THREADS == 0 || idx < PER_ORDER) {
+          Vec<T, V> w;
+          const bool ok = (valid >> i) & 1u;
+#pragma unroll
+          for (int e = 0; e < V; ++e) w.v[e] = ok ? r[i].v[e] : T(0);
+          store_vec<T, V>(&tile[o][idx / VPR][(idx % VPR) * V], w);
+        }
       }
     }
   }
@@ -369,7 +382,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   attn_key_range(S, q_block, causal, ranges, lo, hi);
   // Key block kb0+16's K and V rows are fetched into registers while block kb0's
   // MFMAs run, where the registers allow (otherwise staged when needed).
-  constexpr bool kPrefetchStage = (K + 1) * D * static_cast<int>(sizeof(T)) <= 640 * 4;
+  // (registers: accumulators + two staged row sets + operand ring + score series)
+  constexpr int kW = static_cast<int>(sizeof(A) / 4);
+  constexpr bool kPrefetchStage =
+      (K + 1) * NS * 4 * kW + 2 * RowStager<T, K, D, kAttnBN>::ITERS * 4 + 2 * (K + 1) * 4 * kW +
+          2 * (K + 1) * 4 * kW <= 330;
   RowStager<T, K, D, kAttnBN> stage_k, stage_v;
   if constexpr (kPrefetchStage) {
     if (lo < hi) {
@@ -391,8 +408,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
         const int key = kb0 + r;
         Vec<T, V> kx, vx;
         if (key < S) {
-          kx = load_vec<T, V>(Kp.p[o] + (head * S + key) * D + cv);
-          vx = load_vec<T, V>(Vp.p[o] + (head * S + key) * D + cv);
+          kx = load_vec<T, V>(order_ptr<K>(Kp, o) + (head * S + key) * D + cv);
+          vx = load_vec<T, V>(order_ptr<K>(Vp, o) + (head * S + key) * D + cv);
         } else {
 #pragma unroll
           for (int e = 0; e < V; ++e) kx.v[e] = vx.v[e] = T(0);
@@ -402,13 +419,6 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       }
     }
     __syncthreads();
-    if constexpr (kPrefetchStage) {
-      if (kb0 + kAttnBN < hi) {
-        stage_k.fetch(Kp, head * S, kb0 + kAttnBN, S);
-        stage_v.fetch(Vp, head * S, kb0 + kAttnBN, S);
-      }
-      __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of this block's MFMAs
-    }
 
     // S^T_k = sum_{a+b=k} K_b Q_a^T and dP^T_k = sum_{a+b=k} V_b G_a^T (keys x queries)
     acc_t sc[K + 1], dp[K + 1];
@@ -437,6 +447,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
           for (int a = 0; a <= k; ++a) dp[k] = MF::mma(vb[k - a].v[s], ga[a].v[s], dp[k]);
     };
     attn_bwd_contract<T, K, DB>(gq, load_glob, s_step, p_step);
+    // The next block's K/V rows are fetched after the contraction's global loads (memory
+    // waits complete in order), so they overlap the dS series and the dQ products.
+    if constexpr (kPrefetchStage) {
+      if (kb0 + kAttnBN < hi) {
+        stage_k.fetch(Kp, head * S, kb0 + kAttnBN, S);
+        stage_v.fetch(Vp, head * S, kb0 + kAttnBN, S);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // dS^T in place of the scores
 #pragma unroll
@@ -553,8 +572,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
         const int q = qb0 + r;
         Vec<T, V> qx, gx;
         if (q < L) {
-          qx = load_vec<T, V>(Q.p[o] + (head * L + q) * D + cv);
-          gx = load_vec<T, V>(G.p[o] + (head * L + q) * D + cv);
+          qx = load_vec<T, V>(order_ptr<K>(Q, o) + (head * L + q) * D + cv);
+          gx = load_vec<T, V>(order_ptr<K>(G, o) + (head * L + q) * D + cv);
         } else {
 #pragma unroll
           for (int e = 0; e < V; ++e) qx.v[e] = gx.v[e] = T(0);
