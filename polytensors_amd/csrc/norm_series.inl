@@ -137,20 +137,30 @@ __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
   const bool active = row < rows;
   const int64_t base = row * static_cast<int64_t>(n);
 
-  Vec<T, V> raw[CHUNKS][K + 1];
+  // Every load is issued unconditionally (lanes past the row or past rows read
+  // vector 0, which exists) and then masked: a load under a per-lane branch is
+  // waited for where the branch ends, which would serialize the loads. The
+  // weight and bias vectors are fetched with the input.
+  Vec<T, V> raw[CHUNKS][K + 1], wv[CHUNKS], bv[CHUNKS];
+  const T* wp = w != nullptr ? w : x.p[0];
+  const T* bp = b != nullptr ? b : x.p[0];
 #pragma unroll
   for (int ch = 0; ch < CHUNKS; ++ch) {
     const int col = (ch * tpr + tid) * V;
     const bool in = active && col < n;
+    const int64_t at = in ? base + col : 0;
 #pragma unroll
-    for (int k = 0; k <= K; ++k) {
-      if (in) {
-        raw[ch][k] = load_vec_nt<T, V>(x.p[k] + base + col);
-      } else {
+    for (int k = 0; k <= K; ++k) raw[ch][k] = load_vec_nt<T, V>(x.p[k] + at);
+    wv[ch] = load_vec<T, V>(wp + (in ? col : 0));
+    bv[ch] = load_vec<T, V>(bp + (in ? col : 0));
+  }
 #pragma unroll
-        for (int e = 0; e < V; ++e) raw[ch][k].v[e] = from_acc<T>(A(0));
-      }
-    }
+  for (int ch = 0; ch < CHUNKS; ++ch) {
+    const bool in = active && (ch * tpr + tid) * V < n;
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+#pragma unroll
+      for (int e = 0; e < V; ++e) raw[ch][k].v[e] = in ? raw[ch][k].v[e] : from_acc<T>(A(0));
   }
 
   // mean[k] stays zero for RMSNorm; padding elements are excluded below.
@@ -204,17 +214,12 @@ __global__ __launch_bounds__(1024) void norm_series_reg_kernel(
     const int col = (ch * tpr + tid) * V;
     if (col >= n) continue;
     A wf[V], bf[V];
-    if (w != nullptr) {
-      unpack_vec(load_vec<T, V>(w + col), wf);
-    } else {
+    unpack_vec(wv[ch], wf);
+    unpack_vec(bv[ch], bf);
 #pragma unroll
-      for (int e = 0; e < V; ++e) wf[e] = A(1);
-    }
-    if (b != nullptr) {
-      unpack_vec(load_vec<T, V>(b + col), bf);
-    } else {
-#pragma unroll
-      for (int e = 0; e < V; ++e) bf[e] = A(0);
+    for (int e = 0; e < V; ++e) {
+      wf[e] = w != nullptr ? wf[e] : A(1);
+      bf[e] = b != nullptr ? bf[e] : A(0);
     }
     // Elements in pairs: y_k = sum_i (w c_i) r_{k-i}, written over the consumed inputs.
 #pragma unroll
