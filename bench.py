@@ -13,7 +13,9 @@ with HIP events on that stream; ``value`` is the workload's throughput and
 ``roofline`` compares it to MI355X's published peak (fp32 MFMA 157.3 TFLOP/s,
 HBM 8 TB/s). ``cpu_baseline`` times the CPU oracle (the op-for-op restatement
 of the reference's general path) on a bounded sample of the same workload on
-this host. Rank 0 prints one JSON line.
+this host. ``stream_ceiling`` is the measured rate of plain streaming copies and
+reads on the same GPU (the library's probe kernels, and torch's copy), a
+practical HBM ceiling beside the published peak. Rank 0 prints one JSON line.
 """
 
 import argparse
@@ -483,6 +485,40 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def stream_ceiling(device, steps=10, warmup=2):
+    """Measured HBM ceiling: the library's streaming probes (pt_stream_copy /
+    pt_stream_read: 16-byte non-temporal accesses, the series kernels' pattern)
+    over 2 GiB each way, best over a sweep of grid sizes, beside torch's own copy."""
+    import torch
+    from polytensors_amd import _lib
+
+    lib = _lib.load()
+    stream = _lib.stream_of(device)
+    nbytes = 2 << 30
+    src = torch.ones(nbytes // 4, device=device)
+    dst = torch.empty_like(src)
+    out = torch.empty(65536, dtype=torch.int32, device=device)
+    best = {"copy": (0.0, 0), "read": (0.0, 0)}
+    for blocks in (1024, 2048, 4096, 8192, 16384):
+        def copy():
+            _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks, stream), "stream copy")
+
+        def read():
+            _lib.check(lib.pt_stream_read(src.data_ptr(), nbytes, blocks, out.data_ptr(), stream), "stream read")
+
+        for name, fn, moved in (("copy", copy, 2 * nbytes), ("read", read, nbytes)):
+            rate = moved / (time_steps(fn, steps, warmup) * 1e-3) / 1e9
+            if rate > best[name][0]:
+                best[name] = (rate, blocks)
+    torch_copy = 2 * nbytes / (time_steps(lambda: dst.copy_(src), steps, warmup) * 1e-3) / 1e9
+    del src, dst, out
+    torch.cuda.empty_cache()
+    return {"copy": round(best["copy"][0], 1), "read": round(best["read"][0], 1),
+            "torch_copy": round(torch_copy, 1), "unit": "GB/s",
+            "how": (f"pt_stream_copy / pt_stream_read over 2 GiB (read + write / read), best grid "
+                    f"{best['copy'][1]} / {best['read'][1]} blocks of 256; torch copy_ of the same buffers")}
+
+
 def measure(name, device, steps, warmup, min_seconds=0.0):
     """Time ``steps`` steps (raised so the timed region lasts at least ``min_seconds``)."""
     w = WORKLOADS[name](device)
@@ -546,6 +582,7 @@ def main():
                      "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4) if w["peak"] else None,
                      "traffic": profiled_traffic(w["kernel"]) if w["peak"] else None},
     }
+    line["stream_ceiling"] = stream_ceiling(device)
     cpu_samplers = {}
     if not args.no_components:
         comps = {}

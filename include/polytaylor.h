@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 6
+#define PT_ABI_VERSION 7
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -367,6 +367,19 @@ typedef enum pt_binary {
 int pt_series_binary(int dtype, int degree, int op, const void* const* a,
                      const void* const* b, void* const* y, int64_t numel,
                      void* stream);
+
+/*
+ * Streaming probes (measurement only; no counterpart in the reference): the
+ * practical HBM ceiling beside the published peak, with the access pattern of
+ * the memory-bound series kernels (16-byte non-temporal loads and stores).
+ * pt_stream_copy copies `bytes` (a multiple of 16, 16-byte aligned pointers);
+ * pt_stream_read reads them and writes out[b] = XOR of the 32-bit words read by
+ * block b, for b < the block count (`out` holds one uint32 per block).
+ * blocks = 0 takes pt_stream_probe_blocks(); at most 65536.
+ */
+int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, void* stream);
+int pt_stream_read(const void* src, int64_t bytes, int blocks, void* out, void* stream);
+int pt_stream_probe_blocks(void);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -57,6 +57,9 @@ SIGNATURES = {
                                          _c_vpp, _c_vpp, _c_vpp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_int, _c_vp, _c_vp, _c_dbl, _c_vp]),
     "pt_taylor_attention_bwd_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int]),
+    "pt_stream_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
+    "pt_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_vp]),
+    "pt_stream_probe_blocks": (_c_int, []),
     "pt_complex_to_real": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_real_to_complex": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),

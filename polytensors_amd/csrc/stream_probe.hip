@@ -1,0 +1,116 @@
+// Streaming probes: the HBM rates of a plain copy and a plain read with the
+// access pattern of the memory-bound series kernels (16-byte non-temporal loads
+// and stores, kProbeUnroll vectors in flight per thread, one contiguous chunk
+// per block).
+// They measure the practical ceiling those kernels are compared with beside the
+// published 8 TB/s; they compute nothing of the series and have no counterpart
+// in the reference.
+#include "pt_common.h"
+
+namespace pt {
+
+constexpr int kProbeThreads = 256;
+constexpr int kProbeUnroll = 4;
+constexpr int kProbeDefaultBlocks = 2048;   // 8 resident waves per SIMD on 256 CUs
+constexpr int kProbeMaxBlocks = 65536;
+
+// Block b owns the contiguous chunk [b * chunk, (b + 1) * chunk) of the n
+// vectors, as a series kernel's block owns its rows.
+__device__ __forceinline__ void probe_chunk(int64_t n, int64_t& begin, int64_t& end) {
+  const int64_t chunk = (n + gridDim.x - 1) / gridDim.x;
+  begin = min(static_cast<int64_t>(blockIdx.x) * chunk, n);
+  end = min(begin + chunk, n);
+}
+
+__global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(const u32x4_t* __restrict__ src,
+                                                                    u32x4_t* __restrict__ dst, int64_t n) {
+  int64_t i, end;
+  probe_chunk(n, i, end);
+  i += threadIdx.x;
+  for (; i + (kProbeUnroll - 1) * kProbeThreads < end; i += kProbeUnroll * kProbeThreads) {
+    u32x4_t v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * kProbeThreads);
+  }
+  for (; i < end; i += kProbeThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// Reads every 32-bit word once; out[block] = XOR of the block's words, so the
+// loads cannot be dropped and the result is checkable on the host.
+__global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const u32x4_t* __restrict__ src, int64_t n,
+                                                                    uint32_t* __restrict__ out) {
+  __shared__ uint32_t part[kProbeThreads / kWave];
+  int64_t i, end;
+  probe_chunk(n, i, end);
+  i += threadIdx.x;
+  u32x4_t acc = {0u, 0u, 0u, 0u};
+  for (; i + (kProbeUnroll - 1) * kProbeThreads < end; i += kProbeUnroll * kProbeThreads) {
+    u32x4_t v[kProbeUnroll];
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+#pragma unroll
+    for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
+  }
+  for (; i < end; i += kProbeThreads) acc ^= __builtin_nontemporal_load(src + i);
+  uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) x ^= __shfl_xor(x, off);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kProbeThreads / kWave; ++w) t ^= part[w];
+    out[blockIdx.x] = t;
+  }
+}
+
+}  // namespace pt
+
+namespace {
+
+int check_probe(const void* src, int64_t bytes, int blocks, const char* what) {
+  PT_REQUIRE(bytes >= 0 && bytes % 16 == 0, PT_INVALID_ARGUMENT,
+             std::string(what) + ": bytes must be a non-negative multiple of 16");
+  PT_REQUIRE(blocks >= 0 && blocks <= pt::kProbeMaxBlocks, PT_INVALID_ARGUMENT,
+             std::string(what) + ": blocks must be 0 (default) .. 65536");
+  PT_REQUIRE(bytes == 0 || (src != nullptr && pt_host::aligned16(src)), PT_INVALID_ARGUMENT,
+             std::string(what) + ": source must be a 16-byte aligned device pointer");
+  return -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, void* stream) {
+  pt_host::clear_error();
+  const int early = check_probe(src, bytes, blocks, "stream copy");
+  if (early >= 0) return early;
+  if (bytes == 0) return PT_OK;
+  PT_REQUIRE(dst != nullptr && pt_host::aligned16(dst), PT_INVALID_ARGUMENT,
+             "stream copy: destination must be a 16-byte aligned device pointer");
+  const unsigned grid = static_cast<unsigned>(blocks > 0 ? blocks : pt::kProbeDefaultBlocks);
+  pt::stream_copy_kernel<<<grid, pt::kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const pt::u32x4_t*>(src), static_cast<pt::u32x4_t*>(dst), bytes / 16);
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
+
+int pt_stream_read(const void* src, int64_t bytes, int blocks, void* out, void* stream) {
+  pt_host::clear_error();
+  const int early = check_probe(src, bytes, blocks, "stream read");
+  if (early >= 0) return early;
+  PT_REQUIRE(out != nullptr, PT_INVALID_ARGUMENT, "stream read: out (one uint32 per block) is required");
+  const unsigned grid = static_cast<unsigned>(blocks > 0 ? blocks : pt::kProbeDefaultBlocks);
+  pt::stream_read_kernel<<<grid, pt::kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const pt::u32x4_t*>(src), bytes / 16, static_cast<uint32_t*>(out));
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
+
+int pt_stream_probe_blocks(void) { return pt::kProbeDefaultBlocks; }
+
+}  // extern "C"
