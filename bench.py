@@ -13,9 +13,9 @@ with HIP events on that stream; ``value`` is the workload's throughput and
 ``roofline`` compares it to MI355X's published peak (fp32 MFMA 157.3 TFLOP/s,
 HBM 8 TB/s). ``cpu_baseline`` times the CPU oracle (the op-for-op restatement
 of the reference's general path) on a bounded sample of the same workload on
-this host. ``stream_ceiling`` is the measured rate of plain streaming copies and
-reads on the same GPU (the library's probe kernels, and torch's copy), a
-practical HBM ceiling beside the published peak. Rank 0 prints one JSON line.
+this host. For memory-bound workloads ``roofline.stream_ceiling`` is the measured rate
+of a plain streaming read or copy of the same byte count on the same GPU (the
+library's probe kernels), a practical HBM ceiling beside the published peak. Rank 0 prints one JSON line.
 """
 
 import argparse
@@ -203,7 +203,7 @@ def wl_norm(device):
         return _ops.norm_series(x, [w], [], n, 1e-6, False)
 
     nbytes = 2 * (K + 1) * rows * n * 2 + n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
                 kernel="norm_series", dtype="bf16",
                 workload=f"rms_norm_series [{K + 1},{rows},{n}] bf16 weight eps=1e-6",
                 cpu=lambda: cpu_norm(rows, n, K))
@@ -224,7 +224,7 @@ def wl_ce(device):
         return _ops.cross_entropy_series(z, y, -100, 1, 0.0)
 
     nbytes = (K + 1) * rows * classes * 4 + rows * 8 + (K + 1) * rows * 4
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="read", peak=PEAK_HBM, bytes=nbytes,
                 kernel="cross_entropy_series", dtype="fp32",
                 workload=f"cross_entropy_series [{K + 1},{rows},{classes}] fp32 mean",
                 cpu=lambda: cpu_ce(rows, classes, K))
@@ -243,7 +243,7 @@ def wl_activation(device):
         return _ops.activation_series(x, "gelu")
 
     nbytes = 2 * (K + 1) * rows * n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
                 kernel="activation_series", dtype="bf16",
                 workload=f"gelu_series [{K + 1},{rows},{n}] bf16",
                 cpu=lambda: cpu_activation(rows, n, K))
@@ -263,7 +263,7 @@ def wl_norm_bwd(device):
         return _ops.norm_series_backward(x, g, n, 1e-6, False)
 
     nbytes = 3 * (K + 1) * rows * n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
                 kernel="norm_series_bwd", dtype="bf16",
                 workload=f"rms_norm_series_backward [{K + 1},{rows},{n}] bf16",
                 cpu=lambda: cpu_norm_bwd(rows, n, K))
@@ -286,7 +286,7 @@ def wl_ce_bwd(device):
         return _ops.cross_entropy_series_backward(z, y, -100, 0.0, lse, cot)
 
     nbytes = 2 * (K + 1) * rows * classes * 4 + rows * 8 + 2 * (K + 1) * rows * 4
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", peak=PEAK_HBM, bytes=nbytes,
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
                 kernel="cross_entropy_series_bwd", dtype="fp32",
                 workload=f"cross_entropy_series_backward [{K + 1},{rows},{classes}] fp32",
                 cpu=lambda: cpu_ce_bwd(rows, classes, K))
@@ -485,38 +485,48 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def stream_ceiling(device, steps=10, warmup=2):
-    """Measured HBM ceiling: the library's streaming probes (pt_stream_copy /
-    pt_stream_read: 16-byte non-temporal accesses, the series kernels' pattern)
-    over 2 GiB each way, best over a sweep of grid sizes, beside torch's own copy."""
+def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
+    """Measured HBM ceiling for a workload moving ``nbytes`` algorithmic bytes.
+
+    pattern "read": pt_stream_read over nbytes; "copy": pt_stream_copy of nbytes / 2
+    each way (read + write). The probes use the series kernels' access pattern
+    (16-byte non-temporal accesses); the best over grid sizes and two layouts (a
+    contiguous chunk per block, a grid-stride walk) is reported, beside torch's own
+    copy for "copy".
+    """
     import torch
     from polytensors_amd import _lib
 
     lib = _lib.load()
     stream = _lib.stream_of(device)
-    nbytes = 2 << 30
-    src = torch.ones(nbytes // 4, device=device)
-    dst = torch.empty_like(src)
+    each = (nbytes // 2 if pattern == "copy" else nbytes) // 16 * 16
+    src = torch.empty(each // 4, device=device).fill_(1.0)
+    dst = torch.empty_like(src) if pattern == "copy" else None
     out = torch.empty(65536, dtype=torch.int32, device=device)
-    best = {"copy": (0.0, 0), "read": (0.0, 0)}
-    for blocks in (1024, 2048, 4096, 8192, 16384):
-        def copy():
-            _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks, stream), "stream copy")
-
-        def read():
-            _lib.check(lib.pt_stream_read(src.data_ptr(), nbytes, blocks, out.data_ptr(), stream), "stream read")
-
-        for name, fn, moved in (("copy", copy, 2 * nbytes), ("read", read, nbytes)):
-            rate = moved / (time_steps(fn, steps, warmup) * 1e-3) / 1e9
-            if rate > best[name][0]:
-                best[name] = (rate, blocks)
-    torch_copy = 2 * nbytes / (time_steps(lambda: dst.copy_(src), steps, warmup) * 1e-3) / 1e9
+    moved = 2 * each if pattern == "copy" else each
+    best, best_how = 0.0, ""
+    for chunked in (1, 0):
+        for blocks in (1024, 2048, 4096, 8192, 16384):
+            if pattern == "copy":
+                def fn():
+                    _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), each, blocks, chunked, stream),
+                               "stream copy")
+            else:
+                def fn():
+                    _lib.check(lib.pt_stream_read(src.data_ptr(), each, blocks, chunked, out.data_ptr(), stream),
+                               "stream read")
+            reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup), 1e-3)))   # >= 50 ms timed
+            rate = moved / (time_steps(fn, reps, 1) * 1e-3) / 1e9
+            if rate > best:
+                best, best_how = rate, f"{blocks} blocks of 256, {'chunked' if chunked else 'grid-stride'}"
+    entry = {"pattern": pattern, "bytes": moved, "rate": round(best, 1), "unit": "GB/s",
+             "how": f"pt_stream_{pattern} ({best_how}; best of a sweep of grids and layouts)"}
+    if pattern == "copy":
+        reps = max(steps, math.ceil(50.0 / max(time_steps(lambda: dst.copy_(src), 2, warmup), 1e-3)))
+        entry["torch_copy"] = round(moved / (time_steps(lambda: dst.copy_(src), reps, 1) * 1e-3) / 1e9, 1)
     del src, dst, out
     torch.cuda.empty_cache()
-    return {"copy": round(best["copy"][0], 1), "read": round(best["read"][0], 1),
-            "torch_copy": round(torch_copy, 1), "unit": "GB/s",
-            "how": (f"pt_stream_copy / pt_stream_read over 2 GiB (read + write / read), best grid "
-                    f"{best['copy'][1]} / {best['read'][1]} blocks of 256; torch copy_ of the same buffers")}
+    return entry
 
 
 def measure(name, device, steps, warmup, min_seconds=0.0):
@@ -582,7 +592,10 @@ def main():
                      "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4) if w["peak"] else None,
                      "traffic": profiled_traffic(w["kernel"]) if w["peak"] else None},
     }
-    line["stream_ceiling"] = stream_ceiling(device)
+    if w["bound"] == "hbm":
+        ceil = stream_ceiling(device, w["pattern"], w["bytes"])
+        ceil["frac"] = round(w["achieved"] / ceil["rate"], 4)
+        line["roofline"]["stream_ceiling"] = ceil
     cpu_samplers = {}
     if not args.no_components:
         comps = {}
@@ -594,6 +607,10 @@ def main():
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
                            "frac": round(c["achieved"] / c["peak"], 4) if c["peak"] else None,
                            "traffic": profiled_traffic(c["kernel"]) if c["peak"] else None}
+            if c["bound"] == "hbm":
+                ceil = stream_ceiling(device, c["pattern"], c["bytes"])
+                ceil["frac"] = round(c["achieved"] / ceil["rate"], 4)
+                comps[name]["stream_ceiling"] = ceil
             cpu_samplers[name] = c["cpu"]
             del c
             torch.cuda.empty_cache()

@@ -375,10 +375,11 @@ int pt_series_binary(int dtype, int degree, int op, const void* const* a,
  * pt_stream_copy copies `bytes` (a multiple of 16, 16-byte aligned pointers);
  * pt_stream_read reads them and writes out[b] = XOR of the 32-bit words read by
  * block b, for b < the block count (`out` holds one uint32 per block).
- * blocks = 0 takes pt_stream_probe_blocks(); at most 65536.
+ * blocks = 0 takes pt_stream_probe_blocks(); at most 65536. chunked != 0: block
+ * b walks its own contiguous chunk; 0: the grid walks the buffer together.
  */
-int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, void* stream);
-int pt_stream_read(const void* src, int64_t bytes, int blocks, void* out, void* stream);
+int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, int chunked, void* stream);
+int pt_stream_read(const void* src, int64_t bytes, int blocks, int chunked, void* out, void* stream);
 int pt_stream_probe_blocks(void);
 
 #ifdef __cplusplus

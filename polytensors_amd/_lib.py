@@ -57,8 +57,8 @@ SIGNATURES = {
                                          _c_vpp, _c_vpp, _c_vpp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_int, _c_vp, _c_vp, _c_dbl, _c_vp]),
     "pt_taylor_attention_bwd_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int]),
-    "pt_stream_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_vp]),
-    "pt_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_vp]),
+    "pt_stream_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
+    "pt_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "pt_stream_probe_blocks": (_c_int, []),
     "pt_complex_to_real": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_real_to_complex": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),

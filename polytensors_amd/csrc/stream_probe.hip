@@ -1,7 +1,7 @@
 // Streaming probes: the HBM rates of a plain copy and a plain read with the
 // access pattern of the memory-bound series kernels (16-byte non-temporal loads
-// and stores, kProbeUnroll vectors in flight per thread, one contiguous chunk
-// per block).
+// and stores, kProbeUnroll vectors in flight per thread; a contiguous chunk per
+// block or a grid-stride walk).
 // They measure the practical ceiling those kernels are compared with beside the
 // published 8 TB/s; they compute nothing of the series and have no counterpart
 // in the reference.
@@ -14,46 +14,60 @@ constexpr int kProbeUnroll = 4;
 constexpr int kProbeDefaultBlocks = 2048;   // 8 resident waves per SIMD on 256 CUs
 constexpr int kProbeMaxBlocks = 65536;
 
-// Block b owns the contiguous chunk [b * chunk, (b + 1) * chunk) of the n
-// vectors, as a series kernel's block owns its rows.
-__device__ __forceinline__ void probe_chunk(int64_t n, int64_t& begin, int64_t& end) {
-  const int64_t chunk = (n + gridDim.x - 1) / gridDim.x;
-  begin = min(static_cast<int64_t>(blockIdx.x) * chunk, n);
-  end = min(begin + chunk, n);
-}
+// The vectors a thread visits: CHUNKED, block b owns the contiguous chunk
+// [b * chunk, (b + 1) * chunk) (as a series kernel's block owns its rows) and
+// its threads step by the block width; otherwise the whole grid steps through
+// the buffer together (grid-stride). Which is faster depends on the size.
+template <bool CHUNKED>
+struct ProbeRange {
+  int64_t i, end, step;
+  __device__ __forceinline__ explicit ProbeRange(int64_t n) {
+    if constexpr (CHUNKED) {
+      const int64_t chunk = (n + gridDim.x - 1) / gridDim.x;
+      const int64_t begin = min(static_cast<int64_t>(blockIdx.x) * chunk, n);
+      end = min(begin + chunk, n);
+      i = begin + threadIdx.x;
+      step = kProbeThreads;
+    } else {
+      end = n;
+      i = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
+      step = static_cast<int64_t>(gridDim.x) * kProbeThreads;
+    }
+  }
+};
 
+template <bool CHUNKED>
 __global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(const u32x4_t* __restrict__ src,
                                                                     u32x4_t* __restrict__ dst, int64_t n) {
-  int64_t i, end;
-  probe_chunk(n, i, end);
-  i += threadIdx.x;
-  for (; i + (kProbeUnroll - 1) * kProbeThreads < end; i += kProbeUnroll * kProbeThreads) {
+  ProbeRange<CHUNKED> r(n);
+  int64_t i = r.i;
+  for (; i + (kProbeUnroll - 1) * r.step < r.end; i += kProbeUnroll * r.step) {
     u32x4_t v[kProbeUnroll];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * r.step);
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * kProbeThreads);
+    for (int u = 0; u < kProbeUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * r.step);
   }
-  for (; i < end; i += kProbeThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+  for (; i < r.end; i += r.step) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 // Reads every 32-bit word once; out[block] = XOR of the block's words, so the
 // loads cannot be dropped and the result is checkable on the host.
+template <bool CHUNKED>
 __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const u32x4_t* __restrict__ src, int64_t n,
                                                                     uint32_t* __restrict__ out) {
   __shared__ uint32_t part[kProbeThreads / kWave];
-  int64_t i, end;
-  probe_chunk(n, i, end);
-  i += threadIdx.x;
+  ProbeRange<CHUNKED> r(n);
+  int64_t i = r.i;
   u32x4_t acc = {0u, 0u, 0u, 0u};
-  for (; i + (kProbeUnroll - 1) * kProbeThreads < end; i += kProbeUnroll * kProbeThreads) {
+  for (; i + (kProbeUnroll - 1) * r.step < r.end; i += kProbeUnroll * r.step) {
     u32x4_t v[kProbeUnroll];
 #pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kProbeThreads);
+    for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * r.step);
 #pragma unroll
     for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
   }
-  for (; i < end; i += kProbeThreads) acc ^= __builtin_nontemporal_load(src + i);
+  for (; i < r.end; i += r.step) acc ^= __builtin_nontemporal_load(src + i);
   uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
 #pragma unroll
   for (int off = kWave / 2; off > 0; off /= 2) x ^= __shfl_xor(x, off);
@@ -85,7 +99,7 @@ int check_probe(const void* src, int64_t bytes, int blocks, const char* what) {
 
 extern "C" {
 
-int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, void* stream) {
+int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, int chunked, void* stream) {
   pt_host::clear_error();
   const int early = check_probe(src, bytes, blocks, "stream copy");
   if (early >= 0) return early;
@@ -93,20 +107,30 @@ int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, void* 
   PT_REQUIRE(dst != nullptr && pt_host::aligned16(dst), PT_INVALID_ARGUMENT,
              "stream copy: destination must be a 16-byte aligned device pointer");
   const unsigned grid = static_cast<unsigned>(blocks > 0 ? blocks : pt::kProbeDefaultBlocks);
-  pt::stream_copy_kernel<<<grid, pt::kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const pt::u32x4_t*>(src), static_cast<pt::u32x4_t*>(dst), bytes / 16);
+  const auto* s = static_cast<const pt::u32x4_t*>(src);
+  auto* d = static_cast<pt::u32x4_t*>(dst);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (chunked)
+    pt::stream_copy_kernel<true><<<grid, pt::kProbeThreads, 0, st>>>(s, d, bytes / 16);
+  else
+    pt::stream_copy_kernel<false><<<grid, pt::kProbeThreads, 0, st>>>(s, d, bytes / 16);
   PT_LAUNCH_CHECK();
   return PT_OK;
 }
 
-int pt_stream_read(const void* src, int64_t bytes, int blocks, void* out, void* stream) {
+int pt_stream_read(const void* src, int64_t bytes, int blocks, int chunked, void* out, void* stream) {
   pt_host::clear_error();
   const int early = check_probe(src, bytes, blocks, "stream read");
   if (early >= 0) return early;
   PT_REQUIRE(out != nullptr, PT_INVALID_ARGUMENT, "stream read: out (one uint32 per block) is required");
   const unsigned grid = static_cast<unsigned>(blocks > 0 ? blocks : pt::kProbeDefaultBlocks);
-  pt::stream_read_kernel<<<grid, pt::kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const pt::u32x4_t*>(src), bytes / 16, static_cast<uint32_t*>(out));
+  const auto* s = static_cast<const pt::u32x4_t*>(src);
+  auto* o = static_cast<uint32_t*>(out);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (chunked)
+    pt::stream_read_kernel<true><<<grid, pt::kProbeThreads, 0, st>>>(s, bytes / 16, o);
+  else
+    pt::stream_read_kernel<false><<<grid, pt::kProbeThreads, 0, st>>>(s, bytes / 16, o);
   PT_LAUNCH_CHECK();
   return PT_OK;
 }

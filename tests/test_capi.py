@@ -51,10 +51,10 @@ def _vpp(n):
     ("pt_rms_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 3, _vpp(2), 4, 8, 1e-5, None), 1, "weight_orders"),
     ("pt_layer_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 0, None, 1, _vpp(2), 4, 8, 1e-5, None), 1, "bias"),
     ("pt_rms_norm_series_fwd", lambda: (0, 1, _vpp(2), None, 0, _vpp(2), 4, 0, 1e-5, None), 1, "n >= 1"),
-    ("pt_stream_copy", lambda: (1 << 20, 1 << 21, 24, 0, None), 1, "multiple of 16"),
-    ("pt_stream_copy", lambda: ((1 << 20) + 4, 1 << 21, 32, 0, None), 1, "aligned"),
-    ("pt_stream_read", lambda: (1 << 20, 32, 70000, 1 << 21, None), 1, "blocks"),
-    ("pt_stream_read", lambda: (1 << 20, 32, 0, None, None), 1, "out"),
+    ("pt_stream_copy", lambda: (1 << 20, 1 << 21, 24, 0, 1, None), 1, "multiple of 16"),
+    ("pt_stream_copy", lambda: ((1 << 20) + 4, 1 << 21, 32, 0, 1, None), 1, "aligned"),
+    ("pt_stream_read", lambda: (1 << 20, 32, 70000, 1, 1 << 21, None), 1, "blocks"),
+    ("pt_stream_read", lambda: (1 << 20, 32, 0, 0, None, None), 1, "out"),
 ])
 def test_argument_errors_return_before_launch(entry, args, status, needle):
     lib = _lib.load()

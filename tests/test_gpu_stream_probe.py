@@ -20,12 +20,13 @@ def _words(nbytes, seed):
 
 @pytest.mark.parametrize("nbytes", [0, 16, 4096 + 48, 1 << 20, (3 << 20) + 16 * 7])
 @pytest.mark.parametrize("blocks", [0, 1, 3, 1024])
-def test_copy_moves_every_byte(nbytes, blocks):
+@pytest.mark.parametrize("chunked", [0, 1])
+def test_copy_moves_every_byte(nbytes, blocks, chunked):
     host = _words(nbytes, nbytes + blocks)
     src = host.cuda()
     dst = torch.full_like(src, -1)
     lib = _lib.load()
-    _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks, _lib.stream_of(src.device)),
+    _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, blocks, chunked, _lib.stream_of(src.device)),
                "stream copy")
     torch.cuda.synchronize()
     assert torch.equal(dst.cpu(), host)
@@ -33,13 +34,14 @@ def test_copy_moves_every_byte(nbytes, blocks):
 
 @pytest.mark.parametrize("nbytes", [0, 16, 4096 + 48, 1 << 20, (3 << 20) + 16 * 7])
 @pytest.mark.parametrize("blocks", [0, 1, 3, 1024])
-def test_read_checksum_covers_every_word(nbytes, blocks):
+@pytest.mark.parametrize("chunked", [0, 1])
+def test_read_checksum_covers_every_word(nbytes, blocks, chunked):
     host = _words(nbytes, 7 * nbytes + blocks)
     src = host.cuda()
     lib = _lib.load()
     grid = blocks or lib.pt_stream_probe_blocks()
     out = torch.full((grid,), 12345, dtype=torch.int32, device="cuda")
-    _lib.check(lib.pt_stream_read(src.data_ptr(), nbytes, blocks, out.data_ptr(), _lib.stream_of(src.device)),
+    _lib.check(lib.pt_stream_read(src.data_ptr(), nbytes, blocks, chunked, out.data_ptr(), _lib.stream_of(src.device)),
                "stream read")
     torch.cuda.synchronize()
     got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)) if grid else 0
