@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload attention|attention_window|attention_bwd|matmul|norm|ce|activation|norm_bwd|ce_bwd|decoder]
-                    [--no-cpu-baseline] [--no-components] [--component-seconds S]
+                    [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
 One step is one launch of the workload's fused kernel on one batch of synthetic
@@ -552,6 +552,7 @@ def main():
     parser.add_argument("--workload", default="attention", choices=sorted(WORKLOADS))
     parser.add_argument("--no-components", action="store_true", help="skip timing the other three kernels")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-ceiling", action="store_true", help="skip the measured HBM ceilings (profiling runs)")
     parser.add_argument("--component-seconds", type=float, default=0.2,
                         help="minimum timed duration of each component kernel (0: steps/2 steps)")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -592,7 +593,7 @@ def main():
                      "unit": w["unit"], "frac": round(w["achieved"] / w["peak"], 4) if w["peak"] else None,
                      "traffic": profiled_traffic(w["kernel"]) if w["peak"] else None},
     }
-    if w["bound"] == "hbm":
+    if w["bound"] == "hbm" and not args.no_ceiling:
         ceil = stream_ceiling(device, w["pattern"], w["bytes"])
         ceil["frac"] = round(w["achieved"] / ceil["rate"], 4)
         line["roofline"]["stream_ceiling"] = ceil
@@ -607,7 +608,7 @@ def main():
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
                            "frac": round(c["achieved"] / c["peak"], 4) if c["peak"] else None,
                            "traffic": profiled_traffic(c["kernel"]) if c["peak"] else None}
-            if c["bound"] == "hbm":
+            if c["bound"] == "hbm" and not args.no_ceiling:
                 ceil = stream_ceiling(device, c["pattern"], c["bytes"])
                 ceil["frac"] = round(c["achieved"] / ceil["rate"], 4)
                 comps[name]["stream_ceiling"] = ceil
