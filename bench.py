@@ -1,7 +1,8 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|attention_window|attention_bwd|matmul|norm|ce|activation|norm_bwd|ce_bwd|decoder]
+                    [--workload attention|attention_window|attention_bwd|attention_bwd_window|matmul|norm|ce|
+                                activation|norm_bwd|ce_bwd|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
@@ -138,6 +139,41 @@ def wl_attention_bwd(device):
                 bytes=nbytes, kernel="taylor_attention_bwd", dtype="fp32",
                 workload=f"taylor_attention_bwd B={B} H={H} L={L} d={d} K={K} fp32 causal line inputs",
                 cpu=lambda: cpu_attention_bwd(L, d, K))
+
+
+def wl_attention_bwd_window(device):
+    """The attention gradient series of ``attention_bwd`` with the boolean sliding-window mask of
+    ``attention_window`` (0 <= i - j < 256) instead of causal. Work: five series products over
+    the admissible pairs."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K, W = 4, 16, 2048, 128, 4, 256
+    g = _gen(12, device)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [base, direction] + [torch.zeros(B * H, L, d, device=device) for _ in range(2, K + 1)]
+
+    q, k, v = line(), line(), line()
+    cot = [torch.randn(B * H, L, d, generator=g, device=device) * 0.5 ** o for o in range(K + 1)]
+    i = torch.arange(L, device=device)
+    mask = ((i[:, None] - i[None, :]) >= 0) & ((i[:, None] - i[None, :]) < W)
+    scale = 1 / math.sqrt(d)
+    out, lse = _ops.taylor_attention_fwd(q, k, v, mask, False, scale, K)
+
+    def step():
+        return _ops.taylor_attention_bwd(q, k, v, out, lse, cot, mask, False, scale)
+
+    pairs = (K + 1) * (K + 2) // 2
+    admissible = W * (W + 1) // 2 + (L - W) * W
+    flops = 5 * pairs * 2 * d * B * H * admissible
+    nbytes = 8 * (K + 1) * B * H * L * d * 4 + L * L
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_FP32_MFMA,
+                bytes=nbytes, kernel="taylor_attention_bwd_window", dtype="fp32",
+                workload=f"taylor_attention_bwd B={B} H={H} L={L} d={d} K={K} fp32 sliding window {W} (bool mask)",
+                cpu=lambda: cpu_attention_bwd(L, d, K, window=W))
 
 
 def wl_decoder(device):
@@ -295,6 +331,7 @@ def wl_ce_bwd(device):
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
              "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
+             "attention_bwd_window": wl_attention_bwd_window,
              "decoder": wl_decoder}
 
 
@@ -348,21 +385,27 @@ def cpu_attention_window(L, d, K, W, heads=16):
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 window {W}", seconds=t)
 
 
-def cpu_attention_bwd(L, d, K, heads=16):
+def cpu_attention_bwd(L, d, K, heads=16, window=None):
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(8)
     q, k, v, cot = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(4))
+    mask = None
+    if window is not None:
+        i = torch.arange(L)
+        mask = ((i[:, None] - i[None, :]) >= 0) & ((i[:, None] - i[None, :]) < window)
 
     def some_heads():
         for _ in range(heads):
-            oracle.attention_backward(q, k, v, cot, is_causal=True)
+            oracle.attention_backward(q, k, v, cot, attn_mask=mask, is_causal=mask is None)
 
     t = _cpu_time(some_heads, reps=1)
-    flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
+    pairs = L * (L + 1) / 2 if window is None else window * (window + 1) // 2 + (L - window) * window
+    flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * pairs
+    what = "causal" if window is None else f"window {window}"
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
-                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
+                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 {what}", seconds=t)
 
 
 def cpu_decoder(layers, d, heads, vocab, K, seq=64):

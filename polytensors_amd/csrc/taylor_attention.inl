@@ -175,6 +175,19 @@ __device__ __forceinline__ void attn_key_range(int S, int q_block, int causal, c
   }
 }
 
+// Byte (row, col) of an (L, S) boolean mask, read unconditionally: indices are
+// clamped into the mask and without a mask a valid dummy byte is read (the
+// caller ignores it). Callers issue these reads ahead of their prefetches: a
+// load under a per-lane branch, or one issued after a prefetch and used soon,
+// makes the compiler wait for every load in flight (memory waits complete in
+// order).
+__device__ __forceinline__ uint8_t attn_mask_byte(const uint8_t* mask, const void* dummy, int row, int col, int L,
+                                                  int S) {
+  const uint8_t* base = mask != nullptr ? mask : static_cast<const uint8_t*>(dummy);
+  const int64_t at = mask != nullptr ? static_cast<int64_t>(min(row, L - 1)) * S + min(col, S - 1) : 0;
+  return base[at];
+}
+
 // E is the head-dim interleave of the output accumulators: accumulator
 // g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
 // (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).
@@ -342,6 +355,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
   attn_key_range(S, q_block, causal, ranges, lo, hi);
 
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
+    uint8_t mbyte[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + MF::acc_row(h, r), L, S);
     __syncthreads();
     // ---- stage K and V rows kb0 .. kb0+15 of every order (zero past S) ----
     {
@@ -407,7 +423,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
       const int key = kb0 + MF::acc_row(h, r);
       bool ok = q_ok && key < S;
       if (causal) ok = ok && key <= my_q;
-      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+      if (mask != nullptr) ok = ok && mbyte[r] != 0;
       valid[r] = ok;
       s0[r] = ok ? static_cast<A>(sc[0][r]) * scale : kNegInf;
     }

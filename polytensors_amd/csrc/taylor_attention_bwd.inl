@@ -334,7 +334,9 @@ __device__ __forceinline__ void attn_bwd_contract(Vec<T, 4> (&ring)[RING][K + 1]
 
 // STORE: also write the P and dS series of every visited 16 x 16 (query, key)
 // tile to PT / DST (attn_tile_offset layout) for taylor_attention_bwd_kv_mat_kernel.
-template <typename T, int K, int D, int NS, bool STORE>
+// MASKED: a boolean mask is given (the unmasked instantiation holds no mask
+// registers: at K = 4, D = 128 four of them cost the causal case 3%).
+template <typename T, int K, int D, int NS, bool STORE, bool MASKED>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, MPtrs<T> PT, MPtrs<T> DST, int L, int S,
@@ -416,6 +418,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
     }
   }
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
+    uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this lane's keys, read ahead of the block's prefetches
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + MF::acc_row(h, r), L, S);
+    }
     __syncthreads();   // the previous block's MFMAs are done with the tiles
     if constexpr (kPrefetchStage) {
       stage_k.commit(Ks);
@@ -484,7 +491,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       const int key = kb0 + MF::acc_row(h, r);
       bool ok = q_ok && key < S;
       if (causal) ok = ok && key <= my_q;
-      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(my_q) * S + key] != 0;
+      if constexpr (MASKED) ok = ok && mbyte[r] != 0;
       A p[K + 1], ds[K + 1];
       attn_prob_series<A, K>(sc, r, lse, ok, scale, p);
       attn_ds_series<A, K>(p, dp, r, delta, ds);
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 }
 
 // WHAT: 1 = dV, 2 = dK, 3 = both.
-template <typename T, int K, int D, int NS, int WHAT>
+template <typename T, int K, int D, int NS, int WHAT, bool MASKED>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
@@ -583,6 +590,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
     hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
   }
   for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
+    uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this lane's queries, read ahead of the block's loads
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], qb0 + MF::acc_row(h, r), my_k, L, S);
+    }
     __syncthreads();
     {
       constexpr int VPR = D / V;
@@ -650,7 +662,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
       const int q = qb0 + qr;
       bool ok = k_ok && q < L;
       if (causal) ok = ok && my_k <= q;
-      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(q) * S + my_k] != 0;
+      if constexpr (MASKED) ok = ok && mbyte[r] != 0;
       A lse[K + 1], p[K + 1];
 #pragma unroll
       for (int o = 0; o <= K; ++o) lse[o] = Ls[o][qr];
@@ -710,7 +722,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
 // into the B-operand registers (masked by admissibility: tiles the dQ kernel
 // did not visit hold no admissible pair). Two products per pair instead of the
 // four of the recomputing kernel. WHAT: 1 = dV, 2 = dK, 3 = both.
-template <typename T, int K, int D, int NS, int WHAT>
+template <typename T, int K, int D, int NS, int WHAT, bool MASKED>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_mat_kernel(
     CPtrs<T> Q, CPtrs<T> G, CPtrs<T> PT, CPtrs<T> DST, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
     const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
@@ -788,6 +800,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
     if constexpr (DO_V) stage_g.commit(Gs);
     if constexpr (DO_K) stage_q.commit(Qs);
     __syncthreads();
+    uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this block's queries, read ahead of the prefetch
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int sidx = 0; sidx < 4; ++sidx)
+        mbyte[sidx] = attn_mask_byte(mask, Q.p[0], qb0 + MF::acc_row(h, sidx), my_k, L, S);
+    }
     if (qb0 + kBM < hi) fetch(qb0 + kBM);
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of this block's MFMAs
 
@@ -796,7 +814,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
       const int q = qb0 + MF::acc_row(h, sidx);
       bool ok = k_ok && q < L;
       if (causal) ok = ok && my_k <= q;
-      if (mask != nullptr && ok) ok = mask[static_cast<int64_t>(q) * S + my_k] != 0;
+      if constexpr (MASKED) ok = ok && mbyte[sidx] != 0;
 #pragma unroll
       for (int o = 0; o <= K; ++o) {
         if constexpr (DO_V) pv[o].v[sidx] = ok ? pv[o].v[sidx] : T(0);
@@ -872,35 +890,44 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
     if (need_q && rows > 0) {
       constexpr int SL = Plan::DB / Plan::NS_Q;
       const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
+#define PT_ATTN_BWD_Q(STORE, MASKED)                                                                   \
+  taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, STORE, MASKED><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>( \
+      q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale)
+      const bool masked = a.mask != nullptr;
       if constexpr (kCanStore) {
-        if (a.materialize)   // (without a dq output the kernel still writes the P and dS tiles)
-          taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, true><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-              q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale);
+        if (a.materialize) {   // (without a dq output the kernel still writes the P and dS tiles)
+          if (masked) PT_ATTN_BWD_Q(true, true);
+          else PT_ATTN_BWD_Q(true, false);
+        }
       }
-      if (!a.materialize)
-        taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, false><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale);
+      if (!a.materialize) {
+        if (masked) PT_ATTN_BWD_Q(false, true);
+        else PT_ATTN_BWD_Q(false, false);
+      }
+#undef PT_ATTN_BWD_Q
       PT_LAUNCH_CHECK();
     }
     if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
       const dim3 block(kAttnWaves * kWave);
+#define PT_ATTN_BWD_KV(KERNEL, NS, WHAT, ARGS)                                      \
+  do {                                                                              \
+    if (a.mask != nullptr) KERNEL<T, K, D, NS, WHAT, true><<<grid, block, 0, a.stream>>> ARGS; \
+    else KERNEL<T, K, D, NS, WHAT, false><<<grid, block, 0, a.stream>>> ARGS;                  \
+  } while (0)
       if (a.materialize) {
        if constexpr (kCanStore) {
         constexpr int SL = Plan::DB / Plan::NS_KM;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
         if constexpr (Plan::km_fused) {
-          taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 3><<<grid, block, 0, a.stream>>>(
-              q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 3, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
           PT_LAUNCH_CHECK();
         } else {
           if (a.dv != nullptr) {
-            taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 1><<<grid, block, 0, a.stream>>>(
-                q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 1, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
           if (a.dk != nullptr) {
-            taylor_attention_bwd_kv_mat_kernel<T, K, D, Plan::NS_KM, 2><<<grid, block, 0, a.stream>>>(
-                q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 2, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
         }
@@ -909,22 +936,20 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
         constexpr int SL = Plan::DB / Plan::NS_KV;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
         if constexpr (Plan::kv_fused) {
-          taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 3><<<grid, block, 0, a.stream>>>(
-              q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 3, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
           PT_LAUNCH_CHECK();
         } else {
           if (a.dv != nullptr) {
-            taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 1><<<grid, block, 0, a.stream>>>(
-                q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 1, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
           if (a.dk != nullptr) {
-            taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, 2><<<grid, block, 0, a.stream>>>(
-                q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale);
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 2, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
         }
       }
+#undef PT_ATTN_BWD_KV
     }
     return PT_OK;
   }
