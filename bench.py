@@ -603,7 +603,7 @@ def main():
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the Taylor kernels are single-GPU "
-              "in this build; multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+              "in this build (each path shards over heads, rows or output tiles; that sharding is not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch
