@@ -177,15 +177,23 @@ __device__ __forceinline__ void attn_bwd_store(const AccT (&acc)[K + 1][NS], MPt
 }
 
 // Offset of element (query qi, key ki) of 16 x 16 tile (qt, kt) of one head in
-// the P / dS tile buffers: tiles are [head][query tile][key tile], and within a
-// tile the element sits where the consumer's (queries x keys) accumulator
-// layout holds it: lane (row_group(qi), ki), register row_reg(qi). A consumer
-// lane reads its four values with one load.
-template <typename MF>
+// the P / dS tile buffers (float): tiles are [head][query tile][key tile], and
+// within a tile the element sits at (ki % 4) * 64 + (ki / 4) * 16 + qi. The
+// producer's lane (query c, lane group h) holds keys 4h + r in register r, so
+// one store instruction (fixed r) writes 256 contiguous bytes; the consumer's
+// lane (key c, lane group h) needs queries 4h .. 4h + 3 of its key, which are
+// consecutive: one 16-byte load (attn_tile_consumer_offset).
+__device__ __forceinline__ int64_t attn_tile_base(int64_t head, int qt, int kt, int nqt, int nkt) {
+  return ((head * nqt + qt) * nkt + kt) * 256;
+}
 __device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt, int nqt, int nkt, int qi,
                                                     int ki) {
-  const int64_t tile = (head * nqt + qt) * nkt + kt;
-  return tile * 256 + (MF::row_group(qi) * 16 + ki) * 4 + MF::row_reg(qi);
+  return attn_tile_base(head, qt, kt, nqt, nkt) + (ki % 4) * 64 + (ki / 4) * 16 + qi;
+}
+// first of the four consecutive values (queries 4h .. 4h + 3 of key c) a consumer lane reads
+__device__ __forceinline__ int64_t attn_tile_consumer_offset(int64_t head, int qt, int kt, int nqt, int nkt, int c,
+                                                             int h) {
+  return attn_tile_base(head, qt, kt, nqt, nkt) + (c % 4) * 64 + (c / 4) * 16 + 4 * h;
 }
 
 // Register-staged copy of ROWS rows (from row `first`, zero past `limit`) of the
@@ -498,10 +506,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 #pragma unroll
       for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(ds[o]);
       if constexpr (STORE) {
+        static_assert(sizeof(T) == 4, "the tile layout follows the float accumulator layout (acc_row = 4h + r)");
         // (a wave whose 16 queries all lie past L owns no tile)
         if (slice == 0 && q_block + wave * kAttnQPerWave < L) {
           // element (query c, key acc_row(h, r)) of the wave's tile
-          const int64_t at = attn_tile_offset<MF>(head, q_block / 16 + wave, kb0 / 16, (L + 15) / 16,
+          const int64_t at = attn_tile_offset(head, q_block / 16 + wave, kb0 / 16, (L + 15) / 16,
                                                   (S + 15) / 16, c, MF::acc_row(h, r));
 #pragma unroll
           for (int o = 0; o <= K; ++o) {
@@ -756,6 +765,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
   const int my_k = kv_block + wave * 16 + c;
   const bool k_ok = my_k < S;
   const int nqt = (L + 15) / 16, nkt = (S + 15) / 16;
+  static_assert(sizeof(T) == 4, "the tile layout follows the float accumulator layout (acc_row = 4h + r)");
   const int kt = min(kv_block / 16 + wave, nkt - 1);   // a wave past S reads a valid tile, all masked
 
   acc_t acc_v[DO_V ? K + 1 : 1][NS], acc_k[DO_K ? K + 1 : 1][NS];
@@ -779,7 +789,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
   RowStager<T, K, D, kBM> stage_g, stage_q;
   Vec<T, 4> pn[DO_V ? K + 1 : 1], sn[DO_K ? K + 1 : 1];   // next block's tile values
   auto fetch = [&](int qb) {
-    const int64_t at = (((head * nqt + qb / 16) * nkt + kt) * 256) + lane * 4;
+    const int64_t at = attn_tile_consumer_offset(head, qb / 16, kt, nqt, nkt, c, h);
 #pragma unroll
     for (int o = 0; o <= K; ++o) {
       if constexpr (DO_V) pn[o] = *reinterpret_cast<const Vec<T, 4>*>(PT.p[o] + at);
