@@ -69,7 +69,11 @@ def matmul(a, b, below_autograd=False):
             return [c.reshape(1, rows, cols).contiguous() for c in coeffs]
         return [c.expand(*batch, rows, cols).reshape(-1, rows, cols).contiguous() for c in coeffs]
 
-    out = _ops.cauchy_matmul(flat(A, m, kd), flat(B, kd, n), degree, False)
+    if all(c.ndim == 2 and not c.is_contiguous() and c.t().is_contiguous() for c in B):
+        # a transposed [n, k] matrix (a linear layer's weight): the kernel reads it in place
+        out = _ops.cauchy_matmul(flat(A, m, kd), [c.t().reshape(1, n, kd) for c in B], degree, True)
+    else:
+        out = _ops.cauchy_matmul(flat(A, m, kd), flat(B, kd, n), degree, False)
     out = out.view(degree + 1, *batch, m, n)
     if squeeze_m:
         out = out.squeeze(-2)

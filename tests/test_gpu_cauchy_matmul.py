@@ -103,6 +103,19 @@ def test_linear_uses_transposed_weight(bias):
     _check(y.coeffs, want, dtype)
 
 
+@pytest.mark.parametrize("plain_b", [False, True])
+def test_matmul_by_transposed_view(plain_b):
+    # x @ W.t() with W contiguous [n, k]: the kernel reads W in place (its transposed-B mode)
+    degree, dtype = 2, torch.float32
+    X = _series((3, 33, 48), degree, 15, dtype)
+    W = _series((40, 48), 0 if plain_b else degree, 16, dtype)
+    with torch.no_grad(), PolyTensor.plain_range():
+        w = W[0].cuda().t() if plain_b else PolyTensor(tuple(c.cuda().t() for c in W))
+        y = _poly(X) @ w
+    want = oracle.matmul([x.double() for x in X], [c.double().t() for c in W])
+    _check(y.coeffs, want, dtype)
+
+
 def test_vector_operands():
     degree, dtype = 2, torch.float64
     A, v = _series((30, 20), degree, 13, dtype), _series((20,), degree, 14, dtype)
