@@ -528,6 +528,18 @@ def time_steps(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def cpu_model():
+    """The host CPU's model name (as lscpu reports it), for the CPU baseline."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
     """Measured HBM ceiling for a workload moving ``nbytes`` algorithmic bytes.
 
@@ -663,10 +675,13 @@ def main():
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
 
+        model = cpu_model()
+
         def cpu_entry(sampler):
             cpu = sampler()
             return {"value": round(cpu["value"], 6), "unit": cpu["unit"], "cores": torch.get_num_threads(),
-                    "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3)}
+                    "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3),
+                    "cpu_model": model}
 
         line["cpu_baseline"] = cpu_entry(w["cpu"])
         for name, sampler in cpu_samplers.items():   # the reference's CPU path beside each component
