@@ -563,11 +563,11 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
     for chunked in (1, 0):
         for blocks in (1024, 2048, 4096, 8192, 16384):
             if pattern == "copy":
-                def fn():
+                def fn(blocks=blocks, chunked=chunked):
                     _lib.check(lib.pt_stream_copy(src.data_ptr(), dst.data_ptr(), each, blocks, chunked, stream),
                                "stream copy")
             else:
-                def fn():
+                def fn(blocks=blocks, chunked=chunked):
                     _lib.check(lib.pt_stream_read(src.data_ptr(), each, blocks, chunked, out.data_ptr(), stream),
                                "stream read")
             reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup), 1e-3)))   # >= 50 ms timed
