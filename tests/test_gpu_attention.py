@@ -107,6 +107,31 @@ def test_shift_of_the_pipelined_kernel(case, causal):
     _check(out.coeffs, want, torch.float32)
 
 
+@pytest.mark.parametrize("L,S", [(1, 16), (17, 16), (65, 33), (130, 47)])
+@pytest.mark.parametrize("mode", ["causal", "mask_with_empty_row", "none"])
+def test_pipelined_kernel_short_and_ragged(L, S, mode):
+    # float32, full orders: the pipelined kernel. Few key blocks leave some waves of the shift pass
+    # with no block of their own; rows past L and rows with no admissible key must come out as in
+    # the oracle (empty rows: zero, the fused-kernel convention).
+    Q = _series((1, 2, L, 64), 2, 70, torch.float32)
+    K, V = (_series((1, 2, S, 64), 2, 71 + i, torch.float32) for i in range(2))
+    mask = None
+    if mode == "mask_with_empty_row":
+        g = torch.Generator().manual_seed(73)
+        mask = torch.rand(L, S, generator=g) < 0.6
+        mask[L // 2] = False
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=None if mask is None else mask.cuda(),
+               is_causal=mode == "causal")
+    want = oracle.attention([c.double() for c in Q], [c.double() for c in K], [c.double() for c in V],
+                            attn_mask=mask, is_causal=mode == "causal")
+    if mask is not None:   # the plain-range rule gives NaN on a row with no admissible key; the kernels 0
+        empty = ~mask.any(-1)
+        want = [torch.where(empty[:, None], torch.zeros_like(w), w) for w in want]
+        for c in out.coeffs:
+            assert torch.equal(c.cpu()[..., empty, :], torch.zeros_like(c.cpu()[..., empty, :]))
+    _check(out.coeffs, want, torch.float32)
+
+
 def test_scale_argument_and_default():
     shape = (1, 2, 40, 64)
     Q, K, V = (_series(shape, 3, 30 + i, torch.float64) for i in range(3))
