@@ -119,7 +119,47 @@ __global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __
   }
   __syncthreads();
   int lo = INT32_MAX, hi = -1;
-  if (b < nqb) {
+  // 16-byte reads where the rows allow them (S % 16 == 0, aligned mask): a chunk
+  // with any nonzero byte gives its first and last such byte from the four words
+  const bool vec = S % 16 == 0 && (reinterpret_cast<uintptr_t>(mask) & 15u) == 0;
+  auto chunk_bounds = [](const uint4 w, int& first, int& last) {
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+    first = 16;
+    last = -1;
+#pragma unroll
+    for (int i = 3; i >= 0; --i)
+      if (v[i] != 0) first = 4 * i + __builtin_ctz(v[i]) / 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (v[i] != 0) last = 4 * i + (31 - __builtin_clz(v[i])) / 8;
+  };
+  if (vec && b < nqb) {
+    const int r0 = b * kAttnRangeBlock, nr = min(kAttnRangeBlock, L - r0);
+    const int cpr = S / 16;   // chunks per row
+    for (int idx = threadIdx.x; idx < nr * cpr; idx += 256) {
+      const int r = idx / cpr, ch = idx % cpr;
+      const uint4 w = *reinterpret_cast<const uint4*>(mask + static_cast<int64_t>(r0 + r) * S + ch * 16);
+      int first, last;
+      chunk_bounds(w, first, last);
+      if (last >= 0) {
+        lo = min(lo, ch * 16 + first);
+        hi = max(hi, ch * 16 + last);
+      }
+    }
+  } else if (vec) {
+    // key block of 64 columns: four 16-byte chunks of each row (all inside S, as S % 16 == 0)
+    const int c0 = (b - nqb) * kAttnRangeBlock;
+    const int col0 = c0 + (threadIdx.x % 4) * 16;
+    if (col0 < S) {
+      for (int r = threadIdx.x / 4; r < L; r += 64) {
+        const uint4 w = *reinterpret_cast<const uint4*>(mask + static_cast<int64_t>(r) * S + col0);
+        if ((w.x | w.y | w.z | w.w) != 0) {
+          lo = min(lo, r);
+          hi = max(hi, r);
+        }
+      }
+    }
+  } else if (b < nqb) {
     const int r0 = b * kAttnRangeBlock, nr = min(kAttnRangeBlock, L - r0);
     for (int r = 0; r < nr; ++r) {
       const uint8_t* row = mask + static_cast<int64_t>(r0 + r) * S;

@@ -290,10 +290,16 @@ def _ranges_reference(mask, block=64):
     return out
 
 
-@pytest.mark.parametrize("L,S", [(150, 150), (64, 200), (300, 37), (1, 1)])
+@pytest.mark.parametrize("L,S", [(150, 150), (64, 200), (300, 37), (1, 1), (256, 320), (130, 208), (96, 272)])
 def test_mask_ranges_kernel(L, S):
+    # (S a multiple of 16: the kernel's 16-byte path; (96, 272): one admissible key per row, at a
+    # random column, so the first and last admissible byte of each chunk are checked exactly)
     g = torch.Generator().manual_seed(L + S)
-    mask = _window_mask(max(L, S), 23)[:L, :S] & (torch.rand(L, S, generator=g) > 0.3)
+    if (L, S) == (96, 272):
+        mask = torch.zeros(L, S, dtype=torch.bool)
+        mask[torch.arange(L), torch.randint(0, S, (L,), generator=g)] = True
+    else:
+        mask = _window_mask(max(L, S), 23)[:L, :S] & (torch.rand(L, S, generator=g) > 0.3)
     if L > 70:
         mask[64:128] = False          # a query block with no admissible key
     if S > 70:
