@@ -136,6 +136,7 @@ __global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __
   if (vec && b < nqb) {
     const int r0 = b * kAttnRangeBlock, nr = min(kAttnRangeBlock, L - r0);
     const int cpr = S / 16;   // chunks per row
+#pragma unroll 8
     for (int idx = threadIdx.x; idx < nr * cpr; idx += 256) {
       const int r = idx / cpr, ch = idx % cpr;
       const uint4 w = *reinterpret_cast<const uint4*>(mask + static_cast<int64_t>(r0 + r) * S + ch * 16);
@@ -151,6 +152,7 @@ __global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __
     const int c0 = (b - nqb) * kAttnRangeBlock;
     const int col0 = c0 + (threadIdx.x % 4) * 16;
     if (col0 < S) {
+#pragma unroll 8
       for (int r = threadIdx.x / 4; r < L; r += 64) {
         const uint4 w = *reinterpret_cast<const uint4*>(mask + static_cast<int64_t>(r) * S + col0);
         if ((w.x | w.y | w.z | w.w) != 0) {
