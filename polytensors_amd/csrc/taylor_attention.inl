@@ -90,12 +90,27 @@ struct AttnShape {
 // as the fast index gives every XCD an equal share of each query-block level
 // (the same eight-head residue class on each XCD, which also keeps its K/V
 // rows in that XCD's L2).
-__device__ __forceinline__ void attn_work_item(int L, int64_t& head, int& q_block) {
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup t to XCD t % 8),
+// each with its own L2. Causal: heads run fastest and the heaviest query blocks
+// go first across the whole grid, so the launch ends on light blocks. Otherwise
+// (query blocks of equal work), when the head count is a multiple of 8, XCD x
+// takes heads x, x + 8, ... one after another with all query blocks of a head
+// together, which then read the head's K/V rows from one L2 at about the same
+// time (1.7% faster on a sliding window; grouping causal blocks this way was
+// 8.5% slower, the XCDs ending on heavy blocks).
+constexpr int kXcds = 8;
+__device__ __forceinline__ void attn_work_item(int L, int causal, int64_t& head, int& q_block) {
   const int nqb = (L + kAttnBM - 1) / kAttnBM;
   const int64_t bh = gridDim.x / nqb;
   const int64_t t = blockIdx.x;
-  head = t % bh;
-  q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
+  if (!causal && bh % kXcds == 0) {
+    const int64_t j = t / kXcds;
+    head = t % kXcds + kXcds * (j / nqb);
+    q_block = (nqb - 1 - static_cast<int>(j % nqb)) * kAttnBM;   // last (in masks, often fullest) first
+  } else {
+    head = t % bh;
+    q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
+  }
 }
 
 // Block ranges of a boolean (L, S) mask, the reference's _mask_ranges
@@ -367,7 +382,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
   const int h = lane / 16;        // lane group
   int64_t head;
   int q_block;
-  attn_work_item(L, head, q_block);
+  attn_work_item(L, causal, head, q_block);
   const int q0 = q_block + wave * kAttnQPerWave;
   const int my_q = q0 + c;
   const bool q_ok = my_q < L;
@@ -680,7 +695,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
   const int h = lane / 16;
   int64_t head;
   int q_block;
-  attn_work_item(L, head, q_block);
+  attn_work_item(L, causal, head, q_block);
   const int q0_wave = q_block + wave * kAttnQPerWave;
   const int my_q = q0_wave + c;
   const bool q_ok = my_q < L;
