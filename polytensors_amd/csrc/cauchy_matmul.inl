@@ -54,6 +54,12 @@ void cauchy_matmul_kernel(
 
   __shared__ T As[AO][BM][LDK];
   __shared__ T Bs[BO][BN][LDK];
+  // B stored [Kd][N] (float): its tile is transposed into Bs by scalar writes, which
+  // with rows of LDK = BK + 4 values would fall 4 ways onto the same banks. The
+  // 16-byte chunks of row n are XOR-swizzled by (n / 16) % 4, which makes those
+  // writes and the 16-byte operand reads of 16 consecutive rows conflict-free.
+  constexpr bool kSwizzleB = !TRANS_B && sizeof(T) == 4 && BK / QV == 4;
+  auto bchunk = [](int n, int c) { return kSwizzleB ? (c ^ ((n >> 4) & 3)) : c; };
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -145,7 +151,7 @@ void cauchy_matmul_kernel(
         } else {
           const int kk = v / (BN / V), nv = (v % (BN / V)) * V;
 #pragma unroll
-          for (int e = 0; e < V; ++e) Bs[o][nv + e][kk] = rb[o][it].v[e];
+          for (int e = 0; e < V; ++e) Bs[o][nv + e][bchunk(nv + e, kk / QV) * QV + kk % QV] = rb[o][it].v[e];
         }
       }
   };
@@ -181,7 +187,8 @@ void cauchy_matmul_kernel(
       for (int o = 0; o < BO; ++o)
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn)
-          bv[o][fn] = *reinterpret_cast<const Vec<T, QV>*>(&Bs[o][col_b + fn * MF::N][kbase + q * QV]);
+          bv[o][fn] = *reinterpret_cast<const Vec<T, QV>*>(
+              &Bs[o][col_b + fn * MF::N][bchunk(col_b + fn * MF::N, kbase / QV + q) * QV]);
 #pragma unroll
       for (int ss = 0; ss < QV; ++ss) {
 #pragma unroll
