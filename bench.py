@@ -1,4 +1,4 @@
-"""Benchmark of the gfx950 truncated-Taylor kernels on BASELINE's configurations.
+"""Benchmark of the gfx950 truncated-Taylor kernels on benchmark configs 2-5 (shapes in each workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload attention|attention_window|attention_bwd|attention_bwd_window|matmul|norm|ce|
@@ -46,7 +46,7 @@ def _gen(seed, device):
 # Workloads: each returns a dict with the step closure and its algorithmic work.
 
 def wl_attention(device, dense_orders=False):
-    """B=4 H=16 L=2048 d=128, K=4, fp32, causal, scale 1/sqrt(128)."""
+    """benchmark config 3: B=4 H=16 L=2048 d=128, K=4, fp32, causal, scale 1/sqrt(128)."""
     import torch
     from polytensors_amd import _ops
 
@@ -177,7 +177,7 @@ def wl_attention_bwd_window(device):
 
 
 def wl_decoder(device):
-    """GPT-style decoder forward plus mean cross entropy in Taylor mode. 12 layers,
+    """benchmark config 5: GPT-style decoder forward plus mean cross entropy in Taylor mode. 12 layers,
     d_model 768, 12 heads, seq 1024, batch 8, vocab 32000, K=3; weights N(0, 0.02) (ordinary tensors:
     zero higher coefficients); a complex64 direction N(0,1) + i N(0,1) on the token embeddings."""
     import torch
@@ -206,7 +206,7 @@ def wl_decoder(device):
 
 
 def wl_matmul(device):
-    """A, B [5, 4096, 4096] fp32 (K=4), coefficient k scaled by 0.5^k."""
+    """benchmark config 2: A, B [5, 4096, 4096] fp32 (K=4), coefficient k scaled by 0.5^k."""
     import torch
     from polytensors_amd import _ops
 
@@ -226,7 +226,7 @@ def wl_matmul(device):
 
 
 def wl_norm(device):
-    """BASELINE config 4a: RMSNorm series x [5, 8192, 4096] bf16, eps 1e-6, weight 1+0.02 N(0,1)."""
+    """benchmark config 4a: RMSNorm series x [5, 8192, 4096] bf16, eps 1e-6, weight 1+0.02 N(0,1)."""
     import torch
     from polytensors_amd import _ops
 
@@ -246,7 +246,7 @@ def wl_norm(device):
 
 
 def wl_ce(device):
-    """BASELINE config 4b: logits [5, 8192, 32000] fp32, base N(0,2^2), order k N(0,1) 0.5^k, mean."""
+    """benchmark config 4b: logits [5, 8192, 32000] fp32, base N(0,2^2), order k N(0,1) 0.5^k, mean."""
     import torch
     from polytensors_amd import _ops
 

@@ -1,7 +1,7 @@
 """Writes tests/golden/known_answers.json: known-answer vectors for the series path.
 
 Inputs are the fixed data of the reference's own tests (cited per case) or
-BASELINE config 1's seeded inputs; expected outputs are independent Taylor
+benchmark config 1's seeded inputs; expected outputs are independent Taylor
 coefficients from nested ``torch.func.jvp`` (tests/jets.py) in float64, or the
 closed-form answers those tests assert. Nothing here imports or runs the
 reference. Run from the repository root:
@@ -41,7 +41,7 @@ def math_attention(q, k, v, excluded=None, is_causal=False, scale=None):
 
 
 def config1_inputs():
-    """BASELINE config 1 (seed 0, float64): Q/K/V = x + t v with x, v ~ N(0,1)/8, W ~ N(0,1)/8."""
+    """benchmark config 1 (seed 0, float64): Q/K/V = x + t v with x, v ~ N(0,1)/8, W ~ N(0,1)/8."""
     g = torch.Generator().manual_seed(0)
     shape = (1, 1, 128, 64)
     lines = [(torch.randn(shape, generator=g, dtype=torch.float64) / 8,
@@ -109,7 +109,7 @@ def main():
         "v": [enc(values[2]), enc(directions[2])],
         "expected_rows_1_2": [enc(c[..., 1:, :]) for c in at]}
 
-    # causal attention, logits = out.view(128, 64) @ W, mean cross entropy, degree 3.
+    # benchmark config 1: causal attention, logits = out.view(128, 64) @ W, mean cross entropy, degree 3.
     # The inputs are regenerated from the seed; their checksums guard against generator drift.
     lines, W, y = config1_inputs()
     def loss_fn(q, k, v):

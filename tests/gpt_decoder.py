@@ -1,4 +1,4 @@
-"""GPT-style decoder of BASELINE config 5, as a workload and a parity case (test helper).
+"""GPT-style decoder of benchmark config 5, as a workload and a parity case (test helper).
 
 ``forward`` is written with ordinary torch.nn.functional calls (layer_norm,
 linear, scaled_dot_product_attention, gelu, cross_entropy); given PolyTensor

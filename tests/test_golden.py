@@ -1,6 +1,6 @@
 """The CPU oracle against the committed known-answer vectors (tests/golden/known_answers.json).
 
-The vectors hold the fixed inputs of the reference's own tests (and BASELINE
+The vectors hold the fixed inputs of the reference's own tests (and benchmark
 config 1's seeded inputs) with expected coefficients from nested forward-mode
 AD; tests/golden/make_known_answers.py writes them. The GPU kernels are checked
 against the same file in tests/test_gpu_golden.py.

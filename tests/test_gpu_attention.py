@@ -193,7 +193,7 @@ def test_lse_series_output():
 
 
 def test_config1_fp64_attention_and_projected_cross_entropy():
-    # K=3, fp64, Q/K/V [1,1,128,64] = x + t v with x, v ~ N(0,1)/8 (seed 0), causal;
+    # benchmark config 1: K=3, fp64, Q/K/V [1,1,128,64] = x + t v with x, v ~ N(0,1)/8 (seed 0), causal;
     # logits = out.view(128, 64) @ W with W ~ N(0,1)/8 [64, 256], integer targets in [0, 256), mean CE.
     g = torch.Generator().manual_seed(0)
     shape = (1, 1, 128, 64)
@@ -217,7 +217,7 @@ def test_config1_fp64_attention_and_projected_cross_entropy():
 
 
 def test_full_size_config3_one_head():
-    # B=4 H=16 L=2048 d=128, K=4, fp32, causal; line inputs (x + t v). One (b, h) of
+    # benchmark config 3: B=4 H=16 L=2048 d=128, K=4, fp32, causal; line inputs (x + t v). One (b, h) of
     # the full launch is checked against the oracle; every head's order-0 output is checked against
     # torch's own fp32 attention (the ordinary softmax attention that order 0 equals).
     B, H, L, d, degree = 4, 16, 2048, 128, 4

@@ -196,7 +196,7 @@ def test_float64_materialize_is_refused():
 
 
 def test_full_size_config3_backward():
-    # BASELINE config 3 shape (B=4 H=16 L=2048 d=128, K=4, fp32, causal) with line inputs and a
+    # benchmark config 3 shape (B=4 H=16 L=2048 d=128, K=4, fp32, causal) with line inputs and a
     # random cotangent series: one head against the oracle; on every head, linearity in the
     # cotangent (bwd(G1 + G2) = bwd(G1) + bwd(G2)), a size-independent property.
     B, H, L, d, degree = 4, 16, 2048, 128, 4

@@ -139,7 +139,7 @@ def test_known_answer_real_analog():
 
 
 def test_full_size_config_sampled_rows():
-    # A, B [5, 4096, 4096] fp32, coefficient k scaled by 0.5^k. Rows of C are checked
+    # benchmark config 2: A, B [5, 4096, 4096] fp32, coefficient k scaled by 0.5^k. Rows of C are checked
     # on a seeded sample; the full product's linearity is checked through C(A + A') = C(A) + C(A').
     degree, n = 4, 4096
     g = torch.Generator(device="cuda").manual_seed(1)

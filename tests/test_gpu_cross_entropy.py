@@ -115,7 +115,7 @@ def test_large_common_offset_keeps_higher_orders_exact():
 
 
 def test_full_size_config_rows_sample():
-    # BASELINE config 4b: [5, 8192, 32000] fp32, base N(0, 2^2), order k N(0,1) 0.5^k; the mean must
+    # benchmark config 4b: [5, 8192, 32000] fp32, base N(0, 2^2), order k N(0,1) 0.5^k; the mean must
     # equal the mean of the per-row losses, and a seeded sample of rows must match the oracle.
     degree, N, C = 4, 8192, 32000
     g = torch.Generator(device="cuda").manual_seed(4)

@@ -1,7 +1,7 @@
 """The gfx950 kernels against the committed known-answer vectors (tests/golden/known_answers.json).
 
 Each case runs through the PolyTensor API on the GPU in float64 (the reference's
-fixed test data) and is compared with the stored expected
+fixed test data, benchmark config 1) and is compared with the stored expected
 coefficients at 1e-10 relative to each order's largest value. The attention
 case pads the head dim from 2 to 16 with zeros (the kernels take 16..128; zero
 columns change neither the scores nor the kept output columns) and, as the

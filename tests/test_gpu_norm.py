@@ -146,7 +146,7 @@ def test_noncontiguous_input_and_rows_from_a_stacked_buffer():
 
 
 def test_full_size_config_rows_sample():
-    # BASELINE config 4a: [5, 8192, 4096] bf16, eps 1e-6, weight 1 + 0.02 N(0,1). Checked on a
+    # benchmark config 4a: [5, 8192, 4096] bf16, eps 1e-6, weight 1 + 0.02 N(0,1). Checked on a
     # seeded sample of rows against the oracle, and for the row mean-square identity of order 0.
     degree, rows, n = 4, 8192, 4096
     g = torch.Generator().manual_seed(3)
