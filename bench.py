@@ -43,6 +43,66 @@ def _gen(seed, device):
 
 
 # ---------------------------------------------------------------------------
+# The config-5 network: a GPT-style decoder written with ordinary torch.nn.functional
+# calls (layer_norm, linear, scaled_dot_product_attention, gelu, cross_entropy). Given
+# PolyTensor hidden states it runs the whole forward plus loss in Taylor mode through
+# polytensors_amd's kernels. Pre-LayerNorm blocks with tanh-GELU MLPs (GPT-2 layout) and
+# an untied head; weights N(0, 0.02) are ordinary tensors (zero higher coefficients).
+
+def gpt_init_params(layers, d, vocab, seq, seed=0, device="cpu", dtype=None):
+    import torch
+
+    dtype = torch.float32 if dtype is None else dtype
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def normal(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=dtype) * 0.02
+
+    def zeros(*shape):
+        return torch.zeros(*shape, device=device, dtype=dtype)
+
+    def ones(*shape):
+        return torch.ones(*shape, device=device, dtype=dtype)
+
+    blocks = [dict(ln1_w=ones(d), ln1_b=zeros(d), attn_w=normal(3 * d, d), attn_b=zeros(3 * d),
+                   proj_w=normal(d, d), proj_b=zeros(d), ln2_w=ones(d), ln2_b=zeros(d),
+                   fc_w=normal(4 * d, d), fc_b=zeros(4 * d), fc2_w=normal(d, 4 * d), fc2_b=zeros(d))
+              for _ in range(layers)]
+    return dict(blocks=blocks, wte=normal(vocab, d), wpe=normal(seq, d), lnf_w=ones(d), lnf_b=zeros(d),
+                head=normal(vocab, d))
+
+
+def gpt_embed(params, tokens):
+    """Token plus position embeddings (ordinary tensors): the base of the perturbed series."""
+    return params["wte"][tokens] + params["wpe"][: tokens.shape[1]]
+
+
+def gpt_forward(params, x, targets, heads, attention=None):
+    """Mean next-token cross entropy of hidden states x [B, T, d] (a PolyTensor in Taylor mode).
+
+    ``attention(q, k, v, is_causal=True)`` defaults to F.scaled_dot_product_attention
+    (tests pass a math version to differentiate).
+    """
+    import torch.nn.functional as F
+
+    attention = F.scaled_dot_product_attention if attention is None else attention
+    B, T, d = x.shape
+    hd = d // heads
+    for blk in params["blocks"]:
+        h = F.layer_norm(x, (d,), blk["ln1_w"], blk["ln1_b"])
+        q, k, v = F.linear(h, blk["attn_w"], blk["attn_b"]).split(d, dim=-1)
+        q, k, v = (t.reshape(B, T, heads, hd).transpose(1, 2) for t in (q, k, v))
+        y = attention(q, k, v, is_causal=True)
+        x = x + F.linear(y.transpose(1, 2).reshape(B, T, d), blk["proj_w"], blk["proj_b"])
+        h = F.layer_norm(x, (d,), blk["ln2_w"], blk["ln2_b"])
+        h = F.gelu(F.linear(h, blk["fc_w"], blk["fc_b"]), approximate="tanh")
+        x = x + F.linear(h, blk["fc2_w"], blk["fc2_b"])
+    x = F.layer_norm(x, (d,), params["lnf_w"], params["lnf_b"])
+    logits = F.linear(x, params["head"])
+    return F.cross_entropy(logits.reshape(B * T, -1), targets.reshape(-1))
+
+
+# ---------------------------------------------------------------------------
 # Workloads: each returns a dict with the step closure and its algorithmic work.
 
 def wl_attention(device, dense_orders=False):
@@ -182,21 +242,20 @@ def wl_decoder(device):
     zero higher coefficients); a complex64 direction N(0,1) + i N(0,1) on the token embeddings."""
     import torch
     from polytensors_amd import PolyTensor
-    from tests import gpt_decoder
 
     layers, d, heads, vocab, batch, seq, K = 12, 768, 12, 32000, 8, 1024, 3
-    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=10, device=device)
+    params = gpt_init_params(layers, d, vocab, seq, seed=10, device=device)
     g = _gen(11, device)
     tokens = torch.randint(0, vocab, (batch, seq), generator=g, device=device)
     targets = torch.randint(0, vocab, (batch, seq), generator=g, device=device)
-    base = gpt_decoder.embed(params, tokens)
+    base = gpt_embed(params, tokens)
     direction = torch.complex(torch.randn(batch, seq, d, generator=g, device=device),
                               torch.randn(batch, seq, d, generator=g, device=device))
 
     def step():
         with torch.no_grad(), PolyTensor.plain_range():
             x = PolyTensor((base, direction), degree=K)
-            return gpt_decoder.forward(params, x, targets, heads)
+            return gpt_forward(params, x, targets, heads)
 
     return dict(step=step, work=batch * seq, unit="tokens/s", bound=None, peak=None, bytes=None,
                 kernel="gpt_decoder", dtype="fp32 (complex64 directions)",
@@ -410,16 +469,16 @@ def cpu_attention_bwd(L, d, K, heads=16, window=None):
 
 def cpu_decoder(layers, d, heads, vocab, K, seq=64):
     import torch
-    from tests import gpt_decoder
+    import oracle
 
-    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=10)
+    params = gpt_init_params(layers, d, vocab, seq, seed=10)
     g = torch.Generator().manual_seed(11)
     tokens = torch.randint(0, vocab, (1, seq), generator=g)
     targets = torch.randint(0, vocab, (1, seq), generator=g)
-    base = gpt_decoder.embed(params, tokens)
+    base = gpt_embed(params, tokens)
     direction = torch.complex(torch.randn(1, seq, d, generator=g), torch.randn(1, seq, d, generator=g))
     X = [base, direction] + [torch.zeros(1, seq, d, dtype=torch.complex64) for _ in range(K - 1)]
-    t = _cpu_time(lambda: gpt_decoder.oracle_forward(params, X, targets, heads), reps=1)
+    t = _cpu_time(lambda: oracle.gpt_forward(params, X, targets, heads), reps=1)
     return dict(value=seq / t, unit="tokens/s", seconds=t,
                 sample=f"one sequence of {seq} tokens (attention cost grows with seq), full width, K={K} complex64")
 

@@ -20,3 +20,4 @@ from .series import cauchy, exp_series, log_series, quotient, rsqrt_series, soft
 from .paths import attention, cross_entropy, layer_norm, layer_norm_backward, matmul, rms_norm  # noqa: F401
 from .paths import attention_backward, cross_entropy_backward, rms_norm_backward  # noqa: F401
 from .activations import activation, activation_backward  # noqa: F401
+from .decoder import gpt_forward  # noqa: F401

@@ -57,9 +57,16 @@ def eligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, 
 
 
 def _rows(coeffs):
-    """Coefficients whose rows are unit-stride with one common row stride (a padded slice is fine)."""
+    """Coefficients whose rows are unit-stride with one common row stride (a padded slice is fine).
+
+    Rows that overlap (a row stride below the row length, such as the stride 0
+    of an expanded row) are made contiguous: the kernels read rows at
+    ``row_stride >= classes`` apart.
+    """
     first = coeffs[0]
-    if first.stride(-1) == 1 and all(c.stride() == first.stride() for c in coeffs):
+    rows, classes = first.shape
+    if (first.stride(-1) == 1 and (rows <= 1 or first.stride(0) >= classes)
+            and all(c.stride() == first.stride() for c in coeffs)):
         return list(coeffs)
     return [c.contiguous() for c in coeffs]
 

@@ -326,3 +326,10 @@ def test_sliding_window_skips_blocks(dtype):
         keep = torch.ones(L, dtype=torch.bool)
         keep[256:320] = False
         assert rel_err(a[..., keep, :], b[..., keep, :]) <= TOL[dtype], k
+
+
+def test_float64_head_dim_128_beyond_lds_is_refused_with_a_reason():
+    q = _poly(_series((1, 1, 32, 128), 4, seed=40, dtype=torch.float64))
+    assert not _fused_attention.eligible(q, q, q, is_causal=True)
+    with pytest.raises(NotImplementedError, match="LDS"):
+        _run(q, q, q, is_causal=True)

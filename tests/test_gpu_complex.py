@@ -7,7 +7,7 @@ interpolating at i, or by splitting bilinear products into real and imaginary
 parts (polytensors_amd/_complex.py). The oracle instead runs the reference's
 recurrences in complex arithmetic (complex128 on upcast inputs), so agreement
 pins both. Every fused operation is covered, plus the config-5 GPT decoder
-(tests/gpt_decoder.py) at reduced size, at full width, and at full size through
+(bench.gpt_forward) at reduced size, at full width, and at full size through
 properties. Per-order tolerance max|got - want| / max|want|: 1e-10 complex128,
 1e-4 complex64.
 """
@@ -20,7 +20,7 @@ import torch.nn.functional as F
 
 import oracle
 from polytensors_amd import PolyTensor
-from tests import gpt_decoder
+import bench
 from tests.jets import rel_err
 
 pytestmark = pytest.mark.gpu
@@ -189,11 +189,11 @@ def test_complex_base_and_reverse_mode_are_refused():
 
 
 def _decoder_case(layers, d, heads, vocab, batch, seq, degree, seed):
-    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=seed, dtype=torch.float64)
+    params = bench.gpt_init_params(layers, d, vocab, seq, seed=seed, dtype=torch.float64)
     g = torch.Generator().manual_seed(seed + 1)
     tokens = torch.randint(0, vocab, (batch, seq), generator=g)
     targets = torch.randint(0, vocab, (batch, seq), generator=g)
-    base = gpt_decoder.embed(params, tokens)
+    base = bench.gpt_embed(params, tokens)
     direction = torch.complex(torch.randn(batch, seq, d, generator=g, dtype=torch.float64),
                               torch.randn(batch, seq, d, generator=g, dtype=torch.float64))
     return params, base, direction, targets
@@ -207,7 +207,7 @@ def _decoder_gpu(params, base, direction, targets, heads, degree, dtype):
         gp[k] = params[k].to(dtype).cuda()
     with torch.no_grad(), PolyTensor.plain_range():
         x = PolyTensor((base.to(dtype).cuda(), direction.to(cdt).cuda()), degree=degree)
-        return gpt_decoder.forward(gp, x, targets.cuda(), heads)
+        return bench.gpt_forward(gp, x, targets.cuda(), heads)
 
 
 def _decoder_oracle(params, base, direction, targets, heads, degree, dtype):
@@ -218,7 +218,7 @@ def _decoder_oracle(params, base, direction, targets, heads, degree, dtype):
     for k in ("wte", "wpe", "lnf_w", "lnf_b", "head"):
         op[k] = up(params[k])
     X = [up(base), up(direction)] + [torch.zeros(base.shape, dtype=torch.complex128) for _ in range(degree - 1)]
-    return gpt_decoder.oracle_forward(op, X, targets, heads)
+    return oracle.gpt_forward(op, X, targets, heads)
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -250,24 +250,24 @@ def test_decoder_config5_full_size_properties():
     # order 1 is linear in the direction: loss_1(u + i w) = loss_1(u) + i loss_1(w) with the
     # real-direction runs computed separately
     layers, d, heads, vocab, batch, seq, degree = 12, 768, 12, 32000, 8, 1024, 3
-    params = gpt_decoder.init_params(layers, d, vocab, seq, seed=5, device="cuda")
+    params = bench.gpt_init_params(layers, d, vocab, seq, seed=5, device="cuda")
     g = torch.Generator(device="cuda").manual_seed(6)
     tokens = torch.randint(0, vocab, (batch, seq), generator=g, device="cuda")
     targets = torch.randint(0, vocab, (batch, seq), generator=g, device="cuda")
-    base = gpt_decoder.embed(params, tokens)
+    base = bench.gpt_embed(params, tokens)
     u = torch.randn(batch, seq, d, generator=g, device="cuda")
     w = torch.randn(batch, seq, d, generator=g, device="cuda")
     with torch.no_grad(), PolyTensor.plain_range():
-        z = gpt_decoder.forward(params, PolyTensor((base, torch.complex(u, w)), degree=degree), targets, heads)
-        zu = gpt_decoder.forward(params, PolyTensor((base, u), degree=degree), targets, heads)
-        zw = gpt_decoder.forward(params, PolyTensor((base, w), degree=degree), targets, heads)
-        plain = gpt_decoder.forward(params, base, targets, heads)
+        z = bench.gpt_forward(params, PolyTensor((base, torch.complex(u, w)), degree=degree), targets, heads)
+        zu = bench.gpt_forward(params, PolyTensor((base, u), degree=degree), targets, heads)
+        zw = bench.gpt_forward(params, PolyTensor((base, w), degree=degree), targets, heads)
+        plain = bench.gpt_forward(params, base, targets, heads)
     assert math.isfinite(z.coeffs[0].item()) and abs(z.coeffs[0].item() - plain.item()) <= 1e-4 * abs(plain.item())
     first = complex(zu.coeffs[1].item(), zw.coeffs[1].item())
     assert abs(z.coeffs[1].item() - first) <= 1e-4 * abs(first)
     # a real computation has conjugate-symmetric coefficients: loss_k(u - i w) = conj(loss_k(u + i w))
     with torch.no_grad(), PolyTensor.plain_range():
-        zc = gpt_decoder.forward(params, PolyTensor((base, torch.complex(u, -w)), degree=degree), targets, heads)
+        zc = bench.gpt_forward(params, PolyTensor((base, torch.complex(u, -w)), degree=degree), targets, heads)
     for k in range(1, degree + 1):
         a, b = zc.coeffs[k].item(), z.coeffs[k].item().conjugate()
         assert abs(a - b) <= 1e-4 * max(abs(b), 1e-30), k

@@ -172,3 +172,18 @@ def test_softcap_must_be_positive():
     with torch.no_grad(), PolyTensor.plain_range():
         with pytest.raises(NotImplementedError, match="softcap"):
             PolyTensor.cross_entropy(PolyTensor(tuple(c.cuda() for c in Z)), y.cuda(), softcap=-1.0)
+
+
+def test_expanded_logits_rows_are_materialized():
+    # an expanded (broadcast) row has row stride 0; the glue must copy it rather than hand the
+    # kernel overlapping rows
+    degree = 2
+    g = torch.Generator().manual_seed(5)
+    row = [torch.randn(1, 300, generator=g, dtype=torch.float64).mul(0.5 ** k).float() for k in range(degree + 1)]
+    y = torch.randint(0, 300, (6,), generator=g)
+    logits = PolyTensor(tuple(c.cuda().expand(6, 300) for c in row))
+    assert logits.coeffs[0].stride(0) == 0
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = F.cross_entropy(logits, y.cuda(), reduction="none")
+    want = oracle.cross_entropy([c.double().expand(6, 300) for c in row], y, reduction="none")
+    _check(loss.coeffs, want, torch.float32)

@@ -471,18 +471,18 @@ def test_complex_direction_attention_norm_activation_ce():
 
 
 def test_decoder_oracle_matches_complex_jets(monkeypatch):
-    # the config-5 network (tests/gpt_decoder.py) at toy size: the oracle composite with a complex
+    # the config-5 network (bench.gpt_forward) at toy size: the oracle composite with a complex
     # embedding direction vs mixed real partials of the same network (math attention)
-    from tests import gpt_decoder
+    import bench
     from tests.jets import taylor_complex
 
     degree, d, heads, vocab, seq = 3, 16, 2, 11, 5
-    params = gpt_decoder.init_params(2, d, vocab, seq, seed=3, dtype=torch.float64)
+    params = bench.gpt_init_params(2, d, vocab, seq, seed=3, dtype=torch.float64)
     params["blocks"][0]["ln1_w"] = params["blocks"][0]["ln1_w"] + 0.1   # non-trivial affine terms
     g = torch.Generator().manual_seed(4)
     tokens = torch.randint(0, vocab, (1, seq), generator=g)
     targets = torch.randint(0, vocab, (1, seq), generator=g)
-    base = gpt_decoder.embed(params, tokens)
+    base = bench.gpt_embed(params, tokens)
     u, w = (torch.randn(base.shape, generator=g, dtype=torch.float64) for _ in range(2))
 
     def math_sdpa(q, k, v, is_causal):
@@ -490,7 +490,7 @@ def test_decoder_oracle_matches_complex_jets(monkeypatch):
         return _math_attention(q, k, v, excluded=~torch.ones(L, L, dtype=torch.bool).tril())
 
     monkeypatch.setattr(F, "layer_norm", _composite_layer_norm)
-    got = gpt_decoder.oracle_forward(params, _line_series(base, u, w, degree), targets, heads)
-    want = taylor_complex(lambda x: gpt_decoder.forward(params, x, targets, heads, attention=math_sdpa),
+    got = oracle.gpt_forward(params, _line_series(base, u, w, degree), targets, heads)
+    want = taylor_complex(lambda x: bench.gpt_forward(params, x, targets, heads, attention=math_sdpa),
                           [base], [u], [w], degree)
     _check_complex(got, want, 1e-10)

@@ -171,3 +171,14 @@ def test_plain_tensor_cross_entropy_with_softcap_matches_composite():
     y = torch.randint(0, 50, (10,))
     expected = F.cross_entropy(15 * torch.tanh(z / 15), y)
     assert torch.allclose(PolyTensor.cross_entropy(z, y, softcap=15.0), expected)
+
+
+def test_attention_lds_budget_gate():
+    # float64 at head dim 128 stages 16 keys of every order of K and V in LDS: degree 3 fits
+    # the 160 KiB budget, degree 4 does not; float32 fits at every degree up to 8.
+    from polytensors_amd._fused_attention import _tiles_fit_lds
+
+    assert _tiles_fit_lds(torch.float64, 128, 3)
+    assert not _tiles_fit_lds(torch.float64, 128, 4)
+    assert _tiles_fit_lds(torch.float64, 64, 8)
+    assert all(_tiles_fit_lds(torch.float32, d, 8) for d in (16, 32, 64, 128))
