@@ -1,14 +1,17 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on benchmark configs 2-5 (shapes in each workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|attention_window|attention_bwd|attention_bwd_window|matmul|norm|ce|
-                                activation|norm_bwd|ce_bwd|decoder]
+                    [--workload attention|attention_dense|attention_window|attention_bwd|attention_bwd_window|
+                                matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
 One step is one launch of the workload's fused kernel on one batch of synthetic
 input already resident in HBM (inputs are generated on the device with a
-seeded generator before the timed region). The timed region is K back-to-back
+seeded generator before the timed region). The launch-bound ``config1``
+workload (benchmark config 1) times its whole pipeline through the PolyTensor
+API per step, and again as the replay of a HIP graph holding one step
+(``graph``: ms per replay and the graph's kernel count, the launches per step). The timed region is K back-to-back
 steps on the current stream, bracketed by torch.cuda.synchronize() and timed
 with HIP events on that stream; ``value`` is the workload's throughput and
 ``roofline`` compares it to MI355X's published peak (fp32 MFMA 157.3 TFLOP/s,
@@ -264,6 +267,46 @@ def wl_decoder(device):
                 cpu=lambda: cpu_decoder(layers, d, heads, vocab, K))
 
 
+def wl_attention_dense(device):
+    """Config 3 with dense random orders 2..4 (N(0,1) 0.5^k) instead of a line: the same kernel
+    and work count, with no zero input orders."""
+    w = wl_attention(device, dense_orders=True)
+    w["kernel"] = "taylor_attention_dense"
+    return w
+
+
+def wl_config1(device):
+    """benchmark config 1: degree-3 fp64 causal attention on Q, K, V [1,1,128,64] (x + t v with x, v
+    ~ N(0,1)/8, seed 0, scale 1/8), logits = out.view(128, 64) @ W with W ~ N(0,1)/8 [64, 256], mean
+    cross entropy over 256 classes. One step is that whole pipeline through the PolyTensor API
+    (F.scaled_dot_product_attention, @, F.cross_entropy): launch-bound, so the step is also captured
+    in a HIP graph and replayed (``graph``)."""
+    import torch
+    import torch.nn.functional as F
+    from polytensors_amd import PolyTensor
+
+    K, L, d, C = 3, 128, 64, 256
+    g = torch.Generator().manual_seed(0)   # the seeded CPU inputs of the parity test, copied to the device
+    lines = [(torch.randn(1, 1, L, d, generator=g, dtype=torch.float64) / 8,
+              torch.randn(1, 1, L, d, generator=g, dtype=torch.float64) / 8) for _ in range(3)]
+    W = (torch.randn(d, C, generator=g, dtype=torch.float64) / 8).to(device)
+    y = torch.randint(0, C, (L,), generator=g).to(device)
+    q, k, v = (PolyTensor((x.to(device), u.to(device)), degree=K) for x, u in lines)
+
+    def step():
+        with torch.no_grad(), PolyTensor.plain_range():
+            out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            logits = out.reshape(L, d) @ W
+            return F.cross_entropy(logits, y)
+
+    pairs = (K + 1) * (K + 2) // 2
+    flops = 2 * pairs * 2 * d * L * (L + 1) / 2 + 2 * (K + 1) * L * d * C   # attention + series @ plain W
+    return dict(step=step, work=None, unit="ms", bound=None, peak=None, bytes=None, graph=True,
+                flops=flops, kernel="config1", dtype="fp64",
+                workload=f"config1: taylor attention [1,1,{L},{d}] K={K} fp64 causal -> @ W [{d},{C}] -> mean CE",
+                cpu=lambda: cpu_config1(L, d, C, K))
+
+
 def wl_matmul(device):
     """benchmark config 2: A, B [5, 4096, 4096] fp32 (K=4), coefficient k scaled by 0.5^k."""
     import torch
@@ -391,6 +434,7 @@ WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "c
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
              "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
              "attention_bwd_window": wl_attention_bwd_window,
+             "attention_dense": wl_attention_dense, "config1": wl_config1,
              "decoder": wl_decoder}
 
 
@@ -481,6 +525,28 @@ def cpu_decoder(layers, d, heads, vocab, K, seq=64):
     t = _cpu_time(lambda: oracle.gpt_forward(params, X, targets, heads), reps=1)
     return dict(value=seq / t, unit="tokens/s", seconds=t,
                 sample=f"one sequence of {seq} tokens (attention cost grows with seq), full width, K={K} complex64")
+
+
+def cpu_config1(L, d, C, K):
+    import torch
+    import oracle
+    from oracle import paths
+
+    g = torch.Generator().manual_seed(0)
+    lines = [(torch.randn(1, 1, L, d, generator=g, dtype=torch.float64) / 8,
+              torch.randn(1, 1, L, d, generator=g, dtype=torch.float64) / 8) for _ in range(3)]
+    W = torch.randn(d, C, generator=g, dtype=torch.float64) / 8
+    y = torch.randint(0, C, (L,), generator=g)
+    Q, Kk, V = (paths.lift([x, u], K) for x, u in lines)
+
+    def pipeline():
+        out = oracle.attention(Q, Kk, V, is_causal=True)
+        logits = oracle.matmul([o.reshape(L, d) for o in out], [W])
+        return oracle.cross_entropy(logits, y)
+
+    reps = 20
+    t = _cpu_time(lambda: [pipeline() for _ in range(reps)], reps=3) / reps
+    return dict(value=t * 1e3, unit="ms", sample=f"the whole config-1 pipeline, {reps} runs per timing", seconds=t * reps)
 
 
 def cpu_matmul(n, K):
@@ -643,6 +709,49 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
     return entry
 
 
+def graph_nodes(graph):
+    """Node counts by type of a captured HIP graph (hipGraphGetNodes / hipGraphNodeGetType on the
+    runtime torch loaded): {"kernel": n, "memset": n, ...}."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    raw = ctypes.c_void_p(graph.raw_cuda_graph())
+    count = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(raw, None, ctypes.byref(count)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * max(1, count.value))()
+    if hip.hipGraphGetNodes(raw, nodes, ctypes.byref(count)) != 0:
+        return None
+    names = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty"}
+    kinds = {}
+    for i in range(count.value):
+        kind = ctypes.c_int(-1)
+        hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kind))
+        name = names.get(kind.value, f"type{kind.value}")
+        kinds[name] = kinds.get(name, 0) + 1
+    return kinds
+
+
+def graph_replay(step, steps, warmup):
+    """The step captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed: ms per replay,
+    the graph's node counts, and whether the last replay reproduces the eager result bit for bit.
+    A graph holding memset nodes is not timed (such nodes have given wrong results on replay)."""
+    import torch
+
+    eager = step()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        captured = step()
+    nodes = graph_nodes(graph)
+    graph.instantiate()
+    if nodes is None or nodes.get("memset", 0):
+        return {"nodes": nodes, "ms": None, "matches_eager": None}
+    ms = time_steps(graph.replay, steps, warmup)
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(eager.coeffs, captured.coeffs))
+    return {"nodes": nodes, "ms": ms, "matches_eager": same}
+
+
 def measure(name, device, steps, warmup, min_seconds=0.0):
     """Time ``steps`` steps (raised so the timed region lasts at least ``min_seconds``)."""
     w = WORKLOADS[name](device)
@@ -652,9 +761,14 @@ def measure(name, device, steps, warmup, min_seconds=0.0):
         warmup = 1
     ms = time_steps(w["step"], steps, warmup)
     w["steps"] = steps
-    scale = {"TFLOP/s": 1e12, "GB/s": 1e9}.get(w["unit"], 1.0)
-    achieved = w["work"] / (ms * 1e-3) / scale
+    if w["unit"] == "ms":   # launch-bound workloads report time per step
+        achieved = ms
+    else:
+        scale = {"TFLOP/s": 1e12, "GB/s": 1e9}.get(w["unit"], 1.0)
+        achieved = w["work"] / (ms * 1e-3) / scale
     w.update(ms=ms, achieved=achieved)
+    if w.get("graph"):
+        w["graph_result"] = graph_replay(w["step"], steps, warmup)
     return w
 
 
@@ -697,7 +811,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(w["ms"], 4),
-        "higher_is_better": True,
+        "higher_is_better": w["unit"] != "ms",
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": w["dtype"],
@@ -711,6 +825,10 @@ def main():
         ceil = stream_ceiling(device, w["pattern"], w["bytes"])
         ceil["frac"] = round(w["achieved"] / ceil["rate"], 4)
         line["roofline"]["stream_ceiling"] = ceil
+    if "graph_result" in w:
+        gr = w["graph_result"]
+        line["graph"] = {"ms": round(gr["ms"], 4) if gr["ms"] is not None else None, "nodes": gr["nodes"],
+                         "matches_eager": gr["matches_eager"], "launches_per_step": (gr["nodes"] or {}).get("kernel")}
     cpu_samplers = {}
     if not args.no_components:
         comps = {}
@@ -722,6 +840,11 @@ def main():
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
                            "frac": round(c["achieved"] / c["peak"], 4) if c["peak"] else None,
                            "traffic": profiled_traffic(c["kernel"]) if c["peak"] else None}
+            if "graph_result" in c:
+                gr = c["graph_result"]
+                comps[name]["graph"] = {"ms": round(gr["ms"], 4) if gr["ms"] is not None else None,
+                                        "nodes": gr["nodes"], "matches_eager": gr["matches_eager"],
+                                        "launches_per_step": (gr["nodes"] or {}).get("kernel")}
             if c["bound"] == "hbm" and not args.no_ceiling:
                 ceil = stream_ceiling(device, c["pattern"], c["bytes"])
                 ceil["frac"] = round(c["achieved"] / ceil["rate"], 4)

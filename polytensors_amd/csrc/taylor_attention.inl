@@ -43,10 +43,10 @@ struct Mfma16<float> {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
   // accumulator register r of lane l: row 4 (l/16) + r, column l % 16
-  __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * h + r; }
+  __host__ __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * h + r; }
   // the lane group and register holding row i
-  __device__ __forceinline__ static int row_group(int i) { return i / 4; }
-  __device__ __forceinline__ static int row_reg(int i) { return i % 4; }
+  __host__ __device__ __forceinline__ static int row_group(int i) { return i / 4; }
+  __host__ __device__ __forceinline__ static int row_reg(int i) { return i % 4; }
 };
 
 template <>
@@ -57,9 +57,9 @@ struct Mfma16<double> {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
   }
   // accumulator register r of lane l: row 4 r + l/16, column l % 16
-  __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * r + h; }
-  __device__ __forceinline__ static int row_group(int i) { return i % 4; }
-  __device__ __forceinline__ static int row_reg(int i) { return i / 4; }
+  __host__ __device__ __forceinline__ static int acc_row(int h, int r) { return 4 * r + h; }
+  __host__ __device__ __forceinline__ static int row_group(int i) { return i % 4; }
+  __host__ __device__ __forceinline__ static int row_reg(int i) { return i / 4; }
 };
 
 constexpr int kAttnWaves = 4;
@@ -219,16 +219,17 @@ __global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __
 }
 
 // Key range [lo, hi) a query workgroup visits: causal and mask-range bounds,
-// lo rounded down to a key block.
-__device__ __forceinline__ void attn_key_range(int S, int q_block, int causal, const int32_t* ranges, int& lo,
-                                               int& hi) {
+// lo rounded down to a key block. (Host-callable: the index checks replay it.)
+__host__ __device__ __forceinline__ void attn_key_range(int S, int q_block, int causal, const int32_t* ranges,
+                                                        int& lo, int& hi) {
   lo = 0;
   hi = S;
-  if (causal) hi = min(S, q_block + kAttnBM);
+  if (causal) hi = S < q_block + kAttnBM ? S : q_block + kAttnBM;
   if (ranges != nullptr) {
     const int qb = q_block / kAttnRangeBlock;
     lo = ranges[2 * qb] / kAttnBN * kAttnBN;
-    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+    const int rh = static_cast<int>(ranges[2 * qb + 1]);
+    hi = hi < rh ? hi : rh;
   }
 }
 

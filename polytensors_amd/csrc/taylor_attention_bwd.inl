@@ -183,17 +183,54 @@ __device__ __forceinline__ void attn_bwd_store(const AccT (&acc)[K + 1][NS], MPt
 // one store instruction (fixed r) writes 256 contiguous bytes; the consumer's
 // lane (key c, lane group h) needs queries 4h .. 4h + 3 of its key, which are
 // consecutive: one 16-byte load (attn_tile_consumer_offset).
-__device__ __forceinline__ int64_t attn_tile_base(int64_t head, int qt, int kt, int nqt, int nkt) {
+// (Host-callable, like the work-item and range helpers below: the index checks
+// of the tests replay the producer and consumer addressing on the CPU.)
+__host__ __device__ __forceinline__ int64_t attn_tile_base(int64_t head, int qt, int kt, int nqt, int nkt) {
   return ((head * nqt + qt) * nkt + kt) * 256;
 }
-__device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt, int nqt, int nkt, int qi,
-                                                    int ki) {
+__host__ __device__ __forceinline__ int64_t attn_tile_offset(int64_t head, int qt, int kt, int nqt, int nkt, int qi,
+                                                             int ki) {
   return attn_tile_base(head, qt, kt, nqt, nkt) + (ki % 4) * 64 + (ki / 4) * 16 + qi;
 }
 // first of the four consecutive values (queries 4h .. 4h + 3 of key c) a consumer lane reads
-__device__ __forceinline__ int64_t attn_tile_consumer_offset(int64_t head, int qt, int kt, int nqt, int nkt, int c,
-                                                             int h) {
+__host__ __device__ __forceinline__ int64_t attn_tile_consumer_offset(int64_t head, int qt, int kt, int nqt,
+                                                                      int nkt, int c, int h) {
   return attn_tile_base(head, qt, kt, nqt, nkt) + (c % 4) * 64 + (c / 4) * 16 + 4 * h;
+}
+
+// Work item of workgroup t of the query-side kernel (grid: query blocks x heads x
+// slices): head fastest (consecutive workgroups on consecutive XCDs), then
+// head-dim slice, then query block, heaviest (last) query block first.
+__host__ __device__ __forceinline__ void attn_bwd_q_item(int64_t t, int64_t bh, int nqb, int slices, int64_t& head,
+                                                         int& slice, int& q_block) {
+  head = t % bh;
+  slice = static_cast<int>((t / bh) % slices);
+  q_block = (nqb - 1 - static_cast<int>(t / (bh * slices))) * kAttnBM;
+}
+
+// Work item of workgroup t of a key-side kernel (grid: 64-key blocks x heads x
+// slices): head fastest, then slice, then key block, lightest causal work (the
+// last key block) last.
+__host__ __device__ __forceinline__ void attn_bwd_kv_item(int64_t t, int64_t bh, int slices, int64_t& head,
+                                                          int& slice, int& kv_block) {
+  head = t % bh;
+  slice = static_cast<int>((t / bh) % slices);
+  kv_block = static_cast<int>(t / (bh * slices)) * (kAttnWaves * 16);
+}
+
+// Query range [lo, hi) a key workgroup visits: causal (queries from the block's
+// first key on) and mask-range bounds, lo rounded down to a 16-query block.
+__host__ __device__ __forceinline__ void attn_query_range(int L, int kv_block, int causal, const int32_t* ranges,
+                                                          int& lo, int& hi) {
+  lo = causal ? kv_block : 0;
+  hi = L;
+  if (ranges != nullptr) {
+    const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
+    const int kb = nqb + kv_block / kAttnRangeBlock;
+    const int rl = static_cast<int>(ranges[2 * kb]) / 16 * 16, rh = static_cast<int>(ranges[2 * kb + 1]);
+    lo = lo > rl ? lo : rl;
+    hi = hi < rh ? hi : rh;
+  }
 }
 
 // Register-staged copy of ROWS rows (from row `first`, zero past `limit`) of the
@@ -366,14 +403,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   const int wave = threadIdx.x / kWave;
   const int c = lane % 16;
   const int h = lane / 16;
-  // work item: head fastest (consecutive workgroups on consecutive XCDs), then
-  // head-dim slice, then query block, heaviest (last) query block first
   const int nqb = (L + kAttnBM - 1) / kAttnBM;
   const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SLICES);
-  const int64_t t = blockIdx.x;
-  const int64_t head = t % bh;
-  const int slice = static_cast<int>((t / bh) % SLICES);
-  const int q_block = (nqb - 1 - static_cast<int>(t / (bh * SLICES))) * kAttnBM;
+  int64_t head;
+  int slice, q_block;
+  attn_bwd_q_item(blockIdx.x, bh, nqb, SLICES, head, slice, q_block);
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qoff = (head * L + (q_ok ? my_q : 0)) * D;
@@ -558,14 +592,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   const int wave = threadIdx.x / kWave;
   const int c = lane % 16;
   const int h = lane / 16;
-  // work item: head fastest, then slice, then key block, lightest causal work
-  // (the last key block) last
   const int nkb = (S + kBK - 1) / kBK;
   const int64_t bh = gridDim.x / (static_cast<int64_t>(nkb) * SLICES);
-  const int64_t t = blockIdx.x;
-  const int64_t head = t % bh;
-  const int slice = static_cast<int>((t / bh) % SLICES);
-  const int kv_block = static_cast<int>(t / (bh * SLICES)) * kBK;
+  int64_t head;
+  int slice, kv_block;
+  attn_bwd_kv_item(blockIdx.x, bh, SLICES, head, slice, kv_block);
   const int my_k = kv_block + wave * 16 + c;
   const bool k_ok = my_k < S;
   const int64_t koff = (head * S + (k_ok ? my_k : 0)) * D;
@@ -590,14 +621,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   Vec<T, QV> gk[2][K + 1];
   load_glob(gk[0], 0);
 
-  // query range: causal (queries from the block's first key on) and mask-range bounds
-  int lo = causal ? kv_block : 0, hi = L;
-  if (ranges != nullptr) {
-    const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
-    const int kb = nqb + kv_block / kAttnRangeBlock;
-    lo = max(lo, static_cast<int>(ranges[2 * kb]) / kBM * kBM);
-    hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
-  }
+  int lo, hi;
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
   for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
     uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this lane's queries, read ahead of the block's loads
     if constexpr (MASKED) {
@@ -758,10 +783,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
   const int h = lane / 16;
   const int nkb = (S + kBK - 1) / kBK;
   const int64_t bh = gridDim.x / (static_cast<int64_t>(nkb) * SLICES);
-  const int64_t t = blockIdx.x;
-  const int64_t head = t % bh;
-  const int slice = static_cast<int>((t / bh) % SLICES);
-  const int kv_block = static_cast<int>(t / (bh * SLICES)) * kBK;
+  int64_t head;
+  int slice, kv_block;
+  attn_bwd_kv_item(blockIdx.x, bh, SLICES, head, slice, kv_block);
   const int my_k = kv_block + wave * 16 + c;
   const bool k_ok = my_k < S;
   const int nqt = (L + 15) / 16, nkt = (S + 15) / 16;
@@ -777,13 +801,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
     for (int o = 0; o < (DO_K ? K + 1 : 1); ++o) acc_k[o][n] = MF::zero();
   }
 
-  int lo = causal ? kv_block : 0, hi = L;
-  if (ranges != nullptr) {
-    const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
-    const int kb = nqb + kv_block / kAttnRangeBlock;
-    lo = max(lo, static_cast<int>(ranges[2 * kb]) / kBM * kBM);
-    hi = min(hi, static_cast<int>(ranges[2 * kb + 1]));
-  }
+  int lo, hi;
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
   // Block qb0+16's rows and tile values are fetched into registers while block
   // qb0's MFMAs run (register double buffering of the staging).
   RowStager<T, K, D, kBM> stage_g, stage_q;
