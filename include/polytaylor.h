@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 7
+#define PT_ABI_VERSION 8
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -171,6 +171,30 @@ int pt_cross_entropy_series_bwd(int dtype, int degree, const void* const* logits
  * reduction (0 for PT_REDUCTION_NONE). */
 size_t pt_cross_entropy_series_workspace_size(int dtype, int degree,
                                               int64_t rows, int reduction);
+
+/*
+ * pt_cross_entropy_series_fwd without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. It calls
+ * no hipMalloc, hipFree or allocating routine: a mean/sum reduction keeps its
+ * per-row losses in a file-scope device array of PT_CE_NOALLOC_SCRATCH_BYTES
+ * (4 MiB) that each GPU the library runs on holds until the process ends; its
+ * address is looked up once per device on the first call there.
+ * Arguments and results as pt_cross_entropy_series_fwd. A reduction whose
+ * per-row losses, pt_cross_entropy_series_workspace_size(...) bytes, exceed
+ * the array returns PT_UNSUPPORTED (before any device work).
+ * All calls on one GPU share its array: calls that overlap on one GPU (other
+ * streams or host threads) race and must be serialised by the caller.
+ */
+#define PT_CE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+int pt_cross_entropy_series_fwd_noalloc(int dtype, int degree, const void* const* logits,
+                                        int64_t rows, int64_t classes, int64_t row_stride,
+                                        const int64_t* target, int64_t ignore_index,
+                                        double softcap, int reduction, void* const* loss,
+                                        void* const* lse, void* stream);
+
+/* PT_CE_NOALLOC_SCRATCH_BYTES of the built library. */
+size_t pt_cross_entropy_series_noalloc_max_bytes(void);
 
 /*
  * Cauchy-product (truncated series) matrix product

@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -46,6 +46,9 @@ SIGNATURES = {
     "pt_cross_entropy_series_bwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
                                              _c_i64, _c_dbl, _c_vpp, _c_vpp, _c_vpp, _c_vp]),
     "pt_cross_entropy_series_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_int]),
+    "pt_cross_entropy_series_fwd_noalloc": (_c_int, [_c_int, _c_int, _c_vpp, _c_i64, _c_i64, _c_i64, _c_vp,
+                                                     _c_i64, _c_dbl, _c_int, _c_vpp, _c_vpp, _c_vp]),
+    "pt_cross_entropy_series_noalloc_max_bytes": (ctypes.c_size_t, []),
     "pt_cauchy_matmul": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp,
                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp]),
     "pt_taylor_attention_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp, _c_int,
