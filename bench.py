@@ -638,6 +638,11 @@ def profiled_traffic(kernel):
     return None
 
 
+def _progress(message):
+    """One line per finished measurement on stderr (the JSON line alone goes to stdout)."""
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -803,6 +808,7 @@ def main():
                           "GB/s": round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)}), flush=True)
         return
     w = measure(args.workload, device, args.steps, args.warmup)
+    _progress(f"{args.workload}: {w['ms']:.4f} ms per step")
     line = {
         "metric": METRIC,
         "value": round(w["achieved"], 3),
@@ -850,6 +856,7 @@ def main():
                 ceil["frac"] = round(c["achieved"] / ceil["rate"], 4)
                 comps[name]["stream_ceiling"] = ceil
             cpu_samplers[name] = c["cpu"]
+            _progress(f"component {name}: {c['ms']:.4f} ms ({c['achieved']:.1f} {c['unit']})")
             del c
             torch.cuda.empty_cache()
         line["components"] = comps
@@ -866,8 +873,10 @@ def main():
                     "cpu_model": model}
 
         line["cpu_baseline"] = cpu_entry(w["cpu"])
+        _progress(f"cpu baseline {args.workload}: {line['cpu_baseline']['value']} {line['cpu_baseline']['unit']}")
         for name, sampler in cpu_samplers.items():   # the reference's CPU path beside each component
             line["components"][name]["cpu_baseline"] = cpu_entry(sampler)
+            _progress(f"cpu baseline {name}: {line['components'][name]['cpu_baseline']['value']}")
     print(json.dumps(line), flush=True)
 
 
