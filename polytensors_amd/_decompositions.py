@@ -31,10 +31,9 @@ def _has_poly(values):
 
 
 def _needs_grad(args, kwargs):
-    if not torch.is_grad_enabled():
-        return False
-    values = list(args) + list(kwargs.values())
-    return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+    from ._gate import wrapper_grad
+
+    return wrapper_grad(*args, *kwargs.values())
 
 
 def maybe_decompose(function, args, kwargs):

@@ -57,7 +57,7 @@ def _square_mask(attn_mask, L, S):
 
 
 def _needs_grad(*values):
-    return torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+    return _gate.wrapper_grad(*values)
 
 
 def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa):

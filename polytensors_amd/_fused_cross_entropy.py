@@ -128,7 +128,7 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     if _complex.has_complex(input):
         return _complex.at_real_nodes(fused, "cross_entropy", input, target, ignore_index=ignore_index,
                                       reduction=reduction, softcap=softcap)
-    if torch.is_grad_enabled() and input.requires_grad:
+    if _gate.wrapper_grad(input):
         losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
         if reduction == "none":
             return losses
@@ -145,7 +145,7 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
 
 def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mean", label_smoothing=0.0):
     reason = why_ineligible(input, target, weight, reduction, label_smoothing,
-                            allow_grad=torch.is_grad_enabled() and input.requires_grad)
+                            allow_grad=_gate.wrapper_grad(input))
     if reason is not None:
         raise NotImplementedError(f"cross_entropy: {reason}")
     return fused(input, target, ignore_index=ignore_index, reduction=reduction)
@@ -158,7 +158,7 @@ def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="me
 
     if isinstance(logits, PolyTensor):
         reason = why_ineligible(logits, target, None, reduction, 0.0, softcap,
-                                allow_grad=torch.is_grad_enabled() and logits.requires_grad)
+                                allow_grad=_gate.wrapper_grad(logits))
         if reason is not None:
             raise NotImplementedError(f"cross_entropy: {reason}")
         return fused(logits, target, ignore_index=ignore_index, reduction=reduction, softcap=softcap)

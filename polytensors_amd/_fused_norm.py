@@ -67,7 +67,7 @@ def _affine_coeffs(a, input, shape):
 
 
 def _needs_grad(*values):
-    return torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+    return _gate.wrapper_grad(*values)
 
 
 class _SeriesNorm(torch.autograd.Function):
@@ -133,7 +133,8 @@ def _run(input, normalized_shape, weight, bias, eps, layer):
     x = _series_coeffs(input, degree)
     w = _affine_coeffs(weight, input, shape)
     b = _affine_coeffs(bias, input, shape) if layer else []
-    fused_affine = w is not None and b is not None
+    # a coefficient graph differentiates the affine terms as separate series operations
+    fused_affine = w is not None and b is not None and not _gate.coefficient_graph(input, weight, bias)
     out = _ops.norm_series(x, w if fused_affine else [], b if fused_affine else [], math.prod(shape),
                            float(eps), layer)
     result = PolyTensor.from_stacked(out)

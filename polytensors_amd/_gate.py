@@ -54,14 +54,21 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
         return "PolyTensor operands must have the same degree"
     if degree > MAX_DEGREE:
         return f"degree {degree} exceeds the kernels' maximum {MAX_DEGREE}"
+    coeffs = [c for t in tensors for c in coefficients(t, degree)]
     if _coefficient_autograd_enabled.get():
-        return "coefficient_autograd needs series backward kernels, which polytensors_amd does not implement"
-    if torch.is_grad_enabled() and not below_autograd:
+        # the custom ops carry coefficient-level autograd (polytensors_amd._ops); the wrappers
+        # stay outside autograd, so only wrapper gradients are refused
+        if any(p.requires_grad for p in polys):
+            return ("coefficient_autograd differentiates the coefficient tensors: build the PolyTensor "
+                    "wrappers with requires_grad=False")
+        if any(c.is_complex() for c in coeffs):
+            return "coefficient_autograd with complex directions is not implemented"
+    elif torch.is_grad_enabled() and not below_autograd:
         grads = any(t.requires_grad for t in tensors) or any(
             c.requires_grad for p in polys for c in p.coeffs)
         if grads and not allow_plain_grad:
-            return "this fused operation has no series backward kernel; use torch.no_grad()"
-    coeffs = [c for t in tensors for c in coefficients(t, degree)]
+            return ("this operation has no wrapper-level gradient; use torch.no_grad(), or build a "
+                    "coefficient graph inside PolyTensor.coefficient_autograd()")
     if any(t.is_complex() for t in tensors if not isinstance(t, PolyTensor)) or any(
             p.coeffs[0].is_complex() for p in polys):
         return "a complex constant term (complex base) is not implemented; complex directions need a real base"
@@ -71,3 +78,24 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
         return "polytensors_amd runs on HIP (cuda) devices only"
     _lib.load()   # loud failure if the kernels are not built
     return None
+
+
+def coefficient_graph(*values):
+    """Whether this call builds a coefficient-level autograd graph: coefficient_autograd is on,
+    grad mode is enabled and some coefficient (or ordinary tensor operand) requires grad."""
+    from ._tensor import PolyTensor, _coefficient_autograd_enabled
+
+    if not (_coefficient_autograd_enabled.get() and torch.is_grad_enabled()):
+        return False
+    return any((c.requires_grad for c in v.coeffs) if isinstance(v, PolyTensor) else
+               (isinstance(v, torch.Tensor) and v.requires_grad) for v in values)
+
+
+def wrapper_grad(*values):
+    """Whether this call is recorded by wrapper-level (PolyTensor) autograd: grad mode is enabled,
+    coefficient_autograd is off and some operand requires grad."""
+    from ._tensor import _coefficient_autograd_enabled
+
+    if _coefficient_autograd_enabled.get() or not torch.is_grad_enabled():
+        return False
+    return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)

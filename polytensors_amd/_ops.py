@@ -82,12 +82,13 @@ def _(x, weight, bias, n, eps, layer):
 
 @torch.library.custom_op(f"{NAMESPACE}::cross_entropy_series", mutates_args=(), device_types="cuda")
 def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_index: int,
-                         reduction: int, softcap: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
+                         reduction: int, softcap: float) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-order cross entropy of (N, C) logit series; returns (loss, lse).
 
     loss: [K+1, N] (reduction none) or [K+1] (mean/sum), and lse: [K+1, N], both in
     float32 (float64 for float64 logits). ``softcap`` > 0 caps the logit series as
-    softcap * tanh(z / softcap) first.
+    softcap * tanh(z / softcap) first; 0 for none. (No argument has a default: the
+    autograd registration below expects every argument passed.)
     """
     _require(len(z) >= 1, "cross_entropy_series: at least one coefficient is required")
     first = z[0]
@@ -121,7 +122,7 @@ def cross_entropy_series(z: List[torch.Tensor], target: torch.Tensor, ignore_ind
 
 
 @cross_entropy_series.register_fake
-def _(z, target, ignore_index, reduction, softcap=0.0):
+def _(z, target, ignore_index, reduction, softcap):
     rows = z[0].shape[0]
     loss = z[0].new_empty((len(z), rows) if reduction == 0 else (len(z),), dtype=_acc_dtype(z[0].dtype))
     lse = z[0].new_empty((len(z), rows), dtype=_acc_dtype(z[0].dtype))
@@ -493,3 +494,212 @@ def cross_entropy_series_backward(z: List[torch.Tensor], target: torch.Tensor, i
 @cross_entropy_series_backward.register_fake
 def _(z, target, ignore_index, softcap, lse, cot):
     return z[0].new_empty((len(z), *z[0].shape))
+
+
+# ---------------------------------------------------------------------------
+# Coefficient-level autograd (PolyTensor.coefficient_autograd).
+#
+# Each op above maps input coefficients to output coefficients, y_k being
+# coefficient k of f(x(t)). Perturbing x_j by d adds d t^j to x(t), so
+# dy_k/dx_j = J_{k-j}, coefficient k-j of the Jacobian along the curve, and the
+# vector-Jacobian product with output cotangents c_0..c_K is
+#     dL/dx_i = sum_{k>=i} J_{k-i}^T c_k,
+# which is coefficient K-i of the gradient series J(x(t))^T G(t) for the
+# reversed cotangents G_k = c_{K-k}: the backward kernels' own product, read in
+# reverse (at degree 1 the reference's "VJP with cotangents (G1, G0) and orders
+# swapped", /root/reference/docs/api.md:148-153). An operand given with one
+# order (an ordinary tensor) gets coefficient K. These backward functions are
+# not themselves differentiable (as the reference's once_differentiable fused
+# Functions, /root/reference/src/polytensors/_fused_attention.py:166-185).
+
+def _reversed(grad):
+    """Cotangents of a stacked [K+1, ...] output in reverse order, as a coefficient list."""
+    return list(grad.flip(0).unbind(0))
+
+
+def _read_back(series, orders):
+    """Gradients of an operand with ``orders`` coefficients from a gradient series of reversed cotangents."""
+    top = series.shape[0] - 1
+    return [series[top - i] for i in range(orders)]
+
+
+def _grads_flag(tensors):
+    return any(t.requires_grad for t in tensors)
+
+
+def _returned(ctx, *grads):
+    """``grads`` padded with None to the number of arguments the call passed (torch matches the
+    backward's return to the arguments given, defaulted ones excluded)."""
+    return tuple(grads) + (None,) * (ctx.n_inputs - len(grads))
+
+
+def _once(what):
+    if torch.is_grad_enabled():
+        raise NotImplementedError(f"{what}: second-order coefficient autograd through the fused kernels "
+                                  "is not implemented")
+
+
+def _norm_setup(ctx, inputs, output):
+    x, weight, bias, n, eps, layer = inputs
+    ctx.save_for_backward(*x)
+    ctx.meta = (n, eps, layer, bool(weight) or bool(bias))
+    ctx.n_inputs = len(inputs)
+
+
+def _norm_backward(ctx, grad):
+    _once("norm_series")
+    n, eps, layer, affine = ctx.meta
+    if affine:
+        raise NotImplementedError("norm_series: the fused weight/bias has no coefficient gradient; under "
+                                  "autograd apply them as separate series operations")
+    x = list(ctx.saved_tensors)
+    dx = norm_series_backward(x, _reversed(grad), n, eps, layer)
+    return _returned(ctx, _read_back(dx, len(x)), [], [])
+
+
+torch.library.register_autograd(f"{NAMESPACE}::norm_series", _norm_backward, setup_context=_norm_setup)
+
+
+def _ce_setup(ctx, inputs, output):
+    z, target, ignore_index, reduction, softcap = inputs
+    ctx.mark_non_differentiable(output[1])
+    ctx.save_for_backward(*z, target, output[1])
+    ctx.meta = (len(z), ignore_index, reduction, softcap)
+    ctx.n_inputs = len(inputs)
+
+
+def _ce_backward(ctx, grad_loss, grad_lse):
+    _once("cross_entropy_series")
+    n, ignore_index, reduction, softcap = ctx.meta
+    saved = ctx.saved_tensors
+    z, target, lse = list(saved[:n]), saved[n], saved[n + 1]
+    rows = z[0].shape[0]
+    cot = grad_loss.to(lse.dtype)
+    if reduction != 0:   # per-row cotangents of the sum (ignored rows have zero loss and gradient)
+        cot = cot[:, None].expand(n, rows)
+        if reduction == 1:
+            cot = cot / (target != ignore_index).sum().to(lse.dtype)
+    dz = cross_entropy_series_backward(z, target, ignore_index, softcap, lse,
+                                       [c.contiguous() for c in cot.flip(0).unbind(0)])
+    return _returned(ctx, _read_back(dz, n))
+
+
+torch.library.register_autograd(f"{NAMESPACE}::cross_entropy_series", _ce_backward, setup_context=_ce_setup)
+
+
+def _mm_setup(ctx, inputs, output):
+    a, b, degree, trans_b = inputs
+    ctx.save_for_backward(*a, *b)
+    ctx.meta = (len(a), len(b), degree, trans_b, _grads_flag(a), _grads_flag(b))
+    ctx.n_inputs = len(inputs)
+
+
+def _mm_backward(ctx, grad):
+    _once("cauchy_matmul")
+    na, nb, degree, trans_b, need_a, need_b = ctx.meta
+    saved = ctx.saved_tensors
+    a, b = list(saved[:na]), list(saved[na:])
+    c = _reversed(grad)                     # [batch, m, n] each
+    batch = grad.shape[1]
+    ga = gb = None
+    if need_a:   # dA = C (*) B^T
+        da = cauchy_matmul(c, b, degree, not trans_b)
+        if a[0].shape[0] == 1 and batch > 1:
+            da = da.sum(1, keepdim=True)
+        ga = _read_back(da, na)
+    if need_b:   # dB = A^T (*) C, or its transpose for a [batch, n, k] operand
+        if trans_b:
+            db = cauchy_matmul([x.transpose(-1, -2).contiguous() for x in c], a, degree, False)
+        else:
+            db = cauchy_matmul([x.transpose(-1, -2).contiguous() for x in a], c, degree, False)
+        if b[0].shape[0] == 1 and batch > 1:
+            db = db.sum(1, keepdim=True)
+        gb = _read_back(db, nb)
+    return _returned(ctx, ga if ga is not None else [None] * na, gb if gb is not None else [None] * nb)
+
+
+torch.library.register_autograd(f"{NAMESPACE}::cauchy_matmul", _mm_backward, setup_context=_mm_setup)
+
+
+def _attn_setup(ctx, inputs, output):
+    q, k, v, mask, causal, scale, degree = inputs
+    out, lse = output
+    ctx.mark_non_differentiable(lse)
+    ctx.save_for_backward(*q, *k, *v, out, lse, *([] if mask is None else [mask]))
+    ctx.meta = (len(q), len(k), len(v), mask is not None, causal, scale, degree)
+    ctx.n_inputs = len(inputs)
+
+
+def _attn_backward(ctx, grad_out, grad_lse):
+    _once("taylor_attention_fwd")
+    nq, nk, nv, has_mask, causal, scale, degree = ctx.meta
+    s = ctx.saved_tensors
+    q, k, v = list(s[:nq]), list(s[nq:nq + nk]), list(s[nq + nk:nq + nk + nv])
+    out, lse = s[nq + nk + nv], s[nq + nk + nv + 1]
+    mask = s[-1] if has_mask else None
+
+    def full(xs):   # the backward kernels take every order; an ordinary operand has zero higher orders
+        return xs + [torch.zeros_like(xs[0]) for _ in range(degree + 1 - len(xs))]
+
+    dq, dk, dv = taylor_attention_bwd(full(q), full(k), full(v), out, lse, _reversed(grad_out), mask, causal, scale)
+    return _returned(ctx, _read_back(dq, nq), _read_back(dk, nk), _read_back(dv, nv))
+
+
+torch.library.register_autograd(f"{NAMESPACE}::taylor_attention_fwd", _attn_backward, setup_context=_attn_setup)
+
+# the derivative's saved series: the input, or the output where the backward operation takes it
+_ACT_SAVES_OUTPUT = ("tanh", "sigmoid", "exp")
+
+
+def _act_setup(ctx, inputs, output):
+    x, kind = inputs
+    ctx.kind = kind
+    ctx.n_inputs = len(inputs)
+    if kind in _ACT_SAVES_OUTPUT:
+        ctx.save_for_backward(output)
+    else:
+        ctx.save_for_backward(*x)
+
+
+def _act_backward(ctx, grad):
+    _once("activation_series")
+    kind = ctx.kind
+    saved = ctx.saved_tensors
+    saved = list(saved[0].unbind(0)) if kind in _ACT_SAVES_OUTPUT else list(saved)
+    g = _reversed(grad)
+    if kind == "exp":      # exp' = exp: the gradient series is G (*) y
+        dx = series_binary(g, saved, "mul")
+    elif kind == "log":    # log' = 1/x: G / x
+        dx = series_binary(g, saved, "div")
+    else:
+        dx = activation_series_backward(g, saved, kind)
+    return _returned(ctx, _read_back(dx, len(saved)))
+
+
+torch.library.register_autograd(f"{NAMESPACE}::activation_series", _act_backward, setup_context=_act_setup)
+
+
+def _binary_setup(ctx, inputs, output):
+    a, b, op = inputs
+    ctx.op = op
+    ctx.n = len(a)
+    ctx.n_inputs = len(inputs)
+    ctx.save_for_backward(*a, *b, *(list(output.unbind(0)) if op == "div" else []))
+
+
+def _binary_backward(ctx, grad):
+    _once("series_binary")
+    n, op = ctx.n, ctx.op
+    s = ctx.saved_tensors
+    a, b = list(s[:n]), list(s[n:2 * n])
+    g = _reversed(grad)
+    if op == "mul":        # d(a b) = b da + a db
+        da, db = series_binary(g, b, "mul"), series_binary(g, a, "mul")
+    else:                  # d(a / b) = da / b - (a / b) db / b
+        y = list(s[2 * n:])
+        da = series_binary(g, b, "div")
+        db = -series_binary(list(series_binary(g, y, "mul").unbind(0)), b, "div")
+    return _returned(ctx, _read_back(da, n), _read_back(db, n))
+
+
+torch.library.register_autograd(f"{NAMESPACE}::series_binary", _binary_backward, setup_context=_binary_setup)

@@ -26,6 +26,9 @@ from ._plain import plain_range_enabled
 
 _retention_scopes = contextvars.ContextVar("polytensors_amd_retention_scopes", default=())
 _coefficient_autograd_enabled = contextvars.ContextVar("polytensors_amd_coefficient_autograd", default=False)
+_DK = torch._C.DispatchKey
+_COEFFICIENT_AUTOGRAD_KEYS = (_DK.Conjugate, _DK.Negative, _DK.ADInplaceOrView, _DK.Autograd,
+                              _DK.AutogradFunctionality, _DK.AutogradOther, _DK.AutogradCPU, _DK.AutogradCUDA)
 _COMPLEX_OF = {torch.float16: torch.complex32, torch.float32: torch.complex64, torch.float64: torch.complex128}
 
 
@@ -247,8 +250,16 @@ class PolyTensor(torch.Tensor):
     @classmethod
     @contextlib.contextmanager
     def coefficient_autograd(cls):
-        """Ordinary autograd graphs on coefficients. The kernels here are forward-only,
-        so fused operations inside this scope raise NotImplementedError."""
+        """Build an ordinary autograd graph for the coefficient tensors
+        (/root/reference/src/polytensors/_tensor.py:291-323).
+
+        Make the coefficients autograd leaves and wrap them with ``requires_grad=False``;
+        inside the scope every operation records ``grad_fn`` nodes on the coefficients,
+        the fused kernels included (their coefficient gradients are the backward
+        kernels' gradient series of the reversed cotangents). The gradient of loss
+        coefficient k with respect to a parameter's coefficient 0 is coefficient k of
+        the parameter's gradient series. Complex directions are not supported here.
+        """
         token = _coefficient_autograd_enabled.set(True)
         try:
             yield
@@ -301,4 +312,13 @@ class PolyTensor(torch.Tensor):
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
         from ._dispatch import dispatch
 
+        if _coefficient_autograd_enabled.get():
+            # Subclass dispatch runs below the wrapper's autograd layer; re-include the
+            # autograd keys so the rules' operations on the coefficient tensors (and the
+            # kernels' custom ops) record their own graph, as the reference's
+            # /root/reference/src/polytensors/_tensor.py:370-400 does.
+            with contextlib.ExitStack() as stack:
+                for key in _COEFFICIENT_AUTOGRAD_KEYS:
+                    stack.enter_context(torch._C._SetExcludeDispatchKeyGuard(key, False))
+                return dispatch(func, types, args, kwargs)
         return dispatch(func, types, args, kwargs)

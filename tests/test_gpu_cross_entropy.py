@@ -89,7 +89,7 @@ def test_row_strides_and_class_counts(C, pad):
 def test_lse_series_output():
     degree = 4
     Z, y = _logits(40, 2000, degree, seed=3, dtype=torch.float32)
-    _, lse = _ops.cross_entropy_series([c.cuda() for c in Z], y.cuda(), -100, 0)
+    _, lse = _ops.cross_entropy_series([c.cuda() for c in Z], y.cuda(), -100, 0, 0.0)
     want = paths.logsumexp([c.double() for c in Z], 1)
     _check(list(lse.unbind(0)), want, torch.float32)
 
@@ -108,7 +108,7 @@ def test_large_common_offset_keeps_higher_orders_exact():
     # /root/reference/tests/test_series.py:113-120 through the kernel: logits 1e20 + t.
     base = torch.full((3, 2), 1e20, dtype=torch.float32)
     coeffs = (base, torch.ones_like(base), *(torch.zeros_like(base) for _ in range(3)))
-    _, lse = _ops.cross_entropy_series([c.cuda() for c in coeffs], torch.zeros(3, dtype=torch.int64).cuda(), -100, 0)
+    _, lse = _ops.cross_entropy_series([c.cuda() for c in coeffs], torch.zeros(3, dtype=torch.int64).cuda(), -100, 0, 0.0)
     lse = lse.cpu()
     assert torch.equal(lse[1], torch.ones(3))
     assert torch.equal(lse[2:], torch.zeros(3, 3))
@@ -121,8 +121,8 @@ def test_full_size_config_rows_sample():
     g = torch.Generator(device="cuda").manual_seed(4)
     Z = [torch.randn(N, C, generator=g, device="cuda") * (2.0 if k == 0 else 0.5 ** k) for k in range(degree + 1)]
     y = torch.randint(0, C, (N,), generator=g, device="cuda")
-    rows, _ = _ops.cross_entropy_series(Z, y, -100, 0)
-    mean, _ = _ops.cross_entropy_series(Z, y, -100, 1)
+    rows, _ = _ops.cross_entropy_series(Z, y, -100, 0, 0.0)
+    mean, _ = _ops.cross_entropy_series(Z, y, -100, 1, 0.0)
     for k in range(degree + 1):
         assert abs(mean[k].item() - rows[k].double().mean().item()) <= 1e-5 * max(1.0, abs(mean[k].item()))
     pick = torch.randperm(N, generator=torch.Generator().manual_seed(5))[:32].cuda()
