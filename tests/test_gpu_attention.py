@@ -240,6 +240,30 @@ def test_full_size_config3_one_head():
     assert rel_err(out[0].cpu(), ref0.cpu()) <= 1e-4
 
 
+def test_full_size_config3_all_heads_linear_in_the_value_series():
+    # benchmark config 3's full launch (B=4 H=16 L=2048 d=128, K=4, fp32, causal, line inputs): every
+    # head and every order of O(t) = softmax(S(t)) V(t) is linear in the value series, so
+    # O[V + 2 W] = O[V] + 2 O[W] holds for all 64 heads at once (each side a separate launch).
+    B, H, L, d, degree = 4, 16, 2048, 128, 4
+    g = torch.Generator(device="cuda").manual_seed(21)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device="cuda") / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device="cuda")
+        return [base, direction] + [torch.zeros_like(base) for _ in range(degree - 1)]
+
+    q, k, v, w = line(), line(), line(), line()
+    scale = 1 / math.sqrt(d)
+    o_v, _ = _ops.taylor_attention_fwd(q, k, v, None, True, scale, degree)
+    o_w, _ = _ops.taylor_attention_fwd(q, k, w, None, True, scale, degree)
+    o_sum, _ = _ops.taylor_attention_fwd(q, k, [a + 2 * b for a, b in zip(v, w)], None, True, scale, degree)
+    want = o_v + 2 * o_w
+    for order in range(degree + 1):
+        for head in range(B * H):
+            err = ((o_sum[order, head] - want[order, head]).abs().max() / want[order, head].abs().max()).item()
+            assert err <= 1e-4, f"order {order}, head {head}: {err:.3e}"
+
+
 # The pipelined fp32 kernel runs for full-order operands with a key length that is a multiple of 16
 # (and two K/V tiles within LDS); these shapes exercise it.
 @pytest.mark.parametrize("d,degree", [(16, 1), (16, 8), (32, 4), (64, 4), (64, 8), (128, 1), (128, 4)])

@@ -271,3 +271,26 @@ def test_decoder_config5_full_size_properties():
     for k in range(1, degree + 1):
         a, b = zc.coeffs[k].item(), z.coeffs[k].item().conjugate()
         assert abs(a - b) <= 1e-4 * max(abs(b), 1e-30), k
+
+
+@pytest.mark.parametrize("degree", [5, 6, 7, 8])
+def test_complex64_at_high_degree(degree):
+    # the interpolation at lam = i amplifies the real runs' rounding most at high degree; complex64
+    # must still meet the float32 tolerance (1e-4 per order) at every supported degree
+    dt = torch.float32
+    Q, K, V = (_series((2, 2, 70, 32), degree, 7 + i, scale=0.5) for i in range(3))
+    X = _series((6, 96), degree, 6)
+    Z = _series((40, 300), degree, 8, scale=2.0)
+    y = torch.randint(0, 300, (40,), generator=torch.Generator().manual_seed(9))
+    A, B = _series((5, 37), degree, 3), _series((5, 37), degree, 4, positive=True)
+    with torch.no_grad(), PolyTensor.plain_range():
+        att = F.scaled_dot_product_attention(_poly(Q, dt), _poly(K, dt), _poly(V, dt), is_causal=True)
+        ln = F.layer_norm(_poly(X, dt), (96,))
+        ge = F.gelu(_poly(X, dt))
+        ce = F.cross_entropy(_poly(Z, dt), y.cuda())
+        qu = _poly(A, dt) / _poly(B, dt)
+    _check(att.coeffs, oracle.attention(_up(Q, dt), _up(K, dt), _up(V, dt), is_causal=True), dt)
+    _check(ln.coeffs, oracle.layer_norm(_up(X, dt), (96,)), dt)
+    _check(ge.coeffs, oracle.activation(_up(X, dt), "gelu"), dt)
+    _check(ce.coeffs, oracle.cross_entropy(_up(Z, dt), y), dt)
+    _check(qu.coeffs, oracle.quotient(_up(A, dt), _up(B, dt)), dt)
