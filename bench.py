@@ -1,8 +1,8 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on benchmark configs 2-5 (shapes in each workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|attention_dense|attention_window|attention_bwd|attention_bwd_window|
-                                matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
+                    [--workload attention|attention_dense|attention_bf16|attention_window|attention_bwd|
+                                attention_bwd_window|matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
@@ -36,6 +36,7 @@ if ROOT not in sys.path:
 METRIC = "ms & TFLOP/s per degree-K Taylor attention fwd; GB/s norm/CE; % roofline"
 PEAK_FP32_MFMA = 157.3   # TFLOP/s, dense
 PEAK_FP64_MFMA = 78.6    # TFLOP/s, dense
+PEAK_BF16_MFMA = 2500.0  # TFLOP/s, dense (bf16 and fp16)
 PEAK_HBM = 8000.0        # GB/s
 
 
@@ -267,6 +268,36 @@ def wl_decoder(device):
                 cpu=lambda: cpu_decoder(layers, d, heads, vocab, K))
 
 
+def wl_attention_bf16(device):
+    """Config 3's shape and inputs (B=4 H=16 L=2048 d=128, K=4, causal, line inputs, scale 1/sqrt(128))
+    stored in bfloat16: the 16-bit kernel (bf16 MFMA operands, fp32 accumulation). Work is the same
+    dense-series count; the roofline is the bf16 MFMA peak."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(2, device)
+
+    def series():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [x.to(torch.bfloat16) for x in [base, direction] + [torch.zeros_like(base) for _ in range(2, K + 1)]]
+
+    q, k, v = series(), series(), series()
+    scale = 1 / math.sqrt(d)
+
+    def step():
+        return _ops.taylor_attention_fwd(q, k, v, None, True, scale, K)
+
+    pairs = (K + 1) * (K + 2) // 2
+    flops = 2 * pairs * 2 * d * B * H * L * (L + 1) / 2
+    nbytes = 4 * (K + 1) * B * H * L * d * 2
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_MFMA,
+                bytes=nbytes, kernel="taylor_attention_bf16", dtype="bf16 (fp32 accumulate)",
+                workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} bf16 causal line inputs",
+                cpu=lambda: cpu_attention(L, d, K, heads=8, dtype="bf16"))
+
+
 def wl_attention_dense(device):
     """Config 3 with dense random orders 2..4 (N(0,1) 0.5^k) instead of a line: the same kernel
     and work count, with no zero input orders."""
@@ -434,7 +465,7 @@ WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "c
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
              "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
              "attention_bwd_window": wl_attention_bwd_window,
-             "attention_dense": wl_attention_dense, "config1": wl_config1,
+             "attention_dense": wl_attention_dense, "attention_bf16": wl_attention_bf16, "config1": wl_config1,
              "decoder": wl_decoder}
 
 
@@ -452,12 +483,14 @@ def _cpu_time(fn, reps=3):
     return times[len(times) // 2]
 
 
-def cpu_attention(L, d, K, heads=64):
+def cpu_attention(L, d, K, heads=64, dtype=None):
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(2)
     q, k, v = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(3))
+    if dtype == "bf16":   # the reference's general path on bf16 coefficients (torch's CPU bf16 ops)
+        q, k, v = ([c.to(torch.bfloat16) for c in s] for s in (q, k, v))
 
     def all_heads():   # one head at a time (the L x L series of all heads would not fit in host memory)
         for _ in range(heads):
@@ -466,7 +499,8 @@ def cpu_attention(L, d, K, heads=64):
     t = _cpu_time(all_heads, reps=1)
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
-                sample=f"all {heads} (b,h) heads one at a time, L={L} d={d} K={K} fp32 causal", seconds=t)
+                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} {dtype or 'fp32'} causal",
+                seconds=t)
 
 
 def cpu_attention_window(L, d, K, W, heads=16):

@@ -234,7 +234,11 @@ int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
  *   /root/reference/src/polytensors/_attention_kernels.py:27-82 (_forward),
  * generalised to degree K; the series follow the general decomposition
  *   /root/reference/src/polytensors/_decompositions.py:28-43 (_attention).
- * dtype: PT_FLOAT32 or PT_FLOAT64.
+ * dtype: PT_FLOAT32 or PT_FLOAT64 (fp32 / fp64 MFMA), or PT_BFLOAT16 or
+ * PT_FLOAT16 (16-bit MFMA operands, fp32 accumulation and lse, as the
+ * reference's half-type kernel, _fused_attention.py:72-78; the probability
+ * series is rounded to the storage type as the value product's operand;
+ * pointers 16-byte aligned, out 8-byte aligned).
  */
 int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
                             int q_orders, const void* const* k, int k_orders,

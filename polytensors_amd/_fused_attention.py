@@ -26,7 +26,8 @@ import torch
 from . import _complex, _gate, _ops
 
 _enabled = contextvars.ContextVar("polytensors_amd_fused_attention", default=True)
-_HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128)}
+_HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128),
+              torch.bfloat16: (16, 32, 64, 128), torch.float16: (16, 32, 64, 128)}
 
 
 def _tiles_fit_lds(dtype, head_dim, degree):
@@ -36,6 +37,10 @@ def _tiles_fit_lds(dtype, head_dim, degree):
     values; the backward adds two 16-row series of accumulator values
     (AttnShape and AttnBwdPlan in csrc/taylor_attention*.inl).
     """
+    if dtype in (torch.bfloat16, torch.float16):
+        # the 16-bit forward splits its output head dims where needed (every shape fits); its
+        # backward runs the float32 kernels
+        dtype = torch.float32
     item = torch.empty((), dtype=dtype).element_size()
     lds = 2 * (degree + 1) * 16 * (head_dim + 4) * item + 2 * (degree + 1) * 16 * item
     return lds <= 160 * 1024
@@ -88,7 +93,7 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "query, key and value coefficients must share one dtype"
     if dtype not in _HEAD_DIMS:
-        return f"dtype {dtype} is not supported (float32 or float64)"
+        return f"dtype {dtype} is not supported (float32, float64, bfloat16 or float16)"
     if query.ndim < 3 or key.shape != value.shape or query.shape[:-2] != key.shape[:-2]:
         return "shapes must be (..., L, d) and (..., S, d) with equal batch dimensions"
     if query.shape[-1] != key.shape[-1] or query.shape[-1] not in _HEAD_DIMS[dtype]:
@@ -168,7 +173,7 @@ class _SeriesAttention(torch.autograd.Function):
         token = _plain_range.set(True)   # the engine's thread does not see the caller's context
         try:
             g = _full(gradient, degree, shape_q)
-            dq, dk, dv = _ops.taylor_attention_bwd(q, k, v, out, lse, g, mask, causal, scale)
+            dq, dk, dv = _ops.attention_gradient_series(q, k, v, out, lse, g, mask, causal, scale)
             grads = (PolyTensor.from_stacked(dq.view(n, *shape_q)), PolyTensor.from_stacked(dk.view(n, *shape_k)),
                      PolyTensor.from_stacked(dv.view(n, *shape_k)))
         finally:

@@ -201,7 +201,8 @@ def taylor_attention_fwd(q: List[torch.Tensor], k: List[torch.Tensor], v: List[t
         _check_series(f"taylor_attention {name}", s)
         _require(s[0].dim() == 3, f"taylor_attention: {name} must be [bh, length, d]")
     dtype = q[0].dtype
-    _require(dtype in (torch.float32, torch.float64), "taylor_attention: float32 or float64 only")
+    _require(dtype in (torch.float32, torch.float64, torch.bfloat16, torch.float16),
+             "taylor_attention: float32, float64, bfloat16 or float16")
     bh, lq, d = q[0].shape
     _require(k[0].shape == v[0].shape and k[0].shape[0] == bh and k[0].shape[2] == d,
              "taylor_attention: key/value shapes must be [bh, S, d] matching the query")
@@ -231,6 +232,26 @@ def _(q, k, v, mask, causal, scale, degree):
     bh, lq, d = q[0].shape
     return (q[0].new_empty((degree + 1, bh, lq, d)),
             q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))
+
+
+def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale):
+    """Gradient series (dq, dk, dv) of the attention forward for every operand dtype.
+
+    float32/float64 call ``taylor_attention_bwd``. bfloat16/float16 operands run
+    the float32 backward kernels on float32 copies of q, k, v, the forward's
+    output and the cotangents (the forward's lse series is already float32) and
+    round the gradients to the operand dtype: the reference's half-type backward
+    likewise accumulates in float32 (/root/reference/src/polytensors/_fused_attention.py:72-78,
+    tolerance 5e-2 against float32, tests/test_fused_kernels.py:64-72).
+    """
+    dtype = q[0].dtype
+    if dtype in (torch.bfloat16, torch.float16):
+        def up(xs):
+            return [x.float() for x in xs]
+
+        dq, dk, dv = taylor_attention_bwd(up(q), up(k), up(v), out.float(), lse, up(grad), mask, causal, scale)
+        return dq.to(dtype), dk.to(dtype), dv.to(dtype)
+    return taylor_attention_bwd(q, k, v, out, lse, grad, mask, causal, scale)
 
 
 @torch.library.custom_op(f"{NAMESPACE}::taylor_attention_bwd", mutates_args=(), device_types="cuda")
@@ -641,7 +662,8 @@ def _attn_backward(ctx, grad_out, grad_lse):
     def full(xs):   # the backward kernels take every order; an ordinary operand has zero higher orders
         return xs + [torch.zeros_like(xs[0]) for _ in range(degree + 1 - len(xs))]
 
-    dq, dk, dv = taylor_attention_bwd(full(q), full(k), full(v), out, lse, _reversed(grad_out), mask, causal, scale)
+    dq, dk, dv = attention_gradient_series(full(q), full(k), full(v), out, lse, _reversed(grad_out), mask, causal,
+                                           scale)
     return _returned(ctx, _read_back(dq, nq), _read_back(dk, nk), _read_back(dv, nv))
 
 

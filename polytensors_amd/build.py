@@ -12,6 +12,7 @@ Run ``python -m polytensors_amd.build`` (incremental) or ``--force``.
 import concurrent.futures
 import hashlib
 import os
+import re
 import subprocess
 import sys
 
@@ -37,22 +38,35 @@ def _sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _headers_digest():
-    h = hashlib.sha256()
-    paths = [os.path.join(CSRC, f) for f in sorted(os.listdir(CSRC)) if f.endswith((".h", ".inl"))]
-    paths.append(os.path.join(INCLUDE, "polytaylor.h"))
-    for p in paths:
-        with open(p, "rb") as fh:
-            h.update(fh.read())
-    h.update(" ".join(CFLAGS).encode())
-    return h.hexdigest()[:16]
+_INCLUDE_RE = re.compile(rb'^\s*#\s*include\s*"([^"]+)"', re.M)
 
 
-def _object_for(src, digest):
-    with open(src, "rb") as fh:
-        tag = hashlib.sha256(fh.read() + digest.encode()).hexdigest()[:16]
+def _local_includes(path, seen):
+    """``path`` and the files its quoted #includes reach, transitively (csrc/ and include/)."""
+    if path in seen:
+        return
+    seen.add(path)
+    with open(path, "rb") as fh:
+        text = fh.read()
+    for name in _INCLUDE_RE.findall(text):
+        name = name.decode()
+        for base in (os.path.dirname(path), CSRC, INCLUDE):
+            candidate = os.path.normpath(os.path.join(base, name))
+            if os.path.exists(candidate):
+                _local_includes(candidate, seen)
+                break
+
+
+def _object_for(src):
+    """Object path tagged with a digest of the source, every local header it reaches, and the flags."""
+    files = set()
+    _local_includes(src, files)
+    h = hashlib.sha256(" ".join(CFLAGS).encode())
+    for path in sorted(files):
+        with open(path, "rb") as fh:
+            h.update(path.encode() + b"\0" + fh.read())
     name = os.path.splitext(os.path.basename(src))[0]
-    return os.path.join(OBJ_DIR, f"{name}.{tag}.o")
+    return os.path.join(OBJ_DIR, f"{name}.{h.hexdigest()[:16]}.o")
 
 
 def _compile(src, obj):
@@ -71,9 +85,8 @@ def build(force=False, jobs=None, verbose=True):
     """Compile the kernels and link the library; returns its path."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
-    digest = _headers_digest()
     sources = _sources()
-    objects = [_object_for(s, digest) for s in sources]
+    objects = [_object_for(s) for s in sources]
     todo = [(s, o) for s, o in zip(sources, objects) if force or not os.path.exists(o)]
     jobs = jobs or min(8, os.cpu_count() or 1)
     if todo:

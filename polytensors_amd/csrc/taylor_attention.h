@@ -26,6 +26,10 @@ struct AttnArgs {
 template <typename T>
 int launch_attention(const AttnArgs& a);
 
+// bfloat16 / float16 operands on the 16x16x32 MFMAs (taylor_attention_half.inl); T = bf16 or _Float16.
+template <typename T>
+int launch_attention_half(const AttnArgs& a);
+
 // Block ranges of a boolean (L, S) mask into ranges[attention_mask_ranges_count(L, S)].
 int64_t attention_mask_ranges_count(int64_t lq, int64_t lk);
 int launch_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, hipStream_t stream);

@@ -13,8 +13,8 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
              "Taylor attention: degree must be in 0..8");
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention: mask_ranges without a mask");
-  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
-             "Taylor attention: float32 and float64 only");
+  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,
+             PT_UNSUPPORTED, "Taylor attention: float32, float64, bfloat16 or float16");
   PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention: q, k, v and out pointer arrays are required");
   for (int o : {q_orders, k_orders, v_orders})
@@ -39,7 +39,12 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
                  causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream)};
-  return dtype == PT_FLOAT32 ? pt::launch_attention<float>(a) : pt::launch_attention<double>(a);
+  switch (dtype) {
+    case PT_FLOAT32: return pt::launch_attention<float>(a);
+    case PT_FLOAT64: return pt::launch_attention<double>(a);
+    case PT_BFLOAT16: return pt::launch_attention_half<pt::bf16>(a);
+    default: return pt::launch_attention_half<_Float16>(a);
+  }
 }
 
 int64_t pt_attention_mask_ranges_count(int64_t lq, int64_t lk) {

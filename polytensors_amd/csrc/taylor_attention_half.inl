@@ -1,0 +1,480 @@
+// Flash-style attention forward of degree-K series with bfloat16 / float16
+// operands on the 16x16x32 MFMAs of gfx950 (fp32 accumulation).
+//
+// The series arithmetic is that of taylor_attention.inl: per query row,
+//   exp(S(t)) = exp(S_0) e(t),  e_k = sum_{j=1..k} (j/k) S_j e_{k-j},
+//   l_k = sum_keys exp(S_0 - m) e_k,  N_k = sum_keys sum_{a+b=k} exp(S_0 - m) e_a V_b,
+//   O_k = (N_k - sum_{j=1..k} l_j O_{k-j}) / l_0,
+// the series of the reference's decomposition
+// (/root/reference/src/polytensors/_decompositions.py:28-43), as in its degree-1
+// fused kernel for half types (/root/reference/src/polytensors/_fused_attention.py:72-78,
+// _attention_kernels.py:27-82: half operands, fp32 accumulation). Only the
+// MFMA operands are 16-bit: Q, K and V as stored, and the probability series
+// P_k = exp(S_0 - m) e_k rounded to the storage type for the value product.
+// Scores, the exponential series, the row sums and the output accumulators are
+// fp32; the output is rounded to the storage type once, the lse series is fp32.
+//
+// Work decomposition: a workgroup of 4 waves owns 64 query rows of one head
+// (16 per wave); key blocks of 32 keys are staged in LDS, K row-major and V
+// transposed (head dim x keys). With v_mfma_f32_16x16x32 (lane l supplies A
+// row l % 16 and B column l % 16, contraction elements 8 (l / 16) .. + 7; the
+// accumulator register r of lane l is row 4 (l / 16) + r, column l % 16):
+// * scores transposed, S^T = K Q^T per 16-key half: lane (c, g) = (l % 16,
+//   l / 16) holds keys 4g + r of the half for query c;
+// * the value product O^T += V^T P^T contracts the block's 32 keys with lane
+//   group g's slots 8g .. 8g + 7 standing for keys 4g .. 4g + 3 and
+//   16 + 4g .. 16 + 4g + 3: exactly the eight probabilities the lane holds, so
+//   P goes from the score accumulators into the B operand without leaving the
+//   lane. The A operand (V^T, the same eight keys of head-dim row c) is two
+//   8-byte reads of the transposed V tile.
+// The output accumulators O^T_k (16 head dims x 16 queries per block) and, when
+// the registers allow, the wave's query tile stay in registers for the whole key
+// loop.
+#pragma once
+
+#include "taylor_attention.inl"
+
+namespace pt {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct HalfMfma;
+
+template <>
+struct HalfMfma<bf16> {
+  typedef __bf16 op_t __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static floatx4 mma(u32x4 a, u32x4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(op_t, a), __builtin_bit_cast(op_t, b), c,
+                                                   0, 0, 0);
+  }
+  // two values, round to nearest even, first in the low half
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+  // the two values of a packed word
+  __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // lazy-rescale slack (natural-log units): p <= e^8 (bf16 has the fp32 exponent range)
+  static constexpr float kSlack = 8.0f;
+};
+
+template <>
+struct HalfMfma<_Float16> {
+  typedef _Float16 op_t __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static floatx4 mma(u32x4 a, u32x4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(op_t, a), __builtin_bit_cast(op_t, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    const _Float16 x = static_cast<_Float16>(a), y = static_cast<_Float16>(b);   // round to nearest even
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, x)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, y)) << 16);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+  }
+  __device__ __forceinline__ static float hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  }
+  // float16 overflows at 65504: the running maximum is exact (p <= 1)
+  static constexpr float kSlack = 0.0f;
+};
+
+template <int K, int D>
+struct AttnHalfShape {
+  static constexpr int KB = 32;              // keys per block
+  static constexpr int DC = (D + 31) / 32;   // 32-wide head-dim chunks of the score contraction
+  // Output head-dim slices: the output accumulators of every order at head dim 128 exceed the
+  // registers from degree 5 on; two slices (a grid dimension, each recomputing its scores) keep
+  // every instantiation free of scratch spills (checked with the compiler's resource remarks).
+  static constexpr int SL = D == 128 ? (K >= 8 ? 4 : K >= 5 ? 2 : 1) : 1;
+  static constexpr int DS = D / SL;          // output head dims per slice
+  static constexpr int DB = DS / 16;         // 16-wide output blocks of the slice
+  static constexpr int LDK = D + 8;          // K tile row: 16-byte aligned, 4 banks of skew per row
+  // Transposed V tile row (keys): 40 values (20 dwords) make the 8-byte operand reads of 16 rows x
+  // two lane groups hit 64 distinct banks; 36 where the larger tile would not fit.
+  static constexpr size_t lds_with(int ldv) { return static_cast<size_t>(K + 1) * (KB * LDK + DS * ldv) * 2; }
+  static constexpr int LDV = lds_with(40) <= 160 * 1024 ? 40 : 36;
+  static constexpr size_t LDS = lds_with(LDV);
+  static constexpr bool fits = LDS <= 160 * 1024;
+  // Probability orders 1..K as a hi + lo pair of 16-bit operands (two value-product MFMAs each)
+  // from degree 5 on. The higher probability coefficients exceed the output coefficients they
+  // cancel into by about the factor 10 at high degree, so one rounding of them costs up to 4e-2 of
+  // the output order; the pair keeps it near 1e-3. Up to degree 4 one rounding stays below 5e-3.
+  static constexpr bool split = K >= 5;
+  // The wave's query tile stays in registers when accumulators, tile and working set fit.
+  static constexpr bool q_regs = SL == 1 && (K + 1) * DB * 4 + (K + 1) * DC * 4 + 16 * (K + 1) + 64 +
+                                                    (split ? 4 * K : 0) <= 448;
+};
+
+// Eight 16-bit values (one 16-byte load) at p, or zeros.
+template <typename T>
+__device__ __forceinline__ u32x4 attn_half_load8(const T* p, bool ok) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  return ok ? v : z;
+}
+
+template <typename T, int K, int D>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_kernel(
+    CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O, MPtrs<float> LSE,
+    int L, int S, const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
+  using Sh = AttnHalfShape<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = Sh::KB, DC = Sh::DC, DB = Sh::DB, LDK = Sh::LDK, LDV = Sh::LDV;
+  constexpr float kNegInf = -__builtin_huge_valf();
+  constexpr float kSlack = MM::kSlack;
+  static_assert(Sh::fits, "K/V tiles exceed LDS");
+
+  constexpr int SL = Sh::SL, DS = Sh::DS;
+  __shared__ __align__(16) T Ks[K + 1][KB][LDK];
+  __shared__ __align__(16) T Vt[K + 1][DS][LDV];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;   // query column (score and output accumulators); key / head-dim row of A operands
+  const int g = lane / 16;   // lane group
+  int64_t head;
+  int q_block, slice = 0;
+  if constexpr (SL == 1) {
+    attn_work_item(L, causal, head, q_block);
+  } else {
+    // slices fastest, then heads, heaviest query blocks first
+    const int nqb = (L + kAttnBM - 1) / kAttnBM;
+    const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SL);
+    const int64_t t = blockIdx.x / SL;
+    slice = static_cast<int>(blockIdx.x % SL);
+    head = t % bh;
+    q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
+  }
+  const int d0 = slice * DS;   // first output head dim of this workgroup
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qrow = (head * L + (q_ok ? my_q : 0)) * D;
+
+  // Query operand of order o, chunk dc: Q[my_q][32 dc + 8 g .. + 7] (zero past D, L or the orders given).
+  auto load_q = [&](int o, int dc) -> u32x4 {
+    const bool in = q_ok && o < q_orders && 32 * dc + 8 * g < D;
+    return attn_half_load8<T>(order_ptr<K>(Q, o < q_orders ? o : 0) + qrow + (in ? 32 * dc + 8 * g : 0), in);
+  };
+  u32x4 qreg[Sh::q_regs ? K + 1 : 1][Sh::q_regs ? DC : 1];
+  if constexpr (Sh::q_regs) {
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) qreg[o][dc] = load_q(o, dc);
+  }
+
+  floatx4 acc_o[K + 1][DB];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[o][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_used = kNegInf;
+  float lsum[K + 1];   // this lane's partial row sums (its keys only)
+#pragma unroll
+  for (int o = 0; o <= K; ++o) lsum[o] = 0.f;
+
+  // key range: causal and mask-range bounds, lo rounded down to a 32-key block
+  int lo = 0, hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / KB * KB;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+  }
+
+  for (int kb0 = lo; kb0 < hi; kb0 += KB) {
+    uint8_t mbyte[2][4];   // mask bytes of this lane's eight keys, read ahead of the staging loads
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mbyte[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    __syncthreads();   // the previous block's products are done with the tiles
+    // ---- stage K rows kb0 .. kb0 + 31 of every order, row-major (zero past S / the orders given) ----
+    {
+      constexpr int VPR = D / 8;   // 16-byte vectors per row
+      for (int idx = threadIdx.x; idx < (K + 1) * KB * VPR; idx += kAttnWaves * kWave) {
+        const int o = idx / (KB * VPR);
+        const int rem = idx % (KB * VPR);
+        const int r = rem / VPR, cv = (rem % VPR) * 8;
+        const int key = kb0 + r;
+        const bool in = key < S && o < k_orders;
+        const u32x4 v = attn_half_load8<T>(order_ptr<K>(Kp, o < k_orders ? o : 0) +
+                                               (head * S + min(key, S - 1)) * D + cv, in);
+        *reinterpret_cast<u32x4*>(&Ks[o][r][cv]) = v;
+      }
+    }
+    // ---- stage V rows transposed: Vt[o][dim - d0][key] for the slice's dims, four keys x eight dims per step ----
+    {
+      constexpr int DV = DS / 8;
+      for (int idx = threadIdx.x; idx < (K + 1) * (KB / 4) * DV; idx += kAttnWaves * kWave) {
+        const int o = idx / ((KB / 4) * DV);
+        const int rem = idx % ((KB / 4) * DV);
+        const int kq = rem % (KB / 4), dv = rem / (KB / 4);   // key quad fastest: adjacent lanes, adjacent keys
+        const T* src = order_ptr<K>(Vp, o < v_orders ? o : 0);
+        u32x4 x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kb0 + 4 * kq + j;
+          x[j] = attn_half_load8<T>(src + (head * S + min(key, S - 1)) * D + d0 + 8 * dv, key < S && o < v_orders);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // dim 8 dv + e of keys 4 kq .. 4 kq + 3: the low or high halves of word e / 2
+          const int w = e / 2;
+          uint32_t lo_w, hi_w;
+          if (e % 2 == 0) {
+            lo_w = (x[0][w] & 0xffffu) | (x[1][w] << 16);
+            hi_w = (x[2][w] & 0xffffu) | (x[3][w] << 16);
+          } else {
+            lo_w = (x[0][w] >> 16) | (x[1][w] & 0xffff0000u);
+            hi_w = (x[2][w] >> 16) | (x[3][w] & 0xffff0000u);
+          }
+          *reinterpret_cast<uint2*>(&Vt[o][8 * dv + e][4 * kq]) = make_uint2(lo_w, hi_w);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T for the two 16-key halves (keys x queries) ----
+    floatx4 sc[2][K + 1];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int o = 0; o <= K; ++o) sc[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      u32x4 qa[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        if constexpr (Sh::q_regs) qa[o] = qreg[o][dc];
+        else qa[o] = load_q(o, dc);
+      }
+      const bool din = 32 * dc + 8 * g < D;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        u32x4 kop[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&Ks[o][16 * kh + c][din ? 32 * dc + 8 * g : 0]);
+          const u32x4 z = {0u, 0u, 0u, 0u};
+          kop[o] = din ? v : z;
+        }
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[kh][k] = MM::mma(kop[k - a], qa[a], sc[kh][k]);
+      }
+    }
+
+    // ---- mask, online maximum of the constant order, exponential series ----
+    bool valid[2][4];
+    float s0[2][4];
+    float bmax = kNegInf;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        bool ok = q_ok && key < S;
+        if (causal) ok = ok && key <= my_q;
+        if (mask != nullptr) ok = ok && mbyte[kh][r] != 0;
+        valid[kh][r] = ok;
+        s0[kh][r] = ok ? sc[kh][0][r] * scale : kNegInf;
+        bmax = fmaxf(bmax, s0[kh][r]);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
+    if (__any(raise)) {
+      const float m_new = raise ? bmax : m_used;
+      const float alpha = (raise && m_used != kNegInf) ? exp_fast(m_used - m_new) : (raise ? 0.f : 1.f);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        lsum[o] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+      }
+      m_used = m_new;
+    }
+    u32x4 pb[K + 1];   // probability operands: slots 0..3 keys 4g + r, slots 4..7 keys 16 + 4g + r
+    u32x4 pl[Sh::split ? K + 1 : 1];   // lo parts of orders 1..K (split)
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      float w[K + 1][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = valid[kh][r] ? exp_fast(s0[kh][r] - m_used) : 0.f;
+        float sk[K + 1], e[K + 1];
+#pragma unroll
+        for (int o = 1; o <= K; ++o) sk[o] = sc[kh][o][r] * scale;
+        e[0] = 1.f;
+#pragma unroll
+        for (int k = 1; k <= K; ++k) {
+          float t = 0.f;
+#pragma unroll
+          for (int j = 1; j <= k; ++j) t += (static_cast<float>(j) * sk[j]) * e[k - j];
+          e[k] = t * (1.f / static_cast<float>(k));
+        }
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          w[o][r] = p * e[o];
+          lsum[o] += w[o][r];
+        }
+      }
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const uint32_t w01 = MM::pack2(w[o][0], w[o][1]), w23 = MM::pack2(w[o][2], w[o][3]);
+        pb[o][2 * kh] = w01;
+        pb[o][2 * kh + 1] = w23;
+        if constexpr (Sh::split) {
+          if (o >= 1) {   // the rounding residuals as the lo operand
+            pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
+            pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
+          }
+        }
+      }
+    }
+
+    // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T (head dim x queries), 32 keys per MFMA ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      u32x4 vop[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const uint2 first = *reinterpret_cast<const uint2*>(&Vt[o][16 * db + c][4 * g]);
+        const uint2 second = *reinterpret_cast<const uint2*>(&Vt[o][16 * db + c][16 + 4 * g]);
+        vop[o] = u32x4{first.x, first.y, second.x, second.y};
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+#pragma unroll
+        for (int a = 0; a <= k; ++a) acc_o[k][db] = MM::mma(vop[k - a], pb[a], acc_o[k][db]);
+        if constexpr (Sh::split) {
+#pragma unroll
+          for (int a = 1; a <= k; ++a) acc_o[k][db] = MM::mma(vop[k - a], pl[a], acc_o[k][db]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: row sums over the lane groups, series quotient, output and lse series ----
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  }
+  if (!q_ok) return;
+  const bool empty = !(lsum[0] > 0.f);
+  const float inv_l0 = empty ? 0.f : 1.f / lsum[0];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    float out[4][K + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+        float t = acc_o[k][db][r];
+#pragma unroll
+        for (int j = 1; j <= k; ++j) t -= lsum[j] * out[r][k - j];
+        out[r][k] = t * inv_l0;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k <= K; ++k) {
+      // head dims 16 db + 4 g .. + 3 of this query: one 8-byte store
+      *reinterpret_cast<uint2*>(O.p[k] + (head * L + my_q) * D + d0 + 16 * db + 4 * g) =
+          make_uint2(MM::pack2(out[0][k], out[1][k]), MM::pack2(out[2][k], out[3][k]));
+    }
+  }
+  if (LSE.p[0] != nullptr && g == 0 && slice == 0) {
+    const int64_t at = head * L + my_q;
+    if (empty) {
+      LSE.p[0][at] = __builtin_huge_valf();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][at] = 0.f;
+    } else {
+      float lse[K + 1], nrm[K + 1];
+      lse[0] = m_used + logf(lsum[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        float t = nrm[k];
+#pragma unroll
+        for (int j = 1; j < k; ++j) t -= (static_cast<float>(j) / static_cast<float>(k)) * lse[j] * nrm[k - j];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+    }
+  }
+}
+
+template <typename T, int K, int D>
+static int launch_attention_half_kd(const AttnArgs& a) {
+  if constexpr (!AttnHalfShape<K, D>::fits) {
+    pt_host::set_error("Taylor attention: degree and head dim exceed the LDS budget for this dtype");
+    return PT_UNSUPPORTED;
+  } else {
+    // 16-byte operand loads and 8-byte output stores
+    bool aligned = true;
+    for (int i = 0; i < a.q_orders; ++i) aligned = aligned && pt_host::aligned16(a.q[i]);
+    for (int i = 0; i < a.k_orders; ++i) aligned = aligned && pt_host::aligned16(a.k[i]);
+    for (int i = 0; i < a.v_orders; ++i) aligned = aligned && pt_host::aligned16(a.v[i]);
+    for (int i = 0; i <= K; ++i) aligned = aligned && (reinterpret_cast<uintptr_t>(a.out[i]) % 8 == 0);
+    PT_REQUIRE(aligned, PT_INVALID_ARGUMENT,
+               "Taylor attention: 16-bit operands must be 16-byte aligned and outputs 8-byte aligned");
+    CPtrs<T> q{}, k{}, v{};
+    MPtrs<T> o{};
+    MPtrs<float> lse{};
+    for (int i = 0; i < a.q_orders; ++i) q.p[i] = static_cast<const T*>(a.q[i]);
+    for (int i = 0; i < a.k_orders; ++i) k.p[i] = static_cast<const T*>(a.k[i]);
+    for (int i = 0; i < a.v_orders; ++i) v.p[i] = static_cast<const T*>(a.v[i]);
+    for (int i = 0; i <= K; ++i) {
+      o.p[i] = static_cast<T*>(a.out[i]);
+      if (a.lse != nullptr) lse.p[i] = static_cast<float*>(a.lse[i]);
+    }
+    const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * AttnHalfShape<K, D>::SL));
+    taylor_attention_fwd_half_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+        q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),
+        a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
+    PT_LAUNCH_CHECK();
+    return PT_OK;
+  }
+}
+
+template <typename T, int K>
+static int launch_attention_half_k(const AttnArgs& a) {
+  switch (a.d) {
+    case 16: return launch_attention_half_kd<T, K, 16>(a);
+    case 32: return launch_attention_half_kd<T, K, 32>(a);
+    case 64: return launch_attention_half_kd<T, K, 64>(a);
+    case 128: return launch_attention_half_kd<T, K, 128>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention: head dim must be 16, 32, 64 or 128");
+  return PT_UNSUPPORTED;
+}
+
+template <typename T>
+int launch_attention_half(const AttnArgs& a) {
+  switch (a.degree) {
+    case 0: return launch_attention_half_k<T, 0>(a);
+    case 1: return launch_attention_half_k<T, 1>(a);
+    case 2: return launch_attention_half_k<T, 2>(a);
+    case 3: return launch_attention_half_k<T, 3>(a);
+    case 4: return launch_attention_half_k<T, 4>(a);
+    case 5: return launch_attention_half_k<T, 5>(a);
+    case 6: return launch_attention_half_k<T, 6>(a);
+    case 7: return launch_attention_half_k<T, 7>(a);
+    case 8: return launch_attention_half_k<T, 8>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention: degree outside 0..PT_MAX_DEGREE");
+  return PT_UNSUPPORTED;
+}
+
+}  // namespace pt

@@ -1,0 +1,197 @@
+"""Taylor attention with bfloat16 / float16 operands (GPU).
+
+The 16-bit kernel takes Q, K, V as stored into 16x16x32 MFMAs with fp32
+accumulation; the probability series is rounded to the storage type as the
+value product's operand, the output once at the end. The oracle (the
+reference's plain-range decomposition) runs in float64 on the same stored
+16-bit inputs, upcast. Tolerance: the north star's bf16-input/fp32-accumulate
+bound, max |got - want| / max |want| <= 2e-2 per order; the reference's own
+half-type test compares bf16 with float32 at 2e-2 (outputs) and 5e-2 (gradients),
+/root/reference/tests/test_fused_kernels.py:64-72, mirrored below.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from oracle import paths
+from polytensors_amd import PolyTensor, _fused_attention, _ops
+from tests.jets import rel_err
+
+pytestmark = pytest.mark.gpu
+
+HALF = [torch.bfloat16, torch.float16]
+TOL = 2e-2
+
+
+def _series(shape, degree, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(shape, generator=g, dtype=torch.float64) * scale * 0.5 ** k).to(dtype)
+            for k in range(degree + 1)]
+
+
+def _poly(cs):
+    return PolyTensor(tuple(c.cuda() for c in cs))
+
+
+def _up(cs):
+    return [c.double() for c in cs]
+
+
+def _window_mask(L, window):
+    i = torch.arange(L)
+    return (i[:, None] >= i[None, :]) & (i[:, None] - i[None, :] <= window)
+
+
+def _check(got, want, tol=TOL):
+    for k, (a, b) in enumerate(zip(got, want)):
+        err = rel_err(a.cpu(), b)
+        assert err <= tol, f"order {k}: {err:.3e}"
+
+
+def _run(q, k, v, **kwargs):
+    with torch.no_grad(), PolyTensor.plain_range():
+        return F.scaled_dot_product_attention(q, k, v, **kwargs)
+
+
+@pytest.mark.parametrize("dtype", HALF)
+@pytest.mark.parametrize("causal,window", [(True, None), (False, 37), (False, None)])
+@pytest.mark.parametrize("degree", [1, 4])
+def test_matches_oracle(monkeypatch, dtype, causal, window, degree):
+    calls = []
+    original = _ops.taylor_attention_fwd
+    monkeypatch.setattr(_ops, "taylor_attention_fwd", lambda *a, **k: calls.append(1) or original(*a, **k))
+    shape = (2, 3, 150, 64)
+    Q, K, V = (_series(shape, degree, 10 + i, dtype) for i in range(3))
+    mask = None if window is None else _window_mask(150, window)
+    q, k, v = _poly(Q), _poly(K), _poly(V)
+    with PolyTensor.plain_range():
+        assert _fused_attention.eligible(q, k, v, attn_mask=None if mask is None else mask.cuda(), is_causal=causal)
+    out = _run(q, k, v, attn_mask=None if mask is None else mask.cuda(), is_causal=causal)
+    assert calls == [1] and out.degree == degree and out.dtype == dtype
+    want = oracle.attention(_up(Q), _up(K), _up(V), attn_mask=mask, is_causal=causal)
+    _check(out.coeffs, want)
+
+
+@pytest.mark.parametrize("dtype", HALF)
+@pytest.mark.parametrize("degree", [0, 2, 3, 5, 6, 7, 8])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_every_degree_and_head_dim(dtype, degree, d):
+    # head dim 128 from degree 5 on splits the output head dims over workgroups
+    shape = (1, 2, 70, d)
+    Q, K, V = (_series(shape, degree, 20 + i, dtype) for i in range(3))
+    out = _run(_poly(Q), _poly(K), _poly(V), is_causal=True)
+    _check(out.coeffs, oracle.attention(_up(Q), _up(K), _up(V), is_causal=True))
+
+
+@pytest.mark.parametrize("dtype", HALF)
+def test_lse_series_and_plain_operands(dtype):
+    degree, shape = 3, (1, 2, 96, 32)
+    Q, V = (_series(shape, degree, 30 + i, dtype) for i in range(2))
+    Kp = _series(shape, 0, 32, dtype)[0]
+    q, v = _poly(Q), _poly(V)
+    out = _run(q, Kp.cuda(), v, is_causal=True)
+    Ks = [Kp.double()] + [torch.zeros(shape, dtype=torch.float64) for _ in range(degree)]
+    _check(out.coeffs, oracle.attention(_up(Q), Ks, _up(V), is_causal=True))
+    flat = [c.reshape(2, 96, 32).cuda() for c in Q]
+    _, lse = _ops.taylor_attention_fwd(flat, [Kp.reshape(2, 96, 32).cuda()], [c.reshape(2, 96, 32).cuda() for c in V],
+                                       None, True, 1 / math.sqrt(32), degree)
+    assert lse.dtype == torch.float32
+    scores = oracle.matmul([c.double() / math.sqrt(32) for c in Q], [Kp.double().transpose(-1, -2)])
+    causal = ~torch.ones(96, 96, dtype=torch.bool).tril()
+    scores = [s.masked_fill(causal, -math.inf) if o == 0 else s.masked_fill(causal, 0.0) for o, s in enumerate(scores)]
+    want = paths.logsumexp(scores, -1)
+    _check([x.reshape(1, 2, 96) for x in lse.unbind(0)], want)
+
+
+@pytest.mark.parametrize("dtype", HALF)
+@pytest.mark.parametrize("L,S", [(1, 16), (70, 33), (33, 70), (130, 47)])
+def test_cross_lengths_and_an_empty_row(dtype, L, S):
+    Q = _series((1, 2, L, 64), 2, 40, dtype)
+    K, V = (_series((1, 2, S, 64), 2, 41 + i, dtype) for i in range(2))
+    g = torch.Generator().manual_seed(43)
+    mask = torch.rand(L, S, generator=g) < 0.6
+    mask[L // 2] = False
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=mask.cuda())
+    want = oracle.attention(_up(Q), _up(K), _up(V), attn_mask=mask)
+    empty = ~mask.any(-1)   # the plain-range rule gives NaN there; the kernels 0 (the fused convention)
+    want = [torch.where(empty[:, None], torch.zeros_like(w), w) for w in want]
+    for c in out.coeffs:
+        assert torch.equal(c.cpu()[..., empty, :].float(), torch.zeros_like(c.cpu()[..., empty, :]).float())
+    _check(out.coeffs, want)
+
+
+def test_float16_large_scores_do_not_overflow():
+    # float16 keeps the exact running maximum (probabilities <= 1): order-0 scores near 40 stay finite
+    degree, shape = 3, (1, 1, 64, 64)
+    Q, K, V = (_series(shape, degree, 50 + i, torch.float16) for i in range(3))
+    Q[0], K[0] = (Q[0].double() * 6).half(), (K[0].double() * 6).half()
+    out = _run(_poly(Q), _poly(K), _poly(V), is_causal=True)
+    assert all(torch.isfinite(c).all() for c in out.coeffs)
+    _check(out.coeffs, oracle.attention(_up(Q), _up(K), _up(V), is_causal=True))
+
+
+def test_bfloat16_close_to_float32_with_gradients():
+    # /root/reference/tests/test_fused_kernels.py:64-72 at degree 1 (and here also degree 3): bf16 vs
+    # float32 outputs within 2e-2 and gradient series within 5e-2 (wrapper autograd, G = (1, 0, ...))
+    for degree in (1, 3):
+        shape = (1, 2, 256, 128)
+        base = [_series(shape, degree, 60 + i, torch.float32, scale=0.5) for i in range(3)]
+        results = {}
+        for dtype in (torch.bfloat16, torch.float32):
+            xs = [PolyTensor(tuple(c.to(dtype).cuda() for c in s), requires_grad=True) for s in base]
+            with PolyTensor.retain_wrappers(), PolyTensor.plain_range():
+                out = F.scaled_dot_product_attention(*xs, is_causal=True)
+                out.backward(PolyTensor.constant(torch.ones_like(out.value), degree))
+            results[dtype] = ([c.float() for c in out.coeffs], [[c.float() for c in x.grad.coeffs] for x in xs])
+        (ob, gb), (of, gf) = results[torch.bfloat16], results[torch.float32]
+        for a, b in zip(ob, of):
+            assert rel_err(a.cpu(), b.cpu()) < 2e-2
+        for x_b, x_f in zip(gb, gf):
+            for a, b in zip(x_b, x_f):
+                assert rel_err(a.cpu(), b.cpu()) < 5e-2
+
+
+@pytest.mark.parametrize("dtype", HALF)
+def test_gradient_series_matches_oracle(dtype):
+    degree, shape = 2, (1, 2, 80, 32)
+    Q, K, V, G = (_series(shape, degree, 70 + i, dtype) for i in range(4))
+    flat = lambda cs: [c.reshape(2, 80, 32).cuda() for c in cs]
+    out, lse = _ops.taylor_attention_fwd(flat(Q), flat(K), flat(V), None, True, 1 / math.sqrt(32), degree)
+    dq, dk, dv = _ops.attention_gradient_series(flat(Q), flat(K), flat(V), out, lse, flat(G), None, True,
+                                                1 / math.sqrt(32))
+    assert dq.dtype == dtype
+    # the oracle's VJP series on the same stored inputs (its output series recomputed in float64)
+    want = oracle.attention_backward(_up(Q), _up(K), _up(V), _up(G), is_causal=True)
+    for got, w in zip((dq, dk, dv), want):
+        _check([c.reshape(shape) for c in got.unbind(0)], w, tol=5e-2)
+
+
+@pytest.mark.parametrize("dtype", HALF)
+def test_full_size_config3_one_head(dtype):
+    # benchmark config 3's shape (B=4 H=16 L=2048 d=128, K=4, causal, line inputs) in 16-bit storage;
+    # head 37 of the full launch against the oracle, and linearity in the value series over all heads
+    B, H, L, d, degree = 4, 16, 2048, 128, 4
+    g = torch.Generator(device="cuda").manual_seed(2)
+
+    def line():
+        base = (torch.randn(B * H, L, d, generator=g, device="cuda") / math.sqrt(d)).to(dtype)
+        direction = torch.randn(B * H, L, d, generator=g, device="cuda").to(dtype)
+        return [base, direction] + [torch.zeros_like(base) for _ in range(degree - 1)]
+
+    q, k, v, w = line(), line(), line(), line()
+    scale = 1 / math.sqrt(d)
+    out, _ = _ops.taylor_attention_fwd(q, k, v, None, True, scale, degree)
+    head = 37
+    want = oracle.attention([c[head].cpu().double() for c in q], [c[head].cpu().double() for c in k],
+                            [c[head].cpu().double() for c in v], is_causal=True)
+    _check([o[head] for o in out], want)
+    o_w, _ = _ops.taylor_attention_fwd(q, k, w, None, True, scale, degree)
+    o_sum, _ = _ops.taylor_attention_fwd(q, k, [a + b for a, b in zip(v, w)], None, True, scale, degree)
+    lhs, rhs = o_sum.double(), out.double() + o_w.double()
+    for order in range(degree + 1):
+        err = ((lhs[order] - rhs[order]).abs().amax(dim=(1, 2)) / rhs[order].abs().amax(dim=(1, 2))).max().item()
+        assert err <= 2 * TOL, f"order {order}: {err:.3e}"
