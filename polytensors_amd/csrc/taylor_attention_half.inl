@@ -413,6 +413,373 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined 16-bit kernel for full-order operands, a key length that is a
+// multiple of 32, and two K/V tile buffers within LDS (no head-dim slices):
+// * the K and V tiles of key block j+1 are fetched by LDS DMA
+//   (global_load_lds_dwordx4) into the second buffer while block j's value
+//   products run: no staging registers, one barrier per key block;
+// * both tiles are stored row-major and unpadded, the 16-byte chunks of a row
+//   XOR-swizzled by the row so that the operand reads hit 64 distinct banks:
+//   the K operand is one 16-byte read per lane (16 key rows, one chunk each);
+//   the V^T operand comes straight out of the row-major V tile through two
+//   ds_read_b64_tr_b16 transpose reads. Within each 16-lane group, the lane
+//   4a + b of a transpose read receives element b of the 8-byte pieces addressed
+//   by lanes a, a+4, a+8, a+12 (checked on gfx950 with a lane-layout probe);
+//   so when lane 4j + a of group g addresses V[4g + j][16 db + 4a ..], lane c of
+//   the group receives V[4g + j][16 db + c] for j = 0..3: four keys of its head
+//   dim, the operand slots of the value product.
+template <int K, int D>
+struct AttnHalfPipe {
+  static constexpr int KB = 32;
+  static constexpr int CH = D * 2 / 16;                 // 16-byte chunks per row
+  static constexpr int RPS = 1024 / (D * 2);            // rows per 1 KB DMA segment
+  static constexpr int SEGS = KB / RPS;                 // segments per order tile
+  static constexpr int IT = (SEGS + kAttnWaves - 1) / kAttnWaves;   // per wave and order tile
+  static constexpr int OPS = 2 * (K + 1) * IT;          // DMA operations per wave and key block
+  static constexpr int RSH = CH >= 16 ? 0 : CH == 8 ? 1 : CH == 4 ? 2 : 3;   // log2(16 / CH)
+  static constexpr size_t LDS = 2ull * 2 * (K + 1) * KB * D * 2;
+  static constexpr bool split = AttnHalfShape<K, D>::split;
+  // registers of the accumulators, query tile, scores, probability operands (hi, lo) and
+  // one set of K and V operands; the operand reads run one step ahead where a second set fits
+  static constexpr int regs = (K + 1) * (D / 16 * 4 + (D + 31) / 32 * 4 + 8 + 4 + 8 + 8) + (split ? 4 * K : 0);
+  static constexpr bool ahead = regs + (K + 1) * 16 <= 384;
+  static constexpr bool fits = LDS <= 160 * 1024 && AttnHalfShape<K, D>::SL == 1 && regs <= 400;
+  // swizzles (physical chunk = logical chunk ^ f(row)): K reads take one chunk of 16 rows,
+  // V transpose reads 8-byte pieces of 2 chunks of 8 rows per 32 lanes
+  __device__ __forceinline__ static int fk(int row) { return (row >> RSH) & (CH - 1); }
+  __device__ __forceinline__ static int fv(int row) { return CH >= 4 ? 2 * ((row >> RSH) & (CH / 2 - 1)) : 0; }
+};
+
+// DMA operation i of this wave's share of key block kb0 into one buffer
+// (tiles[kv][order][row][d]); i is a compile-time constant at every call.
+// A buffer load into LDS (buffer_load_dwordx4 ... lds: lane l's 16 bytes land
+// at M0 + 16 l): the operand base in the resource, the block's offset (below
+// 2^31 bytes, checked by the launcher) as the scalar offset, a 32-bit lane
+// offset. It is written as inline assembly so that the compiler's wait
+// insertion, which cannot tell the two LDS buffers apart, does not wait for
+// this DMA before every read of the other buffer; the kernel waits for it
+// itself (s_waitcnt vmcnt(0) before the barrier of the next key block).
+// Vector loads complete in issue order, so the compiler's own counted waits
+// for ordinary loads stay sufficient with these loads in flight.
+typedef int AttnInt4 __attribute__((ext_vector_type(4)));
+
+template <typename T, int K, int D>
+__device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], const CPtrs<T>& Kp,
+                                                   const CPtrs<T>& Vp, int bytes, int64_t head, int S, int kb0,
+                                                   int lane, int wave, int i) {
+  using P = AttnHalfPipe<K, D>;
+  constexpr int CH = P::CH, RPS = P::RPS, SEGS = P::SEGS, IT = P::IT;
+  const int kv = i / ((K + 1) * IT), o = (i / IT) % (K + 1), it = i % IT;
+  const int seg = it * kAttnWaves + wave;
+  if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
+  const int row = seg * RPS + lane / CH;
+  const int lch = (lane % CH) ^ (kv ? P::fv(row) : P::fk(row));
+  const uint64_t base = reinterpret_cast<uint64_t>(kv ? Vp.p[o] : Kp.p[o]);
+  // raw buffer resource: 48-bit base, stride 0, num_records = operand bytes, dword 3 = 0x00020000
+  const AttnInt4 rsrc = {static_cast<int>(base), static_cast<int>((base >> 32) & 0xffff), bytes, 0x00020000};
+  const int soff = static_cast<int>((head * S + kb0) * D * static_cast<int64_t>(sizeof(T)));
+  const int voff = (row * D + lch * 8) * static_cast<int>(sizeof(T));
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) void*)&buf[kv][o][seg * RPS][0]));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory", "m0");
+}
+
+typedef short AttnShortx4 __attribute__((ext_vector_type(4)));
+
+template <typename T, int K, int D>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S, int kv_bytes,
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
+  using P = AttnHalfPipe<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = P::KB, DC = (D + 31) / 32, DB = D / 16, OPS = P::OPS;
+  constexpr float kNegInf = -__builtin_huge_valf();
+  constexpr float kSlack = MM::kSlack;
+  static_assert(P::LDS <= 160 * 1024, "two K/V tiles exceed LDS");
+
+  // two buffers of [0 = K, 1 = V][order][key row][head dim], rows unpadded and chunk-swizzled
+  using Tiles = T[2][K + 1][KB][D];
+  __shared__ __attribute__((aligned(16))) Tiles tiles[2];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c = lane % 16;
+  const int g = lane / 16;
+  int64_t head;
+  int q_block;
+  attn_work_item(L, causal, head, q_block);
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
+
+  // the wave's query tile of every order, resident in registers
+  u32x4 qreg[K + 1][DC];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      const bool din = 32 * dc + 8 * g < D;
+      qreg[o][dc] = attn_half_load8<T>(Q.p[o] + qrow + (din ? 32 * dc + 8 * g : 0), din);
+    }
+
+  int lo = 0, hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / KB * KB;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+  }
+  // a workgroup whose rows admit no key keeps one (fully masked) block, so the
+  // pipeline always has a first block (the launcher requires S >= 32)
+  if (hi <= lo) {
+    lo = 0;
+    hi = KB;
+  }
+  const int nblocks = (hi - lo + KB - 1) / KB;
+  const int last_kb0 = lo + (nblocks - 1) * KB;
+
+  floatx4 acc_o[K + 1][DB];
+#pragma unroll
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[o][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_used = kNegInf;
+  float lsum[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) lsum[o] = 0.f;
+
+  // the first block's DMA is issued after the query loads: LDS-DMA loads pending
+  // beside ordinary loads make the compiler wait for every load in flight
+#pragma unroll
+  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, kv_bytes, head, S, lo, lane, wave, i);
+
+  // key block j from buffer cur; the DMA of block j+1 into nxt
+  auto block = [&](Tiles& cur, Tiles& nxt, int j) __attribute__((always_inline)) {
+    const int kb0 = lo + j * KB;
+    uint8_t mbyte[2][4];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mbyte[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and the mask bytes)
+    __syncthreads();                 // ... and every wave's; block j-1's buffer is free
+
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves; chunk reads one step ahead ----
+    floatx4 sc[2][K + 1];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int o = 0; o <= K; ++o) sc[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load_k = [&](u32x4 (&dst)[K + 1], int step) {
+      const int dc = step / 2, kh = step % 2;
+      const int row = 16 * kh + c;
+      const bool din = 32 * dc + 8 * g < D;
+      const int pch = ((4 * dc + g) & (P::CH - 1)) ^ P::fk(row);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&cur[0][o][row][pch * 8]);
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        dst[o] = din ? v : z;
+      }
+    };
+    constexpr int KSTEPS = 2 * DC;
+    constexpr int NK = P::ahead ? 2 : 1;
+    u32x4 kop[NK][K + 1];
+    if constexpr (P::ahead) load_k(kop[0], 0);
+#pragma unroll
+    for (int st = 0; st < KSTEPS; ++st) {
+      if constexpr (P::ahead) {
+        if (st + 1 < KSTEPS) load_k(kop[(st + 1) % NK], st + 1);
+      } else {
+        load_k(kop[0], st);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const int dc = st / 2, kh = st % 2;
+      const int cur = P::ahead ? st % NK : 0;
+#pragma unroll
+      for (int k = 0; k <= K; ++k)
+#pragma unroll
+        for (int a = 0; a <= k; ++a) sc[kh][k] = MM::mma(kop[cur][k - a], qreg[a][dc], sc[kh][k]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- mask, online maximum of the constant order, exponential series ----
+    bool valid[2][4];
+    float s0[2][4];
+    float bmax = kNegInf;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        bool ok = q_ok && key < hi;
+        if (causal) ok = ok && key <= my_q;
+        if (mask != nullptr) ok = ok && mbyte[kh][r] != 0;
+        valid[kh][r] = ok;
+        s0[kh][r] = ok ? sc[kh][0][r] * scale : kNegInf;
+        bmax = fmaxf(bmax, s0[kh][r]);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
+    if (__any(raise)) {
+      const float m_new = raise ? bmax : m_used;
+      const float alpha = (raise && m_used != kNegInf) ? exp_fast(m_used - m_new) : (raise ? 0.f : 1.f);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        lsum[o] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+      }
+      m_used = m_new;
+    }
+    u32x4 pb[K + 1];
+    u32x4 pl[P::split ? K + 1 : 1];   // lo parts of orders 1..K (split)
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      float w[K + 1][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = valid[kh][r] ? exp_fast(s0[kh][r] - m_used) : 0.f;
+        float sk[K + 1], e[K + 1];
+#pragma unroll
+        for (int o = 1; o <= K; ++o) sk[o] = sc[kh][o][r] * scale;
+        e[0] = 1.f;
+#pragma unroll
+        for (int k = 1; k <= K; ++k) {
+          float t = 0.f;
+#pragma unroll
+          for (int i = 1; i <= k; ++i) t += (static_cast<float>(i) * sk[i]) * e[k - i];
+          e[k] = t * (1.f / static_cast<float>(k));
+        }
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          w[o][r] = p * e[o];
+          lsum[o] += w[o][r];
+        }
+      }
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const uint32_t w01 = MM::pack2(w[o][0], w[o][1]), w23 = MM::pack2(w[o][2], w[o][3]);
+        pb[o][2 * kh] = w01;
+        pb[o][2 * kh + 1] = w23;
+        if constexpr (P::split) {
+          if (o >= 1) {
+            pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
+            pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
+          }
+        }
+      }
+    }
+
+    // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T: V^T operands by transpose reads, one step ahead;
+    // a share of the next block's DMA into the other buffer per step (the last block re-loads
+    // itself, so there is no branch) ----
+    const int next_kb0 = min(kb0 + KB, last_kb0);
+    const int tj = c / 4, ta = c % 4;   // this lane's piece: row 4g + tj (+16), head dims 16 db + 4 ta
+    auto load_v = [&](u32x4 (&dst)[K + 1], int db) {
+      const int row0 = 4 * g + tj, row1 = 16 + 4 * g + tj;
+      const int lch = 2 * db + ta / 2;
+      const int off0 = ((lch ^ P::fv(row0)) * 8) + 4 * (ta % 2);
+      const int off1 = ((lch ^ P::fv(row1)) * 8) + 4 * (ta % 2);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        typedef __attribute__((address_space(3))) AttnShortx4 lds_x4;
+        const AttnShortx4 first = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row0][off0]));
+        const AttnShortx4 second = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row1][off1]));
+        const uint2 f = __builtin_bit_cast(uint2, first), s2 = __builtin_bit_cast(uint2, second);
+        dst[o] = u32x4{f.x, f.y, s2.x, s2.y};
+      }
+    };
+    constexpr int NV = P::ahead ? 2 : 1;
+    u32x4 vop[NV][K + 1];
+    if constexpr (P::ahead) load_v(vop[0], 0);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      if constexpr (P::ahead) {
+        if (db + 1 < DB) load_v(vop[(db + 1) % NV], db + 1);
+      } else {
+        load_v(vop[0], db);
+      }
+#pragma unroll
+      for (int i = db * OPS / DB; i < (db + 1) * OPS / DB; ++i)
+        attn_half_issue_op<T, K, D>(nxt, Kp, Vp, kv_bytes, head, S, next_kb0, lane, wave, i);
+      __builtin_amdgcn_sched_barrier(0);
+      const int cur = P::ahead ? db % NV : 0;
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+#pragma unroll
+        for (int a = 0; a <= k; ++a) acc_o[k][db] = MM::mma(vop[cur][k - a], pb[a], acc_o[k][db]);
+        if constexpr (P::split) {
+#pragma unroll
+          for (int a = 1; a <= k; ++a) acc_o[k][db] = MM::mma(vop[cur][k - a], pl[a], acc_o[k][db]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int j = 0; j < nblocks; ++j) block(tiles[j & 1], tiles[(j + 1) & 1], j);
+  __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMA has landed before the workgroup ends
+
+  // ---- epilogue ----
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  }
+  if (!q_ok) return;
+  const bool empty = !(lsum[0] > 0.f);
+  const float inv_l0 = empty ? 0.f : 1.f / lsum[0];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    float out[4][K + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+        float t = acc_o[k][db][r];
+#pragma unroll
+        for (int jj = 1; jj <= k; ++jj) t -= lsum[jj] * out[r][k - jj];
+        out[r][k] = t * inv_l0;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+      *reinterpret_cast<uint2*>(O.p[k] + (head * L + my_q) * D + 16 * db + 4 * g) =
+          make_uint2(MM::pack2(out[0][k], out[1][k]), MM::pack2(out[2][k], out[3][k]));
+  }
+  if (LSE.p[0] != nullptr && g == 0) {
+    const int64_t at = head * L + my_q;
+    if (empty) {
+      LSE.p[0][at] = __builtin_huge_valf();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][at] = 0.f;
+    } else {
+      float lse[K + 1], nrm[K + 1];
+      lse[0] = m_used + logf(lsum[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        float t = nrm[k];
+#pragma unroll
+        for (int jj = 1; jj < k; ++jj) t -= (static_cast<float>(jj) / static_cast<float>(k)) * lse[jj] * nrm[k - jj];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+    }
+  }
+}
+
 template <typename T, int K, int D>
 static int launch_attention_half_kd(const AttnArgs& a) {
   if constexpr (!AttnHalfShape<K, D>::fits) {
@@ -436,6 +803,20 @@ static int launch_attention_half_kd(const AttnArgs& a) {
     for (int i = 0; i <= K; ++i) {
       o.p[i] = static_cast<T*>(a.out[i]);
       if (a.lse != nullptr) lse.p[i] = static_cast<float*>(a.lse[i]);
+    }
+    if constexpr (AttnHalfPipe<K, D>::fits) {
+      // full-order operands, whole 32-key blocks, and K / V operands addressable with 32-bit offsets
+      const int64_t kv_bytes = a.bh * a.lk * D * static_cast<int64_t>(sizeof(T));
+      const bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= 32 &&
+                        a.lk % 32 == 0 && kv_bytes < (int64_t{1} << 31);
+      if (pipe) {
+        const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
+        taylor_attention_fwd_half_pipe_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), static_cast<int>(kv_bytes), a.mask,
+            a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
+        PT_LAUNCH_CHECK();
+        return PT_OK;
+      }
     }
     const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * AttnHalfShape<K, D>::SL));
     taylor_attention_fwd_half_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(

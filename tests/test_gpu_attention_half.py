@@ -60,13 +60,15 @@ def _run(q, k, v, **kwargs):
 @pytest.mark.parametrize("dtype", HALF)
 @pytest.mark.parametrize("causal,window", [(True, None), (False, 37), (False, None)])
 @pytest.mark.parametrize("degree", [1, 4])
-def test_matches_oracle(monkeypatch, dtype, causal, window, degree):
+@pytest.mark.parametrize("length", [150, 160])
+def test_matches_oracle(monkeypatch, dtype, causal, window, degree, length):
+    # 160 keys are whole 32-key blocks: the DMA-pipelined kernel; 150 the staged one
     calls = []
     original = _ops.taylor_attention_fwd
     monkeypatch.setattr(_ops, "taylor_attention_fwd", lambda *a, **k: calls.append(1) or original(*a, **k))
-    shape = (2, 3, 150, 64)
+    shape = (2, 3, length, 64)
     Q, K, V = (_series(shape, degree, 10 + i, dtype) for i in range(3))
-    mask = None if window is None else _window_mask(150, window)
+    mask = None if window is None else _window_mask(length, window)
     q, k, v = _poly(Q), _poly(K), _poly(V)
     with PolyTensor.plain_range():
         assert _fused_attention.eligible(q, k, v, attn_mask=None if mask is None else mask.cuda(), is_causal=causal)
@@ -74,6 +76,18 @@ def test_matches_oracle(monkeypatch, dtype, causal, window, degree):
     assert calls == [1] and out.degree == degree and out.dtype == dtype
     want = oracle.attention(_up(Q), _up(K), _up(V), attn_mask=mask, is_causal=causal)
     _check(out.coeffs, want)
+
+
+@pytest.mark.parametrize("dtype", HALF)
+@pytest.mark.parametrize("degree", range(9))
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_whole_key_blocks_every_degree_and_head_dim(dtype, degree, d):
+    # 96 keys: the DMA-pipelined kernel wherever its two tile buffers fit (the staged kernel elsewhere)
+    shape = (1, 2, 96, d)
+    causal = degree % 2 == 0
+    Q, K, V = (_series(shape, degree, 80 + i, dtype) for i in range(3))
+    out = _run(_poly(Q), _poly(K), _poly(V), is_causal=causal)
+    _check(out.coeffs, oracle.attention(_up(Q), _up(K), _up(V), is_causal=causal))
 
 
 @pytest.mark.parametrize("dtype", HALF)
@@ -108,13 +122,15 @@ def test_lse_series_and_plain_operands(dtype):
 
 
 @pytest.mark.parametrize("dtype", HALF)
-@pytest.mark.parametrize("L,S", [(1, 16), (70, 33), (33, 70), (130, 47)])
+@pytest.mark.parametrize("L,S", [(1, 16), (70, 33), (33, 70), (130, 47), (1, 32), (70, 64), (33, 128), (130, 96)])
 def test_cross_lengths_and_an_empty_row(dtype, L, S):
     Q = _series((1, 2, L, 64), 2, 40, dtype)
     K, V = (_series((1, 2, S, 64), 2, 41 + i, dtype) for i in range(2))
     g = torch.Generator().manual_seed(43)
     mask = torch.rand(L, S, generator=g) < 0.6
     mask[L // 2] = False
+    if L > 64:
+        mask[:64] = False   # a whole query block admits no key
     out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=mask.cuda())
     want = oracle.attention(_up(Q), _up(K), _up(V), attn_mask=mask)
     empty = ~mask.any(-1)   # the plain-range rule gives NaN there; the kernels 0 (the fused convention)
