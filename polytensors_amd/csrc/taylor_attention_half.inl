@@ -414,11 +414,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined 16-bit kernel for full-order operands, a key length that is a
-// multiple of 32, and two K/V tile buffers within LDS (no head-dim slices):
-// * the K and V tiles of key block j+1 are fetched by LDS DMA
-//   (global_load_lds_dwordx4) into the second buffer while block j's value
-//   products run: no staging registers, one barrier per key block;
+// Pipelined 16-bit kernel for full-order operands where two K/V tile buffers
+// fit LDS and the working set fits the registers (no head-dim slices):
+// * the K and V tiles of key block j+1 are fetched by LDS DMA (buffer loads
+//   into LDS) into the second buffer while block j's value products run: no
+//   staging registers, one barrier per key block;
 // * both tiles are stored row-major and unpadded, the 16-byte chunks of a row
 //   XOR-swizzled by the row so that the operand reads hit 64 distinct banks:
 //   the K operand is one 16-byte read per lane (16 key rows, one chunk each);
@@ -454,9 +454,9 @@ struct AttnHalfPipe {
 // DMA operation i of this wave's share of key block kb0 into one buffer
 // (tiles[kv][order][row][d]); i is a compile-time constant at every call.
 // A buffer load into LDS (buffer_load_dwordx4 ... lds: lane l's 16 bytes land
-// at M0 + 16 l): the operand base in the resource, the block's offset (below
-// 2^31 bytes, checked by the launcher) as the scalar offset, a 32-bit lane
-// offset. It is written as inline assembly so that the compiler's wait
+// at M0 + 16 l) through a resource spanning exactly this head's S rows: rows
+// past S are out of range and load as zeros, so a ragged last key block needs
+// no branch. It is written as inline assembly so that the compiler's wait
 // insertion, which cannot tell the two LDS buffers apart, does not wait for
 // this DMA before every read of the other buffer; the kernel waits for it
 // itself (s_waitcnt vmcnt(0) before the barrier of the next key block).
@@ -466,8 +466,8 @@ typedef int AttnInt4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int K, int D>
 __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], const CPtrs<T>& Kp,
-                                                   const CPtrs<T>& Vp, int bytes, int64_t head, int S, int kb0,
-                                                   int lane, int wave, int i) {
+                                                   const CPtrs<T>& Vp, int64_t head, int S, int kb0, int lane,
+                                                   int wave, int i) {
   using P = AttnHalfPipe<K, D>;
   constexpr int CH = P::CH, RPS = P::RPS, SEGS = P::SEGS, IT = P::IT;
   const int kv = i / ((K + 1) * IT), o = (i / IT) % (K + 1), it = i % IT;
@@ -475,18 +475,19 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
   if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
   const int row = seg * RPS + lane / CH;
   const int lch = (lane % CH) ^ (kv ? P::fv(row) : P::fk(row));
-  const uint64_t base = reinterpret_cast<uint64_t>(kv ? Vp.p[o] : Kp.p[o]);
-  // raw buffer resource: 48-bit base, stride 0, num_records = operand bytes, dword 3 = 0x00020000
-  const AttnInt4 rsrc = {static_cast<int>(base), static_cast<int>((base >> 32) & 0xffff), bytes, 0x00020000};
-  const int soff = static_cast<int>((head * S + kb0) * D * static_cast<int64_t>(sizeof(T)));
-  const int voff = (row * D + lch * 8) * static_cast<int>(sizeof(T));
+  const uint64_t base = reinterpret_cast<uint64_t>((kv ? Vp.p[o] : Kp.p[o]) + head * S * D);
+  // raw buffer resource: 48-bit base, stride 0, num_records = the head's bytes (below 2^31, checked
+  // by the launcher), dword 3 = 0x00020000
+  const AttnInt4 rsrc = {static_cast<int>(base), static_cast<int>((base >> 32) & 0xffff),
+                         S * D * static_cast<int>(sizeof(T)), 0x00020000};
+  const int voff = ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T));
   const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) void*)&buf[kv][o][seg * RPS][0]));
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, %3 offen lds"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
       :
-      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+      : "s"(lds), "v"(voff), "s"(rsrc)
       : "memory", "m0");
 }
 
@@ -494,7 +495,7 @@ typedef short AttnShortx4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
-    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S, int kv_bytes,
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S,
     const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
   using P = AttnHalfPipe<K, D>;
   using MM = HalfMfma<T>;
@@ -535,13 +536,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     lo = ranges[2 * qb] / KB * KB;
     hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
   }
-  // a workgroup whose rows admit no key keeps one (fully masked) block, so the
-  // pipeline always has a first block (the launcher requires S >= 32)
-  if (hi <= lo) {
-    lo = 0;
-    hi = KB;
-  }
-  const int nblocks = (hi - lo + KB - 1) / KB;
+  // a workgroup whose rows admit no key keeps one fully masked block (key < hi fails for every
+  // key), so the pipeline always has a first block
+  if (hi <= lo) lo = hi = 0;
+  const int nblocks = max(1, (hi - lo + KB - 1) / KB);
   const int last_kb0 = lo + (nblocks - 1) * KB;
 
   floatx4 acc_o[K + 1][DB];
@@ -557,7 +555,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   // the first block's DMA is issued after the query loads: LDS-DMA loads pending
   // beside ordinary loads make the compiler wait for every load in flight
 #pragma unroll
-  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, kv_bytes, head, S, lo, lane, wave, i);
+  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, head, S, lo, lane, wave, i);
 
   // key block j from buffer cur; the DMA of block j+1 into nxt
   auto block = [&](Tiles& cur, Tiles& nxt, int j) __attribute__((always_inline)) {
@@ -711,7 +709,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       }
 #pragma unroll
       for (int i = db * OPS / DB; i < (db + 1) * OPS / DB; ++i)
-        attn_half_issue_op<T, K, D>(nxt, Kp, Vp, kv_bytes, head, S, next_kb0, lane, wave, i);
+        attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
       __builtin_amdgcn_sched_barrier(0);
       const int cur = P::ahead ? db % NV : 0;
 #pragma unroll
@@ -805,15 +803,15 @@ static int launch_attention_half_kd(const AttnArgs& a) {
       if (a.lse != nullptr) lse.p[i] = static_cast<float*>(a.lse[i]);
     }
     if constexpr (AttnHalfPipe<K, D>::fits) {
-      // full-order operands, whole 32-key blocks, and K / V operands addressable with 32-bit offsets
-      const int64_t kv_bytes = a.bh * a.lk * D * static_cast<int64_t>(sizeof(T));
-      const bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= 32 &&
-                        a.lk % 32 == 0 && kv_bytes < (int64_t{1} << 31);
+      // full-order operands and a head's K / V rows (plus one block) addressable with 32-bit offsets
+      const int64_t head_bytes = (a.lk + 32) * D * static_cast<int64_t>(sizeof(T));
+      const bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= 1 &&
+                        head_bytes < (int64_t{1} << 31);
       if (pipe) {
         const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
         taylor_attention_fwd_half_pipe_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), static_cast<int>(kv_bytes), a.mask,
-            a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_ranges,
+            a.causal ? 1 : 0, static_cast<float>(a.scale));
         PT_LAUNCH_CHECK();
         return PT_OK;
       }
