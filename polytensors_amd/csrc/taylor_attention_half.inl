@@ -440,11 +440,11 @@ struct AttnHalfPipe {
   static constexpr int RSH = CH >= 16 ? 0 : CH == 8 ? 1 : CH == 4 ? 2 : 3;   // log2(16 / CH)
   static constexpr size_t LDS = 2ull * 2 * (K + 1) * KB * D * 2;
   static constexpr bool split = AttnHalfShape<K, D>::split;
-  // registers of the accumulators, query tile, scores, probability operands (hi, lo) and
-  // one set of K and V operands; the operand reads run one step ahead where a second set fits
-  static constexpr int regs = (K + 1) * (D / 16 * 4 + (D + 31) / 32 * 4 + 8 + 4 + 8 + 8) + (split ? 4 * K : 0);
-  static constexpr bool ahead = regs + (K + 1) * 16 <= 384;
-  static constexpr bool fits = LDS <= 160 * 1024 && AttnHalfShape<K, D>::SL == 1 && regs <= 400;
+  static constexpr int R = 4;   // operand ring: reads run three items ahead
+  // registers of the accumulators, query tile, scores, probability operands (hi, lo) and ring
+  static constexpr int regs =
+      (K + 1) * (D / 16 * 4 + (D + 31) / 32 * 4 + 8 + 4) + 4 * R + (split ? 4 * K : 0);
+  static constexpr bool fits = LDS <= 160 * 1024 && regs <= 400;
   // swizzles (physical chunk = logical chunk ^ f(row)): K reads take one chunk of 16 rows,
   // V transpose reads 8-byte pieces of 2 chunks of 8 rows per 32 lanes
   __device__ __forceinline__ static int fk(int row) { return (row >> RSH) & (CH - 1); }
@@ -568,42 +568,37 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and the mask bytes)
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
 
-    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves; chunk reads one step ahead ----
+    // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves ----
+    // Items t = (step, b) in order: one K_b operand (a 16-byte read) feeds the K+1-b products
+    // S_{a+b} += K_b Q_a; the operand reads run R-1 items ahead through a ring of R registers.
     floatx4 sc[2][K + 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int o = 0; o <= K; ++o) sc[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto load_k = [&](u32x4 (&dst)[K + 1], int step) {
-      const int dc = step / 2, kh = step % 2;
+    constexpr int R = P::R;
+    constexpr int KT = 2 * DC * (K + 1);
+    auto load_k = [&](int t) {
+      const int st = t / (K + 1), o = t % (K + 1);
+      const int dc = st / 2, kh = st % 2;
       const int row = 16 * kh + c;
       const bool din = 32 * dc + 8 * g < D;
       const int pch = ((4 * dc + g) & (P::CH - 1)) ^ P::fk(row);
-#pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(&cur[0][o][row][pch * 8]);
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        dst[o] = din ? v : z;
-      }
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&cur[0][o][row][pch * 8]);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      return din ? v : z;
     };
-    constexpr int KSTEPS = 2 * DC;
-    constexpr int NK = P::ahead ? 2 : 1;
-    u32x4 kop[NK][K + 1];
-    if constexpr (P::ahead) load_k(kop[0], 0);
+    u32x4 kring[R];
 #pragma unroll
-    for (int st = 0; st < KSTEPS; ++st) {
-      if constexpr (P::ahead) {
-        if (st + 1 < KSTEPS) load_k(kop[(st + 1) % NK], st + 1);
-      } else {
-        load_k(kop[0], st);
-      }
+    for (int t = 0; t < R - 1; ++t) kring[t] = load_k(t);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      if (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
       __builtin_amdgcn_sched_barrier(0);
+      const int st = t / (K + 1), bo = t % (K + 1);
       const int dc = st / 2, kh = st % 2;
-      const int cur = P::ahead ? st % NK : 0;
 #pragma unroll
-      for (int k = 0; k <= K; ++k)
-#pragma unroll
-        for (int a = 0; a <= k; ++a) sc[kh][k] = MM::mma(kop[cur][k - a], qreg[a][dc], sc[kh][k]);
+      for (int a = 0; a + bo <= K; ++a) sc[kh][a + bo] = MM::mma(kring[t % R], qreg[a][dc], sc[kh][a + bo]);
       __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -633,9 +628,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       for (int o = 0; o <= K; ++o) {
         lsum[o] *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
+        for (int db = 0; db < DB; ++db) {
+          // out of and back into the accumulation registers here, on this rare path, so that
+          // the accumulators keep one register class across the loop (no copies per block)
+          asm volatile("" : "+a"(acc_o[o][db]));
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+          asm volatile("" : "+a"(acc_o[o][db]));
+        }
       }
       m_used = m_new;
     }
@@ -678,48 +678,42 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       }
     }
 
-    // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T: V^T operands by transpose reads, one step ahead;
-    // a share of the next block's DMA into the other buffer per step (the last block re-loads
-    // itself, so there is no branch) ----
+    // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T ----
+    // Items t = (db, b): one V_b^T operand (two transpose reads) feeds the K+1-b products
+    // O_{a+b} += V_b^T P_a^T (and those of the lo parts); the reads run R-1 items ahead; a share of
+    // the next block's DMA into the other buffer per item (the last block re-loads itself, so
+    // there is no branch).
     const int next_kb0 = min(kb0 + KB, last_kb0);
     const int tj = c / 4, ta = c % 4;   // this lane's piece: row 4g + tj (+16), head dims 16 db + 4 ta
-    auto load_v = [&](u32x4 (&dst)[K + 1], int db) {
+    auto load_v = [&](int t) {
+      const int db = t / (K + 1), o = t % (K + 1);
       const int row0 = 4 * g + tj, row1 = 16 + 4 * g + tj;
       const int lch = 2 * db + ta / 2;
       const int off0 = ((lch ^ P::fv(row0)) * 8) + 4 * (ta % 2);
       const int off1 = ((lch ^ P::fv(row1)) * 8) + 4 * (ta % 2);
-#pragma unroll
-      for (int o = 0; o <= K; ++o) {
-        typedef __attribute__((address_space(3))) AttnShortx4 lds_x4;
-        const AttnShortx4 first = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row0][off0]));
-        const AttnShortx4 second = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row1][off1]));
-        const uint2 f = __builtin_bit_cast(uint2, first), s2 = __builtin_bit_cast(uint2, second);
-        dst[o] = u32x4{f.x, f.y, s2.x, s2.y};
-      }
+      typedef __attribute__((address_space(3))) AttnShortx4 lds_x4;
+      const AttnShortx4 first = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row0][off0]));
+      const AttnShortx4 second = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row1][off1]));
+      const uint2 f = __builtin_bit_cast(uint2, first), s2 = __builtin_bit_cast(uint2, second);
+      return u32x4{f.x, f.y, s2.x, s2.y};
     };
-    constexpr int NV = P::ahead ? 2 : 1;
-    u32x4 vop[NV][K + 1];
-    if constexpr (P::ahead) load_v(vop[0], 0);
+    constexpr int VT = DB * (K + 1);
+    u32x4 vring[R];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      if constexpr (P::ahead) {
-        if (db + 1 < DB) load_v(vop[(db + 1) % NV], db + 1);
-      } else {
-        load_v(vop[0], db);
-      }
+    for (int t = 0; t < R - 1; ++t) vring[t] = load_v(t);
 #pragma unroll
-      for (int i = db * OPS / DB; i < (db + 1) * OPS / DB; ++i)
+    for (int t = 0; t < VT; ++t) {
+      if (t + R - 1 < VT) vring[(t + R - 1) % R] = load_v(t + R - 1);
+#pragma unroll
+      for (int i = t * OPS / VT; i < (t + 1) * OPS / VT; ++i)
         attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
       __builtin_amdgcn_sched_barrier(0);
-      const int cur = P::ahead ? db % NV : 0;
+      const int db = t / (K + 1), bo = t % (K + 1);
 #pragma unroll
-      for (int k = 0; k <= K; ++k) {
+      for (int a = 0; a + bo <= K; ++a) acc_o[a + bo][db] = MM::mma(vring[t % R], pb[a], acc_o[a + bo][db]);
+      if constexpr (P::split) {
 #pragma unroll
-        for (int a = 0; a <= k; ++a) acc_o[k][db] = MM::mma(vop[cur][k - a], pb[a], acc_o[k][db]);
-        if constexpr (P::split) {
-#pragma unroll
-          for (int a = 1; a <= k; ++a) acc_o[k][db] = MM::mma(vop[cur][k - a], pl[a], acc_o[k][db]);
-        }
+        for (int a = 1; a + bo <= K; ++a) acc_o[a + bo][db] = MM::mma(vring[t % R], pl[a], acc_o[a + bo][db]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
