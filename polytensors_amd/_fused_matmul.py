@@ -6,14 +6,17 @@ computes the same product as (K+1)(K+2)/2 separate matmuls
 mm/bmm/matmul/linear/addmm rules of /root/reference/src/polytensors/_range_ops.py:160-176).
 An ordinary-tensor operand is a series with one order (the reference lifts it
 with zero orders, _range_ops.py:37-45), so only K+1 products are formed.
-Batch dimensions broadcast as in torch.matmul; float32 and float64.
+Batch dimensions broadcast as in torch.matmul; float32 and float64, and
+bfloat16 / float16 with fp32 accumulation and one rounding per element.
 """
 
 import torch
 
 from . import _complex, _gate, _ops
 
-_DTYPES = (torch.float32, torch.float64)
+_DTYPES = (torch.float32, torch.float64, torch.bfloat16, torch.float16)
+# the 16-bit kernel addresses each (column-padded) operand matrix with 32-bit byte offsets
+_HALF_MATRIX_LIMIT = 1 << 29
 
 
 def why_ineligible(a, b, below_autograd=False):
@@ -23,9 +26,14 @@ def why_ineligible(a, b, below_autograd=False):
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
     dtype = coeffs[0].dtype
     if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
-        return "operands must share one dtype, float32 or float64"
+        return "operands must share one dtype, float32, float64, bfloat16 or float16"
     if a.ndim == 0 or b.ndim == 0:
         return "matmul of a 0-d tensor"
+    if dtype in (torch.bfloat16, torch.float16):
+        for x in (a, b):
+            rows = x.shape[-2] if x.ndim > 1 else 1
+            if rows * (-(-x.shape[-1] // 8) * 8) >= _HALF_MATRIX_LIMIT:
+                return "16-bit operand matrices must stay below 2^29 elements"
     return None
 
 

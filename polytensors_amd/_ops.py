@@ -145,7 +145,7 @@ def cauchy_matmul(a: List[torch.Tensor], b: List[torch.Tensor], degree: int, tra
         _require(s[0].dim() == 3, f"cauchy_matmul: {name} must be 3-D [batch, rows, cols]")
     dtype = a[0].dtype
     _require(b[0].dtype == dtype and b[0].device == a[0].device, "cauchy_matmul: operand dtype/device differ")
-    _require(dtype in (torch.float32, torch.float64), "cauchy_matmul: float32 or float64 only")
+    _require(dtype in _MATMUL_DTYPES, "cauchy_matmul: float32, float64, bfloat16 or float16")
     ba, m, kd = a[0].shape
     if trans_b:
         bb, n, kb = b[0].shape
@@ -154,6 +154,17 @@ def cauchy_matmul(a: List[torch.Tensor], b: List[torch.Tensor], degree: int, tra
     _require(kb == kd, "cauchy_matmul: inner dimensions differ")
     _require(ba == bb or ba == 1 or bb == 1, "cauchy_matmul: batch dimensions do not broadcast")
     batch = max(ba, bb)
+    n_out = n
+    if dtype in _HALF_DTYPES:
+        # the 16-bit kernel moves 16-byte chunks: zero-pad the contraction (which leaves every
+        # product unchanged) and, for B stored [k, n], the columns to multiples of 8, and give
+        # it 16-byte aligned operands
+        a = _aligned16([_pad_dim(c, -1, 8) for c in a])
+        b = _aligned16([_pad_dim(c, -1 if trans_b else -2, 8) for c in b])
+        if not trans_b:
+            b = [_pad_dim(c, -1, 8) for c in b]
+            n = b[0].shape[-1]
+        kd = a[0].shape[-1]
     out = torch.empty((degree + 1, batch, m, n), dtype=dtype, device=a[0].device)
     lib = _lib.load()
     status = lib.pt_cauchy_matmul(
@@ -161,7 +172,24 @@ def cauchy_matmul(a: List[torch.Tensor], b: List[torch.Tensor], degree: int, tra
         _lib.ptr_array(list(out.unbind(0))), batch, m, n, kd,
         0 if ba == 1 else m * kd, 0 if bb == 1 else n * kd, int(trans_b), _lib.stream_of(a[0].device))
     _lib.check(status, "cauchy_matmul")
-    return out
+    return out if n == n_out else out[..., :n_out].contiguous()
+
+
+_HALF_DTYPES = (torch.bfloat16, torch.float16)
+_MATMUL_DTYPES = (torch.float32, torch.float64) + _HALF_DTYPES
+
+
+def _pad_dim(x, dim, multiple):
+    """x zero-padded at the end of ``dim`` to a multiple of ``multiple`` (x itself if it is one)."""
+    extra = -x.shape[dim] % multiple
+    if extra == 0:
+        return x
+    pad = [0, 0] * (x.dim() - 1 - (dim % x.dim())) + [0, extra]
+    return torch.nn.functional.pad(x, pad)
+
+
+def _aligned16(coeffs):
+    return [c if c.data_ptr() % 16 == 0 else c.clone() for c in coeffs]
 
 
 @cauchy_matmul.register_fake

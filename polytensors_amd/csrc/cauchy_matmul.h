@@ -21,4 +21,8 @@ struct CauchyArgs {
 template <typename T>
 int launch_cauchy(const CauchyArgs& a);
 
+// bfloat16 / float16 operands on the 16x16x32 MFMAs (cauchy_matmul_half.inl); T = bf16 or _Float16.
+template <typename T>
+int launch_cauchy_half(const CauchyArgs& a);
+
 }  // namespace pt

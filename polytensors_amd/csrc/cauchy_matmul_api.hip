@@ -10,8 +10,8 @@ int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
   pt_host::clear_error();
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Cauchy matmul: degree must be in 0..8");
-  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
-             "Cauchy matmul: float32 and float64 only");
+  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,
+             PT_UNSUPPORTED, "Cauchy matmul: float32, float64, bfloat16 or float16");
   PT_REQUIRE(a != nullptr && b != nullptr && c != nullptr, PT_INVALID_ARGUMENT,
              "Cauchy matmul: a, b and c pointer arrays are required");
   PT_REQUIRE(a_orders == 1 || a_orders == degree + 1, PT_INVALID_ARGUMENT,
@@ -34,7 +34,12 @@ int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
   if (batch == 0 || m == 0 || n == 0) return PT_OK;
   pt::CauchyArgs args{degree, a, a_orders, b, b_orders, c, batch, m, n, k,
                       a_batch_stride, b_batch_stride, trans_b != 0, static_cast<hipStream_t>(stream)};
-  return dtype == PT_FLOAT32 ? pt::launch_cauchy<float>(args) : pt::launch_cauchy<double>(args);
+  switch (dtype) {
+    case PT_FLOAT32: return pt::launch_cauchy<float>(args);
+    case PT_FLOAT64: return pt::launch_cauchy<double>(args);
+    case PT_BFLOAT16: return pt::launch_cauchy_half<pt::bf16>(args);
+    default: return pt::launch_cauchy_half<_Float16>(args);
+  }
 }
 
 }  // extern "C"

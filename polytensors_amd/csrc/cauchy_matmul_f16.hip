@@ -1,0 +1,6 @@
+// Instantiates the 16-bit Cauchy-product matmul kernels for one type.
+#include "cauchy_matmul_half.inl"
+
+namespace pt {
+template int launch_cauchy_half<_Float16>(const CauchyArgs&);
+}  // namespace pt

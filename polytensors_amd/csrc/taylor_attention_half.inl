@@ -32,52 +32,11 @@
 // loop.
 #pragma once
 
+#include "half_mfma.h"
 #include "taylor_attention.inl"
 
 namespace pt {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-struct HalfMfma;
-
-template <>
-struct HalfMfma<bf16> {
-  typedef __bf16 op_t __attribute__((ext_vector_type(8)));
-  __device__ __forceinline__ static floatx4 mma(u32x4 a, u32x4 b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(op_t, a), __builtin_bit_cast(op_t, b), c,
-                                                   0, 0, 0);
-  }
-  // two values, round to nearest even, first in the low half
-  __device__ __forceinline__ static uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
-  // the two values of a packed word
-  __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
-  __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-  // lazy-rescale slack (natural-log units): p <= e^8 (bf16 has the fp32 exponent range)
-  static constexpr float kSlack = 8.0f;
-};
-
-template <>
-struct HalfMfma<_Float16> {
-  typedef _Float16 op_t __attribute__((ext_vector_type(8)));
-  __device__ __forceinline__ static floatx4 mma(u32x4 a, u32x4 b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(op_t, a), __builtin_bit_cast(op_t, b), c,
-                                                  0, 0, 0);
-  }
-  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
-    const _Float16 x = static_cast<_Float16>(a), y = static_cast<_Float16>(b);   // round to nearest even
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, x)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, y)) << 16);
-  }
-  __device__ __forceinline__ static float lo(uint32_t w) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
-  }
-  __device__ __forceinline__ static float hi(uint32_t w) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-  }
-  // float16 overflows at 65504: the running maximum is exact (p <= 1)
-  static constexpr float kSlack = 0.0f;
-};
 
 template <int K, int D>
 struct AttnHalfShape {
@@ -452,18 +411,9 @@ struct AttnHalfPipe {
 };
 
 // DMA operation i of this wave's share of key block kb0 into one buffer
-// (tiles[kv][order][row][d]); i is a compile-time constant at every call.
-// A buffer load into LDS (buffer_load_dwordx4 ... lds: lane l's 16 bytes land
-// at M0 + 16 l) through a resource spanning exactly this head's S rows: rows
-// past S are out of range and load as zeros, so a ragged last key block needs
-// no branch. It is written as inline assembly so that the compiler's wait
-// insertion, which cannot tell the two LDS buffers apart, does not wait for
-// this DMA before every read of the other buffer; the kernel waits for it
-// itself (s_waitcnt vmcnt(0) before the barrier of the next key block).
-// Vector loads complete in issue order, so the compiler's own counted waits
-// for ordinary loads stay sufficient with these loads in flight.
-typedef int AttnInt4 __attribute__((ext_vector_type(4)));
-
+// (tiles[kv][order][row][d]); i is a compile-time constant at every call. The
+// resource spans exactly this head's S rows: rows past S are out of range and
+// load as zeros, so a ragged last key block needs no branch.
 template <typename T, int K, int D>
 __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], const CPtrs<T>& Kp,
                                                    const CPtrs<T>& Vp, int64_t head, int S, int kb0, int lane,
@@ -475,23 +425,9 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
   if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
   const int row = seg * RPS + lane / CH;
   const int lch = (lane % CH) ^ (kv ? P::fv(row) : P::fk(row));
-  const uint64_t base = reinterpret_cast<uint64_t>((kv ? Vp.p[o] : Kp.p[o]) + head * S * D);
-  // raw buffer resource: 48-bit base, stride 0, num_records = the head's bytes (below 2^31, checked
-  // by the launcher), dword 3 = 0x00020000
-  const AttnInt4 rsrc = {static_cast<int>(base), static_cast<int>((base >> 32) & 0xffff),
-                         S * D * static_cast<int>(sizeof(T)), 0x00020000};
-  const int voff = ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T));
-  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (__attribute__((address_space(3))) void*)&buf[kv][o][seg * RPS][0]));
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
-      :
-      : "s"(lds), "v"(voff), "s"(rsrc)
-      : "memory", "m0");
+  const BufferRsrc rsrc = buffer_rsrc((kv ? Vp.p[o] : Kp.p[o]) + head * S * D, S * D * static_cast<int>(sizeof(T)));
+  lds_dma16(&buf[kv][o][seg * RPS][0], rsrc, ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
-
-typedef short AttnShortx4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
@@ -691,11 +627,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       const int lch = 2 * db + ta / 2;
       const int off0 = ((lch ^ P::fv(row0)) * 8) + 4 * (ta % 2);
       const int off1 = ((lch ^ P::fv(row1)) * 8) + 4 * (ta % 2);
-      typedef __attribute__((address_space(3))) AttnShortx4 lds_x4;
-      const AttnShortx4 first = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row0][off0]));
-      const AttnShortx4 second = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_x4*)(&cur[1][o][row1][off1]));
-      const uint2 f = __builtin_bit_cast(uint2, first), s2 = __builtin_bit_cast(uint2, second);
-      return u32x4{f.x, f.y, s2.x, s2.y};
+      return lds_read_tr16x2(&cur[1][o][row0][off0], &cur[1][o][row1][off1]);
     };
     constexpr int VT = DB * (K + 1);
     u32x4 vring[R];
