@@ -358,6 +358,28 @@ def wl_matmul(device):
                 cpu=lambda: cpu_matmul(n, K))
 
 
+def wl_matmul_bf16(device):
+    """Config 2's shape and inputs ([5, 4096, 4096] x [5, 4096, 4096], K=4, coefficient k scaled by
+    0.5^k) stored in bfloat16: the 16-bit kernel (bf16 MFMA operands, fp32 accumulation, one rounding
+    per output element). The roofline is the bf16 MFMA peak."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, n = 4, 4096
+    g = _gen(1, device)
+    a = [(torch.randn(1, n, n, generator=g, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+    b = [(torch.randn(1, n, n, generator=g, device=device) * 0.5 ** k).to(torch.bfloat16) for k in range(K + 1)]
+
+    def step():
+        return _ops.cauchy_matmul(a, b, K, False)
+
+    pairs = (K + 1) * (K + 2) // 2
+    return dict(step=step, work=2 * pairs * n ** 3, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_MFMA,
+                bytes=3 * (K + 1) * n * n * 2, kernel="cauchy_matmul_bf16", dtype="bf16 (fp32 accumulate)",
+                workload=f"cauchy_matmul [{K + 1},{n},{n}] x [{K + 1},{n},{n}] bf16",
+                cpu=lambda: cpu_matmul(n, K, dtype="bf16"))
+
+
 def wl_norm(device):
     """benchmark config 4a: RMSNorm series x [5, 8192, 4096] bf16, eps 1e-6, weight 1+0.02 N(0,1)."""
     import torch
@@ -461,7 +483,8 @@ def wl_ce_bwd(device):
                 cpu=lambda: cpu_ce_bwd(rows, classes, K))
 
 
-WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "norm": wl_norm, "ce": wl_ce,
+WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "matmul_bf16": wl_matmul_bf16, "norm": wl_norm,
+             "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
              "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
              "attention_bwd_window": wl_attention_bwd_window,
@@ -583,17 +606,19 @@ def cpu_config1(L, d, C, K):
     return dict(value=t * 1e3, unit="ms", sample=f"the whole config-1 pipeline, {reps} runs per timing", seconds=t * reps)
 
 
-def cpu_matmul(n, K):
+def cpu_matmul(n, K, dtype="fp32"):
     import torch
     import oracle
 
     rows = n // 4
+    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
     g = torch.Generator().manual_seed(1)
-    a = [torch.randn(rows, n, generator=g) * 0.5 ** k for k in range(K + 1)]
-    b = [torch.randn(n, n, generator=g) * 0.5 ** k for k in range(K + 1)]
+    a = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(tdt) for k in range(K + 1)]
+    b = [(torch.randn(n, n, generator=g) * 0.5 ** k).to(tdt) for k in range(K + 1)]
     t = _cpu_time(lambda: oracle.matmul(a, b), reps=1)
     flops = 2 * ((K + 1) * (K + 2) // 2) * rows * n * n
-    return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"{rows} of {n} rows of A, K={K} fp32", seconds=t)
+    return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"{rows} of {n} rows of A, K={K} {dtype}",
+                seconds=t)
 
 
 def cpu_norm(rows, n, K):
