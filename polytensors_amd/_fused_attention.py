@@ -30,17 +30,19 @@ _HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128)
               torch.bfloat16: (16, 32, 64, 128), torch.float16: (16, 32, 64, 128)}
 
 
-def _tiles_fit_lds(dtype, head_dim, degree):
-    """Whether the forward and backward kernels' staged key and value tiles fit in LDS.
+def _tiles_fit_lds(dtype, head_dim, degree, backward):
+    """Whether the kernels' staged key and value tiles fit in LDS.
 
-    Both stage 16 keys of every order of K and V with rows padded to head_dim + 4
-    values; the backward adds two 16-row series of accumulator values
-    (AttnShape and AttnBwdPlan in csrc/taylor_attention*.inl).
+    The forward fits at every degree and head dim (output head-dim slices and, for float64,
+    K and V tiles staged one after the other where both do not fit: AttnShape in
+    csrc/taylor_attention.inl). The backward stages 16 keys of every order of K and V with
+    rows padded to head_dim + 4 values, plus two 16-row series of accumulator values
+    (AttnBwdPlan in csrc/taylor_attention_bwd.inl).
     """
+    if not backward:
+        return True
     if dtype in (torch.bfloat16, torch.float16):
-        # the 16-bit forward splits its output head dims where needed (every shape fits); its
-        # backward runs the float32 kernels
-        dtype = torch.float32
+        dtype = torch.float32   # the 16-bit backward runs the float32 kernels
     item = torch.empty((), dtype=dtype).element_size()
     lds = 2 * (degree + 1) * 16 * (head_dim + 4) * item + 2 * (degree + 1) * 16 * item
     return lds <= 160 * 1024
@@ -99,9 +101,10 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if query.shape[-1] != key.shape[-1] or query.shape[-1] not in _HEAD_DIMS[dtype]:
         return f"head dim {query.shape[-1]} not in {_HEAD_DIMS[dtype]}"
     degree = next(x.degree for x in tensors if isinstance(x, PolyTensor))
-    if not _tiles_fit_lds(dtype, query.shape[-1], degree):
-        return (f"degree {degree} at head dim {query.shape[-1]} in {dtype} exceeds the kernels' 160 KiB "
-                "LDS budget for the staged key/value tiles")
+    backward = grads or _gate.coefficient_graph(*tensors)
+    if not _tiles_fit_lds(dtype, query.shape[-1], degree, backward):
+        return (f"the backward at degree {degree}, head dim {query.shape[-1]} in {dtype} exceeds the kernels' "
+                "160 KiB LDS budget for the staged key/value tiles")
     if is_causal and attn_mask is not None:
         return "is_causal and attn_mask are exclusive"
     if _square_mask(attn_mask, query.shape[-2], key.shape[-2]) is NotImplemented:

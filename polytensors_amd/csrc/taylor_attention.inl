@@ -74,11 +74,25 @@ struct AttnRescale {
 
 template <typename T, int K, int D>
 struct AttnShape {
+  // Output head-dim slices (a grid dimension; each slice's workgroup recomputes the scores and
+  // accumulates D / SL output dims) where K+1 sets of output accumulators over the whole head
+  // dim would spill the register file: float64 at head dim 128 from degree 3 and 64 from degree
+  // 6, float32 at head dim 128 from degree 6 (checked with the compiler's resource remarks).
+  static constexpr int SL = sizeof(T) == 8 ? (D == 128 ? (K >= 6 ? 4 : K >= 3 ? 2 : 1) : D == 64 && K >= 6 ? 2 : 1)
+                                           : (D == 128 && K >= 6 ? 2 : 1);
+  static constexpr int DS = D / SL;    // output head dims per slice
+  static constexpr int DBS = DS / 16;  // 16-wide output blocks per slice
   // Row stride of the staged K/V tiles: D + 4 values. For floats that is 4 mod 64
   // banks, so the 16 key rows of a 16-byte K-operand read and the 4 key rows of
   // a V-operand read fall on distinct banks; for doubles it keeps rows 32-byte aligned.
   static constexpr int LD = D + 4;
-  static constexpr size_t LDS = 2ull * (K + 1) * kAttnBN * LD * sizeof(T);
+  static constexpr int LDV = DS + 4;   // V tile row: the slice's dims
+  static constexpr size_t KT = static_cast<size_t>(K + 1) * kAttnBN * LD;    // K tile values
+  static constexpr size_t VT = static_cast<size_t>(K + 1) * kAttnBN * LDV;   // V tile values
+  // K and V tiles one after the other in one buffer when both do not fit (staged between the
+  // score and value products of each key block)
+  static constexpr bool SEQ = (KT + VT) * sizeof(T) > 160 * 1024;
+  static constexpr size_t LDS = (SEQ ? (KT > VT ? KT : VT) : KT + VT) * sizeof(T);
   static constexpr bool fits = LDS <= 160 * 1024;
 };
 
@@ -249,15 +263,19 @@ __device__ __forceinline__ uint8_t attn_mask_byte(const uint8_t* mask, const voi
 // E is the head-dim interleave of the output accumulators: accumulator
 // g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
 // (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).
-template <typename T, int K, int D, typename AccT, int E = 1>
-__device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
+// The accumulators hold NB 16-wide output blocks from head dim d0 on (a slice of the
+// D head dims); the lse series is written where write_lse holds (one slice).
+template <typename T, int K, int D, typename AccT, int E = 1, int NB = D / 16>
+__device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][NB],
                                                    typename AccOf<T>::type (&lsum)[K + 1],
                                                    typename AccOf<T>::type m_used, MPtrs<T>& O,
                                                    MPtrs<typename AccOf<T>::type>& LSE, int64_t head,
-                                                   int L, int my_q, bool q_ok, int h) {
+                                                   int L, int my_q, bool q_ok, int h, int d0 = 0,
+                                                   bool write_lse = true) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
-  constexpr int DB = D / 16;
+  constexpr int DB = NB;
+  static_assert(E == 1 || NB == D / 16, "interleaved accumulators span the whole head dim");
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
     lsum[o] += __shfl_xor(lsum[o], 16, kWave);
@@ -309,7 +327,7 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
     T* orow = nullptr;
 #pragma unroll
     for (int k = 0; k <= K; ++k) {
-      orow = O.p[k] + (head * L + my_q) * D + db * 16;
+      orow = O.p[k] + (head * L + my_q) * D + d0 + db * 16;
       if constexpr (sizeof(T) == 4) {
         // fp32 layout: registers r = 0..3 hold head-dim columns 4h + r: one 16-byte store
         Vec<T, 4> w;
@@ -322,7 +340,7 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][D / 16],
       }
     }
   }
-  if (LSE.p[0] != nullptr && h == 0) {
+  if (LSE.p[0] != nullptr && h == 0 && write_lse) {
     const int64_t at = head * L + my_q;
     if (empty) {
       LSE.p[0][at] = __builtin_huge_val();
@@ -366,24 +384,39 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
   using Shape = AttnShape<T, K, D>;
-  constexpr int LD = Shape::LD;
-  constexpr int DB = D / 16;                  // 16-wide head-dim chunks / output blocks
+  constexpr int LD = Shape::LD, LDV = Shape::LDV, SL = Shape::SL, DS = Shape::DS;
+  constexpr int DB = D / 16;                  // 16-wide head-dim chunks of the score contraction
+  constexpr int DBS = Shape::DBS;             // 16-wide output blocks of this slice
   constexpr int V = 16 / sizeof(T);           // values per 16-byte load
   constexpr int QV = 4;                       // operand values per lane per 16-wide chunk
   constexpr A kNegInf = -__builtin_huge_val();
   constexpr A kSlack = AttnRescale<T>::value;
   static_assert(Shape::fits, "K/V tiles exceed LDS");
 
-  __shared__ T Ks[K + 1][kAttnBN][LD];
-  __shared__ T Vs[K + 1][kAttnBN][LD];
+  // the K tile (every head dim) and the V tile (the slice's head dims); in one buffer, one after
+  // the other within each key block, when both do not fit
+  __shared__ __attribute__((aligned(16))) T tiles[Shape::LDS / sizeof(T)];
+  T(*Ks)[kAttnBN][LD] = reinterpret_cast<T(*)[kAttnBN][LD]>(&tiles[0]);
+  T(*Vs)[kAttnBN][LDV] = reinterpret_cast<T(*)[kAttnBN][LDV]>(&tiles[Shape::SEQ ? 0 : Shape::KT]);
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int c = lane % 16;        // query column of this lane (and key row for K operands)
   const int h = lane / 16;        // lane group
   int64_t head;
-  int q_block;
-  attn_work_item(L, causal, head, q_block);
+  int q_block, slice = 0;
+  if constexpr (SL == 1) {
+    attn_work_item(L, causal, head, q_block);
+  } else {
+    // slices fastest, then heads, heaviest query blocks first
+    const int nqb = (L + kAttnBM - 1) / kAttnBM;
+    const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SL);
+    const int64_t t = blockIdx.x / SL;
+    slice = static_cast<int>(blockIdx.x % SL);
+    head = t % bh;
+    q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
+  }
+  const int d0 = slice * DS;   // first output head dim of this workgroup
   const int q0 = q_block + wave * kAttnQPerWave;
   const int my_q = q0 + c;
   const bool q_ok = my_q < L;
@@ -399,11 +432,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     qrow[o] = Q.p[o < q_orders ? o : 0] + (head * L + (q_ok ? my_q : 0)) * D;
   }
 
-  acc_t acc_o[K + 1][DB];
+  acc_t acc_o[K + 1][DBS];
 #pragma unroll
   for (int o = 0; o <= K; ++o)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) acc_o[o][db] = MF::zero();
+    for (int db = 0; db < DBS; ++db) acc_o[o][db] = MF::zero();
   A m_used = kNegInf;
   A lsum[K + 1];   // per-lane partial row sums (this lane's keys only)
 #pragma unroll
@@ -417,33 +450,27 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 #pragma unroll
     for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + MF::acc_row(h, r), L, S);
     __syncthreads();
-    // ---- stage K and V rows kb0 .. kb0+15 of every order (zero past S) ----
-    {
-      constexpr int VPR = D / V;   // 16-byte vectors per row
-      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
-        const int o = idx / (kAttnBN * VPR);
-        const int rem = idx % (kAttnBN * VPR);
-        const int r = rem / VPR, cv = (rem % VPR) * V;
+    // ---- stage rows kb0 .. kb0+15 of every order (zero past S / the orders given): K over every
+    // head dim, V over the slice's (V after the scores when the two share the buffer) ----
+    auto stage = [&](auto dst, const CPtrs<T>& src, int orders, int dims, int first) {
+      const int vpr = dims / V;   // 16-byte vectors per row
+      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * vpr; idx += kAttnWaves * kWave) {
+        const int o = idx / (kAttnBN * vpr);
+        const int rem = idx % (kAttnBN * vpr);
+        const int r = rem / vpr, cv = (rem % vpr) * V;
         const int key = kb0 + r;
-        Vec<T, V> kx, vx;
-        const bool kin = key < S && o < k_orders;
-        const bool vin = key < S && o < v_orders;
-        if (kin) {
-          kx = load_vec<T, V>(order_ptr<K>(Kp, o) + (head * S + key) * D + cv);
+        Vec<T, V> x;
+        if (key < S && o < orders) {
+          x = load_vec<T, V>(order_ptr<K>(src, o) + (head * S + key) * D + first + cv);
         } else {
 #pragma unroll
-          for (int e = 0; e < V; ++e) kx.v[e] = T(0);
+          for (int e = 0; e < V; ++e) x.v[e] = T(0);
         }
-        if (vin) {
-          vx = load_vec<T, V>(order_ptr<K>(Vp, o) + (head * S + key) * D + cv);
-        } else {
-#pragma unroll
-          for (int e = 0; e < V; ++e) vx.v[e] = T(0);
-        }
-        store_vec<T, V>(&Ks[o][r][cv], kx);
-        store_vec<T, V>(&Vs[o][r][cv], vx);
+        store_vec<T, V>(&dst[o][r][cv], x);
       }
-    }
+    };
+    stage(Ks, Kp, k_orders, D, 0);
+    if constexpr (!Shape::SEQ) stage(Vs, Vp, v_orders, DS, d0);
     __syncthreads();
 
     // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T (keys x queries) ----
@@ -524,9 +551,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
       }
     }
 
+    if constexpr (Shape::SEQ) {
+      __syncthreads();   // every wave's scores are done with the K tile
+      stage(Vs, Vp, v_orders, DS, d0);
+      __syncthreads();
+    }
+
     // ---- O^T_k += sum_{a+b=k} V_b^T E_a^T (head dim x queries) ----
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int db = 0; db < DBS; ++db) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int key_row = MF::acc_row(h, s);   // key held in score register s by this lane group
@@ -542,7 +575,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     }
   }
 
-  attention_epilogue<T, K, D>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
+  attention_epilogue<T, K, D, acc_t, 1, DBS>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h, d0, slice == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1074,7 +1107,8 @@ static int launch_attention_kd(const AttnArgs& a) {
         return PT_OK;
       }
     }
-    taylor_attention_fwd_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
+    const dim3 sgrid(grid.x * AttnShape<T, K, D>::SL);
+    taylor_attention_fwd_kernel<T, K, D><<<sgrid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
         q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
         static_cast<int>(a.lk), a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale));
     PT_LAUNCH_CHECK();

@@ -58,8 +58,11 @@ struct AttnBwdPlan {
   // fused dK and dV also hold both tile series twice (current and prefetched block)
   static constexpr bool km_fused = (K + 1) * DB * kAccRegs * 2 + 4 * (K + 1) * kAccRegs <= kMatBudget;
   static constexpr int NS_KM = attn_bwd_chunks(K + 1, kAccRegs, km_fused ? 2 : 1, DB, kMatBudget);
-  static constexpr size_t kv_lds = AttnShape<T, K, D>::LDS + 2ull * (K + 1) * 16 * sizeof(A);
-  static constexpr bool fits = AttnShape<T, K, D>::fits && kv_lds <= 160 * 1024;
+  // two whole-head-dim tiles of 16 rows of every order (K and V, or Q and G) and two 16-row
+  // accumulator series
+  static constexpr size_t kv_lds =
+      2ull * (K + 1) * kAttnBN * AttnShape<T, K, D>::LD * sizeof(T) + 2ull * (K + 1) * 16 * sizeof(A);
+  static constexpr bool fits = kv_lds <= 160 * 1024;
 };
 
 // N consecutive values at p (16-byte loads when the run is a whole number of them).

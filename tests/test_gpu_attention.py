@@ -352,8 +352,36 @@ def test_sliding_window_skips_blocks(dtype):
         assert rel_err(a[..., keep, :], b[..., keep, :]) <= TOL[dtype], k
 
 
-def test_float64_head_dim_128_beyond_lds_is_refused_with_a_reason():
-    q = _poly(_series((1, 1, 32, 128), 4, seed=40, dtype=torch.float64))
-    assert not _fused_attention.eligible(q, q, q, is_causal=True)
+@pytest.mark.parametrize("degree", range(9))
+@pytest.mark.parametrize("d", [64, 128])
+def test_float64_every_degree_with_output_slices(degree, d):
+    # float64 splits the output head dims over workgroups at head dim 128 from degree 3 and 64
+    # from degree 6, and stages K then V through one LDS buffer at head dim 128 from degree 7
+    shape = (1, 2, 70, d)
+    Q, K, V = (_series(shape, degree, 140 + i, torch.float64) for i in range(3))
+    mask = _window_mask(70, 23) if degree % 2 else None
+    out = _run(_poly(Q), _poly(K), _poly(V), attn_mask=None if mask is None else mask.cuda(), is_causal=mask is None)
+    want = oracle.attention(Q, K, V, attn_mask=mask, is_causal=mask is None)
+    _check(out.coeffs, want, torch.float64)
+
+
+def test_float64_plain_key_with_output_slices():
+    degree, shape = 5, (1, 2, 40, 128)
+    Q, V = (_series(shape, degree, 150 + i, torch.float64) for i in range(2))
+    Kp = _series(shape, 0, 152, torch.float64)[0]
+    out = _run(_poly(Q), Kp.cuda(), _poly(V), is_causal=True)
+    Ks = [Kp] + [torch.zeros_like(Kp) for _ in range(degree)]
+    _check(out.coeffs, oracle.attention(Q, Ks, V, is_causal=True), torch.float64)
+
+
+def test_float64_head_dim_128_backward_beyond_lds_is_refused_with_a_reason():
+    # the forward runs at every degree; the backward's K/V tiles of degree 4 exceed LDS
+    q = PolyTensor(tuple(c.cuda() for c in _series((1, 1, 32, 128), 4, seed=40, dtype=torch.float64)),
+                   requires_grad=True)
+    with PolyTensor.plain_range():
+        assert "backward" in _fused_attention.why_ineligible(q, q, q, None, 0.0, True, False)
+        with torch.no_grad():
+            assert _fused_attention.eligible(q, q, q, is_causal=True)
     with pytest.raises(NotImplementedError, match="LDS"):
-        _run(q, q, q, is_causal=True)
+        with PolyTensor.plain_range():
+            F.scaled_dot_product_attention(q, q, q, is_causal=True)

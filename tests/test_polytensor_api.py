@@ -174,11 +174,20 @@ def test_plain_tensor_cross_entropy_with_softcap_matches_composite():
 
 
 def test_attention_lds_budget_gate():
-    # float64 at head dim 128 stages 16 keys of every order of K and V in LDS: degree 3 fits
-    # the 160 KiB budget, degree 4 does not; float32 fits at every degree up to 8.
-    from polytensors_amd._fused_attention import _tiles_fit_lds
+    # the forward fits everywhere (output head-dim slices, sequential K/V staging for float64);
+    # the backward stages 16 keys of every order of K and V in LDS: float64 at head dim 128 fits
+    # the 160 KiB budget at degree 3, not at degree 4; float32 fits at every degree up to 8.
+    from polytensors_amd._fused_attention import _tiles_fit_lds, why_ineligible
 
-    assert _tiles_fit_lds(torch.float64, 128, 3)
-    assert not _tiles_fit_lds(torch.float64, 128, 4)
-    assert _tiles_fit_lds(torch.float64, 64, 8)
-    assert all(_tiles_fit_lds(torch.float32, d, 8) for d in (16, 32, 64, 128))
+    assert all(_tiles_fit_lds(torch.float64, 128, k, backward=False) for k in range(9))
+    assert _tiles_fit_lds(torch.float64, 128, 3, backward=True)
+    assert not _tiles_fit_lds(torch.float64, 128, 4, backward=True)
+    assert _tiles_fit_lds(torch.float64, 64, 8, backward=True)
+    assert all(_tiles_fit_lds(torch.float32, d, 8, backward=True) for d in (16, 32, 64, 128))
+    x = PolyTensor(tuple(torch.randn(1, 1, 8, 128, dtype=torch.float64) for _ in range(5)))
+    with PolyTensor.plain_range():
+        reason = why_ineligible(x, x, x, None, 0.0, False, False)
+        assert reason is None or "HIP" in reason   # no LDS refusal without gradients
+        g = PolyTensor(tuple(torch.randn(1, 1, 8, 128, dtype=torch.float64) for _ in range(5)), requires_grad=True)
+        assert "backward" in why_ineligible(g, g, g, None, 0.0, False, False) or \
+            "HIP" in why_ineligible(g, g, g, None, 0.0, False, False)
