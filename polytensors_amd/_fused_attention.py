@@ -35,17 +35,19 @@ def _tiles_fit_lds(dtype, head_dim, degree, backward):
 
     The forward fits at every degree and head dim (output head-dim slices and, for float64,
     K and V tiles staged one after the other where both do not fit: AttnShape in
-    csrc/taylor_attention.inl). The backward stages 16 keys of every order of K and V with
-    rows padded to head_dim + 4 values, plus two 16-row series of accumulator values
-    (AttnBwdPlan in csrc/taylor_attention_bwd.inl).
+    csrc/taylor_attention.inl). The backward stages 16 rows of every order of two operands
+    with rows padded to head_dim + 4 values, plus two 16-row series of accumulator values,
+    the two tiles taking turns in one buffer where both do not fit (AttnBwdPlan in
+    csrc/taylor_attention_bwd.inl).
     """
     if not backward:
         return True
     if dtype in (torch.bfloat16, torch.float16):
         dtype = torch.float32   # the 16-bit backward runs the float32 kernels
     item = torch.empty((), dtype=dtype).element_size()
-    lds = 2 * (degree + 1) * 16 * (head_dim + 4) * item + 2 * (degree + 1) * 16 * item
-    return lds <= 160 * 1024
+    tile = (degree + 1) * 16 * (head_dim + 4) * item
+    acc = 2 * (degree + 1) * 16 * item
+    return tile + acc <= 160 * 1024   # (with room for both tiles, one buffer each)
 
 
 def default_scale(head_dim):

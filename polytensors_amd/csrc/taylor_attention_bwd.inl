@@ -59,9 +59,12 @@ struct AttnBwdPlan {
   static constexpr bool km_fused = (K + 1) * DB * kAccRegs * 2 + 4 * (K + 1) * kAccRegs <= kMatBudget;
   static constexpr int NS_KM = attn_bwd_chunks(K + 1, kAccRegs, km_fused ? 2 : 1, DB, kMatBudget);
   // two whole-head-dim tiles of 16 rows of every order (K and V, or Q and G) and two 16-row
-  // accumulator series
-  static constexpr size_t kv_lds =
-      2ull * (K + 1) * kAttnBN * AttnShape<T, K, D>::LD * sizeof(T) + 2ull * (K + 1) * 16 * sizeof(A);
+  // accumulator series; where the two tiles do not fit (float64 at head dim 128 from degree 4)
+  // they take turns in one buffer, staged one after the other within each block (seq)
+  static constexpr size_t tile_bytes = static_cast<size_t>(K + 1) * kAttnBN * AttnShape<T, K, D>::LD * sizeof(T);
+  static constexpr size_t acc_bytes = 2ull * (K + 1) * 16 * sizeof(A);
+  static constexpr bool seq = 2 * tile_bytes + acc_bytes > 160 * 1024;
+  static constexpr size_t kv_lds = (seq ? 1 : 2) * tile_bytes + acc_bytes;
   static constexpr bool fits = kv_lds <= 160 * 1024;
 };
 
@@ -398,9 +401,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   constexpr int SLICES = DB / NS;
   constexpr int V = 16 / sizeof(T);
   constexpr int QV = 4;
+  constexpr bool SEQ = AttnBwdPlan<T, K, D>::seq;   // K and V tiles take turns in one buffer
 
-  __shared__ T Ks[K + 1][kAttnBN][LD];
-  __shared__ T Vs[K + 1][kAttnBN][LD];
+  __shared__ T tiles[SEQ ? 1 : 2][K + 1][kAttnBN][LD];
+  auto& Ks = tiles[0];
+  auto& Vs = tiles[SEQ ? 0 : 1];
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -453,8 +458,26 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   // (registers: accumulators + two staged row sets + operand ring + score series)
   constexpr int kW = static_cast<int>(sizeof(A) / 4);
   constexpr bool kPrefetchStage =
-      (K + 1) * NS * 4 * kW + 2 * RowStager<T, K, D, kAttnBN>::ITERS * 4 + 2 * (K + 1) * 4 * kW +
-          2 * (K + 1) * 4 * kW <= 330;
+      !SEQ && (K + 1) * NS * 4 * kW + 2 * RowStager<T, K, D, kAttnBN>::ITERS * 4 + 2 * (K + 1) * 4 * kW +
+                      2 * (K + 1) * 4 * kW <= 330;
+  // rows kb0 .. kb0+15 of every order of one operand into a tile (zero past S)
+  auto stage_rows = [&](T(&tile)[K + 1][kAttnBN][LD], const CPtrs<T>& src, int kb0) {
+    constexpr int VPR = D / V;
+    for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
+      const int o = idx / (kAttnBN * VPR);
+      const int rem = idx % (kAttnBN * VPR);
+      const int r = rem / VPR, cv = (rem % VPR) * V;
+      const int key = kb0 + r;
+      Vec<T, V> x;
+      if (key < S) {
+        x = load_vec<T, V>(order_ptr<K>(src, o) + (head * S + key) * D + cv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) x.v[e] = T(0);
+      }
+      store_vec<T, V>(&tile[o][r][cv], x);
+    }
+  };
   RowStager<T, K, D, kAttnBN> stage_k, stage_v;
   if constexpr (kPrefetchStage) {
     if (lo < hi) {
@@ -473,22 +496,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       stage_k.commit(Ks);
       stage_v.commit(Vs);
     } else {
-      constexpr int VPR = D / V;
-      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * VPR; idx += kAttnWaves * kWave) {
-        const int o = idx / (kAttnBN * VPR);
-        const int rem = idx % (kAttnBN * VPR);
-        const int r = rem / VPR, cv = (rem % VPR) * V;
-        const int key = kb0 + r;
-        Vec<T, V> kx, vx;
-        if (key < S) {
-          kx = load_vec<T, V>(order_ptr<K>(Kp, o) + (head * S + key) * D + cv);
-          vx = load_vec<T, V>(order_ptr<K>(Vp, o) + (head * S + key) * D + cv);
-        } else {
-#pragma unroll
-          for (int e = 0; e < V; ++e) kx.v[e] = vx.v[e] = T(0);
-        }
-        store_vec<T, V>(&Ks[o][r][cv], kx);
-        store_vec<T, V>(&Vs[o][r][cv], vx);
+      if constexpr (SEQ) {
+        stage_rows(Vs, Vp, kb0);   // dP first: V now, K after it
+      } else {
+        stage_rows(Ks, Kp, kb0);
+        stage_rows(Vs, Vp, kb0);
       }
     }
     __syncthreads();
@@ -519,7 +531,24 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
 #pragma unroll
           for (int a = 0; a <= k; ++a) dp[k] = MF::mma(vb[k - a].v[s], ga[a].v[s], dp[k]);
     };
-    attn_bwd_contract<T, K, DB, 2, kRing>(gq, load_glob, s_step, p_step);
+    if constexpr (SEQ) {
+      // dP^T with the V tile, then the K tile in its place for S^T (and the dQ products)
+      for (int dc = 0; dc < DB; ++dc) {
+        Vec<T, QV> ga[K + 1];
+        load_glob(ga, DB + dc);
+        p_step(dc, ga);
+      }
+      __syncthreads();   // every wave is done with the V tile
+      stage_rows(Ks, Kp, kb0);
+      __syncthreads();
+      for (int dc = 0; dc < DB; ++dc) {
+        Vec<T, QV> qa[K + 1];
+        load_glob(qa, dc);
+        s_step(dc, qa);
+      }
+    } else {
+      attn_bwd_contract<T, K, DB, 2, kRing>(gq, load_glob, s_step, p_step);
+    }
     // The next block's K/V rows are fetched after the contraction's global loads (memory
     // waits complete in order), so they overlap the dS series and the dQ products.
     if constexpr (kPrefetchStage) {
@@ -585,9 +614,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   static_assert(kBK == kAttnRangeBlock, "key blocks are the mask-range blocks");
   constexpr bool DO_V = (WHAT & 1) != 0;
   constexpr bool DO_K = (WHAT & 2) != 0;
+  constexpr bool SEQ = AttnBwdPlan<T, K, D>::seq;   // Q and G tiles take turns in one buffer
+  static_assert(!SEQ || WHAT != 3, "with one tile buffer dK and dV run as separate passes");
 
-  __shared__ T Qs[K + 1][kBM][LD];
-  __shared__ T Gs[K + 1][kBM][LD];
+  __shared__ T tiles[SEQ ? 1 : 2][K + 1][kBM][LD];
+  auto& Qs = tiles[0];
+  auto& Gs = tiles[SEQ ? 0 : 1];
   __shared__ A Ls[K + 1][kBM];
   __shared__ A Ds[K + 1][kBM];
 
@@ -633,23 +665,32 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
       for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], qb0 + MF::acc_row(h, r), my_k, L, S);
     }
     __syncthreads();
-    {
+    // rows qb0 .. qb0+15 of every order of one operand into a tile (zero past L)
+    auto stage_rows = [&](T(&tile)[K + 1][kBM][LD], const CPtrs<T>& src) {
       constexpr int VPR = D / V;
       for (int idx = threadIdx.x; idx < (K + 1) * kBM * VPR; idx += kAttnWaves * kWave) {
         const int o = idx / (kBM * VPR);
         const int rem = idx % (kBM * VPR);
         const int r = rem / VPR, cv = (rem % VPR) * V;
         const int q = qb0 + r;
-        Vec<T, V> qx, gx;
+        Vec<T, V> x;
         if (q < L) {
-          qx = load_vec<T, V>(order_ptr<K>(Q, o) + (head * L + q) * D + cv);
-          gx = load_vec<T, V>(order_ptr<K>(G, o) + (head * L + q) * D + cv);
+          x = load_vec<T, V>(order_ptr<K>(src, o) + (head * L + q) * D + cv);
         } else {
 #pragma unroll
-          for (int e = 0; e < V; ++e) qx.v[e] = gx.v[e] = T(0);
+          for (int e = 0; e < V; ++e) x.v[e] = T(0);
         }
-        store_vec<T, V>(&Qs[o][r][cv], qx);
-        store_vec<T, V>(&Gs[o][r][cv], gx);
+        store_vec<T, V>(&tile[o][r][cv], x);
+      }
+    };
+    {
+      if constexpr (!SEQ) {
+        stage_rows(Qs, Q);
+        stage_rows(Gs, G);
+      } else if constexpr (DO_K) {
+        stage_rows(Gs, G);   // dP first: G now, Q after it
+      } else {
+        stage_rows(Qs, Q);   // S first: Q now, G after it
       }
       for (int idx = threadIdx.x; idx < (K + 1) * kBM; idx += kAttnWaves * kWave) {
         const int o = idx / kBM, r = idx % kBM;
@@ -690,7 +731,25 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
             for (int a = 0; a <= k; ++a) dp[k] = MF::mma(ga[a].v[s], vb[k - a].v[s], dp[k]);
       }
     };
-    attn_bwd_contract<T, K, DB, DO_K ? 2 : 1>(gk, load_glob, s_step, p_step);
+    if constexpr (SEQ) {
+      if constexpr (DO_K) {   // dP with the G tile, then the Q tile in its place for S (and dK)
+        for (int dc = 0; dc < DB; ++dc) {
+          Vec<T, QV> vb[K + 1];
+          load_glob(vb, DB + dc);
+          p_step(dc, vb);
+        }
+        __syncthreads();   // every wave is done with the G tile
+        stage_rows(Qs, Q);
+        __syncthreads();
+      }
+      for (int dc = 0; dc < DB; ++dc) {
+        Vec<T, QV> kb[K + 1];
+        load_glob(kb, dc);
+        s_step(dc, kb);
+      }
+    } else {
+      attn_bwd_contract<T, K, DB, DO_K ? 2 : 1>(gk, load_glob, s_step, p_step);
+    }
 
     // P in place of the scores (dV), dS in place of dP (dK)
 #pragma unroll
@@ -716,6 +775,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
 #pragma unroll
         for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(p[o]);
       }
+    }
+
+    if constexpr (SEQ && DO_V) {   // the G tile in the Q tile's place for the dV products
+      __syncthreads();
+      stage_rows(Gs, G);
+      __syncthreads();
     }
 
     // dV^T_k += sum_{a+b=k} G_b^T P_a and dK^T_k += sum_{a+b=k} Q_b^T dS_a (head dim x keys)

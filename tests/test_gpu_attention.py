@@ -374,14 +374,17 @@ def test_float64_plain_key_with_output_slices():
     _check(out.coeffs, oracle.attention(Q, Ks, V, is_causal=True), torch.float64)
 
 
-def test_float64_head_dim_128_backward_beyond_lds_is_refused_with_a_reason():
-    # the forward runs at every degree; the backward's K/V tiles of degree 4 exceed LDS
-    q = PolyTensor(tuple(c.cuda() for c in _series((1, 1, 32, 128), 4, seed=40, dtype=torch.float64)),
-                   requires_grad=True)
-    with PolyTensor.plain_range():
-        assert "backward" in _fused_attention.why_ineligible(q, q, q, None, 0.0, True, False)
-        with torch.no_grad():
-            assert _fused_attention.eligible(q, q, q, is_causal=True)
-    with pytest.raises(NotImplementedError, match="LDS"):
-        with PolyTensor.plain_range():
-            F.scaled_dot_product_attention(q, q, q, is_causal=True)
+def test_float64_head_dim_128_gradients_at_degree_4():
+    # wrapper autograd through the forward's output slices and the backward's shared tile buffer,
+    # against the oracle's VJP series (G = the all-ones constant series)
+    degree, shape = 4, (1, 1, 40, 128)
+    Q, K, V = (_series(shape, degree, 160 + i, torch.float64) for i in range(3))
+    xs = [PolyTensor(tuple(c.cuda() for c in X), requires_grad=True) for X in (Q, K, V)]
+    with PolyTensor.retain_wrappers(), PolyTensor.plain_range():
+        assert _fused_attention.eligible(*xs, is_causal=True)
+        out = F.scaled_dot_product_attention(*xs, is_causal=True)
+        out.backward(PolyTensor.constant(torch.ones_like(out.value), degree))
+    G = [torch.ones(shape, dtype=torch.float64)] + [torch.zeros(shape, dtype=torch.float64)] * degree
+    want = oracle.attention_backward(Q, K, V, G, is_causal=True)
+    for x, w in zip(xs, want):
+        _check(x.grad.coeffs, w, torch.float64)
