@@ -207,7 +207,10 @@ size_t pt_cross_entropy_series_noalloc_max_bytes(void);
  * b: b_orders pointers (1 or K+1), each [batch, k, n], or [batch, n, k] if
  *    trans_b (then B_j is used transposed), batch stride b_batch_stride.
  * c: K+1 pointers, each [batch, m, n] contiguous.
- * dtype: PT_FLOAT32 (fp32 MFMA) or PT_FLOAT64 (fp64 MFMA).
+ * dtype: PT_FLOAT32 (fp32 MFMA), PT_FLOAT64 (fp64 MFMA), or PT_BFLOAT16 / PT_FLOAT16 (16-bit MFMA
+ * operands, fp32 accumulation, each output element rounded once; needs k and, unless trans_b, n
+ * to be multiples of 8, 16-byte aligned operands, batch strides that are multiples of 8 and each
+ * matrix below 1 GiB, else PT_UNSUPPORTED).
  */
 int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
                      const void* const* b, int b_orders, void* const* c,
