@@ -394,8 +394,8 @@ def wl_norm(device):
         return _ops.norm_series(x, [w], [], n, 1e-6, False)
 
     nbytes = 2 * (K + 1) * rows * n * 2 + n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
-                kernel="norm_series", dtype="bf16",
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", streams=(K + 1, K + 1), peak=PEAK_HBM,
+                bytes=nbytes, kernel="norm_series", dtype="bf16",
                 workload=f"rms_norm_series [{K + 1},{rows},{n}] bf16 weight eps=1e-6",
                 cpu=lambda: cpu_norm(rows, n, K))
 
@@ -415,8 +415,8 @@ def wl_ce(device):
         return _ops.cross_entropy_series(z, y, -100, 1, 0.0)
 
     nbytes = (K + 1) * rows * classes * 4 + rows * 8 + (K + 1) * rows * 4
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="read", peak=PEAK_HBM, bytes=nbytes,
-                kernel="cross_entropy_series", dtype="fp32",
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="read", peak=PEAK_HBM,
+                bytes=nbytes, kernel="cross_entropy_series", dtype="fp32",
                 workload=f"cross_entropy_series [{K + 1},{rows},{classes}] fp32 mean",
                 cpu=lambda: cpu_ce(rows, classes, K))
 
@@ -434,8 +434,8 @@ def wl_activation(device):
         return _ops.activation_series(x, "gelu")
 
     nbytes = 2 * (K + 1) * rows * n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
-                kernel="activation_series", dtype="bf16",
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", streams=(K + 1, K + 1), peak=PEAK_HBM,
+                bytes=nbytes, kernel="activation_series", dtype="bf16",
                 workload=f"gelu_series [{K + 1},{rows},{n}] bf16",
                 cpu=lambda: cpu_activation(rows, n, K))
 
@@ -454,8 +454,8 @@ def wl_norm_bwd(device):
         return _ops.norm_series_backward(x, g, n, 1e-6, False)
 
     nbytes = 3 * (K + 1) * rows * n * 2
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
-                kernel="norm_series_bwd", dtype="bf16",
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", streams=(2 * (K + 1), K + 1), peak=PEAK_HBM,
+                bytes=nbytes, kernel="norm_series_bwd", dtype="bf16",
                 workload=f"rms_norm_series_backward [{K + 1},{rows},{n}] bf16",
                 cpu=lambda: cpu_norm_bwd(rows, n, K))
 
@@ -477,8 +477,8 @@ def wl_ce_bwd(device):
         return _ops.cross_entropy_series_backward(z, y, -100, 0.0, lse, cot)
 
     nbytes = 2 * (K + 1) * rows * classes * 4 + rows * 8 + 2 * (K + 1) * rows * 4
-    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", peak=PEAK_HBM, bytes=nbytes,
-                kernel="cross_entropy_series_bwd", dtype="fp32",
+    return dict(step=step, work=nbytes, unit="GB/s", bound="hbm", pattern="copy", streams=(K + 1, K + 1), peak=PEAK_HBM,
+                bytes=nbytes, kernel="cross_entropy_series_bwd", dtype="fp32",
                 workload=f"cross_entropy_series_backward [{K + 1},{rows},{classes}] fp32",
                 cpu=lambda: cpu_ce_bwd(rows, classes, K))
 
@@ -729,7 +729,7 @@ def cpu_model():
     return "unknown"
 
 
-def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
+def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2, streams=None):
     """Measured HBM ceiling for a workload moving ``nbytes`` algorithmic bytes.
 
     pattern "read": pt_stream_read over nbytes; "copy": pt_stream_copy of nbytes / 2
@@ -737,6 +737,11 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
     (16-byte non-temporal accesses); the best over grid sizes and two layouts (a
     contiguous chunk per block, a grid-stride walk) is reported, beside torch's own
     copy for "copy".
+
+    ``streams`` = (sources, destinations): the same bytes over that many separate
+    buffers with the series kernels' own pattern (one 16-byte vector of every order per
+    thread, pt_stream_series), reported as ``series_rate``: the ceiling of the
+    kernels' multi-order access pattern, the median of five timings.
     """
     import torch
     from polytensors_amd import _lib
@@ -770,6 +775,24 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2):
         entry["torch_copy"] = round(moved / (time_steps(lambda: dst.copy_(src), reps, 1) * 1e-3) / 1e9, 1)
     del src, dst, out
     torch.cuda.empty_cache()
+    if streams is not None:
+        ns, nd = streams
+        each = nbytes // (ns + nd) // 16 * 16
+        srcs = [torch.empty(each // 4, device=device).fill_(1.0) for _ in range(ns)]
+        dsts = [torch.empty(each // 4, device=device) for _ in range(nd)]
+        blk = torch.empty(max(1, lib.pt_stream_series_blocks(each)), dtype=torch.int32, device=device)
+        sp, dp = _lib.ptr_array(srcs), _lib.ptr_array(dsts) if nd else None
+
+        def fn():
+            _lib.check(lib.pt_stream_series(sp, ns, dp, nd, each, blk.data_ptr(), stream), "stream series")
+
+        reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup), 1e-3)))
+        rates = sorted(each * (ns + nd) / (time_steps(fn, reps, 1) * 1e-3) / 1e9 for _ in range(5))
+        entry["series_rate"] = round(rates[2], 1)
+        entry["series_how"] = (f"pt_stream_series: {ns} source and {nd} destination buffers of {each} bytes, "
+                               "one 16-byte vector of each per thread (median of 5)")
+        del srcs, dsts, blk
+        torch.cuda.empty_cache()
     return entry
 
 
@@ -887,8 +910,10 @@ def main():
                      "traffic": profiled_traffic(w["kernel"]) if w["peak"] else None},
     }
     if w["bound"] == "hbm" and not args.no_ceiling:
-        ceil = stream_ceiling(device, w["pattern"], w["bytes"])
+        ceil = stream_ceiling(device, w["pattern"], w["bytes"], streams=w.get("streams"))
         ceil["frac"] = round(w["achieved"] / ceil["rate"], 4)
+        if "series_rate" in ceil:
+            ceil["series_frac"] = round(w["achieved"] / ceil["series_rate"], 4)
         line["roofline"]["stream_ceiling"] = ceil
     if "graph_result" in w:
         gr = w["graph_result"]
@@ -911,8 +936,10 @@ def main():
                                         "nodes": gr["nodes"], "matches_eager": gr["matches_eager"],
                                         "launches_per_step": (gr["nodes"] or {}).get("kernel")}
             if c["bound"] == "hbm" and not args.no_ceiling:
-                ceil = stream_ceiling(device, c["pattern"], c["bytes"])
+                ceil = stream_ceiling(device, c["pattern"], c["bytes"], streams=c.get("streams"))
                 ceil["frac"] = round(c["achieved"] / ceil["rate"], 4)
+                if "series_rate" in ceil:
+                    ceil["series_frac"] = round(c["achieved"] / ceil["series_rate"], 4)
                 comps[name]["stream_ceiling"] = ceil
             cpu_samplers[name] = c["cpu"]
             _progress(f"component {name}: {c['ms']:.4f} ms ({c['achieved']:.1f} {c['unit']})")

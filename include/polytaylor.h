@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 8
+#define PT_ABI_VERSION 9
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -412,6 +412,16 @@ int pt_series_binary(int dtype, int degree, int op, const void* const* a,
 int pt_stream_copy(const void* src, void* dst, int64_t bytes, int blocks, int chunked, void* stream);
 int pt_stream_read(const void* src, int64_t bytes, int blocks, int chunked, void* out, void* stream);
 int pt_stream_probe_blocks(void);
+/*
+ * The series kernels' own pattern over separate buffers (the K+1 orders of a series): ns
+ * sources (1..18) and nd destinations (0..9) of bytes_each bytes each; every thread reads one
+ * 16-byte vector of every source at its index and writes their XOR to every destination, a
+ * block per 256 indices. With nd = 0 it writes out[b] = XOR of block b's words (out holds
+ * pt_stream_series_blocks(bytes_each) uint32 values).
+ */
+int pt_stream_series(const void* const* src, int ns, void* const* dst, int nd, int64_t bytes_each, void* out,
+                     void* stream);
+int64_t pt_stream_series_blocks(int64_t bytes_each);
 
 #ifdef __cplusplus
 }

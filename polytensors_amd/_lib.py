@@ -13,7 +13,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -63,6 +63,8 @@ SIGNATURES = {
     "pt_stream_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "pt_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "pt_stream_probe_blocks": (_c_int, []),
+    "pt_stream_series": (_c_int, [_c_vpp, _c_int, _c_vpp, _c_int, _c_i64, _c_vp, _c_vp]),
+    "pt_stream_series_blocks": (_c_i64, [_c_i64]),
     "pt_complex_to_real": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_real_to_complex": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_dblp, _c_dblp, _c_vpp, _c_i64, _c_vp]),
     "pt_activation_series_fwd": (_c_int, [_c_int, _c_int, _c_int, _c_vpp, _c_vpp, _c_i64, _c_vp]),

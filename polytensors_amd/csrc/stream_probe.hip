@@ -5,6 +5,8 @@
 // They measure the practical ceiling those kernels are compared with beside the
 // published 8 TB/s; they compute nothing of the series and have no counterpart
 // in the reference.
+#include <algorithm>
+
 #include "pt_common.h"
 
 namespace pt {
@@ -81,6 +83,52 @@ __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const u32x4_
   }
 }
 
+// Series-kernel pattern: ns source and nd destination buffers of n vectors each
+// (the K+1 orders of a series and their outputs). Each thread takes one 16-byte
+// vector of every source at its index, reads them all, then writes their XOR to
+// every destination (or, with none, accumulates it into out[block]), as the
+// elementwise series kernels take one vector of every order per thread; a block
+// per 256 indices, striding past kProbeMaxSeriesBlocks blocks.
+constexpr int kProbeMaxStreams = 2 * kMaxOrders;
+constexpr int64_t kProbeMaxSeriesBlocks = int64_t(1) << 20;
+struct ProbeStreams {
+  const u32x4_t* src[kProbeMaxStreams];
+  u32x4_t* dst[kMaxOrders];
+};
+
+__global__ __launch_bounds__(kProbeThreads) void stream_series_kernel(ProbeStreams p, int ns, int nd, int64_t n,
+                                                                      uint32_t* __restrict__ out) {
+  __shared__ uint32_t part[kProbeThreads / kWave];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kProbeThreads;
+  u32x4_t total = {0u, 0u, 0u, 0u};
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x; i < n; i += stride) {
+    u32x4_t v[kProbeMaxStreams];
+#pragma unroll
+    for (int s = 0; s < kProbeMaxStreams; ++s)
+      if (s < ns) v[s] = __builtin_nontemporal_load(p.src[s] + i);
+    u32x4_t x = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < kProbeMaxStreams; ++s)
+      if (s < ns) x ^= v[s];
+#pragma unroll
+    for (int d = 0; d < kMaxOrders; ++d)
+      if (d < nd) __builtin_nontemporal_store(x, p.dst[d] + i);
+    total ^= x;
+  }
+  if (nd > 0) return;
+  uint32_t x = total.x ^ total.y ^ total.z ^ total.w;
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) x ^= __shfl_xor(x, off);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kProbeThreads / kWave; ++w) t ^= part[w];
+    out[blockIdx.x] = t;
+  }
+}
+
 }  // namespace pt
 
 namespace {
@@ -136,5 +184,41 @@ int pt_stream_read(const void* src, int64_t bytes, int blocks, int chunked, void
 }
 
 int pt_stream_probe_blocks(void) { return pt::kProbeDefaultBlocks; }
+
+int pt_stream_series(const void* const* src, int ns, void* const* dst, int nd, int64_t bytes_each, void* out,
+                     void* stream) {
+  pt_host::clear_error();
+  PT_REQUIRE(ns >= 1 && ns <= pt::kProbeMaxStreams && nd >= 0 && nd <= pt::kMaxOrders, PT_INVALID_ARGUMENT,
+             "stream series: 1..18 sources and 0..9 destinations");
+  PT_REQUIRE(bytes_each >= 0 && bytes_each % 16 == 0, PT_INVALID_ARGUMENT,
+             "stream series: bytes_each must be a non-negative multiple of 16");
+  PT_REQUIRE(src != nullptr && (nd == 0 || dst != nullptr), PT_INVALID_ARGUMENT,
+             "stream series: pointer arrays are required");
+  PT_REQUIRE(nd > 0 || out != nullptr, PT_INVALID_ARGUMENT,
+             "stream series: out (one uint32 per block) is required without destinations");
+  pt::ProbeStreams p{};
+  for (int s = 0; s < ns; ++s) {
+    PT_REQUIRE(bytes_each == 0 || (src[s] != nullptr && pt_host::aligned16(src[s])), PT_INVALID_ARGUMENT,
+               "stream series: sources must be 16-byte aligned device pointers");
+    p.src[s] = static_cast<const pt::u32x4_t*>(src[s]);
+  }
+  for (int d = 0; d < nd; ++d) {
+    PT_REQUIRE(bytes_each == 0 || (dst[d] != nullptr && pt_host::aligned16(dst[d])), PT_INVALID_ARGUMENT,
+               "stream series: destinations must be 16-byte aligned device pointers");
+    p.dst[d] = static_cast<pt::u32x4_t*>(dst[d]);
+  }
+  const int64_t n = bytes_each / 16;
+  if (n == 0) return PT_OK;
+  const int64_t blocks = std::min<int64_t>((n + pt::kProbeThreads - 1) / pt::kProbeThreads, pt::kProbeMaxSeriesBlocks);
+  pt::stream_series_kernel<<<static_cast<unsigned>(blocks), pt::kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      p, ns, nd, n, static_cast<uint32_t*>(out));
+  PT_LAUNCH_CHECK();
+  return PT_OK;
+}
+
+int64_t pt_stream_series_blocks(int64_t bytes_each) {
+  if (bytes_each <= 0) return 0;
+  return std::min<int64_t>((bytes_each / 16 + pt::kProbeThreads - 1) / pt::kProbeThreads, pt::kProbeMaxSeriesBlocks);
+}
 
 }  // extern "C"

@@ -47,3 +47,26 @@ def test_read_checksum_covers_every_word(nbytes, blocks, chunked):
     got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)) if grid else 0
     want = np.bitwise_xor.reduce(host.numpy().view(np.uint32)) if nbytes else np.uint32(0)
     assert int(got) == int(want)
+
+
+@pytest.mark.parametrize("nbytes", [0, 16, 4096 + 48, (1 << 20) + 16 * 5])
+@pytest.mark.parametrize("ns,nd", [(1, 1), (5, 5), (10, 5), (5, 0), (18, 9)])
+def test_series_pattern_touches_every_vector(nbytes, ns, nd):
+    # every destination receives the XOR of the sources at each vector; without destinations the
+    # per-block words XOR to that of every source word
+    srcs_host = [_words(nbytes, 100 * nbytes + 3 * s + ns) for s in range(ns)]
+    srcs = [h.cuda() for h in srcs_host]
+    dsts = [torch.full((nbytes // 4,), -1, dtype=torch.int32, device="cuda") for _ in range(nd)]
+    lib = _lib.load()
+    blocks = max(1, lib.pt_stream_series_blocks(nbytes))
+    out = torch.full((blocks,), 12345, dtype=torch.int32, device="cuda")
+    _lib.check(lib.pt_stream_series(_lib.ptr_array(srcs), ns, _lib.ptr_array(dsts) if nd else None, nd, nbytes,
+                                    out.data_ptr(), _lib.stream_of(out.device)), "stream series")
+    torch.cuda.synchronize()
+    x = np.zeros(nbytes // 4, dtype=np.uint32)
+    for h in srcs_host:
+        x ^= h.numpy().view(np.uint32)
+    for d in dsts:
+        assert np.array_equal(d.cpu().numpy().view(np.uint32), x)
+    if nd == 0 and nbytes:
+        assert int(np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))) == int(np.bitwise_xor.reduce(x))
