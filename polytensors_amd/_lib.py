@@ -13,6 +13,8 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
+# the operators' PyTorch registration (csrc/torch_ops.cpp), linked with libpolytaylor.so
+TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor_torch.so")
 ABI_VERSION = 9
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
@@ -107,6 +109,28 @@ def load():
             raise LibraryMissingError(f"{LIB_PATH} has ABI {lib.pt_abi_version()}, expected {ABI_VERSION}: rebuild it")
         _lib = lib
     return _lib
+
+
+_torch_ops_loaded = False
+
+
+def load_torch_ops():
+    """Load the C++ operator registration once; False when it is not built (or the kernel
+    library it links against is missing or of another ABI)."""
+    global _torch_ops_loaded
+    if _torch_ops_loaded:
+        return True
+    if not os.path.exists(TORCH_LIB_PATH):
+        return False
+    try:
+        load()   # the kernel library first, with its ABI check (takes the lock itself)
+    except (LibraryMissingError, OSError):
+        return False
+    with _lock:
+        if not _torch_ops_loaded:
+            torch.ops.load_library(TORCH_LIB_PATH)
+            _torch_ops_loaded = True
+    return True
 
 
 def available():

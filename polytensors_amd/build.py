@@ -1,10 +1,14 @@
-"""Build ``libpolytaylor.so`` (the C-ABI library of the gfx950 kernels) in-tree.
+"""Build ``libpolytaylor.so`` (the C-ABI library of the gfx950 kernels) and its
+PyTorch registration ``libpolytaylor_torch.so`` in-tree.
 
 Every ``csrc/*.hip`` file is compiled with ``hipcc --offload-arch=gfx950`` into
 an object under ``csrc/_build/``, in parallel, and the objects are linked into
 ``polytensors_amd/_lib/libpolytaylor.so``. The library links the HIP runtime by
 soname (``libamdhip64.so.7``), so inside a process that imported torch first it
-binds to the runtime torch already loaded.
+binds to the runtime torch already loaded. ``csrc/torch_ops.cpp`` (host code:
+the ``polytensors_amd::*`` operator schemas and their HIP implementations over
+the C ABI) is compiled against the installed torch's headers and linked with
+``libpolytaylor.so`` (found beside it) and torch's libraries.
 
 Run ``python -m polytensors_amd.build`` (incremental) or ``--force``.
 """
@@ -21,6 +25,9 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(CSRC, "_build")
 LIB_DIR = os.path.join(HERE, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpolytaylor.so")
+TORCH_LIB_PATH = os.path.join(LIB_DIR, "libpolytaylor_torch.so")
+TORCH_SRC = os.path.join(CSRC, "torch_ops.cpp")
+CXX = os.environ.get("CXX", "g++")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -111,7 +118,51 @@ def build(force=False, jobs=None, verbose=True):
         os.replace(tmp, LIB_PATH)
         if verbose:
             print(f"[polytaylor] linked {LIB_PATH}", flush=True)
+    build_torch_ops(force=force or bool(todo), verbose=verbose)
     return LIB_PATH
+
+
+def _torch_flags():
+    import torch
+    import torch.utils.cpp_extension as ext
+
+    try:
+        incs, libs = ext.include_paths(device_type="cuda"), ext.library_paths(device_type="cuda")
+    except TypeError:   # older signature
+        incs, libs = ext.include_paths(cuda=True), ext.library_paths(cuda=True)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return ([f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM"] +
+            [f"-I{d}" for d in incs], [f"-L{d}" for d in libs] + [f"-Wl,-rpath,{d}" for d in libs])
+
+
+def build_torch_ops(force=False, verbose=True):
+    """Compile csrc/torch_ops.cpp into _lib/libpolytaylor_torch.so (skipped when up to date)."""
+    files = set()
+    _local_includes(TORCH_SRC, files)
+    cflags, ldflags = _torch_flags()
+    h = hashlib.sha256(" ".join(cflags + ldflags).encode())
+    for path in sorted(files):
+        with open(path, "rb") as fh:
+            h.update(path.encode() + b"\0" + fh.read())
+    stamp = TORCH_LIB_PATH + ".digest"
+    digest = h.hexdigest()
+    if not force and os.path.exists(TORCH_LIB_PATH) and os.path.exists(stamp):
+        with open(stamp) as fh:
+            if fh.read().strip() == digest:
+                return TORCH_LIB_PATH
+    tmp = TORCH_LIB_PATH + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-shared", *cflags, TORCH_SRC, "-o", tmp,
+           f"-L{LIB_DIR}", "-lpolytaylor", *ldflags, "-Wl,-rpath,$ORIGIN",
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build of libpolytaylor_torch.so failed:\n{proc.stderr}")
+    os.replace(tmp, TORCH_LIB_PATH)
+    with open(stamp, "w") as fh:
+        fh.write(digest + "\n")
+    if verbose:
+        print(f"[polytaylor] built {TORCH_LIB_PATH}", flush=True)
+    return TORCH_LIB_PATH
 
 
 if __name__ == "__main__":

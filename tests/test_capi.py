@@ -9,6 +9,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from polytensors_amd import _lib
 
@@ -67,3 +68,15 @@ def test_empty_rows_is_a_no_op():
     lib = _lib.load()
     assert lib.pt_rms_norm_series_fwd(0, 2, _vpp(3), None, 0, _vpp(3), 0, 16, 1e-5, None) == 0
     assert lib.pt_last_error().decode() == ""
+
+
+def test_operator_schemas_match_the_cpp_registration():
+    # polytensors_amd/_ops.py states the schemas the C++ extension (csrc/torch_ops.cpp) registers,
+    # for the stand-in used when the extension is not built; the two must not drift apart
+    from polytensors_amd import _ops
+
+    if not _ops.NATIVE:
+        pytest.skip("libpolytaylor_torch.so is not built")
+    for name, schema in _ops.SCHEMAS.items():
+        got = str(getattr(torch.ops.polytensors_amd, name).default._schema)
+        assert got == f"polytensors_amd::{name}{schema}", name
