@@ -30,6 +30,7 @@ import functools
 import torch
 
 from . import _ops
+from ._tensor import PolyTensor
 
 _NODE_RADIUS = {1: 1.0, 2: 1.5, 3: 1.5}
 
@@ -51,8 +52,6 @@ def nodes_and_weights(degree):
 
 
 def _is_complex_series(x):
-    from ._tensor import PolyTensor
-
     return isinstance(x, PolyTensor) and any(c.is_complex() for c in x.coeffs)
 
 
@@ -71,8 +70,6 @@ def has_complex(*values):
 
 
 def _check(values, what):
-    from ._tensor import PolyTensor
-
     for v in values:
         if isinstance(v, PolyTensor) and v.coeffs[0].is_complex():
             raise NotImplementedError(f"{what}: a complex constant coefficient (complex base) is not implemented; "
@@ -100,8 +97,6 @@ def _planes(x):
 
 def _variants(x, alpha, beta):
     """Real-direction series alpha_v Re + beta_v Im of x's higher orders (order 0 shared), one per v."""
-    from ._tensor import PolyTensor
-
     planes = _ops.complex_to_real(_planes(x), list(alpha), list(beta))
     return [PolyTensor((x.coeffs[0],) + tuple(v.unbind(0))) for v in planes.unbind(0)]
 
@@ -117,8 +112,6 @@ def _substitute(x, table):
 
 def _combine(outputs, weights):
     """Complex series sum_m w_m Y_m in the higher orders; order 0 of the first run."""
-    from ._tensor import PolyTensor
-
     first = outputs[0]
     orders = first.degree
     if orders == 0:
@@ -134,8 +127,6 @@ def at_real_nodes(fn, what, *args, **kwargs):
     ``fn`` returns one PolyTensor. The real variants of every complex-direction
     operand are formed in one pass per operand (all nodes at once).
     """
-    from ._tensor import PolyTensor
-
     values = _flatten(list(args) + list(kwargs.values()))
     _check(values, what)
     degree = next(v.degree for v in values if isinstance(v, PolyTensor))
@@ -161,8 +152,6 @@ def bilinear(fn, what, a, b, *rest, **kwargs):
     one: an ordinary operand does not mix orders), so it forms K products, not
     K+1. Two series operands use the four real runs of the complex product.
     """
-    from ._tensor import PolyTensor
-
     _check([a, b], what)
     ac, bc = _is_complex_series(a), _is_complex_series(b)
     if ac != bc and not isinstance(b if ac else a, PolyTensor):
@@ -198,8 +187,6 @@ def bilinear(fn, what, a, b, *rest, **kwargs):
 
 def _combine_parts(real, imag_orders):
     """Series with order 0 of ``real`` and orders k >= 1 = real_k + i imag_orders[k-1]."""
-    from ._tensor import PolyTensor
-
     orders = real.degree
     if orders == 0:
         return real

@@ -14,6 +14,9 @@ reason (it has no general rules).
 import torch
 import torch.nn.functional as F
 
+from ._tensor import PolyTensor
+from . import _fused_attention, _fused_cross_entropy, _fused_matmul, _fused_norm
+
 _RMS_NORM = frozenset((F.rms_norm, torch.rms_norm))
 _LAYER_NORM = frozenset((F.layer_norm, torch.layer_norm))
 _ATTENTION = frozenset((F.scaled_dot_product_attention,))
@@ -25,8 +28,6 @@ _MATMUL = frozenset((torch.matmul, torch.Tensor.matmul, torch.Tensor.__matmul__,
 
 
 def _has_poly(values):
-    from ._tensor import PolyTensor
-
     return any(isinstance(v, PolyTensor) for v in values)
 
 
@@ -46,7 +47,6 @@ def maybe_decompose(function, args, kwargs):
         bound.update(kwargs)
         if not _has_poly((bound.get("input"), bound.get("weight"), bound.get("bias"))):
             return NotImplemented
-        from . import _fused_norm
 
         shape = tuple(bound["normalized_shape"]) if not isinstance(bound["normalized_shape"], int) \
             else (bound["normalized_shape"],)
@@ -62,7 +62,6 @@ def maybe_decompose(function, args, kwargs):
             return NotImplemented
         if bound.get("size_average") is not None or bound.get("reduce") is not None:
             raise NotImplementedError("cross_entropy: the deprecated size_average/reduce arguments are not supported")
-        from . import _fused_cross_entropy
 
         loss = _fused_cross_entropy.fused_or_raise(
             bound["input"], bound["target"], weight=bound.get("weight"),
@@ -77,18 +76,15 @@ def maybe_decompose(function, args, kwargs):
         bound.update(kwargs)
         if not _has_poly(bound.values()):
             return NotImplemented
-        from . import _fused_attention
 
         _fused_attention.require_eligible(bound["query"], bound["key"], bound["value"], bound.get("attn_mask"),
                                           bound.get("dropout_p", 0.0), bound.get("is_causal", False),
                                           bound.get("enable_gqa", False))
-        return _fused_attention.attention(bound["query"], bound["key"], bound["value"],
+        return _fused_attention.attention_checked(bound["query"], bound["key"], bound["value"],
                                           attn_mask=bound.get("attn_mask"), is_causal=bound.get("is_causal", False),
                                           scale=bound.get("scale"))
 
     if function in _MATMUL:
-        from . import _fused_matmul
-
         if _needs_grad(args, kwargs):
             # Let autograd record mm/bmm/addmm; they reach the kernel through __torch_dispatch__,
             # and so do the products of their backward.

@@ -25,6 +25,9 @@ package.
 import torch
 from torch.utils._python_dispatch import return_and_correct_aliasing
 
+from ._tensor import PolyTensor
+from . import _fused_activation, _fused_elementwise, _fused_matmul
+
 aten = torch.ops.aten
 
 _VIEW_OPS = {
@@ -70,8 +73,6 @@ def _gelu_kind(approximate):
 
 
 def _is_poly(x):
-    from ._tensor import PolyTensor
-
     return type(x) is PolyTensor
 
 
@@ -87,8 +88,6 @@ def _collect(x, out):
 
 
 def _wrap(coeffs):
-    from ._tensor import PolyTensor
-
     return PolyTensor(tuple(coeffs), requires_grad=False)
 
 
@@ -216,7 +215,6 @@ def _dispatch(func, types, args, kwargs, polys):
         return _wrap((other - alpha * x.coeffs[0], *(-alpha * c for c in x.coeffs[1:])))
     if func is aten.reciprocal.default:
         # quotient(1, x) (/root/reference/src/polytensors/_range_ops.py:86-93,157-158)
-        from . import _fused_elementwise
 
         return _fused_elementwise.binary(torch.ones_like(args[0].coeffs[0]), args[0], "div")
 
@@ -235,8 +233,6 @@ def _dispatch(func, types, args, kwargs, polys):
         if func in _DIV and kwargs.get("rounding_mode") is not None:
             raise NotImplementedError("PolyTensor does not implement rounded division")
         if (_is_poly(a) and _is_poly(b)) or (func in _DIV and _is_poly(b)):
-            from . import _fused_elementwise
-
             if not isinstance(a, torch.Tensor):
                 a = torch.as_tensor(a, dtype=b.dtype, device=b.device)
             return _fused_elementwise.binary(a, b, "mul" if func in _MUL else "div")
@@ -248,13 +244,9 @@ def _dispatch(func, types, args, kwargs, polys):
         return _wrap(func(*_per_order(args, k), **kwargs) for k in range(count))
 
     if func in _MATMUL or func is aten.addmm.default:
-        from . import _fused_matmul
-
         return _fused_matmul.from_dispatch(func, args, kwargs)
 
     if func in _ACTIVATION or func is aten.gelu.default:
-        from . import _fused_activation
-
         if func is aten.gelu.default:
             kind = _gelu_kind(args[1] if len(args) > 1 else kwargs.get("approximate", "none"))
         else:
@@ -262,8 +254,6 @@ def _dispatch(func, types, args, kwargs, polys):
         return _fused_activation.activation(args[0], kind)
 
     if func in _ACTIVATION_BACKWARD or func is aten.gelu_backward.default:
-        from . import _fused_activation
-
         if func is aten.gelu_backward.default:
             kind = _gelu_kind(args[2] if len(args) > 2 else kwargs.get("approximate", "none"))
         else:

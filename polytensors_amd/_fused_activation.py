@@ -14,14 +14,13 @@ Half and bfloat16 compute in float32, float64 in float64.
 import torch
 
 from . import _complex, _gate, _ops
+from ._tensor import PolyTensor
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 BACKWARD_KINDS = ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu")
 
 
 def why_ineligible(*operands, complex_ok=False):
-    from ._tensor import PolyTensor
-
     # Reached from __torch_dispatch__ only: autograd above has recorded the native
     # backward operation (gelu_backward, tanh_backward, ...), which routes here too.
     reason = _gate.common_reason(operands, below_autograd=True, complex_ok=complex_ok)
@@ -40,8 +39,6 @@ def why_ineligible(*operands, complex_ok=False):
 
 
 def _coeffs(x, degree):
-    from ._tensor import PolyTensor
-
     if isinstance(x, PolyTensor):
         return [c.contiguous() for c in x.coeffs]
     base = x.contiguous()
@@ -50,8 +47,6 @@ def _coeffs(x, degree):
 
 def activation(x, kind):
     """Series of ``f(x)`` for ``kind`` in gelu, gelu_tanh, tanh, sigmoid, silu, exp, log."""
-    from ._tensor import PolyTensor
-
     reason = why_ineligible(x, complex_ok=True)
     if reason is not None:
         raise NotImplementedError(f"{kind}: {reason}")
@@ -67,8 +62,6 @@ def backward(grad, saved, kind):
     ``saved`` is the forward input for gelu, gelu_tanh and silu and the forward
     output for tanh and sigmoid, as the aten backward operations take them.
     """
-    from ._tensor import PolyTensor
-
     if kind not in BACKWARD_KINDS:
         raise NotImplementedError(f"{kind}_backward has no series kernel")
     reason = why_ineligible(grad, saved)

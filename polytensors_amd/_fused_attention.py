@@ -24,6 +24,7 @@ import math
 import torch
 
 from . import _complex, _gate, _ops
+from ._tensor import PolyTensor
 
 _enabled = contextvars.ContextVar("polytensors_amd_fused_attention", default=True)
 _HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128),
@@ -70,8 +71,6 @@ def _needs_grad(*values):
 
 
 def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gqa):
-    from ._tensor import PolyTensor
-
     if not _enabled.get():
         return ("the fused attention kernel is disabled (PolyTensor.fused_attention(False)) and "
                 "polytensors_amd has no general series rules")
@@ -131,8 +130,6 @@ def _flat(coeffs, shape):
 
 def _full(x, degree, shape):
     """K+1 flattened [bh, T, d] coefficients; an ordinary tensor gets zero higher orders."""
-    from ._tensor import PolyTensor
-
     if isinstance(x, PolyTensor):
         return _flat(x.coeffs, shape)
     base = _flat([x], shape)[0]
@@ -151,8 +148,6 @@ class _SeriesAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, key, value, mask, causal, scale):
-        from ._tensor import PolyTensor
-
         degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
         q = _full(query, degree, query.shape)
         k = _full(key, degree, key.shape)
@@ -166,8 +161,6 @@ class _SeriesAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gradient):
         from ._plain import _plain_range
-        from ._tensor import PolyTensor
-
         if torch.is_grad_enabled():
             raise NotImplementedError("second-order reverse mode through the fused attention is not implemented")
         degree, mask, causal, scale, shape_q, shape_k = ctx.meta
@@ -188,9 +181,12 @@ class _SeriesAttention(torch.autograd.Function):
 
 def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
     """Fused degree-K attention of an eligible call (see ``eligible``)."""
-    from ._tensor import PolyTensor
-
     require_eligible(query, key, value, attn_mask, 0.0, is_causal, False)
+    return attention_checked(query, key, value, attn_mask, is_causal, scale)
+
+
+def attention_checked(query, key, value, attn_mask=None, is_causal=False, scale=None):
+    """``attention`` for a call whose eligibility (including dropout and GQA) the caller checked."""
     if _complex.has_complex(query, key, value):
         return _complex.at_real_nodes(attention, "scaled_dot_product_attention", query, key, value,
                                       attn_mask=attn_mask, is_causal=is_causal, scale=scale)

@@ -16,6 +16,7 @@ import contextvars
 import torch
 
 from . import _complex, _gate, _lib, _ops
+from ._tensor import PolyTensor
 
 _enabled = contextvars.ContextVar("polytensors_amd_fused_cross_entropy", default=True)
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
@@ -23,8 +24,6 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing=0.0, softcap=None,
                    allow_grad=False):
-    from ._tensor import PolyTensor
-
     if not _enabled.get():
         return ("the fused cross-entropy kernel is disabled (PolyTensor.fused_cross_entropy(False)) and "
                 "polytensors_amd has no general series rules")
@@ -82,8 +81,6 @@ class _SeriesCrossEntropy(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, target, ignore_index, softcap):
-        from ._tensor import PolyTensor
-
         z = _rows(logits.coeffs)
         target = target.contiguous()
         loss, lse = _ops.cross_entropy_series(z, target, int(ignore_index), 0, float(softcap or 0.0))
@@ -94,8 +91,6 @@ class _SeriesCrossEntropy(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gradient):
         from ._plain import _plain_range
-        from ._tensor import PolyTensor
-
         if torch.is_grad_enabled():
             raise NotImplementedError("second-order reverse mode through the fused cross entropy is not implemented")
         logits, target, lse = ctx.saved_tensors
@@ -123,8 +118,6 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     sum (and division by the count of kept rows), as the reference's
     /root/reference/src/polytensors/_fused_cross_entropy.py:163-170.
     """
-    from ._tensor import PolyTensor
-
     if _complex.has_complex(input):
         return _complex.at_real_nodes(fused, "cross_entropy", input, target, ignore_index=ignore_index,
                                       reduction=reduction, softcap=softcap)
@@ -154,8 +147,6 @@ def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mea
 def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="mean"):
     """``PolyTensor.cross_entropy``: series logits use the fused kernel (at least float32 out);
     ordinary tensors use the composite, as /root/reference/src/polytensors/_fused_cross_entropy.py:173-187."""
-    from ._tensor import PolyTensor
-
     if isinstance(logits, PolyTensor):
         reason = why_ineligible(logits, target, None, reduction, 0.0, softcap,
                                 allow_grad=_gate.wrapper_grad(logits))

@@ -12,13 +12,12 @@ when their shapes differ). Reached from ``__torch_dispatch__``, under autograd.
 import torch
 
 from . import _complex, _gate, _ops
+from ._tensor import PolyTensor
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
 def why_ineligible(a, b):
-    from ._tensor import PolyTensor
-
     reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True)
     if reason is not None:
         return reason
@@ -31,8 +30,6 @@ def why_ineligible(a, b):
 
 def binary(a, b, op):
     """Series of ``a * b`` (op "mul") or ``a / b`` (op "div")."""
-    from ._tensor import PolyTensor
-
     reason = why_ineligible(a, b)
     if reason is not None:
         raise NotImplementedError(f"series {op}: {reason}")

@@ -13,6 +13,7 @@ bfloat16 / float16 with fp32 accumulation and one rounding per element.
 import torch
 
 from . import _complex, _gate, _ops
+from ._tensor import PolyTensor
 
 _DTYPES = (torch.float32, torch.float64, torch.bfloat16, torch.float16)
 # the 16-bit kernel addresses each (column-padded) operand matrix with 32-bit byte offsets
@@ -42,15 +43,11 @@ def eligible(a, b):
 
 
 def _degree(*xs):
-    from ._tensor import PolyTensor
-
     return next(x.degree for x in xs if isinstance(x, PolyTensor))
 
 
 def matmul(a, b, below_autograd=False):
     """Series of ``torch.matmul(a, b)``."""
-    from ._tensor import PolyTensor
-
     reason = why_ineligible(a, b, below_autograd)
     if reason is not None:
         raise NotImplementedError(f"matmul: {reason}")
@@ -92,8 +89,6 @@ def matmul(a, b, below_autograd=False):
 
 def linear(x, weight, bias=None):
     """Series of ``torch.nn.functional.linear``: x @ weight^T (+ bias)."""
-    from ._tensor import PolyTensor
-
     reason = why_ineligible(x, weight)
     if reason is not None:
         raise NotImplementedError(f"linear: {reason}")

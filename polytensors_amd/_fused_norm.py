@@ -18,13 +18,12 @@ import math
 import torch
 
 from . import _complex, _gate, _ops
+from ._tensor import PolyTensor
 
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
 def why_ineligible(input, normalized_shape, weight=None, bias=None, allow_grad=False):
-    from ._tensor import PolyTensor
-
     reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad, complex_ok=True)
     if reason is not None:
         return reason
@@ -46,8 +45,6 @@ def eligible(input, normalized_shape, weight=None, bias=None):
 
 
 def _series_coeffs(x, degree):
-    from ._tensor import PolyTensor
-
     if isinstance(x, PolyTensor):
         return [c.contiguous() for c in x.coeffs]
     return [x.contiguous()] + [torch.zeros_like(x, memory_format=torch.contiguous_format)
@@ -56,8 +53,6 @@ def _series_coeffs(x, degree):
 
 def _affine_coeffs(a, input, shape):
     """Kernel-side coefficients of a weight/bias, or None if it must be applied separately."""
-    from ._tensor import PolyTensor
-
     if a is None:
         return []
     coeffs = a.coeffs if isinstance(a, PolyTensor) else (a,)
@@ -104,14 +99,10 @@ class _SeriesNorm(torch.autograd.Function):
 
 
 def _from_stacked(stacked):
-    from ._tensor import PolyTensor
-
     return PolyTensor.from_stacked(stacked)
 
 
 def _run(input, normalized_shape, weight, bias, eps, layer):
-    from ._tensor import PolyTensor
-
     shape = tuple(normalized_shape)
     grads = _needs_grad(input, weight, bias)
     reason = why_ineligible(input, shape, weight, bias, allow_grad=grads)

@@ -12,6 +12,7 @@ import torch
 
 from . import _lib
 from ._plain import plain_range_enabled
+from ._tensor import PolyTensor, _coefficient_autograd_enabled
 
 MAX_DEGREE = 8
 _REAL_OF = {torch.complex32: torch.float16, torch.complex64: torch.float32, torch.complex128: torch.float64}
@@ -24,8 +25,6 @@ def real_dtype(dtype):
 
 def coefficients(x, degree):
     """The coefficient tuple of a PolyTensor, or (x,) for an ordinary tensor (a plain operand)."""
-    from ._tensor import PolyTensor
-
     if isinstance(x, PolyTensor):
         return tuple(x.coeffs)
     return (x,)
@@ -40,8 +39,6 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
     ``complex_ok``: the entry point runs complex directions through its real kernel
     (polytensors_amd._complex); a complex constant coefficient is still refused.
     """
-    from ._tensor import PolyTensor, _coefficient_autograd_enabled
-
     tensors = [v for v in values if isinstance(v, torch.Tensor)]
     polys = [v for v in tensors if isinstance(v, PolyTensor)]
     if not polys:
@@ -83,8 +80,6 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
 def coefficient_graph(*values):
     """Whether this call builds a coefficient-level autograd graph: coefficient_autograd is on,
     grad mode is enabled and some coefficient (or ordinary tensor operand) requires grad."""
-    from ._tensor import PolyTensor, _coefficient_autograd_enabled
-
     if not (_coefficient_autograd_enabled.get() and torch.is_grad_enabled()):
         return False
     return any((c.requires_grad for c in v.coeffs) if isinstance(v, PolyTensor) else
@@ -94,8 +89,6 @@ def coefficient_graph(*values):
 def wrapper_grad(*values):
     """Whether this call is recorded by wrapper-level (PolyTensor) autograd: grad mode is enabled,
     coefficient_autograd is off and some operand requires grad."""
-    from ._tensor import _coefficient_autograd_enabled
-
     if _coefficient_autograd_enabled.get() or not torch.is_grad_enabled():
         return False
     return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)

@@ -33,13 +33,17 @@ _COMPLEX_OF = {torch.float16: torch.complex32, torch.float32: torch.complex64, t
 
 
 def _extent(t):
-    """[start, end) byte range of a strided tensor within its storage (conservative for gaps)."""
-    if t.numel() == 0:
+    """[start, end) byte addresses of a strided tensor's elements (conservative for gaps)."""
+    n = t.numel()
+    if n == 0:
         return 0, 0
-    span = 1 + sum((n - 1) * abs(st) for n, st in zip(t.shape, t.stride()))
-    start = t.storage_offset() - sum((n - 1) * abs(st) for n, st in zip(t.shape, t.stride()) if st < 0)
     size = t.element_size()
-    return start * size, (start + span) * size
+    start = t.data_ptr()
+    if t.is_contiguous():
+        return start, start + n * size
+    span = 1 + sum((d - 1) * abs(st) for d, st in zip(t.shape, t.stride()))
+    start -= size * sum((d - 1) * abs(st) for d, st in zip(t.shape, t.stride()) if st < 0)
+    return start, start + span * size
 
 
 def _overlaps(a, b):
@@ -47,10 +51,11 @@ def _overlaps(a, b):
 
     ``torch._C._overlaps`` (which the reference uses, _tensor.py:93,124) reports any two views of
     one storage as overlapping, so it would clone every order of a coefficient-stacked buffer.
-    This compares byte ranges instead: exact for the disjoint slices of a stacked [K+1, ...]
-    buffer, conservative for interleaved strided views.
+    This compares the byte addresses the two tensors span instead (live allocations never share
+    addresses): exact for the disjoint slices of a stacked [K+1, ...] buffer, conservative for
+    interleaved strided views.
     """
-    if a.device != b.device or a.untyped_storage().data_ptr() != b.untyped_storage().data_ptr():
+    if a.device != b.device:
         return False
     (s0, e0), (s1, e1) = _extent(a), _extent(b)
     return s0 < e1 and s1 < e0
@@ -155,7 +160,27 @@ class PolyTensor(torch.Tensor):
 
     @staticmethod
     def __new__(cls, coeffs, *, degree=None, requires_grad=False):
-        coeffs = _coerce_coeffs(coeffs, degree)
+        return cls._wrap(_coerce_coeffs(coeffs, degree), requires_grad)
+
+    def __init__(self, coeffs, *, degree=None, requires_grad=False):
+        pass
+
+    @classmethod
+    def from_stacked(cls, stacked, requires_grad=False):
+        """Wrap a coefficient-stacked ``[K+1, ...]`` tensor without copying.
+
+        The orders of a contiguous real stack (every kernel's output) are disjoint slices of one
+        shape, device and dtype, so they satisfy every coercion rule as they are and skip the
+        checks; any other stack goes through them."""
+        coeffs = tuple(stacked.unbind(0))
+        if (type(stacked) is torch.Tensor and stacked.layout == torch.strided and stacked.is_contiguous()
+                and stacked.dtype.is_floating_point and stacked.dim() >= 1 and stacked.shape[0] >= 1):
+            return cls._wrap(coeffs, requires_grad)
+        return cls(coeffs, requires_grad=requires_grad)
+
+    @classmethod
+    def _wrap(cls, coeffs, requires_grad=False):
+        """A PolyTensor over coefficients already known to satisfy the coercion rules."""
         head = coeffs[0]
         out = torch.Tensor._make_wrapper_subclass(
             cls, head.shape, strides=head.stride(), storage_offset=head.storage_offset(),
@@ -166,14 +191,6 @@ class PolyTensor(torch.Tensor):
         for scope in _retention_scopes.get():
             scope.append(out)
         return out
-
-    def __init__(self, coeffs, *, degree=None, requires_grad=False):
-        pass
-
-    @classmethod
-    def from_stacked(cls, stacked, requires_grad=False):
-        """Wrap a coefficient-stacked ``[K+1, ...]`` tensor without copying."""
-        return cls(tuple(stacked.unbind(0)), requires_grad=requires_grad)
 
     def _set_coeffs(self, coeffs):
         self.coeffs = _coerce_coeffs(coeffs)
@@ -300,8 +317,6 @@ class PolyTensor(torch.Tensor):
     @classmethod
     def __torch_function__(cls, func, types, args=(), kwargs=None):
         kwargs = {} if kwargs is None else kwargs
-        from ._decompositions import maybe_decompose
-
         result = maybe_decompose(func, args, kwargs)
         if result is not NotImplemented:
             return result
@@ -310,8 +325,6 @@ class PolyTensor(torch.Tensor):
 
     @classmethod
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
-        from ._dispatch import dispatch
-
         if _coefficient_autograd_enabled.get():
             # Subclass dispatch runs below the wrapper's autograd layer; re-include the
             # autograd keys so the rules' operations on the coefficient tensors (and the
@@ -322,3 +335,8 @@ class PolyTensor(torch.Tensor):
                     stack.enter_context(torch._C._SetExcludeDispatchKeyGuard(key, False))
                 return dispatch(func, types, args, kwargs)
         return dispatch(func, types, args, kwargs)
+
+
+# The routing modules import PolyTensor themselves, so they come after the class.
+from ._decompositions import maybe_decompose  # noqa: E402
+from ._dispatch import dispatch  # noqa: E402
