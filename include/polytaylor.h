@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 9
+#define PT_ABI_VERSION 10
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -250,6 +250,23 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
                             int64_t lq, int64_t lk, int64_t d, int causal,
                             const uint8_t* mask, const int32_t* mask_ranges,
                             double scale, void* stream);
+
+/*
+ * pt_taylor_attention_fwd with a workspace for launches of few workgroups (no counterpart in
+ * the reference; its kernels have no such split): the float32/float64 generic kernel then
+ * divides each query block's key range over several workgroups, which write partial sums
+ * into the workspace, and a second kernel merges them (same results up to the order of the
+ * floating-point sums). pt_taylor_attention_fwd_workspace_size gives the bytes this needs
+ * (0: the launch does not split, and the workspace may be NULL); a smaller workspace
+ * runs the launch unsplit. The workspace must be 16-byte aligned.
+ */
+size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
+                                              int64_t bh, int64_t lq, int64_t lk, int64_t d);
+int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int q_orders,
+                               const void* const* k, int k_orders, const void* const* v, int v_orders,
+                               void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
+                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Block ranges of a boolean [lq, lk] attention mask (nonzero = admissible),

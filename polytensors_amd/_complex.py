@@ -52,7 +52,8 @@ def nodes_and_weights(degree):
 
 
 def _is_complex_series(x):
-    return isinstance(x, PolyTensor) and any(c.is_complex() for c in x.coeffs)
+    # the higher orders share one dtype, complex when any order is (PolyTensor's coercion rules)
+    return isinstance(x, PolyTensor) and x.coeffs[-1].is_complex()
 
 
 def has_complex(*values):

@@ -38,6 +38,7 @@ _VIEW_OPS = {
     aten.narrow.default, aten.unfold.default, aten.diagonal.default, aten.as_strided.default,
     aten.view_as_real.default, aten.view_as_complex.default,
 }
+_COERCED_VIEWS = {aten.as_strided.default, aten.view_as_real.default, aten.view_as_complex.default}
 _COPY_OPS = {
     aten.clone.default, aten.detach.default, aten._to_copy.default, aten.contiguous.default,
     aten.index_select.default, aten.gather.default, aten.index.Tensor, aten.flip.default,
@@ -89,6 +90,10 @@ def _collect(x, out):
 
 def _wrap(coeffs):
     return PolyTensor(tuple(coeffs), requires_grad=False)
+
+
+def _wrap_views(coeffs):
+    return PolyTensor._wrap(tuple(coeffs))
 
 
 def _per_order(args, k):
@@ -158,11 +163,20 @@ def _dispatch(func, types, args, kwargs, polys):
 
     if func in _VIEW_OPS:
         source = args[0]
-        results = [func(*_per_order(args, k), **_per_order(kwargs, k)) for k in range(count)]
-        if isinstance(results[0], (tuple, list)):
-            out = type(results[0])(_wrap(r[i] for r in results) for i in range(len(results[0])))
+        if len(polys) == 1 and source is polys[0]:
+            rest = args[1:]
+            results = [func(c, *rest, **kwargs) for c in source.coeffs]
         else:
-            out = _wrap(results)
+            results = [func(*_per_order(args, k), **_per_order(kwargs, k)) for k in range(count)]
+        # A view of each order lies inside that order's memory, so the views of well-formed
+        # coefficients are disjoint, of one shape, dtype and device: wrapped as they are. The
+        # views that may leave their coefficient's memory (as_strided) or change the dtype go
+        # through the coercion rules.
+        wrap = _wrap if func in _COERCED_VIEWS else _wrap_views
+        if isinstance(results[0], (tuple, list)):
+            out = type(results[0])(wrap([r[i] for r in results]) for i in range(len(results[0])))
+        else:
+            out = wrap(results)
         del source
         return return_and_correct_aliasing(func, args, kwargs, out)
 

@@ -92,9 +92,10 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
         # ordinary operand would be a series, which autograd cannot hand to it
         return "an ordinary (non-PolyTensor) operand requires grad"
     dtype = query.dtype
-    coeffs = [c for x in tensors for c in _gate.coefficients(x, 0)]
-    if any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
-        return "query, key and value coefficients must share one dtype"
+    for x in tensors:   # (a series' higher orders share one dtype: its last order stands for them)
+        coeffs = _gate.coefficients(x, 0)
+        if coeffs[0].dtype != dtype or _gate.real_dtype(coeffs[-1].dtype) != dtype:
+            return "query, key and value coefficients must share one dtype"
     if dtype not in _HEAD_DIMS:
         return f"dtype {dtype} is not supported (float32, float64, bfloat16 or float16)"
     if query.ndim < 3 or key.shape != value.shape or query.shape[:-2] != key.shape[:-2]:
@@ -125,7 +126,9 @@ def require_eligible(query, key, value, attn_mask=None, dropout_p=0.0, is_causal
 
 def _flat(coeffs, shape):
     """[bh, T, d] contiguous coefficients (no copy when already contiguous)."""
-    return [c.expand(shape).reshape(-1, shape[-2], shape[-1]).contiguous() for c in coeffs]
+    rows, d = shape[-2], shape[-1]
+    return [c.view(-1, rows, d) if c.shape == shape and c.is_contiguous() else
+            c.expand(shape).reshape(-1, rows, d).contiguous() for c in coeffs]
 
 
 def _full(x, degree, shape):

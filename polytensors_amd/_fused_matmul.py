@@ -66,12 +66,18 @@ def matmul(a, b, below_autograd=False):
     kb, n = B[0].shape[-2:]
     if kd != kb:
         raise RuntimeError(f"matmul: inner dimensions differ ({kd} vs {kb})")
-    batch = torch.broadcast_shapes(A[0].shape[:-2], B[0].shape[:-2])
+    batch_a, batch_b = A[0].shape[:-2], B[0].shape[:-2]
+    batch = batch_a if batch_a == batch_b or not batch_b else \
+        batch_b if not batch_a else torch.broadcast_shapes(batch_a, batch_b)
 
     def flat(coeffs, rows, cols):
         own = coeffs[0].shape[:-2]
         if len(own) == 0 or (tuple(own) != tuple(batch) and all(s == 1 for s in own)):
-            return [c.reshape(1, rows, cols).contiguous() for c in coeffs]
+            return [c.view(1, rows, cols) if c.is_contiguous() else c.reshape(1, rows, cols).contiguous()
+                    for c in coeffs]
+        if own == batch:
+            return [c.view(-1, rows, cols) if c.is_contiguous() else c.reshape(-1, rows, cols).contiguous()
+                    for c in coeffs]
         return [c.expand(*batch, rows, cols).reshape(-1, rows, cols).contiguous() for c in coeffs]
 
     if all(c.ndim == 2 and not c.is_contiguous() and c.t().is_contiguous() for c in B):

@@ -51,14 +51,17 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
         return "PolyTensor operands must have the same degree"
     if degree > MAX_DEGREE:
         return f"degree {degree} exceeds the kernels' maximum {MAX_DEGREE}"
-    coeffs = [c for t in tensors for c in coefficients(t, degree)]
+    plain = [t for t in tensors if not isinstance(t, PolyTensor)]
+    # A series' orders share one device, its higher orders one dtype (the coercion rules of
+    # PolyTensor), so the constant and the last order stand for every coefficient below.
+    complex_dirs = any(p.coeffs[-1].is_complex() for p in polys) or any(t.is_complex() for t in plain)
     if _coefficient_autograd_enabled.get():
         # the custom ops carry coefficient-level autograd (polytensors_amd._ops); the wrappers
         # stay outside autograd, so only wrapper gradients are refused
         if any(p.requires_grad for p in polys):
             return ("coefficient_autograd differentiates the coefficient tensors: build the PolyTensor "
                     "wrappers with requires_grad=False")
-        if any(c.is_complex() for c in coeffs):
+        if complex_dirs:
             return "coefficient_autograd with complex directions is not implemented"
     elif torch.is_grad_enabled() and not below_autograd:
         grads = any(t.requires_grad for t in tensors) or any(
@@ -66,12 +69,11 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
         if grads and not allow_plain_grad:
             return ("this operation has no wrapper-level gradient; use torch.no_grad(), or build a "
                     "coefficient graph inside PolyTensor.coefficient_autograd()")
-    if any(t.is_complex() for t in tensors if not isinstance(t, PolyTensor)) or any(
-            p.coeffs[0].is_complex() for p in polys):
+    if any(t.is_complex() for t in plain) or any(p.coeffs[0].is_complex() for p in polys):
         return "a complex constant term (complex base) is not implemented; complex directions need a real base"
-    if not complex_ok and any(c.is_complex() for c in coeffs):
+    if not complex_ok and complex_dirs:
         return "complex directions are not implemented for this operation"
-    if any(c.device.type != "cuda" for c in coeffs):
+    if not (all(p.coeffs[0].is_cuda for p in polys) and all(t.is_cuda for t in plain)):
         return "polytensors_amd runs on HIP (cuda) devices only"
     _lib.load()   # loud failure if the kernels are not built
     return None

@@ -64,8 +64,25 @@ def _register():
 NATIVE = _register()   # True: the C++ extension registered the operators
 
 
+_below_autograd = torch._C._AutoDispatchBelowAutograd
+
+
 def _op(name):
-    return getattr(getattr(torch.ops, NAMESPACE), name)
+    """The operator ``polytensors_amd::name``. With grad mode off no graph can be recorded, so the
+    call goes straight to the HIP implementation, past the Python autograd kernel (which would
+    only redispatch below itself)."""
+    overload = getattr(getattr(torch.ops, NAMESPACE), name).default
+    grad_enabled = torch.is_grad_enabled
+
+    def call(*args, **kwargs):
+        if grad_enabled():
+            return overload(*args, **kwargs)
+        with _below_autograd():
+            return overload(*args, **kwargs)
+
+    call.__name__ = call.__qualname__ = name
+    call.overload = overload
+    return call
 
 
 def _acc_dtype(dtype):

@@ -317,10 +317,14 @@ class PolyTensor(torch.Tensor):
     @classmethod
     def __torch_function__(cls, func, types, args=(), kwargs=None):
         kwargs = {} if kwargs is None else kwargs
-        result = maybe_decompose(func, args, kwargs)
-        if result is not NotImplemented:
-            return result
+        # The routed paths run with this hook disabled too: their reads of the operands' shape,
+        # dtype and flags then go straight to the tensor instead of back through this method, and
+        # the torch calls they make on PolyTensors (none of them routed) reach __torch_dispatch__
+        # as they would from the default branch.
         with torch._C.DisableTorchFunctionSubclass():
+            result = maybe_decompose(func, args, kwargs)
+            if result is not NotImplemented:
+                return result
             return func(*args, **kwargs)
 
     @classmethod

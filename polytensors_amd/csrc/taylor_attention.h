@@ -1,9 +1,26 @@
 // Launch interface of the Taylor attention kernels (definitions in taylor_attention.inl).
 #pragma once
 
+#include <algorithm>
+
 #include "pt_common.h"
 
 namespace pt {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnQPerWave = 16;
+constexpr int kAttnBM = kAttnWaves * kAttnQPerWave;   // query rows per workgroup
+constexpr int kAttnBN = 16;                           // keys per block of the fp32/fp64 kernels
+
+// Output head-dim slices of the staged kernel (a grid dimension; each slice's workgroup
+// recomputes the scores and accumulates D / SL output dims) where K+1 sets of output
+// accumulators over the whole head dim would spill the register file: float64 at head dim 128
+// from degree 3 and 64 from degree 6, float32 at head dim 128 from degree 6 (checked with the
+// compiler's resource remarks). elem = sizeof(T).
+__host__ __device__ constexpr int attn_slices(int elem, int K, int D) {
+  return elem == 8 ? (D == 128 ? (K >= 6 ? 4 : K >= 3 ? 2 : 1) : D == 64 && K >= 6 ? 2 : 1)
+                   : (D == 128 && K >= 6 ? 2 : 1);
+}
 
 struct AttnArgs {
   int degree;
@@ -21,10 +38,49 @@ struct AttnArgs {
   const int32_t* mask_ranges;   // null, or the block ranges of mask (launch_attention_mask_ranges)
   double scale;
   hipStream_t stream;
+  void* workspace = nullptr;   // partial sums of a key-split launch (attention_split), or null
+  size_t workspace_bytes = 0;
 };
 
 template <typename T>
 int launch_attention(const AttnArgs& a);
+
+// Key split of the staged float32/float64 kernel for launches with few workgroups: `chunks`
+// workgroups per work item, each over `chunk_keys` consecutive keys, whose partial sums
+// (bytes of workspace) a second kernel merges. chunks = 1: no split. The pipelined float32
+// kernel (full-order operands, whole 16-key blocks) and the 16-bit kernels never split.
+struct AttnSplit {
+  int chunks = 1, chunk_keys = 0;
+  size_t bytes = 0;
+};
+
+// dtype: PT_FLOAT32 / PT_FLOAT64 (others never split). A launch of fewer than 128 workgroups
+// takes up to 256 / workgroups key shares of at least one 16-key block each.
+inline AttnSplit attention_split(int dtype, int degree, int q_orders, int k_orders, int v_orders, int64_t bh,
+                                 int64_t lq, int64_t lk, int64_t d) {
+  AttnSplit sp;
+  if (dtype != PT_FLOAT32 && dtype != PT_FLOAT64) return sp;
+  const bool full = q_orders == degree + 1 && k_orders == degree + 1 && v_orders == degree + 1;
+  if (dtype == PT_FLOAT32 && full && lk >= kAttnBN && lk % kAttnBN == 0) return sp;   // the pipelined kernel
+  const int elem = dtype == PT_FLOAT64 ? 8 : 4;
+  const int64_t items = (lq + kAttnBM - 1) / kAttnBM * bh * attn_slices(elem, degree, static_cast<int>(d));
+  const int64_t nkb = (lk + kAttnBN - 1) / kAttnBN;
+  if (items >= 128 || nkb < 2 || items == 0) return sp;
+  int64_t chunks = std::min<int64_t>((256 + items - 1) / items, nkb);
+  const int64_t per = (nkb + chunks - 1) / chunks;   // key blocks per share
+  chunks = (nkb + per - 1) / per;
+  if (chunks < 2) return sp;
+  sp.chunks = static_cast<int>(chunks);
+  sp.chunk_keys = static_cast<int>(per * kAttnBN);
+  const int64_t rows = bh * lq;
+  sp.bytes = static_cast<size_t>(chunks) * static_cast<size_t>(rows) * static_cast<size_t>(1 + (degree + 1) * (1 + d)) *
+             static_cast<size_t>(elem);
+  return sp;
+}
+
+inline AttnSplit attention_split(const AttnArgs& a, int dtype) {
+  return attention_split(dtype, a.degree, a.q_orders, a.k_orders, a.v_orders, a.bh, a.lq, a.lk, a.d);
+}
 
 // bfloat16 / float16 operands on the 16x16x32 MFMAs (taylor_attention_half.inl); T = bf16 or _Float16.
 template <typename T>

@@ -62,10 +62,6 @@ struct Mfma16<double> {
   __host__ __device__ __forceinline__ static int row_reg(int i) { return i / 4; }
 };
 
-constexpr int kAttnWaves = 4;
-constexpr int kAttnQPerWave = 16;
-constexpr int kAttnBM = kAttnWaves * kAttnQPerWave;   // query rows per workgroup
-constexpr int kAttnBN = 16;                           // keys per block
 
 template <typename T>
 struct AttnRescale {
@@ -74,12 +70,7 @@ struct AttnRescale {
 
 template <typename T, int K, int D>
 struct AttnShape {
-  // Output head-dim slices (a grid dimension; each slice's workgroup recomputes the scores and
-  // accumulates D / SL output dims) where K+1 sets of output accumulators over the whole head
-  // dim would spill the register file: float64 at head dim 128 from degree 3 and 64 from degree
-  // 6, float32 at head dim 128 from degree 6 (checked with the compiler's resource remarks).
-  static constexpr int SL = sizeof(T) == 8 ? (D == 128 ? (K >= 6 ? 4 : K >= 3 ? 2 : 1) : D == 64 && K >= 6 ? 2 : 1)
-                                           : (D == 128 && K >= 6 ? 2 : 1);
+  static constexpr int SL = attn_slices(static_cast<int>(sizeof(T)), K, D);
   static constexpr int DS = D / SL;    // output head dims per slice
   static constexpr int DBS = DS / 16;  // 16-wide output blocks per slice
   // Row stride of the staged K/V tiles: D + 4 values. For floats that is 4 mod 64
@@ -113,10 +104,11 @@ struct AttnShape {
 // time (1.7% faster on a sliding window; grouping causal blocks this way was
 // 8.5% slower, the XCDs ending on heavy blocks).
 constexpr int kXcds = 8;
-__device__ __forceinline__ void attn_work_item(int L, int causal, int64_t& head, int& q_block) {
+// Work item t of `items` (query blocks x heads).
+__device__ __forceinline__ void attn_work_item_at(int L, int causal, int64_t t, int64_t items, int64_t& head,
+                                                  int& q_block) {
   const int nqb = (L + kAttnBM - 1) / kAttnBM;
-  const int64_t bh = gridDim.x / nqb;
-  const int64_t t = blockIdx.x;
+  const int64_t bh = items / nqb;
   if (!causal && bh % kXcds == 0) {
     const int64_t j = t / kXcds;
     head = t % kXcds + kXcds * (j / nqb);
@@ -125,6 +117,9 @@ __device__ __forceinline__ void attn_work_item(int L, int causal, int64_t& head,
     head = t % bh;
     q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
   }
+}
+__device__ __forceinline__ void attn_work_item(int L, int causal, int64_t& head, int& q_block) {
+  attn_work_item_at(L, causal, blockIdx.x, gridDim.x, head, q_block);
 }
 
 // Block ranges of a boolean (L, S) mask, the reference's _mask_ranges
@@ -379,7 +374,8 @@ template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
     MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask,
-    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale, int chunks, int chunk_keys,
+    typename AccOf<T>::type* __restrict__ part) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -405,14 +401,19 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
   const int h = lane / 16;        // lane group
   int64_t head;
   int q_block, slice = 0;
+  // key chunks fastest (chunks > 1: each workgroup takes one contiguous share of the key range
+  // and writes unnormalised partial sums, attn_split_combine_kernel merges them), then slices,
+  // then the work items
+  const int chunk = static_cast<int>(blockIdx.x % chunks);
+  const int64_t wi = blockIdx.x / chunks, items = gridDim.x / chunks;
+  const int nqb = (L + kAttnBM - 1) / kAttnBM;
+  const int64_t bh = items / (static_cast<int64_t>(nqb) * SL);
   if constexpr (SL == 1) {
-    attn_work_item(L, causal, head, q_block);
+    attn_work_item_at(L, causal, wi, items, head, q_block);
   } else {
     // slices fastest, then heads, heaviest query blocks first
-    const int nqb = (L + kAttnBM - 1) / kAttnBM;
-    const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SL);
-    const int64_t t = blockIdx.x / SL;
-    slice = static_cast<int>(blockIdx.x % SL);
+    const int64_t t = wi / SL;
+    slice = static_cast<int>(wi % SL);
     head = t % bh;
     q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
   }
@@ -444,6 +445,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 
   int lo, hi;
   attn_key_range(S, q_block, causal, ranges, lo, hi);
+  if (chunks > 1) {   // this workgroup's share (chunk_keys is a multiple of the key block)
+    lo += chunk * chunk_keys;
+    hi = min(hi, lo + chunk_keys);
+  }
 
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
     uint8_t mbyte[4];
@@ -575,7 +580,105 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     }
   }
 
+  if (chunks > 1) {
+    // partial results of this key share: the row's shift, its row-sum series and the
+    // unnormalised output series N_k, all relative to exp(-m_used)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+      lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+    }
+    if (!q_ok) return;
+    const int64_t rows = bh * L, row = head * L + my_q;
+    A* pm = part;                                                   // [chunks][rows]
+    A* pl = part + static_cast<int64_t>(chunks) * rows;             // [chunks][K+1][rows]
+    A* pn = pl + static_cast<int64_t>(chunks) * (K + 1) * rows;    // [chunks][K+1][rows][D]
+    if (h == 0 && slice == 0) {
+      pm[chunk * rows + row] = m_used;
+#pragma unroll
+      for (int o = 0; o <= K; ++o) pl[(static_cast<int64_t>(chunk) * (K + 1) + o) * rows + row] = lsum[o];
+    }
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int db = 0; db < DBS; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          pn[((static_cast<int64_t>(chunk) * (K + 1) + o) * rows + row) * D + d0 + db * 16 + MF::acc_row(h, r)] =
+              static_cast<A>(acc_o[o][db][r]);
+    return;
+  }
   attention_epilogue<T, K, D, acc_t, 1, DBS>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h, d0, slice == 0);
+}
+
+// Merges the key shares of a split launch: per row, the shift m = max_c m_c, the weights
+// exp(m_c - m), then the row-sum and output series as their weighted sums, the series quotient
+// O_k = (N_k - sum_{j=1..k} l_j O_{k-j}) / l_0 and the lse series, as the single-launch epilogue.
+// One thread per (row, head dim).
+template <typename T, int K>
+__global__ __launch_bounds__(256) void attn_split_combine_kernel(const typename AccOf<T>::type* __restrict__ part,
+                                                                 int chunks, int64_t rows, int D, MPtrs<T> O,
+                                                                 MPtrs<typename AccOf<T>::type> LSE) {
+  using A = typename AccOf<T>::type;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows * D) return;
+  const int64_t row = idx / D;
+  const int d = static_cast<int>(idx % D);
+  const A* pm = part;
+  const A* pl = part + static_cast<int64_t>(chunks) * rows;
+  const A* pn = pl + static_cast<int64_t>(chunks) * (K + 1) * rows;
+  // (the chunk loops unrolled so that their independent loads are in flight together: the
+  // kernel is a few load round trips long)
+  A m = -__builtin_huge_val();
+#pragma unroll 8
+  for (int c = 0; c < chunks; ++c) m = fmax(m, pm[c * rows + row]);
+  A l[K + 1], n[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) l[o] = n[o] = A(0);
+  if (m != -__builtin_huge_val()) {
+#pragma unroll 4
+    for (int c = 0; c < chunks; ++c) {
+      const A mc = pm[c * rows + row];
+      const A w = mc == -__builtin_huge_val() ? A(0) : exp_fast(mc - m);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        l[o] += w * pl[(static_cast<int64_t>(c) * (K + 1) + o) * rows + row];
+        n[o] += w * pn[((static_cast<int64_t>(c) * (K + 1) + o) * rows + row) * D + d];
+      }
+    }
+  }
+  const bool empty = !(l[0] > A(0));
+  const A inv_l0 = empty ? A(0) : A(1) / l[0];
+  A out[K + 1];
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+    A t = n[k];
+#pragma unroll
+    for (int j = 1; j <= k; ++j) t -= l[j] * out[k - j];
+    out[k] = t * inv_l0;
+    O.p[k][row * D + d] = static_cast<T>(out[k]);
+  }
+  if (d == 0 && LSE.p[0] != nullptr) {
+    if (empty) {
+      LSE.p[0][row] = __builtin_huge_val();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][row] = A(0);
+    } else {
+      A lse[K + 1], nrm[K + 1];
+      lse[0] = m + log_acc(l[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = l[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A t = nrm[k];
+#pragma unroll
+        for (int j = 1; j < k; ++j) t -= (A(j) / A(k)) * lse[j] * nrm[k - j];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][row] = lse[k];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1107,11 +1210,21 @@ static int launch_attention_kd(const AttnArgs& a) {
         return PT_OK;
       }
     }
-    const dim3 sgrid(grid.x * AttnShape<T, K, D>::SL);
+    const AttnSplit sp = attention_split(a, sizeof(T) == 8 ? PT_FLOAT64 : PT_FLOAT32);
+    const bool split = sp.chunks > 1 && a.workspace != nullptr && a.workspace_bytes >= sp.bytes;
+    const int chunks = split ? sp.chunks : 1;
+    const dim3 sgrid(grid.x * AttnShape<T, K, D>::SL * chunks);
     taylor_attention_fwd_kernel<T, K, D><<<sgrid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
         q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
-        static_cast<int>(a.lk), a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale));
+        static_cast<int>(a.lk), a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale), chunks,
+        split ? sp.chunk_keys : 0, split ? static_cast<A*>(a.workspace) : nullptr);
     PT_LAUNCH_CHECK();
+    if (split) {
+      const int64_t rows = a.bh * a.lq, threads = rows * D;
+      attn_split_combine_kernel<T, K><<<dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, a.stream>>>(
+          static_cast<const A*>(a.workspace), chunks, rows, static_cast<int>(D), o, lse);
+      PT_LAUNCH_CHECK();
+    }
     return PT_OK;
   }
 }

@@ -8,7 +8,25 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
                             void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
                             int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
                             void* stream) {
+  return pt_taylor_attention_fwd_ws(dtype, degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
+                                    causal, mask, mask_ranges, scale, nullptr, 0, stream);
+}
+
+size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
+                                              int64_t bh, int64_t lq, int64_t lk, int64_t d) {
+  if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0 || lk < 0 || d <= 0) return 0;
+  const pt::AttnSplit sp = pt::attention_split(dtype, degree, q_orders, k_orders, v_orders, bh, lq, lk, d);
+  return sp.chunks > 1 ? sp.bytes : 0;
+}
+
+int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int q_orders,
+                               const void* const* k, int k_orders, const void* const* v, int v_orders,
+                               void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
+                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
+                               void* workspace, size_t workspace_bytes, void* stream) {
   pt_host::clear_error();
+  PT_REQUIRE(workspace_bytes == 0 || pt_host::aligned16(workspace), PT_INVALID_ARGUMENT,
+             "Taylor attention: workspace must be 16-byte aligned");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention: degree must be in 0..8");
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
@@ -38,7 +56,8 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
   }
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
-                 causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream)};
+                 causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream),
+                 workspace_bytes > 0 ? workspace : nullptr, workspace_bytes};
   switch (dtype) {
     case PT_FLOAT32: return pt::launch_attention<float>(a);
     case PT_FLOAT64: return pt::launch_attention<double>(a);

@@ -340,11 +340,19 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
   const auto ranges = mask_ranges(mask, lq, lk);
   auto qs = cptrs(q), ks = cptrs(k), vs = cptrs(v);
   auto os = slices(out), ls = slices(lse);
-  const int status = pt_taylor_attention_fwd(
-      dtype_code(dtype), static_cast<int>(degree), qs.data(), static_cast<int>(q.size()), ks.data(),
+  const int code = dtype_code(dtype);
+  // launches of few workgroups split each key range over several (partial sums in a workspace)
+  const size_t wbytes = pt_taylor_attention_fwd_workspace_size(
+      code, static_cast<int>(degree), static_cast<int>(q.size()), static_cast<int>(k.size()),
+      static_cast<int>(v.size()), bh, lq, lk, d);
+  Tensor workspace;
+  if (wbytes > 0) workspace = at::empty({static_cast<int64_t>(wbytes)}, q[0].options().dtype(at::kByte));
+  const int status = pt_taylor_attention_fwd_ws(
+      code, static_cast<int>(degree), qs.data(), static_cast<int>(q.size()), ks.data(),
       static_cast<int>(k.size()), vs.data(), static_cast<int>(v.size()), os.data(), ls.data(), bh, lq, lk, d,
       causal ? 1 : 0, mask ? static_cast<const uint8_t*>(mask->data_ptr()) : nullptr,
-      ranges ? ranges->data_ptr<int32_t>() : nullptr, scale, stream_of(q[0]));
+      ranges ? ranges->data_ptr<int32_t>() : nullptr, scale, wbytes > 0 ? workspace.data_ptr() : nullptr, wbytes,
+      stream_of(q[0]));
   check_status(status, "taylor_attention_fwd");
   return {out, lse};
 }

@@ -80,3 +80,18 @@ def test_operator_schemas_match_the_cpp_registration():
     for name, schema in _ops.SCHEMAS.items():
         got = str(getattr(torch.ops.polytensors_amd, name).default._schema)
         assert got == f"polytensors_amd::{name}{schema}", name
+
+
+def test_attention_key_split_plan():
+    # few workgroups split (config 1: one head of 128 queries); config 3 does not; the pipelined
+    # float32 kernel (full orders, whole 16-key blocks) and the 16-bit kernels never split
+    lib = _lib.load()
+    size = lib.pt_taylor_attention_fwd_workspace_size
+    assert size(1, 3, 4, 4, 4, 1, 128, 128, 64) > 0                    # float64, config 1
+    assert size(1, 4, 5, 5, 5, 64, 2048, 2048, 128) == 0               # float64, many workgroups
+    assert size(0, 3, 4, 4, 4, 1, 128, 128, 64) == 0                   # float32, pipelined kernel
+    assert size(0, 3, 4, 4, 4, 1, 128, 70, 64) > 0                     # float32, generic kernel
+    assert size(2, 3, 4, 4, 4, 1, 128, 128, 64) == 0                   # bfloat16
+    # bytes: chunks x rows x (1 + (K+1)(1+d)) values
+    b = size(1, 3, 4, 4, 4, 1, 128, 128, 64)
+    assert b % (128 * (1 + 4 * 65) * 8) == 0

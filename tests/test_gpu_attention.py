@@ -388,3 +388,46 @@ def test_float64_head_dim_128_gradients_at_degree_4():
     want = oracle.attention_backward(Q, K, V, G, is_causal=True)
     for x, w in zip(xs, want):
         _check(x.grad.coeffs, w, torch.float64)
+
+
+@pytest.mark.parametrize("dtype,L,S,causal,masked", [(torch.float64, 128, 128, True, False),
+                                                    (torch.float64, 96, 150, False, True),
+                                                    (torch.float32, 128, 70, True, False),
+                                                    (torch.float64, 1, 300, False, False)])
+def test_key_split_launch_matches_the_unsplit_one(dtype, L, S, causal, masked):
+    # launches of few workgroups divide each key range over several workgroups and merge their
+    # partial sums (pt_taylor_attention_fwd_ws, which the operator calls); the plain entry point runs
+    # the same launch unsplit
+    from polytensors_amd import _lib
+
+    degree, d, bh = 3, 64, 1
+    Q = _series((bh, L, d), degree, 170, dtype)
+    K, V = (_series((bh, S, d), degree, 171 + i, dtype) for i in range(2))
+    mask = (torch.rand(L, S, generator=torch.Generator().manual_seed(9)) < 0.5) if masked else None
+    lib = _lib.load()
+    code = _lib.DTYPE_CODES[dtype]
+    assert lib.pt_taylor_attention_fwd_workspace_size(code, degree, degree + 1, degree + 1, degree + 1, bh, L, S, d) > 0
+    q, k, v = ([c.cuda() for c in X] for X in (Q, K, V))
+    m = None if mask is None else mask.cuda()
+    out, lse = _ops.taylor_attention_fwd(q, k, v, m, causal, 0.125, degree)
+    ref_out = torch.empty_like(out)
+    ref_lse = torch.empty_like(lse)
+    ranges = None if m is None else _ops._mask_ranges(m, L, S)
+    _lib.check(lib.pt_taylor_attention_fwd(code, degree, _lib.ptr_array(q), len(q), _lib.ptr_array(k), len(k),
+                                           _lib.ptr_array(v), len(v), _lib.ptr_array(list(ref_out.unbind(0))),
+                                           _lib.ptr_array(list(ref_lse.unbind(0))), bh, L, S, d, int(causal),
+                                           None if m is None else m.data_ptr(),
+                                           None if ranges is None else ranges.data_ptr(), 0.125,
+                                           _lib.stream_of(out.device)), "unsplit")
+    torch.cuda.synchronize()
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    for k_ in range(degree + 1):
+        assert rel_err(out[k_].cpu(), ref_out[k_].cpu()) <= tol
+        finite = torch.isfinite(ref_lse[k_])
+        assert torch.equal(torch.isfinite(lse[k_]), finite)
+        assert rel_err(lse[k_][finite].cpu(), ref_lse[k_][finite].cpu()) <= tol
+    want = oracle.attention([c.unsqueeze(0).double() for c in Q], [c.unsqueeze(0).double() for c in K],
+                            [c.unsqueeze(0).double() for c in V], attn_mask=mask, is_causal=causal, scale=0.125)
+    empty = torch.zeros(L, dtype=torch.bool) if mask is None else ~mask.any(-1)
+    want = [torch.where(empty[:, None], torch.zeros_like(w[0]), w[0]) for w in want]
+    _check([o for o in out], want, dtype)
