@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 10
+#define PT_ABI_VERSION 11
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -259,14 +259,21 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
  * floating-point sums). pt_taylor_attention_fwd_workspace_size gives the bytes this needs
  * (0: the launch does not split, and the workspace may be NULL); a smaller workspace
  * runs the launch unsplit. The workspace must be 16-byte aligned.
+ * mask_add: NULL, or an additive float mask, the reference's float attn_mask
+ *   (/root/reference/src/polytensors/_decompositions.py:38-40: added to the scores, so to
+ *   their constant order, after scaling): [lq, lk] values of the accumulator type (float for
+ *   PT_FLOAT32, double for PT_FLOAT64; PT_UNSUPPORTED for the 16-bit types). mask must then
+ *   be given and mark exactly its finite entries (an entry of -inf excludes its key; a row
+ *   with none admissible gets the empty-row output above).
  */
 size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
                                               int64_t bh, int64_t lq, int64_t lk, int64_t d);
 int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int q_orders,
                                const void* const* k, int k_orders, const void* const* v, int v_orders,
                                void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
-                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
-                               void* workspace, size_t workspace_bytes, void* stream);
+                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges,
+                               const void* mask_add, double scale, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /*
  * Block ranges of a boolean [lq, lk] attention mask (nonzero = admissible),
@@ -299,7 +306,9 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk,
  *   admissible pair instead of eight (S and dP are then not recomputed for dK
  *   and dV), at the cost of that workspace. PT_FLOAT32 only (PT_UNSUPPORTED
  *   for PT_FLOAT64).
- * mask, mask_ranges: as in pt_taylor_attention_fwd.
+ * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add: as in
+ *   pt_taylor_attention_fwd_ws (the forward's additive mask; with it the scores
+ *   are recomputed and materialize does not apply).
  * Pointers must be 16-byte aligned. Deterministic (no atomics).
  * Replaces the degree-1 fused backward
  *   /root/reference/src/polytensors/_fused_attention.py:144-163 (backward),
@@ -314,7 +323,7 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
                             void* const* dk, void* const* dv, void* workspace,
                             int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
                             int causal, const uint8_t* mask,
-                            const int32_t* mask_ranges, double scale,
+                            const int32_t* mask_ranges, const void* mask_add, double scale,
                             void* stream);
 
 /* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row

@@ -139,8 +139,9 @@ def attention_backward(Q, K, V, G, attn_mask=None, is_causal=False, scale=None):
     (_plain.py:262-273), dV = P^T G, dP = G V^T, dS = P (dP - rowsum(P dP)),
     dQ = scale dS K, dK = scale dS^T Q -- the reference's degree-1 backward
     (/root/reference/src/polytensors/_attention_kernels.py:85-201) at degree K.
-    Boolean masks only. A query row with no admissible key has P = 0, as in the
-    fused kernels (lse = +inf, _attention_kernels.py:80-81).
+    A float mask is added to the order-0 scores (as in ``attention``); its -inf
+    entries exclude their keys. A query row with no admissible key has P = 0, as
+    in the fused kernels (lse = +inf, _attention_kernels.py:80-81).
     """
     degree = max(len(Q), len(K), len(V), len(G)) - 1
     Q, K, V, G = (lift(x, degree) for x in (Q, K, V, G))
@@ -150,8 +151,11 @@ def attention_backward(Q, K, V, G, attn_mask=None, is_causal=False, scale=None):
     keep = torch.ones(L, S, dtype=torch.bool)
     if is_causal:
         keep = keep.tril(diagonal=0)
-    if attn_mask is not None:
+    if attn_mask is not None and attn_mask.dtype == torch.bool:
         keep = keep & attn_mask
+    elif attn_mask is not None:
+        keep = keep & ~torch.isneginf(attn_mask)
+        scores = _add_to_order0(scores, torch.where(keep, attn_mask, torch.zeros((), dtype=attn_mask.dtype)))
     scores = [torch.where(keep, c, torch.full((), float("-inf") if k == 0 else 0.0, dtype=c.dtype))
               for k, c in enumerate(scores)]
     empty = ~keep.any(-1, keepdim=True)

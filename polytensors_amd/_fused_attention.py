@@ -9,9 +9,12 @@ constant-order scores only, the exponential series of the higher orders is
 formed from ``k E_k = sum_j j S_j E_{k-j}`` (/root/reference/src/polytensors/_plain.py:153-159),
 and the output is the series quotient of the accumulated numerator and row sum.
 Eligibility and conventions follow the degree-1 kernel of the reference
-(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or a
-boolean (L, S) mask (not both), no dropout or GQA, default scale 1/sqrt(d), and
-a query row with no admissible key gets output zero.
+(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or an
+(L, S) mask (not both), no dropout or GQA, default scale 1/sqrt(d), and a query
+row with no admissible key gets output zero. A floating mask is added to the
+scores, so to their constant order, as the reference's general rule does
+(/root/reference/src/polytensors/_decompositions.py:38-40); its -inf entries
+exclude their keys (16-bit operands with such a mask run the float32 kernel).
 
 Under autograd (a PolyTensor operand requiring grad) the call records
 ``_SeriesAttention``, whose backward is the degree-K gradient series kernel
@@ -56,10 +59,12 @@ def default_scale(head_dim):
 
 
 def _square_mask(attn_mask, L, S):
-    """A boolean mask as an (L, S) tensor, None if absent, NotImplemented if batch-dependent or additive."""
+    """A boolean or floating (additive) mask as an (L, S) tensor, None if absent, NotImplemented
+    if batch-dependent or of another dtype."""
     if attn_mask is None:
         return None
-    if attn_mask.dtype != torch.bool or tuple(attn_mask.shape[-2:]) != (L, S):
+    if not (attn_mask.dtype == torch.bool or attn_mask.dtype.is_floating_point) or \
+            tuple(attn_mask.shape[-2:]) != (L, S):
         return NotImplemented
     if any(size != 1 for size in attn_mask.shape[:-2]):
         return NotImplemented
@@ -110,7 +115,7 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if is_causal and attn_mask is not None:
         return "is_causal and attn_mask are exclusive"
     if _square_mask(attn_mask, query.shape[-2], key.shape[-2]) is NotImplemented:
-        return "only a boolean (L, S) mask is supported"
+        return "only a boolean or floating (L, S) mask is supported"
     return None
 
 

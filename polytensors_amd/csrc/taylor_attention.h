@@ -40,6 +40,9 @@ struct AttnArgs {
   hipStream_t stream;
   void* workspace = nullptr;   // partial sums of a key-split launch (attention_split), or null
   size_t workspace_bytes = 0;
+  // null, or an (L, S) additive mask in the accumulator type (float32/float64 operands only),
+  // with mask its finite entries
+  const void* mask_add = nullptr;
 };
 
 template <typename T>
@@ -111,6 +114,9 @@ struct AttnBwdArgs {
   double scale;
   bool materialize;   // store P and dS tiles in the workspace (5 products per pair instead of 8)
   hipStream_t stream;
+  // null, or an (L, S) additive mask in the accumulator type with mask its finite entries (the
+  // scores are then recomputed: materialize does not apply)
+  const void* mask_add = nullptr;
 };
 
 template <typename T>

@@ -255,6 +255,14 @@ __device__ __forceinline__ uint8_t attn_mask_byte(const uint8_t* mask, const voi
   return base[at];
 }
 
+// Value (row, col) of an (L, S) additive mask (the accumulator type), indices clamped into it
+// as attn_mask_byte's. Its -inf entries are also 0 in the boolean mask the launch is given, so a
+// read value is used for admissible keys only.
+template <typename A>
+__device__ __forceinline__ A attn_mask_add(const A* madd, int row, int col, int L, int S) {
+  return madd[static_cast<int64_t>(min(row, L - 1)) * S + min(col, S - 1)];
+}
+
 // E is the head-dim interleave of the output accumulators: accumulator
 // g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
 // (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).
@@ -370,12 +378,14 @@ __device__ __forceinline__ const T* order_ptr(const CPtrs<T>& s, int o) {
   return p;
 }
 
-template <typename T, int K, int D>
+// ADD: an additive (L, S) mask madd is given with the boolean mask of its finite entries; it
+// adds to the constant-order scores after scaling.
+template <typename T, int K, int D, bool ADD>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
     MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask,
-    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale, int chunks, int chunk_keys,
-    typename AccOf<T>::type* __restrict__ part) {
+    const typename AccOf<T>::type* __restrict__ madd, const int32_t* __restrict__ ranges, int causal,
+    typename AccOf<T>::type scale, int chunks, int chunk_keys, typename AccOf<T>::type* __restrict__ part) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -452,8 +462,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
     uint8_t mbyte[4];
+    A add[ADD ? 4 : 1];
 #pragma unroll
     for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + MF::acc_row(h, r), L, S);
+    if constexpr (ADD) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) add[r] = attn_mask_add(madd, my_q, kb0 + MF::acc_row(h, r), L, S);
+    }
     __syncthreads();
     // ---- stage rows kb0 .. kb0+15 of every order (zero past S / the orders given): K over every
     // head dim, V over the slice's (V after the scores when the two share the buffer) ----
@@ -515,7 +530,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
       if (causal) ok = ok && key <= my_q;
       if (mask != nullptr) ok = ok && mbyte[r] != 0;
       valid[r] = ok;
-      s0[r] = ok ? static_cast<A>(sc[0][r]) * scale : kNegInf;
+      A s = static_cast<A>(sc[0][r]) * scale;
+      if constexpr (ADD) s += add[r];
+      s0[r] = ok ? s : kNegInf;
     }
     A bmax = fmax(fmax(s0[0], s0[1]), fmax(s0[2], s0[3]));
     bmax = fmax(bmax, __shfl_xor(bmax, 16, kWave));
@@ -1195,8 +1212,9 @@ static int launch_attention_kd(const AttnArgs& a) {
     }
     const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
     if constexpr (sizeof(T) == 4 && AttnPipeShape<K, D>::fits) {
-      // the pipelined kernel reads each lane's four mask bytes as one 32-bit word
-      bool pipe = a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= kAttnBN &&
+      // the pipelined kernel reads each lane's four mask bytes as one 32-bit word (and takes no
+      // additive mask)
+      bool pipe = a.mask_add == nullptr && a.q_orders == K + 1 && a.k_orders == K + 1 && a.v_orders == K + 1 && a.lk >= kAttnBN &&
                   a.lk % kAttnBN == 0 && reinterpret_cast<uintptr_t>(a.mask) % 4 == 0 &&
                   a.lk * D * sizeof(float) < (size_t{1} << 31) &&   // 32-bit buffer offsets: per-head keys,
                   (a.mask == nullptr || a.lq * a.lk < (int64_t{1} << 31));   // ... and the whole mask
@@ -1214,10 +1232,15 @@ static int launch_attention_kd(const AttnArgs& a) {
     const bool split = sp.chunks > 1 && a.workspace != nullptr && a.workspace_bytes >= sp.bytes;
     const int chunks = split ? sp.chunks : 1;
     const dim3 sgrid(grid.x * AttnShape<T, K, D>::SL * chunks);
-    taylor_attention_fwd_kernel<T, K, D><<<sgrid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-        q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq),
-        static_cast<int>(a.lk), a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale), chunks,
-        split ? sp.chunk_keys : 0, split ? static_cast<A*>(a.workspace) : nullptr);
+    const A* madd = static_cast<const A*>(a.mask_add);
+#define PT_ATTN_STAGED(ADD)                                                                                  \
+  taylor_attention_fwd_kernel<T, K, D, ADD><<<sgrid, dim3(kAttnWaves * kWave), 0, a.stream>>>(               \
+      q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),   \
+      a.mask, madd, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale), chunks, split ? sp.chunk_keys : 0, \
+      split ? static_cast<A*>(a.workspace) : nullptr)
+    if (madd != nullptr) PT_ATTN_STAGED(true);
+    else PT_ATTN_STAGED(false);
+#undef PT_ATTN_STAGED
     PT_LAUNCH_CHECK();
     if (split) {
       const int64_t rows = a.bh * a.lq, threads = rows * D;

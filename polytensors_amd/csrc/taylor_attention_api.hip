@@ -9,7 +9,7 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
                             int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
                             void* stream) {
   return pt_taylor_attention_fwd_ws(dtype, degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
-                                    causal, mask, mask_ranges, scale, nullptr, 0, stream);
+                                    causal, mask, mask_ranges, nullptr, scale, nullptr, 0, stream);
 }
 
 size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
@@ -22,8 +22,9 @@ size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_order
 int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int q_orders,
                                const void* const* k, int k_orders, const void* const* v, int v_orders,
                                void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
-                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
-                               void* workspace, size_t workspace_bytes, void* stream) {
+                               int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges,
+                               const void* mask_add, double scale, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(workspace_bytes == 0 || pt_host::aligned16(workspace), PT_INVALID_ARGUMENT,
              "Taylor attention: workspace must be 16-byte aligned");
@@ -31,8 +32,12 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
              "Taylor attention: degree must be in 0..8");
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention: mask_ranges without a mask");
+  PT_REQUIRE(mask_add == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
+             "Taylor attention: an additive mask needs the boolean mask of its finite entries");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,
              PT_UNSUPPORTED, "Taylor attention: float32, float64, bfloat16 or float16");
+  PT_REQUIRE(mask_add == nullptr || dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
+             "Taylor attention: additive masks take float32 or float64 operands");
   PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention: q, k, v and out pointer arrays are required");
   for (int o : {q_orders, k_orders, v_orders})
@@ -57,7 +62,7 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
                  causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream),
-                 workspace_bytes > 0 ? workspace : nullptr, workspace_bytes};
+                 workspace_bytes > 0 ? workspace : nullptr, workspace_bytes, mask_add};
   switch (dtype) {
     case PT_FLOAT32: return pt::launch_attention<float>(a);
     case PT_FLOAT64: return pt::launch_attention<double>(a);
@@ -91,11 +96,13 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
                             const void* const* v, const void* const* out, const void* const* lse,
                             const void* const* grad, void* const* dq, void* const* dk, void* const* dv,
                             void* workspace, int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
-                            int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
-                            void* stream) {
+                            int causal, const uint8_t* mask, const int32_t* mask_ranges, const void* mask_add,
+                            double scale, void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention backward: mask_ranges without a mask");
+  PT_REQUIRE(mask_add == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
+             "Taylor attention backward: an additive mask needs the boolean mask of its finite entries");
   // The stored-tile path is float32 only: a float64 run of it (degree 8, head dim 64) took a GPU
   // memory fault whose cause is not established, so float64 always recomputes.
   PT_REQUIRE(!(materialize && dtype == PT_FLOAT64), PT_UNSUPPORTED,
@@ -139,7 +146,8 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   }
   if (bh == 0) return PT_OK;
   pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
-                    causal != 0, mask, mask_ranges, scale, materialize != 0, static_cast<hipStream_t>(stream)};
+                    causal != 0, mask, mask_ranges, scale, materialize != 0, static_cast<hipStream_t>(stream),
+                    mask_add};
   return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
 }
 

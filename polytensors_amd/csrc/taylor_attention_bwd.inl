@@ -123,11 +123,12 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(CPtrs<T> G, CPtrs<T
 }
 
 // Probability series of one score element from its raw score accumulators
-// (unscaled), the row's lse series and admissibility.
+// (unscaled), its additive mask value (0 without one), the row's lse series and
+// admissibility.
 template <typename A, int K, typename AccT>
 __device__ __forceinline__ void attn_prob_series(const AccT (&sc)[K + 1], int r, const A (&lse)[K + 1],
-                                                 bool valid, A scale, A (&p)[K + 1]) {
-  p[0] = valid ? exp_fast(static_cast<A>(sc[0][r]) * scale - lse[0]) : A(0);
+                                                 bool valid, A scale, A add, A (&p)[K + 1]) {
+  p[0] = valid ? exp_fast(static_cast<A>(sc[0][r]) * scale + add - lse[0]) : A(0);
   A x[K + 1];
 #pragma unroll
   for (int i = 1; i <= K; ++i) x[i] = static_cast<A>(sc[i][r]) * scale - lse[i];
@@ -385,14 +386,17 @@ __device__ __forceinline__ void attn_bwd_contract(Vec<T, 4> (&ring)[RING][K + 1]
 
 // STORE: also write the P and dS series of every visited 16 x 16 (query, key)
 // tile to PT / DST (attn_tile_offset layout) for taylor_attention_bwd_kv_mat_kernel.
-// MASKED: a boolean mask is given (the unmasked instantiation holds no mask
+// MASK: 0 no mask, 1 a boolean mask, 2 a boolean mask and the additive mask madd
+// whose finite entries it marks (the unmasked instantiation holds no mask
 // registers: at K = 4, D = 128 four of them cost the causal case 3%).
-template <typename T, int K, int D, int NS, bool STORE, bool MASKED>
+template <typename T, int K, int D, int NS, bool STORE, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, MPtrs<T> PT, MPtrs<T> DST, int L, int S,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
-    typename AccOf<T>::type scale) {
+    const uint8_t* __restrict__ mask, const typename AccOf<T>::type* __restrict__ madd,
+    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+  constexpr bool MASKED = MASK != 0, ADD = MASK == 2;
+  static_assert(!(ADD && STORE), "an additive mask runs the recomputing path");
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -487,9 +491,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   }
   for (int kb0 = lo; kb0 < hi; kb0 += kAttnBN) {
     uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this lane's keys, read ahead of the block's prefetches
+    A add[ADD ? 4 : 1] = {};
     if constexpr (MASKED) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + MF::acc_row(h, r), L, S);
+    }
+    if constexpr (ADD) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) add[r] = attn_mask_add(madd, my_q, kb0 + MF::acc_row(h, r), L, S);
     }
     __syncthreads();   // the previous block's MFMAs are done with the tiles
     if constexpr (kPrefetchStage) {
@@ -567,7 +576,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
       if (causal) ok = ok && key <= my_q;
       if constexpr (MASKED) ok = ok && mbyte[r] != 0;
       A p[K + 1], ds[K + 1];
-      attn_prob_series<A, K>(sc, r, lse, ok, scale, p);
+      attn_prob_series<A, K>(sc, r, lse, ok, scale, ADD ? add[r] : A(0), p);
       attn_ds_series<A, K>(p, dp, r, delta, ds);
 #pragma unroll
       for (int o = 0; o <= K; ++o) sc[o][r] = static_cast<T>(ds[o]);
@@ -594,13 +603,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   if (q_ok && DQ.p[0] != nullptr) attn_bwd_store<T, K, NS>(acc, DQ, (head * L + my_q) * D, slice * NS, h, scale);
 }
 
-// WHAT: 1 = dV, 2 = dK, 3 = both.
-template <typename T, int K, int D, int NS, int WHAT, bool MASKED>
+// WHAT: 1 = dV, 2 = dK, 3 = both. MASK as the dQ kernel's.
+template <typename T, int K, int D, int NS, int WHAT, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
-    typename AccOf<T>::type scale) {
+    const uint8_t* __restrict__ mask, const typename AccOf<T>::type* __restrict__ madd,
+    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+  constexpr bool MASKED = MASK != 0, ADD = MASK == 2;
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
   using acc_t = typename MF::acc_t;
@@ -660,9 +670,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   attn_query_range(L, kv_block, causal, ranges, lo, hi);
   for (int qb0 = lo; qb0 < hi; qb0 += kBM) {
     uint8_t mbyte[MASKED ? 4 : 1];   // mask bytes of this lane's queries, read ahead of the block's loads
+    A add[ADD ? 4 : 1] = {};
     if constexpr (MASKED) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) mbyte[r] = attn_mask_byte(mask, Q.p[0], qb0 + MF::acc_row(h, r), my_k, L, S);
+    }
+    if constexpr (ADD) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) add[r] = attn_mask_add(madd, qb0 + MF::acc_row(h, r), my_k, L, S);
     }
     __syncthreads();
     // rows qb0 .. qb0+15 of every order of one operand into a tile (zero past L)
@@ -762,7 +777,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
       A lse[K + 1], p[K + 1];
 #pragma unroll
       for (int o = 0; o <= K; ++o) lse[o] = Ls[o][qr];
-      attn_prob_series<A, K>(sc, r, lse, ok, scale, p);
+      attn_prob_series<A, K>(sc, r, lse, ok, scale, ADD ? add[r] : A(0), p);
       if constexpr (DO_K) {
         A delta[K + 1], ds[K + 1];
 #pragma unroll
@@ -960,15 +975,18 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
     const int L = static_cast<int>(a.lq), S = static_cast<int>(a.lk);
     const A scale = static_cast<A>(a.scale);
     const int causal = a.causal ? 1 : 0;
-    // the stored-tile path is built for float32 only (the C ABI refuses it for float64)
+    // the stored-tile path is built for float32 only (the C ABI refuses it for float64); with an
+    // additive mask the scores are recomputed
     constexpr bool kCanStore = sizeof(T) == 4;
     if (!kCanStore && a.materialize) {
       pt_host::set_error("Taylor attention backward: materialize is float32 only");
       return PT_UNSUPPORTED;
     }
+    const bool materialize = a.materialize && a.mask_add == nullptr;
+    const A* madd = static_cast<const A*>(a.mask_add);
     MPtrs<T> pt{}, dst{};
     CPtrs<T> pt_in{}, dst_in{};
-    if (a.materialize) {
+    if (materialize) {
       const AttnBwdLayout lay = attention_bwd_layout(sizeof(A), sizeof(T), K, a.bh, a.lq, a.lk);
       for (int i = 0; i <= K; ++i) {
         pt.p[i] = reinterpret_cast<T*>(static_cast<char*>(a.workspace) + lay.tiles_offset + i * lay.tile_bytes);
@@ -983,23 +1001,24 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
           g, o, delta, rows);
       PT_LAUNCH_CHECK();
     }
-    const bool need_q = a.dq != nullptr || a.materialize;
+    const bool need_q = a.dq != nullptr || materialize;
     if (need_q && rows > 0) {
       constexpr int SL = Plan::DB / Plan::NS_Q;
       const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
-#define PT_ATTN_BWD_Q(STORE, MASKED)                                                                   \
-  taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, STORE, MASKED><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>( \
-      q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_ranges, causal, scale)
+#define PT_ATTN_BWD_Q(STORE, MASK)                                                                     \
+  taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, STORE, MASK><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>( \
+      q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, madd, a.mask_ranges, causal, scale)
       const bool masked = a.mask != nullptr;
       if constexpr (kCanStore) {
-        if (a.materialize) {   // (without a dq output the kernel still writes the P and dS tiles)
-          if (masked) PT_ATTN_BWD_Q(true, true);
-          else PT_ATTN_BWD_Q(true, false);
+        if (materialize) {   // (without a dq output the kernel still writes the P and dS tiles)
+          if (masked) PT_ATTN_BWD_Q(true, 1);
+          else PT_ATTN_BWD_Q(true, 0);
         }
       }
-      if (!a.materialize) {
-        if (masked) PT_ATTN_BWD_Q(false, true);
-        else PT_ATTN_BWD_Q(false, false);
+      if (!materialize) {
+        if (madd != nullptr) PT_ATTN_BWD_Q(false, 2);
+        else if (masked) PT_ATTN_BWD_Q(false, 1);
+        else PT_ATTN_BWD_Q(false, 0);
       }
 #undef PT_ATTN_BWD_Q
       PT_LAUNCH_CHECK();
@@ -1011,7 +1030,19 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
     if (a.mask != nullptr) KERNEL<T, K, D, NS, WHAT, true><<<grid, block, 0, a.stream>>> ARGS; \
     else KERNEL<T, K, D, NS, WHAT, false><<<grid, block, 0, a.stream>>> ARGS;                  \
   } while (0)
-      if (a.materialize) {
+#define PT_ATTN_BWD_KV_RECOMPUTE(WHAT)                                                                       \
+  do {                                                                                                       \
+    if (madd != nullptr)                                                                                     \
+      taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 2><<<grid, block, 0, a.stream>>>(           \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+    else if (a.mask != nullptr)                                                                              \
+      taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 1><<<grid, block, 0, a.stream>>>(           \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+    else                                                                                                     \
+      taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 0><<<grid, block, 0, a.stream>>>(           \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+  } while (0)
+      if (materialize) {
        if constexpr (kCanStore) {
         constexpr int SL = Plan::DB / Plan::NS_KM;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
@@ -1033,20 +1064,21 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
         constexpr int SL = Plan::DB / Plan::NS_KV;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
         if constexpr (Plan::kv_fused) {
-          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 3, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+          PT_ATTN_BWD_KV_RECOMPUTE(3);
           PT_LAUNCH_CHECK();
         } else {
           if (a.dv != nullptr) {
-            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 1, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+            PT_ATTN_BWD_KV_RECOMPUTE(1);
             PT_LAUNCH_CHECK();
           }
           if (a.dk != nullptr) {
-            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_kernel, Plan::NS_KV, 2, (q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+            PT_ATTN_BWD_KV_RECOMPUTE(2);
             PT_LAUNCH_CHECK();
           }
         }
       }
 #undef PT_ATTN_BWD_KV
+#undef PT_ATTN_BWD_KV_RECOMPUTE
     }
     return PT_OK;
   }

@@ -12,6 +12,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <limits>
 #include <string>
 #include <vector>
 
@@ -305,14 +306,30 @@ c10::optional<Tensor> mask_ranges(const c10::optional<Tensor>& mask, int64_t lq,
   return ranges;
 }
 
-c10::optional<Tensor> attention_mask(const c10::optional<Tensor>& mask, const Tensor& q0, int64_t lq, int64_t lk,
-                                     bool causal, const char* name) {
-  if (!mask) return c10::nullopt;
-  TORCH_CHECK_VALUE(mask->scalar_type() == at::kBool && mask->dim() == 2 && mask->size(0) == lq &&
+// A boolean (L, S) mask as it is, or a floating one (added to the constant-order scores) as the
+// boolean mask of its entries above -inf and its values in the accumulator type.
+struct AttnMask {
+  c10::optional<Tensor> keep, add;
+  const uint8_t* keep_ptr() const { return keep ? static_cast<const uint8_t*>(keep->data_ptr()) : nullptr; }
+  const void* add_ptr() const { return add ? add->data_ptr() : nullptr; }
+};
+
+AttnMask attention_mask(const c10::optional<Tensor>& mask, const Tensor& q0, int64_t lq, int64_t lk, bool causal,
+                        const char* name) {
+  AttnMask m;
+  if (!mask) return m;
+  const at::ScalarType type = mask->scalar_type();
+  TORCH_CHECK_VALUE((type == at::kBool || at::isFloatingType(type)) && mask->dim() == 2 && mask->size(0) == lq &&
                         mask->size(1) == lk && mask->device() == q0.device(),
-                    name, ": mask must be a bool (L, S) tensor on the query's device");
+                    name, ": mask must be a bool or floating (L, S) tensor on the query's device");
   TORCH_CHECK_VALUE(!causal, name, ": mask and causal are exclusive");
-  return mask->contiguous();
+  if (type == at::kBool) {
+    m.keep = mask->contiguous();
+    return m;
+  }
+  m.add = mask->to(acc_type(q0.scalar_type())).contiguous();
+  m.keep = at::ne(*m.add, -std::numeric_limits<double>::infinity());
+  return m;
 }
 
 std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const TensorList& k, const TensorList& v,
@@ -334,10 +351,20 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
   TORCH_CHECK_VALUE(k[0].scalar_type() == dtype && v[0].scalar_type() == dtype, "taylor_attention: dtypes differ");
   const int64_t lk = k[0].size(1);
   c10::DeviceGuard guard(q[0].device());
+  if (mask_in && mask_in->scalar_type() != at::kBool && (dtype == at::kBFloat16 || dtype == at::kHalf)) {
+    // the additive mask runs on the float32 kernel: 16-bit operands are widened, the output rounded
+    auto widen = [](const TensorList& xs) {
+      std::vector<Tensor> out;
+      for (const Tensor& x : xs) out.push_back(x.to(at::kFloat));
+      return out;
+    };
+    auto [o32, l32] = taylor_attention_fwd(widen(q), widen(k), widen(v), mask_in, causal, scale, degree);
+    return {o32.to(dtype), l32};
+  }
   const auto mask = attention_mask(mask_in, q[0], lq, lk, causal, "taylor_attention");
   Tensor out = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor lse = at::empty({degree + 1, bh, lq}, q[0].options().dtype(acc_type(dtype)));
-  const auto ranges = mask_ranges(mask, lq, lk);
+  const auto ranges = mask_ranges(mask.keep, lq, lk);
   auto qs = cptrs(q), ks = cptrs(k), vs = cptrs(v);
   auto os = slices(out), ls = slices(lse);
   const int code = dtype_code(dtype);
@@ -350,9 +377,8 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
   const int status = pt_taylor_attention_fwd_ws(
       code, static_cast<int>(degree), qs.data(), static_cast<int>(q.size()), ks.data(),
       static_cast<int>(k.size()), vs.data(), static_cast<int>(v.size()), os.data(), ls.data(), bh, lq, lk, d,
-      causal ? 1 : 0, mask ? static_cast<const uint8_t*>(mask->data_ptr()) : nullptr,
-      ranges ? ranges->data_ptr<int32_t>() : nullptr, scale, wbytes > 0 ? workspace.data_ptr() : nullptr, wbytes,
-      stream_of(q[0]));
+      causal ? 1 : 0, mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(), scale,
+      wbytes > 0 ? workspace.data_ptr() : nullptr, wbytes, stream_of(q[0]));
   check_status(status, "taylor_attention_fwd");
   return {out, lse};
 }
@@ -387,10 +413,11 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   const int64_t lk = k[0].size(1);
   c10::DeviceGuard guard(q[0].device());
   const auto mask = attention_mask(mask_in, q[0], lq, lk, causal, "taylor_attention_bwd");
+  if (mask.add) materialize = 0;   // an additive mask recomputes the scores
   Tensor dq = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor dk = at::empty({degree + 1, bh, lk, d}, q[0].options());
   Tensor dv = at::empty_like(dk);
-  const auto ranges = mask_ranges(mask, lq, lk);
+  const auto ranges = mask_ranges(mask.keep, lq, lk);
   const int code = dtype_code(dtype);
   if (materialize < 0) {   // float32 only: the library refuses the stored-tile path for float64
     const size_t size = pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, 1);
@@ -408,8 +435,7 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   const int status = pt_taylor_attention_bwd(
       code, static_cast<int>(degree), qs.data(), ks.data(), vs.data(), oc.data(), lc.data(), gs.data(), dqs.data(),
       dks.data(), dvs.data(), workspace.data_ptr(), static_cast<int>(materialize), bh, lq, lk, d, causal ? 1 : 0,
-      mask ? static_cast<const uint8_t*>(mask->data_ptr()) : nullptr, ranges ? ranges->data_ptr<int32_t>() : nullptr,
-      scale, stream_of(q[0]));
+      mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(), scale, stream_of(q[0]));
   check_status(status, "taylor_attention_bwd");
   return {dq, dk, dv};
 }

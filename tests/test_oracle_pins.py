@@ -313,7 +313,26 @@ def test_cross_entropy_backward_series_matches_jets_of_vjp(softcap):
     _check(got, taylor(vjp, [Z, C], degree), 1e-12)
 
 
-@pytest.mark.parametrize("mode,degree", (("causal", 1), ("causal", 3), ("window", 2), ("none", 3)))
+def test_attention_reference_case_additive_mask():
+    # data and additive mask of /root/reference/tests/test_attention.py:13-17,53-54: -inf entries
+    # exclude their keys, the others add to the constant-order scores; row 0 has no admissible key
+    g = torch.Generator().manual_seed(27)
+    values = [torch.randn(1, 1, 3, 2, generator=g, dtype=torch.float64) / 3 for _ in range(3)]
+    directions = [torch.randn(c.shape, generator=g, dtype=c.dtype) / 4 for c in values]
+    inf = float("-inf")
+    mask = torch.tensor([[inf] * 3, [0.2, inf, -0.1], [0.1, -0.3, 0.0]], dtype=torch.float64)
+    Q, K, V = (paths.lift([x, d], 3) for x, d in zip(values, directions))
+    got = oracle.attention(Q, K, V, attn_mask=mask)
+    finite = torch.where(torch.isneginf(mask), torch.zeros(()), mask)
+    want = taylor(lambda q, k, v: _math_attention(q, k, v, excluded=torch.isneginf(mask), additive=finite),
+                  [[values[i], directions[i]] for i in range(3)], 3)
+    for k in range(4):
+        assert torch.isnan(got[k][..., 0, :]).all()
+        torch.testing.assert_close(got[k][..., 1:, :], want[k][..., 1:, :], atol=2e-14, rtol=2e-12)
+
+
+@pytest.mark.parametrize("mode,degree", (("causal", 1), ("causal", 3), ("window", 2), ("none", 3),
+                                         ("additive", 3)))
 def test_attention_backward_series_matches_jets_of_vjp(mode, degree):
     L, S, d = 7, 9, 4
     Q = _series((2, L, d), degree, seed=61)
@@ -322,12 +341,16 @@ def test_attention_backward_series_matches_jets_of_vjp(mode, degree):
     i, j = torch.arange(L)[:, None], torch.arange(S)[None, :]
     window = (i + 2 >= j) & (i + 2 - j <= 3)
     window[3] = False                                      # a query row with no admissible key
-    mask = {"causal": None, "window": window, "none": None}[mode]
-    excluded = {"causal": ~torch.ones(L, S, dtype=torch.bool).tril(), "window": ~window}.get(mode)
+    additive = torch.randn(L, S, generator=torch.Generator().manual_seed(65), dtype=torch.float64)
+    additive = additive.masked_fill(~window, float("-inf"))
+    mask = {"causal": None, "window": window, "none": None, "additive": additive}[mode]
+    excluded = {"causal": ~torch.ones(L, S, dtype=torch.bool).tril(), "window": ~window,
+                "additive": ~window}.get(mode)
+    finite = additive.masked_fill(~window, 0.0) if mode == "additive" else 0.0
 
     def vjp(q, k, v, g):
         def f(a, b, c):
-            s = 0.4 * (a @ b.transpose(-2, -1))
+            s = 0.4 * (a @ b.transpose(-2, -1)) + finite
             if excluded is None:
                 return torch.softmax(s, -1) @ c
             empty = excluded.all(-1, keepdim=True)          # such a row: zero output, no gradient
