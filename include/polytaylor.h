@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 11
+#define PT_ABI_VERSION 12
 #define PT_MAX_DEGREE 8
 
 typedef enum pt_dtype {
@@ -265,6 +265,12 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
  *   PT_FLOAT32, double for PT_FLOAT64; PT_UNSUPPORTED for the 16-bit types). mask must then
  *   be given and mark exactly its finite entries (an entry of -inf excludes its key; a row
  *   with none admissible gets the empty-row output above).
+ * mask_map: NULL (mask, mask_ranges and mask_add hold one mask, shared by every head), or
+ *   three int64 {div, outer, inner} in host memory: they then hold a set of masks, [n, lq, lk]
+ *   each (mask_ranges: n sets of pt_attention_mask_ranges_count(lq, lk) entries), and head b
+ *   (0 .. bh-1) uses mask (b / div) * outer + (b % div) * inner. This is the broadcast of the
+ *   reference's attn_mask over batch and heads (a [B, 1, lq, lk] mask over H heads per batch
+ *   is {H, 1, 0}; [1, H, lq, lk] is {H, 0, 1}; one per head is {1, 1, 0}).
  */
 size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
                                               int64_t bh, int64_t lq, int64_t lk, int64_t d);
@@ -272,8 +278,8 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
                                const void* const* k, int k_orders, const void* const* v, int v_orders,
                                void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
                                int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges,
-                               const void* mask_add, double scale, void* workspace, size_t workspace_bytes,
-                               void* stream);
+                               const void* mask_add, const int64_t* mask_map, double scale, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /*
  * Block ranges of a boolean [lq, lk] attention mask (nonzero = admissible),
@@ -281,12 +287,13 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
  *   /root/reference/src/polytensors/_fused_attention.py:81-99:
  * for each 64-row query block the first and one-past-last admissible key,
  * then for each 64-key block the first and one-past-last query admitting one of
- * its keys ((0, 0) when none). ranges: pt_attention_mask_ranges_count(lq, lk)
- * int32 of device memory. Computed once per mask, reused by any number of
- * forward and backward calls with that mask.
+ * its keys ((0, 0) when none). mask: n_masks masks [n_masks, lq, lk] (n_masks
+ * at most 65535); ranges: n_masks * pt_attention_mask_ranges_count(lq, lk)
+ * int32 of device memory, the masks' ranges one after the other. Computed once
+ * per mask, reused by any number of forward and backward calls with that mask.
  */
 int64_t pt_attention_mask_ranges_count(int64_t lq, int64_t lk);
-int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk,
+int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, int64_t lk,
                              int32_t* ranges, void* stream);
 
 /*
@@ -306,8 +313,8 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk,
  *   admissible pair instead of eight (S and dP are then not recomputed for dK
  *   and dV), at the cost of that workspace. PT_FLOAT32 only (PT_UNSUPPORTED
  *   for PT_FLOAT64).
- * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add: as in
- *   pt_taylor_attention_fwd_ws (the forward's additive mask; with it the scores
+ * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add, mask_map: as in
+ *   pt_taylor_attention_fwd_ws (the forward's additive mask: with it the scores
  *   are recomputed and materialize does not apply).
  * Pointers must be 16-byte aligned. Deterministic (no atomics).
  * Replaces the degree-1 fused backward
@@ -323,7 +330,8 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q,
                             void* const* dk, void* const* dv, void* workspace,
                             int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
                             int causal, const uint8_t* mask,
-                            const int32_t* mask_ranges, const void* mask_add, double scale,
+                            const int32_t* mask_ranges, const void* mask_add, const int64_t* mask_map,
+                            double scale,
                             void* stream);
 
 /* Bytes of device workspace pt_taylor_attention_bwd needs (the per-row

@@ -9,9 +9,11 @@ constant-order scores only, the exponential series of the higher orders is
 formed from ``k E_k = sum_j j S_j E_{k-j}`` (/root/reference/src/polytensors/_plain.py:153-159),
 and the output is the series quotient of the accumulated numerator and row sum.
 Eligibility and conventions follow the degree-1 kernel of the reference
-(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or an
-(L, S) mask (not both), no dropout or GQA, default scale 1/sqrt(d), and a query
-row with no admissible key gets output zero. A floating mask is added to the
+(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or a mask
+(not both), no dropout or GQA, default scale 1/sqrt(d), and a query row with no
+admissible key gets output zero. The mask is (..., L, S), broadcasting over the
+batch as in the reference's general rule (one shared mask, one per batch entry,
+one per head, or any mix of these). A floating mask is added to the
 scores, so to their constant order, as the reference's general rule does
 (/root/reference/src/polytensors/_decompositions.py:38-40); its -inf entries
 exclude their keys (16-bit operands with such a mask run the float32 kernel).
@@ -58,17 +60,31 @@ def default_scale(head_dim):
     return 1 / math.sqrt(head_dim)
 
 
-def _square_mask(attn_mask, L, S):
-    """A boolean or floating (additive) mask as an (L, S) tensor, None if absent, NotImplemented
-    if batch-dependent or of another dtype."""
+def _kernel_mask(attn_mask, batch, L, S):
+    """The mask as the kernels take it, ``(mask, mask_map)``: ``(None, None)`` without one, an
+    (L, S) mask shared by every head with map None, or a set of masks (n, L, S) with the map
+    (div, outer, inner) of heads to masks (head b of the flattened batch uses mask
+    ``(b // div) * outer + (b % div) * inner``). The mask broadcasts against the batch
+    dimensions ``batch`` as in torch's scaled_dot_product_attention. NotImplemented for a mask
+    that is neither boolean nor floating or does not broadcast."""
     if attn_mask is None:
-        return None
-    if not (attn_mask.dtype == torch.bool or attn_mask.dtype.is_floating_point) or \
-            tuple(attn_mask.shape[-2:]) != (L, S):
+        return None, None
+    if not (attn_mask.dtype == torch.bool or attn_mask.dtype.is_floating_point) or attn_mask.ndim < 2 or \
+            tuple(attn_mask.shape[-2:]) != (L, S) or attn_mask.ndim - 2 > len(batch):
         return NotImplemented
-    if any(size != 1 for size in attn_mask.shape[:-2]):
+    lead = (1,) * (len(batch) - (attn_mask.ndim - 2)) + tuple(attn_mask.shape[:-2])
+    if any(m not in (1, b) for m, b in zip(lead, batch)):
         return NotImplemented
-    return attn_mask.reshape(L, S)
+    if all(m == 1 for m in lead):
+        return attn_mask.reshape(L, S), None
+    if len(batch) >= 2 and all(m == 1 for m in lead[:-2]):
+        H = batch[-1]
+        if lead[-1] == 1 and math.prod(batch[:-2]) == 1:   # a mask per batch entry, over its H heads
+            return attn_mask.reshape(lead[-2], L, S), (H, 1, 0)
+        if lead[-2] == 1:   # a mask per head, the same in every batch entry
+            return attn_mask.reshape(lead[-1], L, S), (H, 0, 1)
+    # otherwise a mask per head of the flattened batch
+    return attn_mask.expand(*batch, L, S).reshape(-1, L, S), (1, 1, 0)
 
 
 def _needs_grad(*values):
@@ -114,8 +130,8 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
                 "160 KiB LDS budget for the staged key/value tiles")
     if is_causal and attn_mask is not None:
         return "is_causal and attn_mask are exclusive"
-    if _square_mask(attn_mask, query.shape[-2], key.shape[-2]) is NotImplemented:
-        return "only a boolean or floating (L, S) mask is supported"
+    if _kernel_mask(attn_mask, tuple(query.shape[:-2]), query.shape[-2], key.shape[-2]) is NotImplemented:
+        return "the mask must be boolean or floating, of shape (..., L, S) broadcasting over the batch"
     return None
 
 
@@ -155,12 +171,12 @@ class _SeriesAttention(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, query, key, value, mask, causal, scale):
+    def forward(ctx, query, key, value, mask, causal, scale):   # mask: (mask, mask_map) of _kernel_mask
         degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
         q = _full(query, degree, query.shape)
         k = _full(key, degree, key.shape)
         v = _full(value, degree, value.shape)
-        out, lse = _ops.taylor_attention_fwd(q, k, v, mask, causal, scale, degree)
+        out, lse = _ops.taylor_attention_fwd(q, k, v, mask[0], causal, scale, degree, mask_map=mask[1])
         ctx.save_for_backward(*q, *k, *v, out, lse)
         ctx.meta = (degree, mask, causal, scale, query.shape, key.shape)
         ctx.poly = tuple(isinstance(x, PolyTensor) for x in (query, key, value))
@@ -179,7 +195,7 @@ class _SeriesAttention(torch.autograd.Function):
         token = _plain_range.set(True)   # the engine's thread does not see the caller's context
         try:
             g = _full(gradient, degree, shape_q)
-            dq, dk, dv = _ops.attention_gradient_series(q, k, v, out, lse, g, mask, causal, scale)
+            dq, dk, dv = _ops.attention_gradient_series(q, k, v, out, lse, g, mask[0], causal, scale, mask[1])
             grads = (PolyTensor.from_stacked(dq.view(n, *shape_q)), PolyTensor.from_stacked(dk.view(n, *shape_k)),
                      PolyTensor.from_stacked(dv.view(n, *shape_k)))
         finally:
@@ -200,12 +216,12 @@ def attention_checked(query, key, value, attn_mask=None, is_causal=False, scale=
                                       attn_mask=attn_mask, is_causal=is_causal, scale=scale)
     degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
     L, S = query.shape[-2], key.shape[-2]
-    mask = _square_mask(attn_mask, L, S)
+    mask = _kernel_mask(attn_mask, tuple(query.shape[:-2]), L, S)   # (mask, mask_map)
     scale = default_scale(query.shape[-1]) if scale is None else scale
     if _needs_grad(query, key, value):
         return _SeriesAttention.apply(query, key, value, mask, bool(is_causal), float(scale))
     q = _flat(_gate.coefficients(query, degree), query.shape)
     k = _flat(_gate.coefficients(key, degree), key.shape)
     v = _flat(_gate.coefficients(value, degree), value.shape)
-    out, _ = _ops.taylor_attention_fwd(q, k, v, mask, bool(is_causal), float(scale), degree)
+    out, _ = _ops.taylor_attention_fwd(q, k, v, mask[0], bool(is_causal), float(scale), degree, mask_map=mask[1])
     return PolyTensor.from_stacked(out.view(degree + 1, *query.shape))

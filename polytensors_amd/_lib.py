@@ -15,7 +15,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
 # the operators' PyTorch registration (csrc/torch_ops.cpp), linked with libpolytaylor.so
 TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor_torch.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
@@ -60,12 +60,12 @@ SIGNATURES = {
                                                                  _c_i64, _c_i64, _c_i64]),
     "pt_taylor_attention_fwd_ws": (_c_int, [_c_int, _c_int, _c_vpp, _c_int, _c_vpp, _c_int, _c_vpp, _c_int,
                                             _c_vpp, _c_vpp, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp,
-                                            _c_vp, _c_vp, _c_dbl, _c_vp, ctypes.c_size_t, _c_vp]),
+                                            _c_vp, _c_vp, _c_vp, _c_dbl, _c_vp, ctypes.c_size_t, _c_vp]),
     "pt_attention_mask_ranges_count": (_c_i64, [_c_i64, _c_i64]),
-    "pt_attention_mask_ranges": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "pt_attention_mask_ranges": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
     "pt_taylor_attention_bwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_vpp, _c_vpp, _c_vpp, _c_vpp,
                                          _c_vpp, _c_vpp, _c_vpp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
-                                         _c_int, _c_vp, _c_vp, _c_vp, _c_dbl, _c_vp]),
+                                         _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_dbl, _c_vp]),
     "pt_taylor_attention_bwd_workspace_size": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int]),
     "pt_stream_copy": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_vp]),
     "pt_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),

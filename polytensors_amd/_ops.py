@@ -31,9 +31,10 @@ SCHEMAS = {
                                       "Tensor[] cot) -> Tensor"),
     "cauchy_matmul": "(Tensor[] a, Tensor[] b, int degree, bool trans_b) -> Tensor",
     "taylor_attention_fwd": ("(Tensor[] q, Tensor[] k, Tensor[] v, Tensor? mask, bool causal, float scale, "
-                             "int degree) -> (Tensor, Tensor)"),
+                             "int degree, int[]? mask_map=None) -> (Tensor, Tensor)"),
     "taylor_attention_bwd": ("(Tensor[] q, Tensor[] k, Tensor[] v, Tensor out, Tensor lse, Tensor[] grad, "
-                             "Tensor? mask, bool causal, float scale, int materialize=-1) -> (Tensor, Tensor, Tensor)"),
+                             "Tensor? mask, bool causal, float scale, int materialize=-1, int[]? mask_map=None) "
+                             "-> (Tensor, Tensor, Tensor)"),
     "complex_to_real": "(Tensor[] src, float[] alpha, float[] beta) -> Tensor",
     "real_to_complex": "(Tensor[] src, int orders, float[] wre, float[] wim) -> Tensor",
     "activation_series": "(Tensor[] x, str kind) -> Tensor",
@@ -136,7 +137,7 @@ def _mask_ranges(mask, lq, lk):
     them internally (pt_attention_mask_ranges; a direct handle for tests)."""
     lib = _lib.load()
     ranges = torch.empty(max(lib.pt_attention_mask_ranges_count(lq, lk), 1), dtype=torch.int32, device=mask.device)
-    _lib.check(lib.pt_attention_mask_ranges(mask.data_ptr(), lq, lk, ranges.data_ptr(), _lib.stream_of(mask.device)),
+    _lib.check(lib.pt_attention_mask_ranges(mask.data_ptr(), 1, lq, lk, ranges.data_ptr(), _lib.stream_of(mask.device)),
                "attention_mask_ranges")
     return ranges
 
@@ -145,13 +146,13 @@ taylor_attention_fwd = _op("taylor_attention_fwd")
 
 
 @torch.library.register_fake(f"{NAMESPACE}::taylor_attention_fwd")
-def _(q, k, v, mask, causal, scale, degree):
+def _(q, k, v, mask, causal, scale, degree, mask_map=None):
     bh, lq, d = q[0].shape
     return (q[0].new_empty((degree + 1, bh, lq, d)),
             q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))
 
 
-def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale):
+def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale, mask_map=None):
     """Gradient series (dq, dk, dv) of the attention forward for every operand dtype.
 
     float32/float64 call ``taylor_attention_bwd``. bfloat16/float16 operands run
@@ -166,16 +167,17 @@ def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale):
         def up(xs):
             return [x.float() for x in xs]
 
-        dq, dk, dv = taylor_attention_bwd(up(q), up(k), up(v), out.float(), lse, up(grad), mask, causal, scale)
+        dq, dk, dv = taylor_attention_bwd(up(q), up(k), up(v), out.float(), lse, up(grad), mask, causal, scale,
+                                          mask_map=mask_map)
         return dq.to(dtype), dk.to(dtype), dv.to(dtype)
-    return taylor_attention_bwd(q, k, v, out, lse, grad, mask, causal, scale)
+    return taylor_attention_bwd(q, k, v, out, lse, grad, mask, causal, scale, mask_map=mask_map)
 
 
 taylor_attention_bwd = _op("taylor_attention_bwd")
 
 
 @torch.library.register_fake(f"{NAMESPACE}::taylor_attention_bwd")
-def _(q, k, v, out, lse, grad, mask, causal, scale, materialize=-1):
+def _(q, k, v, out, lse, grad, mask, causal, scale, materialize=-1, mask_map=None):
     return (q[0].new_empty((len(q), *q[0].shape)), k[0].new_empty((len(k), *k[0].shape)),
             k[0].new_empty((len(k), *k[0].shape)))
 
@@ -281,9 +283,10 @@ def _grads_flag(tensors):
 
 
 def _returned(ctx, *grads):
-    """``grads`` padded with None to the number of arguments the call passed (torch matches the
-    backward's return to the arguments given, defaulted ones excluded)."""
-    return tuple(grads) + (None,) * (ctx.n_inputs - len(grads))
+    """``grads`` padded with None to the number of arguments the call passed: torch matches the
+    backward's return to the arguments given (defaulted ones excluded, and so is a keyword
+    argument passed at its default), whose structure ``ctx.needs_input_grad`` has here."""
+    return tuple(grads) + (None,) * (len(ctx.needs_input_grad) - len(grads))
 
 
 def _once(what):
@@ -375,17 +378,18 @@ torch.library.register_autograd(f"{NAMESPACE}::cauchy_matmul", _mm_backward, set
 
 
 def _attn_setup(ctx, inputs, output):
-    q, k, v, mask, causal, scale, degree = inputs
+    q, k, v, mask, causal, scale, degree = inputs[:7]
+    mask_map = inputs[7] if len(inputs) > 7 else None
     out, lse = output
     ctx.mark_non_differentiable(lse)
     ctx.save_for_backward(*q, *k, *v, out, lse, *([] if mask is None else [mask]))
-    ctx.meta = (len(q), len(k), len(v), mask is not None, causal, scale, degree)
+    ctx.meta = (len(q), len(k), len(v), mask is not None, causal, scale, degree, mask_map)
     ctx.n_inputs = len(inputs)
 
 
 def _attn_backward(ctx, grad_out, grad_lse):
     _once("taylor_attention_fwd")
-    nq, nk, nv, has_mask, causal, scale, degree = ctx.meta
+    nq, nk, nv, has_mask, causal, scale, degree, mask_map = ctx.meta
     s = ctx.saved_tensors
     q, k, v = list(s[:nq]), list(s[nq:nq + nk]), list(s[nq + nk:nq + nk + nv])
     out, lse = s[nq + nk + nv], s[nq + nk + nv + 1]
@@ -395,7 +399,7 @@ def _attn_backward(ctx, grad_out, grad_lse):
         return xs + [torch.zeros_like(xs[0]) for _ in range(degree + 1 - len(xs))]
 
     dq, dk, dv = attention_gradient_series(full(q), full(k), full(v), out, lse, _reversed(grad_out), mask, causal,
-                                           scale)
+                                           scale, mask_map)
     return _returned(ctx, _read_back(dq, nq), _read_back(dk, nk), _read_back(dv, nv))
 
 

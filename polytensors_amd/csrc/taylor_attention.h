@@ -22,6 +22,24 @@ __host__ __device__ constexpr int attn_slices(int elem, int K, int D) {
                    : (D == 128 && K >= 6 ? 2 : 1);
 }
 
+// Which of a set of (L, S) masks a head uses: head b (0 .. bh-1) takes mask
+// (b / div) * outer + (b % div) * inner. One shared mask: {1, 0, 0}; masks per
+// batch over H heads each ([B, 1, L, S]): {H, 1, 0}; per head of each batch
+// ([1, H, L, S]): {H, 0, 1}; one per head ([bh, L, S]): {1, 1, 0}.
+struct AttnMaskMap {
+  int64_t div = 1, outer = 0, inner = 0;
+};
+
+__host__ __device__ inline int64_t attn_mask_index(const AttnMaskMap& m, int64_t head) {
+  return (head / m.div) * m.outer + (head % m.div) * m.inner;
+}
+
+// int32 entries of one mask's block ranges (launch_attention_mask_ranges): a (lo, hi)
+// pair per 64-row query block, then per 64-key block.
+__host__ __device__ constexpr int64_t attn_ranges_count(int64_t lq, int64_t lk) {
+  return 2 * ((lq + 63) / 64 + (lk + 63) / 64);
+}
+
 struct AttnArgs {
   int degree;
   const void* const* q;
@@ -43,6 +61,7 @@ struct AttnArgs {
   // null, or an (L, S) additive mask in the accumulator type (float32/float64 operands only),
   // with mask its finite entries
   const void* mask_add = nullptr;
+  AttnMaskMap mask_map{};   // mask (mask_ranges, mask_add) of each head, from a set of masks
 };
 
 template <typename T>
@@ -89,9 +108,11 @@ inline AttnSplit attention_split(const AttnArgs& a, int dtype) {
 template <typename T>
 int launch_attention_half(const AttnArgs& a);
 
-// Block ranges of a boolean (L, S) mask into ranges[attention_mask_ranges_count(L, S)].
+// Block ranges of n_masks boolean (L, S) masks ([n_masks, L, S]) into ranges[n_masks *
+// attention_mask_ranges_count(L, S)].
 int64_t attention_mask_ranges_count(int64_t lq, int64_t lk);
-int launch_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, hipStream_t stream);
+int launch_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, int64_t lk, int32_t* ranges,
+                                 hipStream_t stream);
 
 // Backward: every series has degree+1 orders; dq/dk/dv may be null (not
 // computed). workspace holds (degree+1) * bh * lq accumulator-type values.
@@ -117,6 +138,7 @@ struct AttnBwdArgs {
   // null, or an (L, S) additive mask in the accumulator type with mask its finite entries (the
   // scores are then recomputed: materialize does not apply)
   const void* mask_add = nullptr;
+  AttnMaskMap mask_map{};
 };
 
 template <typename T>

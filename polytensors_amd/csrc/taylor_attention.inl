@@ -132,8 +132,11 @@ __device__ __forceinline__ void attn_work_item(int L, int causal, int64_t& head,
 constexpr int kAttnRangeBlock = 64;
 
 template <int Unused = 0>   // a template: this header is included by several translation units
-__global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __restrict__ mask, int L, int S,
-                                                               int32_t* __restrict__ ranges) {
+__global__ __launch_bounds__(256) void attn_mask_ranges_kernel(const uint8_t* __restrict__ masks, int L, int S,
+                                                               int32_t* __restrict__ all_ranges) {
+  // mask blockIdx.y of the [n, L, S] set, its ranges at blockIdx.y * attn_ranges_count(L, S)
+  const uint8_t* __restrict__ mask = masks + static_cast<int64_t>(blockIdx.y) * L * S;
+  int32_t* __restrict__ ranges = all_ranges + static_cast<int64_t>(blockIdx.y) * attn_ranges_count(L, S);
   __shared__ int lo_s, hi_s;
   const int nqb = (L + kAttnRangeBlock - 1) / kAttnRangeBlock;
   const int b = blockIdx.x;
@@ -383,8 +386,8 @@ __device__ __forceinline__ const T* order_ptr(const CPtrs<T>& s, int o) {
 template <typename T, int K, int D, bool ADD>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O,
-    MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask,
-    const typename AccOf<T>::type* __restrict__ madd, const int32_t* __restrict__ ranges, int causal,
+    MPtrs<typename AccOf<T>::type> LSE, int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap,
+    const typename AccOf<T>::type* __restrict__ madd_all, const int32_t* __restrict__ ranges_all, int causal,
     typename AccOf<T>::type scale, int chunks, int chunk_keys, typename AccOf<T>::type* __restrict__ part) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
@@ -428,6 +431,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
   }
   const int d0 = slice * DS;   // first output head dim of this workgroup
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const typename AccOf<T>::type* madd = madd_all != nullptr ? madd_all + mask_index * L * S : nullptr;
   const int q0 = q_block + wave * kAttnQPerWave;
   const int my_q = q0 + c;
   const bool q_ok = my_q < L;
@@ -830,7 +838,8 @@ __device__ __forceinline__ void attn_load_v_step(Vec<float, AttnPvE<D>::value> (
 template <int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_kernel(
     CPtrs<float> Q, CPtrs<float> Kp, CPtrs<float> Vp, MPtrs<float> O, MPtrs<float> LSE, int L, int S,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
+    float scale) {
   using A = float;
   using MF = Mfma16<float>;
   using acc_t = MF::acc_t;
@@ -850,6 +859,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
   int64_t head;
   int q_block;
   attn_work_item(L, causal, head, q_block);
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
   const int q0_wave = q_block + wave * kAttnQPerWave;
   const int my_q = q0_wave + c;
   const bool q_ok = my_q < L;
@@ -1222,7 +1235,7 @@ static int launch_attention_kd(const AttnArgs& a) {
         pipe = pt_host::aligned16(a.q[i]) && pt_host::aligned16(a.k[i]) && pt_host::aligned16(a.v[i]);
       if (pipe) {
         taylor_attention_fwd_pipe_kernel<K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_ranges,
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges,
             a.causal ? 1 : 0, static_cast<A>(a.scale));
         PT_LAUNCH_CHECK();
         return PT_OK;
@@ -1236,7 +1249,7 @@ static int launch_attention_kd(const AttnArgs& a) {
 #define PT_ATTN_STAGED(ADD)                                                                                  \
   taylor_attention_fwd_kernel<T, K, D, ADD><<<sgrid, dim3(kAttnWaves * kWave), 0, a.stream>>>(               \
       q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),   \
-      a.mask, madd, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale), chunks, split ? sp.chunk_keys : 0, \
+      a.mask, a.mask_map, madd, a.mask_ranges, a.causal ? 1 : 0, static_cast<A>(a.scale), chunks, split ? sp.chunk_keys : 0, \
       split ? static_cast<A*>(a.workspace) : nullptr)
     if (madd != nullptr) PT_ATTN_STAGED(true);
     else PT_ATTN_STAGED(false);

@@ -1,6 +1,19 @@
 // C ABI of the Taylor attention kernels.
 #include "taylor_attention.h"
 
+namespace {
+
+// The mask map of the C ABI (NULL: one mask shared by every head), checked.
+bool read_mask_map(const int64_t* map, pt::AttnMaskMap& m) {
+  if (map == nullptr) return true;
+  m.div = map[0];
+  m.outer = map[1];
+  m.inner = map[2];
+  return m.div >= 1 && m.outer >= 0 && m.inner >= 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_orders,
@@ -9,7 +22,7 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q, int q_o
                             int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges, double scale,
                             void* stream) {
   return pt_taylor_attention_fwd_ws(dtype, degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
-                                    causal, mask, mask_ranges, nullptr, scale, nullptr, 0, stream);
+                                    causal, mask, mask_ranges, nullptr, nullptr, scale, nullptr, 0, stream);
 }
 
 size_t pt_taylor_attention_fwd_workspace_size(int dtype, int degree, int q_orders, int k_orders, int v_orders,
@@ -23,9 +36,12 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
                                const void* const* k, int k_orders, const void* const* v, int v_orders,
                                void* const* out, void* const* lse, int64_t bh, int64_t lq, int64_t lk,
                                int64_t d, int causal, const uint8_t* mask, const int32_t* mask_ranges,
-                               const void* mask_add, double scale, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+                               const void* mask_add, const int64_t* mask_map, double scale, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   pt_host::clear_error();
+  pt::AttnMaskMap map;
+  PT_REQUIRE(read_mask_map(mask_map, map), PT_INVALID_ARGUMENT,
+             "Taylor attention: mask_map must hold div >= 1, outer >= 0, inner >= 0");
   PT_REQUIRE(workspace_bytes == 0 || pt_host::aligned16(workspace), PT_INVALID_ARGUMENT,
              "Taylor attention: workspace must be 16-byte aligned");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
@@ -62,7 +78,7 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
   if (bh == 0 || lq == 0) return PT_OK;
   pt::AttnArgs a{degree, q, q_orders, k, k_orders, v, v_orders, out, lse, bh, lq, lk, d,
                  causal != 0, mask, mask_ranges, scale, static_cast<hipStream_t>(stream),
-                 workspace_bytes > 0 ? workspace : nullptr, workspace_bytes, mask_add};
+                 workspace_bytes > 0 ? workspace : nullptr, workspace_bytes, mask_add, map};
   switch (dtype) {
     case PT_FLOAT32: return pt::launch_attention<float>(a);
     case PT_FLOAT64: return pt::launch_attention<double>(a);
@@ -76,13 +92,16 @@ int64_t pt_attention_mask_ranges_count(int64_t lq, int64_t lk) {
   return pt::attention_mask_ranges_count(lq, lk);
 }
 
-int pt_attention_mask_ranges(const uint8_t* mask, int64_t lq, int64_t lk, int32_t* ranges, void* stream) {
+int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, int64_t lk, int32_t* ranges,
+                             void* stream) {
   pt_host::clear_error();
   PT_REQUIRE(lq >= 0 && lk >= 0 && lq <= INT32_MAX && lk <= INT32_MAX, PT_INVALID_ARGUMENT,
              "attention mask ranges: sizes out of range");
+  PT_REQUIRE(n_masks >= 0 && n_masks <= 65535, PT_INVALID_ARGUMENT,
+             "attention mask ranges: n_masks must be in 0..65535");
   PT_REQUIRE((mask != nullptr || lq * lk == 0) && (ranges != nullptr || lq + lk == 0), PT_INVALID_ARGUMENT,
              "attention mask ranges: mask and ranges are required");
-  return pt::launch_attention_mask_ranges(mask, lq, lk, ranges, static_cast<hipStream_t>(stream));
+  return pt::launch_attention_mask_ranges(mask, n_masks, lq, lk, ranges, static_cast<hipStream_t>(stream));
 }
 
 size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq, int64_t lk,
@@ -97,8 +116,11 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
                             const void* const* grad, void* const* dq, void* const* dk, void* const* dv,
                             void* workspace, int materialize, int64_t bh, int64_t lq, int64_t lk, int64_t d,
                             int causal, const uint8_t* mask, const int32_t* mask_ranges, const void* mask_add,
-                            double scale, void* stream) {
+                            const int64_t* mask_map, double scale, void* stream) {
   pt_host::clear_error();
+  pt::AttnMaskMap map;
+  PT_REQUIRE(read_mask_map(mask_map, map), PT_INVALID_ARGUMENT,
+             "Taylor attention backward: mask_map must hold div >= 1, outer >= 0, inner >= 0");
   PT_REQUIRE(mask_ranges == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention backward: mask_ranges without a mask");
   PT_REQUIRE(mask_add == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
@@ -147,7 +169,7 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   if (bh == 0) return PT_OK;
   pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
                     causal != 0, mask, mask_ranges, scale, materialize != 0, static_cast<hipStream_t>(stream),
-                    mask_add};
+                    mask_add, map};
   return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
 }
 

@@ -393,8 +393,8 @@ template <typename T, int K, int D, int NS, bool STORE, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DQ, MPtrs<T> PT, MPtrs<T> DST, int L, int S,
-    const uint8_t* __restrict__ mask, const typename AccOf<T>::type* __restrict__ madd,
-    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const typename AccOf<T>::type* __restrict__ madd_all,
+    const int32_t* __restrict__ ranges_all, int causal, typename AccOf<T>::type scale) {
   constexpr bool MASKED = MASK != 0, ADD = MASK == 2;
   static_assert(!(ADD && STORE), "an additive mask runs the recomputing path");
   using A = typename AccOf<T>::type;
@@ -420,6 +420,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_ker
   int64_t head;
   int slice, q_block;
   attn_bwd_q_item(blockIdx.x, bh, nqb, SLICES, head, slice, q_block);
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const typename AccOf<T>::type* madd = madd_all != nullptr ? madd_all + mask_index * L * S : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qoff = (head * L + (q_ok ? my_q : 0)) * D;
@@ -608,8 +613,8 @@ template <typename T, int K, int D, int NS, int WHAT, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<typename AccOf<T>::type> LSE,
     CPtrs<typename AccOf<T>::type> DELTA, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
-    const uint8_t* __restrict__ mask, const typename AccOf<T>::type* __restrict__ madd,
-    const int32_t* __restrict__ ranges, int causal, typename AccOf<T>::type scale) {
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const typename AccOf<T>::type* __restrict__ madd_all,
+    const int32_t* __restrict__ ranges_all, int causal, typename AccOf<T>::type scale) {
   constexpr bool MASKED = MASK != 0, ADD = MASK == 2;
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
@@ -642,6 +647,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
   int64_t head;
   int slice, kv_block;
   attn_bwd_kv_item(blockIdx.x, bh, SLICES, head, slice, kv_block);
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const typename AccOf<T>::type* madd = madd_all != nullptr ? madd_all + mask_index * L * S : nullptr;
   const int my_k = kv_block + wave * 16 + c;
   const bool k_ok = my_k < S;
   const int64_t koff = (head * S + (k_ok ? my_k : 0)) * D;
@@ -842,7 +852,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ke
 template <typename T, int K, int D, int NS, int WHAT, bool MASKED>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_mat_kernel(
     CPtrs<T> Q, CPtrs<T> G, CPtrs<T> PT, CPtrs<T> DST, MPtrs<T> DK, MPtrs<T> DV, int L, int S,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal,
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
     typename AccOf<T>::type scale) {
   using A = typename AccOf<T>::type;
   using MF = Mfma16<T>;
@@ -869,6 +879,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ma
   int64_t head;
   int slice, kv_block;
   attn_bwd_kv_item(blockIdx.x, bh, SLICES, head, slice, kv_block);
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
   const int my_k = kv_block + wave * 16 + c;
   const bool k_ok = my_k < S;
   const int nqt = (L + 15) / 16, nkt = (S + 15) / 16;
@@ -1007,7 +1021,7 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
       const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
 #define PT_ATTN_BWD_Q(STORE, MASK)                                                                     \
   taylor_attention_bwd_q_kernel<T, K, D, Plan::NS_Q, STORE, MASK><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>( \
-      q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, madd, a.mask_ranges, causal, scale)
+      q, k, v, g, lse, delta_in, dq, pt, dst, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale)
       const bool masked = a.mask != nullptr;
       if constexpr (kCanStore) {
         if (materialize) {   // (without a dq output the kernel still writes the P and dS tiles)
@@ -1034,28 +1048,28 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
   do {                                                                                                       \
     if (madd != nullptr)                                                                                     \
       taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 2><<<grid, block, 0, a.stream>>>(           \
-          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);              \
     else if (a.mask != nullptr)                                                                              \
       taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 1><<<grid, block, 0, a.stream>>>(           \
-          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);              \
     else                                                                                                     \
       taylor_attention_bwd_kv_kernel<T, K, D, Plan::NS_KV, WHAT, 0><<<grid, block, 0, a.stream>>>(           \
-          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, madd, a.mask_ranges, causal, scale);              \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);              \
   } while (0)
       if (materialize) {
        if constexpr (kCanStore) {
         constexpr int SL = Plan::DB / Plan::NS_KM;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
         if constexpr (Plan::km_fused) {
-          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 3, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 3, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
           PT_LAUNCH_CHECK();
         } else {
           if (a.dv != nullptr) {
-            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 1, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 1, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
           if (a.dk != nullptr) {
-            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 2, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_ranges, causal, scale));
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 2, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
           }
         }

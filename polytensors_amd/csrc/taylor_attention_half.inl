@@ -76,7 +76,8 @@ __device__ __forceinline__ u32x4 attn_half_load8(const T* p, bool ok) {
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O, MPtrs<float> LSE,
-    int L, int S, const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
+    int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all,
+    int causal, float scale) {
   using Sh = AttnHalfShape<K, D>;
   using MM = HalfMfma<T>;
   constexpr int KB = Sh::KB, DC = Sh::DC, DB = Sh::DB, LDK = Sh::LDK, LDV = Sh::LDV;
@@ -106,6 +107,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     q_block = (nqb - 1 - static_cast<int>(t / bh)) * kAttnBM;
   }
   const int d0 = slice * DS;   // first output head dim of this workgroup
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qrow = (head * L + (q_ok ? my_q : 0)) * D;
@@ -432,7 +437,8 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
 template <typename T, int K, int D>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S,
-    const uint8_t* __restrict__ mask, const int32_t* __restrict__ ranges, int causal, float scale) {
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
+    float scale) {
   using P = AttnHalfPipe<K, D>;
   using MM = HalfMfma<T>;
   constexpr int KB = P::KB, DC = (D + 31) / 32, DB = D / 16, OPS = P::OPS;
@@ -451,6 +457,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   int64_t head;
   int q_block;
   attn_work_item(L, causal, head, q_block);
+  // this head's mask, its block ranges (and additive values)
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
@@ -736,7 +746,7 @@ static int launch_attention_half_kd(const AttnArgs& a) {
       if (pipe) {
         const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
         taylor_attention_fwd_half_pipe_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_ranges,
+            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges,
             a.causal ? 1 : 0, static_cast<float>(a.scale));
         PT_LAUNCH_CHECK();
         return PT_OK;
@@ -745,7 +755,7 @@ static int launch_attention_half_kd(const AttnArgs& a) {
     const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * AttnHalfShape<K, D>::SL));
     taylor_attention_fwd_half_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
         q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),
-        a.mask, a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
+        a.mask, a.mask_map, a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
     PT_LAUNCH_CHECK();
     return PT_OK;
   }

@@ -12,6 +12,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <array>
 #include <limits>
 #include <string>
 #include <vector>
@@ -295,34 +296,54 @@ Tensor cauchy_matmul(const TensorList& a_in, const TensorList& b_in, int64_t deg
 
 // ---- Taylor attention --------------------------------------------------------
 
-// Block ranges of a bool (L, S) mask on its device (the key / query blocks the kernels visit).
-c10::optional<Tensor> mask_ranges(const c10::optional<Tensor>& mask, int64_t lq, int64_t lk) {
-  if (!mask) return c10::nullopt;
-  Tensor ranges = at::empty({std::max<int64_t>(1, pt_attention_mask_ranges_count(lq, lk))},
-                            mask->options().dtype(at::kInt));
-  check_status(pt_attention_mask_ranges(static_cast<const uint8_t*>(mask->data_ptr()), lq, lk,
-                                        ranges.data_ptr<int32_t>(), stream_of(*mask)),
-               "attention_mask_ranges");
-  return ranges;
-}
-
-// A boolean (L, S) mask as it is, or a floating one (added to the constant-order scores) as the
-// boolean mask of its entries above -inf and its values in the accumulator type.
+// An attention mask as the kernels take it: the boolean mask of the admissible entries (a
+// floating mask's entries above -inf), a floating mask's values in the accumulator type (added
+// to the constant-order scores), and for a set of masks [n, L, S] the map of heads to masks.
 struct AttnMask {
   c10::optional<Tensor> keep, add;
+  int64_t count = 1;
+  std::array<int64_t, 3> map{1, 0, 0};
+  bool mapped = false;
   const uint8_t* keep_ptr() const { return keep ? static_cast<const uint8_t*>(keep->data_ptr()) : nullptr; }
   const void* add_ptr() const { return add ? add->data_ptr() : nullptr; }
+  const int64_t* map_ptr() const { return mapped ? map.data() : nullptr; }
 };
 
-AttnMask attention_mask(const c10::optional<Tensor>& mask, const Tensor& q0, int64_t lq, int64_t lk, bool causal,
-                        const char* name) {
+// mask: (L, S), shared by every head, or (n, L, S) with mask_map (div, outer, inner): head b
+// uses mask (b / div) * outer + (b % div) * inner (without a map, n == bh and head b uses mask b).
+AttnMask attention_mask(const c10::optional<Tensor>& mask, at::OptionalIntArrayRef mask_map, const Tensor& q0,
+                        int64_t bh, int64_t lq, int64_t lk, bool causal, const char* name) {
   AttnMask m;
-  if (!mask) return m;
+  const bool has_map = mask_map.has_value() && !mask_map->empty();
+  if (!mask) {
+    TORCH_CHECK_VALUE(!has_map, name, ": mask_map without a mask");
+    return m;
+  }
   const at::ScalarType type = mask->scalar_type();
-  TORCH_CHECK_VALUE((type == at::kBool || at::isFloatingType(type)) && mask->dim() == 2 && mask->size(0) == lq &&
-                        mask->size(1) == lk && mask->device() == q0.device(),
-                    name, ": mask must be a bool or floating (L, S) tensor on the query's device");
+  const int64_t dim = mask->dim();
+  TORCH_CHECK_VALUE((type == at::kBool || at::isFloatingType(type)) && (dim == 2 || dim == 3) &&
+                        mask->size(dim - 2) == lq && mask->size(dim - 1) == lk && mask->device() == q0.device(),
+                    name, ": mask must be a bool or floating (L, S) or (n, L, S) tensor on the query's device");
   TORCH_CHECK_VALUE(!causal, name, ": mask and causal are exclusive");
+  if (dim == 3) {
+    m.count = mask->size(0);
+    TORCH_CHECK_VALUE(m.count >= 1 && m.count <= 65535, name, ": a mask set holds 1 to 65535 masks");
+    if (has_map) {
+      TORCH_CHECK_VALUE(mask_map->size() == 3 && (*mask_map)[0] >= 1 && (*mask_map)[1] >= 0 && (*mask_map)[2] >= 0,
+                        name, ": mask_map must be (div >= 1, outer >= 0, inner >= 0)");
+      m.map = {(*mask_map)[0], (*mask_map)[1], (*mask_map)[2]};
+    } else {
+      TORCH_CHECK_VALUE(m.count == bh, name, ": an (n, L, S) mask without mask_map needs one mask per head");
+      m.map = {1, 1, 0};
+    }
+    if (bh > 0) {   // the largest mask index any head takes
+      const int64_t top = ((bh - 1) / m.map[0]) * m.map[1] + (std::min(m.map[0], bh) - 1) * m.map[2];
+      TORCH_CHECK_VALUE(top < m.count, name, ": mask_map sends a head past the ", m.count, " masks given");
+    }
+    m.mapped = true;
+  } else {
+    TORCH_CHECK_VALUE(!has_map, name, ": mask_map needs an (n, L, S) mask");
+  }
   if (type == at::kBool) {
     m.keep = mask->contiguous();
     return m;
@@ -332,9 +353,19 @@ AttnMask attention_mask(const c10::optional<Tensor>& mask, const Tensor& q0, int
   return m;
 }
 
+// Block ranges of every mask of m on its device (the key / query blocks the kernels visit).
+c10::optional<Tensor> mask_ranges(const AttnMask& m, int64_t lq, int64_t lk) {
+  if (!m.keep) return c10::nullopt;
+  const int64_t per = pt_attention_mask_ranges_count(lq, lk);
+  Tensor ranges = at::empty({std::max<int64_t>(1, m.count * per)}, m.keep->options().dtype(at::kInt));
+  check_status(pt_attention_mask_ranges(m.keep_ptr(), m.count, lq, lk, ranges.data_ptr<int32_t>(), stream_of(*m.keep)),
+               "attention_mask_ranges");
+  return ranges;
+}
+
 std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const TensorList& k, const TensorList& v,
                                                 const c10::optional<Tensor>& mask_in, bool causal, double scale,
-                                                int64_t degree) {
+                                                int64_t degree, at::OptionalIntArrayRef mask_map) {
   check_abi();
   for (const auto& [name, s] :
        {std::pair<const char*, const TensorList*>{"q", &q}, {"k", &k}, {"v", &v}}) {
@@ -358,13 +389,13 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
       for (const Tensor& x : xs) out.push_back(x.to(at::kFloat));
       return out;
     };
-    auto [o32, l32] = taylor_attention_fwd(widen(q), widen(k), widen(v), mask_in, causal, scale, degree);
+    auto [o32, l32] = taylor_attention_fwd(widen(q), widen(k), widen(v), mask_in, causal, scale, degree, mask_map);
     return {o32.to(dtype), l32};
   }
-  const auto mask = attention_mask(mask_in, q[0], lq, lk, causal, "taylor_attention");
+  const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention");
   Tensor out = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor lse = at::empty({degree + 1, bh, lq}, q[0].options().dtype(acc_type(dtype)));
-  const auto ranges = mask_ranges(mask.keep, lq, lk);
+  const auto ranges = mask_ranges(mask, lq, lk);
   auto qs = cptrs(q), ks = cptrs(k), vs = cptrs(v);
   auto os = slices(out), ls = slices(lse);
   const int code = dtype_code(dtype);
@@ -377,8 +408,8 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
   const int status = pt_taylor_attention_fwd_ws(
       code, static_cast<int>(degree), qs.data(), static_cast<int>(q.size()), ks.data(),
       static_cast<int>(k.size()), vs.data(), static_cast<int>(v.size()), os.data(), ls.data(), bh, lq, lk, d,
-      causal ? 1 : 0, mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(), scale,
-      wbytes > 0 ? workspace.data_ptr() : nullptr, wbytes, stream_of(q[0]));
+      causal ? 1 : 0, mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(),
+      mask.map_ptr(), scale, wbytes > 0 ? workspace.data_ptr() : nullptr, wbytes, stream_of(q[0]));
   check_status(status, "taylor_attention_fwd");
   return {out, lse};
 }
@@ -386,7 +417,8 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
 std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, const TensorList& k,
                                                         const TensorList& v, const Tensor& out, const Tensor& lse,
                                                         const TensorList& grad, const c10::optional<Tensor>& mask_in,
-                                                        bool causal, double scale, int64_t materialize) {
+                                                        bool causal, double scale, int64_t materialize,
+                                                        at::OptionalIntArrayRef mask_map) {
   check_abi();
   const int64_t degree = static_cast<int64_t>(q.size()) - 1;
   for (const auto& [name, s] : {std::pair<const char*, const TensorList*>{"q", &q}, {"k", &k}, {"v", &v},
@@ -412,12 +444,12 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
                     "taylor_attention_bwd: lse must be the forward's contiguous [K+1, bh, L] output");
   const int64_t lk = k[0].size(1);
   c10::DeviceGuard guard(q[0].device());
-  const auto mask = attention_mask(mask_in, q[0], lq, lk, causal, "taylor_attention_bwd");
+  const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention_bwd");
   if (mask.add) materialize = 0;   // an additive mask recomputes the scores
   Tensor dq = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor dk = at::empty({degree + 1, bh, lk, d}, q[0].options());
   Tensor dv = at::empty_like(dk);
-  const auto ranges = mask_ranges(mask.keep, lq, lk);
+  const auto ranges = mask_ranges(mask, lq, lk);
   const int code = dtype_code(dtype);
   if (materialize < 0) {   // float32 only: the library refuses the stored-tile path for float64
     const size_t size = pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, 1);
@@ -435,7 +467,8 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   const int status = pt_taylor_attention_bwd(
       code, static_cast<int>(degree), qs.data(), ks.data(), vs.data(), oc.data(), lc.data(), gs.data(), dqs.data(),
       dks.data(), dvs.data(), workspace.data_ptr(), static_cast<int>(materialize), bh, lq, lk, d, causal ? 1 : 0,
-      mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(), scale, stream_of(q[0]));
+      mask.keep_ptr(), ranges ? ranges->data_ptr<int32_t>() : nullptr, mask.add_ptr(), mask.map_ptr(), scale,
+      stream_of(q[0]));
   check_status(status, "taylor_attention_bwd");
   return {dq, dk, dv};
 }
@@ -576,9 +609,9 @@ TORCH_LIBRARY(polytensors_amd, m) {
         "Tensor[] cot) -> Tensor");
   m.def("cauchy_matmul(Tensor[] a, Tensor[] b, int degree, bool trans_b) -> Tensor");
   m.def("taylor_attention_fwd(Tensor[] q, Tensor[] k, Tensor[] v, Tensor? mask, bool causal, float scale, "
-        "int degree) -> (Tensor, Tensor)");
+        "int degree, int[]? mask_map=None) -> (Tensor, Tensor)");
   m.def("taylor_attention_bwd(Tensor[] q, Tensor[] k, Tensor[] v, Tensor out, Tensor lse, Tensor[] grad, "
-        "Tensor? mask, bool causal, float scale, int materialize=-1) -> (Tensor, Tensor, Tensor)");
+        "Tensor? mask, bool causal, float scale, int materialize=-1, int[]? mask_map=None) -> (Tensor, Tensor, Tensor)");
   m.def("complex_to_real(Tensor[] src, float[] alpha, float[] beta) -> Tensor");
   m.def("real_to_complex(Tensor[] src, int orders, float[] wre, float[] wim) -> Tensor");
   m.def("activation_series(Tensor[] x, str kind) -> Tensor");

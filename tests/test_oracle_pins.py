@@ -517,3 +517,31 @@ def test_decoder_oracle_matches_complex_jets(monkeypatch):
     want = taylor_complex(lambda x: bench.gpt_forward(params, x, targets, heads, attention=math_sdpa),
                           [base], [u], [w], degree)
     _check_complex(got, want, 1e-10)
+
+
+def test_attention_oracle_broadcast_masks_match_per_entry_calls():
+    # a mask over the batch ([B, 1, L, S], [1, H, L, S], [B, H, L, S], boolean and additive) gives
+    # each (batch, head) entry what the pinned (L, S) path gives it with that entry's mask
+    B, H, L, S, d, degree = 2, 3, 7, 9, 4, 2
+    Q = _series((B, H, L, d), degree, seed=70)
+    K, V, G = (_series((B, H, S, d), degree, seed=71 + i) for i in range(3))
+    G = _series((B, H, L, d), degree, seed=74)
+    g = torch.Generator().manual_seed(75)
+    for shape in ((B, 1, L, S), (1, H, L, S), (B, H, L, S)):
+        keep = torch.rand(shape, generator=g) < 0.7
+        keep[..., 2, :] = False                            # rows with no admissible key
+        additive = torch.randn(shape, generator=g, dtype=torch.float64).masked_fill(~keep, float("-inf"))
+        for mask in (keep, additive):
+            got = oracle.attention(Q, K, V, attn_mask=mask, scale=0.4)
+            grads = oracle.attention_backward(Q, K, V, G, attn_mask=mask, scale=0.4)
+            for b in range(B):
+                for h in range(H):
+                    m = mask[b % mask.shape[0], h % mask.shape[1]]
+                    pick = lambda X: [x[b:b + 1, h:h + 1] for x in X]   # noqa: E731
+                    want = oracle.attention(pick(Q), pick(K), pick(V), attn_mask=m, scale=0.4)
+                    for a, w in zip(got, want):
+                        torch.testing.assert_close(a[b:b + 1, h:h + 1], w, equal_nan=True, rtol=0, atol=0)
+                    want_g = oracle.attention_backward(pick(Q), pick(K), pick(V), pick(G), attn_mask=m, scale=0.4)
+                    for gs, ws in zip(grads, want_g):
+                        for a, w in zip(gs, ws):
+                            torch.testing.assert_close(a[b:b + 1, h:h + 1], w, rtol=0, atol=0)
