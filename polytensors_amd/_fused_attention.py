@@ -9,8 +9,8 @@ constant-order scores only, the exponential series of the higher orders is
 formed from ``k E_k = sum_j j S_j E_{k-j}`` (/root/reference/src/polytensors/_plain.py:153-159),
 and the output is the series quotient of the accumulated numerator and row sum.
 Eligibility and conventions follow the degree-1 kernel of the reference
-(/root/reference/src/polytensors/_fused_attention.py:188-316): causal or a mask
-(not both), no dropout or GQA, default scale 1/sqrt(d), and a query row with no
+(/root/reference/src/polytensors/_fused_attention.py:188-316): causal, a mask or
+both (as the general rule, which applies each), no dropout or GQA, default scale 1/sqrt(d), and a query row with no
 admissible key gets output zero. The mask is (..., L, S), broadcasting over the
 batch as in the reference's general rule (one shared mask, one per batch entry,
 one per head, or any mix of these). A floating mask is added to the
@@ -128,8 +128,6 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if not _tiles_fit_lds(dtype, query.shape[-1], degree, backward):
         return (f"the backward at degree {degree}, head dim {query.shape[-1]} in {dtype} exceeds the kernels' "
                 "160 KiB LDS budget for the staged key/value tiles")
-    if is_causal and attn_mask is not None:
-        return "is_causal and attn_mask are exclusive"
     if _kernel_mask(attn_mask, tuple(query.shape[:-2]), query.shape[-2], key.shape[-2]) is NotImplemented:
         return "the mask must be boolean or floating, of shape (..., L, S) broadcasting over the batch"
     return None
@@ -216,6 +214,12 @@ def attention_checked(query, key, value, attn_mask=None, is_causal=False, scale=
                                       attn_mask=attn_mask, is_causal=is_causal, scale=scale)
     degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
     L, S = query.shape[-2], key.shape[-2]
+    if is_causal and attn_mask is not None:
+        # both: the causal rule applied to the mask (the general rule masks the scores with each,
+        # /root/reference/src/polytensors/_decompositions.py:36-41)
+        keep = torch.ones(L, S, dtype=torch.bool, device=attn_mask.device).tril()
+        attn_mask = attn_mask & keep if attn_mask.dtype == torch.bool else attn_mask.masked_fill(~keep, float("-inf"))
+        is_causal = False
     mask = _kernel_mask(attn_mask, tuple(query.shape[:-2]), L, S)   # (mask, mask_map)
     scale = default_scale(query.shape[-1]) if scale is None else scale
     if _needs_grad(query, key, value):

@@ -6,9 +6,10 @@ The reference's general rule broadcasts ``attn_mask`` against the scores
 mask), one per head ([1, H, L, S]), one per (batch, head), or another rank of
 batch. The kernels take such a mask as a set of (L, S) masks with a map from
 heads to masks (the ``mask_map`` of the attention entry points). Checked: the
-forward series of boolean and additive masks of every such shape, their lse,
-the gradient series through autograd, bfloat16 operands, and the operator's
-refusal of a map that sends a head past the masks given. The oracle
+forward series of boolean and additive masks of every such shape, the gradient
+series through autograd, bfloat16 operands, a mask together with is_causal, a
+mask set with an explicit map against one mask per head (outputs and lse), and
+the operator's refusal of a map that sends a head past the masks given. The oracle
 (``oracle.attention`` / ``oracle.attention_backward``, whose broadcast masks match
 per-entry calls exactly: tests/test_oracle_pins.py) runs in float64 on the same
 (upcast) inputs; rows with no admissible key are compared as zero (the fused
@@ -152,3 +153,25 @@ def test_operator_mask_sets_and_maps():
         _ops.taylor_attention_fwd(q, k, v, masks.cuda(), False, 0.25, degree)
     with pytest.raises(ValueError, match="mask_map"):
         _ops.taylor_attention_fwd(q, k, v, masks[0].cuda(), False, 0.25, degree, mask_map=[1, 1, 0])
+
+
+@pytest.mark.parametrize("additive", [False, True])
+def test_causal_together_with_a_mask(additive):
+    # the general rule applies both (/root/reference/src/polytensors/_decompositions.py:36-41)
+    degree, shape = 2, (2, 3, 100, 32)
+    Q, K, V, G = (_series(shape, degree, 60 + i) for i in range(4))
+    g = torch.Generator().manual_seed(64)
+    mask = torch.rand(2, 1, 100, 100, generator=g) < 0.6
+    if additive:
+        mask = torch.randn(2, 1, 100, 100, generator=g, dtype=torch.float64).masked_fill(~mask, float("-inf"))
+    q, k, v = (_poly(s, torch.float64, grad=True) for s in (Q, K, V))
+    with PolyTensor.plain_range():
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask.cuda(), is_causal=True)
+        out.backward(_poly(G, torch.float64))
+    keep = (mask if not additive else ~torch.isneginf(mask)) & torch.ones(100, 100, dtype=torch.bool).tril()
+    empty = (~keep.any(-1)).expand(2, 3, 100)
+    _check(out.coeffs, oracle.attention(Q, K, V, attn_mask=mask, is_causal=True), empty, torch.float64)
+    grads = oracle.attention_backward(Q, K, V, G, attn_mask=mask, is_causal=True)
+    none = torch.zeros(2, 3, 100, dtype=torch.bool)
+    for name, x, b in zip(("dq", "dk", "dv"), (q, k, v), grads):
+        _check(x.grad.coeffs, b, none, torch.float64, what=name)
