@@ -119,16 +119,18 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
             return "query, key and value coefficients must share one dtype"
     if dtype not in _HEAD_DIMS:
         return f"dtype {dtype} is not supported (float32, float64, bfloat16 or float16)"
-    if query.ndim < 3 or key.shape != value.shape or query.shape[:-2] != key.shape[:-2]:
+    qs, ks = query.shape, key.shape
+    if len(qs) < 3 or ks != value.shape or qs[:-2] != ks[:-2]:
         return "shapes must be (..., L, d) and (..., S, d) with equal batch dimensions"
-    if query.shape[-1] != key.shape[-1] or query.shape[-1] not in _HEAD_DIMS[dtype]:
-        return f"head dim {query.shape[-1]} not in {_HEAD_DIMS[dtype]}"
-    degree = next(x.degree for x in tensors if isinstance(x, PolyTensor))
-    backward = grads or _gate.coefficient_graph(*tensors)
-    if not _tiles_fit_lds(dtype, query.shape[-1], degree, backward):
-        return (f"the backward at degree {degree}, head dim {query.shape[-1]} in {dtype} exceeds the kernels' "
-                "160 KiB LDS budget for the staged key/value tiles")
-    if _kernel_mask(attn_mask, tuple(query.shape[:-2]), query.shape[-2], key.shape[-2]) is NotImplemented:
+    d = qs[-1]
+    if d != ks[-1] or d not in _HEAD_DIMS[dtype]:
+        return f"head dim {d} not in {_HEAD_DIMS[dtype]}"
+    if grads or _gate.coefficient_graph(*tensors):
+        degree = next(x.degree for x in tensors if isinstance(x, PolyTensor))
+        if not _tiles_fit_lds(dtype, d, degree, True):
+            return (f"the backward at degree {degree}, head dim {d} in {dtype} exceeds the kernels' "
+                    "160 KiB LDS budget for the staged key/value tiles")
+    if attn_mask is not None and _kernel_mask(attn_mask, tuple(qs[:-2]), qs[-2], ks[-2]) is NotImplemented:
         return "the mask must be boolean or floating, of shape (..., L, S) broadcasting over the batch"
     return None
 
@@ -148,6 +150,10 @@ def _flat(coeffs, shape):
     rows, d = shape[-2], shape[-1]
     return [c.view(-1, rows, d) if c.shape == shape and c.is_contiguous() else
             c.expand(shape).reshape(-1, rows, d).contiguous() for c in coeffs]
+
+
+def _contiguous(coeffs):
+    return [c if c.is_contiguous() else c.contiguous() for c in coeffs]
 
 
 def _full(x, degree, shape):
@@ -224,8 +230,9 @@ def attention_checked(query, key, value, attn_mask=None, is_causal=False, scale=
     scale = default_scale(query.shape[-1]) if scale is None else scale
     if _needs_grad(query, key, value):
         return _SeriesAttention.apply(query, key, value, mask, bool(is_causal), float(scale))
-    q = _flat(_gate.coefficients(query, degree), query.shape)
-    k = _flat(_gate.coefficients(key, degree), key.shape)
-    v = _flat(_gate.coefficients(value, degree), value.shape)
+    # the operator takes [..., T, d] coefficients (batch dimensions flattened to heads in order)
+    q = _contiguous(_gate.coefficients(query, degree))
+    k = _contiguous(_gate.coefficients(key, degree))
+    v = _contiguous(_gate.coefficients(value, degree))
     out, _ = _ops.taylor_attention_fwd(q, k, v, mask[0], bool(is_causal), float(scale), degree, mask_map=mask[1])
-    return PolyTensor.from_stacked(out.view(degree + 1, *query.shape))
+    return PolyTensor.from_stacked(out)

@@ -11,7 +11,7 @@ adds what belongs in Python: the fake (shape) implementations and the
 coefficient-level autograd of every operator. Outputs never alias inputs.
 """
 
-
+import math
 
 import torch
 
@@ -147,9 +147,9 @@ taylor_attention_fwd = _op("taylor_attention_fwd")
 
 @torch.library.register_fake(f"{NAMESPACE}::taylor_attention_fwd")
 def _(q, k, v, mask, causal, scale, degree, mask_map=None):
-    bh, lq, d = q[0].shape
-    return (q[0].new_empty((degree + 1, bh, lq, d)),
-            q[0].new_empty((degree + 1, bh, lq), dtype=_acc_dtype(q[0].dtype)))
+    *batch, lq, d = q[0].shape   # batch dimensions, flattened to bh heads in the lse series
+    return (q[0].new_empty((degree + 1, *batch, lq, d)),
+            q[0].new_empty((degree + 1, math.prod(batch), lq), dtype=_acc_dtype(q[0].dtype)))
 
 
 def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale, mask_map=None):
@@ -395,12 +395,16 @@ def _attn_backward(ctx, grad_out, grad_lse):
     out, lse = s[nq + nk + nv], s[nq + nk + nv + 1]
     mask = s[-1] if has_mask else None
 
+    shape_q, shape_k = q[0].shape, k[0].shape   # [..., L, d], [..., S, d]: flattened to [bh, T, d] here
+
     def full(xs):   # the backward kernels take every order; an ordinary operand has zero higher orders
+        xs = [x.reshape(-1, *x.shape[-2:]) for x in xs]
         return xs + [torch.zeros_like(xs[0]) for _ in range(degree + 1 - len(xs))]
 
-    dq, dk, dv = attention_gradient_series(full(q), full(k), full(v), out, lse, _reversed(grad_out), mask, causal,
-                                           scale, mask_map)
-    return _returned(ctx, _read_back(dq, nq), _read_back(dk, nk), _read_back(dv, nv))
+    dq, dk, dv = attention_gradient_series(full(q), full(k), full(v), out.reshape(degree + 1, -1, *shape_q[-2:]),
+                                           lse, full(_reversed(grad_out)), mask, causal, scale, mask_map)
+    return _returned(ctx, _read_back(dq.view(degree + 1, *shape_q), nq), _read_back(dk.view(degree + 1, *shape_k), nk),
+                     _read_back(dv.view(degree + 1, *shape_k), nv))
 
 
 torch.library.register_autograd(f"{NAMESPACE}::taylor_attention_fwd", _attn_backward, setup_context=_attn_setup)

@@ -373,14 +373,20 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
     TORCH_CHECK_VALUE(len == 1 || len == degree + 1, "taylor_attention: ", name,
                       " needs 1 or degree+1 coefficients");
     check_series(std::string("taylor_attention ") + name, *s);
-    TORCH_CHECK_VALUE((*s)[0].dim() == 3, "taylor_attention: ", name, " must be [bh, length, d]");
+    TORCH_CHECK_VALUE((*s)[0].dim() >= 3, "taylor_attention: ", name, " must be [..., length, d]");
   }
+  // batch dimensions [...] (flattened to bh heads in order), then length and head dim
   const at::ScalarType dtype = q[0].scalar_type();
-  const int64_t bh = q[0].size(0), lq = q[0].size(1), d = q[0].size(2);
-  TORCH_CHECK_VALUE(k[0].sizes() == v[0].sizes() && k[0].size(0) == bh && k[0].size(2) == d,
-                    "taylor_attention: key/value shapes must be [bh, S, d] matching the query");
+  const int64_t nd = q[0].dim();
+  const auto batch = q[0].sizes().slice(0, nd - 2);
+  const int64_t lq = q[0].size(nd - 2), d = q[0].size(nd - 1);
+  int64_t bh = 1;
+  for (const int64_t b : batch) bh *= b;
+  TORCH_CHECK_VALUE(k[0].sizes() == v[0].sizes() && k[0].dim() == nd && k[0].sizes().slice(0, nd - 2) == batch &&
+                        k[0].size(nd - 1) == d,
+                    "taylor_attention: key/value shapes must be [..., S, d] matching the query");
   TORCH_CHECK_VALUE(k[0].scalar_type() == dtype && v[0].scalar_type() == dtype, "taylor_attention: dtypes differ");
-  const int64_t lk = k[0].size(1);
+  const int64_t lk = k[0].size(nd - 2);
   c10::DeviceGuard guard(q[0].device());
   if (mask_in && mask_in->scalar_type() != at::kBool && (dtype == at::kBFloat16 || dtype == at::kHalf)) {
     // the additive mask runs on the float32 kernel: 16-bit operands are widened, the output rounded
@@ -393,7 +399,11 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
     return {o32.to(dtype), l32};
   }
   const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention");
-  Tensor out = at::empty({degree + 1, bh, lq, d}, q[0].options());
+  std::vector<int64_t> out_shape{degree + 1};
+  out_shape.insert(out_shape.end(), batch.begin(), batch.end());
+  out_shape.push_back(lq);
+  out_shape.push_back(d);
+  Tensor out = at::empty(out_shape, q[0].options());
   Tensor lse = at::empty({degree + 1, bh, lq}, q[0].options().dtype(acc_type(dtype)));
   const auto ranges = mask_ranges(mask, lq, lk);
   auto qs = cptrs(q), ks = cptrs(k), vs = cptrs(v);
