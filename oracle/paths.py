@@ -170,7 +170,7 @@ def attention_backward(Q, K, V, G, attn_mask=None, is_causal=False, scale=None):
     return dQ, dK, dV
 
 
-def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
+def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None, weight=None, label_smoothing=0.0):
     """Per-order loss series of ``F.cross_entropy(z, target)`` on (N, C) logits.
 
     The log-softmax series (/root/reference/src/polytensors/_plain.py:262-273)
@@ -178,14 +178,39 @@ def cross_entropy(Z, target, ignore_index=-100, reduction="mean", softcap=None):
     With ``softcap`` the logits are first ``softcap * tanh(z / softcap)``, the
     composite of /root/reference/src/polytensors/_fused_cross_entropy.py:184-187:
     per-coefficient scalar division and product around the plain-range tanh
-    rule (_plain.py:256-259, 303-304).
+    rule (_plain.py:256-259, 303-304). With class weights or label smoothing the
+    reference has no fused rule (_fused_cross_entropy.py:142) and torch's
+    cross_entropy decomposes into log_softmax and its linear loss terms
+    (/root/reference/src/polytensors/_decompositions.py:66-67), applied here to
+    every order of the log-softmax series (``_smoothed``).
     """
     if softcap is not None:
         from .activations import activation
 
         Z = [softcap * t for t in activation([z / softcap for z in Z], "tanh")]
     _, log_softmax, _ = softmax_family(Z, 1)
-    return [_nll(lp, target, ignore_index, reduction) for lp in log_softmax]
+    if weight is None and label_smoothing == 0.0:
+        return [_nll(lp, target, ignore_index, reduction) for lp in log_softmax]
+    return [_smoothed(lp, target, weight, ignore_index, reduction, label_smoothing) for lp in log_softmax]
+
+
+def _smoothed(lp, target, weight, ignore_index, reduction, eps):
+    """torch's cross-entropy terms of one order of log-probabilities ``lp`` (N, C): (1 - eps) times
+    the weighted NLL -w_y lp_y plus eps / C times -sum_c w_c lp_c, both zero on ignored rows;
+    "mean" divides by the kept rows' total target weight (the count without weights)."""
+    C = lp.shape[1]
+    keep = target != ignore_index
+    safe = torch.where(keep, target, torch.zeros((), dtype=target.dtype))
+    w = torch.ones(C, dtype=lp.real.dtype) if weight is None else weight.to(lp.real.dtype)
+    wy = torch.where(keep, w[safe], torch.zeros((), dtype=w.dtype))
+    nll = -lp.gather(1, safe[:, None]).squeeze(1) * wy
+    smooth = torch.where(keep, -(lp * w).sum(1), torch.zeros((), dtype=lp.dtype))
+    per_row = (1 - eps) * nll + (eps / C) * smooth
+    if reduction == "none":
+        return per_row
+    if reduction == "sum":
+        return per_row.sum()
+    return per_row.sum() / wy.sum()
 
 
 def _nll(lp, target, ignore_index, reduction):

@@ -1,4 +1,4 @@
-"""Fused cross entropy of degree-K series of (N, C) logits on gfx950.
+"""Fused cross entropy of degree-K series of (N, C) (or (N, C, d1, ...)) logits on gfx950.
 
 For logits ``z(t) = sum_k z_k t^k`` and integer targets ``y``, one streaming
 pass per row computes the log-sum-exp series ``lse(t)`` of the row, and the
@@ -32,18 +32,22 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
     reason = _gate.common_reason((input,), allow_plain_grad=allow_grad, complex_ok=True)
     if reason is not None:
         return reason
-    if input.ndim != 2:
-        return "logits must be (N, C)"
+    if input.ndim < 2:
+        return "logits must be (N, C) or (N, C, d1, ...)"
     if input.dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != input.dtype for c in input.coeffs):
         return "logits must be float16/bfloat16/float32/float64 in every order"
     if isinstance(target, PolyTensor) or not isinstance(target, torch.Tensor) or target.dtype != torch.int64:
         return "targets must be an ordinary int64 tensor (class indices)"
-    if target.shape != input.shape[:1] or target.device != input.device:
-        return "targets must be (N,) on the logits' device"
-    if weight is not None:
-        return "class weights are not implemented"
-    if label_smoothing != 0.0:
-        return "label smoothing is not implemented"
+    if target.shape != input.shape[:1] + input.shape[2:] or target.device != input.device:
+        return "targets must be (N,) (or (N, d1, ...)) on the logits' device"
+    if weight is not None and (isinstance(weight, PolyTensor) or not isinstance(weight, torch.Tensor) or
+                               weight.shape != input.shape[1:2] or not weight.dtype.is_floating_point or
+                               weight.device != input.device):
+        return "class weights must be an ordinary floating (C,) tensor on the logits' device"
+    if not 0.0 <= label_smoothing <= 1.0:
+        return "label_smoothing must be in [0, 1]"
+    if softcap is not None and (weight is not None or label_smoothing != 0.0):
+        return "softcap with class weights or label smoothing is not implemented"
     if reduction not in _lib.REDUCTIONS:
         return f"unknown reduction {reduction!r}"
     if softcap is not None and not (isinstance(softcap, (int, float)) and 0 < softcap < float("inf")):
@@ -108,7 +112,7 @@ class _SeriesCrossEntropy(torch.autograd.Function):
         return dz, None, None, None
 
 
-def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
+def fused(input, target, ignore_index=-100, reduction="mean", softcap=None, weight=None, label_smoothing=0.0):
     """Loss series (a PolyTensor in float32, or float64 for float64 logits).
 
     ``softcap`` caps the logit series as ``softcap * tanh(z / softcap)`` inside the
@@ -116,11 +120,21 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     (/root/reference/src/polytensors/_cross_entropy_kernels.py:7-17). Under grad the
     per-row losses come from ``_SeriesCrossEntropy`` and the reduction is a series
     sum (and division by the count of kept rows), as the reference's
-    /root/reference/src/polytensors/_fused_cross_entropy.py:163-170.
+    /root/reference/src/polytensors/_fused_cross_entropy.py:163-170. Logits
+    (N, C, d1, ...) are rows of C classes (moved last); class weights and label
+    smoothing are ``_weighted``.
     """
     if _complex.has_complex(input):
         return _complex.at_real_nodes(fused, "cross_entropy", input, target, ignore_index=ignore_index,
-                                      reduction=reduction, softcap=softcap)
+                                      reduction=reduction, softcap=softcap, weight=weight,
+                                      label_smoothing=label_smoothing)
+    if input.ndim > 2:
+        classes = input.shape[1]
+        flat = fused(input.movedim(1, -1).reshape(-1, classes), target.reshape(-1), ignore_index, reduction, softcap,
+                     weight, label_smoothing)
+        return flat.reshape(target.shape) if reduction == "none" else flat
+    if weight is not None or label_smoothing != 0.0:
+        return _weighted(input, target, ignore_index, reduction, weight, label_smoothing)
     if _gate.wrapper_grad(input):
         losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
         if reduction == "none":
@@ -136,12 +150,50 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None):
     return PolyTensor.from_stacked(loss)
 
 
+def _weighted(input, target, ignore_index, reduction, weight, label_smoothing):
+    """``F.cross_entropy`` with class weights w and label smoothing eps on (N, C) logits.
+
+    The reference has no fused rule for these (/root/reference/src/polytensors/_fused_cross_entropy.py:142):
+    torch's cross_entropy decomposes into log_softmax and linear loss terms, which
+    its general rules apply to every order. Per kept row, with lse the row's
+    log-sum-exp series and the kernel's loss l = lse - z_y:
+        (1 - eps) w_y l + (eps / C) (W lse - sum_c w_c z_c),   W = sum_c w_c,
+    (w = 1 without weights); ignored rows are zero, and "mean" divides by the kept
+    rows' total target weight (their count without weights), as torch's
+    cross_entropy. The terms beyond l are series operations on the logits (gather,
+    weighted row sums), so autograd records them as it does the kernel's losses.
+    """
+    losses = fused(input, target, ignore_index=ignore_index, reduction="none")
+    dtype = losses.dtype
+    keep = target != ignore_index
+    safe = torch.where(keep, target, torch.zeros((), dtype=target.dtype, device=target.device))
+    kept = keep.to(dtype)
+    w = None if weight is None else weight.to(dtype)
+    wy = kept if w is None else w[safe] * kept
+    per_row = losses * wy
+    if label_smoothing != 0.0:
+        classes = input.shape[1]
+        z = input if input.dtype == dtype else input.to(dtype)
+        zy = z.gather(1, safe[:, None]).squeeze(1)
+        wz = z.sum(1) if w is None else (z * w).sum(1)
+        total_w = float(classes) if w is None else w.sum()
+        smooth = ((losses + zy) * total_w - wz) * kept
+        per_row = per_row * (1.0 - label_smoothing) + smooth * (label_smoothing / classes)
+    if reduction == "none":
+        return per_row
+    total = per_row.sum()
+    if reduction == "sum":
+        return total
+    return total / wy.sum()
+
+
 def fused_or_raise(input, target, weight=None, ignore_index=-100, reduction="mean", label_smoothing=0.0):
     reason = why_ineligible(input, target, weight, reduction, label_smoothing,
                             allow_grad=_gate.wrapper_grad(input))
     if reason is not None:
         raise NotImplementedError(f"cross_entropy: {reason}")
-    return fused(input, target, ignore_index=ignore_index, reduction=reduction)
+    return fused(input, target, ignore_index=ignore_index, reduction=reduction, weight=weight,
+                 label_smoothing=label_smoothing)
 
 
 def cross_entropy(logits, target, softcap=None, ignore_index=-100, reduction="mean"):

@@ -187,3 +187,66 @@ def test_expanded_logits_rows_are_materialized():
         loss = F.cross_entropy(logits, y.cuda(), reduction="none")
     want = oracle.cross_entropy([c.double().expand(6, 300) for c in row], y, reduction="none")
     _check(loss.coeffs, want, torch.float32)
+
+
+# Class weights and label smoothing: the reference's general rule (torch's cross_entropy decomposed
+# into log_softmax and its linear terms, /root/reference/src/polytensors/_decompositions.py:66-67);
+# the oracle restates those terms per order and is pinned by jets of torch's own cross_entropy.
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("weighted,smoothing", [(True, 0.0), (False, 0.1), (True, 0.3)])
+def test_weights_and_label_smoothing(dtype, reduction, weighted, smoothing):
+    degree = 3
+    Z, y = _logits(200, 700, degree, seed=60, dtype=dtype)
+    y[::9] = -1
+    w = (torch.rand(700, generator=torch.Generator().manual_seed(61), dtype=torch.float64) + 0.5).to(dtype) \
+        if weighted else None
+    logits = PolyTensor(tuple(c.cuda() for c in Z))
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = F.cross_entropy(logits, y.cuda(), weight=None if w is None else w.cuda(), ignore_index=-1,
+                               reduction=reduction, label_smoothing=smoothing)
+    assert loss.dtype == dtype and loss.degree == degree
+    want = oracle.cross_entropy([c.double() for c in Z], y, ignore_index=-1, reduction=reduction,
+                                weight=None if w is None else w.double(), label_smoothing=smoothing)
+    _check(loss.coeffs, want, dtype)
+
+
+@pytest.mark.parametrize("reduction", ["none", "mean"])
+def test_logits_with_extra_dimensions(reduction):
+    # (N, C, d1, d2) logits with (N, d1, d2) targets: rows of C classes, as torch's cross_entropy
+    degree, N, C = 2, 3, 40
+    g = torch.Generator().manual_seed(62)
+    Z = [torch.randn(N, C, 5, 7, generator=g, dtype=torch.float64) * 0.5 ** k for k in range(degree + 1)]
+    y = torch.randint(0, C, (N, 5, 7), generator=g)
+    y[0, 1] = -100
+    logits = PolyTensor(tuple(c.cuda() for c in Z))
+    with torch.no_grad(), PolyTensor.plain_range():
+        loss = F.cross_entropy(logits, y.cuda(), reduction=reduction, label_smoothing=0.2)
+    rows = [z.movedim(1, -1).reshape(-1, C) for z in Z]
+    want = oracle.cross_entropy(rows, y.reshape(-1), reduction=reduction, label_smoothing=0.2)
+    if reduction == "none":
+        want = [x.reshape(N, 5, 7) for x in want]
+    _check(loss.coeffs, want, torch.float64)
+
+
+@pytest.mark.parametrize("weighted,smoothing", [(True, 0.0), (False, 0.15), (True, 0.15)])
+def test_weights_and_label_smoothing_gradient_series(weighted, smoothing):
+    # PolyTensor.backward of the mean loss: the gradient series of the logits must be the Taylor
+    # series of torch.func.grad of torch's own cross_entropy along the curve
+    from tests.jets import taylor
+
+    degree = 3
+    Z, y = _logits(40, 60, degree, seed=63, dtype=torch.float64, base_scale=1.5)
+    y[::6] = -1
+    w = torch.rand(60, generator=torch.Generator().manual_seed(64), dtype=torch.float64) + 0.5 if weighted else None
+
+    def loss(z):
+        return F.cross_entropy(z, y, weight=w, ignore_index=-1, label_smoothing=smoothing)
+
+    x = PolyTensor(tuple(c.cuda() for c in Z), requires_grad=True)
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        out = F.cross_entropy(x, y.cuda(), weight=None if w is None else w.cuda(), ignore_index=-1,
+                              label_smoothing=smoothing)
+        out.backward()
+    _check(out.coeffs, taylor(loss, [Z], degree), torch.float64)
+    _check(x.grad.coeffs, taylor(lambda z: torch.func.grad(loss)(z), [Z], degree), torch.float64)

@@ -254,6 +254,20 @@ def test_cross_entropy_general_series(reduction):
     _check(got, want, 1e-12)
 
 
+@pytest.mark.parametrize("reduction", ("none", "mean", "sum"))
+@pytest.mark.parametrize("weighted,smoothing", ((True, 0.0), (False, 0.1), (True, 0.25)))
+def test_cross_entropy_weights_and_label_smoothing(reduction, weighted, smoothing):
+    # torch's own cross_entropy with class weights / label smoothing, differentiated along the curve
+    Z = _series((12, 37), 4, seed=44, scale=2.0)
+    y = torch.randint(0, 37, (12,), generator=torch.Generator().manual_seed(45))
+    y[::5] = -1
+    w = torch.rand(37, generator=torch.Generator().manual_seed(46), dtype=torch.float64) + 0.5 if weighted else None
+    got = oracle.cross_entropy(Z, y, ignore_index=-1, reduction=reduction, weight=w, label_smoothing=smoothing)
+    want = taylor(lambda z: F.cross_entropy(z, y, weight=w, ignore_index=-1, reduction=reduction,
+                                            label_smoothing=smoothing), [Z], 4)
+    _check(got, want, 1e-12)
+
+
 @pytest.mark.parametrize("reduction", ("none", "mean"))
 def test_cross_entropy_softcap_general_series(reduction):
     # the composite of /root/reference/src/polytensors/_fused_cross_entropy.py:184-187
