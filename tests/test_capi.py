@@ -56,6 +56,18 @@ def _vpp(n):
     ("pt_stream_copy", lambda: ((1 << 20) + 4, 1 << 21, 32, 0, 1, None), 1, "aligned"),
     ("pt_stream_read", lambda: (1 << 20, 32, 70000, 1, 1 << 21, None), 1, "blocks"),
     ("pt_stream_read", lambda: (1 << 20, 32, 0, 0, None, None), 1, "out"),
+    # attention masks: a map of heads to masks, additive masks, mask sets
+    ("pt_taylor_attention_fwd_ws", lambda: (0, 1, _vpp(2), 2, _vpp(2), 2, _vpp(2), 2, _vpp(2), None, 1, 16, 16, 64,
+                                            0, 1 << 20, None, None, (ctypes.c_int64 * 3)(0, 0, 0), 0.125, None, 0,
+                                            None), 1, "mask_map"),
+    ("pt_taylor_attention_fwd_ws", lambda: (0, 1, _vpp(2), 2, _vpp(2), 2, _vpp(2), 2, _vpp(2), None, 1, 16, 16, 64,
+                                            0, None, None, 1 << 20, None, 0.125, None, 0, None), 1, "boolean mask"),
+    ("pt_taylor_attention_fwd_ws", lambda: (2, 1, _vpp(2), 2, _vpp(2), 2, _vpp(2), 2, _vpp(2), None, 1, 16, 16, 64,
+                                            0, 1 << 20, None, 1 << 20, None, 0.125, None, 0, None), 2, "additive"),
+    ("pt_taylor_attention_bwd", lambda: (0, 1, _vpp(2), _vpp(2), _vpp(2), _vpp(2), _vpp(2), _vpp(2), None, None, None,
+                                         1 << 20, 0, 1, 16, 16, 64, 0, 1 << 20, None, None,
+                                         (ctypes.c_int64 * 3)(1, -1, 0), 0.125, None), 1, "mask_map"),
+    ("pt_attention_mask_ranges", lambda: (1 << 20, 70000, 16, 16, 1 << 21, None), 1, "n_masks"),
 ])
 def test_argument_errors_return_before_launch(entry, args, status, needle):
     lib = _lib.load()
