@@ -104,6 +104,8 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
         return "query, key and value must be tensors"
     if isinstance(attn_mask, PolyTensor):
         return "the mask must be an ordinary tensor"
+    if attn_mask is not None and attn_mask.requires_grad and torch.is_grad_enabled():
+        return "a mask that requires grad is not supported (no gradient flows to attn_mask)"
     grads = _needs_grad(*tensors)
     reason = _gate.common_reason(tensors, allow_plain_grad=grads, complex_ok=True)
     if reason is not None:

@@ -29,6 +29,8 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
                 "polytensors_amd has no general series rules")
     if not isinstance(input, PolyTensor):
         return "logits must be a PolyTensor"
+    if isinstance(weight, torch.Tensor) and weight.requires_grad and torch.is_grad_enabled():
+        return "class weights that require grad are not supported (no gradient flows to weight)"
     reason = _gate.common_reason((input,), allow_plain_grad=allow_grad, complex_ok=True)
     if reason is not None:
         return reason

@@ -183,3 +183,18 @@ def test_attention_lds_budget_gate():
         for d in (16, 32, 64, 128):
             assert all(_tiles_fit_lds(dtype, d, k, backward=b) for k in range(9) for b in (False, True))
     assert not _tiles_fit_lds(torch.float64, 128, 9, backward=True)
+
+
+def test_masks_and_class_weights_that_require_grad_are_refused():
+    # no gradient flows to attn_mask or to class weights: such calls are refused, not silently cut
+    from polytensors_amd import _fused_attention, _fused_cross_entropy
+
+    x = PolyTensor((torch.randn(1, 1, 8, 16), torch.randn(1, 1, 8, 16)))
+    mask = torch.zeros(8, 8, requires_grad=True)
+    assert "requires grad" in _fused_attention.why_ineligible(x, x, x, mask, 0.0, False, False)
+    z = PolyTensor((torch.randn(4, 10), torch.randn(4, 10)))
+    y = torch.randint(0, 10, (4,))
+    w = torch.ones(10, requires_grad=True)
+    assert "require grad" in _fused_cross_entropy.why_ineligible(z, y, w)
+    with torch.no_grad():
+        assert "requires grad" not in (_fused_attention.why_ineligible(x, x, x, mask, 0.0, False, False) or "")
