@@ -155,21 +155,12 @@ def _(q, k, v, mask, causal, scale, degree, mask_map=None):
 def attention_gradient_series(q, k, v, out, lse, grad, mask, causal, scale, mask_map=None):
     """Gradient series (dq, dk, dv) of the attention forward for every operand dtype.
 
-    float32/float64 call ``taylor_attention_bwd``. bfloat16/float16 operands run
-    the float32 backward kernels on float32 copies of q, k, v, the forward's
-    output and the cotangents (the forward's lse series is already float32) and
-    round the gradients to the operand dtype: the reference's half-type backward
-    likewise accumulates in float32 (/root/reference/src/polytensors/_fused_attention.py:72-78,
-    tolerance 5e-2 against float32, tests/test_fused_kernels.py:64-72).
+    bfloat16/float16 operands run the 16-bit backward kernels (16-bit MFMA
+    operands, float32 accumulation; the forward's lse series is float32), as the
+    reference's half-type backward accumulates in float32
+    (/root/reference/src/polytensors/_fused_attention.py:72-78, tolerance 5e-2
+    against float32, tests/test_fused_kernels.py:64-72).
     """
-    dtype = q[0].dtype
-    if dtype in (torch.bfloat16, torch.float16):
-        def up(xs):
-            return [x.float() for x in xs]
-
-        dq, dk, dv = taylor_attention_bwd(up(q), up(k), up(v), out.float(), lse, up(grad), mask, causal, scale,
-                                          mask_map=mask_map)
-        return dq.to(dtype), dk.to(dtype), dv.to(dtype)
     return taylor_attention_bwd(q, k, v, out, lse, grad, mask, causal, scale, mask_map=mask_map)
 
 

@@ -143,6 +143,9 @@ struct AttnBwdArgs {
 
 template <typename T>
 int launch_attention_bwd(const AttnBwdArgs& a);
+// bfloat16 / float16 operands (16-bit MFMA, fp32 accumulation; lse in float32)
+template <typename T>
+int launch_attention_bwd_half(const AttnBwdArgs& a);
 
 // Workspace of the backward: the rowsum(G O) series ((K+1) bh lq accumulator
 // values), then, when materializing, the P and dS tiles of every order

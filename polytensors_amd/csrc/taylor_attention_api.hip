@@ -107,7 +107,9 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
 size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq, int64_t lk,
                                               int materialize) {
   if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0 || lk < 0) return 0;
-  const size_t size = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);   // accumulator = element type
+  // the rowsum(G O) series in the accumulator type (float64, else float32); the stored tiles (float32
+  // only) in the element type
+  const size_t size = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);
   return pt::attention_bwd_layout(size, size, degree, bh, lq, lk, materialize != 0).total;
 }
 
@@ -127,12 +129,12 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
              "Taylor attention backward: an additive mask needs the boolean mask of its finite entries");
   // The stored-tile path is float32 only: a float64 run of it (degree 8, head dim 64) took a GPU
   // memory fault whose cause is not established, so float64 always recomputes.
-  PT_REQUIRE(!(materialize && dtype == PT_FLOAT64), PT_UNSUPPORTED,
+  PT_REQUIRE(!materialize || dtype == PT_FLOAT32, PT_UNSUPPORTED,
              "Taylor attention backward: materialize is float32 only");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention backward: degree must be in 0..8");
-  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
-             "Taylor attention backward: float32 and float64 only");
+  PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,
+             PT_UNSUPPORTED, "Taylor attention backward: dtype must be float32, float64, bfloat16 or float16");
   PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr && lse != nullptr &&
                  grad != nullptr,
              PT_INVALID_ARGUMENT, "Taylor attention backward: q, k, v, out, lse and grad are required");
@@ -170,7 +172,12 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
   pt::AttnBwdArgs a{degree, q, k, v, out, lse, grad, dq, dk, dv, workspace, bh, lq, lk, d,
                     causal != 0, mask, mask_ranges, scale, materialize != 0, static_cast<hipStream_t>(stream),
                     mask_add, map};
-  return dtype == PT_FLOAT32 ? pt::launch_attention_bwd<float>(a) : pt::launch_attention_bwd<double>(a);
+  switch (dtype) {
+    case PT_FLOAT32: return pt::launch_attention_bwd<float>(a);
+    case PT_FLOAT64: return pt::launch_attention_bwd<double>(a);
+    case PT_BFLOAT16: return pt::launch_attention_bwd_half<pt::bf16>(a);
+    default: return pt::launch_attention_bwd_half<_Float16>(a);
+  }
 }
 
 }  // extern "C"

@@ -1039,6 +1039,8 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
     }
     if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
       const dim3 block(kAttnWaves * kWave);
+      // the fused pass writes both outputs: with one of them not wanted (NULL) that one's pass runs alone
+      const bool both = a.dk != nullptr && a.dv != nullptr;
 #define PT_ATTN_BWD_KV(KERNEL, NS, WHAT, ARGS)                                      \
   do {                                                                              \
     if (a.mask != nullptr) KERNEL<T, K, D, NS, WHAT, true><<<grid, block, 0, a.stream>>> ARGS; \
@@ -1060,10 +1062,15 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
        if constexpr (kCanStore) {
         constexpr int SL = Plan::DB / Plan::NS_KM;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+        bool fused = false;
         if constexpr (Plan::km_fused) {
-          PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 3, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
-          PT_LAUNCH_CHECK();
-        } else {
+          if (both) {
+            PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 3, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
+            PT_LAUNCH_CHECK();
+            fused = true;
+          }
+        }
+        if (!fused) {
           if (a.dv != nullptr) {
             PT_ATTN_BWD_KV(taylor_attention_bwd_kv_mat_kernel, Plan::NS_KM, 1, (q, g, pt_in, dst_in, dk, dv, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale));
             PT_LAUNCH_CHECK();
@@ -1077,10 +1084,15 @@ static int launch_attention_bwd_kd(const AttnBwdArgs& a) {
       } else {
         constexpr int SL = Plan::DB / Plan::NS_KV;
         const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+        bool fused = false;
         if constexpr (Plan::kv_fused) {
-          PT_ATTN_BWD_KV_RECOMPUTE(3);
-          PT_LAUNCH_CHECK();
-        } else {
+          if (both) {
+            PT_ATTN_BWD_KV_RECOMPUTE(3);
+            PT_LAUNCH_CHECK();
+            fused = true;
+          }
+        }
+        if (!fused) {
           if (a.dv != nullptr) {
             PT_ATTN_BWD_KV_RECOMPUTE(1);
             PT_LAUNCH_CHECK();

@@ -1,0 +1,578 @@
+// Flash-style attention backward of degree-K series with bfloat16 / float16
+// operands on the 16x16x32 MFMAs of gfx950 (fp32 accumulation).
+//
+// The series arithmetic is that of taylor_attention_bwd.inl (the VJP of
+// O = softmax(scale Q K^T) V in truncated series arithmetic):
+//   P = exp(scale Q (*) K^T - lse),  dP = G (*) V^T,  Delta = rowsum(G (*) O),
+//   dS = P (*) (dP - Delta),  dQ = scale dS (*) K,  dK = scale dS^T (*) Q,  dV = P^T (*) G,
+// the reference's degree-1 backward for half types
+// (/root/reference/src/polytensors/_attention_kernels.py:85-201: half operands,
+// fp32 accumulation, _fused_attention.py:72-78) at degree K. Only the MFMA
+// operands are 16-bit: Q, K, V and G as stored, and P and dS rounded to the
+// storage type for the products that contract them (from degree 5 as a hi + lo
+// pair, as the forward's probabilities). Scores, dP, the exponential series,
+// dS and every accumulator are fp32; lse and Delta are fp32 series; each
+// gradient is rounded to the storage type once.
+//
+// With v_mfma_f32_16x16x32 (lane l = 16 g + c supplies A row c and B column c,
+// contraction elements 8 g .. 8 g + 7; accumulator register r of lane l is row
+// 4 g + r, column c) both kernels form the scores so that the probability and
+// dS values a lane holds are the B operand of its output product without
+// leaving the lane (as the forward's value product does):
+// * taylor_attention_bwd_q_half_kernel: 64 queries per workgroup (16 per wave),
+//   key blocks of 32 keys with K and V staged row-major in LDS. S^T = K Q^T and
+//   dP^T = V G^T per 16-key half: lane (c, g) holds keys 4 g + r (+ 16) of query
+//   c, whose lse and Delta are per-lane constants. dQ^T += K^T dS^T contracts the
+//   block's 32 keys with lane group g's slots 8 g .. 8 g + 7 standing for keys
+//   4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3; its A operand (K^T) is two
+//   transpose reads (ds_read_b64_tr_b16) of the row-major K tile.
+// * taylor_attention_bwd_kv_half_kernel: 64 keys per workgroup (16 per wave),
+//   query blocks of 32 queries with Q and G (and their lse and Delta series)
+//   staged in LDS. S = Q K^T and dP = G V^T per 16-query half: lane (c, g) holds
+//   queries 4 g + r (+ 16) of key c. dV^T += G^T P and dK^T += Q^T dS take their
+//   A operands (G^T, Q^T) from transpose reads of the row-major tiles.
+// Output accumulators beyond a register budget are split into head-dim slices
+// (a grid dimension; each slice recomputes its scores), and dK and dV get one
+// pass each when both do not fit. Deterministic (no atomics).
+#pragma once
+
+#include "half_mfma.h"
+#include "taylor_attention_bwd.inl"
+#include "taylor_attention_half.inl"
+
+namespace pt {
+
+template <int K, int D>
+struct AttnHalfBwdShape {
+  static constexpr int KB = 32;              // keys (dQ kernel) or queries (dK/dV kernel) per block
+  static constexpr int DC = (D + 31) / 32;   // 32-wide head-dim chunks of the score contractions
+  static constexpr int DB = D / 16;          // 16-wide output blocks
+  static constexpr int LD = D + 8;           // tile row: 16-byte aligned, 4 banks of skew per row
+  static constexpr size_t LDS = 2ull * (K + 1) * KB * LD * 2 + 2ull * (K + 1) * KB * 4;
+  static constexpr bool fits = LDS <= 160 * 1024;
+  static constexpr bool split = K >= 5;      // P and dS orders 1..K as hi + lo operand pairs
+  // output accumulator registers per lane: the score and dP series, the 16-bit operands and, from
+  // degree 5, the lo operands take the rest
+  static constexpr int kBudget = K >= 5 ? 96 : 160;
+  static constexpr int slices(int outputs) {
+    int sl = 1;
+    while (sl < DB && outputs * (K + 1) * (DB / sl) * 4 > kBudget) sl *= 2;
+    return sl;
+  }
+  static constexpr int SL_Q = slices(1);
+  static constexpr bool kv_fused = 2 * (K + 1) * DB * 4 <= kBudget;   // dK and dV in one pass
+  static constexpr int SL_KV = slices(kv_fused ? 2 : 1);
+};
+
+// ROWS rows from row `first` (zero from row `limit` on, limit >= 1) of the K+1
+// orders of a [*, D] 16-bit series at row_base into an LDS tile [K+1][ROWS][LD].
+// Every lane issues all of its 16-byte loads (clamped rows, no branch) before
+// its stores.
+template <typename T, int K, int D, int ROWS, int LD>
+__device__ __forceinline__ void attn_half_stage(T (&tile)[K + 1][ROWS][LD], const CPtrs<T>& src,
+                                                int64_t row_base, int first, int limit) {
+  constexpr int VPR = D / 8;   // 16-byte vectors per row
+  constexpr int N = (K + 1) * ROWS * VPR;
+  constexpr int THREADS = kAttnWaves * kWave;
+  constexpr int IT = (N + THREADS - 1) / THREADS;
+  u32x4 v[IT];
+#pragma unroll
+  for (int j = 0; j < IT; ++j) {
+    const int e = min(static_cast<int>(threadIdx.x) + THREADS * j, N - 1);
+    const int o = e / (ROWS * VPR), rem = e % (ROWS * VPR);
+    const int row = first + rem / VPR, cv = (rem % VPR) * 8;
+    v[j] = *reinterpret_cast<const u32x4*>(order_ptr<K>(src, o) + (row_base + min(row, limit - 1)) * D + cv);
+  }
+#pragma unroll
+  for (int j = 0; j < IT; ++j) {
+    const int idx = static_cast<int>(threadIdx.x) + THREADS * j;
+    if (N % THREADS == 0 || idx < N) {
+      const int o = idx / (ROWS * VPR), rem = idx % (ROWS * VPR);
+      const int r = rem / VPR, cv = (rem % VPR) * 8;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&tile[o][r][cv]) = first + r < limit ? v[j] : z;
+    }
+  }
+}
+
+// Packs the series w[o][0..3] of one 16-row half into slots 4 h .. 4 h + 3 of the
+// 16-bit operands hi[o] (and, when split, the rounding residuals of orders
+// 1..K into lo[o]).
+template <typename T, int K, bool SPLIT, int NLO>
+__device__ __forceinline__ void attn_half_pack(const float (&w)[K + 1][4], int h, u32x4 (&hi)[K + 1],
+                                               u32x4 (&lo)[NLO]) {
+  using MM = HalfMfma<T>;
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    const uint32_t w01 = MM::pack2(w[o][0], w[o][1]), w23 = MM::pack2(w[o][2], w[o][3]);
+    hi[o][2 * h] = w01;
+    hi[o][2 * h + 1] = w23;
+    if constexpr (SPLIT) {
+      if (o >= 1) {
+        lo[o][2 * h] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
+        lo[o][2 * h + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
+      }
+    }
+  }
+}
+
+// acc[k] += sum_{a+b=k} X_b^T W_a for one 16-wide output block: xt[b] the A operands, W the
+// packed B operands (hi, and lo for orders 1..K when split).
+template <typename T, int K, bool SPLIT, int NLO>
+__device__ __forceinline__ void attn_half_series_mma(floatx4 (&acc)[K + 1], const u32x4 (&xt)[K + 1],
+                                                     const u32x4 (&hi)[K + 1], const u32x4 (&lo)[NLO]) {
+  using MM = HalfMfma<T>;
+#pragma unroll
+  for (int k = 0; k <= K; ++k) {
+#pragma unroll
+    for (int a = 0; a <= k; ++a) acc[k] = MM::mma(xt[k - a], hi[a], acc[k]);
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int a = 1; a <= k; ++a) acc[k] = MM::mma(xt[k - a], lo[a], acc[k]);
+    }
+  }
+}
+
+// Stores the accumulators acc[db][k] of one 16-row output tile: head dims d0 + 16 db + 4 g .. + 3
+// of row `row` (8 bytes per order and block), times factor.
+template <typename T, int K, int NB>
+__device__ __forceinline__ void attn_half_store(const floatx4 (&acc)[NB][K + 1], MPtrs<T>& out, int64_t row,
+                                                int d0, int g, float factor) {
+  using MM = HalfMfma<T>;
+#pragma unroll
+  for (int db = 0; db < NB; ++db)
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+      *reinterpret_cast<uint2*>(out.p[k] + row + d0 + 16 * db + 4 * g) =
+          make_uint2(MM::pack2(acc[db][k][0] * factor, acc[db][k][1] * factor),
+                     MM::pack2(acc[db][k][2] * factor, acc[db][k][3] * factor));
+}
+
+// MASK: 0 no mask, 1 a boolean mask, 2 a boolean mask and the additive mask madd (float) whose
+// finite entries it marks.
+template <typename T, int K, int D, int SL, int MASK>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_half_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ, int L,
+    int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const float* __restrict__ madd_all,
+    const int32_t* __restrict__ ranges_all, int causal, float scale) {
+  using Sh = AttnHalfBwdShape<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = Sh::KB, DC = Sh::DC, LD = Sh::LD;
+  constexpr int DS = D / SL, DBS = DS / 16;
+  constexpr bool SPLIT = Sh::split;
+  constexpr int NLO = SPLIT ? K + 1 : 1;
+  static_assert(Sh::fits, "K/V tiles exceed LDS");
+  __shared__ __align__(16) T Ks[K + 1][KB][LD];
+  __shared__ __align__(16) T Vs[K + 1][KB][LD];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;   // query column of the score accumulators; A row of the operands
+  const int g = lane / 16;   // lane group
+  const int nqb = (L + kAttnBM - 1) / kAttnBM;
+  const int64_t bh = gridDim.x / (static_cast<int64_t>(nqb) * SL);
+  int64_t head;
+  int slice, q_block;
+  attn_bwd_q_item(blockIdx.x, bh, nqb, SL, head, slice, q_block);
+  const int d0 = slice * DS;
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = MASK != 0 ? mask_all + mask_index * L * S : nullptr;
+  const float* madd = MASK == 2 ? madd_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
+  float lse[K + 1], delta[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lse[o] = q_ok ? LSE.p[o][head * L + my_q] : 0.f;
+    delta[o] = q_ok ? DELTA.p[o][head * L + my_q] : 0.f;
+  }
+  // operand of the lane's query row, order o, chunk dc: X[my_q][32 dc + 8 g .. + 7] (zero past D)
+  auto load_row = [&](const CPtrs<T>& X, int o, int dc) -> u32x4 {
+    const bool din = 32 * dc + 8 * g < D;
+    return attn_half_load8<T>(X.p[o] + qrow + (din ? 32 * dc + 8 * g : 0), din);
+  };
+
+  floatx4 acc[DBS][K + 1];   // dQ^T series of each 16-wide head-dim block
+#pragma unroll
+  for (int db = 0; db < DBS; ++db)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) acc[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // key range: causal and mask-range bounds, lo rounded down to a 32-key block
+  int lo = 0, hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / KB * KB;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+  }
+  const int tj = c / 4, ta = c % 4;   // transpose reads: this lane addresses row 4 g + tj (+ 16), dims + 4 ta
+
+  for (int kb0 = lo; kb0 < hi; kb0 += KB) {
+    uint8_t mbyte[2][4];
+    float add[2][4];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        mbyte[kh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], my_q, key, L, S) : uint8_t(1);
+        add[kh][r] = MASK == 2 ? attn_mask_add(madd, my_q, key, L, S) : 0.f;
+      }
+    __syncthreads();   // the previous block's products are done with the tiles
+    attn_half_stage<T, K, D, KB, LD>(Ks, Kp, head * S, kb0, S);
+    attn_half_stage<T, K, D, KB, LD>(Vs, Vp, head * S, kb0, S);
+    __syncthreads();
+
+    // ---- S^T_k = sum_{a+b=k} K_b Q_a^T and dP^T_k = sum_{a+b=k} V_b G_a^T (keys x queries) ----
+    // (one contraction after the other: their operands are not live together)
+    floatx4 sc[2][K + 1], dp[2][K + 1];
+    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, const T (&tile)[K + 1][KB][LD]) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int o = 0; o <= K; ++o) acc[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        u32x4 xa[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) xa[o] = load_row(X, o, dc);
+        const bool din = 32 * dc + 8 * g < D;
+        const int col = din ? 32 * dc + 8 * g : 0;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          u32x4 top[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) {
+            const u32x4 t = *reinterpret_cast<const u32x4*>(&tile[o][16 * kh + c][col]);
+            top[o] = din ? t : z;
+          }
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc[kh][k] = MM::mma(top[k - a], xa[a], acc[kh][k]);
+        }
+      }
+    };
+    contract(sc, Q, Ks);
+    contract(dp, G, Vs);
+
+    // ---- probability and dS series; dS^T as the B operand (slots 4 kh + r: key 16 kh + 4 g + r) ----
+    u32x4 dsb[K + 1], dsl[NLO];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      float w[K + 1][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        bool ok = q_ok && key < S;
+        if (causal) ok = ok && key <= my_q;
+        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        float p[K + 1], ds[K + 1];
+        attn_prob_series<float, K>(sc[kh], r, lse, ok, scale, add[kh][r], p);
+        attn_ds_series<float, K>(p, dp[kh], r, delta, ds);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) w[o][r] = ds[o];
+      }
+      attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
+    }
+
+    // ---- dQ^T_k += sum_{a+b=k} K_b^T dS^T_a (head dim x queries), 32 keys per MFMA ----
+#pragma unroll
+    for (int db = 0; db < DBS; ++db) {
+      u32x4 kt[K + 1];
+      const int col = d0 + 16 * db + 4 * ta;
+#pragma unroll
+      for (int o = 0; o <= K; ++o) kt[o] = lds_read_tr16x2(&Ks[o][4 * g + tj][col], &Ks[o][16 + 4 * g + tj][col]);
+      attn_half_series_mma<T, K, SPLIT, NLO>(acc[db], kt, dsb, dsl);
+    }
+  }
+
+  if (q_ok) attn_half_store<T, K, DBS>(acc, DQ, (head * L + my_q) * D, d0, g, scale);
+}
+
+// WHAT: 1 = dV, 2 = dK, 3 = both. MASK as the dQ kernel's.
+template <typename T, int K, int D, int SL, int WHAT, int MASK>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_half_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DK,
+    MPtrs<T> DV, int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap,
+    const float* __restrict__ madd_all, const int32_t* __restrict__ ranges_all, int causal, float scale) {
+  using Sh = AttnHalfBwdShape<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = Sh::KB, DC = Sh::DC, LD = Sh::LD;
+  constexpr int DS = D / SL, DBS = DS / 16;
+  constexpr bool SPLIT = Sh::split;
+  constexpr int NLO = SPLIT ? K + 1 : 1;
+  constexpr bool DO_V = (WHAT & 1) != 0, DO_K = (WHAT & 2) != 0;
+  static_assert(Sh::fits, "Q/G tiles exceed LDS");
+  __shared__ __align__(16) T Qs[K + 1][KB][LD];
+  __shared__ __align__(16) T Gs[K + 1][KB][LD];
+  __shared__ __align__(16) float Ls[K + 1][KB];
+  __shared__ __align__(16) float Ds[K + 1][KB];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % 16;   // key column of the score accumulators; A row of the operands
+  const int g = lane / 16;
+  const int64_t bh = gridDim.x / (static_cast<int64_t>((S + 63) / 64) * SL);
+  int64_t head;
+  int slice, kv_block;
+  attn_bwd_kv_item(blockIdx.x, bh, SL, head, slice, kv_block);
+  const int d0 = slice * DS;
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = MASK != 0 ? mask_all + mask_index * L * S : nullptr;
+  const float* madd = MASK == 2 ? madd_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const int my_k = kv_block + wave * 16 + c;
+  const bool k_ok = my_k < S;
+  const int64_t krow = (head * S + (k_ok ? my_k : S - 1)) * D;
+  auto load_row = [&](const CPtrs<T>& X, int o, int dc) -> u32x4 {
+    const bool din = 32 * dc + 8 * g < D;
+    return attn_half_load8<T>(X.p[o] + krow + (din ? 32 * dc + 8 * g : 0), din);
+  };
+
+  floatx4 acc_v[DO_V ? DBS : 1][K + 1], acc_k[DO_K ? DBS : 1][K + 1];
+#pragma unroll
+  for (int db = 0; db < DBS; ++db)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) acc_v[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (DO_K) acc_k[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  int lo, hi;
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
+  lo = lo / KB * KB;
+  const int tj = c / 4, ta = c % 4;
+
+  for (int qb0 = lo; qb0 < hi; qb0 += KB) {
+    uint8_t mbyte[2][4];
+    float add[2][4];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = qb0 + 16 * qh + 4 * g + r;
+        mbyte[qh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], q, my_k, L, S) : uint8_t(1);
+        add[qh][r] = MASK == 2 ? attn_mask_add(madd, q, my_k, L, S) : 0.f;
+      }
+    __syncthreads();   // the previous block's products are done with the tiles
+    attn_half_stage<T, K, D, KB, LD>(Qs, Q, head * L, qb0, L);
+    attn_half_stage<T, K, D, KB, LD>(Gs, G, head * L, qb0, L);
+    for (int idx = threadIdx.x; idx < (K + 1) * KB; idx += kAttnWaves * kWave) {
+      const int o = idx / KB, i = idx % KB, q = qb0 + i;
+      const int64_t at = head * L + min(q, L - 1);
+      const float l = order_ptr<K>(LSE, o)[at], dl = order_ptr<K>(DELTA, o)[at];
+      Ls[o][i] = q < L ? l : 0.f;
+      Ds[o][i] = q < L ? dl : 0.f;
+    }
+    __syncthreads();
+
+    // ---- S_k = sum_{a+b=k} Q_a K_b^T and dP_k = sum_{a+b=k} G_a V_b^T (queries x keys) ----
+    // (one contraction after the other: their operands are not live together)
+    floatx4 sc[2][K + 1], dp[DO_K ? 2 : 1][K + 1];
+    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, const T (&tile)[K + 1][KB][LD]) {
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+        for (int o = 0; o <= K; ++o) acc[qh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        u32x4 xb[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) xb[o] = load_row(X, o, dc);
+        const bool din = 32 * dc + 8 * g < D;
+        const int col = din ? 32 * dc + 8 * g : 0;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          u32x4 ta_[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) {
+            const u32x4 t = *reinterpret_cast<const u32x4*>(&tile[o][16 * qh + c][col]);
+            ta_[o] = din ? t : z;
+          }
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) acc[qh][k] = MM::mma(ta_[a], xb[k - a], acc[qh][k]);
+        }
+      }
+    };
+    contract(sc, Kp, Qs);
+    if constexpr (DO_K) contract(dp, Vp, Gs);
+
+    // ---- P and dS series as B operands (slots 4 qh + r: query 16 qh + 4 g + r) ----
+    u32x4 pb[K + 1], pl[NLO], dsb[K + 1], dsl[NLO];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+      float wp[K + 1][4], wd[K + 1][4];
+      floatx4 l4[K + 1], d4[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        l4[o] = *reinterpret_cast<const floatx4*>(&Ls[o][16 * qh + 4 * g]);
+        if constexpr (DO_K) d4[o] = *reinterpret_cast<const floatx4*>(&Ds[o][16 * qh + 4 * g]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = qb0 + 16 * qh + 4 * g + r;
+        bool ok = k_ok && q < L;
+        if (causal) ok = ok && my_k <= q;
+        if constexpr (MASK != 0) ok = ok && mbyte[qh][r] != 0;
+        float lse[K + 1], p[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) lse[o] = l4[o][r];
+        attn_prob_series<float, K>(sc[qh], r, lse, ok, scale, add[qh][r], p);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) wp[o][r] = p[o];
+        if constexpr (DO_K) {
+          float delta[K + 1], ds[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) delta[o] = d4[o][r];
+          attn_ds_series<float, K>(p, dp[qh], r, delta, ds);
+#pragma unroll
+          for (int o = 0; o <= K; ++o) wd[o][r] = ds[o];
+        }
+      }
+      if constexpr (DO_V) attn_half_pack<T, K, SPLIT, NLO>(wp, qh, pb, pl);
+      if constexpr (DO_K) attn_half_pack<T, K, SPLIT, NLO>(wd, qh, dsb, dsl);
+    }
+
+    // ---- dV^T_k += sum_{a+b=k} G_b^T P_a and dK^T_k += sum_{a+b=k} Q_b^T dS_a, 32 queries per MFMA ----
+#pragma unroll
+    for (int db = 0; db < DBS; ++db) {
+      const int col = d0 + 16 * db + 4 * ta;
+      if constexpr (DO_V) {
+        u32x4 gt[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) gt[o] = lds_read_tr16x2(&Gs[o][4 * g + tj][col], &Gs[o][16 + 4 * g + tj][col]);
+        attn_half_series_mma<T, K, SPLIT, NLO>(acc_v[db], gt, pb, pl);
+      }
+      if constexpr (DO_K) {
+        u32x4 qt[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) qt[o] = lds_read_tr16x2(&Qs[o][4 * g + tj][col], &Qs[o][16 + 4 * g + tj][col]);
+        attn_half_series_mma<T, K, SPLIT, NLO>(acc_k[db], qt, dsb, dsl);
+      }
+    }
+  }
+
+  if (!k_ok) return;
+  const int64_t row = (head * S + my_k) * D;
+  if constexpr (DO_V) attn_half_store<T, K, DBS>(acc_v, DV, row, d0, g, 1.f);
+  if constexpr (DO_K) attn_half_store<T, K, DBS>(acc_k, DK, row, d0, g, scale);
+}
+
+template <typename T, int K, int D>
+static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
+  using Sh = AttnHalfBwdShape<K, D>;
+  static_assert(Sh::fits, "every 16-bit backward shape fits LDS");
+  CPtrs<T> q{}, k{}, v{}, o{}, g{};
+  CPtrs<float> lse{}, delta_in{};
+  MPtrs<float> delta{};
+  MPtrs<T> dq{}, dk{}, dv{};
+  const int64_t rows = a.bh * a.lq;
+  for (int i = 0; i <= K; ++i) {
+    q.p[i] = static_cast<const T*>(a.q[i]);
+    k.p[i] = static_cast<const T*>(a.k[i]);
+    v.p[i] = static_cast<const T*>(a.v[i]);
+    o.p[i] = static_cast<const T*>(a.out[i]);
+    g.p[i] = static_cast<const T*>(a.grad[i]);
+    lse.p[i] = static_cast<const float*>(a.lse[i]);
+    delta.p[i] = static_cast<float*>(a.workspace) + i * rows;
+    delta_in.p[i] = delta.p[i];
+    if (a.dq != nullptr) dq.p[i] = static_cast<T*>(a.dq[i]);
+    if (a.dk != nullptr) dk.p[i] = static_cast<T*>(a.dk[i]);
+    if (a.dv != nullptr) dv.p[i] = static_cast<T*>(a.dv[i]);
+  }
+  const int L = static_cast<int>(a.lq), S = static_cast<int>(a.lk);
+  const float scale = static_cast<float>(a.scale);
+  const int causal = a.causal ? 1 : 0;
+  const float* madd = static_cast<const float*>(a.mask_add);
+  const int mask_kind = madd != nullptr ? 2 : a.mask != nullptr ? 1 : 0;
+  const dim3 block(kAttnWaves * kWave);
+  if (rows > 0 && (a.dq != nullptr || ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0))) {
+    attn_bwd_delta_kernel<T, K, D><<<dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0, a.stream>>>(
+        g, o, delta, rows);
+    PT_LAUNCH_CHECK();
+  }
+  if (a.dq != nullptr && rows > 0) {
+    constexpr int SL = Sh::SL_Q;
+    const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
+#define PT_ATTN_BWD_Q_HALF(MASK)                                                                             \
+  taylor_attention_bwd_q_half_kernel<T, K, D, SL, MASK><<<grid, block, 0, a.stream>>>(                       \
+      q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale)
+    if (mask_kind == 2) PT_ATTN_BWD_Q_HALF(2);
+    else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF(1);
+    else PT_ATTN_BWD_Q_HALF(0);
+#undef PT_ATTN_BWD_Q_HALF
+    PT_LAUNCH_CHECK();
+  }
+  if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
+    constexpr int SL = Sh::SL_KV;
+    const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
+#define PT_ATTN_BWD_KV_HALF(WHAT)                                                                           \
+  do {                                                                                                       \
+    if (mask_kind == 2)                                                                                      \
+      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 2><<<grid, block, 0, a.stream>>>(               \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
+    else if (mask_kind == 1)                                                                                 \
+      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 1><<<grid, block, 0, a.stream>>>(               \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
+    else                                                                                                     \
+      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 0><<<grid, block, 0, a.stream>>>(               \
+          q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
+    PT_LAUNCH_CHECK();                                                                                       \
+  } while (0)
+    // the fused pass writes both outputs: with one of them not wanted (NULL) that one's pass runs alone
+    bool fused = false;
+    if constexpr (Sh::kv_fused) {
+      if (a.dk != nullptr && a.dv != nullptr) {
+        PT_ATTN_BWD_KV_HALF(3);
+        fused = true;
+      }
+    }
+    if (!fused) {
+      if (a.dv != nullptr) PT_ATTN_BWD_KV_HALF(1);
+      if (a.dk != nullptr) PT_ATTN_BWD_KV_HALF(2);
+    }
+#undef PT_ATTN_BWD_KV_HALF
+  }
+  return PT_OK;
+}
+
+template <typename T, int K>
+static int launch_attention_bwd_half_k(const AttnBwdArgs& a) {
+  switch (a.d) {
+    case 16: return launch_attention_bwd_half_kd<T, K, 16>(a);
+    case 32: return launch_attention_bwd_half_kd<T, K, 32>(a);
+    case 64: return launch_attention_bwd_half_kd<T, K, 64>(a);
+    case 128: return launch_attention_bwd_half_kd<T, K, 128>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention backward: head dim must be 16, 32, 64 or 128");
+  return PT_UNSUPPORTED;
+}
+
+template <typename T>
+int launch_attention_bwd_half(const AttnBwdArgs& a) {
+  switch (a.degree) {
+    case 0: return launch_attention_bwd_half_k<T, 0>(a);
+    case 1: return launch_attention_bwd_half_k<T, 1>(a);
+    case 2: return launch_attention_bwd_half_k<T, 2>(a);
+    case 3: return launch_attention_bwd_half_k<T, 3>(a);
+    case 4: return launch_attention_bwd_half_k<T, 4>(a);
+    case 5: return launch_attention_bwd_half_k<T, 5>(a);
+    case 6: return launch_attention_bwd_half_k<T, 6>(a);
+    case 7: return launch_attention_bwd_half_k<T, 7>(a);
+    case 8: return launch_attention_bwd_half_k<T, 8>(a);
+    default: break;
+  }
+  pt_host::set_error("Taylor attention backward: degree outside 0..PT_MAX_DEGREE");
+  return PT_UNSUPPORTED;
+}
+
+}  // namespace pt

@@ -439,7 +439,7 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
     TORCH_CHECK_VALUE((*s)[0].dim() == 3, "taylor_attention_bwd: ", name, " must be [bh, length, d]");
   }
   const at::ScalarType dtype = q[0].scalar_type();
-  TORCH_CHECK_VALUE(dtype == at::kFloat || dtype == at::kDouble, "taylor_attention_bwd: float32 or float64 only");
+  TORCH_CHECK_VALUE(has_code(dtype), "taylor_attention_bwd: float32, float64, bfloat16 or float16 only");
   const int64_t bh = q[0].size(0), lq = q[0].size(1), d = q[0].size(2);
   TORCH_CHECK_VALUE(k[0].sizes() == v[0].sizes() && k[0].size(0) == bh && k[0].size(2) == d,
                     "taylor_attention_bwd: key/value shapes must be [bh, S, d] matching the query");
