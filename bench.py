@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload attention|attention_dense|attention_bf16|attention_window|attention_bwd|
-                                attention_bwd_window|matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
+                                attention_bwd_bf16|attention_bwd_window|matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
@@ -203,6 +203,39 @@ def wl_attention_bwd(device):
                 bytes=nbytes, kernel="taylor_attention_bwd", dtype="fp32",
                 workload=f"taylor_attention_bwd B={B} H={H} L={L} d={d} K={K} fp32 causal line inputs",
                 cpu=lambda: cpu_attention_bwd(L, d, K))
+
+
+def wl_attention_bwd_bf16(device):
+    """``attention_bwd`` (config 3's shape, K=4, causal, line inputs, cotangent series G_k ~ N(0,1) 0.5^k)
+    with every operand stored in bfloat16: the 16-bit backward kernels (bf16 MFMA operands, fp32
+    accumulation, lse and Delta in fp32). Work is the same five-product count; the roofline is the
+    bf16 MFMA peak."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(8, device)
+
+    def line():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [x.to(torch.bfloat16) for x in [base, direction] + [torch.zeros_like(base) for _ in range(2, K + 1)]]
+
+    q, k, v = line(), line(), line()
+    cot = [(torch.randn(B * H, L, d, generator=g, device=device) * 0.5 ** o).to(torch.bfloat16) for o in range(K + 1)]
+    scale = 1 / math.sqrt(d)
+    out, lse = _ops.taylor_attention_fwd(q, k, v, None, True, scale, K)
+
+    def step():
+        return _ops.attention_gradient_series(q, k, v, out, lse, cot, None, True, scale)
+
+    pairs = (K + 1) * (K + 2) // 2
+    flops = 5 * pairs * 2 * d * B * H * L * (L + 1) / 2
+    nbytes = 8 * (K + 1) * B * H * L * d * 2               # q, k, v, out, G read; dq, dk, dv written
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_MFMA,
+                bytes=nbytes, kernel="taylor_attention_bwd_bf16", dtype="bf16 (fp32 accumulate)",
+                workload=f"taylor_attention_bwd B={B} H={H} L={L} d={d} K={K} bf16 causal line inputs",
+                cpu=lambda: cpu_attention_bwd(L, d, K, heads=2, dtype="bf16"))
 
 
 def wl_attention_bwd_window(device):
@@ -486,7 +519,8 @@ def wl_ce_bwd(device):
 WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "matmul_bf16": wl_matmul_bf16, "norm": wl_norm,
              "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
-             "attention_bwd": wl_attention_bwd, "attention_window": wl_attention_window,
+             "attention_bwd": wl_attention_bwd, "attention_bwd_bf16": wl_attention_bwd_bf16,
+             "attention_window": wl_attention_window,
              "attention_bwd_window": wl_attention_bwd_window,
              "attention_dense": wl_attention_dense, "attention_bf16": wl_attention_bf16, "config1": wl_config1,
              "decoder": wl_decoder}
@@ -545,12 +579,14 @@ def cpu_attention_window(L, d, K, W, heads=16):
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 window {W}", seconds=t)
 
 
-def cpu_attention_bwd(L, d, K, heads=16, window=None):
+def cpu_attention_bwd(L, d, K, heads=16, window=None, dtype=None):
     import torch
     import oracle
 
     g = torch.Generator().manual_seed(8)
     q, k, v, cot = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(4))
+    if dtype == "bf16":   # the reference's general path on bf16 coefficients (torch's CPU bf16 ops)
+        q, k, v, cot = ([c.to(torch.bfloat16) for c in s] for s in (q, k, v, cot))
     mask = None
     if window is not None:
         i = torch.arange(L)
@@ -565,7 +601,8 @@ def cpu_attention_bwd(L, d, K, heads=16, window=None):
     flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * pairs
     what = "causal" if window is None else f"window {window}"
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
-                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 {what}", seconds=t)
+                sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} {dtype or 'fp32'} {what}",
+                seconds=t)
 
 
 def cpu_decoder(layers, d, heads, vocab, K, seq=64):

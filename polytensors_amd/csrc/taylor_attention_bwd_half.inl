@@ -62,6 +62,21 @@ struct AttnHalfBwdShape {
   static constexpr int SL_Q = slices(1);
   static constexpr bool kv_fused = 2 * (K + 1) * DB * 4 <= kBudget;   // dK and dV in one pass
   static constexpr int SL_KV = slices(kv_fused ? 2 : 1);
+  // How many of `ops` row tiles of the lane (every order, the whole head dim) stay in registers
+  // beside `outputs` accumulator series of nb 16-wide blocks and the working set: scores, dP and
+  // the series (about 30 (K+1) registers), the lo operands of `packed` split series and the mask
+  // values. The bound of 410 keeps every instantiation free of scratch spills (the compiler's
+  // resource remarks).
+  static constexpr int resident(int ops, int outputs, int nb, int packed, bool masked) {
+    const int fixed = outputs * (K + 1) * nb * 4 + 30 * (K + 1) + (split ? packed * 4 * (K + 1) : 0) +
+                      (masked ? 16 : 0);
+    int n = ops;
+    while (n > 0 && n * (K + 1) * DC * 4 + fixed > 410) --n;
+    return n;
+  }
+  // operands not resident are read one 32-wide chunk ahead through a two-slot ring, except at
+  // degree 8 and head dim 128, where the ring's registers make the kernels spill
+  static constexpr bool ring = !(K >= 8 && D == 128);
 };
 
 // ROWS rows from row `first` (zero from row `limit` on, limit >= 1) of the K+1
@@ -193,6 +208,17 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     const bool din = 32 * dc + 8 * g < D;
     return attn_half_load8<T>(X.p[o] + qrow + (din ? 32 * dc + 8 * g : 0), din);
   };
+  // The lane's Q and G rows are the same for every key block: resident in registers when they fit
+  // beside the accumulators and the score series, else read (from L2) per block.
+  constexpr int NRES = Sh::resident(2, 1, DBS, 1, MASK != 0);   // Q, then G
+  u32x4 rows[NRES > 0 ? NRES : 1][K + 1][DC];
+#pragma unroll
+  for (int i = 0; i < NRES; ++i)
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) rows[i][o][dc] = load_row(i == 0 ? Q : G, o, dc);
+  u32x4 ring[2][2][K + 1];   // chunk ring of each operand not resident
 
   floatx4 acc[DBS][K + 1];   // dQ^T series of each 16-wide head-dim block
 #pragma unroll
@@ -221,6 +247,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         mbyte[kh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], my_q, key, L, S) : uint8_t(1);
         add[kh][r] = MASK == 2 ? attn_mask_add(madd, my_q, key, L, S) : 0.f;
       }
+    // chunk 0 of the operands not resident, in flight during the staging
+#pragma unroll
+    for (int i = NRES; i < 2; ++i)
+#pragma unroll
+      for (int o = 0; o <= K; ++o)
+        if constexpr (Sh::ring) ring[i][0][o] = load_row(i == 0 ? Q : G, o, 0);
     __syncthreads();   // the previous block's products are done with the tiles
     attn_half_stage<T, K, D, KB, LD>(Ks, Kp, head * S, kb0, S);
     attn_half_stage<T, K, D, KB, LD>(Vs, Vp, head * S, kb0, S);
@@ -229,16 +261,23 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     // ---- S^T_k = sum_{a+b=k} K_b Q_a^T and dP^T_k = sum_{a+b=k} V_b G_a^T (keys x queries) ----
     // (one contraction after the other: their operands are not live together)
     floatx4 sc[2][K + 1], dp[2][K + 1];
-    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, const T (&tile)[K + 1][KB][LD]) {
+    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, int which, const T (&tile)[K + 1][KB][LD]) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int o = 0; o <= K; ++o) acc[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
+        // resident rows, or the ring: chunk dc + 1 is loaded while chunk dc's products run
         u32x4 xa[K + 1];
+        if (Sh::ring && which >= NRES && dc + 1 < DC) {
 #pragma unroll
-        for (int o = 0; o <= K; ++o) xa[o] = load_row(X, o, dc);
+          for (int o = 0; o <= K; ++o) ring[which][(dc + 1) & 1][o] = load_row(X, o, dc + 1);
+        }
+#pragma unroll
+        for (int o = 0; o <= K; ++o)
+          xa[o] = which < NRES ? rows[which < NRES ? which : 0][o][dc]
+                               : (Sh::ring ? ring[which][dc & 1][o] : load_row(X, o, dc));
         const bool din = 32 * dc + 8 * g < D;
         const int col = din ? 32 * dc + 8 * g : 0;
         const u32x4 z = {0u, 0u, 0u, 0u};
@@ -257,8 +296,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         }
       }
     };
-    contract(sc, Q, Ks);
-    contract(dp, G, Vs);
+    contract(sc, Q, 0, Ks);
+    contract(dp, G, 1, Vs);
 
     // ---- probability and dS series; dS^T as the B operand (slots 4 kh + r: key 16 kh + 4 g + r) ----
     u32x4 dsb[K + 1], dsl[NLO];
@@ -333,6 +372,18 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
     const bool din = 32 * dc + 8 * g < D;
     return attn_half_load8<T>(X.p[o] + krow + (din ? 32 * dc + 8 * g : 0), din);
   };
+  // The lane's K (and, for dK, V) rows are the same for every query block: resident in registers
+  // when they fit, else read (from L2) per block.
+  constexpr int NRES = Sh::resident(DO_K ? 2 : 1, (DO_K ? 1 : 0) + (DO_V ? 1 : 0), DBS,
+                                    (DO_K ? 1 : 0) + (DO_V ? 1 : 0), MASK != 0);   // K, then V
+  u32x4 rows[NRES > 0 ? NRES : 1][K + 1][DC];
+#pragma unroll
+  for (int i = 0; i < NRES; ++i)
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) rows[i][o][dc] = load_row(i == 0 ? Kp : Vp, o, dc);
+  u32x4 ring[2][2][K + 1];   // chunk ring of each operand not resident
 
   floatx4 acc_v[DO_V ? DBS : 1][K + 1], acc_k[DO_K ? DBS : 1][K + 1];
 #pragma unroll
@@ -359,6 +410,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
         mbyte[qh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], q, my_k, L, S) : uint8_t(1);
         add[qh][r] = MASK == 2 ? attn_mask_add(madd, q, my_k, L, S) : 0.f;
       }
+    // chunk 0 of the operands not resident, in flight during the staging
+#pragma unroll
+    for (int i = NRES; i < (DO_K ? 2 : 1); ++i)
+#pragma unroll
+      for (int o = 0; o <= K; ++o)
+        if constexpr (Sh::ring) ring[i][0][o] = load_row(i == 0 ? Kp : Vp, o, 0);
     __syncthreads();   // the previous block's products are done with the tiles
     attn_half_stage<T, K, D, KB, LD>(Qs, Q, head * L, qb0, L);
     attn_half_stage<T, K, D, KB, LD>(Gs, G, head * L, qb0, L);
@@ -374,16 +431,23 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
     // ---- S_k = sum_{a+b=k} Q_a K_b^T and dP_k = sum_{a+b=k} G_a V_b^T (queries x keys) ----
     // (one contraction after the other: their operands are not live together)
     floatx4 sc[2][K + 1], dp[DO_K ? 2 : 1][K + 1];
-    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, const T (&tile)[K + 1][KB][LD]) {
+    auto contract = [&](floatx4 (&acc)[2][K + 1], const CPtrs<T>& X, int which, const T (&tile)[K + 1][KB][LD]) {
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
         for (int o = 0; o <= K; ++o) acc[qh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
+        // resident rows, or the ring: chunk dc + 1 is loaded while chunk dc's products run
         u32x4 xb[K + 1];
+        if (Sh::ring && which >= NRES && dc + 1 < DC) {
 #pragma unroll
-        for (int o = 0; o <= K; ++o) xb[o] = load_row(X, o, dc);
+          for (int o = 0; o <= K; ++o) ring[which][(dc + 1) & 1][o] = load_row(X, o, dc + 1);
+        }
+#pragma unroll
+        for (int o = 0; o <= K; ++o)
+          xb[o] = which < NRES ? rows[which < NRES ? which : 0][o][dc]
+                               : (Sh::ring ? ring[which][dc & 1][o] : load_row(X, o, dc));
         const bool din = 32 * dc + 8 * g < D;
         const int col = din ? 32 * dc + 8 * g : 0;
         const u32x4 z = {0u, 0u, 0u, 0u};
@@ -402,8 +466,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
         }
       }
     };
-    contract(sc, Kp, Qs);
-    if constexpr (DO_K) contract(dp, Vp, Gs);
+    contract(sc, Kp, 0, Qs);
+    if constexpr (DO_K) contract(dp, Vp, 1, Gs);
 
     // ---- P and dS series as B operands (slots 4 qh + r: query 16 qh + 4 g + r) ----
     u32x4 pb[K + 1], pl[NLO], dsb[K + 1], dsl[NLO];
