@@ -333,6 +333,236 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   if (q_ok) attn_half_store<T, K, DBS>(acc, DQ, (head * L + my_q) * D, d0, g, scale);
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined dQ kernel: the K and V tiles of key block j+1 move by LDS DMA while
+// block j's products run (the layout and DMA geometry of the forward's
+// pipelined kernel: rows unpadded, 16-byte chunks XOR-swizzled by the row with
+// AttnHalfPipe::fk). K is read to the end of a block (the dQ product) and takes
+// two buffers; V is read by the dP product only and takes one, refilled once
+// every wave is past it:
+//   top of block j: this wave's DMAs have landed (s_waitcnt), barrier;
+//     DMA K_{j+1} into the other K buffer;
+//   S and dP per 16-key half, then P and dS;
+//   barrier (every wave is done with V_j); DMA V_{j+1};
+//   dQ += K_j^T dS^T.
+// The DMA is hidden from the compiler (lds_dma16), so a compiler-visible load
+// issued after one waits for it too (loads complete in order): inside the loop
+// only the G chunks, when G is not resident, are loaded, after the K DMA that
+// the score products give time to land.
+template <int K, int D>
+struct AttnHalfBwdPipe {
+  using P = AttnHalfPipe<K, D>;
+  static constexpr int KB = 32;
+  static constexpr size_t tile = static_cast<size_t>(K + 1) * KB * D * 2;
+  // (head dim 16 stays on the staged kernel: at degree 0 the compiler places the DMA's buffer
+  // resource in vector registers, which the instruction does not take)
+  static constexpr bool fits_q = 3 * tile <= 160 * 1024 && D >= 32;
+  static constexpr int OPT = (K + 1) * P::IT;   // DMA operations per wave and tile
+};
+
+// DMA operation i (0 <= i < (K+1) IT) of this wave's share of rows first .. first + 31 of a
+// head's [rows, D] series into a tile [K+1][32][D] (chunks swizzled with fk; rows past `rows`
+// load zeros).
+template <typename T, int K, int D>
+__device__ __forceinline__ void attn_half_dma_tile(T (&tile)[K + 1][32][D], const CPtrs<T>& src, int64_t head,
+                                                   int rows, int first, int lane, int wave, int i) {
+  using P = AttnHalfPipe<K, D>;
+  constexpr int CH = P::CH, RPS = P::RPS, SEGS = P::SEGS, IT = P::IT;
+  const int o = i / IT, it = i % IT;
+  const int seg = it * kAttnWaves + wave;
+  if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
+  const int row = seg * RPS + lane / CH;
+  const int lch = (lane % CH) ^ P::fk(row);
+  const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * rows * D, rows * D * static_cast<int>(sizeof(T)));
+  lds_dma16(&tile[o][seg * RPS][0], rsrc, ((first + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
+}
+
+// Row operand of a swizzled tile: row `row`, 16-byte logical chunk `ch` (zero when din is false).
+template <typename T, int K, int D>
+__device__ __forceinline__ u32x4 attn_half_tile_row(const T (&tile)[K + 1][32][D], int o, int row, int ch, bool din) {
+  using P = AttnHalfPipe<K, D>;
+  const int pch = (ch & (P::CH - 1)) ^ P::fk(row);
+  const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[o][row][pch * 8]);
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  return din ? v : z;
+}
+
+// Transposed operand of a swizzled tile: head dims 16 db + c of rows 4 g .. 4 g + 3 and
+// 16 + 4 g .. 16 + 4 g + 3 (two ds_read_b64_tr_b16; lane c = 4 tj + ta addresses row 4 g + tj).
+template <typename T, int K, int D>
+__device__ __forceinline__ u32x4 attn_half_tile_tr(const T (&tile)[K + 1][32][D], int o, int db, int g, int tj,
+                                                   int ta) {
+  using P = AttnHalfPipe<K, D>;
+  const int row0 = 4 * g + tj, row1 = 16 + 4 * g + tj;
+  const int lch = 2 * db + ta / 2;
+  const int off0 = ((lch ^ P::fk(row0)) * 8) + 4 * (ta % 2);
+  const int off1 = ((lch ^ P::fk(row1)) * 8) + 4 * (ta % 2);
+  return lds_read_tr16x2(&tile[o][row0][off0], &tile[o][row1][off1]);
+}
+
+template <typename T, int K, int D, int MASK>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_half_pipe_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ, int L,
+    int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const float* __restrict__ madd_all,
+    const int32_t* __restrict__ ranges_all, int causal, float scale) {
+  using Sh = AttnHalfBwdShape<K, D>;
+  using BP = AttnHalfBwdPipe<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = BP::KB, DC = Sh::DC, DB = Sh::DB, OPT = BP::OPT;
+  constexpr bool SPLIT = Sh::split;
+  constexpr int NLO = SPLIT ? K + 1 : 1;
+  static_assert(BP::fits_q, "K/V tiles exceed LDS");
+  using Tile = T[K + 1][KB][D];
+  __shared__ __attribute__((aligned(16))) Tile Kt[2];
+  __shared__ __attribute__((aligned(16))) Tile Vt;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c = lane % 16;
+  const int g = lane / 16;
+  const int nqb = (L + kAttnBM - 1) / kAttnBM;
+  const int64_t bh = gridDim.x / static_cast<int64_t>(nqb);
+  int64_t head;
+  int slice, q_block;
+  attn_bwd_q_item(blockIdx.x, bh, nqb, 1, head, slice, q_block);
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = MASK != 0 ? mask_all + mask_index * L * S : nullptr;
+  const float* madd = MASK == 2 ? madd_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
+  float lse[K + 1], delta[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lse[o] = q_ok ? LSE.p[o][head * L + my_q] : 0.f;
+    delta[o] = q_ok ? DELTA.p[o][head * L + my_q] : 0.f;
+  }
+  auto load_row = [&](const CPtrs<T>& X, int o, int dc) -> u32x4 {
+    const bool din = 32 * dc + 8 * g < D;
+    return attn_half_load8<T>(X.p[o] + qrow + (din ? 32 * dc + 8 * g : 0), din);
+  };
+  constexpr int NRES = Sh::resident(2, 1, DB, 1, MASK != 0) >= 1 ? Sh::resident(2, 1, DB, 1, MASK != 0) : 1;
+  u32x4 rows[NRES][K + 1][DC];   // Q, then G when it fits
+#pragma unroll
+  for (int i = 0; i < NRES; ++i)
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) rows[i][o][dc] = load_row(i == 0 ? Q : G, o, dc);
+
+  floatx4 acc[DB][K + 1];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) acc[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  int lo = 0, hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / KB * KB;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
+  }
+  // a workgroup whose rows admit no key keeps one fully masked block (key < hi fails for every
+  // key), so the pipeline always has a first block
+  if (hi <= lo) lo = hi = 0;
+  const int nblocks = max(1, (hi - lo + KB - 1) / KB);
+  const int last_kb0 = lo + (nblocks - 1) * KB;
+  const int tj = c / 4, ta = c % 4;
+
+  // block 0's tiles (after the row loads: the compiler's waits for those would wait for the DMA)
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    attn_half_dma_tile<T, K, D>(Kt[0], Kp, head, S, lo, lane, wave, i);
+    attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, lo, lane, wave, i);
+  }
+
+  for (int j = 0; j < nblocks; ++j) {
+    const int kb0 = lo + j * KB;
+    const int next_kb0 = min(kb0 + KB, last_kb0);   // the last block re-loads itself: no branch
+    Tile& cur = Kt[j & 1];
+    Tile& nxt = Kt[(j + 1) & 1];
+    uint8_t mbyte[2][4];
+    float add[2][4];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        mbyte[kh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], my_q, key, L, S) : uint8_t(1);
+        add[kh][r] = MASK == 2 ? attn_mask_add(madd, my_q, key, L, S) : 0.f;
+      }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
+    __syncthreads();                 // ... and every wave's; block j-1 is done with nxt
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
+
+    // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
+    u32x4 dsb[K + 1], dsl[NLO];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      floatx4 sc[K + 1], dp[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) sc[o] = dp[o] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const bool din = 32 * dc + 8 * g < D;
+        u32x4 kop[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) kop[o] = attn_half_tile_row<T, K, D>(cur, o, 16 * kh + c, 4 * dc + g, din);
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MM::mma(kop[k - a], rows[0][a][dc], sc[k]);
+      }
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const bool din = 32 * dc + 8 * g < D;
+        u32x4 ga[K + 1], vop[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          ga[o] = NRES >= 2 ? rows[NRES >= 2 ? 1 : 0][o][dc] : load_row(G, o, dc);
+          vop[o] = attn_half_tile_row<T, K, D>(Vt, o, 16 * kh + c, 4 * dc + g, din);
+        }
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) dp[k] = MM::mma(vop[k - a], ga[a], dp[k]);
+      }
+      float w[K + 1][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        bool ok = q_ok && key < hi;
+        if (causal) ok = ok && key <= my_q;
+        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        float p[K + 1], ds[K + 1];
+        attn_prob_series<float, K>(sc, r, lse, ok, scale, add[kh][r], p);
+        attn_ds_series<float, K>(p, dp, r, delta, ds);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) w[o][r] = ds[o];
+      }
+      attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
+    }
+    __syncthreads();   // every wave is done with V_j
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, next_kb0, lane, wave, i);
+
+    // ---- dQ^T_k += sum_{a+b=k} K_b^T dS^T_a ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      u32x4 kt[K + 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) kt[o] = attn_half_tile_tr<T, K, D>(cur, o, db, g, tj, ta);
+      attn_half_series_mma<T, K, SPLIT, NLO>(acc[db], kt, dsb, dsl);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMAs have landed before the workgroup ends
+
+  if (q_ok) attn_half_store<T, K, DB>(acc, DQ, (head * L + my_q) * D, 0, g, scale);
+}
+
 // WHAT: 1 = dV, 2 = dK, 3 = both. MASK as the dQ kernel's.
 template <typename T, int K, int D, int SL, int WHAT, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_half_kernel(
@@ -565,15 +795,33 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   }
   if (a.dq != nullptr && rows > 0) {
     constexpr int SL = Sh::SL_Q;
-    const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
+    bool done = false;
+    if constexpr (AttnHalfBwdPipe<K, D>::fits_q && SL == 1) {
+      // the DMA's buffer resource spans a head's K / V rows (plus one block) with 32-bit offsets
+      if (a.lk >= 1 && (a.lk + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31)) {
+        const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
+#define PT_ATTN_BWD_Q_HALF_PIPE(MASK)                                                                        \
+  taylor_attention_bwd_q_half_pipe_kernel<T, K, D, MASK><<<grid, block, 0, a.stream>>>(                      \
+      q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale)
+        if (mask_kind == 2) PT_ATTN_BWD_Q_HALF_PIPE(2);
+        else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF_PIPE(1);
+        else PT_ATTN_BWD_Q_HALF_PIPE(0);
+#undef PT_ATTN_BWD_Q_HALF_PIPE
+        PT_LAUNCH_CHECK();
+        done = true;
+      }
+    }
+    if (!done) {
+      const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * SL));
 #define PT_ATTN_BWD_Q_HALF(MASK)                                                                             \
   taylor_attention_bwd_q_half_kernel<T, K, D, SL, MASK><<<grid, block, 0, a.stream>>>(                       \
       q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale)
-    if (mask_kind == 2) PT_ATTN_BWD_Q_HALF(2);
-    else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF(1);
-    else PT_ATTN_BWD_Q_HALF(0);
+      if (mask_kind == 2) PT_ATTN_BWD_Q_HALF(2);
+      else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF(1);
+      else PT_ATTN_BWD_Q_HALF(0);
 #undef PT_ATTN_BWD_Q_HALF
-    PT_LAUNCH_CHECK();
+      PT_LAUNCH_CHECK();
+    }
   }
   if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
     constexpr int SL = Sh::SL_KV;
