@@ -302,6 +302,8 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
  *   P = exp(scale Q K^T - lse), dV = P^T G, dP = G V^T,
  *   dS = P (dP - rowsum(G O)), dQ = scale dS K, dK = scale dS^T Q
  * in truncated series arithmetic (products are Cauchy products of orders).
+ * dtype: PT_FLOAT32, PT_FLOAT64, or PT_BFLOAT16 / PT_FLOAT16 (16-bit MFMA
+ *   operands, fp32 accumulation; lse float32, as the forward writes it).
  * q, k, v, out, grad: K+1 pointers each (a plain operand or cotangent passes
  *   zeros for orders 1..K); shapes as in pt_taylor_attention_fwd; out and lse
  *   are that call's outputs for the same q, k, v, mask and scale.
@@ -312,7 +314,7 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
  *   tile in the workspace (2 (K+1) bh lq lk values): five series products per
  *   admissible pair instead of eight (S and dP are then not recomputed for dK
  *   and dV), at the cost of that workspace. PT_FLOAT32 only (PT_UNSUPPORTED
- *   for PT_FLOAT64).
+ *   for the other dtypes).
  * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add, mask_map: as in
  *   pt_taylor_attention_fwd_ws (the forward's additive mask: with it the scores
  *   are recomputed and materialize does not apply).

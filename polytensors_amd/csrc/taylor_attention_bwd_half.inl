@@ -67,12 +67,26 @@ struct AttnHalfBwdShape {
   // the series (about 30 (K+1) registers), the lo operands of `packed` split series and the mask
   // values. The bound of 410 keeps every instantiation free of scratch spills (the compiler's
   // resource remarks).
-  static constexpr int resident(int ops, int outputs, int nb, int packed, bool masked) {
+  static constexpr int resident(int ops, int outputs, int nb, int packed, bool masked, int extra = 0) {
     const int fixed = outputs * (K + 1) * nb * 4 + 30 * (K + 1) + (split ? packed * 4 * (K + 1) : 0) +
-                      (masked ? 16 : 0);
+                      (masked ? 16 : 0) + extra;
     int n = ops;
     while (n > 0 && n * (K + 1) * DC * 4 + fixed > 410) --n;
     return n;
+  }
+  // whether `rings` operands fit a two-slot chunk ring beside the same working set (else they are
+  // loaded chunk by chunk)
+  static constexpr bool ring_fits(int rings, int outputs, int nb, int packed, bool masked, int extra) {
+    return outputs * (K + 1) * nb * 4 + 30 * (K + 1) + (split ? packed * 4 * (K + 1) : 0) + (masked ? 16 : 0) +
+               extra + rings * 2 * (K + 1) * 4 <= 460;
+  }
+  // the pipelined dK/dV kernel's operands (K, then V for dK) resident or in a ring (masked case,
+  // its DMA bookkeeping counted): else the staged kernel runs
+  static constexpr bool kv_pipe_regs(int what) {
+    const int nops = (what & 2) ? 2 : 1, outs = ((what & 2) ? 1 : 0) + ((what & 1) ? 1 : 0);
+    const int extra = (what & 2) ? 32 : 0;
+    const int nr = resident(nops, outs, DB, outs, true, extra);
+    return nr == nops || ring_fits(nops - nr, outs, DB, outs, true, extra);
   }
   // operands not resident are read one 32-wide chunk ahead through a two-slot ring, except at
   // degree 8 and head dim 128, where the ring's registers make the kernels spill
@@ -348,15 +362,16 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
 // The DMA is hidden from the compiler (lds_dma16), so a compiler-visible load
 // issued after one waits for it too (loads complete in order): inside the loop
 // only the G chunks, when G is not resident, are loaded, after the K DMA that
-// the score products give time to land.
+// the score products give time to land (issuing the K DMA after the dP product
+// instead measured 3% slower at degree 4, head dim 128).
 template <int K, int D>
 struct AttnHalfBwdPipe {
   using P = AttnHalfPipe<K, D>;
   static constexpr int KB = 32;
   static constexpr size_t tile = static_cast<size_t>(K + 1) * KB * D * 2;
-  // (head dim 16 stays on the staged kernel: at degree 0 the compiler places the DMA's buffer
-  // resource in vector registers, which the instruction does not take)
-  static constexpr bool fits_q = 3 * tile <= 160 * 1024 && D >= 32;
+  // (degree 0 and head dim 16 stay on the staged kernels: at degree 0 the compiler places the
+  // DMA's buffer resource in vector registers, which the instruction does not take)
+  static constexpr bool fits_q = 3 * tile <= 160 * 1024 && D >= 32 && K >= 1;
   static constexpr int OPT = (K + 1) * P::IT;   // DMA operations per wave and tile
 };
 
@@ -760,6 +775,281 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
   if constexpr (DO_K) attn_half_store<T, K, DBS>(acc_k, DK, row, d0, g, scale);
 }
 
+// Pipelined dK/dV kernel (WHAT as the staged kernel's): the Q and G tiles of query
+// block j+1 (and its lse and Delta series) move while block j's products run. A
+// tile read to the end of a block takes two buffers, one read by the score
+// products only takes one, refilled once every wave is past it:
+//   dV (WHAT 1): Q for S (one buffer), G for dV (two);
+//   dK (WHAT 2): Q for S and dK (two), G for dP (one);
+//   both (WHAT 3): two each.
+// The lse and Delta series of block j+1 are loaded at the top of block j (before
+// that block's DMA, so that waiting for them does not wait for it) and written to
+// LDS once every wave is done with block j's.
+template <int K, int D, int WHAT>
+struct AttnHalfBwdKvPipe {
+  static constexpr int NQ = (WHAT & 2) ? 2 : 1;
+  static constexpr int NG = (WHAT & 1) ? 2 : 1;
+  static constexpr size_t LDS = (NQ + NG) * AttnHalfBwdPipe<K, D>::tile + 2ull * (K + 1) * 32 * 4;
+  static constexpr bool fits = LDS <= 160 * 1024 && D >= 32 && K >= 1;
+};
+
+template <typename T, int K, int D, int WHAT, int MASK>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_half_pipe_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DK,
+    MPtrs<T> DV, int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap,
+    const float* __restrict__ madd_all, const int32_t* __restrict__ ranges_all, int causal, float scale) {
+  using Sh = AttnHalfBwdShape<K, D>;
+  using BP = AttnHalfBwdPipe<K, D>;
+  using KP = AttnHalfBwdKvPipe<K, D, WHAT>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = BP::KB, DC = Sh::DC, DB = Sh::DB, OPT = BP::OPT;
+  constexpr bool SPLIT = Sh::split;
+  constexpr int NLO = SPLIT ? K + 1 : 1;
+  constexpr bool DO_V = (WHAT & 1) != 0, DO_K = (WHAT & 2) != 0;
+  constexpr int NQ = KP::NQ, NG = KP::NG;
+  static_assert(KP::fits, "Q/G tiles exceed LDS");
+  using Tile = T[K + 1][KB][D];
+  __shared__ __attribute__((aligned(16))) Tile Qt[NQ];
+  __shared__ __attribute__((aligned(16))) Tile Gt[NG];
+  __shared__ __attribute__((aligned(16))) float Ls[K + 1][KB];
+  __shared__ __attribute__((aligned(16))) float Ds[K + 1][KB];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c = lane % 16;
+  const int g = lane / 16;
+  const int64_t bh = gridDim.x / static_cast<int64_t>((S + 63) / 64);
+  int64_t head;
+  int slice, kv_block;
+  attn_bwd_kv_item(blockIdx.x, bh, 1, head, slice, kv_block);
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = MASK != 0 ? mask_all + mask_index * L * S : nullptr;
+  const float* madd = MASK == 2 ? madd_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const int my_k = kv_block + wave * 16 + c;
+  const bool k_ok = my_k < S;
+  const int64_t krow = (head * S + (k_ok ? my_k : S - 1)) * D;
+  auto load_row = [&](const CPtrs<T>& X, int o, int dc) -> u32x4 {
+    const bool din = 32 * dc + 8 * g < D;
+    return attn_half_load8<T>(X.p[o] + krow + (din ? 32 * dc + 8 * g : 0), din);
+  };
+  // K, then V, resident when they fit (the DMA bookkeeping takes about 32 registers more than the
+  // staged kernel's staging); the others go through a two-slot chunk ring
+  constexpr int NOPS = DO_K ? 2 : 1, OUTS = (DO_K ? 1 : 0) + (DO_V ? 1 : 0), EXTRA = DO_K ? 32 : 0;
+  constexpr int NR0 = Sh::resident(NOPS, OUTS, DB, OUTS, MASK != 0, EXTRA);
+  // K always resident: loading both K and V chunk by chunk measured 33% slower for the dK pass at
+  // degree 4, head dim 128, where the resident K costs a few registers of scratch spill instead
+  // (4 to 7, the compiler's resource remarks)
+  constexpr int NR = NR0 > 0 ? NR0 : 1;
+  constexpr bool RING = NR < NOPS && Sh::ring_fits(NOPS - NR, OUTS, DB, OUTS, MASK != 0, EXTRA + (NR - NR0) * (K + 1) * DC * 4);
+  constexpr bool EARLY = NR == NOPS;   // the score products load nothing: the DMA may precede them
+  u32x4 rows[NR > 0 ? NR : 1][K + 1][DC];
+  u32x4 ring[2][2][K + 1];   // [operand][slot]: step s = 2-slot sequence over (half, chunk)
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int o = 0; o <= K; ++o)
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) rows[i][o][dc] = load_row(i == 0 ? Kp : Vp, o, dc);
+
+  floatx4 acc_v[DO_V ? DB : 1][K + 1], acc_k[DO_K ? DB : 1][K + 1];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) acc_v[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (DO_K) acc_k[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  int lo, hi;
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
+  lo = lo / KB * KB;
+  // a workgroup whose keys no query admits keeps one fully masked block (q < hi fails)
+  if (hi <= lo) lo = hi = 0;
+  const int nblocks = max(1, (hi - lo + KB - 1) / KB);
+  const int last_qb0 = lo + (nblocks - 1) * KB;
+  const int tj = c / 4, ta = c % 4;
+
+  // the lse and Delta series of query rows qb0 .. qb0 + 31 (zero past L): NV values per thread
+  constexpr int NV = ((K + 1) * KB + kAttnWaves * kWave - 1) / (kAttnWaves * kWave);
+  float lv[NV], dv_[NV];
+  auto load_rows = [&](int qb0) {
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int idx = min(static_cast<int>(threadIdx.x) + kAttnWaves * kWave * t, (K + 1) * KB - 1);
+      const int o = idx / KB, q = qb0 + idx % KB;
+      const int64_t at = head * L + min(q, L - 1);
+      lv[t] = order_ptr<K>(LSE, o)[at];
+      if constexpr (DO_K) dv_[t] = order_ptr<K>(DELTA, o)[at];
+    }
+  };
+  auto store_rows = [&](int qb0) {
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int idx = static_cast<int>(threadIdx.x) + kAttnWaves * kWave * t;
+      if (((K + 1) * KB) % (kAttnWaves * kWave) == 0 || idx < (K + 1) * KB) {
+        const int o = idx / KB, i = idx % KB;
+        const bool in = qb0 + i < L;
+        Ls[o][i] = in ? lv[t] : 0.f;
+        if constexpr (DO_K) Ds[o][i] = in ? dv_[t] : 0.f;
+      }
+    }
+  };
+
+  // block 0: its lse / Delta rows, then its tiles
+  load_rows(lo);
+  store_rows(lo);
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    attn_half_dma_tile<T, K, D>(Qt[0], Q, head, L, lo, lane, wave, i);
+    attn_half_dma_tile<T, K, D>(Gt[0], G, head, L, lo, lane, wave, i);
+  }
+
+  for (int j = 0; j < nblocks; ++j) {
+    const int qb0 = lo + j * KB;
+    const int next_qb0 = min(qb0 + KB, last_qb0);   // the last block re-loads itself: no branch
+    Tile& qcur = Qt[NQ == 2 ? (j & 1) : 0];
+    Tile& gcur = Gt[NG == 2 ? (j & 1) : 0];
+    uint8_t mbyte[2][4];
+    float add[2][4];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = qb0 + 16 * qh + 4 * g + r;
+        mbyte[qh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], q, my_k, L, S) : uint8_t(1);
+        add[qh][r] = MASK == 2 ? attn_mask_add(madd, q, my_k, L, S) : 0.f;
+      }
+    load_rows(next_qb0);             // block j+1's lse / Delta, ahead of this block's DMA
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the loads above)
+    __syncthreads();                 // ... and every wave's; block j-1 is done with the other buffers
+    // tiles read to the end of the block: block j+1's into their other buffer, here when the score
+    // products load nothing (every row operand resident), else after them with the others (their
+    // loads would wait for the DMA)
+    auto dma_double = [&]() {
+#pragma unroll
+      for (int i = 0; i < OPT; ++i) {
+        if constexpr (NQ == 2) attn_half_dma_tile<T, K, D>(Qt[(j + 1) & 1], Q, head, L, next_qb0, lane, wave, i);
+        if constexpr (NG == 2) attn_half_dma_tile<T, K, D>(Gt[(j + 1) & 1], G, head, L, next_qb0, lane, wave, i);
+      }
+    };
+    if constexpr (EARLY) dma_double();
+    // chunk 0 of the operands not resident (no DMA in flight ahead of them)
+#pragma unroll
+    for (int i = NR; i < NOPS; ++i)
+#pragma unroll
+      for (int o = 0; o <= K; ++o)
+        if constexpr (RING) ring[i][0][o] = load_row(i == 0 ? Kp : Vp, o, 0);
+
+    // ---- per 16-query half: S = Q K^T, dP = G V^T (queries x keys), then the P and dS series ----
+    u32x4 pb[K + 1], pl[NLO], dsb[K + 1], dsl[NLO];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+      floatx4 sc[K + 1], dp[DO_K ? K + 1 : 1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        sc[o] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (DO_K) dp[o] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+      // operand `which` of (half qh, chunk dc): resident, or ring step qh DC + dc, whose successor's
+      // chunk is loaded now
+      auto operand = [&](int which, int dc, u32x4 (&x)[K + 1]) {
+        const int st = qh * DC + dc;
+        if (RING && which >= NR && st + 1 < 2 * DC) {
+#pragma unroll
+          for (int o = 0; o <= K; ++o) ring[which][(st + 1) & 1][o] = load_row(which == 0 ? Kp : Vp, o, (dc + 1) % DC);
+        }
+#pragma unroll
+        for (int o = 0; o <= K; ++o)
+          x[o] = which < NR ? rows[which < NR ? which : 0][o][dc]
+                            : (RING ? ring[which][st & 1][o] : load_row(which == 0 ? Kp : Vp, o, dc));
+      };
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        const bool din = 32 * dc + 8 * g < D;
+        u32x4 qa[K + 1], kb[K + 1];
+        operand(0, dc, kb);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) qa[o] = attn_half_tile_row<T, K, D>(qcur, o, 16 * qh + c, 4 * dc + g, din);
+#pragma unroll
+        for (int k = 0; k <= K; ++k)
+#pragma unroll
+          for (int a = 0; a <= k; ++a) sc[k] = MM::mma(qa[a], kb[k - a], sc[k]);
+      }
+      if constexpr (DO_K) {
+#pragma unroll
+        for (int dc = 0; dc < DC; ++dc) {
+          const bool din = 32 * dc + 8 * g < D;
+          u32x4 ga[K + 1], vb[K + 1];
+          operand(1, dc, vb);
+#pragma unroll
+          for (int o = 0; o <= K; ++o) ga[o] = attn_half_tile_row<T, K, D>(gcur, o, 16 * qh + c, 4 * dc + g, din);
+#pragma unroll
+          for (int k = 0; k <= K; ++k)
+#pragma unroll
+            for (int a = 0; a <= k; ++a) dp[k] = MM::mma(ga[a], vb[k - a], dp[k]);
+        }
+      }
+      float wp[K + 1][4], wd[K + 1][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = qb0 + 16 * qh + 4 * g + r;
+        bool ok = k_ok && q < hi;
+        if (causal) ok = ok && my_k <= q;
+        if constexpr (MASK != 0) ok = ok && mbyte[qh][r] != 0;
+        // (read per element: the row series of all four elements at once cost registers that spill)
+        float lse[K + 1], p[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) lse[o] = Ls[o][16 * qh + 4 * g + r];
+        attn_prob_series<float, K>(sc, r, lse, ok, scale, add[qh][r], p);
+#pragma unroll
+        for (int o = 0; o <= K; ++o) wp[o][r] = p[o];
+        if constexpr (DO_K) {
+          float delta[K + 1], ds[K + 1];
+#pragma unroll
+          for (int o = 0; o <= K; ++o) delta[o] = Ds[o][16 * qh + 4 * g + r];
+          attn_ds_series<float, K>(p, dp, r, delta, ds);
+#pragma unroll
+          for (int o = 0; o <= K; ++o) wd[o][r] = ds[o];
+        }
+      }
+      if constexpr (DO_V) attn_half_pack<T, K, SPLIT, NLO>(wp, qh, pb, pl);
+      if constexpr (DO_K) attn_half_pack<T, K, SPLIT, NLO>(wd, qh, dsb, dsl);
+    }
+    __syncthreads();   // every wave is done with the single-buffered tile and this block's lse / Delta
+    store_rows(next_qb0);
+    if constexpr (!EARLY) dma_double();
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      if constexpr (NQ == 1) attn_half_dma_tile<T, K, D>(Qt[0], Q, head, L, next_qb0, lane, wave, i);
+      if constexpr (NG == 1) attn_half_dma_tile<T, K, D>(Gt[0], G, head, L, next_qb0, lane, wave, i);
+    }
+
+    // ---- dV^T_k += sum_{a+b=k} G_b^T P_a, dK^T_k += sum_{a+b=k} Q_b^T dS_a ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      if constexpr (DO_V) {
+        u32x4 gt[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) gt[o] = attn_half_tile_tr<T, K, D>(gcur, o, db, g, tj, ta);
+        attn_half_series_mma<T, K, SPLIT, NLO>(acc_v[db], gt, pb, pl);
+      }
+      if constexpr (DO_K) {
+        u32x4 qt[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) qt[o] = attn_half_tile_tr<T, K, D>(qcur, o, db, g, tj, ta);
+        attn_half_series_mma<T, K, SPLIT, NLO>(acc_k[db], qt, dsb, dsl);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMAs have landed before the workgroup ends
+
+  if (!k_ok) return;
+  const int64_t row = (head * S + my_k) * D;
+  if constexpr (DO_V) attn_half_store<T, K, DB>(acc_v, DV, row, 0, g, 1.f);
+  if constexpr (DO_K) attn_half_store<T, K, DB>(acc_k, DK, row, 0, g, scale);
+}
+
 template <typename T, int K, int D>
 static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   using Sh = AttnHalfBwdShape<K, D>;
@@ -826,18 +1116,33 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
     constexpr int SL = Sh::SL_KV;
     const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
-#define PT_ATTN_BWD_KV_HALF(WHAT)                                                                           \
+    // the pipelined kernel (one slice): the DMA's buffer resource spans a head's Q / G rows (plus
+    // one block) with 32-bit offsets
+    const bool pipe_ok =
+        SL == 1 && a.lq >= 1 && (a.lq + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31);
+#define PT_ATTN_BWD_KV_HALF_LAUNCH(KERNEL, ...)                                                              \
   do {                                                                                                       \
     if (mask_kind == 2)                                                                                      \
-      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 2><<<grid, block, 0, a.stream>>>(               \
+      KERNEL<__VA_ARGS__, 2><<<grid, block, 0, a.stream>>>(                                                  \
           q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
     else if (mask_kind == 1)                                                                                 \
-      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 1><<<grid, block, 0, a.stream>>>(               \
+      KERNEL<__VA_ARGS__, 1><<<grid, block, 0, a.stream>>>(                                                  \
           q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
     else                                                                                                     \
-      taylor_attention_bwd_kv_half_kernel<T, K, D, SL, WHAT, 0><<<grid, block, 0, a.stream>>>(               \
+      KERNEL<__VA_ARGS__, 0><<<grid, block, 0, a.stream>>>(                                                  \
           q, k, v, g, lse, delta_in, dk, dv, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale);  \
     PT_LAUNCH_CHECK();                                                                                       \
+  } while (0)
+#define PT_ATTN_BWD_KV_HALF(WHAT)                                                                           \
+  do {                                                                                                       \
+    bool piped = false;                                                                                      \
+    if constexpr (SL == 1 && AttnHalfBwdKvPipe<K, D, WHAT>::fits && Sh::kv_pipe_regs(WHAT)) {               \
+      if (pipe_ok) {                                                                                         \
+        PT_ATTN_BWD_KV_HALF_LAUNCH(taylor_attention_bwd_kv_half_pipe_kernel, T, K, D, WHAT);                 \
+        piped = true;                                                                                        \
+      }                                                                                                      \
+    }                                                                                                        \
+    if (!piped) PT_ATTN_BWD_KV_HALF_LAUNCH(taylor_attention_bwd_kv_half_kernel, T, K, D, SL, WHAT);          \
   } while (0)
     // the fused pass writes both outputs: with one of them not wanted (NULL) that one's pass runs alone
     bool fused = false;
@@ -852,6 +1157,7 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
       if (a.dk != nullptr) PT_ATTN_BWD_KV_HALF(2);
     }
 #undef PT_ATTN_BWD_KV_HALF
+#undef PT_ATTN_BWD_KV_HALF_LAUNCH
   }
   return PT_OK;
 }
