@@ -165,4 +165,18 @@ inline AttnBwdLayout attention_bwd_layout(size_t acc_size, size_t elem_size, int
   return l;
 }
 
+// Workspace of the 16-bit backward: the rowsum(G O) series (float32), then, when storing tiles,
+// the P and dS series of every (query, key) pair as 16-bit values [K+1][bh][row / 32][lq][32]
+// (32-key blocks; row = attention_bwd_half_row(lk), lk rounded up to a multiple of 64).
+inline int64_t attention_bwd_half_row(int64_t lk) { return (lk + 63) / 64 * 64; }
+inline AttnBwdLayout attention_bwd_half_layout(int degree, int64_t bh, int64_t lq, int64_t lk, bool materialize) {
+  AttnBwdLayout l{};
+  l.delta_bytes = static_cast<size_t>(degree + 1) * static_cast<size_t>(bh) * static_cast<size_t>(lq) * 4;
+  l.tiles_offset = (l.delta_bytes + 255) / 256 * 256;
+  l.tile_bytes = (static_cast<size_t>(bh) * static_cast<size_t>(lq) * static_cast<size_t>(attention_bwd_half_row(lk)) *
+                      2 + 255) / 256 * 256;
+  l.total = materialize ? l.tiles_offset + 2 * static_cast<size_t>(degree + 1) * l.tile_bytes : l.delta_bytes;
+  return l;
+}
+
 }  // namespace pt

@@ -107,6 +107,8 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
 size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh, int64_t lq, int64_t lk,
                                               int materialize) {
   if (degree < 0 || degree > PT_MAX_DEGREE || bh < 0 || lq < 0 || lk < 0) return 0;
+  if (dtype == PT_BFLOAT16 || dtype == PT_FLOAT16)   // stored tiles at degrees 1..4
+    return pt::attention_bwd_half_layout(degree, bh, lq, lk, materialize != 0 && degree >= 1 && degree <= 4).total;
   // the rowsum(G O) series in the accumulator type (float64, else float32); the stored tiles (float32
   // only) in the element type
   const size_t size = dtype == PT_FLOAT64 ? sizeof(double) : sizeof(float);
@@ -127,10 +129,10 @@ int pt_taylor_attention_bwd(int dtype, int degree, const void* const* q, const v
              "Taylor attention backward: mask_ranges without a mask");
   PT_REQUIRE(mask_add == nullptr || mask != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention backward: an additive mask needs the boolean mask of its finite entries");
-  // The stored-tile path is float32 only: a float64 run of it (degree 8, head dim 64) took a GPU
-  // memory fault whose cause is not established, so float64 always recomputes.
-  PT_REQUIRE(!materialize || dtype == PT_FLOAT32, PT_UNSUPPORTED,
-             "Taylor attention backward: materialize is float32 only");
+  // The stored-tile path is float32 and 16-bit only: a float64 run of it (degree 8, head dim 64)
+  // took a GPU memory fault whose cause is not established, so float64 always recomputes.
+  PT_REQUIRE(!materialize || dtype != PT_FLOAT64, PT_UNSUPPORTED,
+             "Taylor attention backward: materialize is not available for float64 (float32 and 16-bit only)");
   PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
              "Taylor attention backward: degree must be in 0..8");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,

@@ -415,11 +415,16 @@ __device__ __forceinline__ u32x4 attn_half_tile_tr(const T (&tile)[K + 1][32][D]
   return lds_read_tr16x2(&tile[o][row0][off0], &tile[o][row1][off1]);
 }
 
-template <typename T, int K, int D, int MASK>
+// STORE: also write the P and dS series of every visited (query, key) pair to PT / DST (the dS
+// values as rounded for the dQ product) for taylor_attention_bwd_kv_half_mat_kernel, in 32-key
+// blocks: [head][srow / 32 key blocks][L queries][32 keys] 16-bit values, so that a wave's two
+// stores of a block (its 16 queries' keys 0..15, then 16..31) fill one contiguous kilobyte.
+// Degrees 1..4 (one 16-bit operand per value).
+template <typename T, int K, int D, int MASK, bool STORE>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_half_pipe_kernel(
-    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ, int L,
-    int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const float* __restrict__ madd_all,
-    const int32_t* __restrict__ ranges_all, int causal, float scale) {
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ,
+    MPtrs<T> PT, MPtrs<T> DST, int64_t srow, int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap,
+    const float* __restrict__ madd_all, const int32_t* __restrict__ ranges_all, int causal, float scale) {
   using Sh = AttnHalfBwdShape<K, D>;
   using BP = AttnHalfBwdPipe<K, D>;
   using MM = HalfMfma<T>;
@@ -545,7 +550,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
 #pragma unroll
           for (int a = 0; a <= k; ++a) dp[k] = MM::mma(vop[k - a], ga[a], dp[k]);
       }
-      float w[K + 1][4];
+      float w[K + 1][4], wp[STORE ? K + 1 : 1][4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kb0 + 16 * kh + 4 * g + r;
@@ -556,9 +561,25 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         attn_prob_series<float, K>(sc, r, lse, ok, scale, add[kh][r], p);
         attn_ds_series<float, K>(p, dp, r, delta, ds);
 #pragma unroll
-        for (int o = 0; o <= K; ++o) w[o][r] = ds[o];
+        for (int o = 0; o <= K; ++o) {
+          w[o][r] = ds[o];
+          if constexpr (STORE) wp[o][r] = p[o];
+        }
       }
       attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
+      if constexpr (STORE) {
+        static_assert(!SPLIT, "stored tiles hold one 16-bit value per pair");
+        // keys kb0 + 16 kh + 4 g .. + 3 of the lane's query: one 8-byte store per series and order
+        if (q_ok) {
+          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 16 * kh + 4 * g;
+#pragma unroll
+          for (int o = 0; o <= K; ++o) {   // (plain stores: non-temporal ones measured 8% slower)
+            *reinterpret_cast<uint2*>(PT.p[o] + at) =
+                make_uint2(MM::pack2(wp[o][0], wp[o][1]), MM::pack2(wp[o][2], wp[o][3]));
+            *reinterpret_cast<uint2*>(DST.p[o] + at) = make_uint2(dsb[o][2 * kh], dsb[o][2 * kh + 1]);
+          }
+        }
+      }
     }
     __syncthreads();   // every wave is done with V_j
 #pragma unroll
@@ -575,7 +596,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   }
   __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMAs have landed before the workgroup ends
 
-  if (q_ok) attn_half_store<T, K, DB>(acc, DQ, (head * L + my_q) * D, 0, g, scale);
+  if (q_ok && DQ.p[0] != nullptr) attn_half_store<T, K, DB>(acc, DQ, (head * L + my_q) * D, 0, g, scale);
 }
 
 // WHAT: 1 = dV, 2 = dK, 3 = both. MASK as the dQ kernel's.
@@ -1050,6 +1071,159 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
   if constexpr (DO_K) attn_half_store<T, K, DB>(acc_k, DK, row, 0, g, scale);
 }
 
+// ---------------------------------------------------------------------------
+// Stored-tile dK / dV kernel: the dQ kernel has written the P and dS series of
+// every visited pair (dense 16-bit rows [bh][L][srow]), so each output takes one
+// series product per block (five products per pair in all instead of eight, and
+// no exponential series here). Per 32-query block the X tile (G for dV, Q for
+// dK) and the block's stored P (or dS) values of the workgroup's 64 keys move by
+// LDS DMA, double-buffered. The stored values are the B operand, read by
+// transpose reads (lane c receives key c's queries 4 g .. 4 g + 3 and 16 + 4 g ..),
+// and masked by admissibility: a pair the dQ kernel did not visit (a block
+// outside its mask range) holds no written value.
+template <int K, int D, int WHAT>
+struct AttnHalfBwdMat {
+  static constexpr int KB = 32;
+  static constexpr int NOUT = ((WHAT & 1) ? 1 : 0) + ((WHAT & 2) ? 1 : 0);
+  static constexpr size_t xtile = static_cast<size_t>(K + 1) * KB * D * 2;
+  static constexpr size_t stile = static_cast<size_t>(K + 1) * KB * 64 * 2;
+  static constexpr size_t LDS = 2 * NOUT * (xtile + stile);
+  static constexpr bool fits = LDS <= 160 * 1024 && D >= 32 && K >= 1 && K <= 4;
+};
+
+// This wave's DMA of one order of a stored tile: query rows first + 8 wave .. + 7 of the 64 keys
+// from key0 (two 32-key blocks of a head's [srow / 32][rows][32] 16-bit series) into LDS [32][64]
+// (row r: keys key0 .. key0 + 63 of query first + r). Rows past `rows` read the next key block's
+// first rows, or zeros past the head's series: their pairs are inadmissible and masked.
+template <typename T, int K>
+__device__ __forceinline__ void attn_half_dma_stored(T (&tile)[K + 1][32][64], const CPtrs<T>& src, int64_t head,
+                                                     int rows, int64_t srow, int first, int key0, int lane, int wave,
+                                                     int o) {
+  const int row = 8 * wave + lane / 8, ch = lane % 8;
+  const int64_t nkb = srow / 32;
+  const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * nkb * rows * 32, static_cast<int>(nkb * rows * 32 * 2));
+  const int64_t at = ((key0 / 32 + ch / 4) * static_cast<int64_t>(rows) + first + row) * 32 + 8 * (ch % 4);
+  lds_dma16(&tile[o][8 * wave][0], rsrc, static_cast<int>(at * 2));
+}
+
+template <typename T, int K, int D, int WHAT, bool MASKED>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_half_mat_kernel(
+    CPtrs<T> Q, CPtrs<T> G, CPtrs<T> PT, CPtrs<T> DST, MPtrs<T> DK, MPtrs<T> DV, int64_t srow, int L, int S,
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
+    float scale) {
+  using BP = AttnHalfBwdPipe<K, D>;
+  using MT = AttnHalfBwdMat<K, D, WHAT>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = MT::KB, DB = D / 16, OPT = BP::OPT, NOUT = MT::NOUT;
+  constexpr bool DO_V = (WHAT & 1) != 0, DO_K = (WHAT & 2) != 0;
+  constexpr int SV = 0, SK = DO_V ? 1 : 0;   // slots of the dV and dK inputs
+  static_assert(MT::fits, "tiles exceed LDS");
+  using XTile = T[K + 1][KB][D];
+  using STile = T[K + 1][KB][64];
+  __shared__ __attribute__((aligned(16))) XTile Xt[2][NOUT];
+  __shared__ __attribute__((aligned(16))) STile St[2][NOUT];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c = lane % 16;
+  const int g = lane / 16;
+  const int64_t bh = gridDim.x / static_cast<int64_t>((S + 63) / 64);
+  int64_t head;
+  int slice, kv_block;
+  attn_bwd_kv_item(blockIdx.x, bh, 1, head, slice, kv_block);
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = MASKED ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const int my_k = kv_block + wave * 16 + c;
+  const bool k_ok = my_k < S;
+
+  floatx4 acc_v[DO_V ? DB : 1][K + 1], acc_k[DO_K ? DB : 1][K + 1];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) acc_v[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (DO_K) acc_k[db][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  int lo, hi;
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
+  lo = lo / KB * KB;
+  if (hi <= lo) lo = hi = 0;   // one fully masked block (q < hi fails): the pipeline always has a first
+  const int nblocks = max(1, (hi - lo + KB - 1) / KB);
+  const int last_qb0 = lo + (nblocks - 1) * KB;
+  const int tj = c / 4, ta = c % 4;
+
+  // (the stored tiles first: with the X-tile DMAs, which some waves skip at head dim 32, ahead of
+  // them the compiler placed their buffer resources in vector registers, which the instruction
+  // does not take)
+  auto dma = [&](int buf, int qb0) {
+#pragma unroll
+    for (int o = 0; o <= K; ++o) {
+      if constexpr (DO_V) attn_half_dma_stored<T, K>(St[buf][SV], PT, head, L, srow, qb0, kv_block, lane, wave, o);
+      if constexpr (DO_K) attn_half_dma_stored<T, K>(St[buf][SK], DST, head, L, srow, qb0, kv_block, lane, wave, o);
+    }
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      if constexpr (DO_V) attn_half_dma_tile<T, K, D>(Xt[buf][SV], G, head, L, qb0, lane, wave, i);
+      if constexpr (DO_K) attn_half_dma_tile<T, K, D>(Xt[buf][SK], Q, head, L, qb0, lane, wave, i);
+    }
+  };
+  dma(0, lo);
+
+  for (int j = 0; j < nblocks; ++j) {
+    const int qb0 = lo + j * KB;
+    const int cur = j & 1;
+    uint8_t mbyte[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      mbyte[s] = MASKED ? attn_mask_byte(mask, Q.p[0], qb0 + 16 * (s / 4) + 4 * g + s % 4, my_k, L, S) : uint8_t(1);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask bytes)
+    __syncthreads();                 // ... and every wave's; block j-1 is done with the other buffers
+    dma(cur ^ 1, min(qb0 + KB, last_qb0));   // block j+1 (the last block re-loads itself: no branch)
+
+    // admissibility of the eight pairs behind the lane's operand slots (slot 4 qh + r: query
+    // qb0 + 16 qh + 4 g + r, key my_k), as 16-bit lane masks
+    u32x4 keep;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int s = 2 * w + h;
+        const int q = qb0 + 16 * (s / 4) + 4 * g + s % 4;
+        bool ok = k_ok && q < hi;
+        if (causal) ok = ok && my_k <= q;
+        if constexpr (MASKED) ok = ok && mbyte[s] != 0;
+        m |= ok ? (0xffffu << (16 * h)) : 0u;
+      }
+      keep[w] = m;
+    }
+    auto products = [&](floatx4 (&acc)[DB][K + 1], const XTile& xt, const STile& st) {
+      u32x4 b[K + 1], none[1];
+#pragma unroll
+      for (int o = 0; o <= K; ++o)
+        b[o] = lds_read_tr16x2(&st[o][4 * g + tj][16 * wave + 4 * ta], &st[o][16 + 4 * g + tj][16 * wave + 4 * ta]) &
+               keep;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        u32x4 x[K + 1];
+#pragma unroll
+        for (int o = 0; o <= K; ++o) x[o] = attn_half_tile_tr<T, K, D>(xt, o, db, g, tj, ta);
+        attn_half_series_mma<T, K, false, 1>(acc[db], x, b, none);
+      }
+    };
+    if constexpr (DO_V) products(acc_v, Xt[cur][SV], St[cur][SV]);
+    if constexpr (DO_K) products(acc_k, Xt[cur][SK], St[cur][SK]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMAs have landed before the workgroup ends
+
+  if (!k_ok) return;
+  const int64_t row = (head * S + my_k) * D;
+  if constexpr (DO_V) attn_half_store<T, K, DB>(acc_v, DV, row, 0, g, 1.f);
+  if constexpr (DO_K) attn_half_store<T, K, DB>(acc_k, DK, row, 0, g, scale);
+}
+
 template <typename T, int K, int D>
 static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   using Sh = AttnHalfBwdShape<K, D>;
@@ -1078,24 +1252,58 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   const float* madd = static_cast<const float*>(a.mask_add);
   const int mask_kind = madd != nullptr ? 2 : a.mask != nullptr ? 1 : 0;
   const dim3 block(kAttnWaves * kWave);
+  // the DMA's buffer resources span a head's K / V rows and Q / G rows (plus one block) with 32-bit
+  // offsets
+  const bool q_pipe_ok = a.lk >= 1 && (a.lk + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31);
+  const bool kv_pipe_ok = a.lq >= 1 && (a.lq + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31);
+  // Stored tiles (degrees 1..4, the pipelined dQ kernel): the dQ kernel writes the P and dS series,
+  // the dK / dV kernels read them (five products per pair instead of eight). Elsewhere the request
+  // is a hint and the scores are recomputed.
+  const int64_t srow = attention_bwd_half_row(a.lk);
+  bool mat = false;
+  MPtrs<T> pt{}, dst{};
+  CPtrs<T> pt_in{}, dst_in{};
+  if constexpr (K >= 1 && K <= 4 && AttnHalfBwdPipe<K, D>::fits_q && Sh::SL_Q == 1 &&
+                AttnHalfBwdMat<K, D, 1>::fits && AttnHalfBwdMat<K, D, 2>::fits) {
+    mat = a.materialize && rows > 0 && (a.dk != nullptr || a.dv != nullptr) && q_pipe_ok && kv_pipe_ok &&
+          (a.lq + 32) * srow * 2 < (int64_t{1} << 31);
+    if (mat) {
+      const AttnBwdLayout lay = attention_bwd_half_layout(K, a.bh, a.lq, a.lk, true);
+      for (int i = 0; i <= K; ++i) {
+        pt.p[i] = reinterpret_cast<T*>(static_cast<char*>(a.workspace) + lay.tiles_offset + i * lay.tile_bytes);
+        dst.p[i] = reinterpret_cast<T*>(static_cast<char*>(a.workspace) + lay.tiles_offset +
+                                        (K + 1 + i) * lay.tile_bytes);
+        pt_in.p[i] = pt.p[i];
+        dst_in.p[i] = dst.p[i];
+      }
+    }
+  }
   if (rows > 0 && (a.dq != nullptr || ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0))) {
     attn_bwd_delta_kernel<T, K, D><<<dim3(static_cast<unsigned>((rows + 15) / 16)), dim3(256), 0, a.stream>>>(
         g, o, delta, rows);
     PT_LAUNCH_CHECK();
   }
-  if (a.dq != nullptr && rows > 0) {
+  if ((a.dq != nullptr || mat) && rows > 0) {   // (with stored tiles and no dq the kernel still writes them)
     constexpr int SL = Sh::SL_Q;
     bool done = false;
     if constexpr (AttnHalfBwdPipe<K, D>::fits_q && SL == 1) {
-      // the DMA's buffer resource spans a head's K / V rows (plus one block) with 32-bit offsets
-      if (a.lk >= 1 && (a.lk + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31)) {
+      if (q_pipe_ok) {
         const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
-#define PT_ATTN_BWD_Q_HALF_PIPE(MASK)                                                                        \
-  taylor_attention_bwd_q_half_pipe_kernel<T, K, D, MASK><<<grid, block, 0, a.stream>>>(                      \
-      q, k, v, g, lse, delta_in, dq, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal, scale)
-        if (mask_kind == 2) PT_ATTN_BWD_Q_HALF_PIPE(2);
-        else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF_PIPE(1);
-        else PT_ATTN_BWD_Q_HALF_PIPE(0);
+#define PT_ATTN_BWD_Q_HALF_PIPE(MASK, STORE)                                                                 \
+  taylor_attention_bwd_q_half_pipe_kernel<T, K, D, MASK, STORE><<<grid, block, 0, a.stream>>>(               \
+      q, k, v, g, lse, delta_in, dq, pt, dst, srow, L, S, a.mask, a.mask_map, madd, a.mask_ranges, causal,    \
+      scale)
+        if (mat) {
+          if constexpr (K >= 1 && K <= 4) {
+            if (mask_kind == 2) PT_ATTN_BWD_Q_HALF_PIPE(2, true);
+            else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF_PIPE(1, true);
+            else PT_ATTN_BWD_Q_HALF_PIPE(0, true);
+          }
+        } else {
+          if (mask_kind == 2) PT_ATTN_BWD_Q_HALF_PIPE(2, false);
+          else if (mask_kind == 1) PT_ATTN_BWD_Q_HALF_PIPE(1, false);
+          else PT_ATTN_BWD_Q_HALF_PIPE(0, false);
+        }
 #undef PT_ATTN_BWD_Q_HALF_PIPE
         PT_LAUNCH_CHECK();
         done = true;
@@ -1113,13 +1321,36 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
       PT_LAUNCH_CHECK();
     }
   }
-  if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
+  if (mat) {
+    if constexpr (K >= 1 && K <= 4 && AttnHalfBwdMat<K, D, 1>::fits && AttnHalfBwdMat<K, D, 2>::fits) {
+      const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh));
+#define PT_ATTN_BWD_KV_HALF_MAT(WHAT)                                                                        \
+  do {                                                                                                       \
+    if (a.mask != nullptr)                                                                                   \
+      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, true><<<grid, block, 0, a.stream>>>(            \
+          q, g, pt_in, dst_in, dk, dv, srow, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale);        \
+    else                                                                                                     \
+      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, false><<<grid, block, 0, a.stream>>>(           \
+          q, g, pt_in, dst_in, dk, dv, srow, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale);        \
+    PT_LAUNCH_CHECK();                                                                                       \
+  } while (0)
+      bool fused = false;
+      if constexpr (AttnHalfBwdMat<K, D, 3>::fits) {
+        if (a.dk != nullptr && a.dv != nullptr) {
+          PT_ATTN_BWD_KV_HALF_MAT(3);
+          fused = true;
+        }
+      }
+      if (!fused) {
+        if (a.dv != nullptr) PT_ATTN_BWD_KV_HALF_MAT(1);
+        if (a.dk != nullptr) PT_ATTN_BWD_KV_HALF_MAT(2);
+      }
+#undef PT_ATTN_BWD_KV_HALF_MAT
+    }
+  } else if ((a.dk != nullptr || a.dv != nullptr) && a.lk > 0) {
     constexpr int SL = Sh::SL_KV;
     const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh * SL));
-    // the pipelined kernel (one slice): the DMA's buffer resource spans a head's Q / G rows (plus
-    // one block) with 32-bit offsets
-    const bool pipe_ok =
-        SL == 1 && a.lq >= 1 && (a.lq + 32) * D * static_cast<int64_t>(sizeof(T)) < (int64_t{1} << 31);
+    const bool pipe_ok = SL == 1 && kv_pipe_ok;   // the pipelined kernel (one slice)
 #define PT_ATTN_BWD_KV_HALF_LAUNCH(KERNEL, ...)                                                              \
   do {                                                                                                       \
     if (mask_kind == 2)                                                                                      \

@@ -455,17 +455,18 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   const int64_t lk = k[0].size(1);
   c10::DeviceGuard guard(q[0].device());
   const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention_bwd");
-  if (mask.add) materialize = 0;   // an additive mask recomputes the scores
+  if (mask.add && dtype == at::kFloat) materialize = 0;   // float32 recomputes with an additive mask
   Tensor dq = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor dk = at::empty({degree + 1, bh, lk, d}, q[0].options());
   Tensor dv = at::empty_like(dk);
   const auto ranges = mask_ranges(mask, lq, lk);
   const int code = dtype_code(dtype);
-  if (materialize < 0) {   // float32 only: the library refuses the stored-tile path for float64
+  if (materialize < 0) {   // stored tiles where the workspace takes at most a quarter of the device;
+                           // the library refuses them for float64
     const size_t size = pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, 1);
     size_t free_bytes = 0, total_bytes = 0;
     if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) total_bytes = 0;
-    materialize = dtype == at::kFloat && total_bytes > 0 && size <= total_bytes / 4 ? 1 : 0;
+    materialize = dtype != at::kDouble && total_bytes > 0 && size <= total_bytes / 4 ? 1 : 0;
   }
   const size_t wbytes =
       pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, static_cast<int>(materialize));

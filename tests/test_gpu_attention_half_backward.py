@@ -56,19 +56,21 @@ def _check(got, want, what, floor=0.0, tol=TOL):
         assert err <= tol, f"{what} order {k}: {err:.3e} > {tol:.0e}"
 
 
-def _grads(Q, K, V, G, mask=None, causal=False):
-    """Forward then the 16-bit backward on [bh, T, d] series (mask: bool or float (L, S))."""
+def _grads(Q, K, V, G, mask=None, causal=False, materialize=-1):
+    """Forward then the 16-bit backward on [bh, T, d] series (mask: bool or float (L, S));
+    materialize 1: the dQ kernel stores the P and dS series and the dK / dV kernels read them
+    (degrees 1..4), 0: the scores are recomputed, -1: the operator's choice."""
     q, k, v, g = ([c.cuda() for c in s] for s in (Q, K, V, G))
     degree, scale = len(q) - 1, 1 / math.sqrt(q[0].shape[-1])
     m = None if mask is None else (mask.cuda() if mask.dtype == torch.bool else mask.float().cuda())
     out, lse = _ops.taylor_attention_fwd(q, k, v, m, causal, scale, degree)
-    dq, dk, dv = _ops.attention_gradient_series(q, k, v, out, lse, g, m, causal, scale)
+    dq, dk, dv = _ops.taylor_attention_bwd(q, k, v, out, lse, g, m, causal, scale, materialize)
     assert dq.dtype == dk.dtype == dv.dtype == q[0].dtype
     return dq.unbind(0), dk.unbind(0), dv.unbind(0)
 
 
-def _compare(Q, K, V, G, mask=None, causal=False, what=""):
-    got = _grads(Q, K, V, G, mask=mask, causal=causal)
+def _compare(Q, K, V, G, mask=None, causal=False, what="", materialize=-1):
+    got = _grads(Q, K, V, G, mask=mask, causal=causal, materialize=materialize)
     want = oracle.attention_backward(_up(Q), _up(K), _up(V), _up(G),
                                      attn_mask=mask if mask is None or mask.dtype == torch.bool else mask.double(),
                                      is_causal=causal)
@@ -78,19 +80,21 @@ def _compare(Q, K, V, G, mask=None, causal=False, what=""):
         _check(a, b, f"{what} {name}", floor=floor)
 
 
+@pytest.mark.parametrize("materialize", [0, 1])
 @pytest.mark.parametrize("dtype", HALF)
 @pytest.mark.parametrize("degree", range(9))
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
-def test_every_degree_and_head_dim(dtype, degree, d):
+def test_every_degree_and_head_dim(dtype, degree, d, materialize):
     Q, K, V, G = (_series((2, 80, d), degree, 10 + i, dtype) for i in range(4))
-    _compare(Q, K, V, G, causal=True, what=f"K={degree} d={d}")
+    _compare(Q, K, V, G, causal=True, what=f"K={degree} d={d}", materialize=materialize)
 
 
+@pytest.mark.parametrize("materialize", [0, 1])
 @pytest.mark.parametrize("dtype", HALF)
 @pytest.mark.parametrize("mode", ["none", "causal", "window", "additive"])
 @pytest.mark.parametrize("L,S", [(150, 150), (70, 33), (33, 70), (1, 40), (130, 96)])
 @pytest.mark.parametrize("degree", [1, 4, 6])
-def test_masks_and_lengths(dtype, mode, L, S, degree):
+def test_masks_and_lengths(dtype, mode, L, S, degree, materialize):
     Q, K, V, G = (_series((3, T, 64), degree, 20 + i, dtype) for i, T in enumerate((L, S, S, L)))
     mask, causal = None, mode == "causal"
     if mode == "window":
@@ -100,11 +104,12 @@ def test_masks_and_lengths(dtype, mode, L, S, degree):
         keep = torch.rand(L, S, generator=g) < 0.7
         keep[:, 0] = True   # every row admits a key (the oracle's NaN rows are covered elsewhere)
         mask = torch.randn(L, S, generator=g, dtype=torch.float64).masked_fill(~keep, float("-inf"))
-    _compare(Q, K, V, G, mask=mask, causal=causal, what=f"{mode} L={L} S={S} K={degree}")
+    _compare(Q, K, V, G, mask=mask, causal=causal, what=f"{mode} L={L} S={S} K={degree}", materialize=materialize)
 
 
+@pytest.mark.parametrize("materialize", [0, 1])
 @pytest.mark.parametrize("dtype", HALF)
-def test_rows_and_columns_without_admissible_pairs(dtype):
+def test_rows_and_columns_without_admissible_pairs(dtype, materialize):
     # a window with a query block masked out and a key block that no query admits: skipped blocks
     # of both kernels; their gradients are zero
     L, d, degree = 320, 32, 2
@@ -112,11 +117,11 @@ def test_rows_and_columns_without_admissible_pairs(dtype):
     mask[64:128] = False
     mask[:, 192:256] = False
     Q, K, V, G = (_series((2, L, d), degree, 30 + i, dtype) for i in range(4))
-    dq, dk, dv = _grads(Q, K, V, G, mask=mask)
+    dq, dk, dv = _grads(Q, K, V, G, mask=mask, materialize=materialize)
     for o in range(degree + 1):
         assert dq[o][:, 64:128].abs().max().item() == 0
         assert dk[o][:, 192:256].abs().max().item() == 0 and dv[o][:, 192:256].abs().max().item() == 0
-    _compare(Q, K, V, G, mask=mask, what="skipped blocks")
+    _compare(Q, K, V, G, mask=mask, what="skipped blocks", materialize=materialize)
 
 
 @pytest.mark.parametrize("dtype", HALF)
@@ -158,8 +163,8 @@ def _abi_bwd(q, k, v, out, lse, g, dtype, materialize, want_q=True, want_k=True,
     return outs
 
 
-@pytest.mark.parametrize("dtype,materialize", [(torch.bfloat16, 0), (torch.float16, 0), (torch.float32, 0),
-                                               (torch.float32, 1)])
+@pytest.mark.parametrize("dtype,materialize", [(torch.bfloat16, 0), (torch.float16, 0), (torch.bfloat16, 1),
+                                               (torch.float16, 1), (torch.float32, 0), (torch.float32, 1)])
 @pytest.mark.parametrize("d", [32, 128])
 def test_gradients_not_wanted_are_not_written(dtype, materialize, d):
     # NULL dq / dk / dv: the other outputs equal the full call's bit for bit and the NULL one's buffer
@@ -191,8 +196,9 @@ def test_close_to_float32(dtype):
                 assert rel_err(x.float().cpu(), y.cpu()) < 5e-2
 
 
+@pytest.mark.parametrize("materialize", [0, 1])
 @pytest.mark.parametrize("dtype", HALF)
-def test_full_size_config3(dtype):
+def test_full_size_config3(dtype, materialize):
     # benchmark config 3's shape (B=4 H=16 L=2048 d=128, K=4, causal, line inputs) in 16-bit storage
     # with a random cotangent series: one head against the oracle; on every head, linearity in G
     # (bwd(G1 + G2) = bwd(G1) + bwd(G2) within twice the rounding tolerance)
@@ -211,13 +217,14 @@ def test_full_size_config3(dtype):
     g1, g2 = cot(), cot()
     scale = 1 / math.sqrt(d)
     out, lse = _ops.taylor_attention_fwd(q, k, v, None, True, scale, degree)
-    r1 = _ops.attention_gradient_series(q, k, v, out, lse, g1, None, True, scale)
+    r1 = _ops.taylor_attention_bwd(q, k, v, out, lse, g1, None, True, scale, materialize)
     head = 21
     want = oracle.attention_backward(*([c[head].cpu().double() for c in s] for s in (q, k, v, g1)), is_causal=True)
     for name, got, w in zip(("dq", "dk", "dv"), r1, want):
         _check([c[head] for c in got], w, name)
-    r2 = _ops.attention_gradient_series(q, k, v, out, lse, g2, None, True, scale)
-    r12 = _ops.attention_gradient_series(q, k, v, out, lse, [a + b for a, b in zip(g1, g2)], None, True, scale)
+    r2 = _ops.taylor_attention_bwd(q, k, v, out, lse, g2, None, True, scale, materialize)
+    r12 = _ops.taylor_attention_bwd(q, k, v, out, lse, [a + b for a, b in zip(g1, g2)], None, True, scale,
+                                    materialize)
     for name, a, b, ab in zip(("dq", "dk", "dv"), r1, r2, r12):
         for o in range(degree + 1):
             lhs, rhs = ab[o].double(), a[o].double() + b[o].double()
