@@ -313,8 +313,9 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
  * materialize: nonzero stores the P and dS series of every visited 16 x 16
  *   tile in the workspace (2 (K+1) bh lq lk values): five series products per
  *   admissible pair instead of eight (S and dP are then not recomputed for dK
- *   and dV), at the cost of that workspace. PT_FLOAT32 only (PT_UNSUPPORTED
- *   for the other dtypes).
+ *   and dV), at the cost of that workspace. PT_FLOAT32, and PT_BFLOAT16 /
+ *   PT_FLOAT16 at degrees 1..4 and head dims 32..128 (other 16-bit calls
+ *   recompute and ignore it); PT_UNSUPPORTED for PT_FLOAT64.
  * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add, mask_map: as in
  *   pt_taylor_attention_fwd_ws (the forward's additive mask: with it the scores
  *   are recomputed and materialize does not apply).

@@ -6,11 +6,13 @@ rounded to the storage type as operands of the products that contract them
 (a hi + lo pair from degree 5), and every gradient is rounded once. The oracle
 (``oracle.attention_backward``, pinned against jets of torch.func.vjp in
 tests/test_oracle_pins.py) runs in float64 on the same stored 16-bit inputs,
-upcast. Cases: every degree 0..8 and head dim, causal / boolean window / unmasked /
-additive masks, unequal and ragged lengths, a single query, masks over the batch
-through autograd, one gradient not wanted (NULL outputs through the C ABI, here
-and for float32), and the full config-3 shape (one head against the oracle,
-linearity in G over all heads).
+upcast. Both paths run: P and dS recomputed by the dK / dV kernels, and stored by
+the dQ kernel (degrees 1..4, materialize=1; elsewhere the request falls back to
+recomputing). Cases: every degree 0..8 and head dim, causal / boolean window /
+unmasked / additive masks, unequal and ragged lengths, a single query, skipped
+blocks, masks over the batch through autograd, one gradient not wanted (NULL
+outputs through the C ABI, here and for float32), and the full config-3 shape (one
+head against the oracle, linearity in G over all heads).
 Tolerance per order, max|got - want| / max|want|: 2e-2 (the north star's
 bf16-input / fp32-accumulate bound; the reference compares its half-type
 gradients with float32 at 5e-2, /root/reference/tests/test_fused_kernels.py:64-72).
