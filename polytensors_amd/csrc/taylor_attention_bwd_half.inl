@@ -417,9 +417,10 @@ __device__ __forceinline__ u32x4 attn_half_tile_tr(const T (&tile)[K + 1][32][D]
 
 // STORE: also write the P and dS series of every visited (query, key) pair to PT / DST (the dS
 // values as rounded for the dQ product) for taylor_attention_bwd_kv_half_mat_kernel, in 32-key
-// blocks: [head][srow / 32 key blocks][L queries][32 keys] 16-bit values, so that a wave's two
-// stores of a block (its 16 queries' keys 0..15, then 16..31) fill one contiguous kilobyte.
-// Degrees 1..4 (one 16-bit operand per value).
+// blocks: [head][srow / 32 key blocks][L queries][32 positions] 16-bit values, key 16 h + 4 g + r
+// of a block at position 8 g + 4 h + r (the eight keys a lane holds are adjacent), so that a
+// wave's store of a block fills one contiguous kilobyte. Degrees 1..4 (one 16-bit operand per
+// value).
 template <typename T, int K, int D, int MASK, bool STORE>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_half_pipe_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ,
@@ -519,7 +520,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
 
     // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
-    u32x4 dsb[K + 1], dsl[NLO];
+    u32x4 dsb[K + 1], dsl[NLO], ppk[STORE ? K + 1 : 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       floatx4 sc[K + 1], dp[K + 1];
@@ -569,15 +570,23 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
       attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
       if constexpr (STORE) {
         static_assert(!SPLIT, "stored tiles hold one 16-bit value per pair");
-        // keys kb0 + 16 kh + 4 g .. + 3 of the lane's query: one 8-byte store per series and order
-        if (q_ok) {
-          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 16 * kh + 4 * g;
 #pragma unroll
-          for (int o = 0; o <= K; ++o) {   // (plain stores: non-temporal ones measured 8% slower)
-            *reinterpret_cast<uint2*>(PT.p[o] + at) =
-                make_uint2(MM::pack2(wp[o][0], wp[o][1]), MM::pack2(wp[o][2], wp[o][3]));
-            *reinterpret_cast<uint2*>(DST.p[o] + at) = make_uint2(dsb[o][2 * kh], dsb[o][2 * kh + 1]);
-          }
+        for (int o = 0; o <= K; ++o) {
+          ppk[o][2 * kh] = MM::pack2(wp[o][0], wp[o][1]);
+          ppk[o][2 * kh + 1] = MM::pack2(wp[o][2], wp[o][3]);
+        }
+      }
+    }
+    if constexpr (STORE) {
+      // the lane's eight keys (4 g + r and 16 + 4 g + r of the block) of its query, at positions
+      // 8 g .. 8 g + 7 of the block's 32: one 16-byte store per series and order, a contiguous
+      // kilobyte per wave (plain stores: non-temporal ones measured 8% slower)
+      if (q_ok) {
+        const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g;
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          *reinterpret_cast<u32x4*>(PT.p[o] + at) = ppk[o];
+          *reinterpret_cast<u32x4*>(DST.p[o] + at) = dsb[o];
         }
       }
     }
@@ -1201,10 +1210,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
     }
     auto products = [&](floatx4 (&acc)[DB][K + 1], const XTile& xt, const STile& st) {
       u32x4 b[K + 1], none[1];
+      // the wave's keys kv_block + 16 wave + c: block wave / 2, key 16 (wave % 2) + c at position
+      // 8 (c / 4) + 4 (wave % 2) + c % 4; this lane addresses the four positions of lanes 4 ta ..
+      const int col = 32 * (wave / 2) + 4 * (wave % 2) + 8 * ta;
 #pragma unroll
       for (int o = 0; o <= K; ++o)
-        b[o] = lds_read_tr16x2(&st[o][4 * g + tj][16 * wave + 4 * ta], &st[o][16 + 4 * g + tj][16 * wave + 4 * ta]) &
-               keep;
+        b[o] = lds_read_tr16x2(&st[o][4 * g + tj][col], &st[o][16 + 4 * g + tj][col]) & keep;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         u32x4 x[K + 1];
