@@ -167,8 +167,9 @@ inline AttnBwdLayout attention_bwd_layout(size_t acc_size, size_t elem_size, int
 
 // Workspace of the 16-bit backward: the rowsum(G O) series (float32), then, when storing tiles,
 // the P and dS series of every (query, key) pair as 16-bit values [K+1][bh][row / 32][lq][32]
-// (32-key blocks; row = attention_bwd_half_row(lk), lk rounded up to a multiple of 64).
-inline int64_t attention_bwd_half_row(int64_t lk) { return (lk + 63) / 64 * 64; }
+// (32-key blocks; row = attention_bwd_half_row(lk), lk rounded up to a multiple of 128, the keys
+// of one workgroup of the reading kernel).
+inline int64_t attention_bwd_half_row(int64_t lk) { return (lk + 127) / 128 * 128; }
 inline AttnBwdLayout attention_bwd_half_layout(int degree, int64_t bh, int64_t lq, int64_t lk, bool materialize) {
   AttnBwdLayout l{};
   l.delta_bytes = static_cast<size_t>(degree + 1) * static_cast<size_t>(bh) * static_cast<size_t>(lq) * 4;

@@ -520,7 +520,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
 
     // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
-    u32x4 dsb[K + 1], dsl[NLO], ppk[STORE ? K + 1 : 1];
+    // (the P operands of both halves are held for one store where the registers allow: without a
+    // mask; with one, each half's are stored as they are formed)
+    constexpr bool ONE_STORE = MASK == 0;
+    u32x4 dsb[K + 1], dsl[NLO], ppk[STORE && ONE_STORE ? K + 1 : 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       floatx4 sc[K + 1], dp[K + 1];
@@ -570,14 +573,24 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
       attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
       if constexpr (STORE) {
         static_assert(!SPLIT, "stored tiles hold one 16-bit value per pair");
+        if constexpr (ONE_STORE) {
 #pragma unroll
-        for (int o = 0; o <= K; ++o) {
-          ppk[o][2 * kh] = MM::pack2(wp[o][0], wp[o][1]);
-          ppk[o][2 * kh + 1] = MM::pack2(wp[o][2], wp[o][3]);
+          for (int o = 0; o <= K; ++o) {
+            ppk[o][2 * kh] = MM::pack2(wp[o][0], wp[o][1]);
+            ppk[o][2 * kh + 1] = MM::pack2(wp[o][2], wp[o][3]);
+          }
+        } else if (q_ok) {   // this half's four keys, positions 8 g + 4 kh .. + 3: an 8-byte store
+          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g + 4 * kh;
+#pragma unroll
+          for (int o = 0; o <= K; ++o) {
+            *reinterpret_cast<uint2*>(PT.p[o] + at) =
+                make_uint2(MM::pack2(wp[o][0], wp[o][1]), MM::pack2(wp[o][2], wp[o][3]));
+            *reinterpret_cast<uint2*>(DST.p[o] + at) = make_uint2(dsb[o][2 * kh], dsb[o][2 * kh + 1]);
+          }
         }
       }
     }
-    if constexpr (STORE) {
+    if constexpr (STORE && ONE_STORE) {
       // the lane's eight keys (4 g + r and 16 + 4 g + r of the block) of its query, at positions
       // 8 g .. 8 g + 7 of the block's 32: one 16-byte store per series and order, a contiguous
       // kilobyte per wave (plain stores: non-temporal ones measured 8% slower)
@@ -1082,53 +1095,103 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
 
 // ---------------------------------------------------------------------------
 // Stored-tile dK / dV kernel: the dQ kernel has written the P and dS series of
-// every visited pair (dense 16-bit rows [bh][L][srow]), so each output takes one
-// series product per block (five products per pair in all instead of eight, and
-// no exponential series here). Per 32-query block the X tile (G for dV, Q for
-// dK) and the block's stored P (or dS) values of the workgroup's 64 keys move by
-// LDS DMA, double-buffered. The stored values are the B operand, read by
-// transpose reads (lane c receives key c's queries 4 g .. 4 g + 3 and 16 + 4 g ..),
-// and masked by admissibility: a pair the dQ kernel did not visit (a block
-// outside its mask range) holds no written value.
-template <int K, int D, int WHAT>
+// every visited pair, so each output takes one series product per block (five
+// products per pair in all instead of eight, and no exponential series here).
+// A workgroup owns KEYS keys (16 per wave: 128 where the tiles fit LDS, so that
+// each Q / G tile read serves twice the keys and two waves share each SIMD, else
+// 64). Per 32-query block the X tile (G for dV, Q for dK) and the block's stored
+// P (or dS) values of the workgroup's keys move by LDS DMA, double-buffered. The
+// stored values are the B operand, read by transpose reads (lane c receives key
+// c's queries 4 g .. 4 g + 3 and 16 + 4 g ..), and masked by admissibility: a
+// pair the dQ kernel did not visit (a block outside its mask range) holds no
+// written value.
+template <int K, int D, int WHAT, int KEYS>
 struct AttnHalfBwdMat {
   static constexpr int KB = 32;
+  static constexpr int WAVES = KEYS / 16;
   static constexpr int NOUT = ((WHAT & 1) ? 1 : 0) + ((WHAT & 2) ? 1 : 0);
   static constexpr size_t xtile = static_cast<size_t>(K + 1) * KB * D * 2;
-  static constexpr size_t stile = static_cast<size_t>(K + 1) * KB * 64 * 2;
+  static constexpr size_t stile = static_cast<size_t>(K + 1) * KB * KEYS * 2;
   static constexpr size_t LDS = 2 * NOUT * (xtile + stile);
-  static constexpr bool fits = LDS <= 160 * 1024 && D >= 32 && K >= 1 && K <= 4;
+  // (128 keys: two waves per SIMD, so at most 256 registers per lane: the output accumulators
+  // of one output, up to 160)
+  static constexpr bool fits = LDS <= 160 * 1024 && D >= 32 && K >= 1 && K <= 4 &&
+                               (KEYS == 64 || NOUT * (K + 1) * (D / 16) * 4 <= 160);
 };
+template <int K, int D, int WHAT>
+constexpr int attn_half_mat_keys() {
+  return AttnHalfBwdMat<K, D, WHAT, 128>::fits ? 128 : 64;
+}
 
-// This wave's DMA of one order of a stored tile: query rows first + 8 wave .. + 7 of the 64 keys
-// from key0 (two 32-key blocks of a head's [srow / 32][rows][32] 16-bit series) into LDS [32][64]
-// (row r: keys key0 .. key0 + 63 of query first + r). Rows past `rows` read the next key block's
-// first rows, or zeros past the head's series: their pairs are inadmissible and masked.
-template <typename T, int K>
-__device__ __forceinline__ void attn_half_dma_stored(T (&tile)[K + 1][32][64], const CPtrs<T>& src, int64_t head,
+// DMA operation i (0 <= i < (K+1) ceil(segments / WAVES)) of this wave's share of rows
+// first .. first + 31 of a head's [rows, D] series into a tile [K+1][32][D] (as
+// attn_half_dma_tile, for a workgroup of WAVES waves).
+template <typename T, int K, int D, int WAVES>
+__device__ __forceinline__ void attn_half_dma_tile_w(T (&tile)[K + 1][32][D], const CPtrs<T>& src, int64_t head,
+                                                     int rows, int first, int lane, int wave, int i) {
+  using P = AttnHalfPipe<K, D>;
+  constexpr int CH = P::CH, RPS = P::RPS, SEGS = P::SEGS, IT = (SEGS + WAVES - 1) / WAVES;
+  const int o = i / IT, it = i % IT;
+  const int seg = it * WAVES + wave;
+  if (SEGS % WAVES != 0 && seg >= SEGS) return;
+  const int row = seg * RPS + lane / CH;
+  const int lch = (lane % CH) ^ P::fk(row);
+  const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * rows * D, rows * D * static_cast<int>(sizeof(T)));
+  lds_dma16(&tile[o][seg * RPS][0], rsrc, ((first + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
+}
+
+// This wave's DMA of one order of a stored tile: its 512 / KEYS query rows (of first .. first + 31)
+// of the KEYS keys from key0 (32-key blocks of a head's [srow / 32][rows][32] 16-bit series) into
+// LDS [32][KEYS] (row r: positions of keys key0 .. key0 + KEYS - 1 of query first + r). Rows past
+// `rows` read the next key block's first rows, or zeros past the head's series: their pairs are
+// inadmissible and masked.
+template <typename T, int K, int KEYS>
+__device__ __forceinline__ void attn_half_dma_stored(T (&tile)[K + 1][32][KEYS], const CPtrs<T>& src, int64_t head,
                                                      int rows, int64_t srow, int first, int key0, int lane, int wave,
                                                      int o) {
-  const int row = 8 * wave + lane / 8, ch = lane % 8;
+  constexpr int CPR = KEYS / 8, RPS = 64 / CPR;   // 16-byte chunks per row, rows per 1 KB segment
+  const int row = RPS * wave + lane / CPR, ch = lane % CPR;
   const int64_t nkb = srow / 32;
   const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * nkb * rows * 32, static_cast<int>(nkb * rows * 32 * 2));
   const int64_t at = ((key0 / 32 + ch / 4) * static_cast<int64_t>(rows) + first + row) * 32 + 8 * (ch % 4);
-  lds_dma16(&tile[o][8 * wave][0], rsrc, static_cast<int>(at * 2));
+  lds_dma16(&tile[o][RPS * wave][0], rsrc, static_cast<int>(at * 2));
 }
 
-template <typename T, int K, int D, int WHAT, bool MASKED>
-__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_half_mat_kernel(
+// Query range [lo, hi) of keys kv_block .. kv_block + KEYS - 1: the union over their 64-key
+// range blocks (an empty one, hi <= lo, adds nothing).
+template <int KEYS>
+__device__ __forceinline__ void attn_query_range_keys(int L, int S, int kv_block, int causal, const int32_t* ranges,
+                                                      int& lo, int& hi) {
+  attn_query_range(L, kv_block, causal, ranges, lo, hi);
+#pragma unroll
+  for (int b = 64; b < KEYS; b += 64) {
+    if (kv_block + b < S) {
+      int l2, h2;
+      attn_query_range(L, kv_block + b, causal, ranges, l2, h2);
+      if (hi <= lo) {
+        lo = l2;
+        hi = h2;
+      } else if (l2 < h2) {
+        lo = min(lo, l2);
+        hi = max(hi, h2);
+      }
+    }
+  }
+}
+
+template <typename T, int K, int D, int WHAT, int KEYS, bool MASKED>
+__global__ __launch_bounds__(KEYS * 4) void taylor_attention_bwd_kv_half_mat_kernel(
     CPtrs<T> Q, CPtrs<T> G, CPtrs<T> PT, CPtrs<T> DST, MPtrs<T> DK, MPtrs<T> DV, int64_t srow, int L, int S,
     const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
     float scale) {
-  using BP = AttnHalfBwdPipe<K, D>;
-  using MT = AttnHalfBwdMat<K, D, WHAT>;
-  using MM = HalfMfma<T>;
-  constexpr int KB = MT::KB, DB = D / 16, OPT = BP::OPT, NOUT = MT::NOUT;
+  using MT = AttnHalfBwdMat<K, D, WHAT, KEYS>;
+  constexpr int KB = MT::KB, DB = D / 16, NOUT = MT::NOUT, WAVES = MT::WAVES;
+  constexpr int OPT = (K + 1) * ((AttnHalfPipe<K, D>::SEGS + WAVES - 1) / WAVES);
   constexpr bool DO_V = (WHAT & 1) != 0, DO_K = (WHAT & 2) != 0;
   constexpr int SV = 0, SK = DO_V ? 1 : 0;   // slots of the dV and dK inputs
   static_assert(MT::fits, "tiles exceed LDS");
   using XTile = T[K + 1][KB][D];
-  using STile = T[K + 1][KB][64];
+  using STile = T[K + 1][KB][KEYS];
   __shared__ __attribute__((aligned(16))) XTile Xt[2][NOUT];
   __shared__ __attribute__((aligned(16))) STile St[2][NOUT];
 
@@ -1136,10 +1199,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int c = lane % 16;
   const int g = lane / 16;
-  const int64_t bh = gridDim.x / static_cast<int64_t>((S + 63) / 64);
-  int64_t head;
-  int slice, kv_block;
-  attn_bwd_kv_item(blockIdx.x, bh, 1, head, slice, kv_block);
+  const int64_t bh = gridDim.x / static_cast<int64_t>((S + KEYS - 1) / KEYS);
+  const int64_t head = blockIdx.x % bh;   // heads fastest: a head's key blocks share an XCD
+  const int kv_block = static_cast<int>(blockIdx.x / bh) * KEYS;
   const int64_t mask_index = attn_mask_index(mmap, head);
   const uint8_t* mask = MASKED ? mask_all + mask_index * L * S : nullptr;
   const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
@@ -1156,7 +1218,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
     }
 
   int lo, hi;
-  attn_query_range(L, kv_block, causal, ranges, lo, hi);
+  attn_query_range_keys<KEYS>(L, S, kv_block, causal, ranges, lo, hi);
   lo = lo / KB * KB;
   if (hi <= lo) lo = hi = 0;   // one fully masked block (q < hi fails): the pipeline always has a first
   const int nblocks = max(1, (hi - lo + KB - 1) / KB);
@@ -1169,13 +1231,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_kv_ha
   auto dma = [&](int buf, int qb0) {
 #pragma unroll
     for (int o = 0; o <= K; ++o) {
-      if constexpr (DO_V) attn_half_dma_stored<T, K>(St[buf][SV], PT, head, L, srow, qb0, kv_block, lane, wave, o);
-      if constexpr (DO_K) attn_half_dma_stored<T, K>(St[buf][SK], DST, head, L, srow, qb0, kv_block, lane, wave, o);
+      if constexpr (DO_V)
+        attn_half_dma_stored<T, K, KEYS>(St[buf][SV], PT, head, L, srow, qb0, kv_block, lane, wave, o);
+      if constexpr (DO_K)
+        attn_half_dma_stored<T, K, KEYS>(St[buf][SK], DST, head, L, srow, qb0, kv_block, lane, wave, o);
     }
 #pragma unroll
     for (int i = 0; i < OPT; ++i) {
-      if constexpr (DO_V) attn_half_dma_tile<T, K, D>(Xt[buf][SV], G, head, L, qb0, lane, wave, i);
-      if constexpr (DO_K) attn_half_dma_tile<T, K, D>(Xt[buf][SK], Q, head, L, qb0, lane, wave, i);
+      if constexpr (DO_V) attn_half_dma_tile_w<T, K, D, WAVES>(Xt[buf][SV], G, head, L, qb0, lane, wave, i);
+      if constexpr (DO_K) attn_half_dma_tile_w<T, K, D, WAVES>(Xt[buf][SK], Q, head, L, qb0, lane, wave, i);
     }
   };
   dma(0, lo);
@@ -1275,7 +1339,7 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
   MPtrs<T> pt{}, dst{};
   CPtrs<T> pt_in{}, dst_in{};
   if constexpr (K >= 1 && K <= 4 && AttnHalfBwdPipe<K, D>::fits_q && Sh::SL_Q == 1 &&
-                AttnHalfBwdMat<K, D, 1>::fits && AttnHalfBwdMat<K, D, 2>::fits) {
+                AttnHalfBwdMat<K, D, 1, 64>::fits && AttnHalfBwdMat<K, D, 2, 64>::fits) {
     mat = a.materialize && rows > 0 && (a.dk != nullptr || a.dv != nullptr) && q_pipe_ok && kv_pipe_ok &&
           (a.lq + 32) * srow * 2 < (int64_t{1} << 31);
     if (mat) {
@@ -1333,20 +1397,21 @@ static int launch_attention_bwd_half_kd(const AttnBwdArgs& a) {
     }
   }
   if (mat) {
-    if constexpr (K >= 1 && K <= 4 && AttnHalfBwdMat<K, D, 1>::fits && AttnHalfBwdMat<K, D, 2>::fits) {
-      const dim3 grid(static_cast<unsigned>((a.lk + 63) / 64 * a.bh));
+    if constexpr (K >= 1 && K <= 4 && AttnHalfBwdMat<K, D, 1, 64>::fits && AttnHalfBwdMat<K, D, 2, 64>::fits) {
 #define PT_ATTN_BWD_KV_HALF_MAT(WHAT)                                                                        \
   do {                                                                                                       \
+    constexpr int KEYS = attn_half_mat_keys<K, D, WHAT>();                                                   \
+    const dim3 grid(static_cast<unsigned>((a.lk + KEYS - 1) / KEYS * a.bh)), mblock(KEYS * 4);               \
     if (a.mask != nullptr)                                                                                   \
-      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, true><<<grid, block, 0, a.stream>>>(            \
+      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, KEYS, true><<<grid, mblock, 0, a.stream>>>(     \
           q, g, pt_in, dst_in, dk, dv, srow, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale);        \
     else                                                                                                     \
-      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, false><<<grid, block, 0, a.stream>>>(           \
+      taylor_attention_bwd_kv_half_mat_kernel<T, K, D, WHAT, KEYS, false><<<grid, mblock, 0, a.stream>>>(    \
           q, g, pt_in, dst_in, dk, dv, srow, L, S, a.mask, a.mask_map, a.mask_ranges, causal, scale);        \
     PT_LAUNCH_CHECK();                                                                                       \
   } while (0)
       bool fused = false;
-      if constexpr (AttnHalfBwdMat<K, D, 3>::fits) {
+      if constexpr (AttnHalfBwdMat<K, D, 3, 64>::fits) {
         if (a.dk != nullptr && a.dv != nullptr) {
           PT_ATTN_BWD_KV_HALF_MAT(3);
           fused = true;
