@@ -455,7 +455,9 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   const int64_t lk = k[0].size(1);
   c10::DeviceGuard guard(q[0].device());
   const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention_bwd");
-  if (mask.add && dtype == at::kFloat) materialize = 0;   // float32 recomputes with an additive mask
+  // float32 and float64 recompute with an additive mask (materialize is ignored); the 16-bit
+  // stored tiles carry it
+  if (mask.add && (dtype == at::kFloat || dtype == at::kDouble)) materialize = 0;
   Tensor dq = at::empty({degree + 1, bh, lq, d}, q[0].options());
   Tensor dk = at::empty({degree + 1, bh, lk, d}, q[0].options());
   Tensor dv = at::empty_like(dk);
