@@ -1145,12 +1145,22 @@ __device__ __forceinline__ void attn_half_dma_tile_w(T (&tile)[K + 1][32][D], co
 // LDS [32][KEYS] (row r: positions of keys key0 .. key0 + KEYS - 1 of query first + r). Rows past
 // `rows` read the next key block's first rows, or zeros past the head's series: their pairs are
 // inadmissible and masked.
+// 16-byte chunk swizzle of a stored tile [32][KEYS] in LDS (physical chunk = logical ^ f(row)):
+// rows of 256 (128) bytes all start on bank 0 (0 or 32), so the transpose reads of rows
+// 4 g .. 4 g + 3 at four chunks would fall on 8 banks; with f the 64 pieces of a read spread
+// evenly over the 16 chunks, four to a chunk (SQ_LDS_BANK_CONFLICT had been 28% of the cycles).
+template <int KEYS>
+__device__ __forceinline__ int attn_stored_swz(int row) {
+  return KEYS == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
+}
+
 template <typename T, int K, int KEYS>
 __device__ __forceinline__ void attn_half_dma_stored(T (&tile)[K + 1][32][KEYS], const CPtrs<T>& src, int64_t head,
                                                      int rows, int64_t srow, int first, int key0, int lane, int wave,
                                                      int o) {
   constexpr int CPR = KEYS / 8, RPS = 64 / CPR;   // 16-byte chunks per row, rows per 1 KB segment
-  const int row = RPS * wave + lane / CPR, ch = lane % CPR;
+  const int row = RPS * wave + lane / CPR;
+  const int ch = (lane % CPR) ^ attn_stored_swz<KEYS>(row);   // the logical chunk this lane's slot holds
   const int64_t nkb = srow / 32;
   const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * nkb * rows * 32, static_cast<int>(nkb * rows * 32 * 2));
   const int64_t at = ((key0 / 32 + ch / 4) * static_cast<int64_t>(rows) + first + row) * 32 + 8 * (ch % 4);
@@ -1276,10 +1286,11 @@ __global__ __launch_bounds__(KEYS * 4) void taylor_attention_bwd_kv_half_mat_ker
       u32x4 b[K + 1], none[1];
       // the wave's keys kv_block + 16 wave + c: block wave / 2, key 16 (wave % 2) + c at position
       // 8 (c / 4) + 4 (wave % 2) + c % 4; this lane addresses the four positions of lanes 4 ta ..
-      const int col = 32 * (wave / 2) + 4 * (wave % 2) + 8 * ta;
+      const int lch = 4 * (wave / 2) + ta, off = 4 * (wave % 2);   // logical chunk, offset in it
+      const int r0 = 4 * g + tj, r1 = 16 + 4 * g + tj;
+      const int c0 = 8 * (lch ^ attn_stored_swz<KEYS>(r0)) + off, c1 = 8 * (lch ^ attn_stored_swz<KEYS>(r1)) + off;
 #pragma unroll
-      for (int o = 0; o <= K; ++o)
-        b[o] = lds_read_tr16x2(&st[o][4 * g + tj][col], &st[o][16 + 4 * g + tj][col]) & keep;
+      for (int o = 0; o <= K; ++o) b[o] = lds_read_tr16x2(&st[o][r0][c0], &st[o][r1][c1]) & keep;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         u32x4 x[K + 1];
