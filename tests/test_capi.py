@@ -107,3 +107,24 @@ def test_attention_key_split_plan():
     # bytes: chunks x rows x (1 + (K+1)(1+d)) values
     b = size(1, 3, 4, 4, 4, 1, 128, 128, 64)
     assert b % (128 * (1 + 4 * 65) * 8) == 0
+
+
+def test_attention_backward_workspace_sizes():
+    # float32 / float64: the rowsum(G O) series in the accumulator type, plus with materialize the
+    # P and dS tiles (2 (K+1) bh ceil(L/16) ceil(S/16) tiles of 256 values); 16-bit: the series in
+    # float32, plus at degrees 1..4 dense 16-bit tiles [2 (K+1)][bh][L][S rounded up to 128]
+    lib = _lib.load()
+    size = lib.pt_taylor_attention_bwd_workspace_size
+    r256 = lambda x: (x + 255) // 256 * 256
+    bh, L, S = 3, 100, 70
+    for code, acc in ((0, 4), (1, 8)):
+        assert size(code, 2, bh, L, S, 0) == 3 * bh * L * acc
+    tiles32 = r256(bh * 7 * 5 * 256 * 4)
+    assert size(0, 2, bh, L, S, 1) == r256(3 * bh * L * 4) + 2 * 3 * tiles32
+    for code in (2, 3):   # bfloat16, float16
+        assert size(code, 2, bh, L, S, 0) == 3 * bh * L * 4
+        assert size(code, 2, bh, L, S, 1) == r256(3 * bh * L * 4) + 2 * 3 * r256(bh * L * 128 * 2)
+        assert size(code, 0, bh, L, S, 1) == bh * L * 4            # degree 0: recomputed, series only
+        assert size(code, 5, bh, L, S, 1) == 6 * bh * L * 4        # degrees 5..8: recomputed
+        assert size(code, 4, bh, L, 129, 1) == r256(5 * bh * L * 4) + 2 * 5 * r256(bh * L * 256 * 2)
+    assert size(0, 9, bh, L, S, 0) == 0 and size(0, 2, -1, L, S, 0) == 0   # out of range
