@@ -36,24 +36,36 @@
 
 namespace pt {
 
-template <int AO, int BO>
+// Workgroup tile: WMW x WNW waves, each owning FM x FN MFMA blocks of 16 x 16 of every C_k. The
+// narrow tile (64 x 64, 4 waves of 32 x 32) leaves LDS for two workgroups per CU; the wide tile
+// (128 x 128, 8 waves of 64 x 32) reads a third fewer LDS bytes per MFMA and half the HBM
+// re-reads, and fills one CU with its 8 waves when both operands are series of degree <= 4.
+template <int AO, int BO, bool WIDE>
 struct CauchyHalfTile {
-  static constexpr int BM = 64, BN = 64, BK = 32;
-  static constexpr size_t LDS = 2ull * (AO + BO) * 64 * BK * 2;
+  static constexpr int WMW = 2, WNW = WIDE ? 4 : 2, FM = WIDE ? 4 : 2, FN = 2;
+  static constexpr int BM = 16 * FM * WMW, BN = 16 * FN * WNW, BK = 32;
+  static constexpr int kWaves = WMW * WNW, kThreads = kWaves * kWave;
+  static constexpr size_t LDS = 2ull * (AO * BM + BO * BN) * BK * 2;
+  // every order tile of A ([BM][BK]) and of B ([BK][BN] or [BN][BK]) is one 1 KB DMA segment per wave
+  static_assert(BM * BK * 2 == 1024 * kWaves && BN * BK * 2 == 1024 * kWaves, "one DMA segment per wave");
 };
 
-// physical 16-byte chunk of logical chunk ch in row r of a [row][32] tile / of a [k][64] tile
+// physical 16-byte chunk of logical chunk ch in row r of a [row][32] tile / of a [k][BN] tile
+// (BN = 64: 128-byte rows, two rows per bank sweep; BN = 128: 256-byte rows, one per sweep)
 __host__ __device__ __forceinline__ int cauchy_swz_rows(int r, int ch) { return ch ^ ((r >> 2) & 3); }
+template <bool WIDE>
 __host__ __device__ __forceinline__ int cauchy_swz_k(int k, int ch) {
+  if constexpr (WIDE) return ch ^ (2 * ((k & 3) | (((k >> 3) & 1) << 2)));
   return ch ^ (2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1)));
 }
 
-template <typename T, int K, int AO, int BO, bool TRANS_B>
-__global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPtrs<T> B, MPtrs<T> C, int M, int N,
-                                                                 int Kd, int64_t a_bs, int64_t b_bs) {
-  using Tile = CauchyHalfTile<AO, BO>;
+template <typename T, int K, int AO, int BO, bool TRANS_B, bool WIDE>
+__global__ __launch_bounds__((CauchyHalfTile<AO, BO, WIDE>::kThreads)) void cauchy_matmul_half_kernel(
+    CPtrs<T> A, CPtrs<T> B, MPtrs<T> C, int M, int N, int Kd, int64_t a_bs, int64_t b_bs) {
+  using Tile = CauchyHalfTile<AO, BO, WIDE>;
   using MM = HalfMfma<T>;
-  constexpr int BM = Tile::BM, BN = Tile::BN, BK = Tile::BK;
+  constexpr int BM = Tile::BM, BN = Tile::BN, BK = Tile::BK, FM = Tile::FM, FN = Tile::FN;
+  constexpr int CPR = BN / 8;   // 16-byte chunks per k row of a [BK][BN] B tile
   static_assert(Tile::LDS <= 160 * 1024, "LDS budget");
   static_assert((AO == 1 || AO == K + 1) && (BO == 1 || BO == K + 1), "operand orders are 1 or K+1");
 
@@ -63,7 +75,7 @@ __global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPt
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int c = lane % 16, g = lane / 16;
-  const int wm = wave / 2, wn = wave % 2;
+  const int wm = wave / Tile::WNW, wn = wave % Tile::WNW;
   const int tile_m = blockIdx.y * BM, tile_n = blockIdx.x * BN;
   const int64_t batch = blockIdx.z;
   const int a_bytes = M * Kd * static_cast<int>(sizeof(T));
@@ -78,7 +90,7 @@ __global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPt
       const int voff = (gm < M && gk < Kd) ? (gm * Kd + gk) * static_cast<int>(sizeof(T)) : kBufferOutOfRange;
 #pragma unroll
       for (int o = 0; o < AO; ++o)
-        lds_dma16(&As[buf][o][16 * wave * BK], buffer_rsrc(A.p[o] + batch * a_bs, a_bytes), voff);
+        lds_dma16(&As[buf][o][512 * wave], buffer_rsrc(A.p[o] + batch * a_bs, a_bytes), voff);
     }
     int voff;
     if constexpr (TRANS_B) {   // B stored [N][Kd]: as A
@@ -86,25 +98,43 @@ __global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPt
       const int lch = cauchy_swz_rows(row, lane % 4);
       const int gn = tile_n + row, gk = k0 + 8 * lch;
       voff = (gn < N && gk < Kd) ? (gn * Kd + gk) * static_cast<int>(sizeof(T)) : kBufferOutOfRange;
-    } else {                   // B stored [Kd][N]: k rows 8 wave + lane / 8, physical chunk lane % 8
-      const int kr = 8 * wave + lane / 8;
-      const int lch = cauchy_swz_k(kr, lane % 8);
+    } else {                   // B stored [Kd][N]: k rows (64 / CPR) wave + lane / CPR, physical chunk lane % CPR
+      const int kr = (64 / CPR) * wave + lane / CPR;
+      const int lch = cauchy_swz_k<WIDE>(kr, lane % CPR);
       const int gk = k0 + kr, gn = tile_n + 8 * lch;
       voff = (gk < Kd && gn < N) ? (gk * N + gn) * static_cast<int>(sizeof(T)) : kBufferOutOfRange;
     }
 #pragma unroll
     for (int o = 0; o < BO; ++o)
-      lds_dma16(&Bs[buf][o][(TRANS_B ? 16 : 8) * wave * (TRANS_B ? BK : BN)], buffer_rsrc(B.p[o] + batch * b_bs, b_bytes),
-                voff);
+      lds_dma16(&Bs[buf][o][512 * wave], buffer_rsrc(B.p[o] + batch * b_bs, b_bytes), voff);
   };
 
-  floatx4 acc[K + 1][2][2];
+  // operand reads: A^T columns (rows of A) and B^T rows (columns of B) of one order
+  auto read_a = [&](int buf, int o, int fm) {
+    const int row = FM * 16 * wm + 16 * fm + c;
+    return *reinterpret_cast<const u32x4*>(&As[buf][o][row * BK + cauchy_swz_rows(row, g) * 8]);
+  };
+  auto read_b = [&](int buf, int o, int fn) {
+    const int n0 = FN * 16 * wn + 16 * fn;
+    if constexpr (TRANS_B) {
+      const int row = n0 + c;
+      return *reinterpret_cast<const u32x4*>(&Bs[buf][o][row * BK + cauchy_swz_rows(row, g) * 8]);
+    } else {
+      const int j = c / 4, a = c % 4;
+      const int k1 = 8 * g + j, k2 = 8 * g + 4 + j;
+      const int lch = n0 / 8 + a / 2, e = 4 * (a % 2);
+      return lds_read_tr16x2(&Bs[buf][o][k1 * BN + cauchy_swz_k<WIDE>(k1, lch) * 8 + e],
+                             &Bs[buf][o][k2 * BN + cauchy_swz_k<WIDE>(k2, lch) * 8 + e]);
+    }
+  };
+
+  floatx4 acc[K + 1][FM][FN];
 #pragma unroll
   for (int o = 0; o <= K; ++o)
 #pragma unroll
-    for (int fm = 0; fm < 2; ++fm)
+    for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < 2; ++fn) acc[o][fm][fn] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int fn = 0; fn < FN; ++fn) acc[o][fm][fn] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int chunks = (Kd + BK - 1) / BK;
   issue(0, 0);
@@ -114,43 +144,50 @@ __global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPt
     __syncthreads();                 // ... and every wave's; chunk ch-1's buffer is free
     if (ch + 1 < chunks) issue(buf ^ 1, (ch + 1) * BK);
 
-    // operands: A^T columns (rows of A) and B^T rows (columns of B), every order
-    u32x4 af[AO][2], bf[BO][2];
+    u32x4 bf[BO][FN];
+    if constexpr (!WIDE) {   // every operand of the chunk in registers, products by output order
+      u32x4 af[AO][FM];
 #pragma unroll
-    for (int o = 0; o < AO; ++o)
+      for (int o = 0; o < AO; ++o)
 #pragma unroll
-      for (int fm = 0; fm < 2; ++fm) {
-        const int row = 32 * wm + 16 * fm + c;
-        af[o][fm] = *reinterpret_cast<const u32x4*>(&As[buf][o][row * BK + cauchy_swz_rows(row, g) * 8]);
-      }
+        for (int fm = 0; fm < FM; ++fm) af[o][fm] = read_a(buf, o, fm);
 #pragma unroll
-    for (int o = 0; o < BO; ++o)
+      for (int o = 0; o < BO; ++o)
 #pragma unroll
-      for (int fn = 0; fn < 2; ++fn) {
-        const int n0 = 32 * wn + 16 * fn;
-        if constexpr (TRANS_B) {
-          const int row = n0 + c;
-          bf[o][fn] = *reinterpret_cast<const u32x4*>(&Bs[buf][o][row * BK + cauchy_swz_rows(row, g) * 8]);
-        } else {
-          const int j = c / 4, a = c % 4;
-          const int k1 = 8 * g + j, k2 = 8 * g + 4 + j;
-          const int lch = n0 / 8 + a / 2, e = 4 * (a % 2);
-          bf[o][fn] = lds_read_tr16x2(&Bs[buf][o][k1 * BN + cauchy_swz_k(k1, lch) * 8 + e],
-                                      &Bs[buf][o][k2 * BN + cauchy_swz_k(k2, lch) * 8 + e]);
+        for (int fn = 0; fn < FN; ++fn) bf[o][fn] = read_b(buf, o, fn);
+#pragma unroll
+      for (int k = 0; k <= K; ++k)
+#pragma unroll
+        for (int i = 0; i <= k; ++i) {
+          const int j = k - i;
+          if (i < AO && j < BO) {   // compile-time after unrolling
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+              for (int fn = 0; fn < FN; ++fn) acc[k][fm][fn] = MM::mma(bf[j][fn], af[i][fm], acc[k][fm][fn]);
+          }
+        }
+    } else {                 // B operands held, A read one order at a time (register budget of 2 waves/SIMD)
+#pragma unroll
+      for (int o = 0; o < BO; ++o)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) bf[o][fn] = read_b(buf, o, fn);
+#pragma unroll
+      for (int i = 0; i < AO; ++i) {
+        u32x4 af[FM];
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) af[fm] = read_a(buf, i, fm);
+#pragma unroll
+        for (int j = 0; j < BO; ++j) {
+          if (i + j <= K) {   // compile-time after unrolling
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+              for (int fn = 0; fn < FN; ++fn) acc[i + j][fm][fn] = MM::mma(bf[j][fn], af[fm], acc[i + j][fm][fn]);
+          }
         }
       }
-#pragma unroll
-    for (int k = 0; k <= K; ++k)
-#pragma unroll
-      for (int i = 0; i <= k; ++i) {
-        const int j = k - i;
-        if (i < AO && j < BO) {   // compile-time after unrolling
-#pragma unroll
-          for (int fm = 0; fm < 2; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < 2; ++fn) acc[k][fm][fn] = MM::mma(bf[j][fn], af[i][fm], acc[k][fm][fn]);
-        }
-      }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
 
@@ -160,11 +197,11 @@ __global__ __launch_bounds__(256) void cauchy_matmul_half_kernel(CPtrs<T> A, CPt
   for (int o = 0; o <= K; ++o) {
     T* base = C.p[o] + batch * static_cast<int64_t>(M) * N;
 #pragma unroll
-    for (int fm = 0; fm < 2; ++fm)
+    for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < 2; ++fn) {
-        const int row = tile_m + 32 * wm + 16 * fm + c;
-        const int col = tile_n + 32 * wn + 16 * fn + 4 * g;
+      for (int fn = 0; fn < FN; ++fn) {
+        const int row = tile_m + FM * 16 * wm + 16 * fm + c;
+        const int col = tile_n + FN * 16 * wn + 16 * fn + 4 * g;
         if (row >= M) continue;
         const floatx4 v = acc[o][fm][fn];
         T* p = base + static_cast<int64_t>(row) * N + col;
@@ -191,17 +228,28 @@ __global__ __launch_bounds__(256) void cauchy_half_zero_orders_kernel(MPtrs<T> C
       reinterpret_cast<uint16_t*>(C.p[o])[i] = 0;
 }
 
-template <typename T, int K, int AO, int BO>
-static int launch_cauchy_half_orders(const CauchyArgs& a, const CPtrs<T>& A, const CPtrs<T>& B, const MPtrs<T>& C) {
-  using Tile = CauchyHalfTile<AO, BO>;
+template <typename T, int K, int AO, int BO, bool WIDE>
+static int launch_cauchy_half_tile(const CauchyArgs& a, const CPtrs<T>& A, const CPtrs<T>& B, const MPtrs<T>& C) {
+  using Tile = CauchyHalfTile<AO, BO, WIDE>;
   const dim3 grid((a.n + Tile::BN - 1) / Tile::BN, (a.m + Tile::BM - 1) / Tile::BM, a.batch);
+  const dim3 block(Tile::kThreads);
   const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), Kd = static_cast<int>(a.k);
   if (a.trans_b)
-    cauchy_matmul_half_kernel<T, K, AO, BO, true><<<grid, dim3(256), 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
+    cauchy_matmul_half_kernel<T, K, AO, BO, true, WIDE><<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
   else
-    cauchy_matmul_half_kernel<T, K, AO, BO, false><<<grid, dim3(256), 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
+    cauchy_matmul_half_kernel<T, K, AO, BO, false, WIDE><<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
   PT_LAUNCH_CHECK();
   return PT_OK;
+}
+
+// The wide tile where its LDS fits, its (K+1) x 32 accumulator registers leave room for the
+// operands within 256 (K <= 4), and both output sides span at least two of its tiles.
+template <typename T, int K, int AO, int BO>
+static int launch_cauchy_half_orders(const CauchyArgs& a, const CPtrs<T>& A, const CPtrs<T>& B, const MPtrs<T>& C) {
+  if constexpr (K <= 4 && CauchyHalfTile<AO, BO, true>::LDS <= 160 * 1024) {
+    if (a.m >= 256 && a.n >= 256) return launch_cauchy_half_tile<T, K, AO, BO, true>(a, A, B, C);
+  }
+  return launch_cauchy_half_tile<T, K, AO, BO, false>(a, A, B, C);
 }
 
 template <typename T, int K>

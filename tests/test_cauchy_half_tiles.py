@@ -1,0 +1,114 @@
+"""CPU replay of the 16-bit Cauchy matmul's LDS tiles (no GPU).
+
+`csrc/cauchy_matmul_half.inl` moves operand tiles into LDS with the LDS DMA
+(`buffer_load_dwordx4 ... lds`: lane l's 16 bytes land at byte 16 l of its
+wave's 1 KB segment) and picks, per lane, which logical 16-byte chunk to load so
+that the tile is XOR-swizzled. The MFMA operands are then read back with 16-byte
+reads (A, and B stored [n][k]) or with pairs of `ds_read_b64_tr_b16` transpose
+reads (B stored [k][n]). This replay places every DMA chunk, performs every
+operand read of every wave for both workgroup tiles (narrow 64 x 64, wide
+128 x 128), and checks that
+
+* the DMA covers each element of the tile exactly once;
+* every lane receives exactly the eight contraction elements its MFMA operand
+  needs (row or column `16 f + lane % 16`, elements `8 (lane / 16) ... + 7`);
+* each read pass (16 lanes of a 16-byte read, 32 lanes of an 8-byte read) hits
+  64 distinct 4-byte banks.
+
+The transpose read's lane mapping (within each 16-lane group, lane 4a + b
+receives element b of the 8-byte pieces addressed by lanes a, a+4, a+8, a+12)
+was probed on gfx950. A swizzle that dropped a term, or a read that used the
+other tile's swizzle, fails the second or third check.
+"""
+
+import pytest
+
+BK = 32
+
+
+def swz_rows(r, ch):   # cauchy_swz_rows
+    return ch ^ ((r >> 2) & 3)
+
+
+def swz_k(wide, k, ch):   # cauchy_swz_k<WIDE>
+    if wide:
+        return ch ^ (2 * ((k & 3) | (((k >> 3) & 1) << 2)))
+    return ch ^ (2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1)))
+
+
+def tile(wide):
+    wmw, wnw, fm, fn = (2, 4, 4, 2) if wide else (2, 2, 2, 2)
+    return dict(WMW=wmw, WNW=wnw, FM=fm, FN=fn, BM=16 * fm * wmw, BN=16 * fn * wnw, waves=wmw * wnw)
+
+
+def banks_distinct(addrs, nbytes):
+    """addrs: half-element addresses of one read pass; each lane reads nbytes."""
+    banks = [((2 * a) // 4 + w) % 64 for a in addrs for w in range(nbytes // 4)]
+    return len(set(banks)) == len(banks) == 64
+
+
+def rows_tile_lds(rows, waves):
+    """DMA placement of a [rows][BK] tile: half address -> logical (row, k)."""
+    lds = {}
+    for wave in range(waves):
+        for lane in range(64):
+            row = 16 * wave + lane // 4
+            lch = swz_rows(row, lane % 4)
+            for e in range(8):
+                lds[512 * wave + 8 * lane + e] = (row, 8 * lch + e)
+    return lds
+
+
+@pytest.mark.parametrize("wide", [False, True])
+@pytest.mark.parametrize("side", ["a", "b_trans"])
+def test_row_tiles(wide, side):
+    t = tile(wide)
+    rows = t["BM"] if side == "a" else t["BN"]
+    lds = rows_tile_lds(rows, t["waves"])
+    assert sorted(lds.values()) == [(r, k) for r in range(rows) for k in range(BK)]
+    for wave in range(t["waves"]):
+        wm, wn = wave // t["WNW"], wave % t["WNW"]
+        for f in range(t["FM"] if side == "a" else t["FN"]):
+            base = t["FM"] * 16 * wm + 16 * f if side == "a" else t["FN"] * 16 * wn + 16 * f
+            addrs = []
+            for lane in range(64):
+                c, g = lane % 16, lane // 16
+                row = base + c
+                addr = row * BK + swz_rows(row, g) * 8
+                addrs.append(addr)
+                assert [lds[addr + e] for e in range(8)] == [(row, 8 * g + e) for e in range(8)]
+            for p in range(4):
+                assert banks_distinct(addrs[16 * p:16 * p + 16], 16)
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_kn_tile_transpose_reads(wide):
+    t = tile(wide)
+    bn, cpr = t["BN"], t["BN"] // 8
+    lds = {}
+    for wave in range(t["waves"]):
+        for lane in range(64):
+            kr = (64 // cpr) * wave + lane // cpr
+            lch = swz_k(wide, kr, lane % cpr)
+            for e in range(8):
+                lds[512 * wave + 8 * lane + e] = (kr, 8 * lch + e)
+    assert sorted(lds.values()) == [(k, n) for k in range(BK) for n in range(bn)]
+    for wn in range(t["WNW"]):
+        for fn in range(t["FN"]):
+            n0 = t["FN"] * 16 * wn + 16 * fn
+            first, second = [], []
+            for lane in range(64):
+                c, g = lane % 16, lane // 16
+                j, a = c // 4, c % 4
+                k1, k2 = 8 * g + j, 8 * g + 4 + j
+                lch, e = n0 // 8 + a // 2, 4 * (a % 2)
+                first.append(k1 * bn + swz_k(wide, k1, lch) * 8 + e)
+                second.append(k2 * bn + swz_k(wide, k2, lch) * 8 + e)
+            for lane in range(64):
+                c, g = lane % 16, lane // 16
+                grp, a, b = 16 * g, c // 4, c % 4
+                got = [lds[first[grp + a + 4 * q] + b] for q in range(4)]
+                got += [lds[second[grp + a + 4 * q] + b] for q in range(4)]
+                assert got == [(8 * g + s, n0 + c) for s in range(8)]
+            for addrs in (first, second):
+                assert banks_distinct(addrs[:32], 8) and banks_distinct(addrs[32:], 8)

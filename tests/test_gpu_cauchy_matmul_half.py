@@ -74,6 +74,23 @@ def test_every_degree_both_layouts(dtype, degree, trans_b):
 
 
 @pytest.mark.parametrize("dtype", HALF)
+@pytest.mark.parametrize("degree", [0, 1, 2, 4])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("orders", ["both", "left", "right"])
+@pytest.mark.parametrize("m,kd,n", [(256, 64, 256), (300, 136, 264), (520, 40, 392)])
+def test_wide_tile_ragged_edges(dtype, degree, trans_b, orders, m, kd, n):
+    # outputs of at least 256 x 256 at degree <= 4 run the 128 x 128 workgroup tile; these shapes
+    # leave partial tiles on both output sides and a partial last contraction chunk
+    A = _series((m, kd), degree if orders != "right" else 0, 7, dtype)
+    B = _series((n, kd) if trans_b else (kd, n), degree if orders != "left" else 0, 8, dtype)
+    flat = lambda cs: [c.unsqueeze(0).cuda() for c in cs]
+    C = _ops.cauchy_matmul(flat(A), flat(B), degree, trans_b)
+    want = oracle.matmul(_up(A), [b.t() for b in _up(B)] if trans_b else _up(B))
+    want += [torch.zeros_like(want[0])] * (degree + 1 - len(want))
+    _check([c[0] for c in C], want, dtype)
+
+
+@pytest.mark.parametrize("dtype", HALF)
 @pytest.mark.parametrize("side", ["left", "right"])
 def test_plain_operand_uses_one_order(dtype, side):
     degree = 4
