@@ -1,8 +1,9 @@
 """Benchmark of the gfx950 truncated-Taylor kernels on benchmark configs 2-5 (shapes in each workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload attention|attention_dense|attention_bf16|attention_window|attention_bwd|
-                                attention_bwd_bf16|attention_bwd_window|matmul|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
+                    [--workload attention|attention_dense|attention_bf16|attention_fp64|attention_window|
+                                attention_bwd|attention_bwd_bf16|attention_bwd_window|matmul|matmul_bf16|
+                                matmul_fp64|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
 
@@ -13,11 +14,14 @@ workload (benchmark config 1) times its whole pipeline through the PolyTensor
 API per step, and again as the replay of a HIP graph holding one step
 (``graph``: ms per replay and the graph's kernel count, the launches per step). The timed region is K back-to-back
 steps on the current stream, bracketed by torch.cuda.synchronize() and timed
-with HIP events on that stream; ``value`` is the workload's throughput and
+with HIP events on that stream (``ms_per_step``, the mean); ``ms_median`` is the
+median over 21 further steps of each step's own event interval. ``value`` is the
+workload's throughput (from the mean) and
 ``roofline`` compares it to MI355X's published peak (fp32 MFMA 157.3 TFLOP/s,
-HBM 8 TB/s). ``cpu_baseline`` times the CPU oracle (the op-for-op restatement
-of the reference's general path) on a bounded sample of the same workload on
-this host. For memory-bound workloads ``roofline.stream_ceiling`` is the measured rate
+fp64 MFMA 78.6 TFLOP/s, bf16 MFMA 2.5 PFLOP/s, HBM 8 TB/s). ``cpu_baseline``
+times the CPU oracle (the op-for-op restatement of the reference's general
+path) on a bounded sample of the same workload on this host: the median of
+three timings after one warm-up run. For memory-bound workloads ``roofline.stream_ceiling`` is the measured rate
 of a plain streaming read or copy of the same byte count on the same GPU (the
 library's probe kernels), a practical HBM ceiling beside the published peak. Rank 0 prints one JSON line.
 """
@@ -331,6 +335,36 @@ def wl_attention_bf16(device):
                 cpu=lambda: cpu_attention(L, d, K, heads=8, dtype="bf16"))
 
 
+def wl_attention_fp64(device):
+    """Config 3's shape and inputs (B=4 H=16 L=2048 d=128, K=4, causal, line inputs, scale 1/sqrt(128))
+    in float64: the fp64 MFMA kernels (v_mfma_f64_16x16x4_f64, fp64 scores, series and accumulators).
+    Work is the same dense-series count; the roofline is the fp64 MFMA peak (78.6 TFLOP/s)."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(2, device)
+
+    def series():
+        base = torch.randn(B * H, L, d, generator=g, device=device, dtype=torch.float64) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device, dtype=torch.float64)
+        return [base, direction] + [torch.zeros_like(base) for _ in range(2, K + 1)]
+
+    q, k, v = series(), series(), series()
+    scale = 1 / math.sqrt(d)
+
+    def step():
+        return _ops.taylor_attention_fwd(q, k, v, None, True, scale, K)
+
+    pairs = (K + 1) * (K + 2) // 2
+    flops = 2 * pairs * 2 * d * B * H * L * (L + 1) / 2
+    nbytes = 4 * (K + 1) * B * H * L * d * 8
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_FP64_MFMA,
+                bytes=nbytes, kernel="taylor_attention_fp64", dtype="fp64",
+                workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} fp64 causal line inputs",
+                cpu=lambda: cpu_attention(L, d, K, heads=16, dtype="fp64"))
+
+
 def wl_attention_dense(device):
     """Config 3 with dense random orders 2..4 (N(0,1) 0.5^k) instead of a line: the same kernel
     and work count, with no zero input orders."""
@@ -411,6 +445,28 @@ def wl_matmul_bf16(device):
                 bytes=3 * (K + 1) * n * n * 2, kernel="cauchy_matmul_bf16", dtype="bf16 (fp32 accumulate)",
                 workload=f"cauchy_matmul [{K + 1},{n},{n}] x [{K + 1},{n},{n}] bf16",
                 cpu=lambda: cpu_matmul(n, K, dtype="bf16"))
+
+
+def wl_matmul_fp64(device):
+    """Config 2's shape and inputs ([5, 4096, 4096] x [5, 4096, 4096], K=4, coefficient k scaled by
+    0.5^k) in float64: the fp64 MFMA kernel (v_mfma_f64_16x16x4_f64, fp64 accumulation). The roofline
+    is the fp64 MFMA peak (78.6 TFLOP/s)."""
+    import torch
+    from polytensors_amd import _ops
+
+    K, n = 4, 4096
+    g = _gen(1, device)
+    a = [torch.randn(1, n, n, generator=g, device=device, dtype=torch.float64) * 0.5 ** k for k in range(K + 1)]
+    b = [torch.randn(1, n, n, generator=g, device=device, dtype=torch.float64) * 0.5 ** k for k in range(K + 1)]
+
+    def step():
+        return _ops.cauchy_matmul(a, b, K, False)
+
+    pairs = (K + 1) * (K + 2) // 2
+    return dict(step=step, work=2 * pairs * n ** 3, unit="TFLOP/s", bound="mfma", peak=PEAK_FP64_MFMA,
+                bytes=3 * (K + 1) * n * n * 8, kernel="cauchy_matmul_fp64", dtype="fp64",
+                workload=f"cauchy_matmul [{K + 1},{n},{n}] x [{K + 1},{n},{n}] fp64",
+                cpu=lambda: cpu_matmul(n, K, dtype="fp64"))
 
 
 def wl_norm(device):
@@ -516,7 +572,8 @@ def wl_ce_bwd(device):
                 cpu=lambda: cpu_ce_bwd(rows, classes, K))
 
 
-WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "matmul_bf16": wl_matmul_bf16, "norm": wl_norm,
+WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "matmul_bf16": wl_matmul_bf16,
+             "matmul_fp64": wl_matmul_fp64, "attention_fp64": wl_attention_fp64, "norm": wl_norm,
              "ce": wl_ce,
              "activation": wl_activation, "norm_bwd": wl_norm_bwd, "ce_bwd": wl_ce_bwd,
              "attention_bwd": wl_attention_bwd, "attention_bwd_bf16": wl_attention_bwd_bf16,
@@ -546,14 +603,15 @@ def cpu_attention(L, d, K, heads=64, dtype=None):
 
     g = torch.Generator().manual_seed(2)
     q, k, v = ([torch.randn(1, 1, L, d, generator=g) * (0.5 ** o) for o in range(K + 1)] for _ in range(3))
-    if dtype == "bf16":   # the reference's general path on bf16 coefficients (torch's CPU bf16 ops)
-        q, k, v = ([c.to(torch.bfloat16) for c in s] for s in (q, k, v))
+    if dtype in ("bf16", "fp64"):   # the reference's general path on bf16 / fp64 coefficients
+        tdt = torch.bfloat16 if dtype == "bf16" else torch.float64
+        q, k, v = ([c.to(tdt) for c in s] for s in (q, k, v))
 
     def all_heads():   # one head at a time (the L x L series of all heads would not fit in host memory)
         for _ in range(heads):
             oracle.attention(q, k, v, is_causal=True)
 
-    t = _cpu_time(all_heads, reps=1)
+    t = _cpu_time(all_heads, reps=3)
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * (L + 1) / 2
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} {dtype or 'fp32'} causal",
@@ -573,7 +631,7 @@ def cpu_attention_window(L, d, K, W, heads=16):
         for _ in range(heads):
             oracle.attention(q, k, v, attn_mask=mask)
 
-    t = _cpu_time(some_heads, reps=1)
+    t = _cpu_time(some_heads, reps=3)
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * (W * (W + 1) // 2 + (L - W) * W)
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 window {W}", seconds=t)
@@ -596,7 +654,7 @@ def cpu_attention_bwd(L, d, K, heads=16, window=None, dtype=None):
         for _ in range(heads):
             oracle.attention_backward(q, k, v, cot, attn_mask=mask, is_causal=mask is None)
 
-    t = _cpu_time(some_heads, reps=1)
+    t = _cpu_time(some_heads, reps=3)
     pairs = L * (L + 1) / 2 if window is None else window * (window + 1) // 2 + (L - window) * window
     flops = heads * 5 * ((K + 1) * (K + 2) // 2) * 2 * d * pairs
     what = "causal" if window is None else f"window {window}"
@@ -616,7 +674,7 @@ def cpu_decoder(layers, d, heads, vocab, K, seq=64):
     base = gpt_embed(params, tokens)
     direction = torch.complex(torch.randn(1, seq, d, generator=g), torch.randn(1, seq, d, generator=g))
     X = [base, direction] + [torch.zeros(1, seq, d, dtype=torch.complex64) for _ in range(K - 1)]
-    t = _cpu_time(lambda: oracle.gpt_forward(params, X, targets, heads), reps=1)
+    t = _cpu_time(lambda: oracle.gpt_forward(params, X, targets, heads), reps=3)
     return dict(value=seq / t, unit="tokens/s", seconds=t,
                 sample=f"one sequence of {seq} tokens (attention cost grows with seq), full width, K={K} complex64")
 
@@ -648,11 +706,11 @@ def cpu_matmul(n, K, dtype="fp32"):
     import oracle
 
     rows = n // 4
-    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    tdt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp64": torch.float64}[dtype]
     g = torch.Generator().manual_seed(1)
     a = [(torch.randn(rows, n, generator=g) * 0.5 ** k).to(tdt) for k in range(K + 1)]
     b = [(torch.randn(n, n, generator=g) * 0.5 ** k).to(tdt) for k in range(K + 1)]
-    t = _cpu_time(lambda: oracle.matmul(a, b), reps=1)
+    t = _cpu_time(lambda: oracle.matmul(a, b), reps=3)
     flops = 2 * ((K + 1) * (K + 2) // 2) * rows * n * n
     return dict(value=flops / t / 1e12, unit="TFLOP/s", sample=f"{rows} of {n} rows of A, K={K} {dtype}",
                 seconds=t)
@@ -752,6 +810,22 @@ def time_steps(step, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def time_median(step, reps=21):
+    """Median over ``reps`` steps of each step's own HIP-event interval (events recorded between
+    consecutive steps on the current stream, launched back to back)."""
+    import torch
+
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize()
+    events[0].record()
+    for i in range(reps):
+        step()
+        events[i + 1].record()
+    torch.cuda.synchronize()
+    times = sorted(events[i].elapsed_time(events[i + 1]) for i in range(reps))
+    return times[reps // 2]
 
 
 def cpu_model():
@@ -885,6 +959,7 @@ def measure(name, device, steps, warmup, min_seconds=0.0):
         warmup = 1
     ms = time_steps(w["step"], steps, warmup)
     w["steps"] = steps
+    w["ms_median"] = time_median(w["step"])
     if w["unit"] == "ms":   # launch-bound workloads report time per step
         achieved = ms
     else:
@@ -936,6 +1011,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(w["ms"], 4),
+        "ms_median": round(w["ms_median"], 4),
         "higher_is_better": w["unit"] != "ms",
         "scaling": "weak",
         "vs_baseline": None,
@@ -963,7 +1039,8 @@ def main():
             if name == args.workload:
                 continue
             c = measure(name, device, max(3, args.steps // 2), 2, min_seconds=args.component_seconds)
-            comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "steps": c["steps"],
+            comps[name] = {"workload": c["workload"], "ms": round(c["ms"], 4), "ms_median": round(c["ms_median"], 4),
+                           "steps": c["steps"],
                            "achieved": round(c["achieved"], 3), "unit": c["unit"],
                            "frac": round(c["achieved"] / c["peak"], 4) if c["peak"] else None,
                            "traffic": profiled_traffic(c["kernel"]) if c["peak"] else None}
@@ -993,7 +1070,7 @@ def main():
             cpu = sampler()
             return {"value": round(cpu["value"], 6), "unit": cpu["unit"], "cores": torch.get_num_threads(),
                     "kind": "port", "sample": cpu["sample"], "seconds": round(cpu["seconds"], 3),
-                    "cpu_model": model}
+                    "timing": "median of 3 timings after one warm-up run", "cpu_model": model}
 
         line["cpu_baseline"] = cpu_entry(w["cpu"])
         _progress(f"cpu baseline {args.workload}: {line['cpu_baseline']['value']} {line['cpu_baseline']['unit']}")

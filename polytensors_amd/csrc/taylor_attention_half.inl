@@ -11,6 +11,13 @@
 // _attention_kernels.py:27-82: half operands, fp32 accumulation). Only the
 // MFMA operands are 16-bit: Q, K and V as stored, and the probability series
 // P_k = exp(S_0 - m) e_k rounded to the storage type for the value product.
+// The row sums l_k add those rounded values (hi + lo where split), so numerator
+// and denominator of O = N / l weigh each key alike and O is the exact weighted
+// average for the rounded weights. Summed from the fp32 values instead, the
+// weights' rounding survives the cancellation in the quotient's higher orders:
+// a degree-3 case (d 32, 19 x 13 keys, causal) had order 3 off by 1.05e-2 of its
+// scale (6.4e-3 this way), and its key gradient, through the saved output and lse,
+// by 2.3e-2 (4.0e-3 this way).
 // Scores, the exponential series, the row sums and the output accumulators are
 // fp32; the output is rounded to the storage type once, the lse series is fp32.
 //
@@ -283,20 +290,21 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
           e[k] = t * (1.f / static_cast<float>(k));
         }
 #pragma unroll
-        for (int o = 0; o <= K; ++o) {
-          w[o][r] = p * e[o];
-          lsum[o] += w[o][r];
-        }
+        for (int o = 0; o <= K; ++o) w[o][r] = p * e[o];
       }
 #pragma unroll
       for (int o = 0; o <= K; ++o) {
         const uint32_t w01 = MM::pack2(w[o][0], w[o][1]), w23 = MM::pack2(w[o][2], w[o][3]);
         pb[o][2 * kh] = w01;
         pb[o][2 * kh + 1] = w23;
+        // the row sums add the weights as rounded for the value products
+        lsum[o] += (MM::lo(w01) + MM::hi(w01)) + (MM::lo(w23) + MM::hi(w23));
         if constexpr (Sh::split) {
           if (o >= 1) {   // the rounding residuals as the lo operand
             pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
             pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
+            lsum[o] += (MM::lo(pl[o][2 * kh]) + MM::hi(pl[o][2 * kh])) +
+                       (MM::lo(pl[o][2 * kh + 1]) + MM::hi(pl[o][2 * kh + 1]));
           }
         }
       }
@@ -605,20 +613,21 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
           e[k] = t * (1.f / static_cast<float>(k));
         }
 #pragma unroll
-        for (int o = 0; o <= K; ++o) {
-          w[o][r] = p * e[o];
-          lsum[o] += w[o][r];
-        }
+        for (int o = 0; o <= K; ++o) w[o][r] = p * e[o];
       }
 #pragma unroll
       for (int o = 0; o <= K; ++o) {
         const uint32_t w01 = MM::pack2(w[o][0], w[o][1]), w23 = MM::pack2(w[o][2], w[o][3]);
         pb[o][2 * kh] = w01;
         pb[o][2 * kh + 1] = w23;
+        // the row sums add the weights as rounded for the value products
+        lsum[o] += (MM::lo(w01) + MM::hi(w01)) + (MM::lo(w23) + MM::hi(w23));
         if constexpr (P::split) {
           if (o >= 1) {
             pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
             pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
+            lsum[o] += (MM::lo(pl[o][2 * kh]) + MM::hi(pl[o][2 * kh])) +
+                       (MM::lo(pl[o][2 * kh + 1]) + MM::hi(pl[o][2 * kh + 1]));
           }
         }
       }

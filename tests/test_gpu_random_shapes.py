@@ -9,9 +9,12 @@ Cauchy matmul with broadcast batches
 and plain operands, RMSNorm / LayerNorm with series weights, cross entropy with
 ignored rows, weights and label smoothing, and the elementwise activations.
 The oracle runs in float64 on the same (rounded) inputs. Per-order tolerance
-max|got - want| / max(max|want|, floor): 1e-9 float64, 2e-4 float32, 3e-2
-bfloat16 (a little above the pinned-case tolerances: random sizes reach
-longer sums and larger orders).
+is the contract's: max|got - want| / max|want| <= 1e-10 float64, 1e-4 float32,
+2e-2 bfloat16, each order normalised by its own largest value. An order whose
+exact value is zero everywhere must come out zero to within that tolerance in
+absolute terms. The one floor is where an order's exact value is zero
+analytically but its computed value is rounding noise (attention's key gradient
+with a single key; see the case).
 """
 
 import random
@@ -25,7 +28,7 @@ from polytensors_amd import PolyTensor
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float64: 1e-9, torch.float32: 2e-4, torch.bfloat16: 3e-2}
+TOL = {torch.float64: 1e-10, torch.float32: 1e-4, torch.bfloat16: 2e-2}
 CASES = 40
 MODES = ("causal", "bool", "additive", "batched", "none")
 
@@ -47,9 +50,12 @@ def _check(got, want, dtype, what, rows=None, floor=0.0):
         a, b = a.detach().cpu().double(), b.double()
         if rows is not None:
             a, b = a[rows], b[rows]
-        scale = max(b.abs().max().item() if b.numel() else 0.0, floor)
-        err = (a - b).abs().max().item() / scale if b.numel() and scale > 0 else 0.0
-        assert err <= TOL[dtype], f"{what}: order {k} error {err:.3e}"
+        if not b.numel():
+            continue
+        scale = max(b.abs().max().item(), floor)
+        diff = (a - b).abs().max().item()
+        err = diff / scale if scale > 0 else diff
+        assert err <= TOL[dtype], f"{what}: order {k} error {err:.3e} (scale {scale:.3e})"
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -95,7 +101,10 @@ def test_attention(case):
     if grad:
         grads = oracle.attention_backward(*up, _rounded(Gs, dtype), attn_mask=m, is_causal=causal)
         for name, x, b in zip(("dq", "dk", "dv"), (q, k, v), grads):
-            _check(x.grad.coeffs, b, dtype, f"{what} {name}", floor=1.0 if S == 1 else 0.0)
+            # With one key the softmax is identically 1, so dS = 0 and dq, dk are exactly zero;
+            # the kernels' values there are rounding noise of G.V - Delta, measured against the
+            # scale of the cotangent (1) rather than against zero.
+            _check(x.grad.coeffs, b, dtype, f"{what} {name}", floor=1.0 if S == 1 and name != "dv" else 0.0)
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -115,8 +124,7 @@ def test_matmul(case):
     with torch.no_grad(), PolyTensor.plain_range():
         out = a @ b
     want = oracle.matmul(_rounded(A, dtype), _rounded(Bm, dtype))
-    _check(out.coeffs, want, dtype, f"matmul {dtype} K={degree} {batch_a}{(m, kd)} @ {batch_b}{(kd, n)}",
-           floor=1.0)
+    _check(out.coeffs, want, dtype, f"matmul {dtype} K={degree} {batch_a}{(m, kd)} @ {batch_b}{(kd, n)}")
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -143,7 +151,7 @@ def test_norms(case):
         want = oracle.layer_norm(Xr, (n,), Wr, None if Bias is None else _rounded(Bias, dtype), eps=1e-5)
     else:
         want = oracle.rms_norm(Xr, (n,), Wr, eps=1e-6)
-    _check(out.coeffs, want, dtype, f"{'layer' if layer else 'rms'}_norm {dtype} K={degree} [{rows}, {n}]", floor=1.0)
+    _check(out.coeffs, want, dtype, f"{'layer' if layer else 'rms'}_norm {dtype} K={degree} [{rows}, {n}]")
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -167,7 +175,7 @@ def test_cross_entropy(case):
     want = oracle.cross_entropy(_rounded(Z, dtype), y, reduction=reduction,
                                 weight=None if weight is None else weight.to(dtype).double(), label_smoothing=smoothing)
     _check(loss.coeffs, want, dtype, f"cross_entropy {dtype} K={degree} [{rows}, {classes}] {reduction} "
-           f"w={weight is not None} eps={smoothing}", floor=1.0)
+           f"w={weight is not None} eps={smoothing}")
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -183,4 +191,4 @@ def test_activations(case):
     with torch.no_grad(), PolyTensor.plain_range():
         out = fn(_poly(X, dtype))
     want = oracle.activation(_rounded(X, dtype), kind)
-    _check(out.coeffs, want, dtype, f"{kind} {dtype} K={degree}", floor=1.0)
+    _check(out.coeffs, want, dtype, f"{kind} {dtype} K={degree}")
