@@ -26,6 +26,8 @@
 // stay in registers for the whole key loop.
 #pragma once
 
+#include <type_traits>
+
 #include "mfma.h"
 #include "taylor_attention.h"
 
@@ -68,6 +70,14 @@ struct AttnRescale {
   static constexpr float value = 8.0f;   // lazy-rescale slack (natural-log units): p <= e^8
 };
 
+// The largest divisor of `per` (vectors per thread of a staging step) up to `most`: the loads
+// of a staging step go out in groups of that many.
+constexpr int attn_stage_group(int per, int most) {
+  int g = most < per ? most : per;
+  while (g > 1 && per % g != 0) --g;
+  return g < 1 ? 1 : g;
+}
+
 template <typename T, int K, int D>
 struct AttnShape {
   static constexpr int SL = attn_slices(static_cast<int>(sizeof(T)), K, D);
@@ -85,6 +95,12 @@ struct AttnShape {
   static constexpr bool SEQ = (KT + VT) * sizeof(T) > 160 * 1024;
   static constexpr size_t LDS = (SEQ ? (KT > VT ? KT : VT) : KT + VT) * sizeof(T);
   static constexpr bool fits = LDS <= 160 * 1024;
+  // Query operands read one head-dim chunk ahead, and the 16-byte vectors per thread whose
+  // loads a staging step issues before their LDS stores, where the registers allow
+  // (instantiations checked free of scratch spills with the compiler's resource remarks).
+  static constexpr int kAccRegs = (K + 1) * DBS * 4 * static_cast<int>(sizeof(T) / 4);
+  static constexpr bool kQAhead = K <= 4 && kAccRegs <= 160;
+  static constexpr int kStageGroup = kAccRegs > 160 ? 1 : 8;
 };
 
 // Shared epilogue: row sums across the 4 lane groups, series quotient
@@ -480,25 +496,43 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     __syncthreads();
     // ---- stage rows kb0 .. kb0+15 of every order (zero past S / the orders given): K over every
     // head dim, V over the slice's (V after the scores when the two share the buffer) ----
-    auto stage = [&](auto dst, const CPtrs<T>& src, int orders, int dims, int first) {
-      const int vpr = dims / V;   // 16-byte vectors per row
-      for (int idx = threadIdx.x; idx < (K + 1) * kAttnBN * vpr; idx += kAttnWaves * kWave) {
-        const int o = idx / (kAttnBN * vpr);
-        const int rem = idx % (kAttnBN * vpr);
-        const int r = rem / vpr, cv = (rem % vpr) * V;
-        const int key = kb0 + r;
-        Vec<T, V> x;
-        if (key < S && o < orders) {
-          x = load_vec<T, V>(order_ptr<K>(src, o) + (head * S + key) * D + first + cv);
-        } else {
+    // Loads go out in groups of kStageGroup vectors per thread before their LDS stores, each
+    // from a clamped (valid) address with the value zeroed afterwards: a load under a per-lane
+    // branch would be waited for where the branch ends, one round trip per vector.
+    auto stage = [&](auto dst, const CPtrs<T>& src, int orders, auto dims_c, int first) {
+      constexpr int vpr = decltype(dims_c)::value / V;   // 16-byte vectors per row
+      constexpr int total = (K + 1) * kAttnBN * vpr;
+      constexpr int threads = kAttnWaves * kWave;
+      constexpr int per = (total + threads - 1) / threads;
+      constexpr int G = attn_stage_group(per, Shape::kStageGroup);
+#pragma unroll 1
+      for (int g0 = 0; g0 < per; g0 += G) {
+        Vec<T, V> x[G];
+        bool live[G];
 #pragma unroll
-          for (int e = 0; e < V; ++e) x.v[e] = T(0);
+        for (int j = 0; j < G; ++j) {
+          const int idx = (g0 + j) * threads + static_cast<int>(threadIdx.x);
+          const int o = idx / (kAttnBN * vpr);
+          const int rem = idx % (kAttnBN * vpr);
+          const int key = kb0 + rem / vpr, cv = (rem % vpr) * V;
+          live[j] = (total % threads == 0 || idx < total) && key < S && o < orders;
+          const int oc = o < orders ? o : 0, kc = key < S ? key : S - 1;
+          x[j] = load_vec<T, V>(order_ptr<K>(src, oc) + (head * S + kc) * D + first + cv);
         }
-        store_vec<T, V>(&dst[o][r][cv], x);
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+          const int idx = (g0 + j) * threads + static_cast<int>(threadIdx.x);
+          if (total % threads != 0 && idx >= total) continue;
+          const int o = idx / (kAttnBN * vpr);
+          const int rem = idx % (kAttnBN * vpr);
+#pragma unroll
+          for (int e = 0; e < V; ++e) x[j].v[e] = live[j] ? x[j].v[e] : T(0);
+          store_vec<T, V>(&dst[o][rem / vpr][(rem % vpr) * V], x[j]);
+        }
       }
     };
-    stage(Ks, Kp, k_orders, D, 0);
-    if constexpr (!Shape::SEQ) stage(Vs, Vp, v_orders, DS, d0);
+    stage(Ks, Kp, k_orders, std::integral_constant<int, D>{}, 0);
+    if constexpr (!Shape::SEQ) stage(Vs, Vp, v_orders, std::integral_constant<int, DS>{}, d0);
     __syncthreads();
 
     // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T (keys x queries) ----
@@ -506,14 +540,26 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 #pragma unroll
     for (int o = 0; o <= K; ++o) sc[o] = MF::zero();
     // Not unrolled: no register array is indexed by dc, and a rolled loop keeps
-    // the code (and compile time) of the high-degree instantiations small.
+    // the code (and compile time) of the high-degree instantiations small. The query
+    // operands (global, L2-resident) are read one chunk ahead.
+    Vec<T, QV> qn[Shape::kQAhead ? K + 1 : 1];
+    if constexpr (Shape::kQAhead) {
+#pragma unroll
+      for (int o = 0; o <= K; ++o) qn[o] = *reinterpret_cast<const Vec<T, QV>*>(qrow[o] + 4 * h);
+    }
 #pragma unroll 1
     for (int dc = 0; dc < DB; ++dc) {
       // lane operands: K[key = c][d = 16 dc + 4 h + s], Q[my_q][same d], s = 0..3
       Vec<T, QV> qa[K + 1], kb[K + 1];
+      const int dn = !Shape::kQAhead ? dc : dc + 1 < DB ? dc + 1 : dc;   // the next chunk (or this one)
 #pragma unroll
       for (int o = 0; o <= K; ++o) {
-        qa[o] = *reinterpret_cast<const Vec<T, QV>*>(qrow[o] + dc * 16 + 4 * h);
+        if constexpr (Shape::kQAhead) {
+          qa[o] = qn[o];
+          qn[o] = *reinterpret_cast<const Vec<T, QV>*>(qrow[o] + dn * 16 + 4 * h);
+        } else {
+          qa[o] = *reinterpret_cast<const Vec<T, QV>*>(qrow[o] + dc * 16 + 4 * h);
+        }
 #pragma unroll
         for (int e = 0; e < QV; ++e) qa[o].v[e] = q_live[o] ? qa[o].v[e] : T(0);
         kb[o] = *reinterpret_cast<const Vec<T, QV>*>(&Ks[o][c][dc * 16 + 4 * h]);
@@ -583,7 +629,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
 
     if constexpr (Shape::SEQ) {
       __syncthreads();   // every wave's scores are done with the K tile
-      stage(Vs, Vp, v_orders, DS, d0);
+      stage(Vs, Vp, v_orders, std::integral_constant<int, DS>{}, d0);
       __syncthreads();
     }
 
