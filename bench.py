@@ -2,7 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload attention|attention_dense|attention_bf16|attention_fp64|attention_window|
-                                attention_bwd|attention_bwd_bf16|attention_bwd_window|matmul|matmul_bf16|
+                                attention_bf16_additive|attention_bwd|attention_bwd_bf16|attention_bwd_window|
+                                matmul|matmul_bf16|
                                 matmul_fp64|norm|ce|activation|norm_bwd|ce_bwd|config1|decoder]
                     [--no-cpu-baseline] [--no-components] [--no-ceiling] [--component-seconds S]
                     [--copy-calibration]
@@ -365,6 +366,44 @@ def wl_attention_fp64(device):
                 cpu=lambda: cpu_attention(L, d, K, heads=16, dtype="fp64"))
 
 
+def wl_attention_bf16_additive(device):
+    """Config 3's shape in bfloat16 (B=4 H=16 L=2048 d=128, K=4, line inputs, scale 1/sqrt(128)) with a
+    padding-style floating mask instead of causal: batch entry b admits keys j < 2048 - 256 b (mask value
+    0) and excludes the rest (-inf), a [B, 1, L, S] bfloat16 mask over the H heads of each entry. The
+    16-bit kernels take the mask's float32 values; one step includes the operator's mask preparation
+    (float32 values, admissible entries, block ranges). Work is the dense-series count over the
+    admissible pairs."""
+    import torch
+    from polytensors_amd import _ops
+
+    B, H, L, d, K = 4, 16, 2048, 128, 4
+    g = _gen(13, device)
+
+    def series():
+        base = torch.randn(B * H, L, d, generator=g, device=device) / math.sqrt(d)
+        direction = torch.randn(B * H, L, d, generator=g, device=device)
+        return [x.to(torch.bfloat16) for x in [base, direction] + [torch.zeros_like(base) for _ in range(2, K + 1)]]
+
+    q, k, v = series(), series(), series()
+    lengths = [L - 256 * b for b in range(B)]
+    j = torch.arange(L, device=device)
+    mask = torch.stack([torch.where(j < n, 0.0, float("-inf")).expand(L, L) for n in lengths]).to(torch.bfloat16)
+    scale = 1 / math.sqrt(d)
+
+    def step():
+        return _ops.taylor_attention_fwd(q, k, v, mask, False, scale, K, [H, 1, 0])
+
+    pairs = (K + 1) * (K + 2) // 2
+    admissible = H * L * sum(lengths)
+    flops = 2 * pairs * 2 * d * admissible
+    nbytes = 4 * (K + 1) * B * H * L * d * 2 + B * L * L * 2
+    return dict(step=step, work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_MFMA,
+                bytes=nbytes, kernel="taylor_attention_bf16_additive", dtype="bf16 (fp32 accumulate)",
+                workload=f"taylor_attention_fwd B={B} H={H} L={L} d={d} K={K} bf16 padding float mask "
+                         f"(key lengths {lengths}) line inputs",
+                cpu=lambda: cpu_attention_padding(L, d, K, lengths[1], heads=4))
+
+
 def wl_attention_dense(device):
     """Config 3 with dense random orders 2..4 (N(0,1) 0.5^k) instead of a line: the same kernel
     and work count, with no zero input orders."""
@@ -579,7 +618,8 @@ WORKLOADS = {"attention": wl_attention, "matmul": wl_matmul, "matmul_bf16": wl_m
              "attention_bwd": wl_attention_bwd, "attention_bwd_bf16": wl_attention_bwd_bf16,
              "attention_window": wl_attention_window,
              "attention_bwd_window": wl_attention_bwd_window,
-             "attention_dense": wl_attention_dense, "attention_bf16": wl_attention_bf16, "config1": wl_config1,
+             "attention_dense": wl_attention_dense, "attention_bf16": wl_attention_bf16,
+             "attention_bf16_additive": wl_attention_bf16_additive, "config1": wl_config1,
              "decoder": wl_decoder}
 
 
@@ -635,6 +675,28 @@ def cpu_attention_window(L, d, K, W, heads=16):
     flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * (W * (W + 1) // 2 + (L - W) * W)
     return dict(value=flops / t / 1e12, unit="TFLOP/s",
                 sample=f"{heads} of 64 (b,h) heads one at a time, L={L} d={d} K={K} fp32 window {W}", seconds=t)
+
+
+def cpu_attention_padding(L, d, K, length, heads=4):
+    """The reference's general path on bf16 coefficients with an additive padding mask (keys past
+    ``length`` at -inf), one head at a time."""
+    import torch
+    import oracle
+
+    g = torch.Generator().manual_seed(13)
+    q, k, v = ([(torch.randn(1, 1, L, d, generator=g) * (0.5 ** o)).to(torch.bfloat16) for o in range(K + 1)]
+               for _ in range(3))
+    mask = torch.where(torch.arange(L) < length, 0.0, float("-inf")).expand(L, L).to(torch.bfloat16)
+
+    def some_heads():
+        for _ in range(heads):
+            oracle.attention(q, k, v, attn_mask=mask)
+
+    t = _cpu_time(some_heads, reps=3)
+    flops = heads * 2 * ((K + 1) * (K + 2) // 2) * 2 * d * L * length
+    return dict(value=flops / t / 1e12, unit="TFLOP/s",
+                sample=f"{heads} heads one at a time, L={L} d={d} K={K} bf16, padding mask of {length} keys",
+                seconds=t)
 
 
 def cpu_attention_bwd(L, d, K, heads=16, window=None, dtype=None):

@@ -210,7 +210,9 @@ size_t pt_cross_entropy_series_noalloc_max_bytes(void);
  * dtype: PT_FLOAT32 (fp32 MFMA), PT_FLOAT64 (fp64 MFMA), or PT_BFLOAT16 / PT_FLOAT16 (16-bit MFMA
  * operands, fp32 accumulation, each output element rounded once; needs k and, unless trans_b, n
  * to be multiples of 8, 16-byte aligned operands, batch strides that are multiples of 8 and each
- * matrix below 1 GiB, else PT_UNSUPPORTED).
+ * matrix below 1 GiB, else PT_UNSUPPORTED). Any alignment of c is accepted: 16-bit outputs are
+ * written 8 bytes at a time where n is a multiple of 4 and every c[o] is 8-byte aligned, else one
+ * element at a time).
  */
 int pt_cauchy_matmul(int dtype, int degree, const void* const* a, int a_orders,
                      const void* const* b, int b_orders, void* const* c,
@@ -261,8 +263,8 @@ int pt_taylor_attention_fwd(int dtype, int degree, const void* const* q,
  * runs the launch unsplit. The workspace must be 16-byte aligned.
  * mask_add: NULL, or an additive float mask, the reference's float attn_mask
  *   (/root/reference/src/polytensors/_decompositions.py:38-40: added to the scores, so to
- *   their constant order, after scaling): [lq, lk] values of the accumulator type (float for
- *   PT_FLOAT32, double for PT_FLOAT64; PT_UNSUPPORTED for the 16-bit types). mask must then
+ *   their constant order, after scaling): [lq, lk] values of the accumulator type (double for
+ *   PT_FLOAT64, float for PT_FLOAT32, PT_BFLOAT16 and PT_FLOAT16). mask must then
  *   be given and mark exactly its finite entries (an entry of -inf excludes its key; a row
  *   with none admissible gets the empty-row output above).
  * mask_map: NULL (mask, mask_ranges and mask_add hold one mask, shared by every head), or
@@ -317,8 +319,10 @@ int pt_attention_mask_ranges(const uint8_t* mask, int64_t n_masks, int64_t lq, i
  *   PT_FLOAT16 at degrees 1..4 and head dims 32..128 (other 16-bit calls
  *   recompute and ignore it); PT_UNSUPPORTED for PT_FLOAT64.
  * mask, mask_ranges: as in pt_taylor_attention_fwd; mask_add, mask_map: as in
- *   pt_taylor_attention_fwd_ws (the forward's additive mask: with it the scores
- *   are recomputed and materialize does not apply).
+ *   pt_taylor_attention_fwd_ws (the forward's additive mask, [lq, lk] values of the
+ *   accumulator type: double for PT_FLOAT64, float for the other types). With it the
+ *   PT_FLOAT32 / PT_FLOAT64 kernels recompute the scores and materialize does not apply;
+ *   the 16-bit stored-tile kernels take it as they are.
  * Pointers must be 16-byte aligned. Deterministic (no atomics).
  * Replaces the degree-1 fused backward
  *   /root/reference/src/polytensors/_fused_attention.py:144-163 (backward),

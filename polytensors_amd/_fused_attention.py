@@ -36,26 +36,6 @@ _HEAD_DIMS = {torch.float32: (16, 32, 64, 128), torch.float64: (16, 32, 64, 128)
               torch.bfloat16: (16, 32, 64, 128), torch.float16: (16, 32, 64, 128)}
 
 
-def _tiles_fit_lds(dtype, head_dim, degree, backward):
-    """Whether the kernels' staged key and value tiles fit in LDS.
-
-    The forward fits at every degree and head dim (output head-dim slices and, for float64,
-    K and V tiles staged one after the other where both do not fit: AttnShape in
-    csrc/taylor_attention.inl). The backward stages 16 rows of every order of two operands
-    with rows padded to head_dim + 4 values, plus two 16-row series of accumulator values,
-    the two tiles taking turns in one buffer where both do not fit (AttnBwdPlan in
-    csrc/taylor_attention_bwd.inl).
-    """
-    if not backward:
-        return True
-    if dtype in (torch.bfloat16, torch.float16):
-        dtype = torch.float32   # the 16-bit backward runs the float32 kernels
-    item = torch.empty((), dtype=dtype).element_size()
-    tile = (degree + 1) * 16 * (head_dim + 4) * item
-    acc = 2 * (degree + 1) * 16 * item
-    return tile + acc <= 160 * 1024   # (with room for both tiles, one buffer each)
-
-
 def default_scale(head_dim):
     return 1 / math.sqrt(head_dim)
 
@@ -127,11 +107,6 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     d = qs[-1]
     if d != ks[-1] or d not in _HEAD_DIMS[dtype]:
         return f"head dim {d} not in {_HEAD_DIMS[dtype]}"
-    if grads or _gate.coefficient_graph(*tensors):
-        degree = next(x.degree for x in tensors if isinstance(x, PolyTensor))
-        if not _tiles_fit_lds(dtype, d, degree, True):
-            return (f"the backward at degree {degree}, head dim {d} in {dtype} exceeds the kernels' "
-                    "160 KiB LDS budget for the staged key/value tiles")
     if attn_mask is not None and _kernel_mask(attn_mask, tuple(qs[:-2]), qs[-2], ks[-2]) is NotImplemented:
         return "the mask must be boolean or floating, of shape (..., L, S) broadcasting over the batch"
     return None

@@ -61,7 +61,7 @@ __host__ __device__ __forceinline__ int cauchy_swz_k(int k, int ch) {
 
 template <typename T, int K, int AO, int BO, bool TRANS_B, bool WIDE>
 __global__ __launch_bounds__((CauchyHalfTile<AO, BO, WIDE>::kThreads)) void cauchy_matmul_half_kernel(
-    CPtrs<T> A, CPtrs<T> B, MPtrs<T> C, int M, int N, int Kd, int64_t a_bs, int64_t b_bs) {
+    CPtrs<T> A, CPtrs<T> B, MPtrs<T> C, int M, int N, int Kd, int64_t a_bs, int64_t b_bs, int c_vec) {
   using Tile = CauchyHalfTile<AO, BO, WIDE>;
   using MM = HalfMfma<T>;
   constexpr int BM = Tile::BM, BN = Tile::BN, BK = Tile::BK, FM = Tile::FM, FN = Tile::FN;
@@ -192,7 +192,7 @@ __global__ __launch_bounds__((CauchyHalfTile<AO, BO, WIDE>::kThreads)) void cauc
   __builtin_amdgcn_s_waitcnt(0);
 
   // ---- epilogue: lane (c, g) holds C[m0 + c][n0 + 4g .. + 3] of each block ----
-  const bool vec = N % 4 == 0;
+  const bool vec = c_vec != 0;   // N % 4 == 0 and every C_k 8-byte aligned: 8-byte stores
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
     T* base = C.p[o] + batch * static_cast<int64_t>(M) * N;
@@ -234,10 +234,14 @@ static int launch_cauchy_half_tile(const CauchyArgs& a, const CPtrs<T>& A, const
   const dim3 grid((a.n + Tile::BN - 1) / Tile::BN, (a.m + Tile::BM - 1) / Tile::BM, a.batch);
   const dim3 block(Tile::kThreads);
   const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), Kd = static_cast<int>(a.k);
+  int c_vec = N % 4 == 0;
+  for (int o = 0; o <= K; ++o) c_vec = c_vec && reinterpret_cast<uintptr_t>(C.p[o]) % 8 == 0;
   if (a.trans_b)
-    cauchy_matmul_half_kernel<T, K, AO, BO, true, WIDE><<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
+    cauchy_matmul_half_kernel<T, K, AO, BO, true, WIDE>
+        <<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs, c_vec);
   else
-    cauchy_matmul_half_kernel<T, K, AO, BO, false, WIDE><<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs);
+    cauchy_matmul_half_kernel<T, K, AO, BO, false, WIDE>
+        <<<grid, block, 0, a.stream>>>(A, B, C, M, N, Kd, a.a_bs, a.b_bs, c_vec);
   PT_LAUNCH_CHECK();
   return PT_OK;
 }

@@ -52,8 +52,6 @@ int pt_taylor_attention_fwd_ws(int dtype, int degree, const void* const* q, int 
              "Taylor attention: an additive mask needs the boolean mask of its finite entries");
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64 || dtype == PT_BFLOAT16 || dtype == PT_FLOAT16,
              PT_UNSUPPORTED, "Taylor attention: float32, float64, bfloat16 or float16");
-  PT_REQUIRE(mask_add == nullptr || dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
-             "Taylor attention: additive masks take float32 or float64 operands");
   PT_REQUIRE(q != nullptr && k != nullptr && v != nullptr && out != nullptr, PT_INVALID_ARGUMENT,
              "Taylor attention: q, k, v and out pointer arrays are required");
   for (int o : {q_orders, k_orders, v_orders})

@@ -80,11 +80,13 @@ __device__ __forceinline__ u32x4 attn_half_load8(const T* p, bool ok) {
   return ok ? v : z;
 }
 
-template <typename T, int K, int D>
+// ADD: an additive (L, S) mask madd (float32 values) is given with the boolean mask of its finite
+// entries; it adds to the constant-order scores after scaling.
+template <typename T, int K, int D, bool ADD>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_kernel(
     CPtrs<T> Q, int q_orders, CPtrs<T> Kp, int k_orders, CPtrs<T> Vp, int v_orders, MPtrs<T> O, MPtrs<float> LSE,
     int L, int S, const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all,
-    int causal, float scale) {
+    const float* __restrict__ madd_all, int causal, float scale) {
   using Sh = AttnHalfShape<K, D>;
   using MM = HalfMfma<T>;
   constexpr int KB = Sh::KB, DC = Sh::DC, DB = Sh::DB, LDK = Sh::LDK, LDV = Sh::LDV;
@@ -118,6 +120,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   const int64_t mask_index = attn_mask_index(mmap, head);
   const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
   const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const float* madd = ADD ? madd_all + mask_index * L * S : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qrow = (head * L + (q_ok ? my_q : 0)) * D;
@@ -160,6 +163,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mbyte[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    float add[ADD ? 2 : 1][4];   // additive mask values of the same keys
+    if constexpr (ADD) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) add[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    }
     __syncthreads();   // the previous block's products are done with the tiles
     // ---- stage K rows kb0 .. kb0 + 31 of every order, row-major (zero past S / the orders given) ----
     {
@@ -251,7 +261,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         if (causal) ok = ok && key <= my_q;
         if (mask != nullptr) ok = ok && mbyte[kh][r] != 0;
         valid[kh][r] = ok;
-        s0[kh][r] = ok ? sc[kh][0][r] * scale : kNegInf;
+        float sv = sc[kh][0][r] * scale;
+        if constexpr (ADD) sv += add[kh][r];
+        s0[kh][r] = ok ? sv : kNegInf;
         bmax = fmaxf(bmax, s0[kh][r]);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
@@ -442,11 +454,11 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
   lds_dma16(&buf[kv][o][seg * RPS][0], rsrc, ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
 
-template <typename T, int K, int D>
+template <typename T, int K, int D, bool ADD>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S,
-    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all, int causal,
-    float scale) {
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all,
+    const float* __restrict__ madd_all, int causal, float scale) {
   using P = AttnHalfPipe<K, D>;
   using MM = HalfMfma<T>;
   constexpr int KB = P::KB, DC = (D + 31) / 32, DB = D / 16, OPS = P::OPS;
@@ -469,6 +481,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   const int64_t mask_index = attn_mask_index(mmap, head);
   const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
   const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const float* madd = ADD ? madd_all + mask_index * L * S : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
   const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
@@ -519,6 +532,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mbyte[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    float add[ADD ? 2 : 1][4];   // additive mask values of the same keys
+    if constexpr (ADD) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) add[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    }
     __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and the mask bytes)
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
 
@@ -569,7 +589,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         if (causal) ok = ok && key <= my_q;
         if (mask != nullptr) ok = ok && mbyte[kh][r] != 0;
         valid[kh][r] = ok;
-        s0[kh][r] = ok ? sc[kh][0][r] * scale : kNegInf;
+        float sv = sc[kh][0][r] * scale;
+        if constexpr (ADD) sv += add[kh][r];
+        s0[kh][r] = ok ? sv : kNegInf;
         bmax = fmaxf(bmax, s0[kh][r]);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
@@ -740,6 +762,7 @@ static int launch_attention_half_kd(const AttnArgs& a) {
     CPtrs<T> q{}, k{}, v{};
     MPtrs<T> o{};
     MPtrs<float> lse{};
+    const float* madd = static_cast<const float*>(a.mask_add);   // float32 values for 16-bit operands
     for (int i = 0; i < a.q_orders; ++i) q.p[i] = static_cast<const T*>(a.q[i]);
     for (int i = 0; i < a.k_orders; ++i) k.p[i] = static_cast<const T*>(a.k[i]);
     for (int i = 0; i < a.v_orders; ++i) v.p[i] = static_cast<const T*>(a.v[i]);
@@ -754,17 +777,25 @@ static int launch_attention_half_kd(const AttnArgs& a) {
                         head_bytes < (int64_t{1} << 31);
       if (pipe) {
         const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
-        taylor_attention_fwd_half_pipe_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-            q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges,
-            a.causal ? 1 : 0, static_cast<float>(a.scale));
+#define PT_HALF_PIPE(ADDV)                                                                                     \
+  taylor_attention_fwd_half_pipe_kernel<T, K, D, ADDV><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(      \
+      q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges, madd, \
+      a.causal ? 1 : 0, static_cast<float>(a.scale))
+        if (madd != nullptr) PT_HALF_PIPE(true);
+        else PT_HALF_PIPE(false);
+#undef PT_HALF_PIPE
         PT_LAUNCH_CHECK();
         return PT_OK;
       }
     }
     const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh * AttnHalfShape<K, D>::SL));
-    taylor_attention_fwd_half_kernel<T, K, D><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(
-        q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),
-        a.mask, a.mask_map, a.mask_ranges, a.causal ? 1 : 0, static_cast<float>(a.scale));
+#define PT_HALF_STAGED(ADDV)                                                                                   \
+  taylor_attention_fwd_half_kernel<T, K, D, ADDV><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(           \
+      q, a.q_orders, k, a.k_orders, v, a.v_orders, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk),     \
+      a.mask, a.mask_map, a.mask_ranges, madd, a.causal ? 1 : 0, static_cast<float>(a.scale))
+    if (madd != nullptr) PT_HALF_STAGED(true);
+    else PT_HALF_STAGED(false);
+#undef PT_HALF_STAGED
     PT_LAUNCH_CHECK();
     return PT_OK;
   }

@@ -388,16 +388,6 @@ std::tuple<Tensor, Tensor> taylor_attention_fwd(const TensorList& q, const Tenso
   TORCH_CHECK_VALUE(k[0].scalar_type() == dtype && v[0].scalar_type() == dtype, "taylor_attention: dtypes differ");
   const int64_t lk = k[0].size(nd - 2);
   c10::DeviceGuard guard(q[0].device());
-  if (mask_in && mask_in->scalar_type() != at::kBool && (dtype == at::kBFloat16 || dtype == at::kHalf)) {
-    // the additive mask runs on the float32 kernel: 16-bit operands are widened, the output rounded
-    auto widen = [](const TensorList& xs) {
-      std::vector<Tensor> out;
-      for (const Tensor& x : xs) out.push_back(x.to(at::kFloat));
-      return out;
-    };
-    auto [o32, l32] = taylor_attention_fwd(widen(q), widen(k), widen(v), mask_in, causal, scale, degree, mask_map);
-    return {o32.to(dtype), l32};
-  }
   const auto mask = attention_mask(mask_in, mask_map, q[0], bh, lq, lk, causal, "taylor_attention");
   std::vector<int64_t> out_shape{degree + 1};
   out_shape.insert(out_shape.end(), batch.begin(), batch.end());
@@ -463,16 +453,28 @@ std::tuple<Tensor, Tensor, Tensor> taylor_attention_bwd(const TensorList& q, con
   Tensor dv = at::empty_like(dk);
   const auto ranges = mask_ranges(mask, lq, lk);
   const int code = dtype_code(dtype);
-  if (materialize < 0) {   // stored tiles where the workspace takes at most a quarter of the device;
-                           // the library refuses them for float64
+  auto workspace_for = [&](int64_t mat) {
+    const size_t wbytes =
+        pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, static_cast<int>(mat));
+    return at::empty({static_cast<int64_t>(std::max<size_t>(1, wbytes))}, q[0].options().dtype(at::kByte));
+  };
+  Tensor workspace;
+  if (materialize < 0) {   // stored tiles where the workspace takes at most a quarter of the device
+                           // and can be allocated now (else recompute); the library refuses them for
+                           // float64
     const size_t size = pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, 1);
     size_t free_bytes = 0, total_bytes = 0;
     if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) total_bytes = 0;
     materialize = dtype != at::kDouble && total_bytes > 0 && size <= total_bytes / 4 ? 1 : 0;
+    if (materialize) {
+      try {
+        workspace = workspace_for(1);
+      } catch (const c10::OutOfMemoryError&) {   // a busy device: the recomputing kernels need none
+        materialize = 0;
+      }
+    }
   }
-  const size_t wbytes =
-      pt_taylor_attention_bwd_workspace_size(code, static_cast<int>(degree), bh, lq, lk, static_cast<int>(materialize));
-  Tensor workspace = at::empty({static_cast<int64_t>(std::max<size_t>(1, wbytes))}, q[0].options().dtype(at::kByte));
+  if (!workspace.defined()) workspace = workspace_for(materialize);
   auto qs = cptrs(q), ks = cptrs(k), vs = cptrs(v), gs = cptrs(grad);
   auto os = slices(out), ls = slices(lse);
   std::vector<const void*> oc(os.begin(), os.end()), lc(ls.begin(), ls.end());

@@ -62,8 +62,6 @@ def _vpp(n):
                                             None), 1, "mask_map"),
     ("pt_taylor_attention_fwd_ws", lambda: (0, 1, _vpp(2), 2, _vpp(2), 2, _vpp(2), 2, _vpp(2), None, 1, 16, 16, 64,
                                             0, None, None, 1 << 20, None, 0.125, None, 0, None), 1, "boolean mask"),
-    ("pt_taylor_attention_fwd_ws", lambda: (2, 1, _vpp(2), 2, _vpp(2), 2, _vpp(2), 2, _vpp(2), None, 1, 16, 16, 64,
-                                            0, 1 << 20, None, 1 << 20, None, 0.125, None, 0, None), 2, "additive"),
     ("pt_taylor_attention_bwd", lambda: (0, 1, _vpp(2), _vpp(2), _vpp(2), _vpp(2), _vpp(2), _vpp(2), None, None, None,
                                          1 << 20, 0, 1, 16, 16, 64, 0, 1 << 20, None, None,
                                          (ctypes.c_int64 * 3)(1, -1, 0), 0.125, None), 1, "mask_map"),

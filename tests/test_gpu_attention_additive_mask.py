@@ -26,7 +26,7 @@ from tests.jets import rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = {torch.float64: 1e-10, torch.float32: 1e-4, torch.bfloat16: 2e-2}
+TOL = {torch.float64: 1e-10, torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
 
 
 def _series(shape, degree, seed, scale=1.0):
@@ -65,7 +65,7 @@ def _poly(cs, dtype, grad=False):
     return PolyTensor(tuple(c.to(dtype).cuda() for c in cs), requires_grad=grad)
 
 
-@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("window", [None, 37])
 @pytest.mark.parametrize("degree", [1, 3, 8])
 def test_forward_matches_oracle(monkeypatch, dtype, window, degree):
@@ -85,22 +85,27 @@ def test_forward_matches_oracle(monkeypatch, dtype, window, degree):
     assert all(c[..., 7, :].abs().max().item() == 0 for c in out.coeffs)
 
 
-@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("L,S", [(1, 16), (65, 33), (130, 47)])
-def test_forward_ragged_lengths_and_lse(dtype, L, S):
+@pytest.mark.parametrize("plain_q", [False, True])
+def test_forward_ragged_lengths_and_lse(dtype, L, S, plain_q):
+    # every order given (the 16-bit pipelined kernel) and an ordinary query (the staged kernels);
+    # 16-bit operands take the mask's float32 values directly
     degree = 2
-    Q = _series((2, L, 32), degree, 30)
+    Q = _series((2, L, 32), degree, 30)[:1 if plain_q else None]
     K, V = (_series((2, S, 32), degree, 31 + i) for i in range(2))
     mask = _additive(L, S, 33, window=20)
     q, k, v = ([c.to(dtype).cuda() for c in s] for s in (Q, K, V))
     out, lse = _ops.taylor_attention_fwd(q, k, v, mask.to(dtype).cuda(), False, 0.3, degree)
-    up = [[c.to(dtype).double() for c in s] for s in (Q, K, V)]
-    want = oracle.attention(*up, attn_mask=mask, scale=0.3)
+    assert out.dtype == dtype and lse.dtype == (torch.float64 if dtype == torch.float64 else torch.float32)
+    up = [oracle.paths.lift([c.to(dtype).double() for c in s], degree) for s in (Q, K, V)]
+    madd = mask.to(dtype).double()   # the mask's values as the kernel received them
+    want = oracle.attention(*up, attn_mask=madd, scale=0.3)
     _check(out.unbind(0), want, dtype, rows=_kept(mask))
     # lse series of the admissible scores (the constant order shifted by the mask)
     scores = oracle.series.cauchy([c * 0.3 for c in up[0]], [c.transpose(-2, -1) for c in up[1]], matmul=True)
-    keep = ~torch.isneginf(mask)
-    scores = [torch.where(keep, s + (mask if i == 0 else 0.0), torch.full((), float("-inf") if i == 0 else 0.0,
+    keep = ~torch.isneginf(madd)
+    scores = [torch.where(keep, s + (madd if i == 0 else 0.0), torch.full((), float("-inf") if i == 0 else 0.0,
                                                                          dtype=s.dtype))
               for i, s in enumerate(scores)]
     want_lse = oracle.series.softmax_family(scores, -1)[2]

@@ -173,18 +173,6 @@ def test_plain_tensor_cross_entropy_with_softcap_matches_composite():
     assert torch.allclose(PolyTensor.cross_entropy(z, y, softcap=15.0), expected)
 
 
-def test_attention_lds_budget_gate():
-    # the forward fits everywhere (output head-dim slices, sequential K/V staging for float64);
-    # the backward's two operand tiles take turns in one LDS buffer where both do not fit, so it
-    # fits too, up to degree 8 at head dim 128 in float64 (the largest tile: 152 KiB)
-    from polytensors_amd._fused_attention import _tiles_fit_lds
-
-    for dtype in (torch.float64, torch.float32, torch.bfloat16):
-        for d in (16, 32, 64, 128):
-            assert all(_tiles_fit_lds(dtype, d, k, backward=b) for k in range(9) for b in (False, True))
-    assert not _tiles_fit_lds(torch.float64, 128, 9, backward=True)
-
-
 def test_masks_and_class_weights_that_require_grad_are_refused():
     # no gradient flows to attn_mask or to class weights: such calls are refused, not silently cut
     from polytensors_amd import _fused_attention, _fused_cross_entropy
