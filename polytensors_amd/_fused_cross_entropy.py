@@ -159,11 +159,15 @@ def _weighted(input, target, ignore_index, reduction, weight, label_smoothing):
     torch's cross_entropy decomposes into log_softmax and linear loss terms, which
     its general rules apply to every order. Per kept row, with lse the row's
     log-sum-exp series and the kernel's loss l = lse - z_y:
-        (1 - eps) w_y l + (eps / C) (W lse - sum_c w_c z_c),   W = sum_c w_c,
+        (1 - eps) w_y l + (eps / C) sum_c w_c (lse - z_c)
     (w = 1 without weights); ignored rows are zero, and "mean" divides by the kept
     rows' total target weight (their count without weights), as torch's
-    cross_entropy. The terms beyond l are series operations on the logits (gather,
-    weighted row sums), so autograd records them as it does the kernel's losses.
+    cross_entropy. The smoothing sum is formed from the differences lse - z_c, which
+    do not change when an order of the logits is shifted by a constant (as torch's
+    sum of w_c (-log_softmax_c)); W lse - sum_c w_c z_c would subtract two sums that
+    grow with such a shift. The terms beyond l are series operations on the logits
+    (gather, broadcast difference, weighted row sums), so autograd records them as
+    it does the kernel's losses.
     """
     losses = fused(input, target, ignore_index=ignore_index, reduction="none")
     dtype = losses.dtype
@@ -177,9 +181,8 @@ def _weighted(input, target, ignore_index, reduction, weight, label_smoothing):
         classes = input.shape[1]
         z = input if input.dtype == dtype else input.to(dtype)
         zy = z.gather(1, safe[:, None]).squeeze(1)
-        wz = z.sum(1) if w is None else (z * w).sum(1)
-        total_w = float(classes) if w is None else w.sum()
-        smooth = ((losses + zy) * total_w - wz) * kept
+        gap = (losses + zy).unsqueeze(1) - z   # lse - z_c, every class
+        smooth = (gap.sum(1) if w is None else (gap * w).sum(1)) * kept
         per_row = per_row * (1.0 - label_smoothing) + smooth * (label_smoothing / classes)
     if reduction == "none":
         return per_row

@@ -211,6 +211,29 @@ def test_weights_and_label_smoothing(dtype, reduction, weighted, smoothing):
     _check(loss.coeffs, want, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_label_smoothing_with_a_large_common_offset(dtype, weighted):
+    # logits shifted by +100 over C = 32000 classes: the smoothing term sum_c w_c (lse - z_c) does
+    # not depend on such a shift and must not lose precision to it. (A shift of the higher orders
+    # is another matter: the plain-range log-sum-exp series of [z_0, z_1 + c, ...] cancels terms of
+    # size c^k in every formulation, the reference's included, so it is not part of this case.)
+    degree, N, C = 3, 48, 32000
+    Z, y = _logits(N, C, degree, seed=65, dtype=torch.float64, base_scale=2.0)
+    Z = [(c + (100.0 if k == 0 else 0.0)).to(dtype) for k, c in enumerate(Z)]
+    y[::5] = -100
+    w = (torch.rand(C, generator=torch.Generator().manual_seed(66), dtype=torch.float64) + 0.5).to(dtype) \
+        if weighted else None
+    logits = PolyTensor(tuple(c.cuda() for c in Z))
+    for reduction in ("none", "mean"):
+        with torch.no_grad(), PolyTensor.plain_range():
+            loss = F.cross_entropy(logits, y.cuda(), weight=None if w is None else w.cuda(), reduction=reduction,
+                                   label_smoothing=0.1)
+        want = oracle.cross_entropy([c.double() for c in Z], y, reduction=reduction,
+                                    weight=None if w is None else w.double(), label_smoothing=0.1)
+        _check(loss.coeffs, want, dtype)
+
+
 @pytest.mark.parametrize("reduction", ["none", "mean"])
 def test_logits_with_extra_dimensions(reduction):
     # (N, C, d1, d2) logits with (N, d1, d2) targets: rows of C classes, as torch's cross_entropy

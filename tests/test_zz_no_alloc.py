@@ -73,3 +73,54 @@ def test_noalloc_refuses_reductions_beyond_its_scratch_array():
                                                      ptrs, None, None)
     assert status == PT_UNSUPPORTED
     assert "scratch" in lib.pt_last_error().decode()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("reduction", [1, 2])
+def test_noalloc_under_hip_graph_capture(reduction):
+    # the callers it is for: a HIP graph holding the no-alloc call. One eager call first (it
+    # looks up the scratch array's device address; capture records only the kernels). The graph
+    # must hold kernel nodes only (no memset), and each replay, with the inputs rewritten in place
+    # and eager work between replays, must equal the workspace entry point on those inputs.
+    import ctypes as C
+
+    lib = _lib.load()
+    degree, rows, classes = 3, 1500, 700
+    z, y = _series(rows, classes, degree, torch.float32, 7)
+    z, y = [c.cuda() for c in z], y.cuda()
+    loss = torch.empty(degree + 1, dtype=torch.float32, device="cuda")
+    lse = torch.empty(degree + 1, rows, dtype=torch.float32, device="cuda")
+    zp, lp, sp = _lib.ptr_array(z), _lib.ptr_array(list(loss.unbind(0))), _lib.ptr_array(list(lse.unbind(0)))
+
+    def call():
+        _lib.check(lib.pt_cross_entropy_series_fwd_noalloc(0, degree, zp, rows, classes, classes, y.data_ptr(), -100,
+                                                            0.0, reduction, lp, sp, _lib.stream_of(z[0].device)),
+                   "cross_entropy_series_fwd_noalloc")
+
+    call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        call()
+    hip = C.CDLL("libamdhip64.so.7")
+    raw, count = C.c_void_p(graph.raw_cuda_graph()), C.c_size_t(0)
+    assert hip.hipGraphGetNodes(raw, None, C.byref(count)) == 0 and count.value >= 1
+    nodes = (C.c_void_p * count.value)()
+    assert hip.hipGraphGetNodes(raw, nodes, C.byref(count)) == 0
+    kinds = set()
+    for i in range(count.value):
+        kind = C.c_int(-1)
+        hip.hipGraphNodeGetType(C.c_void_p(nodes[i]), C.byref(kind))
+        kinds.add(kind.value)
+    assert kinds == {0}, f"graph node types {kinds} (0 = kernel)"
+    graph.instantiate()
+    for replay in range(3):
+        g = torch.Generator(device="cuda").manual_seed(100 + replay)
+        for c in z:   # new inputs in place (eager work between replays)
+            c.copy_(torch.randn(c.shape, generator=g, device="cuda"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _run(lib, False, z, y, reduction, degree)
+        print(f"[noalloc graph] reduction={reduction} replay={replay}", flush=True)
+        assert torch.equal(loss, want[0]) and torch.equal(lse, want[1])
