@@ -25,11 +25,12 @@ small (about 6 at K = 3, 11 at K = 4, 170 at K = 8: the factor by which the real
 runs' rounding errors can grow in the complex result).
 """
 
+import contextlib
 import functools
 
 import torch
 
-from . import _ops
+from . import _gate, _ops
 from ._tensor import PolyTensor
 
 _NODE_RADIUS = {1: 1.0, 2: 1.5, 3: 1.5}
@@ -75,8 +76,6 @@ def _check(values, what):
         if isinstance(v, PolyTensor) and v.coeffs[0].is_complex():
             raise NotImplementedError(f"{what}: a complex constant coefficient (complex base) is not implemented; "
                                       "complex directions need a real constant term")
-    if torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in values):
-        raise NotImplementedError(f"{what}: reverse mode with complex directions is not implemented")
 
 
 def _flatten(values):
@@ -122,18 +121,114 @@ def _combine(outputs, weights):
     return PolyTensor((first.coeffs[0],) + tuple(planes.unbind(0)))
 
 
+@contextlib.contextmanager
+def _in_plain_range():
+    from ._plain import _plain_range
+
+    token = _plain_range.set(True)
+    try:
+        yield
+    finally:
+        _plain_range.reset(token)
+
+
+class _Variants(torch.autograd.Function):
+    """The real variants of a complex-direction series at the interpolation nodes, under
+    wrapper-level (PolyTensor) autograd.
+
+    Reverse mode needs the gradient series J(x(t))^T G(t) extended multilinearly to
+    complex x and G, as the forward is (/root/reference/docs/api.md:69-76). Its
+    coefficient k is again a polynomial of degree <= k in the substitution
+    c_j -> Re c_j + lam Im c_j applied to x's and G's higher orders (G_0 is real), so it
+    is the Lagrange combination of the real gradient series at the nodes, each formed
+    at the node's variants of x and of G. Hence the backward of "variants" is the
+    combination, and the backward of the combination (``_Combination``) is the
+    cotangent's variants: each node's real graph runs the real backward kernels.
+    """
+
+    @staticmethod
+    def forward(ctx, x):
+        nodes, weights = nodes_and_weights(x.degree)
+        ctx.weights = weights
+        return tuple(_variants(x, [1.0] * len(nodes), nodes))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        with _in_plain_range():   # the engine's thread does not see the caller's context
+            return _combine(list(grads), ctx.weights)
+
+
+class _Shared(torch.autograd.Function):
+    """A real operand (series or ordinary tensor) that requires grad, handed unchanged to every
+    node under wrapper-level autograd: its gradient series is the Lagrange combination of the
+    nodes' gradients (complex in general), not their sum."""
+
+    @staticmethod
+    def forward(ctx, x, degree):
+        nodes, weights = nodes_and_weights(degree)
+        ctx.weights = weights
+        return tuple(x.view_as(x) for _ in nodes)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        if all(isinstance(g, PolyTensor) for g in grads):
+            with _in_plain_range():
+                return _combine(list(grads), ctx.weights), None
+        return grads[0], None   # an ordinary gradient (order 0 only) is the same at every node
+
+
+class _Combination(torch.autograd.Function):
+    """The complex series sum_m w_m Y_m of the node outputs, under wrapper-level autograd
+    (see ``_Variants``): its backward hands each node the variant of the cotangent series."""
+
+    @staticmethod
+    def forward(ctx, *outputs):
+        ctx.degree = outputs[0].degree
+        return _combine(list(outputs), nodes_and_weights(ctx.degree)[1])
+
+    @staticmethod
+    def backward(ctx, grad):
+        nodes, _ = nodes_and_weights(ctx.degree)
+        if not _is_complex_series(grad):   # a real cotangent series is its own variant at every node
+            return tuple(grad for _ in nodes)
+        _check([grad], "reverse mode")
+        with _in_plain_range():
+            return tuple(_variants(grad, [1.0] * len(nodes), nodes))
+
+
 def at_real_nodes(fn, what, *args, **kwargs):
     """``fn(*args, **kwargs)`` for complex-direction series from K+1 runs on real directions.
 
     ``fn`` returns one PolyTensor. The real variants of every complex-direction
-    operand are formed in one pass per operand (all nodes at once).
+    operand are formed in one pass per operand (all nodes at once). Called above
+    autograd (the fused norm, cross entropy and attention) under wrapper-level
+    autograd, the variants and the combination are recorded (``_Variants``,
+    ``_Combination``), so that reverse mode runs each node's real backward
+    kernels; in coefficient autograd the plumbing operators record their own
+    (linear) gradients.
     """
     values = _flatten(list(args) + list(kwargs.values()))
+    return _nodes(fn, what, args, kwargs, values, _gate.wrapper_grad(*values))
+
+
+def at_real_nodes_below_autograd(fn, what, *args, **kwargs):
+    """``at_real_nodes`` for a rule reached from ``__torch_dispatch__`` (under the autograd layer,
+    which has recorded the operation's own backward): nothing is recorded here."""
+    values = _flatten(list(args) + list(kwargs.values()))
+    return _nodes(fn, what, args, kwargs, values, False)
+
+
+def _nodes(fn, what, args, kwargs, values, recorded):
     _check(values, what)
     degree = next(v.degree for v in values if isinstance(v, PolyTensor))
     nodes, weights = nodes_and_weights(degree)
     ones = [1.0] * len(nodes)
-    variants = {id(v): _variants(v, ones, nodes) for v in values if _is_complex_series(v)}
+    variants = {id(v): (_Variants.apply(v) if recorded else _variants(v, ones, nodes))
+                for v in values if _is_complex_series(v)}
+    if recorded:
+        for v in values:
+            if isinstance(v, torch.Tensor) and v.requires_grad and id(v) not in variants:
+                variants[id(v)] = _Shared.apply(v, degree)
     outputs = []
     for m in range(len(nodes)):
         table = {key: vs[m] for key, vs in variants.items()}
@@ -142,6 +237,8 @@ def at_real_nodes(fn, what, *args, **kwargs):
             raise TypeError(f"{what}: a series operation returned {type(out).__name__}")
         outputs.append(out)
     del variants
+    if recorded and any(out.requires_grad for out in outputs):
+        return _Combination.apply(*outputs)
     return _combine(outputs, weights)
 
 

@@ -8,7 +8,8 @@ Only the rules the hot path needs exist here:
     operand (the constant-operand fast path, _range_ops.py:109-132), sum and
     mean (_range_ops.py:178-193);
   * series (*) series and series / series (and ordinary / series), the
-    elementwise Cauchy product and quotient kernel (_range_ops.py:133-149);
+    elementwise Cauchy product and quotient kernel (_range_ops.py:133-149), and
+    pow with a scalar exponent built from them (or from exp and log);
   * the matrix products mm/bmm/addmm/mv/dot, which run the Cauchy-product
     kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84);
   * the elementwise activations gelu (erf and tanh forms), tanh, sigmoid,
@@ -118,6 +119,34 @@ def _to_copy_kwargs(coefficient, kwargs):
     if complex_dtype is None:
         raise TypeError(f"{dtype} cannot hold complex PolyTensor directions")
     return {**kwargs, "dtype": complex_dtype}
+
+
+def _power(x, exponent):
+    """Series of ``x ** exponent`` for a Python scalar exponent: an integral exponent by series
+    products (square and multiply; a negative one as the quotient 1 / x^|n|), any other as
+    exp(exponent * log x), as the reference's rules compose it from products, quotients and the
+    exp/log series (/root/reference/src/polytensors/_range_ops.py:133-149, _plain.py:153-171)."""
+    if isinstance(exponent, complex) or isinstance(exponent, bool):
+        raise NotImplementedError("PolyTensor pow takes a real exponent")
+    head = x.coeffs[0]
+    if float(exponent).is_integer():
+        n = int(exponent)
+        if n == 0:
+            return _wrap((torch.ones_like(head), *(torch.zeros_like(c) for c in x.coeffs[1:])))
+        result, base, m = None, x, abs(n)
+        while m:
+            if m & 1:
+                result = base if result is None else _fused_elementwise.binary(result, base, "mul")
+            m >>= 1
+            if m:
+                base = _fused_elementwise.binary(base, base, "mul")
+        if result is x:
+            result = _wrap(c.clone() for c in x.coeffs)
+        if n < 0:
+            result = _fused_elementwise.binary(torch.ones_like(head), result, "div")
+        return result
+    logs = _fused_activation.activation(x, "log")
+    return _fused_activation.activation(_wrap(c * exponent for c in logs.coeffs), "exp")
 
 
 def dispatch(func, types, args=(), kwargs=None):
@@ -231,6 +260,9 @@ def _dispatch(func, types, args, kwargs, polys):
         # quotient(1, x) (/root/reference/src/polytensors/_range_ops.py:86-93,157-158)
 
         return _fused_elementwise.binary(torch.ones_like(args[0].coeffs[0]), args[0], "div")
+
+    if func is aten.pow.Tensor_Scalar:
+        return _power(args[0], args[1])
 
     if func in _ADD or func in _SUB:
         a, b = args[0], args[1]

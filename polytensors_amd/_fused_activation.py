@@ -51,7 +51,7 @@ def activation(x, kind):
     if reason is not None:
         raise NotImplementedError(f"{kind}: {reason}")
     if _complex.has_complex(x):
-        return _complex.at_real_nodes(activation, kind, x, kind)
+        return _complex.at_real_nodes_below_autograd(activation, kind, x, kind)
     out = _ops.activation_series(_coeffs(x, x.degree), kind)
     return PolyTensor.from_stacked(out)
 
@@ -64,9 +64,11 @@ def backward(grad, saved, kind):
     """
     if kind not in BACKWARD_KINDS:
         raise NotImplementedError(f"{kind}_backward has no series kernel")
-    reason = why_ineligible(grad, saved)
+    reason = why_ineligible(grad, saved, complex_ok=True)
     if reason is not None:
         raise NotImplementedError(f"{kind}_backward: {reason}")
+    if _complex.has_complex(grad, saved):
+        return _complex.at_real_nodes_below_autograd(backward, f"{kind}_backward", grad, saved, kind)
     degree = next(x.degree for x in (grad, saved) if isinstance(x, PolyTensor))
     out = _ops.activation_series_backward(_coeffs(grad, degree), _coeffs(saved, degree), kind)
     return PolyTensor.from_stacked(out)

@@ -36,7 +36,7 @@ def binary(a, b, op):
     if _complex.has_complex(a, b):
         if op == "mul":
             return _complex.bilinear(binary, "series mul", a, b, op)
-        return _complex.at_real_nodes(binary, "series div", a, b, op)
+        return _complex.at_real_nodes_below_autograd(binary, "series div", a, b, op)
     degree = next(x.degree for x in (a, b) if isinstance(x, PolyTensor))
     shape = torch.broadcast_shapes(a.shape, b.shape)
 

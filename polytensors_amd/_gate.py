@@ -61,8 +61,6 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
         if any(p.requires_grad for p in polys):
             return ("coefficient_autograd differentiates the coefficient tensors: build the PolyTensor "
                     "wrappers with requires_grad=False")
-        if complex_dirs:
-            return "coefficient_autograd with complex directions is not implemented"
     elif torch.is_grad_enabled() and not below_autograd:
         grads = any(t.requires_grad for t in tensors) or any(
             c.requires_grad for p in polys for c in p.coeffs)

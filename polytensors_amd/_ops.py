@@ -254,9 +254,13 @@ def _(z, target, ignore_index, softcap, lse, cot):
 # reversed cotangents G_k = c_{K-k}: the backward kernels' own product, read in
 # reverse (at degree 1 the reference's "VJP with cotangents (G1, G0) and orders
 # swapped", /root/reference/docs/api.md:148-153). An operand given with one
-# order (an ordinary tensor) gets coefficient K. These backward functions are
-# not themselves differentiable (as the reference's once_differentiable fused
-# Functions, /root/reference/src/polytensors/_fused_attention.py:166-185).
+# order (an ordinary tensor) gets coefficient K. The backwards of the Cauchy
+# matmul, the series product and quotient, exp and log are themselves products
+# of those operators, so they differentiate again (further reverse derivatives,
+# as the reference's general rules allow, /root/reference/docs/api.md:137-139).
+# The norm, cross-entropy, attention and other activation backwards are single
+# gradient-series kernels without a kernel for their own derivative: they are
+# once-differentiable and refuse a graph of the gradient (create_graph).
 
 def _reversed(grad):
     """Cotangents of a stacked [K+1, ...] output in reverse order, as a coefficient list."""
@@ -342,7 +346,6 @@ def _mm_setup(ctx, inputs, output):
 
 
 def _mm_backward(ctx, grad):
-    _once("cauchy_matmul")
     na, nb, degree, trans_b, need_a, need_b = ctx.meta
     saved = ctx.saved_tensors
     a, b = list(saved[:na]), list(saved[na:])
@@ -415,8 +418,9 @@ def _act_setup(ctx, inputs, output):
 
 
 def _act_backward(ctx, grad):
-    _once("activation_series")
     kind = ctx.kind
+    if kind not in ("exp", "log"):
+        _once(f"activation_series ({kind})")
     saved = ctx.saved_tensors
     saved = list(saved[0].unbind(0)) if kind in _ACT_SAVES_OUTPUT else list(saved)
     g = _reversed(grad)
@@ -441,7 +445,6 @@ def _binary_setup(ctx, inputs, output):
 
 
 def _binary_backward(ctx, grad):
-    _once("series_binary")
     n, op = ctx.n, ctx.op
     s = ctx.saved_tensors
     a, b = list(s[:n]), list(s[n:2 * n])
@@ -456,3 +459,47 @@ def _binary_backward(ctx, grad):
 
 
 torch.library.register_autograd(f"{NAMESPACE}::series_binary", _binary_backward, setup_context=_binary_setup)
+
+
+# The complex-direction plumbing is linear in its inputs. Its gradients follow torch's
+# convention for complex tensors (the gradient of a real loss L with respect to a complex z is
+# dL/dRe z + i dL/dIm z), since in coefficient autograd the complex higher coefficients are
+# ordinary complex leaves: for v_a = alpha_a Re p + beta_a Im p the gradient of plane p is
+# sum_a (alpha_a + i beta_a) g_a; for y_k = sum_m w_m x_{m,k} with real x it is Re(conj(w_m) g_k).
+# Both are written with torch operations, so they differentiate again.
+
+def _c2r_setup(ctx, inputs, output):
+    src, alpha, beta = inputs
+    ctx.meta = (len(src), list(alpha), list(beta))
+    ctx.n_inputs = len(inputs)
+
+
+def _c2r_backward(ctx, grad):
+    planes, alpha, beta = ctx.meta
+    shape = (len(alpha),) + (1,) * (grad.dim() - 1)
+    a = torch.tensor(alpha, dtype=grad.dtype, device=grad.device).view(shape)
+    b = torch.tensor(beta, dtype=grad.dtype, device=grad.device).view(shape)
+    gp = torch.complex((a * grad).sum(0), (b * grad).sum(0))   # [planes, ...]
+    return _returned(ctx, list(gp.unbind(0)))
+
+
+torch.library.register_autograd(f"{NAMESPACE}::complex_to_real", _c2r_backward, setup_context=_c2r_setup)
+
+
+def _r2c_setup(ctx, inputs, output):
+    src, orders, wre, wim = inputs
+    ctx.meta = (len(src), orders, list(wre), list(wim))
+    ctx.n_inputs = len(inputs)
+
+
+def _r2c_backward(ctx, grad):
+    n, orders, wre, wim = ctx.meta
+    re, im = grad.real, grad.imag   # [orders, ...]
+    grads = []
+    for m in range(n // orders):
+        for k in range(orders):
+            grads.append(wre[m] * re[k] + wim[m] * im[k])
+    return _returned(ctx, grads)
+
+
+torch.library.register_autograd(f"{NAMESPACE}::real_to_complex", _r2c_backward, setup_context=_r2c_setup)

@@ -271,11 +271,3 @@ def test_float32_attention_and_cross_entropy_pipeline():
         return oracle.cross_entropy(logits, y)
 
     _compare(dev, cpu, qkv, seed=95, tol=1e-4)
-
-
-def test_complex_directions_are_refused():
-    x = PolyTensor((torch.randn(3, 8, device="cuda", dtype=torch.float64, requires_grad=True),
-                    torch.randn(3, 8, device="cuda", dtype=torch.complex128)))
-    with PolyTensor.plain_range(), PolyTensor.coefficient_autograd(), pytest.raises(NotImplementedError,
-                                                                                    match="complex"):
-        F.gelu(x)
