@@ -242,14 +242,91 @@ def _nodes(fn, what, args, kwargs, values, recorded):
     return _combine(outputs, weights)
 
 
+def has_complex_base(*values):
+    """Whether any operand is complex in its constant term: a series with a complex order 0, or a
+    complex ordinary tensor."""
+    for v in _flatten(list(values)):
+        if isinstance(v, PolyTensor):
+            if v.coeffs[0].is_complex():
+                return True
+        elif isinstance(v, torch.Tensor) and v.is_complex():
+            return True
+    return False
+
+
+def _split(x):
+    """(real part, imaginary part or None) of an operand, every order split (views)."""
+    if isinstance(x, PolyTensor):
+        if not x.coeffs[-1].is_complex() and not x.coeffs[0].is_complex():
+            return x, None
+        re = tuple(c.real if c.is_complex() else c for c in x.coeffs)
+        im = tuple(c.imag if c.is_complex() else torch.zeros_like(c) for c in x.coeffs)
+        return PolyTensor._wrap(re), PolyTensor._wrap(im)
+    if isinstance(x, torch.Tensor) and x.is_complex():
+        return x.real, x.imag
+    return x, None
+
+
+def _join(real, imag):
+    """The series real + i imag (either may be None: zero)."""
+    if imag is None:
+        return real
+    return PolyTensor(tuple(torch.complex(r, i) for r, i in zip(real.coeffs, imag.coeffs)))
+
+
+def _add(x, y, sign=1.0):
+    if x is None:
+        return y if sign > 0 or y is None else PolyTensor._wrap(tuple(-c for c in y.coeffs))
+    if y is None:
+        return x
+    return PolyTensor._wrap(tuple(a + sign * b for a, b in zip(x.coeffs, y.coeffs)))
+
+
+def complex_product(fn, a, b, *rest, **kwargs):
+    """``fn(a, b, ...)`` for a product bilinear in a and b when some operand has a complex constant
+    term (complex arithmetic, /root/reference/docs/notes.md:74-77): the real runs
+    fn(a_R, b_R) - fn(a_I, b_I) + i (fn(a_R, b_I) + fn(a_I, b_R)) of the real kernel, each operand
+    split order by order into its real and imaginary parts (a real operand has none)."""
+    ar, ai = _split(a)
+    br, bi = _split(b)
+    real = fn(ar, br, *rest, **kwargs)
+    imag = None
+    if ai is not None and bi is not None:
+        real = _add(real, fn(ai, bi, *rest, **kwargs), -1.0)
+    if bi is not None:
+        imag = fn(ar, bi, *rest, **kwargs)
+    if ai is not None:
+        imag = _add(imag, fn(ai, br, *rest, **kwargs))
+    return _join(real, imag)
+
+
+def complex_quotient(divide, multiply, a, b):
+    """a / b elementwise when some operand has a complex constant term: a conj(b) / (b conj(b)),
+    where b conj(b) = b_R (*) b_R + b_I (*) b_I is a real series (conj taken order by order, the
+    conjugate of b(t) for real t), so the quotient is two real quotient runs."""
+    br, bi = _split(b)
+    if bi is None:   # a real divisor: each part of a over b
+        ar, ai = _split(a)
+        return _join(divide(ar, b), None if ai is None else divide(ai, b))
+    conj_b = _join(br, PolyTensor._wrap(tuple(-c for c in bi.coeffs)))
+    numerator = complex_product(multiply, a, conj_b)
+    denominator = _add(multiply(br, br), multiply(bi, bi))
+    nr, ni = _split(numerator)
+    return _join(divide(nr, denominator), None if ni is None else divide(ni, denominator))
+
+
 def bilinear(fn, what, a, b, *rest, **kwargs):
     """``fn(a, b, ...)`` for an operation bilinear in the series a, b (Cauchy products).
 
     With one complex-direction series and one ordinary tensor, the imaginary run
     takes the imaginary planes as a series of degree K-1 (orders shifted down by
     one: an ordinary operand does not mix orders), so it forms K products, not
-    K+1. Two series operands use the four real runs of the complex product.
+    K+1. Two series operands use the four real runs of the complex product. An
+    operand with a complex constant term takes the general split
+    (``complex_product``).
     """
+    if has_complex_base(a, b):
+        return complex_product(fn, a, b, *rest, **kwargs)
     _check([a, b], what)
     ac, bc = _is_complex_series(a), _is_complex_series(b)
     if ac != bc and not isinstance(b if ac else a, PolyTensor):

@@ -18,11 +18,11 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
 def why_ineligible(a, b):
-    reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True)
+    reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True, complex_base_ok=True)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
-    dtype = coeffs[0].dtype
+    dtype = _gate.real_dtype(coeffs[0].dtype)
     if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "series operands must share one float16/bfloat16/float32/float64 dtype"
     return None
@@ -33,6 +33,11 @@ def binary(a, b, op):
     reason = why_ineligible(a, b)
     if reason is not None:
         raise NotImplementedError(f"series {op}: {reason}")
+    if _complex.has_complex_base(a, b):
+        mul = lambda x, y: binary(x, y, "mul")   # noqa: E731
+        if op == "mul":
+            return _complex.complex_product(mul, a, b)
+        return _complex.complex_quotient(lambda x, y: binary(x, y, "div"), mul, a, b)
     if _complex.has_complex(a, b):
         if op == "mul":
             return _complex.bilinear(binary, "series mul", a, b, op)

@@ -21,11 +21,11 @@ _HALF_MATRIX_LIMIT = 1 << 29
 
 
 def why_ineligible(a, b, below_autograd=False):
-    reason = _gate.common_reason((a, b), below_autograd=below_autograd, complex_ok=True)
+    reason = _gate.common_reason((a, b), below_autograd=below_autograd, complex_ok=True, complex_base_ok=True)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
-    dtype = coeffs[0].dtype
+    dtype = _gate.real_dtype(coeffs[0].dtype)
     if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for c in coeffs):
         return "operands must share one dtype, float32, float64, bfloat16 or float16"
     if a.ndim == 0 or b.ndim == 0:
@@ -51,7 +51,7 @@ def matmul(a, b, below_autograd=False):
     reason = why_ineligible(a, b, below_autograd)
     if reason is not None:
         raise NotImplementedError(f"matmul: {reason}")
-    if _complex.has_complex(a, b):
+    if _complex.has_complex(a, b) or _complex.has_complex_base(a, b):
         return _complex.bilinear(matmul, "matmul", a, b, below_autograd=below_autograd)
     degree = _degree(a, b)
     A = list(_gate.coefficients(a, degree))
@@ -98,7 +98,7 @@ def linear(x, weight, bias=None):
     reason = why_ineligible(x, weight)
     if reason is not None:
         raise NotImplementedError(f"linear: {reason}")
-    if _complex.has_complex(x, weight):
+    if _complex.has_complex(x, weight) or _complex.has_complex_base(x, weight):
         result = _complex.bilinear(linear, "linear", x, weight)
         return result if bias is None else result + bias
     degree = _degree(x, weight, *([bias] if isinstance(bias, PolyTensor) else []))

@@ -30,14 +30,17 @@ def coefficients(x, degree):
     return (x,)
 
 
-def common_reason(values, *, allow_plain_grad=False, below_autograd=False, complex_ok=False):
+def common_reason(values, *, allow_plain_grad=False, below_autograd=False, complex_ok=False,
+                  complex_base_ok=False):
     """Shared conditions over the tensor operands of one fused call.
 
     ``below_autograd``: the call comes from ``__torch_dispatch__``, under the
     autograd layer, which has already recorded the operation's native backward;
     operands requiring grad are then fine (the backward operations have rules too).
     ``complex_ok``: the entry point runs complex directions through its real kernel
-    (polytensors_amd._complex); a complex constant coefficient is still refused.
+    (polytensors_amd._complex). ``complex_base_ok``: it also takes a complex constant
+    term, in complex arithmetic (the bilinear products); reverse mode at the wrapper
+    level, which would follow torch's conjugating complex autograd, is refused there.
     """
     tensors = [v for v in values if isinstance(v, torch.Tensor)]
     polys = [v for v in tensors if isinstance(v, PolyTensor)]
@@ -68,7 +71,14 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
             return ("this operation has no wrapper-level gradient; use torch.no_grad(), or build a "
                     "coefficient graph inside PolyTensor.coefficient_autograd()")
     if any(t.is_complex() for t in plain) or any(p.coeffs[0].is_complex() for p in polys):
-        return "a complex constant term (complex base) is not implemented; complex directions need a real base"
+        if not complex_base_ok:
+            return ("a complex constant term (complex base) is implemented for the bilinear products "
+                    "(matmul, series product and quotient, integer powers) only; this kernel is real-valued, "
+                    "complex directions need a real base")
+        if wrapper_grad(*tensors) or (torch.is_grad_enabled() and not _coefficient_autograd_enabled.get() and
+                                      any(c.requires_grad for p in polys for c in p.coeffs)):
+            return ("reverse mode with a complex constant term (torch's conjugating complex autograd) is not "
+                    "implemented; use coefficient_autograd or complex directions over a real base")
     if not complex_ok and complex_dirs:
         return "complex directions are not implemented for this operation"
     if not (all(p.coeffs[0].is_cuda for p in polys) and all(t.is_cuda for t in plain)):

@@ -292,3 +292,100 @@ def test_complex64_at_high_degree(degree):
     _check(ge.coeffs, oracle.activation(_up(X, dt), "gelu"), dt)
     _check(ce.coeffs, oracle.cross_entropy(_up(Z, dt), y), dt)
     _check(qu.coeffs, oracle.quotient(_up(A, dt), _up(B, dt)), dt)
+
+
+# ---------------------------------------------------------------------------
+# A complex constant term (complex base): complex arithmetic in the bilinear products
+# (/root/reference/docs/notes.md:74-77: "a complex constant coefficient uses PyTorch's complex
+# semantics"), against the oracle's complex arithmetic (torch.matmul and elementwise products of
+# complex tensors, /root/reference/src/polytensors/_plain.py:118-128).
+
+def _complex_series(shape, degree, seed, dtype=torch.complex128):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.complex(torch.randn(shape, generator=g, dtype=torch.float64),
+                          torch.randn(shape, generator=g, dtype=torch.float64)).to(dtype) * 0.5 ** k
+            for k in range(degree + 1)]
+
+
+def _check_series(got, want, tol, what):
+    for k, (a, b) in enumerate(zip(got, want)):
+        err = rel_err(a.detach().cpu(), b)
+        assert err <= tol, f"{what} order {k}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.complex128, 1e-10), (torch.complex64, 1e-4)])
+@pytest.mark.parametrize("degree", [1, 3])
+def test_complex_base_matmul(dtype, tol, degree):
+    A = _complex_series((2, 17, 24), degree, 300, dtype)
+    B = _complex_series((24, 9), degree, 301, dtype)
+    W = _complex_series((24, 9), 0, 302, dtype)[0]
+    real = torch.float64 if dtype == torch.complex128 else torch.float32
+    Breal = [torch.randn(24, 9, generator=torch.Generator().manual_seed(303 + k), dtype=real) for k in range(degree + 1)]
+    a, b, breal = (PolyTensor(tuple(c.cuda() for c in s)) for s in (A, B, Breal))
+    up = lambda s: [c.to(torch.complex128) for c in s]   # noqa: E731
+    with torch.no_grad(), PolyTensor.plain_range():
+        _check_series((a @ b).coeffs, oracle.matmul(up(A), up(B)), tol, "series @ series")
+        _check_series((a @ W.cuda()).coeffs, oracle.matmul(up(A), [W.to(torch.complex128)]), tol, "series @ plain")
+        _check_series((a @ breal).coeffs, oracle.matmul(up(A), [c.to(torch.complex128) for c in Breal]), tol,
+                      "complex base @ real series")
+        _check_series(F.linear(a, W.t().contiguous().cuda()).coeffs,
+                      oracle.matmul(up(A), [W.to(torch.complex128)]), tol, "linear")
+
+
+@pytest.mark.parametrize("degree", [2, 4])
+def test_complex_base_elementwise_product_quotient_and_powers(degree):
+    X = _complex_series((7, 33), degree, 310)
+    Y = _complex_series((7, 33), degree, 311)
+    Y[0] = Y[0] + 3.0   # keep the divisor away from zero
+    g = torch.Generator().manual_seed(312)
+    R = [torch.randn(7, 33, generator=g, dtype=torch.float64) * 0.5 ** k for k in range(degree + 1)]
+    R[0] = R[0].abs() + 1.0
+    D = [R[0]] + [torch.complex(torch.randn(7, 33, generator=g, dtype=torch.float64),
+                                torch.randn(7, 33, generator=g, dtype=torch.float64)) for _ in range(degree)]
+    x, y, r, d = (PolyTensor(tuple(c.cuda() for c in s)) for s in (X, Y, R, D))
+    with torch.no_grad(), PolyTensor.plain_range():
+        _check_series((x * y).coeffs, oracle.cauchy(X, Y), 1e-10, "x * y")
+        _check_series((x * r).coeffs, oracle.cauchy(X, R), 1e-10, "x * real series")
+        _check_series((x * d).coeffs, oracle.cauchy(X, [c.to(torch.complex128) for c in D]), 1e-10,
+                      "x * complex-direction series")
+        _check_series((x / y).coeffs, oracle.quotient(X, Y), 1e-10, "x / y")
+        _check_series((x / r).coeffs, oracle.quotient(X, R), 1e-10, "x / real series")
+        _check_series((r / y).coeffs, oracle.quotient([c.to(torch.complex128) for c in R], Y), 1e-10,
+                      "real series / y")
+        cube = oracle.cauchy(oracle.cauchy(X, X), X)
+        _check_series(x.pow(3).coeffs, cube, 1e-10, "x ** 3")
+        _check_series(x.pow(-2).coeffs, oracle.quotient([torch.ones_like(X[0])] + [torch.zeros_like(c) for c in X[1:]],
+                                                         oracle.cauchy(X, X)), 1e-10, "x ** -2")
+
+
+def test_complex_base_coefficient_autograd_matches_autograd_of_the_oracle():
+    degree = 2
+    A = _complex_series((5, 12), degree, 320)
+    B = _complex_series((12, 4), degree, 321)
+    Wt = _complex_series((5, 4), degree, 322)
+
+    def loss(a):   # real loss of the complex product's coefficients
+        y = oracle.matmul(a, B)
+        return sum((yk * wk).real.sum() for yk, wk in zip(y, Wt))
+
+    leaves = [c.clone().requires_grad_() for c in A]
+    want = torch.autograd.grad(loss(leaves), leaves)
+    cl = [c.cuda().requires_grad_() for c in A]
+    with PolyTensor.plain_range(), PolyTensor.coefficient_autograd():
+        y = PolyTensor(tuple(cl)) @ PolyTensor(tuple(c.cuda() for c in B))
+    total = sum((yk * wk.cuda()).real.sum() for yk, wk in zip(y.coeffs, Wt))
+    got = torch.autograd.grad(total, cl)
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert rel_err(a.cpu(), b) <= 1e-10, f"gradient of coefficient {k}"
+
+
+def test_complex_base_refusals():
+    with PolyTensor.plain_range():
+        x = PolyTensor(tuple(c.cuda() for c in _complex_series((4, 8), 2, 330)), requires_grad=True)
+        w = torch.randn(8, 3, dtype=torch.complex128, device="cuda")
+        with pytest.raises(NotImplementedError, match="reverse mode with a complex constant term"):
+            x @ w
+        with torch.no_grad(), pytest.raises(NotImplementedError, match="complex base"):
+            F.gelu(x)
+        with torch.no_grad(), pytest.raises(NotImplementedError, match="complex base"):
+            F.layer_norm(x, (8,))
