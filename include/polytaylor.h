@@ -28,8 +28,11 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 12
+#define PT_ABI_VERSION 13
 #define PT_MAX_DEGREE 8
+/* Largest degree of the elementwise kernels (pt_activation_series_*, pt_series_binary): their
+ * register plans are per element, so they run above PT_MAX_DEGREE. */
+#define PT_MAX_ELEMENTWISE_DEGREE 16
 
 typedef enum pt_dtype {
   PT_FLOAT32 = 0,
@@ -59,6 +62,9 @@ int pt_abi_version(void);
 
 /* Largest supported degree K (PT_MAX_DEGREE). */
 int pt_max_degree(void);
+
+/* Largest degree of the elementwise kernels (PT_MAX_ELEMENTWISE_DEGREE). */
+int pt_max_elementwise_degree(void);
 
 /*
  * RMSNorm of a degree-K series over the last `n` elements of each of `rows`
@@ -359,7 +365,7 @@ size_t pt_taylor_attention_bwd_workspace_size(int dtype, int degree, int64_t bh,
  *   beta[v] Im(src[o]) for v < variants (real nodes: (1, lam_v); a real /
  *   imaginary split: (1, 0), (0, 1)).
  * pt_real_to_complex: writes dst[o] = sum_v (wre[v] + i wim[v]) src[v * orders + o].
- * orders <= 8, variants <= 9; PT_FLOAT32 (complex64) or PT_FLOAT64
+ * orders <= 16, variants <= 17; PT_FLOAT32 (complex64) or PT_FLOAT64
  * (complex128); alpha/beta/wre/wim are host arrays. 16-byte aligned planes take
  * 16-byte accesses, others a scalar path.
  */
@@ -378,13 +384,21 @@ typedef enum pt_activation {
   PT_ACT_SIGMOID = 3,
   PT_ACT_SILU = 4,      /* x * sigmoid(x) */
   PT_ACT_EXP = 5,       /* forward only */
-  PT_ACT_LOG = 6        /* forward only */
+  PT_ACT_LOG = 6,       /* forward only */
+  PT_ACT_SIN = 7,       /* forward only */
+  PT_ACT_COS = 8,       /* forward only */
+  PT_ACT_SQRT = 9,      /* forward only */
+  PT_ACT_RSQRT = 10     /* forward only */
 } pt_activation;
 
 /*
- * Elementwise activation of a degree-K series: y(t) = f(x(t)).
+ * Elementwise activation of a degree-K series: y(t) = f(x(t)), K up to
+ * PT_MAX_ELEMENTWISE_DEGREE.
  * x, y: K+1 pointers, each `numel` elements of `dtype` (any shape, dense).
  * Arithmetic float32 (float64 for PT_FLOAT64); order 0 is f(x_0).
+ * PT_ACT_SIN / PT_ACT_COS follow s' = c u', c' = -s u'; PT_ACT_SQRT / PT_ACT_RSQRT the power
+ * recurrence k x_0 y_k = sum_{j=1..k} ((p+1) j - k) x_j y_{k-j} with p = 1/2, -1/2 (for
+ * PT_ACT_RSQRT the reference's poly_rsqrt, /root/reference/src/polytensors/_series.py:83-96).
  * Replaces the fused degree-1 activation of the reference
  *   /root/reference/src/polytensors/_fused_activation.py:5-24 (maybe_activation),
  *   /root/reference/src/polytensors/_activation_kernels.py:8-38 (_activation),
@@ -408,7 +422,8 @@ int pt_activation_series_fwd(int dtype, int degree, int kind,
  *        series x; for PT_ACT_TANH and PT_ACT_SIGMOID the forward OUTPUT
  *        series y (as aten.tanh_backward / aten.sigmoid_backward take it).
  * g, saved, dx: K+1 pointers, each `numel` elements of `dtype`.
- * PT_ACT_EXP and PT_ACT_LOG return PT_UNSUPPORTED.
+ * The forward-only kinds (PT_ACT_EXP, PT_ACT_LOG, PT_ACT_SIN, PT_ACT_COS, PT_ACT_SQRT,
+ * PT_ACT_RSQRT: their gradients are products of forward series) return PT_UNSUPPORTED.
  * Replaces the BACKWARD mode of
  *   /root/reference/src/polytensors/_activation_kernels.py:8-38 (degree 1),
  * generalised with the reference's gradient-series rules
@@ -427,7 +442,8 @@ typedef enum pt_binary {
 } pt_binary;
 
 /*
- * Elementwise product or quotient of two degree-K series of one shape:
+ * Elementwise product or quotient of two degree-K series of one shape (K up to
+ * PT_MAX_ELEMENTWISE_DEGREE):
  *   PT_BINARY_MUL  y_k = sum_{i+j=k} a_i b_j,
  *   PT_BINARY_DIV  y_k = (a_k - sum_{i=1..k} b_i y_{k-i}) / b_0.
  * a, b, y: K+1 pointers, each `numel` elements of `dtype`.

@@ -22,7 +22,10 @@ bilinear form).
 
 Nodes are equispaced on [-r, r] with r chosen per degree to keep sum_m |w_m| r^K
 small (about 6 at K = 3, 11 at K = 4, 170 at K = 8: the factor by which the real
-runs' rounding errors can grow in the complex result).
+runs' rounding errors can grow in the complex result); above degree 12, r = 3
+(measured on the exponential series: relative errors of the combination about
+3e-5 from float32 runs and 1e-13 from float64 runs at degree 16, against 3e-4 and
+1e-12 with r = 2; Chebyshev nodes measured worse at every radius tried).
 """
 
 import contextlib
@@ -40,7 +43,7 @@ _NODE_RADIUS = {1: 1.0, 2: 1.5, 3: 1.5}
 def nodes_and_weights(degree):
     """Real nodes lam_m and the complex Lagrange weights w_m = l_m(i) (Python floats/complex)."""
     n = degree + 1
-    r = _NODE_RADIUS.get(degree, 2.0)
+    r = _NODE_RADIUS.get(degree, 2.0 if degree <= 12 else 3.0)
     nodes = [0.0] if n == 1 else [r * (2 * m / (n - 1) - 1) for m in range(n)]
     weights = []
     for m, xm in enumerate(nodes):

@@ -13,7 +13,8 @@ Only the rules the hot path needs exist here:
   * the matrix products mm/bmm/addmm/mv/dot, which run the Cauchy-product
     kernel (_range_ops.py:160-176 -> convolution(matrix=True), :78-84);
   * the elementwise activations gelu (erf and tanh forms), tanh, sigmoid,
-    silu, exp, log and the gelu/tanh/sigmoid/silu backward operations, which
+    silu, exp, log, sin, cos, sqrt, rsqrt and the gelu/tanh/sigmoid/silu
+    backward operations, which
     run the activation-series kernel (the reference's rules,
     /root/reference/src/polytensors/_plain.py:276-355 and
     /root/reference/src/polytensors/_dispatch.py:460-473,612-638).
@@ -62,7 +63,8 @@ _MUL = {aten.mul.Tensor, aten.mul.Scalar}
 _DIV = {aten.div.Tensor, aten.div.Scalar}
 _MATMUL = {aten.mm.default, aten.bmm.default, aten.mv.default, aten.dot.default, aten.matmul.default}
 _ACTIVATION = {aten.tanh.default: "tanh", aten.sigmoid.default: "sigmoid", aten.silu.default: "silu",
-               aten.exp.default: "exp", aten.log.default: "log"}
+               aten.exp.default: "exp", aten.log.default: "log", aten.sin.default: "sin", aten.cos.default: "cos",
+               aten.sqrt.default: "sqrt", aten.rsqrt.default: "rsqrt"}
 # (grad_output, output) for tanh/sigmoid, (grad_output, self) for silu
 _ACTIVATION_BACKWARD = {aten.tanh_backward.default: "tanh", aten.sigmoid_backward.default: "sigmoid",
                         aten.silu_backward.default: "silu"}
@@ -145,6 +147,8 @@ def _power(x, exponent):
         if n < 0:
             result = _fused_elementwise.binary(torch.ones_like(head), result, "div")
         return result
+    if exponent in (0.5, -0.5):
+        return _fused_activation.activation(x, "sqrt" if exponent > 0 else "rsqrt")
     logs = _fused_activation.activation(x, "log")
     return _fused_activation.activation(_wrap(c * exponent for c in logs.coeffs), "exp")
 
@@ -158,7 +162,7 @@ def dispatch(func, types, args=(), kwargs=None):
         return func(*args, **kwargs)
     from ._plain import _plain_range, in_backward, plain_range_enabled
 
-    if not plain_range_enabled() and in_backward() and any(getattr(p, "_plain", False) for p in polys):
+    if not plain_range_enabled() and in_backward():
         token = _plain_range.set(True)
         try:
             return _dispatch(func, types, args, kwargs, polys)

@@ -1,12 +1,13 @@
-"""Fused elementwise activation series (any degree up to 8) on gfx950.
+"""Fused elementwise activation series (any degree up to 16) on gfx950.
 
 The reference fuses first-order GELU/tanh/sigmoid and their native backward
 operations (/root/reference/src/polytensors/_fused_activation.py:5-24, Triton
 kernel _activation_kernels.py:8-38) and otherwise composes the derivatives of
 the activation at the constant term (/root/reference/src/polytensors/_plain.py:174-259,
 plain_rule :276-355). Here one kernel computes the whole series of
-gelu (erf and tanh forms), tanh, sigmoid, silu, exp and log, and the gradient
-series of the gelu/tanh/sigmoid/silu backward operations, at any degree up to 8.
+gelu (erf and tanh forms), tanh, sigmoid, silu, exp, log, sin, cos, sqrt and
+rsqrt, and the gradient series of the gelu/tanh/sigmoid/silu backward
+operations, at any degree up to 16.
 Inputs are made contiguous first, as the reference's fused path does (:17).
 Half and bfloat16 compute in float32, float64 in float64.
 """
@@ -23,7 +24,8 @@ BACKWARD_KINDS = ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu")
 def why_ineligible(*operands, complex_ok=False):
     # Reached from __torch_dispatch__ only: autograd above has recorded the native
     # backward operation (gelu_backward, tanh_backward, ...), which routes here too.
-    reason = _gate.common_reason(operands, below_autograd=True, complex_ok=complex_ok)
+    reason = _gate.common_reason(operands, below_autograd=True, complex_ok=complex_ok,
+                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     polys = [x for x in operands if isinstance(x, PolyTensor)]
@@ -46,7 +48,8 @@ def _coeffs(x, degree):
 
 
 def activation(x, kind):
-    """Series of ``f(x)`` for ``kind`` in gelu, gelu_tanh, tanh, sigmoid, silu, exp, log."""
+    """Series of ``f(x)`` for ``kind`` in gelu, gelu_tanh, tanh, sigmoid, silu, exp, log, sin, cos,
+    sqrt, rsqrt."""
     reason = why_ineligible(x, complex_ok=True)
     if reason is not None:
         raise NotImplementedError(f"{kind}: {reason}")

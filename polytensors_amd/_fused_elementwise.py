@@ -1,4 +1,4 @@
-"""Elementwise product and quotient of two series (any degree up to 8) on gfx950.
+"""Elementwise product and quotient of two series (any degree up to 16) on gfx950.
 
 The reference multiplies and divides series elementwise by its general rules
 (/root/reference/src/polytensors/_range_ops.py:133-149): the Cauchy product
@@ -18,7 +18,8 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
 def why_ineligible(a, b):
-    reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True, complex_base_ok=True)
+    reason = _gate.common_reason((a, b), below_autograd=True, complex_ok=True, complex_base_ok=True,
+                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]

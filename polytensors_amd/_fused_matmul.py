@@ -7,7 +7,8 @@ mm/bmm/matmul/linear/addmm rules of /root/reference/src/polytensors/_range_ops.p
 An ordinary-tensor operand is a series with one order (the reference lifts it
 with zero orders, _range_ops.py:37-45), so only K+1 products are formed.
 Batch dimensions broadcast as in torch.matmul; float32 and float64, and
-bfloat16 / float16 with fp32 accumulation and one rounding per element.
+bfloat16 / float16 with fp32 accumulation and one rounding per element. Above
+the kernel's degree (8, up to 16) the product runs in blocks of 9 orders.
 """
 
 import torch
@@ -21,7 +22,8 @@ _HALF_MATRIX_LIMIT = 1 << 29
 
 
 def why_ineligible(a, b, below_autograd=False):
-    reason = _gate.common_reason((a, b), below_autograd=below_autograd, complex_ok=True, complex_base_ok=True)
+    reason = _gate.common_reason((a, b), below_autograd=below_autograd, complex_ok=True, complex_base_ok=True,
+                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     coeffs = [c for x in (a, b) for c in _gate.coefficients(x, 0)]
@@ -36,6 +38,62 @@ def why_ineligible(a, b, below_autograd=False):
             if rows * (-(-x.shape[-1] // 8) * 8) >= _HALF_MATRIX_LIMIT:
                 return "16-bit operand matrices must stay below 2^29 elements"
     return None
+
+
+def _cauchy(A, B, degree, trans_b):
+    """The Cauchy-product kernel's stacked [K+1, batch, m, n] result for operand coefficient lists
+    A (1 or K+1 orders) and B; above the kernel's degree, in blocks of its orders.
+
+    With blocks of m = MAX_DEGREE + 1 orders, X = sum_p t^(m p) X^(p) and
+    A (*) B = sum_{p,q} t^(m (p+q)) A^(p) (*) B^(q), each block product being the full product of two
+    degree-(m-1) series: its orders 0..m-1 are one kernel launch, and its orders m..2m-2 another on
+    the blocks with their orders reversed (order r of the reversed product is order 2m-2-r of the
+    forward one). An ordinary operand needs no blocking of its own: C_k = A_k B_0 per block of A.
+    """
+    cap = _gate.MAX_DEGREE
+    if degree <= cap:
+        return _ops.cauchy_matmul(A, B, degree, trans_b)
+    m = cap + 1
+
+    def block(X, p):   # orders m p .. m p + m - 1, zero past the given ones
+        part = list(X[m * p: m * (p + 1)])
+        return part + [torch.zeros_like(X[0]) for _ in range(m - len(part))]
+
+    out = [None] * (degree + 1)
+
+    def add(k, value):
+        out[k] = value if out[k] is None else out[k] + value
+
+    blocks = -(-(degree + 1) // m)
+    if len(A) == 1 or len(B) == 1:
+        for p in range(blocks):
+            low = _ops.cauchy_matmul(block(A, p) if len(A) > 1 else A, block(B, p) if len(B) > 1 else B, cap, trans_b)
+            for j in range(m):
+                if m * p + j <= degree:
+                    add(m * p + j, low[j])
+    else:
+        for p in range(blocks):
+            for q in range(blocks):
+                base = m * (p + q)
+                if base > degree:
+                    continue
+                ap, bq = block(A, p), block(B, q)
+                low = _ops.cauchy_matmul(ap, bq, cap, trans_b)
+                for j in range(min(m, degree - base + 1)):
+                    add(base + j, low[j])
+                if base + m <= degree:
+                    # orders 0..cap-1 of the reversed blocks give orders 2 cap .. cap + 1 of the block product
+                    high = _ops.cauchy_matmul(ap[::-1][:cap], bq[::-1][:cap], cap - 1, trans_b)
+                    for r in range(m - 1):
+                        k = base + 2 * cap - r
+                        if k <= degree:
+                            add(k, high[r])
+    zero = None
+    for k in range(degree + 1):
+        if out[k] is None:
+            zero = torch.zeros_like(out[0]) if zero is None else zero
+            out[k] = zero
+    return torch.stack(out)
 
 
 def eligible(a, b):
@@ -82,9 +140,9 @@ def matmul(a, b, below_autograd=False):
 
     if all(c.ndim == 2 and not c.is_contiguous() and c.t().is_contiguous() for c in B):
         # a transposed [n, k] matrix (a linear layer's weight): the kernel reads it in place
-        out = _ops.cauchy_matmul(flat(A, m, kd), [c.t().reshape(1, n, kd) for c in B], degree, True)
+        out = _cauchy(flat(A, m, kd), [c.t().reshape(1, n, kd) for c in B], degree, True)
     else:
-        out = _ops.cauchy_matmul(flat(A, m, kd), flat(B, kd, n), degree, False)
+        out = _cauchy(flat(A, m, kd), flat(B, kd, n), degree, False)
     out = out.view(degree + 1, *batch, m, n)
     if squeeze_m:
         out = out.squeeze(-2)
@@ -110,7 +168,7 @@ def linear(x, weight, bias=None):
     lead = X[0].shape[:-1]
     X = [c.reshape(1, -1, in_features).contiguous() for c in X]
     W = [c.reshape(1, out_features, in_features).contiguous() for c in W]
-    out = _ops.cauchy_matmul(X, W, degree, True)
+    out = _cauchy(X, W, degree, True)
     result = PolyTensor.from_stacked(out.view(degree + 1, *lead, out_features))
     if bias is not None:
         result = result + bias

@@ -15,6 +15,9 @@ from ._plain import plain_range_enabled
 from ._tensor import PolyTensor, _coefficient_autograd_enabled
 
 MAX_DEGREE = 8
+# the elementwise kernels (activations, series product and quotient) and the Cauchy matmul, which
+# runs above MAX_DEGREE in blocks of orders
+MAX_ELEMENTWISE_DEGREE = 16
 _REAL_OF = {torch.complex32: torch.float16, torch.complex64: torch.float32, torch.complex128: torch.float64}
 
 
@@ -31,7 +34,7 @@ def coefficients(x, degree):
 
 
 def common_reason(values, *, allow_plain_grad=False, below_autograd=False, complex_ok=False,
-                  complex_base_ok=False):
+                  complex_base_ok=False, max_degree=MAX_DEGREE):
     """Shared conditions over the tensor operands of one fused call.
 
     ``below_autograd``: the call comes from ``__torch_dispatch__``, under the
@@ -41,6 +44,8 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
     (polytensors_amd._complex). ``complex_base_ok``: it also takes a complex constant
     term, in complex arithmetic (the bilinear products); reverse mode at the wrapper
     level, which would follow torch's conjugating complex autograd, is refused there.
+    ``max_degree``: the entry point's largest degree (MAX_DEGREE for the MFMA and row
+    kernels, MAX_ELEMENTWISE_DEGREE for the elementwise ones and the matmul).
     """
     tensors = [v for v in values if isinstance(v, torch.Tensor)]
     polys = [v for v in tensors if isinstance(v, PolyTensor)]
@@ -52,8 +57,8 @@ def common_reason(values, *, allow_plain_grad=False, below_autograd=False, compl
     degree = polys[0].degree
     if any(p.degree != degree for p in polys):
         return "PolyTensor operands must have the same degree"
-    if degree > MAX_DEGREE:
-        return f"degree {degree} exceeds the kernels' maximum {MAX_DEGREE}"
+    if degree > max_degree:
+        return f"degree {degree} exceeds this kernel's maximum {max_degree}"
     plain = [t for t in tensors if not isinstance(t, PolyTensor)]
     # A series' orders share one device, its higher orders one dtype (the coercion rules of
     # PolyTensor), so the constant and the last order stand for every coefficient below.

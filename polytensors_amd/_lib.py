@@ -15,13 +15,14 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor.so")
 # the operators' PyTorch registration (csrc/torch_ops.cpp), linked with libpolytaylor.so
 TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libpolytaylor_torch.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PT_OK, PT_INVALID_ARGUMENT, PT_UNSUPPORTED, PT_DEVICE_ERROR = 0, 1, 2, 3
 REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
 # pt_activation codes of include/polytaylor.h
 BINARY_OPS = {"mul": 0, "div": 1}
-ACTIVATIONS = {"gelu": 0, "gelu_tanh": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "exp": 5, "log": 6}
+ACTIVATIONS = {"gelu": 0, "gelu_tanh": 1, "tanh": 2, "sigmoid": 3, "silu": 4, "exp": 5, "log": 6, "sin": 7,
+               "cos": 8, "sqrt": 9, "rsqrt": 10}
 
 DTYPE_CODES = {
     torch.float32: 0,
@@ -39,6 +40,7 @@ SIGNATURES = {
     "pt_last_error": (ctypes.c_char_p, []),
     "pt_abi_version": (_c_int, []),
     "pt_max_degree": (_c_int, []),
+    "pt_max_elementwise_degree": (_c_int, []),
     "pt_rms_norm_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_int, _c_vpp,
                                         _c_i64, _c_i64, _c_dbl, _c_vp]),
     "pt_layer_norm_series_fwd": (_c_int, [_c_int, _c_int, _c_vpp, _c_vpp, _c_int, _c_vpp, _c_int,

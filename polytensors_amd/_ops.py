@@ -404,7 +404,9 @@ def _attn_backward(ctx, grad_out, grad_lse):
 torch.library.register_autograd(f"{NAMESPACE}::taylor_attention_fwd", _attn_backward, setup_context=_attn_setup)
 
 # the derivative's saved series: the input, or the output where the backward operation takes it
-_ACT_SAVES_OUTPUT = ("tanh", "sigmoid", "exp")
+_ACT_SAVES_OUTPUT = ("tanh", "sigmoid", "exp", "sqrt", "rsqrt")
+# kinds whose gradient series is a product of forward series (differentiable again)
+_ACT_PRODUCT_BACKWARD = ("exp", "log", "sin", "cos", "sqrt", "rsqrt")
 
 
 def _act_setup(ctx, inputs, output):
@@ -419,7 +421,7 @@ def _act_setup(ctx, inputs, output):
 
 def _act_backward(ctx, grad):
     kind = ctx.kind
-    if kind not in ("exp", "log"):
+    if kind not in _ACT_PRODUCT_BACKWARD:
         _once(f"activation_series ({kind})")
     saved = ctx.saved_tensors
     saved = list(saved[0].unbind(0)) if kind in _ACT_SAVES_OUTPUT else list(saved)
@@ -428,6 +430,16 @@ def _act_backward(ctx, grad):
         dx = series_binary(g, saved, "mul")
     elif kind == "log":    # log' = 1/x: G / x
         dx = series_binary(g, saved, "div")
+    elif kind == "sin":    # sin' = cos
+        dx = series_binary(g, list(activation_series(saved, "cos").unbind(0)), "mul")
+    elif kind == "cos":    # cos' = -sin
+        dx = -series_binary(g, list(activation_series(saved, "sin").unbind(0)), "mul")
+    elif kind == "sqrt":   # sqrt' = 1 / (2 y)
+        dx = 0.5 * series_binary(g, saved, "div")
+    elif kind == "rsqrt":  # rsqrt' = -y^3 / 2
+        y2 = list(series_binary(saved, saved, "mul").unbind(0))
+        y3 = list(series_binary(y2, saved, "mul").unbind(0))
+        dx = -0.5 * series_binary(g, y3, "mul")
     else:
         dx = activation_series_backward(g, saved, kind)
     return _returned(ctx, _read_back(dx, len(saved)))

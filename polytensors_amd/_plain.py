@@ -18,9 +18,10 @@ def in_backward():
 
     The engine runs a CUDA graph's backward on its own device thread, where the
     caller's ``plain_range()`` context variable is not set. The reference's rules
-    then fall back to its default mode; this package has no other mode, so a
-    backward operation whose operands were created in plain range runs in plain
-    range (``_dispatch.dispatch``), as if the context had travelled with the graph.
+    then fall back to its default mode; this package has no other mode (its
+    forward operations run in plain range only, so every graph reaching backward
+    was recorded there), so backward operations run in plain range
+    (``_dispatch.dispatch``), as if the context had travelled with the graph.
     """
     import torch
 

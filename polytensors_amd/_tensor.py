@@ -22,8 +22,6 @@ import operator
 
 import torch
 
-from ._plain import plain_range_enabled
-
 _retention_scopes = contextvars.ContextVar("polytensors_amd_retention_scopes", default=())
 _coefficient_autograd_enabled = contextvars.ContextVar("polytensors_amd_coefficient_autograd", default=False)
 _DK = torch._C.DispatchKey
@@ -187,7 +185,6 @@ class PolyTensor(torch.Tensor):
             dtype=head.dtype, layout=head.layout, device=head.device, requires_grad=requires_grad)
         out.coeffs = coeffs
         out.degree = len(coeffs) - 1
-        out._plain = plain_range_enabled()
         for scope in _retention_scopes.get():
             scope.append(out)
         return out

@@ -11,6 +11,10 @@
 //   silu     u (*) sigmoid(u)
 //   gelu_tanh 0.5 u (*) (1 + tanh(v)),  v = sqrt(2/pi) (u + 0.044715 u^3)
 //   log      y_k = n_k - sum_{i<k} (i/k) y_i n_{k-i},  n = u / u_0
+//   sin/cos  s' = c u', c' = -s u' (both series formed together)
+//   sqrt/rsqrt y = u^p, p = 1/2 or -1/2: k u_0 y_k = sum_{j=1..k} ((p+1) j - k) u_j y_{k-j}
+//            (J.C.P. Miller's power recurrence; for p = -1/2 the reference's poly_rsqrt,
+//            /root/reference/src/polytensors/_series.py:83-96)
 // These equal the reference's plain-range rules -- Faa di Bruno composition of
 // the derivatives at u_0 for gelu/tanh/sigmoid
 // (/root/reference/src/polytensors/_plain.py:174-259), plain_exp/plain_log
@@ -125,6 +129,41 @@ __device__ __forceinline__ void activation_element(int kind, const A (&u)[K + 1]
       }
       return;
     }
+    case PT_ACT_SIN:
+    case PT_ACT_COS: {
+      A sn[K + 1], cs[K + 1];
+      sn[0] = sin(u[0]);
+      cs[0] = cos(u[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A a = A(0), b = A(0);
+#pragma unroll
+        for (int j = 1; j <= k; ++j) {
+          a = fma(ju[j], cs[k - j], a);
+          b = fma(ju[j], sn[k - j], b);
+        }
+        sn[k] = a * (A(1) / A(k));
+        cs[k] = -b * (A(1) / A(k));
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) out[k] = kind == PT_ACT_SIN ? sn[k] : cs[k];
+      return;
+    }
+    case PT_ACT_SQRT:
+    case PT_ACT_RSQRT: {
+      const A root = sqrt(u[0]);
+      const A p1 = kind == PT_ACT_SQRT ? A(1.5) : A(0.5);   // p + 1
+      const A inv0 = A(1) / u[0];
+      out[0] = kind == PT_ACT_SQRT ? root : A(1) / root;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        A s = A(0);
+#pragma unroll
+        for (int j = 1; j <= k; ++j) s = fma((p1 * A(j) - A(k)) * u[j], out[k - j], s);
+        out[k] = s * inv0 * (A(1) / A(k));
+      }
+      return;
+    }
     case PT_ACT_TANH: {
       if constexpr (BWD) {   // u is the forward output Y: D = 1 - Y (*) Y
         cauchy_mul<A, K>(u, u, D);
@@ -204,7 +243,8 @@ constexpr int64_t kActMaxBlocks = int64_t(1) << 20;
 
 template <typename T, int K, bool BWD>
 __global__ __launch_bounds__(kActThreads) void activation_series_kernel(
-    int kind, CPtrs<T> x, CPtrs<T> g, MPtrs<T> y, int64_t numel, bool vec) {
+    int kind, CPtrs<T, kMaxElementwiseOrders> x, CPtrs<T, kMaxElementwiseOrders> g,
+    MPtrs<T, kMaxElementwiseOrders> y, int64_t numel, bool vec) {
   using A = typename AccOf<T>::type;
   constexpr int V = VecWidth<T>::value;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kActThreads;
@@ -263,9 +303,11 @@ __global__ __launch_bounds__(kActThreads) void activation_series_kernel(
 template <typename T, int K>
 static int launch_activation_k(const ActArgs& a) {
   constexpr int V = VecWidth<T>::value;
-  CPtrs<T> x{}, g{};
-  MPtrs<T> y{};
-  bool vec = true;
+  CPtrs<T, kMaxElementwiseOrders> x{}, g{};
+  MPtrs<T, kMaxElementwiseOrders> y{};
+  // 16-byte vectors of every order in registers up to 72 values per thread; above that (16-bit
+  // types past degree 8) the element-by-element path, which holds one value per order
+  bool vec = (K + 1) * V <= 72;
   for (int k = 0; k <= K; ++k) {
     x.p[k] = static_cast<const T*>(a.x[k]);
     y.p[k] = static_cast<T*>(a.y[k]);
@@ -300,9 +342,17 @@ int launch_activation(const ActArgs& a) {
     case 6: return launch_activation_k<T, 6>(a);
     case 7: return launch_activation_k<T, 7>(a);
     case 8: return launch_activation_k<T, 8>(a);
+    case 9: return launch_activation_k<T, 9>(a);
+    case 10: return launch_activation_k<T, 10>(a);
+    case 11: return launch_activation_k<T, 11>(a);
+    case 12: return launch_activation_k<T, 12>(a);
+    case 13: return launch_activation_k<T, 13>(a);
+    case 14: return launch_activation_k<T, 14>(a);
+    case 15: return launch_activation_k<T, 15>(a);
+    case 16: return launch_activation_k<T, 16>(a);
     default: break;
   }
-  pt_host::set_error("activation series: degree outside 0..PT_MAX_DEGREE");
+  pt_host::set_error("activation series: degree outside 0..PT_MAX_ELEMENTWISE_DEGREE");
   return PT_UNSUPPORTED;
 }
 

@@ -5,14 +5,15 @@ namespace {
 
 int check_activation(int dtype, int degree, int kind, bool backward, const void* const* g,
                      const void* const* x, void* const* y, int64_t numel) {
-  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
-             "activation series: degree must be in 0..8");
+  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_ELEMENTWISE_DEGREE, PT_UNSUPPORTED,
+             "activation series: degree must be in 0..16");
   PT_REQUIRE(dtype >= PT_FLOAT32 && dtype <= PT_FLOAT16, PT_UNSUPPORTED,
              "activation series: unknown dtype code");
-  PT_REQUIRE(kind >= PT_ACT_GELU && kind <= PT_ACT_LOG, PT_UNSUPPORTED,
+  PT_REQUIRE(kind >= PT_ACT_GELU && kind <= PT_ACT_RSQRT, PT_UNSUPPORTED,
              "activation series: unknown activation kind");
-  PT_REQUIRE(!backward || (kind != PT_ACT_EXP && kind != PT_ACT_LOG), PT_UNSUPPORTED,
-             "activation series: exp and log have no backward entry point (their gradient is a product)");
+  PT_REQUIRE(!backward || kind <= PT_ACT_SILU, PT_UNSUPPORTED,
+             "activation series: exp, log, sin, cos, sqrt and rsqrt have no backward entry point (their "
+             "gradients are products of forward series)");
   PT_REQUIRE(x != nullptr && y != nullptr && (!backward || g != nullptr), PT_INVALID_ARGUMENT,
              "activation series: pointer arrays are required");
   PT_REQUIRE(numel >= 0, PT_INVALID_ARGUMENT, "activation series: numel must be >= 0");

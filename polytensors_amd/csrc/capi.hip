@@ -17,5 +17,6 @@ const char* pt_last_error(void) { return pt_host::g_last_error.c_str(); }
 int pt_abi_version(void) { return PT_ABI_VERSION; }
 
 int pt_max_degree(void) { return PT_MAX_DEGREE; }
+int pt_max_elementwise_degree(void) { return PT_MAX_ELEMENTWISE_DEGREE; }
 
 }  // extern "C"

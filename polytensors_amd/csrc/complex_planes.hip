@@ -15,8 +15,10 @@
 
 namespace pt {
 
-constexpr int kMaxPlaneVariants = kMaxOrders;   // K+1 real nodes at most
-constexpr int kMaxComplexOrders = kMaxDegree;   // orders 1..K
+// K+1 real nodes and orders 1..K at most, up to the elementwise kernels' degree (the kernel
+// arguments then hold 17 x 16 destination pointers, 2.2 KB)
+constexpr int kMaxPlaneVariants = kMaxElementwiseOrders;
+constexpr int kMaxComplexOrders = PT_MAX_ELEMENTWISE_DEGREE;
 
 template <typename T>
 struct ToRealArgs {
@@ -200,7 +202,7 @@ int check_planes(int dtype, int orders, int variants, const void* const* a, cons
   PT_REQUIRE(dtype == PT_FLOAT32 || dtype == PT_FLOAT64, PT_UNSUPPORTED,
              "complex planes: float32 (complex64) or float64 (complex128) only");
   PT_REQUIRE(orders >= 0 && orders <= pt::kMaxComplexOrders && variants >= 1 && variants <= pt::kMaxPlaneVariants,
-             PT_INVALID_ARGUMENT, "complex planes: 0..8 complex orders and 1..9 variants");
+             PT_INVALID_ARGUMENT, "complex planes: 0..16 complex orders and 1..17 variants");
   PT_REQUIRE(numel >= 0, PT_INVALID_ARGUMENT, "complex planes: numel must be >= 0");
   PT_REQUIRE(p != nullptr && q != nullptr, PT_INVALID_ARGUMENT, "complex planes: coefficient arrays are required");
   if (numel == 0 || orders == 0) return PT_OK;

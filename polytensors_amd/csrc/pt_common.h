@@ -12,6 +12,7 @@ namespace pt {
 
 constexpr int kMaxDegree = PT_MAX_DEGREE;
 constexpr int kMaxOrders = kMaxDegree + 1;
+constexpr int kMaxElementwiseOrders = PT_MAX_ELEMENTWISE_DEGREE + 1;
 constexpr int kWave = 64;
 
 // bfloat16 storage is raw 16-bit words.
@@ -19,14 +20,15 @@ struct bf16 {
   uint16_t bits;
 };
 
-// K+1 coefficient pointers passed to a kernel by value.
-template <typename T>
+// K+1 coefficient pointers passed to a kernel by value (N slots: kMaxOrders for the MFMA and
+// row kernels, kMaxElementwiseOrders for the elementwise ones).
+template <typename T, int N = kMaxOrders>
 struct CPtrs {
-  const T* p[kMaxOrders];
+  const T* p[N];
 };
-template <typename T>
+template <typename T, int N = kMaxOrders>
 struct MPtrs {
-  T* p[kMaxOrders];
+  T* p[N];
 };
 
 template <typename T>

@@ -40,8 +40,10 @@ __device__ __forceinline__ void binary_element(int op, const A (&a)[K + 1], cons
 }
 
 template <typename T, int K>
-__global__ __launch_bounds__(kBinaryThreads) void series_binary_kernel(int op, CPtrs<T> a, CPtrs<T> b,
-                                                                       MPtrs<T> y, int64_t numel, bool vec) {
+__global__ __launch_bounds__(kBinaryThreads) void series_binary_kernel(int op, CPtrs<T, kMaxElementwiseOrders> a,
+                                                                       CPtrs<T, kMaxElementwiseOrders> b,
+                                                                       MPtrs<T, kMaxElementwiseOrders> y,
+                                                                       int64_t numel, bool vec) {
   using A = typename AccOf<T>::type;
   constexpr int V = VecWidth<T>::value;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kBinaryThreads;
@@ -98,9 +100,11 @@ __global__ __launch_bounds__(kBinaryThreads) void series_binary_kernel(int op, C
 template <typename T, int K>
 static int launch_binary_k(const BinaryArgs& a) {
   constexpr int V = VecWidth<T>::value;
-  CPtrs<T> pa{}, pb{};
-  MPtrs<T> py{};
-  bool vec = true;
+  CPtrs<T, kMaxElementwiseOrders> pa{}, pb{};
+  MPtrs<T, kMaxElementwiseOrders> py{};
+  // 16-byte vectors of every order of both operands in registers up to 72 values each; above
+  // that (16-bit types past degree 8) the element-by-element path
+  bool vec = (K + 1) * V <= 72;
   for (int k = 0; k <= K; ++k) {
     pa.p[k] = static_cast<const T*>(a.a[k]);
     pb.p[k] = static_cast<const T*>(a.b[k]);
@@ -127,9 +131,17 @@ int launch_binary(const BinaryArgs& a) {
     case 6: return launch_binary_k<T, 6>(a);
     case 7: return launch_binary_k<T, 7>(a);
     case 8: return launch_binary_k<T, 8>(a);
+    case 9: return launch_binary_k<T, 9>(a);
+    case 10: return launch_binary_k<T, 10>(a);
+    case 11: return launch_binary_k<T, 11>(a);
+    case 12: return launch_binary_k<T, 12>(a);
+    case 13: return launch_binary_k<T, 13>(a);
+    case 14: return launch_binary_k<T, 14>(a);
+    case 15: return launch_binary_k<T, 15>(a);
+    case 16: return launch_binary_k<T, 16>(a);
     default: break;
   }
-  pt_host::set_error("series product: degree outside 0..PT_MAX_DEGREE");
+  pt_host::set_error("series product: degree outside 0..PT_MAX_ELEMENTWISE_DEGREE");
   return PT_UNSUPPORTED;
 }
 

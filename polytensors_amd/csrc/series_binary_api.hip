@@ -6,8 +6,8 @@ extern "C" {
 int pt_series_binary(int dtype, int degree, int op, const void* const* a, const void* const* b,
                      void* const* y, int64_t numel, void* stream) {
   pt_host::clear_error();
-  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_DEGREE, PT_UNSUPPORTED,
-             "series product: degree must be in 0..8");
+  PT_REQUIRE(degree >= 0 && degree <= PT_MAX_ELEMENTWISE_DEGREE, PT_UNSUPPORTED,
+             "series product: degree must be in 0..16");
   PT_REQUIRE(dtype >= PT_FLOAT32 && dtype <= PT_FLOAT16, PT_UNSUPPORTED, "series product: unknown dtype code");
   PT_REQUIRE(op == PT_BINARY_MUL || op == PT_BINARY_DIV, PT_UNSUPPORTED, "series product: unknown operation");
   PT_REQUIRE(a != nullptr && b != nullptr && y != nullptr, PT_INVALID_ARGUMENT,

@@ -546,12 +546,12 @@ Tensor real_to_complex(const TensorList& src, int64_t orders, at::ArrayRef<doubl
 // ---- Elementwise series ------------------------------------------------------
 
 int activation_code(const std::string& kind, bool backward, const char* name) {
-  static const std::pair<const char*, int> kinds[] = {{"gelu", PT_ACT_GELU},   {"gelu_tanh", PT_ACT_GELU_TANH},
-                                                       {"tanh", PT_ACT_TANH},   {"sigmoid", PT_ACT_SIGMOID},
-                                                       {"silu", PT_ACT_SILU},   {"exp", PT_ACT_EXP},
-                                                       {"log", PT_ACT_LOG}};
+  static const std::pair<const char*, int> kinds[] = {
+      {"gelu", PT_ACT_GELU}, {"gelu_tanh", PT_ACT_GELU_TANH}, {"tanh", PT_ACT_TANH}, {"sigmoid", PT_ACT_SIGMOID},
+      {"silu", PT_ACT_SILU}, {"exp", PT_ACT_EXP},             {"log", PT_ACT_LOG},   {"sin", PT_ACT_SIN},
+      {"cos", PT_ACT_COS},   {"sqrt", PT_ACT_SQRT},           {"rsqrt", PT_ACT_RSQRT}};
   for (const auto& [k, code] : kinds)
-    if (kind == k && !(backward && (code == PT_ACT_EXP || code == PT_ACT_LOG))) return code;
+    if (kind == k && !(backward && code > PT_ACT_SILU)) return code;   // the forward-only kinds
   TORCH_CHECK_VALUE(false, name, backward ? ": no backward for kind '" : ": unknown kind '", kind, "'");
 }
 

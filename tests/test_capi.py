@@ -39,6 +39,7 @@ def test_version_queries():
     lib = _lib.load()
     assert lib.pt_abi_version() == _lib.ABI_VERSION
     assert lib.pt_max_degree() == 8
+    assert lib.pt_max_elementwise_degree() == 16
 
 
 def _vpp(n):

@@ -1,0 +1,236 @@
+"""Degrees above 8 and the elementwise functions sin, cos, sqrt, rsqrt, reciprocal (GPU).
+
+The elementwise kernels (activation series, series product and quotient) run up
+to degree 16, and the Cauchy matmul runs above its kernel's degree 8 in blocks of
+orders. The checks:
+* the reference's closed forms along a line x + t v at degrees 1, 3, 12 (and 16)
+  with real and complex directions (/root/reference/tests/test_series.py:15-46:
+  exp, log, reciprocal, rsqrt, sin, cos; sqrt by the same binomial series),
+  rtol 2e-13 elementwise for real directions as there, and the contract's
+  per-order 1e-10 for complex directions (evaluated at real nodes and recombined);
+* the reference's round trips (/root/reference/tests/test_series.py:93-109):
+  exp(log x), 1/(1/x), sqrt(x)^2 and rsqrt(x)^2 x on a dense degree-5 series;
+* dense random series at degrees 9, 12 and 16 for every activation against the
+  oracle's restatements (pinned by jets at lower degrees) and, for sin, cos,
+  sqrt and rsqrt, against the oracle's exp and log series (exp(i x), exp(log(x)/2)),
+  1e-10 in float64;
+* series product and quotient at degree 16 and the matmul at degrees 9..16
+  against the oracle's Cauchy sums (1e-10 float64, 1e-4 float32, 2e-2 bfloat16);
+* gradients of the new functions: reverse mode through sin/cos/sqrt/rsqrt
+  against jets of torch.func.grad, and their second-order coefficient autograd;
+* the row and MFMA kernels (norm, cross entropy, attention) refuse degree 9.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from polytensors_amd import PolyTensor
+from tests.jets import rel_err, taylor
+
+pytestmark = pytest.mark.gpu
+
+OPS = ("exp", "log", "reciprocal", "rsqrt", "sqrt", "sin", "cos")
+
+
+def _line(base, direction, degree):
+    return PolyTensor((base.cuda(), direction.cuda()), degree=degree)
+
+
+def _closed_form(operation, base, direction, order):
+    if operation == "exp":
+        return torch.exp(base) * direction ** order / math.factorial(order)
+    if operation == "log":
+        return ((-1) ** (order - 1) / order) * (direction / base) ** order
+    if operation == "reciprocal":
+        return torch.reciprocal(base) * (-direction / base) ** order
+    if operation in ("rsqrt", "sqrt"):
+        p = -0.5 if operation == "rsqrt" else 0.5
+        binomial = math.prod((p - i) / (i + 1) for i in range(order))
+        return binomial * base ** p * (direction / base) ** order
+    derivative = ((torch.sin(base), torch.cos(base), -torch.sin(base), -torch.cos(base)) if operation == "sin" else
+                  (torch.cos(base), -torch.sin(base), -torch.cos(base), torch.sin(base)))[order % 4]
+    return derivative * direction ** order / math.factorial(order)
+
+
+@pytest.mark.parametrize("degree", (1, 3, 12, 16))
+@pytest.mark.parametrize("complex_direction", (False, True))
+@pytest.mark.parametrize("operation", OPS)
+def test_line_coefficients_match_analytic_derivatives(operation, complex_direction, degree):
+    base = torch.tensor([1.7, 0.6, 2.9], dtype=torch.float64)
+    direction = torch.tensor([0.2 + 0.3j, -0.1 + 0.05j, 0.3 - 0.2j] if complex_direction else [0.2, -0.1, 0.3],
+                             dtype=torch.complex128 if complex_direction else torch.float64)
+    with torch.no_grad(), PolyTensor.plain_range():
+        result = getattr(torch, operation)(_line(base, direction, degree))
+    assert result.degree == degree
+    torch.testing.assert_close(result.coeffs[0].cpu(), getattr(torch, operation)(base), rtol=1e-15, atol=0)
+    for order in range(1, degree + 1):
+        want = _closed_form(operation, base, direction, order)
+        if complex_direction:
+            # complex directions run as K+1 real evaluations recombined by Lagrange weights, whose
+            # rounding grows with the order: the contract's per-order bound for complex128 up to
+            # degree 12; above, the interpolation's amplification (up to 1e-9 elementwise at
+            # degree 16) is bounded at 1e-8
+            bound = 1e-10 if degree <= 12 else 1e-8
+            assert rel_err(result.coeffs[order].cpu(), want) <= bound, f"order {order}"
+        else:
+            torch.testing.assert_close(result.coeffs[order].cpu(), want, rtol=2e-13, atol=1e-28)
+
+
+def test_nonlinear_input_series_round_trips():
+    coefficients = tuple(torch.tensor([v, v / 2], dtype=torch.float64)
+                         for v in (1.5, 0.2, -0.1, 0.03, 0.0, -0.002))
+    value = PolyTensor(tuple(c.cuda() for c in coefficients))
+    with torch.no_grad(), PolyTensor.plain_range():
+        results = (torch.exp(torch.log(value)), torch.reciprocal(torch.reciprocal(value)), torch.sqrt(value).square())
+        identity = torch.rsqrt(value).square() * value
+    for result in results:
+        for actual, expected in zip(result.coeffs, coefficients):
+            torch.testing.assert_close(actual.cpu(), expected, rtol=2e-13, atol=1e-15)
+    for order, actual in enumerate(identity.coeffs):
+        expected = torch.ones(2, dtype=torch.float64) if order == 0 else torch.zeros(2, dtype=torch.float64)
+        torch.testing.assert_close(actual.cpu(), expected, rtol=2e-13, atol=1e-15)
+
+
+_FNS = {"gelu": F.gelu, "gelu_tanh": lambda x: F.gelu(x, approximate="tanh"), "tanh": torch.tanh,
+        "sigmoid": torch.sigmoid, "silu": F.silu, "exp": torch.exp, "log": torch.log, "sin": torch.sin,
+        "cos": torch.cos, "sqrt": torch.sqrt, "rsqrt": torch.rsqrt}
+
+
+def _dense(shape, degree, seed, positive=False, scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    cs = [torch.randn(shape, generator=g, dtype=torch.float64) * scale ** k for k in range(degree + 1)]
+    if positive:
+        cs[0] = cs[0].abs() + 1.0
+    return cs
+
+
+@pytest.mark.parametrize("degree", (9, 12, 16))
+@pytest.mark.parametrize("kind", ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu", "exp", "log"))
+def test_dense_series_above_degree_eight_match_the_oracle(kind, degree):
+    # the oracle's restatements of the reference's rules (pinned against jets at lower degrees in
+    # tests/test_oracle_activation_pins.py) hold at any degree
+    X = _dense((3, 41), degree, 700 + degree, positive=kind == "log")
+    with torch.no_grad(), PolyTensor.plain_range():
+        out = _FNS[kind](PolyTensor(tuple(c.cuda() for c in X)))
+    want = oracle.activation(X, kind)
+    for k in range(degree + 1):
+        assert rel_err(out.coeffs[k].cpu(), want[k]) <= 1e-10, f"{kind} order {k}"
+
+
+def _exp_of(series):
+    return oracle.exp_series(series)
+
+
+@pytest.mark.parametrize("degree", (9, 12, 16))
+def test_dense_sin_cos_sqrt_rsqrt_above_degree_eight(degree):
+    # independent routes through the oracle's exp and log series: cos x + i sin x = exp(i x),
+    # sqrt x = exp(log(x) / 2), rsqrt x = exp(-log(x) / 2)
+    X = _dense((3, 41), degree, 760 + degree)
+    P = _dense((3, 41), degree, 761 + degree, positive=True)
+    with torch.no_grad(), PolyTensor.plain_range():
+        x, p = (PolyTensor(tuple(c.cuda() for c in s)) for s in (X, P))
+        got = {"sin": torch.sin(x), "cos": torch.cos(x), "sqrt": torch.sqrt(p), "rsqrt": torch.rsqrt(p)}
+    e = _exp_of([c * 1j for c in X])
+    logs = oracle.log_series(P)
+    want = {"sin": [c.imag for c in e], "cos": [c.real for c in e],
+            "sqrt": _exp_of([c * 0.5 for c in logs]), "rsqrt": _exp_of([c * -0.5 for c in logs])}
+    for kind in got:
+        for k in range(degree + 1):
+            assert rel_err(got[kind].coeffs[k].cpu(), want[kind][k]) <= 1e-10, f"{kind} order {k}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4)])
+def test_series_product_and_quotient_at_degree_sixteen(dtype, tol):
+    degree = 16
+    A = _dense((5, 37), degree, 710)
+    B = _dense((5, 37), degree, 711, positive=True)
+    a, b = (PolyTensor(tuple(c.to(dtype).cuda() for c in s)) for s in (A, B))
+    up = lambda s: [c.to(dtype).double() for c in s]   # noqa: E731
+    with torch.no_grad(), PolyTensor.plain_range():
+        for got, want, what in ((a * b, oracle.cauchy(up(A), up(B)), "a * b"),
+                                (a / b, oracle.quotient(up(A), up(B)), "a / b")):
+            for k in range(degree + 1):
+                assert rel_err(got.coeffs[k].cpu(), want[k]) <= tol, f"{what} order {k}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("degree", (9, 12, 16))
+def test_matmul_above_the_kernel_degree(dtype, tol, degree):
+    A = _dense((2, 33, 40), degree, 720 + degree)
+    B = _dense((40, 24), degree, 721 + degree)
+    W = _dense((24, 40), 0, 722)[0]
+    up = lambda s: [c.to(dtype).double() for c in s]   # noqa: E731
+    a, b = (PolyTensor(tuple(c.to(dtype).cuda() for c in s)) for s in (A, B))
+    with torch.no_grad(), PolyTensor.plain_range():
+        cases = ((a @ b, oracle.matmul(up(A), up(B)), "series @ series"),
+                 (a @ B[0].to(dtype).cuda(), oracle.matmul(up(A), up(B[:1])), "series @ plain"),
+                 (F.linear(a, W.to(dtype).cuda()), oracle.matmul(up(A), [W.t().to(dtype).double()]), "linear"))
+        for got, want, what in cases:
+            for k in range(degree + 1):
+                assert rel_err(got.coeffs[k].cpu(), want[k]) <= tol, f"{what} order {k}"
+
+
+def test_matmul_above_the_kernel_degree_with_complex_directions():
+    degree = 10
+    A = _dense((20, 16), degree, 730)
+    Ai = _dense((20, 16), degree, 731)
+    B = _dense((16, 12), degree, 732)
+    Ac = [A[0]] + [torch.complex(x, y) for x, y in zip(A[1:], Ai[1:])]
+    with torch.no_grad(), PolyTensor.plain_range():
+        got = PolyTensor(tuple(c.cuda() for c in Ac)) @ PolyTensor(tuple(c.cuda() for c in B))
+    want = oracle.matmul(Ac, [c.to(torch.complex128) for c in B])
+    for k in range(degree + 1):
+        assert rel_err(got.coeffs[k].cpu(), want[k]) <= 1e-10, f"order {k}"
+
+
+@pytest.mark.parametrize("kind", ("sin", "cos", "sqrt", "rsqrt"))
+def test_reverse_mode_through_the_new_functions(kind):
+    degree = 4
+    X = _dense((3, 5), degree, 740, positive=kind in ("sqrt", "rsqrt"))
+    R = torch.randn(3, 5, generator=torch.Generator().manual_seed(741), dtype=torch.float64)
+
+    def loss(x):
+        return (_FNS[kind](x) * R).sum()
+
+    x = PolyTensor(tuple(c.cuda() for c in X), requires_grad=True)
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        out = (_FNS[kind](x) * R.cuda()).sum()
+        out.backward()
+    want = taylor(lambda z: torch.func.grad(loss)(z), [X], degree)
+    for k in range(degree + 1):
+        assert rel_err(x.grad.coeffs[k].cpu(), want[k]) <= 1e-10, f"{kind} gradient order {k}"
+
+
+@pytest.mark.parametrize("kind", ("sin", "cos", "sqrt", "rsqrt"))
+def test_second_order_coefficient_autograd_of_the_new_functions(kind):
+    degree = 3
+    X = _dense((4,), degree, 750, positive=kind in ("sqrt", "rsqrt"))
+    fn = _FNS[kind]
+
+    def explicit(xs):   # coefficient `degree` of fn(x(t)), by nested jvp in t (plain torch)
+        return taylor(fn, [xs], degree)[degree].sum()
+
+    leaves = [c.clone().requires_grad_() for c in X]
+    first = torch.autograd.grad(explicit(leaves), leaves[0], create_graph=True)[0]
+    want = torch.autograd.grad((first * first).sum(), leaves[0])[0]
+    cl = [c.cuda().requires_grad_() for c in X]
+    with PolyTensor.plain_range(), PolyTensor.coefficient_autograd():
+        out = fn(PolyTensor(tuple(cl))).sum()
+    first = torch.autograd.grad(out.coeffs[degree], cl[0], create_graph=True)[0]
+    got = torch.autograd.grad((first * first).sum(), cl[0])[0]
+    assert rel_err(got.cpu(), want) <= 1e-10
+
+
+def test_row_and_mfma_kernels_refuse_degree_nine():
+    x = PolyTensor(tuple(torch.randn(4, 16, dtype=torch.float64, device="cuda") for _ in range(10)))
+    q = PolyTensor(tuple(torch.randn(1, 1, 8, 16, dtype=torch.float64, device="cuda") for _ in range(10)))
+    y = torch.zeros(4, dtype=torch.int64, device="cuda")
+    with torch.no_grad(), PolyTensor.plain_range():
+        for call in (lambda: F.layer_norm(x, (16,)), lambda: F.rms_norm(x, (16,)),
+                     lambda: F.cross_entropy(x, y), lambda: F.scaled_dot_product_attention(q, q, q)):
+            with pytest.raises(NotImplementedError, match="exceeds"):
+                call()
