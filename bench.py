@@ -14,7 +14,8 @@ seeded generator before the timed region). The launch-bound ``config1``
 workload (benchmark config 1) times its whole pipeline through the PolyTensor
 API per step, and again as the replay of a HIP graph holding one step
 (``graph``: ms per replay and the graph's kernel count, the launches per step). The timed region is K back-to-back
-steps on the current stream, bracketed by torch.cuda.synchronize() and timed
+steps on the current stream, after at least W warm-up steps lasting at least
+0.3 s (the clock ramps up after idle), bracketed by torch.cuda.synchronize() and timed
 with HIP events on that stream (``ms_per_step``, the mean); ``ms_median`` is the
 median over 21 further steps of each step's own event interval. ``value`` is the
 workload's throughput (from the mean) and
@@ -859,11 +860,22 @@ def _progress(message):
     print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
-def time_steps(step, steps, warmup):
+SETTLE_SECONDS = 0.3   # warm-up lasts at least this long: the GPU clock ramps up over ~30 ms of work
+
+
+def time_steps(step, steps, warmup, settle=SETTLE_SECONDS):
+    """Mean ms per step over ``steps`` back-to-back steps, after ``warmup`` untimed steps (continued
+    until ``settle`` seconds of warm-up have passed: the first launches after an idle period run at
+    lower clocks, up to 35% slower for a 1.4 ms kernel)."""
     import torch
 
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t0 < settle:
         step()
+        done += 1
+        if done % 4 == 0 or done >= warmup:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -937,15 +949,15 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2, streams=None):
                 def fn(blocks=blocks, chunked=chunked):
                     _lib.check(lib.pt_stream_read(src.data_ptr(), each, blocks, chunked, out.data_ptr(), stream),
                                "stream read")
-            reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup), 1e-3)))   # >= 50 ms timed
-            rate = moved / (time_steps(fn, reps, 1) * 1e-3) / 1e9
+            reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup, settle=0.0), 1e-3)))   # >= 50 ms
+            rate = moved / (time_steps(fn, reps, 1, settle=0.0) * 1e-3) / 1e9
             if rate > best:
                 best, best_how = rate, f"{blocks} blocks of 256, {'chunked' if chunked else 'grid-stride'}"
     entry = {"pattern": pattern, "bytes": moved, "rate": round(best, 1), "unit": "GB/s",
              "how": f"pt_stream_{pattern} ({best_how}; best of a sweep of grids and layouts)"}
     if pattern == "copy":
-        reps = max(steps, math.ceil(50.0 / max(time_steps(lambda: dst.copy_(src), 2, warmup), 1e-3)))
-        entry["torch_copy"] = round(moved / (time_steps(lambda: dst.copy_(src), reps, 1) * 1e-3) / 1e9, 1)
+        reps = max(steps, math.ceil(50.0 / max(time_steps(lambda: dst.copy_(src), 2, warmup, settle=0.0), 1e-3)))
+        entry["torch_copy"] = round(moved / (time_steps(lambda: dst.copy_(src), reps, 1, settle=0.0) * 1e-3) / 1e9, 1)
     del src, dst, out
     torch.cuda.empty_cache()
     if streams is not None:
@@ -959,8 +971,8 @@ def stream_ceiling(device, pattern, nbytes, steps=10, warmup=2, streams=None):
         def fn():
             _lib.check(lib.pt_stream_series(sp, ns, dp, nd, each, blk.data_ptr(), stream), "stream series")
 
-        reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup), 1e-3)))
-        rates = sorted(each * (ns + nd) / (time_steps(fn, reps, 1) * 1e-3) / 1e9 for _ in range(5))
+        reps = max(steps, math.ceil(50.0 / max(time_steps(fn, 2, warmup, settle=0.0), 1e-3)))
+        rates = sorted(each * (ns + nd) / (time_steps(fn, reps, 1, settle=0.0) * 1e-3) / 1e9 for _ in range(5))
         entry["series_rate"] = round(rates[2], 1)
         entry["series_how"] = (f"pt_stream_series: {ns} source and {nd} destination buffers of {each} bytes, "
                                "one 16-byte vector of each per thread (median of 5)")
@@ -1019,7 +1031,7 @@ def measure(name, device, steps, warmup, min_seconds=0.0):
         estimate = time_steps(w["step"], 3, warmup)
         steps = max(steps, math.ceil(min_seconds * 1e3 / max(estimate, 1e-3)))
         warmup = 1
-    ms = time_steps(w["step"], steps, warmup)
+    ms = time_steps(w["step"], steps, warmup)   # warm-up of at least SETTLE_SECONDS
     w["steps"] = steps
     w["ms_median"] = time_median(w["step"])
     if w["unit"] == "ms":   # launch-bound workloads report time per step
