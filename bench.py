@@ -861,6 +861,7 @@ def _progress(message):
 
 
 SETTLE_SECONDS = 0.3   # warm-up lasts at least this long: the GPU clock ramps up over ~30 ms of work
+_warmup_done = [0]     # warm-up steps the last time_steps call ran (profile summaries index the trace by it)
 
 
 def time_steps(step, steps, warmup, settle=SETTLE_SECONDS):
@@ -874,9 +875,10 @@ def time_steps(step, steps, warmup, settle=SETTLE_SECONDS):
     while done < warmup or time.perf_counter() - t0 < settle:
         step()
         done += 1
-        if done % 4 == 0 or done >= warmup:
+        if done % 4 == 0:   # bounds how far the host runs ahead of the GPU
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    _warmup_done[0] = done
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -1021,7 +1023,7 @@ def graph_replay(step, steps, warmup):
     ms = time_steps(graph.replay, steps, warmup)
     torch.cuda.synchronize()
     same = all(torch.equal(a, b) for a, b in zip(eager.coeffs, captured.coeffs))
-    return {"nodes": nodes, "ms": ms, "matches_eager": same}
+    return {"nodes": nodes, "ms": ms, "matches_eager": same, "warmup_done": _warmup_done[0]}
 
 
 def measure(name, device, steps, warmup, min_seconds=0.0):
@@ -1032,7 +1034,7 @@ def measure(name, device, steps, warmup, min_seconds=0.0):
         steps = max(steps, math.ceil(min_seconds * 1e3 / max(estimate, 1e-3)))
         warmup = 1
     ms = time_steps(w["step"], steps, warmup)   # warm-up of at least SETTLE_SECONDS
-    w["steps"] = steps
+    w["steps"], w["warmup_done"] = steps, _warmup_done[0]
     w["ms_median"] = time_median(w["step"])
     if w["unit"] == "ms":   # launch-bound workloads report time per step
         achieved = ms
@@ -1076,7 +1078,9 @@ def main():
                           "GB/s": round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)}), flush=True)
         return
     w = measure(args.workload, device, args.steps, args.warmup)
-    _progress(f"{args.workload}: {w['ms']:.4f} ms per step")
+    _progress(f"{args.workload}: {w['ms']:.4f} ms per step; {w['warmup_done']} warm-up steps"
+              + (f", graph warm-up {w['graph_result'].get('warmup_done')} replays" if "graph_result" in w else "")
+              + f"; work per step {w.get('work') or 0:.6e}, algorithmic HBM bytes {w.get('bytes') or 0:.6e}")
     line = {
         "metric": METRIC,
         "value": round(w["achieved"], 3),
