@@ -454,7 +454,9 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
   lds_dma16(&buf[kv][o][seg * RPS][0], rsrc, ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
 
-template <typename T, int K, int D, bool ADD>
+// MASK: 0 none (mask_all and madd_all unused), 1 a boolean mask, 2 an additive mask madd (float32
+// values) with the boolean mask of its finite entries. Without a mask no mask memory is read.
+template <typename T, int K, int D, int MASK>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_pipe_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S,
     const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all,
@@ -481,6 +483,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   const int64_t mask_index = attn_mask_index(mmap, head);
   const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
   const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  constexpr bool ADD = MASK == 2;
   const float* madd = ADD ? madd_all + mask_index * L * S : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
@@ -521,26 +524,47 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 
   // the first block's DMA is issued after the query loads: LDS-DMA loads pending
   // beside ordinary loads make the compiler wait for every load in flight
+  // The mask bytes (and additive values) of a block are read one block ahead, before that
+  // block's DMA is issued: loads complete in order, so a read issued at the top of its own block
+  // would hold the block for a full memory round trip (the additive values come from L2 or HBM).
+  uint8_t mnext[MASK ? 2 : 1][4];
+  float anext[ADD ? 2 : 1][4];
+  auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
+    if constexpr (MASK != 0) {
 #pragma unroll
-  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, head, S, lo, lane, wave, i);
-
-  // key block j from buffer cur; the DMA of block j+1 into nxt
-  auto block = [&](Tiles& cur, Tiles& nxt, int j) __attribute__((always_inline)) {
-    const int kb0 = lo + j * KB;
-    uint8_t mbyte[2][4];
+      for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mbyte[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, kb0 + 16 * kh + 4 * g + r, L, S);
-    float add[ADD ? 2 : 1][4];   // additive mask values of the same keys
+        for (int r = 0; r < 4; ++r) mnext[kh][r] = mask[static_cast<int64_t>(min(my_q, L - 1)) * S + min(kb0 + 16 * kh + 4 * g + r, S - 1)];
+    }
     if constexpr (ADD) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) add[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+        for (int r = 0; r < 4; ++r) anext[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
     }
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and the mask bytes)
+  };
+
+#pragma unroll
+  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, head, S, lo, lane, wave, i);
+  fetch_mask(lo);
+
+  // key block j from buffer cur; the DMA of block j+1 into nxt
+  auto block = [&](Tiles& cur, Tiles& nxt, int j) __attribute__((always_inline)) {
+    const int kb0 = lo + j * KB;
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and its mask reads)
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
+    uint8_t mbyte[MASK ? 2 : 1][4];
+    float add[ADD ? 2 : 1][4];   // additive mask values of the same keys
+    if constexpr (MASK != 0) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          mbyte[kh][r] = mnext[kh][r];
+          if constexpr (ADD) add[kh][r] = anext[kh][r];
+        }
+    }
+    fetch_mask(min(kb0 + KB, last_kb0));   // the next block's, ahead of its DMA
 
     // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves ----
     // Items t = (step, b) in order: one K_b operand (a 16-byte read) feeds the K+1-b products
@@ -587,7 +611,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         const int key = kb0 + 16 * kh + 4 * g + r;
         bool ok = q_ok && key < hi;
         if (causal) ok = ok && key <= my_q;
-        if (mask != nullptr) ok = ok && mbyte[kh][r] != 0;
+        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
         valid[kh][r] = ok;
         float sv = sc[kh][0][r] * scale;
         if constexpr (ADD) sv += add[kh][r];
@@ -781,8 +805,9 @@ static int launch_attention_half_kd(const AttnArgs& a) {
   taylor_attention_fwd_half_pipe_kernel<T, K, D, ADDV><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(      \
       q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges, madd, \
       a.causal ? 1 : 0, static_cast<float>(a.scale))
-        if (madd != nullptr) PT_HALF_PIPE(true);
-        else PT_HALF_PIPE(false);
+        if (madd != nullptr) PT_HALF_PIPE(2);
+        else if (a.mask != nullptr) PT_HALF_PIPE(1);
+        else PT_HALF_PIPE(0);
 #undef PT_HALF_PIPE
         PT_LAUNCH_CHECK();
         return PT_OK;
