@@ -357,7 +357,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
 //   top of block j: this wave's DMAs have landed (s_waitcnt), barrier;
 //     DMA K_{j+1} into the other K buffer;
 //   S and dP per 16-key half, then P and dS;
-//   barrier (every wave is done with V_j); DMA V_{j+1};
+//   barrier (every wave is done with V_j); DMA V_{j+1}; (stored tiles) the P / dS stores;
 //   dQ += K_j^T dS^T.
 // The DMA is hidden from the compiler (lds_dma16), so a compiler-visible load
 // issued after one waits for it too (loads complete in order): inside the loop
@@ -492,13 +492,24 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   const int last_kb0 = lo + (nblocks - 1) * KB;
   const int tj = c / 4, ta = c % 4;
 
-  // block 0's tiles (after the row loads: the compiler's waits for those would wait for the DMA)
+  // block 0's tiles (after the row loads: the compiler's waits for those would wait for the DMA).
+  // The row loads are waited for here, once: otherwise the compiler, which sees them pending at
+  // the loop's entry, waits for them inside the loop, on every block, where the count it uses
+  // also covers that block's DMAs and the previous block's stores.
+  __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
     attn_half_dma_tile<T, K, D>(Kt[0], Kp, head, S, lo, lane, wave, i);
     attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, lo, lane, wave, i);
   }
 
+  // The P / dS stores of a block (without a mask: one 16-byte store per series and order) go out
+  // after the block's last DMA, so the next block waits for its DMAs only. A wave with rows
+  // issues all of them (their branch skips only a wave without rows).
+  constexpr bool ONE_STORE = MASK == 0;
+  constexpr int kStoresAfterDma = 2 * (K + 1);   // s_waitcnt vmcnt(2(K+1)) expcnt(0) lgkmcnt(0)
+  static_assert(!STORE || kStoresAfterDma < 16, "vmcnt field");
+  const bool wave_rows = q_block + wave * kAttnQPerWave < L;
   for (int j = 0; j < nblocks; ++j) {
     const int kb0 = lo + j * KB;
     const int next_kb0 = min(kb0 + KB, last_kb0);   // the last block re-loads itself: no branch
@@ -514,7 +525,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         mbyte[kh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], my_q, key, L, S) : uint8_t(1);
         add[kh][r] = MASK == 2 ? attn_mask_add(madd, my_q, key, L, S) : 0.f;
       }
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
+    if (STORE && ONE_STORE && j > 0 && wave_rows) {
+      // this wave's DMAs of block j have landed; the tile stores of block j-1, its last 2(K+1)
+      // vector memory operations (the counter drops in issue order), may still be in flight
+      __builtin_amdgcn_s_waitcnt(kStoresAfterDma);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
+    }
     __syncthreads();                 // ... and every wave's; block j-1 is done with nxt
 #pragma unroll
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
@@ -522,7 +539,6 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
     // (the P operands of both halves are held for one store where the registers allow: without a
     // mask; with one, each half's are stored as they are formed)
-    constexpr bool ONE_STORE = MASK == 0;
     u32x4 dsb[K + 1], dsl[NLO], ppk[STORE && ONE_STORE ? K + 1 : 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -590,10 +606,14 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         }
       }
     }
+    __syncthreads();   // every wave is done with V_j
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, next_kb0, lane, wave, i);
     if constexpr (STORE && ONE_STORE) {
       // the lane's eight keys (4 g + r and 16 + 4 g + r of the block) of its query, at positions
       // 8 g .. 8 g + 7 of the block's 32: one 16-byte store per series and order, a contiguous
       // kilobyte per wave (plain stores: non-temporal ones measured 8% slower)
+      __builtin_amdgcn_sched_barrier(0);
       if (q_ok) {
         const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g;
 #pragma unroll
@@ -602,10 +622,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
           *reinterpret_cast<u32x4*>(DST.p[o] + at) = dsb[o];
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();   // every wave is done with V_j
-#pragma unroll
-    for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, next_kb0, lane, wave, i);
 
     // ---- dQ^T_k += sum_{a+b=k} K_b^T dS^T_a ----
 #pragma unroll

@@ -484,6 +484,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
   const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
   constexpr bool ADD = MASK == 2;
+  // The next block's DMA is issued in shares over the score products, so that it has the
+  // exponential series and the value products to land before the next block's wait (over the
+  // value products it left 0.98 ms at the config-3 shape, against 0.92). With an additive mask
+  // the value products measured faster (1.91 against 2.10 ms on a padding mask).
+  constexpr bool dma_in_scores = MASK != 2;
   const float* madd = ADD ? madd_all + mask_index * L * S : nullptr;
   const int my_q = q_block + wave * kAttnQPerWave + c;
   const bool q_ok = my_q < L;
@@ -565,6 +570,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         }
     }
     fetch_mask(min(kb0 + KB, last_kb0));   // the next block's, ahead of its DMA
+    const int next_kb0 = min(kb0 + KB, last_kb0);
 
     // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves ----
     // Items t = (step, b) in order: one K_b operand (a 16-byte read) feeds the K+1-b products
@@ -592,6 +598,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       if (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
+      if constexpr (dma_in_scores) {
+        // evenly over the score products: issued over their first half only, the tile writes
+        // slowed the operand reads more (0.917 -> 0.943 ms at the config-3 shape)
+#pragma unroll
+        for (int i = t * OPS / KT; i < (t + 1) * OPS / KT; ++i)
+          attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
+      }
       __builtin_amdgcn_sched_barrier(0);
       const int st = t / (K + 1), bo = t % (K + 1);
       const int dc = st / 2, kh = st % 2;
@@ -681,10 +694,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 
     // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T ----
     // Items t = (db, b): one V_b^T operand (two transpose reads) feeds the K+1-b products
-    // O_{a+b} += V_b^T P_a^T (and those of the lo parts); the reads run R-1 items ahead; a share of
-    // the next block's DMA into the other buffer per item (the last block re-loads itself, so
-    // there is no branch).
-    const int next_kb0 = min(kb0 + KB, last_kb0);
+    // O_{a+b} += V_b^T P_a^T (and those of the lo parts); the reads run R-1 items ahead. Where the
+    // DMA is issued here, a share of the next block's per item (the last block re-loads itself,
+    // so there is no branch).
     const int tj = c / 4, ta = c % 4;   // this lane's piece: row 4g + tj (+16), head dims 16 db + 4 ta
     auto load_v = [&](int t) {
       const int db = t / (K + 1), o = t % (K + 1);
@@ -701,9 +713,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 #pragma unroll
     for (int t = 0; t < VT; ++t) {
       if (t + R - 1 < VT) vring[(t + R - 1) % R] = load_v(t + R - 1);
+      if constexpr (!dma_in_scores) {
 #pragma unroll
-      for (int i = t * OPS / VT; i < (t + 1) * OPS / VT; ++i)
-        attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
+        for (int i = t * OPS / VT; i < (t + 1) * OPS / VT; ++i)
+          attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
+      }
       __builtin_amdgcn_sched_barrier(0);
       const int db = t / (K + 1), bo = t % (K + 1);
 #pragma unroll
