@@ -12,8 +12,15 @@ operand read of every wave for both workgroup tiles (narrow 64 x 64, wide
 * the DMA covers each element of the tile exactly once;
 * every lane receives exactly the eight contraction elements its MFMA operand
   needs (row or column `16 f + lane % 16`, elements `8 (lane / 16) ... + 7`);
-* each read pass (16 lanes of a 16-byte read, 32 lanes of an 8-byte read) hits
-  64 distinct 4-byte banks.
+* each read pass hits 64 distinct 4-byte banks. gfx950 serves a 16-byte read
+  in four passes of 16 lanes, {0-3, 12-15, 20-27}, {4-11, 16-19, 28-31} and the
+  same sets plus 32, and an 8-byte read in two passes of 32 consecutive lanes.
+  That grouping was measured on gfx950 with an LDS probe in which only two lanes
+  read, on the same banks at different addresses, for every pair of lanes
+  (SQ_LDS_BANK_CONFLICT nonzero exactly for the pairs of one pass). The model
+  reproduces the counter on whole-wave patterns: zero for contiguous 16-byte
+  reads and for the attention kernel's K operand, four cycles per read for the
+  first A-tile swizzle (`test_bank_model_matches_the_measured_patterns`).
 
 The transpose read's lane mapping (within each 16-lane group, lane 4a + b
 receives element b of the 8-byte pieces addressed by lanes a, a+4, a+8, a+12)
@@ -27,7 +34,13 @@ BK = 32
 
 
 def swz_rows(r, ch):   # cauchy_swz_rows
-    return ch ^ ((r >> 2) & 3)
+    return ch ^ ((0x78 >> (2 * ((r >> 2) & 3))) & 3)
+
+
+# lanes of each pass of a 16-byte LDS read (measured on gfx950)
+B128_PASS = [0, 1, 2, 3, 12, 13, 14, 15, 20, 21, 22, 23, 24, 25, 26, 27]
+B128_PASSES = [B128_PASS, [l for l in range(32) if l not in B128_PASS]]
+B128_PASSES += [[l + 32 for l in p] for p in B128_PASSES]
 
 
 def swz_k(wide, k, ch):   # cauchy_swz_k<WIDE>
@@ -77,8 +90,8 @@ def test_row_tiles(wide, side):
                 addr = row * BK + swz_rows(row, g) * 8
                 addrs.append(addr)
                 assert [lds[addr + e] for e in range(8)] == [(row, 8 * g + e) for e in range(8)]
-            for p in range(4):
-                assert banks_distinct(addrs[16 * p:16 * p + 16], 16)
+            for p in B128_PASSES:
+                assert banks_distinct([addrs[l] for l in p], 16)
 
 
 @pytest.mark.parametrize("wide", [False, True])
@@ -112,3 +125,20 @@ def test_kn_tile_transpose_reads(wide):
                 assert got == [(8 * g + s, n0 + c) for s in range(8)]
             for addrs in (first, second):
                 assert banks_distinct(addrs[:32], 8) and banks_distinct(addrs[32:], 8)
+
+
+def _b128_conflict_free(byte_addrs):
+    return all(banks_distinct([byte_addrs[l] // 2 for l in p], 16) for p in B128_PASSES)
+
+
+def test_bank_model_matches_the_measured_patterns():
+    # whole-wave 16-byte read patterns whose conflict counts were measured with the LDS probe
+    assert sorted(sum(B128_PASSES, [])) == list(range(64))
+    contiguous = [16 * l for l in range(64)]
+    attention_k = [(l % 16) * 256 + ((l // 16) ^ (l % 16)) * 16 for l in range(64)]   # d = 128 K tile
+    first_a = [(l % 16) * 64 + ((l // 16) ^ ((l % 16) >> 2)) * 16 for l in range(64)]   # chunk ^= (row/4)%4
+    assert _b128_conflict_free(contiguous)       # measured 0
+    assert _b128_conflict_free(attention_k)      # measured 0
+    assert not _b128_conflict_free(first_a)      # measured 4 cycles per read
+    # a model of consecutive 16-lane passes would have called the first A swizzle conflict-free
+    assert all(banks_distinct([first_a[l] // 2 for l in range(16 * p, 16 * p + 16)], 16) for p in range(4))
