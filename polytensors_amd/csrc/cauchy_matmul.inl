@@ -16,12 +16,30 @@
 // latency hides behind the matrix work; the registers are committed to LDS
 // between two barriers.
 //
-// LDS layout: As[order][row][k], Bs[order][col][k], k contiguous with a
-// 16-byte pad per row. Within a chunk the contraction index is permuted: MFMA
-// step s uses k = (lane / M) * RUN + s, so each lane reads its RUN operand
-// values of a row with 16-byte LDS loads (the same permutation on A and B
-// leaves the product unchanged); the 16-byte row pad makes those reads
-// bank-conflict-free.
+// LDS layout: As[order][row][k], Bs[order][col][k], k contiguous. Within a
+// chunk the contraction index is permuted: MFMA step s uses k = (lane / M) *
+// RUN + s, so each lane reads its RUN operand values of a row with 16-byte LDS
+// loads (the same permutation on A and B leaves the product unchanged).
+//
+// Banks. gfx950 serves a 16-byte LDS access in four passes of 16 lanes,
+// {0-3, 12-15, 20-27}, {4-11, 16-19, 28-31} and the same sets plus 32, an
+// 8-byte access in two passes of 32 consecutive lanes (measured with a
+// two-lane LDS probe and SQ_LDS_BANK_CONFLICT).
+// * float64: rows unpadded, 16-byte chunks XOR-swizzled by a function of the
+//   row (CauchyLds::fa), chosen under that model so that the operand reads and
+//   the 16-byte tile writes of every pass hit 64 distinct banks (B stored
+//   [Kd][N], transposed by 8-byte writes, keeps a two-way conflict on those
+//   writes). The first layout, a 16-byte row pad, conflicted on all three:
+//   bank conflicts fell from 17.4% to 3.4% of the CU cycles, 33.8 -> 32.0 ms
+//   at config 2's shape.
+// * float32: rows keep a 16-byte pad, which makes the A-operand reads
+//   conflict-free under the model; B stored [Kd][N], transposed by 4-byte
+//   writes, also swizzles its chunks by (n / 16) % 4, which makes those writes
+//   conflict-free and leaves its operand reads two-way in each pass (no XOR
+//   swizzle of two row bits frees both). The float64-style unpadded, swizzled A
+//   tile also removed the A-tile write conflicts (5.5% -> 3.7% of the CU
+//   cycles) but measured 0.5% slower, so float32 keeps the pad.
+// tests/test_cauchy_tiles.py replays these layouts under the bank model.
 #pragma once
 
 #include <algorithm>
@@ -30,6 +48,25 @@
 #include "mfma.h"
 
 namespace pt {
+
+template <typename T, bool TRANS_B>
+struct CauchyLds {
+  static constexpr int BK = 16;
+  static constexpr int QV = 16 / static_cast<int>(sizeof(T));   // values per 16-byte chunk
+  static constexpr bool kF64 = sizeof(T) == 8;
+  static constexpr int LDA = kF64 ? BK : BK + QV;
+  static constexpr int LDB = LDA;
+  // double: 8 chunks per row, chunk bits (r0^r2, r0^r1, r0^r3); float: padded rows, no swizzle
+  __host__ __device__ __forceinline__ static int fa(int r) {
+    if constexpr (kF64) return ((r ^ (r >> 2)) & 1) | (((r ^ (r >> 1)) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
+    else return 0;
+  }
+  __host__ __device__ __forceinline__ static int fb(int n) {
+    if constexpr (kF64) return fa(n);
+    else if constexpr (!TRANS_B) return (n >> 4) & 3;
+    else return 0;
+  }
+};
 
 template <typename T, int K, int AO, int BO, int BM, int BN, int BK, int WAVES_M, int WAVES_N,
           int MIN_WAVES, bool TRANS_B, bool VEC>
@@ -44,7 +81,8 @@ void cauchy_matmul_kernel(
   constexpr int RUN = BK / MF::KK;            // contiguous k per lane per chunk
   constexpr int QV = 16 / sizeof(T);          // values per 16-byte LDS read
   constexpr int V = 16 / sizeof(T);           // values per 16-byte global load
-  constexpr int LDK = BK + 16 / sizeof(T);    // padded row length
+  using Lds = CauchyLds<T, TRANS_B>;
+  static_assert(BK == Lds::BK, "LDS layout is for 16-deep chunks");
   constexpr int NA = BM * BK / V / THREADS;   // A vectors per thread and order
   constexpr int NB = BN * BK / V / THREADS;   // B vectors per thread and order
   static_assert(FM * MF::M == WM && FN * MF::N == WN, "wave tile must be whole MFMA blocks");
@@ -52,14 +90,10 @@ void cauchy_matmul_kernel(
   static_assert(NA * V * THREADS == BM * BK && NB * V * THREADS == BN * BK, "whole vectors per thread");
   static_assert((AO == 1 || AO == K + 1) && (BO == 1 || BO == K + 1), "operand orders are 1 or K+1");
 
-  __shared__ T As[AO][BM][LDK];
-  __shared__ T Bs[BO][BN][LDK];
-  // B stored [Kd][N] (float): its tile is transposed into Bs by scalar writes, which
-  // with rows of LDK = BK + 4 values would fall 4 ways onto the same banks. The
-  // 16-byte chunks of row n are XOR-swizzled by (n / 16) % 4, which makes those
-  // writes and the 16-byte operand reads of 16 consecutive rows conflict-free.
-  constexpr bool kSwizzleB = !TRANS_B && sizeof(T) == 4 && BK / QV == 4;
-  auto bchunk = [](int n, int c) { return kSwizzleB ? (c ^ ((n >> 4) & 3)) : c; };
+  __shared__ T As[AO][BM][Lds::LDA];
+  __shared__ T Bs[BO][BN][Lds::LDB];
+  auto achunk = [](int r, int c) { return c ^ Lds::fa(r); };
+  auto bchunk = [](int n, int c) { return c ^ Lds::fb(n); };
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -139,7 +173,8 @@ void cauchy_matmul_kernel(
 #pragma unroll
       for (int it = 0; it < NA; ++it) {
         const int v = it * THREADS + threadIdx.x;
-        store_vec<T, V>(&As[o][v / (BK / V)][(v % (BK / V)) * V], ra[o][it]);
+        const int r = v / (BK / V);
+        store_vec<T, V>(&As[o][r][achunk(r, v % (BK / V)) * V], ra[o][it]);
       }
 #pragma unroll
     for (int o = 0; o < BO; ++o)
@@ -147,7 +182,8 @@ void cauchy_matmul_kernel(
       for (int it = 0; it < NB; ++it) {
         const int v = it * THREADS + threadIdx.x;
         if constexpr (TRANS_B) {
-          store_vec<T, V>(&Bs[o][v / (BK / V)][(v % (BK / V)) * V], rb[o][it]);
+          const int n = v / (BK / V);
+          store_vec<T, V>(&Bs[o][n][bchunk(n, v % (BK / V)) * V], rb[o][it]);
         } else {
           const int kk = v / (BN / V), nv = (v % (BN / V)) * V;
 #pragma unroll
@@ -182,7 +218,8 @@ void cauchy_matmul_kernel(
       for (int o = 0; o < AO; ++o)
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
-          av[o][fm] = *reinterpret_cast<const Vec<T, QV>*>(&As[o][row_a + fm * MF::M][kbase + q * QV]);
+          av[o][fm] = *reinterpret_cast<const Vec<T, QV>*>(
+              &As[o][row_a + fm * MF::M][achunk(row_a + fm * MF::M, kbase / QV + q) * QV]);
 #pragma unroll
       for (int o = 0; o < BO; ++o)
 #pragma unroll

@@ -30,6 +30,8 @@ other tile's swizzle, fails the second or third check.
 
 import pytest
 
+from tests.lds_banks import PASSES
+
 BK = 32
 
 
@@ -38,9 +40,7 @@ def swz_rows(r, ch):   # cauchy_swz_rows
 
 
 # lanes of each pass of a 16-byte LDS read (measured on gfx950)
-B128_PASS = [0, 1, 2, 3, 12, 13, 14, 15, 20, 21, 22, 23, 24, 25, 26, 27]
-B128_PASSES = [B128_PASS, [l for l in range(32) if l not in B128_PASS]]
-B128_PASSES += [[l + 32 for l in p] for p in B128_PASSES]
+B128_PASSES = PASSES[16]
 
 
 def swz_k(wide, k, ch):   # cauchy_swz_k<WIDE>
