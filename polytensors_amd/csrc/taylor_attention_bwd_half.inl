@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
 // Pipelined dQ kernel: the K and V tiles of key block j+1 move by LDS DMA while
 // block j's products run (the layout and DMA geometry of the forward's
 // pipelined kernel: rows unpadded, 16-byte chunks XOR-swizzled by the row with
-// AttnHalfPipe::fk). K is read to the end of a block (the dQ product) and takes
+// AttnHalfPipe::fs). K is read to the end of a block (the dQ product) and takes
 // two buffers; V is read by the dP product only and takes one, refilled once
 // every wave is past it:
 //   top of block j: this wave's DMAs have landed (s_waitcnt), barrier;
@@ -376,7 +376,7 @@ struct AttnHalfBwdPipe {
 };
 
 // DMA operation i (0 <= i < (K+1) IT) of this wave's share of rows first .. first + 31 of a
-// head's [rows, D] series into a tile [K+1][32][D] (chunks swizzled with fk; rows past `rows`
+// head's [rows, D] series into a tile [K+1][32][D] (chunks swizzled with fs; rows past `rows`
 // load zeros).
 template <typename T, int K, int D>
 __device__ __forceinline__ void attn_half_dma_tile(T (&tile)[K + 1][32][D], const CPtrs<T>& src, int64_t head,
@@ -387,7 +387,7 @@ __device__ __forceinline__ void attn_half_dma_tile(T (&tile)[K + 1][32][D], cons
   const int seg = it * kAttnWaves + wave;
   if (SEGS % kAttnWaves != 0 && seg >= SEGS) return;
   const int row = seg * RPS + lane / CH;
-  const int lch = (lane % CH) ^ P::fk(row);
+  const int lch = (lane % CH) ^ P::fs(row);
   const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * rows * D, rows * D * static_cast<int>(sizeof(T)));
   lds_dma16(&tile[o][seg * RPS][0], rsrc, ((first + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
@@ -396,7 +396,7 @@ __device__ __forceinline__ void attn_half_dma_tile(T (&tile)[K + 1][32][D], cons
 template <typename T, int K, int D>
 __device__ __forceinline__ u32x4 attn_half_tile_row(const T (&tile)[K + 1][32][D], int o, int row, int ch, bool din) {
   using P = AttnHalfPipe<K, D>;
-  const int pch = (ch & (P::CH - 1)) ^ P::fk(row);
+  const int pch = (ch & (P::CH - 1)) ^ P::fs(row);
   const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[o][row][pch * 8]);
   const u32x4 z = {0u, 0u, 0u, 0u};
   return din ? v : z;
@@ -410,17 +410,19 @@ __device__ __forceinline__ u32x4 attn_half_tile_tr(const T (&tile)[K + 1][32][D]
   using P = AttnHalfPipe<K, D>;
   const int row0 = 4 * g + tj, row1 = 16 + 4 * g + tj;
   const int lch = 2 * db + ta / 2;
-  const int off0 = ((lch ^ P::fk(row0)) * 8) + 4 * (ta % 2);
-  const int off1 = ((lch ^ P::fk(row1)) * 8) + 4 * (ta % 2);
+  const int off0 = ((lch ^ P::fs(row0)) * 8) + 4 * (ta % 2);
+  const int off1 = ((lch ^ P::fs(row1)) * 8) + 4 * (ta % 2);
   return lds_read_tr16x2(&tile[o][row0][off0], &tile[o][row1][off1]);
 }
 
 // STORE: also write the P and dS series of every visited (query, key) pair to PT / DST (the dS
 // values as rounded for the dQ product) for taylor_attention_bwd_kv_half_mat_kernel, in 32-key
 // blocks: [head][srow / 32 key blocks][L queries][32 positions] 16-bit values, key 16 h + 4 g + r
-// of a block at position 8 g + 4 h + r (the eight keys a lane holds are adjacent), so that a
-// wave's store of a block fills one contiguous kilobyte. Degrees 1..4 (one 16-bit operand per
-// value).
+// of a block at position 8 g + 4 (h ^ q2) + r, q2 = bit 2 of the query (the eight keys a lane
+// holds are adjacent), so that a wave's store of a block fills one contiguous kilobyte. The
+// consumer's transpose reads of rows 4 g' + j and 4 (g' + 1) + j, the two row groups of one
+// 32-lane pass, then fall on the two halves of their chunks instead of the same half (a two-way
+// bank conflict on every read). Degrees 1..4 (one 16-bit operand per value).
 template <typename T, int K, int D, int MASK, bool STORE>
 __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_half_pipe_kernel(
     CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, CPtrs<T> G, CPtrs<float> LSE, CPtrs<float> DELTA, MPtrs<T> DQ,
@@ -595,8 +597,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
             ppk[o][2 * kh] = MM::pack2(wp[o][0], wp[o][1]);
             ppk[o][2 * kh + 1] = MM::pack2(wp[o][2], wp[o][3]);
           }
-        } else if (q_ok) {   // this half's four keys, positions 8 g + 4 kh .. + 3: an 8-byte store
-          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g + 4 * kh;
+        } else if (q_ok) {   // this half's four keys, positions 8 g + 4 (kh ^ q2) .. + 3: an 8-byte store
+          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g + 4 * (kh ^ ((my_q >> 2) & 1));
 #pragma unroll
           for (int o = 0; o <= K; ++o) {
             *reinterpret_cast<uint2*>(PT.p[o] + at) =
@@ -616,10 +618,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
       __builtin_amdgcn_sched_barrier(0);
       if (q_ok) {
         const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g;
+        const bool q2 = ((my_q >> 2) & 1) != 0;   // the halves swapped
 #pragma unroll
         for (int o = 0; o <= K; ++o) {
-          *reinterpret_cast<u32x4*>(PT.p[o] + at) = ppk[o];
-          *reinterpret_cast<u32x4*>(DST.p[o] + at) = dsb[o];
+          const u32x4 pp = ppk[o], dd = dsb[o];
+          *reinterpret_cast<u32x4*>(PT.p[o] + at) = q2 ? u32x4{pp[2], pp[3], pp[0], pp[1]} : pp;
+          *reinterpret_cast<u32x4*>(DST.p[o] + at) = q2 ? u32x4{dd[2], dd[3], dd[0], dd[1]} : dd;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1153,7 +1157,7 @@ __device__ __forceinline__ void attn_half_dma_tile_w(T (&tile)[K + 1][32][D], co
   const int seg = it * WAVES + wave;
   if (SEGS % WAVES != 0 && seg >= SEGS) return;
   const int row = seg * RPS + lane / CH;
-  const int lch = (lane % CH) ^ P::fk(row);
+  const int lch = (lane % CH) ^ P::fs(row);
   const BufferRsrc rsrc = buffer_rsrc(src.p[o] + head * rows * D, rows * D * static_cast<int>(sizeof(T)));
   lds_dma16(&tile[o][seg * RPS][0], rsrc, ((first + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
@@ -1303,9 +1307,10 @@ __global__ __launch_bounds__(KEYS * 4) void taylor_attention_bwd_kv_half_mat_ker
     auto products = [&](floatx4 (&acc)[DB][K + 1], const XTile& xt, const STile& st) {
       u32x4 b[K + 1], none[1];
       // the wave's keys kv_block + 16 wave + c: block wave / 2, key 16 (wave % 2) + c at position
-      // 8 (c / 4) + 4 (wave % 2) + c % 4; this lane addresses the four positions of lanes 4 ta ..
-      const int lch = 4 * (wave / 2) + ta, off = 4 * (wave % 2);   // logical chunk, offset in it
+      // 8 (c / 4) + 4 ((wave % 2) ^ q2) + c % 4, q2 = bit 2 of the query row (rows r and r + 16 share
+      // it); this lane addresses the four positions of lanes 4 ta ..
       const int r0 = 4 * g + tj, r1 = 16 + 4 * g + tj;
+      const int lch = 4 * (wave / 2) + ta, off = 4 * ((wave % 2) ^ ((r0 >> 2) & 1));   // logical chunk, offset
       const int c0 = 8 * (lch ^ attn_stored_swz<KEYS>(r0)) + off, c1 = 8 * (lch ^ attn_stored_swz<KEYS>(r1)) + off;
 #pragma unroll
       for (int o = 0; o <= K; ++o) b[o] = lds_read_tr16x2(&st[o][r0][c0], &st[o][r1][c1]) & keep;
