@@ -24,6 +24,12 @@ struct HalfMfma<bf16> {
   // the two values of a packed word
   __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // acc + lo(w) + hi(w) in one instruction (v_dot2c_f32_bf16 against (1, 1)): the products are
+  // exact, the sum is in float32
+  __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, w), __builtin_bit_cast(bf2, 0x3F803F80u), acc, false);
+  }
   // lazy-rescale slack (natural-log units): p <= e^8 (bf16 has the fp32 exponent range)
   static constexpr float kSlack = 8.0f;
 };
@@ -45,6 +51,11 @@ struct HalfMfma<_Float16> {
   }
   __device__ __forceinline__ static float hi(uint32_t w) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  }
+  // acc + lo(w) + hi(w) in one instruction (v_dot2c_f32_f16 against (1, 1))
+  __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), __builtin_bit_cast(h2, 0x3C003C00u), acc, false);
   }
   // float16 overflows at 65504: the running maximum is exact (p <= 1)
   static constexpr float kSlack = 0.0f;

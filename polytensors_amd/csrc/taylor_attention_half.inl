@@ -310,13 +310,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         pb[o][2 * kh] = w01;
         pb[o][2 * kh + 1] = w23;
         // the row sums add the weights as rounded for the value products
-        lsum[o] += (MM::lo(w01) + MM::hi(w01)) + (MM::lo(w23) + MM::hi(w23));
+        lsum[o] = MM::sum2(w23, MM::sum2(w01, lsum[o]));
         if constexpr (Sh::split) {
           if (o >= 1) {   // the rounding residuals as the lo operand
             pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
             pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
-            lsum[o] += (MM::lo(pl[o][2 * kh]) + MM::hi(pl[o][2 * kh])) +
-                       (MM::lo(pl[o][2 * kh + 1]) + MM::hi(pl[o][2 * kh + 1]));
+            lsum[o] = MM::sum2(pl[o][2 * kh + 1], MM::sum2(pl[o][2 * kh], lsum[o]));
           }
         }
       }
@@ -528,6 +527,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc_o[o][db] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_used = kNegInf;
+  float iscale[K + 1];   // i scale: the score series' factors in the exponential recurrence
+#pragma unroll
+  for (int i = 0; i <= K; ++i) iscale[i] = static_cast<float>(i) * scale;
   float lsum[K + 1];
 #pragma unroll
   for (int o = 0; o <= K; ++o) lsum[o] = 0.f;
@@ -664,20 +666,18 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       float w[K + 1][4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = valid[kh][r] ? exp_fast(s0[kh][r] - m_used) : 0.f;
-        float sk[K + 1], e[K + 1];
+        // the weights w_k = p e_k directly: w_0 = p, w_k = (1/k) sum_i b_i w_{k-i}, b_i = i scale S_i
+        float b[K + 1];
 #pragma unroll
-        for (int o = 1; o <= K; ++o) sk[o] = sc[kh][o][r] * scale;
-        e[0] = 1.f;
+        for (int o = 1; o <= K; ++o) b[o] = sc[kh][o][r] * iscale[o];
+        w[0][r] = valid[kh][r] ? exp_fast(s0[kh][r] - m_used) : 0.f;
 #pragma unroll
         for (int k = 1; k <= K; ++k) {
-          float t = 0.f;
+          float t = b[1] * w[k - 1][r];
 #pragma unroll
-          for (int i = 1; i <= k; ++i) t += (static_cast<float>(i) * sk[i]) * e[k - i];
-          e[k] = t * (1.f / static_cast<float>(k));
+          for (int i = 2; i <= k; ++i) t = fmaf(b[i], w[k - i][r], t);
+          w[k][r] = t * (1.f / static_cast<float>(k));
         }
-#pragma unroll
-        for (int o = 0; o <= K; ++o) w[o][r] = p * e[o];
       }
 #pragma unroll
       for (int o = 0; o <= K; ++o) {
@@ -685,13 +685,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         pb[o][2 * kh] = w01;
         pb[o][2 * kh + 1] = w23;
         // the row sums add the weights as rounded for the value products
-        lsum[o] += (MM::lo(w01) + MM::hi(w01)) + (MM::lo(w23) + MM::hi(w23));
+        lsum[o] = MM::sum2(w23, MM::sum2(w01, lsum[o]));
         if constexpr (P::split) {
           if (o >= 1) {
             pl[o][2 * kh] = MM::pack2(w[o][0] - MM::lo(w01), w[o][1] - MM::hi(w01));
             pl[o][2 * kh + 1] = MM::pack2(w[o][2] - MM::lo(w23), w[o][3] - MM::hi(w23));
-            lsum[o] += (MM::lo(pl[o][2 * kh]) + MM::hi(pl[o][2 * kh])) +
-                       (MM::lo(pl[o][2 * kh + 1]) + MM::hi(pl[o][2 * kh + 1]));
+            lsum[o] = MM::sum2(pl[o][2 * kh + 1], MM::sum2(pl[o][2 * kh], lsum[o]));
           }
         }
       }
