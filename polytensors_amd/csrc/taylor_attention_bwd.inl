@@ -129,14 +129,16 @@ template <typename A, int K, typename AccT>
 __device__ __forceinline__ void attn_prob_series(const AccT (&sc)[K + 1], int r, const A (&lse)[K + 1],
                                                  bool valid, A scale, A add, A (&p)[K + 1]) {
   p[0] = valid ? exp_fast(static_cast<A>(sc[0][r]) * scale + add - lse[0]) : A(0);
-  A x[K + 1];
+  // b_i = i x_i with x_i = scale S_i - lse_i: one fma per order (i scale and i lse_i do not depend
+  // on the key, so they leave the key loop)
+  A b[K + 1];
 #pragma unroll
-  for (int i = 1; i <= K; ++i) x[i] = static_cast<A>(sc[i][r]) * scale - lse[i];
+  for (int i = 1; i <= K; ++i) b[i] = static_cast<A>(sc[i][r]) * (A(i) * scale) - A(i) * lse[i];
 #pragma unroll
   for (int k = 1; k <= K; ++k) {
-    A t = A(0);
+    A t = b[1] * p[k - 1];
 #pragma unroll
-    for (int i = 1; i <= k; ++i) t += (A(i) * x[i]) * p[k - i];
+    for (int i = 2; i <= k; ++i) t += b[i] * p[k - i];
     p[k] = t * (A(1) / A(k));
   }
 }
