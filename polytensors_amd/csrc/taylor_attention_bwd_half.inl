@@ -572,6 +572,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
 #pragma unroll
           for (int a = 0; a <= k; ++a) dp[k] = MM::mma(vop[k - a], ga[a], dp[k]);
       }
+      if (kh == 1) {
+        // the last read of V_j is behind: V_{j+1} moves during the second half's series, the
+        // stores and the dQ products (after them only, it left its latency to the next block's wait)
+        __syncthreads();   // every wave is done with V_j
+#pragma unroll
+        for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, next_kb0, lane, wave, i);
+      }
       float w[K + 1][4], wp[STORE ? K + 1 : 1][4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -608,9 +615,6 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         }
       }
     }
-    __syncthreads();   // every wave is done with V_j
-#pragma unroll
-    for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, next_kb0, lane, wave, i);
     if constexpr (STORE && ONE_STORE) {
       // the lane's eight keys (4 g + r and 16 + 4 g + r of the block) of its query, at positions
       // 8 g .. 8 g + 7 of the block's 32: one 16-byte store per series and order, a contiguous
