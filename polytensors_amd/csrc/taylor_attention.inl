@@ -937,191 +937,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
                                         : reinterpret_cast<const uint8_t*>(Q.p[0]);
   const int mstep = mask != nullptr ? 1 : 0;
 
-  // ---- pass 1: a shift m_used for the exponentials, at least the row maximum of
-  // the order-0 scores and close to it. With it fixed up front the output
-  // accumulators are never rescaled, so they are touched by MFMAs only. The
-  // output does not depend on the shift (it cancels in O = N / l); it only has
-  // to keep exp(s - m_used) from overflowing (m_used >= max s) and from
-  // underflowing (m_used - max s small).
-  //
-  // The scores of this pass are bf16 products with fp32 accumulation: with
-  // u = 2^-8 the unit roundoff of bf16, each is within 2^-6 scale |q| |k| of the
-  // exact one (Cauchy-Schwarz on (2u + u^2 + 2^-17) sum |q_i k_i|), so
-  // m_used = bf16 row maximum + that bound (max |k| bounded from the keys read)
-  // is at least the exact maximum and at most twice the bound above it. The
-  // waves split the key blocks (wave w takes blocks w, w + 4, ...) and score
-  // them against all 64 query rows of the workgroup, so each key row is read
-  // once per workgroup rather than once per wave; the partial maxima meet in
-  // LDS (the second K/V tile buffer, idle until pass 2). A wave whose bound
-  // exceeds 20 (the largest p could drop below e^-40) recomputes its rows'
-  // exact fp32 maximum over all keys instead.
-  A m_row = kNegInf;
-  {
-    // Key operands and mask words are fetched two blocks ahead with the block
-    // index clamped to the last block, so every load is unconditional. They are
-    // buffer loads: LLVM folds a loop-carried rotation of plain loads back into
-    // a load at the use, which would undo the prefetch.
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(Kp.p[0] + head * S * D), static_cast<short>(0), S * D * 4, kBufferRsrcWord3);
-    // (a buffer resource must be wave-uniform: the mask's is the whole (L, S)
-    // mask, with the lane's row in the offset; without a mask, a 4-byte dummy)
-    const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
-        mask != nullptr ? static_cast<void*>(const_cast<uint8_t*>(mask)) : static_cast<void*>(const_cast<float*>(Q.p[0])),
-        static_cast<short>(0), mask != nullptr ? L * S : 4, kBufferRsrcWord3);
-    const uint32_t kofs = static_cast<uint32_t>((c * D + 4 * h) * 4);
-    const int last = lo + (nblocks - 1) * kAttnBN;
-
-    // |q|^2 of the lane's own row (its share; summed over the lane groups below)
-    A qn2 = A(0);
-    {
-#pragma unroll
-      for (int dc = 0; dc < DB; ++dc) {
-        const Vec<float, 4> qv = load_vec<float, 4>(qrow[0] + dc * 16 + 4 * h);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) qn2 = fmaf(qv.v[s], qv.v[s], qn2);
-      }
-    }
-
-    // The workgroup's four query tiles (rows q_block + 16 t + c) as bf16 B operands.
-    AttnBf16x4 qt[kAttnWaves][DB];
-    uint32_t mofs_t[kAttnWaves];
-    A mt[kAttnWaves];
-#pragma unroll
-    for (int t = 0; t < kAttnWaves; ++t) {
-      const int row_t = min(q_block + t * kAttnQPerWave + c, L - 1);
-#pragma unroll
-      for (int dc = 0; dc < DB; ++dc)
-        qt[t][dc] = attn_pack_bf16x4(load_vec<float, 4>(Q.p[0] + (head * L + row_t) * D + dc * 16 + 4 * h));
-      mofs_t[t] = mask != nullptr ? static_cast<uint32_t>(row_t * S + 4 * h) : 0u;
-      mt[t] = kNegInf;
-    }
-    A kp2 = A(0);   // max over the keys read by this lane of its share of |k|^2
-    const int nb = (nblocks - wave + kAttnWaves - 1) / kAttnWaves;   // this wave's blocks
-    if (nb > 0) {
-      const int my_last = wave + (nb - 1) * kAttnWaves;                // its last block index
-      Vec<float, 4> kb[3][DB];
-      uint32_t mb[3][kAttnWaves];
-      auto fetch = [&](Vec<float, 4>(&kd)[DB], uint32_t(&md)[kAttnWaves], int i) {
-        const int rb = lo + min(wave + i * kAttnWaves, my_last) * kAttnBN;
-#pragma unroll
-        for (int dc = 0; dc < DB; ++dc) kd[dc] = attn_buffer_load4(krs, kofs + (rb * D + dc * 16) * 4);
-#pragma unroll
-        for (int t = 0; t < kAttnWaves; ++t) md[t] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs_t[t] + mstep * rb, 0, 0);
-      };
-      fetch(kb[0], mb[0], 0);
-      __builtin_amdgcn_sched_barrier(0);
-      fetch(kb[1], mb[1], 1);
-      __builtin_amdgcn_sched_barrier(0);
-      // block i's operands go to buffer i % 3 (a static rotation: the loop is
-      // unrolled by three and runs a multiple of three blocks, the surplus ones
-      // re-reading the last block and excluded)
-      for (int i0 = 0; i0 < nb; i0 += 3) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) {
-          const int i = i0 + u;
-          fetch(kb[(u + 2) % 3], mb[(u + 2) % 3], i + 2);
-          __builtin_amdgcn_sched_barrier(0);
-          const bool real = i < nb;
-          const int kb0 = lo + min(wave + i * kAttnWaves, my_last) * kAttnBN;
-          AttnBf16x4 kh[DB];
-          A part = A(0);
-#pragma unroll
-          for (int dc = 0; dc < DB; ++dc) {
-            kh[dc] = attn_pack_bf16x4(kb[u][dc]);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) part = fmaf(kb[u][dc].v[s], kb[u][dc].v[s], part);
-          }
-          kp2 = fmaxf(kp2, part);
-#pragma unroll
-          for (int t = 0; t < kAttnWaves; ++t) {
-            acc_t s0 = MF::zero();
-#pragma unroll
-            for (int dc = 0; dc < DB; ++dc) s0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kh[dc], qt[t][dc], s0, 0, 0, 0);
-            const int q_t = q_block + t * kAttnQPerWave + c;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const bool ok = real & attn_key_ok(mb[u][t], kb0, r, h, q_t, q_t < L, causal, mask != nullptr);
-              mt[t] = fmaxf(mt[t], ok ? s0[r] * scale : kNegInf);
-            }
-          }
-        }
-      }
-    }
-    // partial maxima over this wave's keys per query row; |q| per row; a bound on
-    // max |k| over the wave's keys (sum over lane groups of each group's maximum
-    // share, then the maximum over the 16 key lanes)
-#pragma unroll
-    for (int t = 0; t < kAttnWaves; ++t) {
-      mt[t] = fmaxf(mt[t], __shfl_xor(mt[t], 16, kWave));
-      mt[t] = fmaxf(mt[t], __shfl_xor(mt[t], 32, kWave));
-    }
-    qn2 += __shfl_xor(qn2, 16, kWave);
-    qn2 += __shfl_xor(qn2, 32, kWave);
-    kp2 += __shfl_xor(kp2, 16, kWave);
-    kp2 += __shfl_xor(kp2, 32, kWave);
-#pragma unroll
-    for (int off = 1; off < 16; off *= 2) kp2 = fmaxf(kp2, __shfl_xor(kp2, off, kWave));
-    float* xch = &tiles[1][0][0][0][0];   // [wave][64 rows] partial maxima, then [wave] max |k|^2
-    if (h == 0) {
-#pragma unroll
-      for (int t = 0; t < kAttnWaves; ++t) xch[wave * kAttnBM + t * kAttnQPerWave + c] = mt[t];
-      if (c == 0) xch[kAttnWaves * kAttnBM + wave] = kp2;
-    }
-    __syncthreads();
-    A k2 = A(0);
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      m_row = fmaxf(m_row, xch[w * kAttnBM + wave * kAttnQPerWave + c]);
-      k2 = fmaxf(k2, xch[kAttnWaves * kAttnBM + w]);
-    }
-    // (pass 2 writes this buffer only after its first barrier, when every wave has read it)
-    const A bound = A(0.015625) * fabsf(scale) * sqrtf(qn2 * k2);
-    if (__any(!(bound <= A(20)))) {
-      // exact fp32 maximum over all keys for this wave's rows (a NaN bound lands here too)
-      Vec<float, 4> q0[DB], kb[3][DB];
-      uint32_t mb[3];
-#pragma unroll
-      for (int dc = 0; dc < DB; ++dc) q0[dc] = load_vec<float, 4>(qrow[0] + dc * 16 + 4 * h);
-      const uint32_t mofs = mask != nullptr ? static_cast<uint32_t>(q_row * S + 4 * h) : 0u;
-      A m = kNegInf;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int rb = min(lo + b * kAttnBN, last);
-#pragma unroll
-        for (int dc = 0; dc < DB; ++dc) kb[b][dc] = attn_buffer_load4(krs, kofs + (rb * D + dc * 16) * 4);
-        mb[b] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs + mstep * rb, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      for (int j0 = 0; j0 < nblocks; j0 += 3) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) {
-          const int kb0 = lo + (j0 + u) * kAttnBN;
-          const int ra = min(kb0 + 2 * kAttnBN, last);
-#pragma unroll
-          for (int dc = 0; dc < DB; ++dc) kb[(u + 2) % 3][dc] = attn_buffer_load4(krs, kofs + (ra * D + dc * 16) * 4);
-          mb[(u + 2) % 3] = __builtin_amdgcn_raw_buffer_load_b32(mrs, mofs + mstep * ra, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          acc_t s0 = MF::zero();
-#pragma unroll
-          for (int dc = 0; dc < DB; ++dc)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) s0 = MF::mma(kb[u][dc].v[s], q0[dc].v[s], s0);
-          const bool real = kb0 <= last;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const bool ok = real & attn_key_ok(mb[u], kb0, r, h, my_q, q_ok, causal, mask != nullptr);
-            m = fmaxf(m, ok ? s0[r] * scale : kNegInf);
-          }
-        }
-      }
-      m = fmaxf(m, __shfl_xor(m, 16, kWave));
-      m_row = fmaxf(m, __shfl_xor(m, 32, kWave));
-    } else if (m_row != kNegInf) {
-      m_row += bound;
-    }
-  }
-  // a row with no visible key keeps p = 0 everywhere; any finite shift will do
-  const A m_used = m_row == kNegInf ? A(0) : m_row;
+  // The shift of the exponentials is a running maximum of the order-0 scores, raised lazily:
+  // only when a key block's maximum exceeds it by more than kSlack (so p <= e^kSlack), with the
+  // accumulators rescaled on that rare path. The output does not depend on the shift (it cancels
+  // in O = N / l).
+  constexpr A kSlack = A(8);
+  A m_used = kNegInf;
 
   // the first key block's DMA is issued only now: LDS-DMA loads pending beside
   // ordinary loads make the compiler wait for every load in flight
@@ -1187,7 +1008,34 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
     for (int r = 0; r < 4; ++r) valid[r] = attn_key_ok(mword, kb0, r, h, my_q, q_ok, causal, mask != nullptr);
 
 
-    // ---- exponential series against the fixed row maximum ----
+    // ---- running maximum of the order-0 scores (the row's 16 keys of this block are spread over
+    // the four lane groups), raised lazily ----
+    A bmax = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, valid[r] ? sc[0][r] * scale : kNegInf);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
+    // a row whose shift is still -inf has accumulated nothing: raising it rescales nothing
+    if (__any(raise && m_used != kNegInf)) {
+      const A alpha = (raise && m_used != kNegInf) ? exp_fast(m_used - bmax) : A(1);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        lsum[o] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          // out of and back into the accumulation registers here, on this rare path, so that the
+          // accumulators keep one register class across the loop (no copies per block)
+          asm volatile("" : "+a"(acc_o[o][db]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+          asm volatile("" : "+a"(acc_o[o][db]));
+        }
+      }
+    }
+    if (raise) m_used = bmax;
+
+    // ---- exponential series against the running maximum ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const A p = valid[r] ? exp_fast(sc[0][r] * scale - m_used) : A(0);
@@ -1249,7 +1097,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
   }
 
   __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMA has landed before the workgroup ends
-  attention_epilogue<float, K, D, acc_t, AttnPvE<D>::value>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, h);
+  // (a row with no visible key has p = 0 everywhere: any finite shift will do)
+  attention_epilogue<float, K, D, acc_t, AttnPvE<D>::value>(acc_o, lsum, m_used == kNegInf ? A(0) : m_used, O, LSE,
+                                                           head, L, my_q, q_ok, h);
 }
 
 template <typename T, int K, int D>
