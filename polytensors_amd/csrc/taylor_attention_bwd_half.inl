@@ -494,6 +494,27 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   const int last_kb0 = lo + (nblocks - 1) * KB;
   const int tj = c / 4, ta = c % 4;
 
+  // A block's mask bytes (and additive values) are read one block ahead, right after the barrier
+  // that opens the previous block and before that block's DMA: loads complete in issue order, so
+  // a read issued at the top of its own block would hold the block for a full memory round trip.
+  // (In the stored-tile launches. The recomputing ones, which hold more registers, read them at
+  // the top of their block: ahead, their registers made some instantiations spill.)
+  constexpr bool kAhead = MASK != 0 && STORE;
+  uint8_t mnext[MASK != 0 ? 2 : 1][4];
+  float anext[MASK == 2 ? 2 : 1][4];
+  auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
+    if constexpr (MASK != 0) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb0 + 16 * kh + 4 * g + r;
+          mnext[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, key, L, S);
+          if constexpr (MASK == 2) anext[kh][r] = attn_mask_add(madd, my_q, key, L, S);
+        }
+    }
+  };
+
   // block 0's tiles (after the row loads: the compiler's waits for those would wait for the DMA).
   // The row loads are waited for here, once: otherwise the compiler, which sees them pending at
   // the loop's entry, waits for them inside the loop, on every block, where the count it uses
@@ -504,10 +525,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     attn_half_dma_tile<T, K, D>(Kt[0], Kp, head, S, lo, lane, wave, i);
     attn_half_dma_tile<T, K, D>(Vt, Vp, head, S, lo, lane, wave, i);
   }
+  if constexpr (kAhead) fetch_mask(lo);
 
-  // The P / dS stores of a block (without a mask: one 16-byte store per series and order) go out
-  // after the block's last DMA, so the next block waits for its DMAs only. A wave with rows
-  // issues all of them (their branch skips only a wave without rows).
+  // The P / dS stores of a block go out after its last DMA (without a mask all of them, one 16-byte
+  // store per series and order; with one, the second half's 8-byte stores: 2(K+1) either way), so
+  // the next block waits for its DMAs only. A wave with rows issues all of them (their branch skips
+  // only a wave without rows).
   constexpr bool ONE_STORE = MASK == 0;
   constexpr int kStoresAfterDma = 2 * (K + 1);   // s_waitcnt vmcnt(2(K+1)) expcnt(0) lgkmcnt(0)
   static_assert(!STORE || kStoresAfterDma < 16, "vmcnt field");
@@ -517,24 +540,26 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     const int next_kb0 = min(kb0 + KB, last_kb0);   // the last block re-loads itself: no branch
     Tile& cur = Kt[j & 1];
     Tile& nxt = Kt[(j + 1) & 1];
+    if constexpr (MASK != 0 && !kAhead) fetch_mask(kb0);   // this block's, at its top
+    if (STORE && (ONE_STORE || kAhead) && j > 0 && wave_rows) {
+      // this wave's DMAs of block j have landed; the tile stores of block j-1 that followed its
+      // last DMA, its last 2(K+1) vector memory operations (the counter drops in issue order), may
+      // still be in flight
+      __builtin_amdgcn_s_waitcnt(kStoresAfterDma);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
+    }
+    __syncthreads();                 // ... and every wave's; block j-1 is done with nxt
     uint8_t mbyte[2][4];
     float add[2][4];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = kb0 + 16 * kh + 4 * g + r;
-        mbyte[kh][r] = MASK != 0 ? attn_mask_byte(mask, Q.p[0], my_q, key, L, S) : uint8_t(1);
-        add[kh][r] = MASK == 2 ? attn_mask_add(madd, my_q, key, L, S) : 0.f;
+        mbyte[kh][r] = MASK != 0 ? mnext[kh][r] : uint8_t(1);
+        add[kh][r] = MASK == 2 ? anext[kh][r] : 0.f;
       }
-    if (STORE && ONE_STORE && j > 0 && wave_rows) {
-      // this wave's DMAs of block j have landed; the tile stores of block j-1, its last 2(K+1)
-      // vector memory operations (the counter drops in issue order), may still be in flight
-      __builtin_amdgcn_s_waitcnt(kStoresAfterDma);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
-    }
-    __syncthreads();                 // ... and every wave's; block j-1 is done with nxt
+    if constexpr (kAhead) fetch_mask(next_kb0);   // the next block's, ahead of its DMA
 #pragma unroll
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
 
@@ -1278,17 +1303,28 @@ __global__ __launch_bounds__(KEYS * 4) void taylor_attention_bwd_kv_half_mat_ker
       if constexpr (DO_K) attn_half_dma_tile_w<T, K, D, WAVES>(Xt[buf][SK], Q, head, L, qb0, lane, wave, i);
     }
   };
+  // a block's mask bytes are read one block ahead, before that block's DMA (loads complete in
+  // issue order: read at the top of its own block, they would hold it for a memory round trip)
+  uint8_t mnext[MASKED ? 8 : 1];
+  auto fetch_mask = [&](int qb0) __attribute__((always_inline)) {
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        mnext[s] = attn_mask_byte(mask, Q.p[0], qb0 + 16 * (s / 4) + 4 * g + s % 4, my_k, L, S);
+    }
+  };
   dma(0, lo);
+  fetch_mask(lo);
 
   for (int j = 0; j < nblocks; ++j) {
     const int qb0 = lo + j * KB;
     const int cur = j & 1;
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and its mask bytes)
+    __syncthreads();                 // ... and every wave's; block j-1 is done with the other buffers
     uint8_t mbyte[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      mbyte[s] = MASKED ? attn_mask_byte(mask, Q.p[0], qb0 + 16 * (s / 4) + 4 * g + s % 4, my_k, L, S) : uint8_t(1);
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask bytes)
-    __syncthreads();                 // ... and every wave's; block j-1 is done with the other buffers
+    for (int s = 0; s < 8; ++s) mbyte[s] = MASKED ? mnext[s] : uint8_t(1);
+    fetch_mask(min(qb0 + KB, last_qb0));   // the next block's, ahead of its DMA
     dma(cur ^ 1, min(qb0 + KB, last_qb0));   // block j+1 (the last block re-loads itself: no branch)
 
     // admissibility of the eight pairs behind the lane's operand slots (slot 4 qh + r: query
