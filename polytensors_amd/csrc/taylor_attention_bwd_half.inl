@@ -527,11 +527,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   }
   if constexpr (kAhead) fetch_mask(lo);
 
-  // The P / dS stores of a block go out after its last DMA (without a mask all of them, one 16-byte
-  // store per series and order; with one, the second half's 8-byte stores: 2(K+1) either way), so
-  // the next block waits for its DMAs only. A wave with rows issues all of them (their branch skips
-  // only a wave without rows).
-  constexpr bool ONE_STORE = MASK == 0;
+  // The P / dS stores of a block go out after its last DMA (both halves' in one 16-byte store per
+  // series and order; where the registers do not allow that, at degree 4 and d 128 with a mask, the
+  // second half's 8-byte stores: 2(K+1) either way), so the next block waits for its DMAs only. A
+  // wave with rows issues all of them (their branch skips only a wave without rows). Per-half stores
+  // also cost the second half a reload of the G rows: the compiler cannot move those loads above
+  // the first half's stores.
+  constexpr bool ONE_STORE = MASK == 0 || K < 4 || D < 128;
   constexpr int kStoresAfterDma = 2 * (K + 1);   // s_waitcnt vmcnt(2(K+1)) expcnt(0) lgkmcnt(0)
   static_assert(!STORE || kStoresAfterDma < 16, "vmcnt field");
   const bool wave_rows = q_block + wave * kAttnQPerWave < L;
@@ -564,8 +566,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
 
     // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
-    // (the P operands of both halves are held for one store where the registers allow: without a
-    // mask; with one, each half's are stored as they are formed)
+    // (the P operands of both halves are held for one store where the registers allow; otherwise
+    // each half's are stored as they are formed)
     u32x4 dsb[K + 1], dsl[NLO], ppk[STORE && ONE_STORE ? K + 1 : 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
