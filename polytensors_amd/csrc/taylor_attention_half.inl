@@ -39,6 +39,8 @@
 // loop.
 #pragma once
 
+#include <type_traits>
+
 #include "half_mfma.h"
 #include "taylor_attention.inl"
 
@@ -458,6 +460,64 @@ __device__ __forceinline__ void attn_half_issue_op(T (&buf)[2][K + 1][32][D], co
   lds_dma16(&buf[kv][o][seg * RPS][0], rsrc, ((kb0 + row) * D + lch * 8) * static_cast<int>(sizeof(T)));
 }
 
+// The pipelined kernels' epilogue: the row sums over the lane groups, O_k = (N_k - sum_{j=1..k} l_j
+// O_{k-j}) / l_0 into the outputs, and the lse series (+inf and zeros for a row without keys).
+template <typename T, int K, int DB>
+__device__ __forceinline__ void attn_half_fwd_epilogue(floatx4 (&acc_o)[K + 1][DB], float (&lsum)[K + 1], float m_used,
+                                                       MPtrs<T>& O, MPtrs<float>& LSE, int64_t head, int L, int my_q,
+                                                       bool q_ok, int g) {
+  using MM = HalfMfma<T>;
+  constexpr int D = 16 * DB;
+#pragma unroll
+  for (int o = 0; o <= K; ++o) {
+    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
+    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  }
+  if (!q_ok) return;
+  const bool empty = !(lsum[0] > 0.f);
+  const float inv_l0 = empty ? 0.f : 1.f / lsum[0];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    float out[4][K + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int k = 0; k <= K; ++k) {
+        float t = acc_o[k][db][r];
+#pragma unroll
+        for (int jj = 1; jj <= k; ++jj) t -= lsum[jj] * out[r][k - jj];
+        out[r][k] = t * inv_l0;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k <= K; ++k)
+      *reinterpret_cast<uint2*>(O.p[k] + (head * L + my_q) * D + 16 * db + 4 * g) =
+          make_uint2(MM::pack2(out[0][k], out[1][k]), MM::pack2(out[2][k], out[3][k]));
+  }
+  if (LSE.p[0] != nullptr && g == 0) {
+    const int64_t at = head * L + my_q;
+    if (empty) {
+      LSE.p[0][at] = __builtin_huge_valf();
+#pragma unroll
+      for (int k = 1; k <= K; ++k) LSE.p[k][at] = 0.f;
+    } else {
+      float lse[K + 1], nrm[K + 1];
+      lse[0] = m_used + logf(lsum[0]);
+#pragma unroll
+      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
+#pragma unroll
+      for (int k = 1; k <= K; ++k) {
+        float t = nrm[k];
+#pragma unroll
+        for (int jj = 1; jj < k; ++jj) t -= (static_cast<float>(jj) / static_cast<float>(k)) * lse[jj] * nrm[k - jj];
+        lse[k] = t;
+      }
+#pragma unroll
+      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+    }
+  }
+}
+
 // MASK: 0 none (mask_all and madd_all unused), 1 a boolean mask, 2 an additive mask madd (float32
 // values) with the boolean mask of its finite entries. Without a mask no mask memory is read.
 template <typename T, int K, int D, int MASK>
@@ -601,7 +661,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     };
     u32x4 kring[R];
 #pragma unroll
-    for (int t = 0; t < R - 1; ++t) kring[t] = load_k(t);
+    for (int t = 0; t < R - 1 && t < KT; ++t) kring[t] = load_k(t);   // (no item past the block)
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       if (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
@@ -713,7 +773,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     constexpr int VT = DB * (K + 1);
     u32x4 vring[R];
 #pragma unroll
-    for (int t = 0; t < R - 1; ++t) vring[t] = load_v(t);
+    for (int t = 0; t < R - 1 && t < VT; ++t) vring[t] = load_v(t);
 #pragma unroll
     for (int t = 0; t < VT; ++t) {
       if (t + R - 1 < VT) vring[(t + R - 1) % R] = load_v(t + R - 1);
@@ -736,55 +796,306 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   for (int j = 0; j < nblocks; ++j) block(tiles[j & 1], tiles[(j + 1) & 1], j);
   __builtin_amdgcn_s_waitcnt(0);   // the last block's (redundant) DMA has landed before the workgroup ends
 
-  // ---- epilogue ----
-#pragma unroll
-  for (int o = 0; o <= K; ++o) {
-    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+  attn_half_fwd_epilogue<T, K, DB>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, g);
+}
+
+// Software-pipelined form of the kernel above for degrees 0..4 (one probability operand per
+// order). Iteration j forms key block j+1's scores and, between those products, runs block j's
+// exponential series (VALU work that issues while the MFMAs execute), then block j's value
+// products. The series of a block is cut into units, one order of one row each, spread evenly
+// over the next block's score items.
+// Buffers: the K tile of block j+2 goes where block j's K tile was (read by the previous
+// iteration's scores), the V tile of block j+1 where block j-1's was; both are issued at the top of
+// iteration j and waited for at the top of iteration j+1.
+// f(integral_constant<int, I>) for I = B .. E-1 in order: indices that are constants from the
+// start, so register arrays indexed by them never go to scratch
+template <int B, int E, typename F>
+__device__ __forceinline__ void attn_static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    attn_static_for<B + 1, E>(f);
   }
-  if (!q_ok) return;
-  const bool empty = !(lsum[0] > 0.f);
-  const float inv_l0 = empty ? 0.f : 1.f / lsum[0];
+}
+
+template <int K, int D>
+struct AttnHalfSw {
+  static constexpr bool fits = AttnHalfPipe<K, D>::fits && !AttnHalfPipe<K, D>::split;
+  static constexpr int R = 6;   // operand rings: reads run five items ahead (four: 1% slower at K=4, d=128)
+};
+
+template <typename T, int K, int D, int MASK>
+__global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_sw_kernel(
+    CPtrs<T> Q, CPtrs<T> Kp, CPtrs<T> Vp, MPtrs<T> O, MPtrs<float> LSE, int L, int S,
+    const uint8_t* __restrict__ mask_all, AttnMaskMap mmap, const int32_t* __restrict__ ranges_all,
+    const float* __restrict__ madd_all, int causal, float scale) {
+  using P = AttnHalfPipe<K, D>;
+  using MM = HalfMfma<T>;
+  constexpr int KB = P::KB, DC = (D + 31) / 32, DB = D / 16, OPS = P::OPS, KOPS = OPS / 2;
+  constexpr float kNegInf = -__builtin_huge_valf();
+  constexpr float kSlack = MM::kSlack;
+  constexpr bool ADD = MASK == 2;
+  static_assert(P::LDS <= 160 * 1024 && !P::split, "two K/V tiles within LDS, one operand per order");
+
+  using Tiles = T[2][K + 1][KB][D];
+  __shared__ __attribute__((aligned(16))) Tiles tiles[2];
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c = lane % 16;
+  const int g = lane / 16;
+  int64_t head;
+  int q_block;
+  attn_work_item(L, causal, head, q_block);
+  const int64_t mask_index = attn_mask_index(mmap, head);
+  const uint8_t* mask = mask_all != nullptr ? mask_all + mask_index * L * S : nullptr;
+  const int32_t* ranges = ranges_all != nullptr ? ranges_all + mask_index * attn_ranges_count(L, S) : nullptr;
+  const float* madd = ADD ? madd_all + mask_index * L * S : nullptr;
+  const int my_q = q_block + wave * kAttnQPerWave + c;
+  const bool q_ok = my_q < L;
+  const int64_t qrow = (head * L + (q_ok ? my_q : L - 1)) * D;
+
+  u32x4 qreg[K + 1][DC];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    float out[4][K + 1];
+  for (int o = 0; o <= K; ++o)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int k = 0; k <= K; ++k) {
-        float t = acc_o[k][db][r];
-#pragma unroll
-        for (int jj = 1; jj <= k; ++jj) t -= lsum[jj] * out[r][k - jj];
-        out[r][k] = t * inv_l0;
-      }
+    for (int dc = 0; dc < DC; ++dc) {
+      const bool din = 32 * dc + 8 * g < D;
+      qreg[o][dc] = attn_half_load8<T>(Q.p[o] + qrow + (din ? 32 * dc + 8 * g : 0), din);
     }
-#pragma unroll
-    for (int k = 0; k <= K; ++k)
-      *reinterpret_cast<uint2*>(O.p[k] + (head * L + my_q) * D + 16 * db + 4 * g) =
-          make_uint2(MM::pack2(out[0][k], out[1][k]), MM::pack2(out[2][k], out[3][k]));
+
+  int lo = 0, hi = S;
+  if (causal) hi = min(S, q_block + kAttnBM);
+  if (ranges != nullptr) {
+    const int qb = q_block / kAttnRangeBlock;
+    lo = ranges[2 * qb] / KB * KB;
+    hi = min(hi, static_cast<int>(ranges[2 * qb + 1]));
   }
-  if (LSE.p[0] != nullptr && g == 0) {
-    const int64_t at = head * L + my_q;
-    if (empty) {
-      LSE.p[0][at] = __builtin_huge_valf();
+  if (hi <= lo) lo = hi = 0;
+  const int nblocks = max(1, (hi - lo + KB - 1) / KB);
+  const int last_kb0 = lo + (nblocks - 1) * KB;
+  auto kb_of = [&](int j) { return min(lo + j * KB, last_kb0); };   // past the end: the last block again
+
+  floatx4 acc_o[K + 1][DB];
 #pragma unroll
-      for (int k = 1; k <= K; ++k) LSE.p[k][at] = 0.f;
+  for (int o = 0; o <= K; ++o)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[o][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_used = kNegInf;
+  float iscale[K + 1];
+#pragma unroll
+  for (int i = 0; i <= K; ++i) iscale[i] = static_cast<float>(i) * scale;
+  float lsum[K + 1];
+#pragma unroll
+  for (int o = 0; o <= K; ++o) lsum[o] = 0.f;
+
+  uint8_t mnext[MASK ? 2 : 1][4];
+  float anext[ADD ? 2 : 1][4];
+  auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
+    if constexpr (MASK != 0) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mnext[kh][r] = mask[static_cast<int64_t>(min(my_q, L - 1)) * S + min(kb0 + 16 * kh + 4 * g + r, S - 1)];
+    }
+    if constexpr (ADD) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) anext[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+    }
+  };
+
+  // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T of the block in buffer kt, two 16-key halves ----
+  // Items t = (step, b) as in the kernel above; extra(t) runs the other work of item t (DMA
+  // shares and series units) before the item's products, which execute while it issues.
+  constexpr int R = AttnHalfSw<K, D>::R;
+  constexpr int KT = 2 * DC * (K + 1);
+  auto scores = [&](Tiles& kt, floatx4 (&s)[2][K + 1], auto&& extra) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int o = 0; o <= K; ++o) s[kh][o] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load_k = [&](int t) {
+      const int st = t / (K + 1), o = t % (K + 1);
+      const int dc = st / 2, kh = st % 2;
+      const int row = 16 * kh + c;
+      const bool din = 32 * dc + 8 * g < D;
+      const int pch = ((4 * dc + g) & (P::CH - 1)) ^ P::fs(row);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&kt[0][o][row][pch * 8]);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      return din ? v : z;
+    };
+    u32x4 kring[R];
+#pragma unroll
+    for (int t = 0; t < R - 1 && t < KT; ++t) kring[t] = load_k(t);   // (no item past the block)
+    attn_static_for<0, KT>([&](auto tc) __attribute__((always_inline)) {
+      constexpr int t = decltype(tc)::value;
+      if constexpr (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
+      extra(tc);
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int st = t / (K + 1), bo = t % (K + 1);
+      constexpr int dc = st / 2, kh = st % 2;
+#pragma unroll
+      for (int a = 0; a + bo <= K; ++a) s[kh][a + bo] = MM::mma(kring[t % R], qreg[a][dc], s[kh][a + bo]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T of the block in buffer vt ----
+  const int tj = c / 4, ta = c % 4;
+  auto values = [&](Tiles& vt, const u32x4 (&pb)[K + 1]) __attribute__((always_inline)) {
+    auto load_v = [&](int t) {
+      const int db = t / (K + 1), o = t % (K + 1);
+      const int row0 = 4 * g + tj, row1 = 16 + 4 * g + tj;
+      const int lch = 2 * db + ta / 2;
+      const int off0 = ((lch ^ P::fs(row0)) * 8) + 4 * (ta % 2);
+      const int off1 = ((lch ^ P::fs(row1)) * 8) + 4 * (ta % 2);
+      return lds_read_tr16x2(&vt[1][o][row0][off0], &vt[1][o][row1][off1]);
+    };
+    constexpr int VT = DB * (K + 1);
+    u32x4 vring[R];
+#pragma unroll
+    for (int t = 0; t < R - 1 && t < VT; ++t) vring[t] = load_v(t);
+#pragma unroll
+    for (int t = 0; t < VT; ++t) {
+      if (t + R - 1 < VT) vring[(t + R - 1) % R] = load_v(t + R - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int db = t / (K + 1), bo = t % (K + 1);
+#pragma unroll
+      for (int a = 0; a + bo <= K; ++a) acc_o[a + bo][db] = MM::mma(vring[t % R], pb[a], acc_o[a + bo][db]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  floatx4 scc[2][K + 1], scn[2][K + 1];   // scores of the block in its series, and of the next
+
+  // prologue: block 0's tiles, block 1's K tile, block 0's mask values; block 0's scores
+#pragma unroll
+  for (int i = 0; i < OPS; ++i) attn_half_issue_op<T, K, D>(tiles[0], Kp, Vp, head, S, lo, lane, wave, i);
+#pragma unroll
+  for (int i = 0; i < KOPS; ++i) attn_half_issue_op<T, K, D>(tiles[1], Kp, Vp, head, S, kb_of(1), lane, wave, i);
+  fetch_mask(lo);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  scores(tiles[0], scc, [&](auto) {});
+
+  // iteration j: block j's series and value products, block j+1's scores (LAST: none)
+  auto step = [&](int j, auto last) __attribute__((always_inline)) {
+    constexpr bool LAST = decltype(last)::value;
+    Tiles& cur = tiles[j & 1];
+    Tiles& nxt = tiles[(j + 1) & 1];
+    const int kb0 = lo + j * KB;
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's K(j+1), V(j) and mask values of block j have landed
+    __syncthreads();                 // ... every wave's; K(j) and V(j-1) are no longer read
+    uint8_t mbyte[MASK ? 2 : 1][4];
+    float add[ADD ? 2 : 1][4];
+    if constexpr (MASK != 0) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          mbyte[kh][r] = mnext[kh][r];
+          if constexpr (ADD) add[kh][r] = anext[kh][r];
+        }
+    }
+    if constexpr (!LAST) fetch_mask(kb_of(j + 1));
+
+    // ---- mask, online maximum of the constant order (rescale on a raise) ----
+    bool valid[2][4];
+    float s0[2][4];
+    float bmax = kNegInf;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb0 + 16 * kh + 4 * g + r;
+        bool ok = q_ok && key < hi;
+        if (causal) ok = ok && key <= my_q;
+        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        valid[kh][r] = ok;
+        float sv = scc[kh][0][r] * scale;
+        if constexpr (ADD) sv += add[kh][r];
+        s0[kh][r] = ok ? sv : kNegInf;
+        bmax = fmaxf(bmax, s0[kh][r]);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
+    if (__any(raise)) {
+      const float m_new = raise ? bmax : m_used;
+      const float alpha = (raise && m_used != kNegInf) ? exp_fast(m_used - m_new) : (raise ? 0.f : 1.f);
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        lsum[o] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          asm volatile("" : "+a"(acc_o[o][db]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc_o[o][db][r] *= alpha;
+          asm volatile("" : "+a"(acc_o[o][db]));
+        }
+      }
+      m_used = m_new;
+    }
+
+    // ---- the series in units: unit u is order u % (K+1) of row u / (K+1) (half row / 4, key
+    // register row % 4); after the last order of an odd row the row pair is packed ----
+    u32x4 pb[K + 1];
+    float bser[K + 1];
+    float wrow[2][K + 1];
+    auto unit = [&](auto uc) __attribute__((always_inline)) {
+      constexpr int u = decltype(uc)::value;
+      constexpr int row = u / (K + 1), k = u % (K + 1);
+      constexpr int kh = row / 4, r = row % 4;
+      if constexpr (k == 0) {
+#pragma unroll
+        for (int o = 1; o <= K; ++o) bser[o] = scc[kh][o][r] * iscale[o];
+        wrow[r & 1][0] = valid[kh][r] ? exp_fast(s0[kh][r] - m_used) : 0.f;
+      } else {
+        float t = bser[1] * wrow[r & 1][k - 1];
+#pragma unroll
+        for (int i = 2; i <= k; ++i) t = fmaf(bser[i], wrow[r & 1][k - i], t);
+        wrow[r & 1][k] = t * (1.f / static_cast<float>(k));
+      }
+      if constexpr (k == K && (r & 1)) {
+        // the row sums add the weights as rounded for the value products
+#pragma unroll
+        for (int o = 0; o <= K; ++o) {
+          const uint32_t w2 = MM::pack2(wrow[0][o], wrow[1][o]);
+          pb[o][2 * kh + r / 2] = w2;
+          lsum[o] = MM::sum2(w2, lsum[o]);
+        }
+      }
+    };
+    constexpr int U = 8 * (K + 1);
+    if constexpr (LAST) {
+      attn_static_for<0, U>(unit);
     } else {
-      float lse[K + 1], nrm[K + 1];
-      lse[0] = m_used + logf(lsum[0]);
-#pragma unroll
-      for (int k = 1; k <= K; ++k) nrm[k] = lsum[k] * inv_l0;
-#pragma unroll
-      for (int k = 1; k <= K; ++k) {
-        float t = nrm[k];
-#pragma unroll
-        for (int jj = 1; jj < k; ++jj) t -= (static_cast<float>(jj) / static_cast<float>(k)) * lse[jj] * nrm[k - jj];
-        lse[k] = t;
-      }
-#pragma unroll
-      for (int k = 0; k <= K; ++k) LSE.p[k][at] = lse[k];
+      const int kb_k = kb_of(j + 2), kb_v = kb_of(j + 1);
+      scores(nxt, scn, [&](auto tc) __attribute__((always_inline)) {
+        constexpr int t = decltype(tc)::value;
+        // K(j+2) into this block's K tile, V(j+1) into the other buffer's V tile
+        attn_static_for<t * OPS / KT, (t + 1) * OPS / KT>([&](auto ic) __attribute__((always_inline)) {
+          constexpr int i = decltype(ic)::value;
+          if constexpr (i < KOPS) attn_half_issue_op<T, K, D>(cur, Kp, Vp, head, S, kb_k, lane, wave, i);
+          else attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, kb_v, lane, wave, i);
+        });
+        attn_static_for<t * U / KT, (t + 1) * U / KT>(unit);
+      });
     }
-  }
+    values(cur, pb);
+    if constexpr (!LAST) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int o = 0; o <= K; ++o) scc[kh][o] = scn[kh][o];
+    }
+  };
+  for (int j = 0; j + 1 < nblocks; ++j) step(j, std::false_type{});
+  step(nblocks - 1, std::true_type{});
+  __builtin_amdgcn_s_waitcnt(0);   // the redundant K DMA of the last iterations has landed before the workgroup ends
+
+  attn_half_fwd_epilogue<T, K, DB>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, g);
 }
 
 template <typename T, int K, int D>
@@ -819,13 +1130,19 @@ static int launch_attention_half_kd(const AttnArgs& a) {
                         head_bytes < (int64_t{1} << 31);
       if (pipe) {
         const dim3 grid(static_cast<unsigned>((a.lq + kAttnBM - 1) / kAttnBM * a.bh));
-#define PT_HALF_PIPE(ADDV)                                                                                     \
-  taylor_attention_fwd_half_pipe_kernel<T, K, D, ADDV><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(      \
+#define PT_HALF_PIPE(KERNEL, ADDV)                                                                             \
+  KERNEL<T, K, D, ADDV><<<grid, dim3(kAttnWaves * kWave), 0, a.stream>>>(                                      \
       q, k, v, o, lse, static_cast<int>(a.lq), static_cast<int>(a.lk), a.mask, a.mask_map, a.mask_ranges, madd, \
       a.causal ? 1 : 0, static_cast<float>(a.scale))
-        if (madd != nullptr) PT_HALF_PIPE(2);
-        else if (a.mask != nullptr) PT_HALF_PIPE(1);
-        else PT_HALF_PIPE(0);
+        if constexpr (AttnHalfSw<K, D>::fits) {
+          if (madd != nullptr) PT_HALF_PIPE(taylor_attention_fwd_half_sw_kernel, 2);
+          else if (a.mask != nullptr) PT_HALF_PIPE(taylor_attention_fwd_half_sw_kernel, 1);
+          else PT_HALF_PIPE(taylor_attention_fwd_half_sw_kernel, 0);
+        } else {
+          if (madd != nullptr) PT_HALF_PIPE(taylor_attention_fwd_half_pipe_kernel, 2);
+          else if (a.mask != nullptr) PT_HALF_PIPE(taylor_attention_fwd_half_pipe_kernel, 1);
+          else PT_HALF_PIPE(taylor_attention_fwd_half_pipe_kernel, 0);
+        }
 #undef PT_HALF_PIPE
         PT_LAUNCH_CHECK();
         return PT_OK;
