@@ -185,6 +185,36 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Max and sum over the four 16-lane rows of a wave, for each lane position within a row: the
+// exchanges of __shfl_xor by 16 and by 32 without their LDS round trips. v_permlane16_swap(x, x)
+// yields rows (x0, x0, x2, x2) and (x1, x1, x3, x3), v_permlane32_swap(y, y) halves (lo, lo) and
+// (hi, hi) (both checked on gfx950 with a lane-layout probe). Every lane ends with the same bits,
+// those of the __shfl_xor form. Other types take that form.
+template <typename A>
+__device__ __forceinline__ A rows_max(A x) {
+  if constexpr (sizeof(A) == 4) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  } else {
+    x = fmax(x, __shfl_xor(x, 16, kWave));
+    return fmax(x, __shfl_xor(x, 32, kWave));
+  }
+}
+template <typename A>
+__device__ __forceinline__ A rows_sum(A x) {
+  if constexpr (sizeof(A) == 4) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  } else {
+    x += __shfl_xor(x, 16, kWave);
+    return x + __shfl_xor(x, 32, kWave);
+  }
+}
+
 template <typename A>
 __device__ __forceinline__ A wave_max(A x) {
 #pragma unroll

@@ -300,8 +300,7 @@ __device__ __forceinline__ void attention_epilogue(AccT (&acc_o)[K + 1][NB],
   static_assert(E == 1 || NB == D / 16, "interleaved accumulators span the whole head dim");
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
-    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+    lsum[o] = rows_sum(lsum[o]);
   }
   if (!q_ok) return;
   const bool empty = !(lsum[0] > A(0));
@@ -589,8 +588,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
       s0[r] = ok ? s : kNegInf;
     }
     A bmax = fmax(fmax(s0[0], s0[1]), fmax(s0[2], s0[3]));
-    bmax = fmax(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmax(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = rows_max(bmax);
     const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
     if (__any(raise)) {
       const A m_new = raise ? bmax : m_used;
@@ -656,8 +654,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_kerne
     // unnormalised output series N_k, all relative to exp(-m_used)
 #pragma unroll
     for (int o = 0; o <= K; ++o) {
-      lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-      lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+      lsum[o] = rows_sum(lsum[o]);
     }
     if (!q_ok) return;
     const int64_t rows = bh * L, row = head * L + my_q;
@@ -1013,8 +1010,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_pipe_
     A bmax = kNegInf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, valid[r] ? sc[0][r] * scale : kNegInf);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = rows_max(bmax);
     const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
     // a row whose shift is still -inf has accumulated nothing: raising it rescales nothing
     if (__any(raise && m_used != kNegInf)) {

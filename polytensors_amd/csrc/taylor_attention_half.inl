@@ -268,8 +268,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         s0[kh][r] = ok ? sv : kNegInf;
         bmax = fmaxf(bmax, s0[kh][r]);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = rows_max(bmax);
     const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
     if (__any(raise)) {
       const float m_new = raise ? bmax : m_used;
@@ -348,8 +347,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   // ---- epilogue: row sums over the lane groups, series quotient, output and lse series ----
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
-    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+    lsum[o] = rows_sum(lsum[o]);
   }
   if (!q_ok) return;
   const bool empty = !(lsum[0] > 0.f);
@@ -470,8 +468,7 @@ __device__ __forceinline__ void attn_half_fwd_epilogue(floatx4 (&acc_o)[K + 1][D
   constexpr int D = 16 * DB;
 #pragma unroll
   for (int o = 0; o <= K; ++o) {
-    lsum[o] += __shfl_xor(lsum[o], 16, kWave);
-    lsum[o] += __shfl_xor(lsum[o], 32, kWave);
+    lsum[o] = rows_sum(lsum[o]);
   }
   if (!q_ok) return;
   const bool empty = !(lsum[0] > 0.f);
@@ -698,8 +695,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         s0[kh][r] = ok ? sv : kNegInf;
         bmax = fmaxf(bmax, s0[kh][r]);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = rows_max(bmax);
     const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
     if (__any(raise)) {
       const float m_new = raise ? bmax : m_used;
@@ -1018,8 +1014,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         s0[kh][r] = ok ? sv : kNegInf;
         bmax = fmaxf(bmax, s0[kh][r]);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = rows_max(bmax);
     const bool raise = bmax > m_used + kSlack || (m_used == kNegInf && bmax != kNegInf);
     if (__any(raise)) {
       const float m_new = raise ? bmax : m_used;
