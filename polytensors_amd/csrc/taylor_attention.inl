@@ -282,6 +282,41 @@ __device__ __forceinline__ A attn_mask_add(const A* madd, int row, int col, int 
   return madd[static_cast<int64_t>(min(row, L - 1)) * S + min(col, S - 1)];
 }
 
+// The mask bytes of keys k0 .. k0+3 of row `row` (k0 a multiple of 4) as one word, byte r for key
+// k0 + r, and with ADD their additive values. Where vec holds (attn_mask_vec: S a multiple of 4,
+// the mask 4-byte and the values 16-byte aligned) that is one 4-byte and one 16-byte load: k0 < S
+// then implies k0 + 3 < S, and a group at or past S reads the row's last four keys, whose values
+// are never used (those keys fail key < hi). Otherwise byte by byte, indices clamped as
+// attn_mask_byte's.
+template <bool ADD>
+__device__ __forceinline__ uint32_t attn_mask_word4(const uint8_t* mask, const float* madd, int row, int k0, int L,
+                                                    int S, bool vec, float (&add)[4]) {
+  const int64_t at = static_cast<int64_t>(min(row, L - 1)) * S;
+  if (vec) {
+    const int kc = min(k0, S - 4);
+    if constexpr (ADD) {
+      const float4 v = *reinterpret_cast<const float4*>(madd + at + kc);
+      add[0] = v.x;
+      add[1] = v.y;
+      add[2] = v.z;
+      add[3] = v.w;
+    }
+    return *reinterpret_cast<const uint32_t*>(mask + at + kc);
+  }
+  uint32_t w = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t e = at + min(k0 + r, S - 1);
+    w |= static_cast<uint32_t>(mask[e]) << (8 * r);
+    if constexpr (ADD) add[r] = madd[e];
+  }
+  return w;
+}
+__device__ __forceinline__ bool attn_mask_vec(const uint8_t* mask, const float* madd, int S) {
+  return mask != nullptr && S % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) & 3) == 0 &&
+         (madd == nullptr || (reinterpret_cast<uintptr_t>(madd) & 15) == 0);
+}
+
 // E is the head-dim interleave of the output accumulators: accumulator
 // g*E + e, register r of lane group h holds column g*16E + E*(4h + r) + e
 // (E = 1: the plain 16x16 layout, column 16 db + acc_row(h, r)).

@@ -500,18 +500,16 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   // (In the stored-tile launches. The recomputing ones, which hold more registers, read them at
   // the top of their block: ahead, their registers made some instantiations spill.)
   constexpr bool kAhead = MASK != 0 && STORE;
-  uint8_t mnext[MASK != 0 ? 2 : 1][4];
+  // (one word of mask bytes per half: byte r for key kb0 + 16 kh + 4 g + r)
+  uint32_t mnext[2] = {0u, 0u};
   float anext[MASK == 2 ? 2 : 1][4];
+  const bool mvec = MASK != 0 && attn_mask_vec(mask, madd, S);
   auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
     if constexpr (MASK != 0) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kb0 + 16 * kh + 4 * g + r;
-          mnext[kh][r] = attn_mask_byte(mask, Q.p[0], my_q, key, L, S);
-          if constexpr (MASK == 2) anext[kh][r] = attn_mask_add(madd, my_q, key, L, S);
-        }
+        mnext[kh] = attn_mask_word4<MASK == 2>(mask, madd, my_q, kb0 + 16 * kh + 4 * g, L, S, mvec,
+                                               anext[MASK == 2 ? kh : 0]);
     }
   };
 
@@ -552,15 +550,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
       __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs of block j have landed (and the mask values)
     }
     __syncthreads();                 // ... and every wave's; block j-1 is done with nxt
-    uint8_t mbyte[2][4];
+    const uint32_t mword[2] = {mnext[0], mnext[1]};
     float add[2][4];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        mbyte[kh][r] = MASK != 0 ? mnext[kh][r] : uint8_t(1);
-        add[kh][r] = MASK == 2 ? anext[kh][r] : 0.f;
-      }
+      for (int r = 0; r < 4; ++r) add[kh][r] = MASK == 2 ? anext[kh][r] : 0.f;
     if constexpr (kAhead) fetch_mask(next_kb0);   // the next block's, ahead of its DMA
 #pragma unroll
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
@@ -612,7 +607,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
         const int key = kb0 + 16 * kh + 4 * g + r;
         bool ok = q_ok && key < hi;
         if (causal) ok = ok && key <= my_q;
-        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        if constexpr (MASK != 0) ok = ok && ((mword[kh] >> (8 * r)) & 0xffu) != 0;
         float p[K + 1], ds[K + 1];
         attn_prob_series<float, K>(sc, r, lse, ok, scale, add[kh][r], p);
         attn_ds_series<float, K>(p, dp, r, delta, ds);

@@ -596,20 +596,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   // The mask bytes (and additive values) of a block are read one block ahead, before that
   // block's DMA is issued: loads complete in order, so a read issued at the top of its own block
   // would hold the block for a full memory round trip (the additive values come from L2 or HBM).
-  uint8_t mnext[MASK ? 2 : 1][4];
+  // (one word of mask bytes per half: byte r for key kb0 + 16 kh + 4 g + r)
+  uint32_t mnext[2] = {0u, 0u};
   float anext[ADD ? 2 : 1][4];
+  const bool mvec = MASK != 0 && attn_mask_vec(mask, madd, S);
   auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
     if constexpr (MASK != 0) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mnext[kh][r] = mask[static_cast<int64_t>(min(my_q, L - 1)) * S + min(kb0 + 16 * kh + 4 * g + r, S - 1)];
-    }
-    if constexpr (ADD) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) anext[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+        mnext[kh] = attn_mask_word4<ADD>(mask, madd, my_q, kb0 + 16 * kh + 4 * g, L, S, mvec, anext[ADD ? kh : 0]);
     }
   };
 
@@ -622,16 +617,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     const int kb0 = lo + j * KB;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA of block j has landed (and its mask reads)
     __syncthreads();                 // ... and every wave's; block j-1's buffer is free
-    uint8_t mbyte[MASK ? 2 : 1][4];
+    const uint32_t mword[2] = {mnext[0], mnext[1]};
     float add[ADD ? 2 : 1][4];   // additive mask values of the same keys
-    if constexpr (MASK != 0) {
+    if constexpr (ADD) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          mbyte[kh][r] = mnext[kh][r];
-          if constexpr (ADD) add[kh][r] = anext[kh][r];
-        }
+        for (int r = 0; r < 4; ++r) add[kh][r] = anext[kh][r];
     }
     fetch_mask(min(kb0 + KB, last_kb0));   // the next block's, ahead of its DMA
     const int next_kb0 = min(kb0 + KB, last_kb0);
@@ -688,7 +680,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         const int key = kb0 + 16 * kh + 4 * g + r;
         bool ok = q_ok && key < hi;
         if (causal) ok = ok && key <= my_q;
-        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        if constexpr (MASK != 0) ok = ok && ((mword[kh] >> (8 * r)) & 0xffu) != 0;
         valid[kh][r] = ok;
         float sv = sc[kh][0][r] * scale;
         if constexpr (ADD) sv += add[kh][r];
@@ -884,20 +876,15 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 #pragma unroll
   for (int o = 0; o <= K; ++o) lsum[o] = 0.f;
 
-  uint8_t mnext[MASK ? 2 : 1][4];
+  // (one word of mask bytes per half: byte r for key kb0 + 16 kh + 4 g + r)
+  uint32_t mnext[2] = {0u, 0u};
   float anext[ADD ? 2 : 1][4];
+  const bool mvec = MASK != 0 && attn_mask_vec(mask, madd, S);
   auto fetch_mask = [&](int kb0) __attribute__((always_inline)) {
     if constexpr (MASK != 0) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mnext[kh][r] = mask[static_cast<int64_t>(min(my_q, L - 1)) * S + min(kb0 + 16 * kh + 4 * g + r, S - 1)];
-    }
-    if constexpr (ADD) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) anext[kh][r] = attn_mask_add(madd, my_q, kb0 + 16 * kh + 4 * g + r, L, S);
+        mnext[kh] = attn_mask_word4<ADD>(mask, madd, my_q, kb0 + 16 * kh + 4 * g, L, S, mvec, anext[ADD ? kh : 0]);
     }
   };
 
@@ -983,16 +970,13 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     const int kb0 = lo + j * KB;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's K(j+1), V(j) and mask values of block j have landed
     __syncthreads();                 // ... every wave's; K(j) and V(j-1) are no longer read
-    uint8_t mbyte[MASK ? 2 : 1][4];
+    const uint32_t mword[2] = {mnext[0], mnext[1]};
     float add[ADD ? 2 : 1][4];
-    if constexpr (MASK != 0) {
+    if constexpr (ADD) {
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          mbyte[kh][r] = mnext[kh][r];
-          if constexpr (ADD) add[kh][r] = anext[kh][r];
-        }
+        for (int r = 0; r < 4; ++r) add[kh][r] = anext[kh][r];
     }
     if constexpr (!LAST) fetch_mask(kb_of(j + 1));
 
@@ -1007,7 +991,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
         const int key = kb0 + 16 * kh + 4 * g + r;
         bool ok = q_ok && key < hi;
         if (causal) ok = ok && key <= my_q;
-        if constexpr (MASK != 0) ok = ok && mbyte[kh][r] != 0;
+        if constexpr (MASK != 0) ok = ok && ((mword[kh] >> (8 * r)) & 0xffu) != 0;
         valid[kh][r] = ok;
         float sv = scc[kh][0][r] * scale;
         if constexpr (ADD) sv += add[kh][r];
