@@ -787,8 +787,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   attn_half_fwd_epilogue<T, K, DB>(acc_o, lsum, m_used, O, LSE, head, L, my_q, q_ok, g);
 }
 
-// Software-pipelined form of the kernel above for degrees 0..4 (one probability operand per
-// order). Iteration j forms key block j+1's scores and, between those products, runs block j's
+// Software-pipelined form of the kernel above for degrees 3..4 at head dim 128 (one probability
+// operand per order). Iteration j forms key block j+1's scores and, between those products, runs block j's
 // exponential series (VALU work that issues while the MFMAs execute), then block j's value
 // products. The series of a block is cut into units, one order of one row each, spread evenly
 // over the next block's score items.
@@ -805,9 +805,12 @@ __device__ __forceinline__ void attn_static_for(F&& f) {
   }
 }
 
+// Used at head dim 128 from degree 3, where both kernels run one wave per SIMD. Elsewhere it
+// measured slower: at d 64, K 4 its 263 registers cost the pipelined kernel's second wave per
+// SIMD (0.54 against 0.38 ms at config 3's other sizes); at d 128, K 1..2 it was 1% slower.
 template <int K, int D>
 struct AttnHalfSw {
-  static constexpr bool fits = AttnHalfPipe<K, D>::fits && !AttnHalfPipe<K, D>::split;
+  static constexpr bool fits = AttnHalfPipe<K, D>::fits && !AttnHalfPipe<K, D>::split && D == 128 && K >= 3;
   static constexpr int R = 6;   // operand rings: reads run five items ahead (four: 1% slower at K=4, d=128)
 };
 
