@@ -87,7 +87,9 @@ def why_ineligible(query, key, value, attn_mask, dropout_p, is_causal, enable_gq
     if attn_mask is not None and attn_mask.requires_grad and torch.is_grad_enabled():
         return "a mask that requires grad is not supported (no gradient flows to attn_mask)"
     grads = _needs_grad(*tensors)
-    reason = _gate.common_reason(tensors, allow_plain_grad=grads, complex_ok=True)
+    # (degrees above the kernels' are composed from series operations, to the elementwise limit)
+    reason = _gate.common_reason(tensors, allow_plain_grad=grads, complex_ok=True,
+                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     if grads and any(not isinstance(x, PolyTensor) and x.requires_grad for x in tensors):
@@ -190,12 +192,46 @@ def attention(query, key, value, attn_mask=None, is_causal=False, scale=None):
     return attention_checked(query, key, value, attn_mask, is_causal, scale)
 
 
+def _masked(scores, excluded):
+    """A masked score is (-inf, 0, ..., 0): masked_fill of the lifted -inf
+    (/root/reference/src/polytensors/_range_ops.py:271-277 with _plain.py:70-75)."""
+    return PolyTensor(tuple(torch.where(excluded, torch.full((), float("-inf") if k == 0 else 0.0, dtype=c.dtype,
+                                                             device=c.device), c)
+                            for k, c in enumerate(scores.coeffs)))
+
+
+def _composed(query, key, value, attn_mask, is_causal, scale):
+    """Degrees 9..16, above the attention kernels' register plans.
+
+    The reference's decomposition (/root/reference/src/polytensors/_decompositions.py:28-43) in
+    series operations: the score and value products run the Cauchy matmul (above its degree 8 in
+    blocks of orders); the softmax (/root/reference/src/polytensors/_plain.py:262-273) runs the
+    elementwise series kernels (exp, and the quotient by the row sums) on the scores less the row
+    maximum of their constant order, which changes only that order. A masked score is
+    (-inf, 0, ..., 0) and a float mask adds to the constant order. A row without an admissible key
+    is NaN, as in the reference's general rule.
+    """
+    L, S = query.shape[-2], key.shape[-2]
+    scores = (query * scale) @ key.transpose(-2, -1)
+    if is_causal:
+        keep = torch.ones(L, S, dtype=torch.bool, device=scores.coeffs[0].device).tril()
+        scores = _masked(scores, ~keep)
+    if attn_mask is not None:
+        scores = _masked(scores, ~attn_mask) if attn_mask.dtype == torch.bool else scores + attn_mask
+    top = scores.coeffs[0].detach().amax(-1, keepdim=True)
+    e = (scores - top).exp()
+    return (e / e.sum(-1, keepdim=True)) @ value
+
+
 def attention_checked(query, key, value, attn_mask=None, is_causal=False, scale=None):
     """``attention`` for a call whose eligibility (including dropout and GQA) the caller checked."""
     if _complex.has_complex(query, key, value):
         return _complex.at_real_nodes(attention, "scaled_dot_product_attention", query, key, value,
                                       attn_mask=attn_mask, is_causal=is_causal, scale=scale)
     degree = next(x.degree for x in (query, key, value) if isinstance(x, PolyTensor))
+    if degree > _gate.MAX_DEGREE:
+        scale = default_scale(query.shape[-1]) if scale is None else scale
+        return _composed(query, key, value, attn_mask, is_causal, scale)
     L, S = query.shape[-2], key.shape[-2]
     if is_causal and attn_mask is not None:
         # both: the causal rule applied to the mask (the general rule masks the scores with each,

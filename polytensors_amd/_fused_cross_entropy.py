@@ -31,7 +31,9 @@ def why_ineligible(input, target, weight=None, reduction="mean", label_smoothing
         return "logits must be a PolyTensor"
     if isinstance(weight, torch.Tensor) and weight.requires_grad and torch.is_grad_enabled():
         return "class weights that require grad are not supported (no gradient flows to weight)"
-    reason = _gate.common_reason((input,), allow_plain_grad=allow_grad, complex_ok=True)
+    # (degrees above the kernel's are composed from series operations, to the elementwise limit)
+    reason = _gate.common_reason((input,), allow_plain_grad=allow_grad, complex_ok=True,
+                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     if input.ndim < 2:
@@ -137,8 +139,11 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None, weig
         return flat.reshape(target.shape) if reduction == "none" else flat
     if weight is not None or label_smoothing != 0.0:
         return _weighted(input, target, ignore_index, reduction, weight, label_smoothing)
-    if _gate.wrapper_grad(input):
-        losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
+    if input.degree > _gate.MAX_DEGREE or _gate.wrapper_grad(input):
+        if input.degree > _gate.MAX_DEGREE:
+            losses = _composed_losses(input, target, ignore_index, softcap)
+        else:
+            losses = _SeriesCrossEntropy.apply(input, target, ignore_index, softcap)
         if reduction == "none":
             return losses
         total = losses.sum()
@@ -150,6 +155,27 @@ def fused(input, target, ignore_index=-100, reduction="mean", softcap=None, weig
     loss, _ = _ops.cross_entropy_series(z, target.contiguous(), int(ignore_index), _lib.REDUCTIONS[reduction],
                                         float(softcap) if softcap is not None else 0.0)
     return PolyTensor.from_stacked(loss)
+
+
+def _composed_losses(input, target, ignore_index, softcap):
+    """Per-row loss series lse - z_y (zero for ignored rows) of (N, C) logits at degrees 9..16,
+    above the row kernel's register plan.
+
+    torch's cross_entropy as the reference's general rules decompose it (log-sum-exp and a gather,
+    /root/reference/src/polytensors/_fused_cross_entropy.py:142 and _plain.py:262-273) in series
+    operations: exp and log run the elementwise series kernels on the logits less the row maximum
+    of their constant order (which changes only that order), the row sums and the gather act on
+    each coefficient. The loss dtype is the kernel's: float32, or float64 for float64 logits.
+    """
+    dtype = torch.float64 if input.dtype == torch.float64 else torch.float32
+    z = input if input.dtype == dtype else input.to(dtype)
+    if softcap is not None:
+        z = (z / softcap).tanh() * softcap
+    top = z.coeffs[0].detach().amax(1, keepdim=True)
+    lse = (z - top).exp().sum(1).log() + top.squeeze(1)
+    keep = target != ignore_index
+    safe = torch.where(keep, target, torch.zeros((), dtype=target.dtype, device=target.device))
+    return (lse - z.gather(1, safe[:, None]).squeeze(1)) * keep.to(dtype)
 
 
 def _weighted(input, target, ignore_index, reduction, weight, label_smoothing):

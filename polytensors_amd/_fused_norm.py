@@ -1,4 +1,4 @@
-"""Fused RMSNorm / LayerNorm series (any degree up to 8) on gfx950.
+"""Fused RMSNorm / LayerNorm series (degrees up to 8 in one kernel, 9..16 composed) on gfx950.
 
 ``rms_norm`` mirrors /root/reference/src/polytensors/_fused_norm.py:63-69: the
 normalisation runs in one kernel pass and ``eps`` defaults to
@@ -102,8 +102,31 @@ def _from_stacked(stacked):
     return PolyTensor.from_stacked(stacked)
 
 
+def _composed(input, shape, weight, bias, eps, layer):
+    """Degrees 9..16, above the row kernel's register plan (K+1 <= 9 accumulator sets).
+
+    The reference's decomposition of the norm (/root/reference/src/polytensors/
+    _decompositions.py:14-22): ``x * rsqrt(mean(x*x) + eps)``, layer_norm centring x first,
+    in series operations: the products and rsqrt run the elementwise series kernels (to degree
+    16) and the means act on each coefficient.
+    """
+    dims = tuple(range(-len(shape), 0))
+    x = input
+    if layer:
+        x = x - x.mean(dim=dims, keepdim=True)
+    y = x * ((x * x).mean(dim=dims, keepdim=True) + eps).rsqrt()
+    if weight is not None:
+        y = y * weight
+    if layer and bias is not None:
+        y = y + bias
+    return y
+
+
 def _run(input, normalized_shape, weight, bias, eps, layer):
     shape = tuple(normalized_shape)
+    degree = max((x.degree for x in (input, weight, bias) if isinstance(x, PolyTensor)), default=0)
+    if _gate.MAX_DEGREE < degree <= _gate.MAX_ELEMENTWISE_DEGREE and isinstance(input, PolyTensor):
+        return _composed(input, shape, weight, bias, eps, layer)
     grads = _needs_grad(input, weight, bias)
     reason = why_ineligible(input, shape, weight, bias, allow_grad=grads)
     if reason is not None:

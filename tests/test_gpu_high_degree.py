@@ -18,7 +18,9 @@ orders. The checks:
   against the oracle's Cauchy sums (1e-10 float64, 1e-4 float32, 2e-2 bfloat16);
 * gradients of the new functions: reverse mode through sin/cos/sqrt/rsqrt
   against jets of torch.func.grad, and their second-order coefficient autograd;
-* the row and MFMA kernels (norm, cross entropy, attention) refuse degree 9.
+* above degree 8 the norms, cross entropy and attention are composed from series operations
+  (the reference's decompositions); at degree 12 they match the oracle's restatements at
+  1e-10 in float64, and degree 17 is refused.
 """
 
 import math
@@ -225,9 +227,96 @@ def test_second_order_coefficient_autograd_of_the_new_functions(kind):
     assert rel_err(got.cpu(), want) <= 1e-10
 
 
-def test_row_and_mfma_kernels_refuse_degree_nine():
-    x = PolyTensor(tuple(torch.randn(4, 16, dtype=torch.float64, device="cuda") for _ in range(10)))
-    q = PolyTensor(tuple(torch.randn(1, 1, 8, 16, dtype=torch.float64, device="cuda") for _ in range(10)))
+def _poly(coeffs):
+    return PolyTensor(tuple(c.cuda() for c in coeffs))
+
+
+def _check(out, want, what):
+    got = out.coeffs if isinstance(out, PolyTensor) else (out,)
+    assert len(got) == len(want), what
+    for k, (g, w) in enumerate(zip(got, want)):
+        assert rel_err(g.cpu(), w) <= 1e-10, f"{what}: order {k}"
+
+
+def test_norms_compose_above_degree_eight():
+    degree = 12
+    X = _dense((6, 40), degree, 901)
+    W, B = _dense((40,), degree, 902), _dense((40,), degree, 903)
+    W[0] = W[0] + 2.0
+    with torch.no_grad(), PolyTensor.plain_range():
+        rms = F.rms_norm(_poly(X), (40,), _poly(W), eps=1e-6)
+        layer = F.layer_norm(_poly(X), (40,), _poly(W), _poly(B), eps=1e-5)
+        plain_w = F.rms_norm(_poly(X), (40,), W[0].cuda())
+    assert rms.degree == layer.degree == degree
+    _check(rms, oracle.rms_norm(X, (40,), W, eps=1e-6), "rms_norm")
+    _check(layer, oracle.layer_norm(X, (40,), W, B, eps=1e-5), "layer_norm")
+    _check(plain_w, oracle.rms_norm(X, (40,), [W[0]]), "rms_norm, ordinary weight")
+
+
+@pytest.mark.parametrize("layer", (False, True))
+def test_reverse_mode_through_the_composed_norms(layer):
+    # the composed norm is recorded by autograd as its series operations; the gradient series for
+    # the cotangent (R, 0, ..., 0) of a plain-weighted sum is the oracle's
+    degree = 10
+    X = _dense((5, 24), degree, 930)
+    R = torch.randn(5, 24, generator=torch.Generator().manual_seed(931), dtype=torch.float64)
+    x = PolyTensor(tuple(c.cuda() for c in X), requires_grad=True)
+    with PolyTensor.plain_range(), PolyTensor.retain_wrappers():
+        out = F.layer_norm(x, (24,), eps=1e-5) if layer else F.rms_norm(x, (24,), eps=1e-6)
+        (out * R.cuda()).sum().backward()
+    G = [R] + [torch.zeros_like(R) for _ in range(degree)]
+    want = (oracle.layer_norm_backward(X, G, (24,), eps=1e-5) if layer else
+            oracle.rms_norm_backward(X, G, (24,), eps=1e-6))
+    _check(x.grad, want, "layer_norm gradient" if layer else "rms_norm gradient")
+
+
+@pytest.mark.parametrize("mask", ("causal", "bool", "float"))
+def test_attention_composes_above_degree_eight(mask):
+    degree = 12
+    Q, K, V = (_dense((2, 3, 24, 16), degree, 910 + i, scale=0.3) for i in range(3))
+    g = torch.Generator().manual_seed(915)
+    attn_mask, causal = None, mask == "causal"
+    if mask == "bool":
+        attn_mask = torch.rand(24, 24, generator=g) < 0.7
+        attn_mask |= torch.eye(24, dtype=torch.bool)   # every row keeps a key
+    elif mask == "float":
+        attn_mask = torch.randn(2, 1, 24, 24, generator=g, dtype=torch.float64)
+    with torch.no_grad(), PolyTensor.plain_range():
+        out = F.scaled_dot_product_attention(_poly(Q), _poly(K), _poly(V), is_causal=causal,
+                                             attn_mask=None if attn_mask is None else attn_mask.cuda())
+    assert out.degree == degree
+    _check(out, oracle.attention(Q, K, V, attn_mask=attn_mask, is_causal=causal), f"attention, {mask}")
+
+
+@pytest.mark.parametrize("case", ("mean", "none_ignored", "weighted_smoothed", "softcap"))
+def test_cross_entropy_composes_above_degree_eight(case):
+    degree = 12
+    Z = _dense((7, 33), degree, 920)
+    g = torch.Generator().manual_seed(921)
+    target = torch.randint(0, 33, (7,), generator=g)
+    kwargs, want_kwargs = {}, {}
+    if case == "none_ignored":
+        target[2] = -100
+        kwargs = want_kwargs = {"reduction": "none"}
+    elif case == "weighted_smoothed":
+        target[4] = -100
+        weight = torch.rand(33, generator=g, dtype=torch.float64) + 0.5
+        kwargs = {"weight": weight.cuda(), "label_smoothing": 0.1}
+        want_kwargs = {"weight": weight, "label_smoothing": 0.1}
+    with torch.no_grad(), PolyTensor.plain_range():
+        if case == "softcap":
+            out = PolyTensor.cross_entropy(_poly(Z), target.cuda(), softcap=5.0)
+            want = oracle.cross_entropy(Z, target, softcap=5.0)
+        else:
+            out = F.cross_entropy(_poly(Z), target.cuda(), **kwargs)
+            want = oracle.cross_entropy(Z, target, **want_kwargs)
+    assert out.degree == degree
+    _check(out, want, f"cross_entropy, {case}")
+
+
+def test_row_and_mfma_operations_refuse_degree_seventeen():
+    x = PolyTensor(tuple(torch.randn(4, 16, dtype=torch.float64, device="cuda") for _ in range(18)))
+    q = PolyTensor(tuple(torch.randn(1, 1, 8, 16, dtype=torch.float64, device="cuda") for _ in range(18)))
     y = torch.zeros(4, dtype=torch.int64, device="cuda")
     with torch.no_grad(), PolyTensor.plain_range():
         for call in (lambda: F.layer_norm(x, (16,)), lambda: F.rms_norm(x, (16,)),
