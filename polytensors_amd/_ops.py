@@ -259,8 +259,11 @@ def _(z, target, ignore_index, softcap, lse, cot):
 # of those operators, so they differentiate again (further reverse derivatives,
 # as the reference's general rules allow, /root/reference/docs/api.md:137-139).
 # The norm, cross-entropy, attention and other activation backwards are single
-# gradient-series kernels without a kernel for their own derivative: they are
-# once-differentiable and refuse a graph of the gradient (create_graph).
+# gradient-series kernels without a kernel for their own derivative. When a graph
+# of the gradient is asked for (create_graph), the norm, cross entropy and
+# attention are recomposed from series operations and differentiated
+# (``_regraded``), and tanh, sigmoid, silu and gelu_tanh form G (*) f' from series
+# products (``_series_derivative``); gelu (erf form) refuses it.
 
 def _reversed(grad):
     """Cotangents of a stacked [K+1, ...] output in reverse order, as a coefficient list."""
@@ -290,6 +293,43 @@ def _once(what):
                                   "is not implemented")
 
 
+def _regraded(inputs, cotangents, compose):
+    """A fused operation's gradient as a graph (create_graph), for further reverse derivatives.
+
+    The operation is recomputed from its saved input coefficients by ``compose`` in series
+    operations whose backwards are products of the series kernels (the compositions of the degree
+    9..16 paths, as the reference's general rules), and differentiated with create_graph: the
+    gradient is then a function of the inputs and cotangents that autograd can differentiate
+    again. ``inputs`` are lists of coefficient tensors; returns one list of gradients per list
+    (zeros where a coefficient takes no part).
+    """
+    from ._plain import _plain_range
+    from ._tensor import _coefficient_autograd_enabled
+
+    flat = [t for xs in inputs for t in xs]
+    wanted = [t for t in flat if t.requires_grad]
+    tokens = (_plain_range.set(True), _coefficient_autograd_enabled.set(True))
+    try:
+        pairs = [(y, c) for y, c in zip(compose(*inputs), cotangents) if y.requires_grad]
+        got = torch.autograd.grad([y for y, _ in pairs], wanted, [c for _, c in pairs], create_graph=True,
+                                  allow_unused=True) if wanted and pairs else [None] * len(wanted)
+    finally:
+        _coefficient_autograd_enabled.reset(tokens[1])
+        _plain_range.reset(tokens[0])
+    by_id = {id(t): g for t, g in zip(wanted, got)}
+    result = []
+    for xs in inputs:
+        result.append([by_id.get(id(t)) if by_id.get(id(t)) is not None else torch.zeros_like(t) for t in xs])
+    return result
+
+
+def _poly(coeffs, degree=None):
+    """A PolyTensor of coefficient tensors (an operand with fewer orders padded with zeros)."""
+    from ._tensor import PolyTensor
+
+    return PolyTensor(tuple(coeffs), degree=degree)
+
+
 def _norm_setup(ctx, inputs, output):
     x, weight, bias, n, eps, layer = inputs
     ctx.save_for_backward(*x)
@@ -298,12 +338,20 @@ def _norm_setup(ctx, inputs, output):
 
 
 def _norm_backward(ctx, grad):
-    _once("norm_series")
     n, eps, layer, affine = ctx.meta
     if affine:
         raise NotImplementedError("norm_series: the fused weight/bias has no coefficient gradient; under "
                                   "autograd apply them as separate series operations")
     x = list(ctx.saved_tensors)
+    if torch.is_grad_enabled():   # a graph of the gradient: the composed norm, differentiated
+        from ._fused_norm import _composed
+
+        def compose(xs):
+            y = _composed(_poly([c.reshape(-1, n) for c in xs]), (n,), None, None, eps, layer)
+            return [c.reshape(xs[0].shape) for c in y.coeffs]
+
+        (dx,) = _regraded([x], list(grad.unbind(0)), compose)
+        return _returned(ctx, dx, [], [])
     dx = norm_series_backward(x, _reversed(grad), n, eps, layer)
     return _returned(ctx, _read_back(dx, len(x)), [], [])
 
@@ -320,10 +368,22 @@ def _ce_setup(ctx, inputs, output):
 
 
 def _ce_backward(ctx, grad_loss, grad_lse):
-    _once("cross_entropy_series")
     n, ignore_index, reduction, softcap = ctx.meta
     saved = ctx.saved_tensors
     z, target, lse = list(saved[:n]), saved[n], saved[n + 1]
+    if torch.is_grad_enabled():   # a graph of the gradient: the composed loss, differentiated
+        from ._fused_cross_entropy import _composed_losses
+
+        def compose(zs):
+            losses = _composed_losses(_poly(zs), target, ignore_index, softcap or None)
+            if reduction != 0:
+                losses = losses.sum()
+                if reduction == 1:
+                    losses = losses / (target != ignore_index).sum().to(losses.dtype)
+            return [c.to(grad_loss.dtype) for c in losses.coeffs]
+
+        (dz,) = _regraded([z], list(grad_loss.unbind(0)), compose)
+        return _returned(ctx, dz)
     rows = z[0].shape[0]
     cot = grad_loss.to(lse.dtype)
     if reduction != 0:   # per-row cotangents of the sum (ignored rows have zero loss and gradient)
@@ -382,7 +442,6 @@ def _attn_setup(ctx, inputs, output):
 
 
 def _attn_backward(ctx, grad_out, grad_lse):
-    _once("taylor_attention_fwd")
     nq, nk, nv, has_mask, causal, scale, degree, mask_map = ctx.meta
     s = ctx.saved_tensors
     q, k, v = list(s[:nq]), list(s[nq:nq + nk]), list(s[nq + nk:nq + nk + nv])
@@ -390,6 +449,26 @@ def _attn_backward(ctx, grad_out, grad_lse):
     mask = s[-1] if has_mask else None
 
     shape_q, shape_k = q[0].shape, k[0].shape   # [..., L, d], [..., S, d]: flattened to [bh, T, d] here
+    if torch.is_grad_enabled():   # a graph of the gradient: the composed attention, differentiated
+        from ._fused_attention import _composed
+
+        bh = math.prod(shape_q[:-2])
+        full_mask = None
+        if mask is not None:   # the mask of every flattened head (bool or additive)
+            if mask_map is None:
+                full_mask = mask.reshape(mask.shape[-2:])
+            else:
+                div, outer, inner = mask_map
+                heads = torch.arange(bh, device=mask.device)
+                full_mask = mask[(heads // div) * outer + (heads % div) * inner]
+
+        def compose(qs, ks, vs):
+            flat = lambda xs: _poly([x.reshape(-1, *x.shape[-2:]) for x in xs], degree)   # noqa: E731
+            y = _composed(flat(qs), flat(ks), flat(vs), full_mask, causal, scale)
+            return [c.reshape(shape_q) for c in y.coeffs]
+
+        dq, dk, dv = _regraded([q, k, v], list(grad_out.unbind(0)), compose)
+        return _returned(ctx, dq, dk, dv)
 
     def full(xs):   # the backward kernels take every order; an ordinary operand has zero higher orders
         xs = [x.reshape(-1, *x.shape[-2:]) for x in xs]
@@ -419,14 +498,48 @@ def _act_setup(ctx, inputs, output):
         ctx.save_for_backward(*x)
 
 
+def _series_derivative(kind, saved):
+    """The derivative series f'(x(t)) of tanh, sigmoid, silu and gelu_tanh from series products,
+    sums and the forward kernels (so that the gradient series G (*) f' differentiates again):
+    tanh' = 1 - y^2 and sigmoid' = y - y^2 from the saved output y; silu' = s + x s (1 - s) with
+    s = sigmoid(x); gelu_tanh' = (1 + t) / 2 + x (1 - t^2) c (1 + 3 a x^2) / 2 with
+    t = tanh(c (x + a x^3)), c = sqrt(2 / pi), a = 0.044715."""
+    def mul(a, b):
+        return list(series_binary(a, b, "mul").unbind(0))
+
+    def affine(series, scale, shift):   # scale * series + shift (the shift on the constant order)
+        return [scale * c + (shift if k == 0 else 0.0) for k, c in enumerate(series)]
+
+    def add(a, b):
+        return [x + y for x, y in zip(a, b)]
+
+    if kind == "tanh":
+        return affine(mul(saved, saved), -1.0, 1.0)
+    if kind == "sigmoid":
+        return add(saved, affine(mul(saved, saved), -1.0, 0.0))
+    x = saved
+    if kind == "silu":
+        sg = list(activation_series(x, "sigmoid").unbind(0))
+        return add(sg, mul(x, mul(sg, affine(sg, -1.0, 1.0))))
+    c, a = math.sqrt(2.0 / math.pi), 0.044715
+    x2 = mul(x, x)
+    t = list(activation_series(affine(add(x, affine(mul(x2, x), a, 0.0)), c, 0.0), "tanh").unbind(0))
+    slope = mul(affine(mul(t, t), -1.0, 1.0), affine(x2, 3.0 * a * c, c))
+    return add(affine(t, 0.5, 0.5), affine(mul(x, slope), 0.5, 0.0))
+
+
 def _act_backward(ctx, grad):
     kind = ctx.kind
-    if kind not in _ACT_PRODUCT_BACKWARD:
+    # gelu (erf form) has no product form here: its derivative needs erf's own series
+    regraph = torch.is_grad_enabled() and kind in ("tanh", "sigmoid", "silu", "gelu_tanh")
+    if kind not in _ACT_PRODUCT_BACKWARD and not regraph:
         _once(f"activation_series ({kind})")
     saved = ctx.saved_tensors
     saved = list(saved[0].unbind(0)) if kind in _ACT_SAVES_OUTPUT else list(saved)
     g = _reversed(grad)
-    if kind == "exp":      # exp' = exp: the gradient series is G (*) y
+    if regraph:            # a graph of the gradient: G (*) f' in differentiable series operations
+        dx = series_binary(g, _series_derivative(kind, saved), "mul")
+    elif kind == "exp":    # exp' = exp: the gradient series is G (*) y
         dx = series_binary(g, saved, "mul")
     elif kind == "log":    # log' = 1/x: G / x
         dx = series_binary(g, saved, "div")
@@ -453,7 +566,9 @@ def _binary_setup(ctx, inputs, output):
     ctx.op = op
     ctx.n = len(a)
     ctx.n_inputs = len(inputs)
-    ctx.save_for_backward(*a, *b, *(list(output.unbind(0)) if op == "div" else []))
+    # (the quotient's output saved whole: a view of it made here would be saved without its
+    # graph, and a second derivative would treat it as a constant)
+    ctx.save_for_backward(*a, *b, *([output] if op == "div" else []))
 
 
 def _binary_backward(ctx, grad):
@@ -464,7 +579,7 @@ def _binary_backward(ctx, grad):
     if op == "mul":        # d(a b) = b da + a db
         da, db = series_binary(g, b, "mul"), series_binary(g, a, "mul")
     else:                  # d(a / b) = da / b - (a / b) db / b
-        y = list(s[2 * n:])
+        y = list(s[2 * n].unbind(0))
         da = series_binary(g, b, "div")
         db = -series_binary(list(series_binary(g, y, "mul").unbind(0)), b, "div")
     return _returned(ctx, _read_back(da, n), _read_back(db, n))

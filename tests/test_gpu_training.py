@@ -15,8 +15,12 @@ causal attention, by PolyTensor.backward and by coefficient autograd, against th
 Taylor series of torch.func.grad of the same composite along x + t (u + i w)
 (tests/jets.py:taylor_complex, polarized nested jvp; reference semantics
 /root/reference/docs/api.md:69-92), at 1e-10 in complex128. Then second-order
-coefficient autograd through the Cauchy matmul and the series product, against
-reverse AD of the explicit coefficient sums.
+coefficient autograd ("further reverse derivatives remain supported",
+/root/reference/docs/api.md:137-139): through the Cauchy matmul and the series
+product against reverse AD of the explicit coefficient sums, and through the norms,
+cross entropy, attention and tanh/sigmoid/silu/gelu_tanh against reverse AD of
+plain-torch jets (tests/jets.py:taylor), at 1e-10 in float64; gelu's erf form
+refuses it.
 """
 
 import math
@@ -26,7 +30,7 @@ import torch
 import torch.nn.functional as F
 
 from polytensors_amd import PolyTensor
-from tests.jets import rel_err, taylor_complex
+from tests.jets import rel_err, taylor, taylor_complex
 
 pytestmark = pytest.mark.gpu
 
@@ -271,10 +275,108 @@ def test_second_order_coefficient_autograd_through_matmul_and_product():
     assert rel_err(got.cpu(), want) <= 1e-10
 
 
-def test_second_order_through_a_once_differentiable_kernel_is_refused():
+def _second_order(fn, series_fn, X, degree, wrt=(0, 0)):
+    """d/dX_b of |d coefficient_degree / dX_a|^2 (a, b = wrt): plain-torch jets of ``fn`` on the CPU
+    against coefficient autograd through ``series_fn`` on a PolyTensor of X."""
+    a, b = wrt
+
+    def explicit(xs):
+        return taylor(fn, [xs], degree)[degree].sum()
+
+    leaves = [c.clone().requires_grad_() for c in X]
+    first = torch.autograd.grad(explicit(leaves), leaves[a], create_graph=True)[0]
+    want = torch.autograd.grad((first * first).sum(), leaves[b])[0]
+    cl = [c.to(DEV).requires_grad_() for c in X]
+    with PolyTensor.plain_range(), PolyTensor.coefficient_autograd():
+        out = series_fn(PolyTensor(tuple(cl)))
+    first = torch.autograd.grad(out.coeffs[degree].sum(), cl[a], create_graph=True)[0]
+    got = torch.autograd.grad((first * first).sum(), cl[b])[0]
+    assert rel_err(got.cpu(), want) <= 1e-10
+
+
+def test_second_order_coefficient_autograd_through_the_quotient():
+    # the quotient's backward reads its saved output, which must keep its graph: saved as a view
+    # made in the autograd setup, it entered a second derivative as a constant
+    degree = 2
+    X = _series_input((3, 6), degree, 37)
+    R = torch.randn(3, 6, generator=torch.Generator().manual_seed(38), dtype=torch.float64)
+
+    def f(x, r):
+        e = x.exp()
+        return e / e.sum(-1, keepdim=True) * r
+
+    _second_order(lambda x: f(x, R), lambda x: f(x, R.to(DEV)), X, degree)
+    _second_order(lambda x: 1.0 / (x * x + 1.0) * R, lambda x: 1.0 / (x * x + 1.0) * R.to(DEV), X, degree)
+
+
+def _series_input(shape, degree, seed, scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(shape, generator=g, dtype=torch.float64) * scale ** k for k in range(degree + 1)]
+
+
+@pytest.mark.parametrize("layer", (False, True))
+def test_second_order_coefficient_autograd_through_the_norms(layer):
+    # the fused kernel's gradient is a kernel without its own derivative; asked for a graph of it,
+    # the norm is recomposed from series operations and differentiated. The CPU side is the
+    # norms' definition in plain operations (torch's nested jvp of native_layer_norm gives a
+    # wrong second coefficient: the sum of a layer norm's outputs came out -1.84, not 0), weighted
+    # by R (a layer norm's plain sum vanishes)
+    degree = 2
+    X = _series_input((3, 8), degree, 31)
+    R = torch.randn(3, 8, generator=torch.Generator().manual_seed(36), dtype=torch.float64)
+
+    def plain(x):
+        if layer:
+            x = x - x.mean(-1, keepdim=True)
+            return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-5) * R
+        return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6) * R
+
+    def series(x):
+        y = F.layer_norm(x, (8,), eps=1e-5) if layer else F.rms_norm(x, (8,), eps=1e-6)
+        return y * R.to(DEV)
+
+    _second_order(plain, series, X, degree)
+    _second_order(plain, series, X, degree, wrt=(1, 0))
+
+
+def test_second_order_coefficient_autograd_through_cross_entropy():
+    degree = 2
+    Z = _series_input((5, 7), degree, 32)
+    y = torch.tensor([0, 3, 6, 2, 3])
+    _second_order(lambda z: F.cross_entropy(z, y), lambda z: F.cross_entropy(z, y.to(DEV)), Z, degree)
+
+
+@pytest.mark.parametrize("causal", (False, True))
+def test_second_order_coefficient_autograd_through_attention(causal):
+    degree = 2
+    Q = _series_input((1, 2, 6, 16), degree, 33)
+    g = torch.Generator().manual_seed(34)
+    Kp, Vp = (torch.randn(1, 2, 6, 16, generator=g, dtype=torch.float64) for _ in range(2))
+    keep = torch.ones(6, 6, dtype=torch.bool).tril() if causal else torch.ones(6, 6, dtype=torch.bool)
+
+    def plain(q):   # (torch's CPU attention has no forward AD: its definition in plain operations)
+        s = (q @ Kp.transpose(-2, -1)) / math.sqrt(16)
+        return torch.softmax(s.masked_fill(~keep, float("-inf")), -1) @ Vp
+
+    _second_order(plain, lambda q: F.scaled_dot_product_attention(q, Kp.to(DEV), Vp.to(DEV), is_causal=causal),
+                  Q, degree)
+
+
+@pytest.mark.parametrize("kind", ("tanh", "sigmoid", "silu", "gelu_tanh"))
+def test_second_order_coefficient_autograd_through_activations(kind):
+    degree = 3
+    X = _series_input((4, 5), degree, 35)
+    fn = {"tanh": torch.tanh, "sigmoid": torch.sigmoid, "silu": F.silu,
+          "gelu_tanh": lambda x: F.gelu(x, approximate="tanh")}[kind]
+    _second_order(fn, fn, X, degree)
+
+
+def test_second_order_through_gelu_is_refused():
+    # gelu's erf form has no series-product derivative here
     degree = 2
     x = [torch.randn(3, 8, dtype=torch.float64, device=DEV).requires_grad_() for _ in range(degree + 1)]
     with PolyTensor.plain_range(), PolyTensor.coefficient_autograd():
-        out = F.layer_norm(PolyTensor(tuple(x)), (8,)).sum()
+        out = F.gelu(PolyTensor(tuple(x))).sum()
     with pytest.raises(NotImplementedError, match="second-order"):
         torch.autograd.grad(out.coeffs[degree], x[0], create_graph=True)
+
