@@ -262,8 +262,8 @@ def _(z, target, ignore_index, softcap, lse, cot):
 # gradient-series kernels without a kernel for their own derivative. When a graph
 # of the gradient is asked for (create_graph), the norm, cross entropy and
 # attention are recomposed from series operations and differentiated
-# (``_regraded``), and tanh, sigmoid, silu and gelu_tanh form G (*) f' from series
-# products (``_series_derivative``); gelu (erf form) refuses it.
+# (``_regraded``), and tanh, sigmoid, silu, gelu and gelu_tanh form G (*) f' from
+# series products (``_series_derivative``).
 
 def _reversed(grad):
     """Cotangents of a stacked [K+1, ...] output in reverse order, as a coefficient list."""
@@ -499,11 +499,13 @@ def _act_setup(ctx, inputs, output):
 
 
 def _series_derivative(kind, saved):
-    """The derivative series f'(x(t)) of tanh, sigmoid, silu and gelu_tanh from series products,
-    sums and the forward kernels (so that the gradient series G (*) f' differentiates again):
-    tanh' = 1 - y^2 and sigmoid' = y - y^2 from the saved output y; silu' = s + x s (1 - s) with
-    s = sigmoid(x); gelu_tanh' = (1 + t) / 2 + x (1 - t^2) c (1 + 3 a x^2) / 2 with
-    t = tanh(c (x + a x^3)), c = sqrt(2 / pi), a = 0.044715."""
+    """The derivative series f'(x(t)) of tanh, sigmoid, silu, gelu and gelu_tanh from series
+    products, sums, the forward kernels and per-coefficient torch operations (so that the gradient
+    series G (*) f' differentiates again): tanh' = 1 - y^2 and sigmoid' = y - y^2 from the saved
+    output y; silu' = s + x s (1 - s) with s = sigmoid(x); gelu' = Phi(x) + x phi(x), the normal
+    density phi from the exp kernel and the normal distribution Phi from its ODE
+    (Phi' = phi: k Phi_k = sum_j j x_j phi_{k-j}); gelu_tanh' = (1 + t) / 2 + x (1 - t^2) c (1 + 3 a x^2) / 2
+    with t = tanh(c (x + a x^3)), c = sqrt(2 / pi), a = 0.044715."""
     def mul(a, b):
         return list(series_binary(a, b, "mul").unbind(0))
 
@@ -518,6 +520,12 @@ def _series_derivative(kind, saved):
     if kind == "sigmoid":
         return add(saved, affine(mul(saved, saved), -1.0, 0.0))
     x = saved
+    if kind == "gelu":   # Phi(x) + x phi(x), phi = exp(-x^2 / 2) / sqrt(2 pi), Phi by its ODE k Phi_k = sum j x_j phi_{k-j}
+        phi = [c / math.sqrt(2.0 * math.pi) for c in activation_series(affine(mul(x, x), -0.5, 0.0), "exp").unbind(0)]
+        cdf = [torch.special.ndtr(x[0])]
+        for k in range(1, len(x)):
+            cdf.append(sum(j * x[j] * phi[k - j] for j in range(1, k + 1)) / k)
+        return add(cdf, mul(x, phi))
     if kind == "silu":
         sg = list(activation_series(x, "sigmoid").unbind(0))
         return add(sg, mul(x, mul(sg, affine(sg, -1.0, 1.0))))
@@ -530,8 +538,7 @@ def _series_derivative(kind, saved):
 
 def _act_backward(ctx, grad):
     kind = ctx.kind
-    # gelu (erf form) has no product form here: its derivative needs erf's own series
-    regraph = torch.is_grad_enabled() and kind in ("tanh", "sigmoid", "silu", "gelu_tanh")
+    regraph = torch.is_grad_enabled() and kind in ("tanh", "sigmoid", "silu", "gelu", "gelu_tanh")
     if kind not in _ACT_PRODUCT_BACKWARD and not regraph:
         _once(f"activation_series ({kind})")
     saved = ctx.saved_tensors

@@ -18,9 +18,8 @@ Taylor series of torch.func.grad of the same composite along x + t (u + i w)
 coefficient autograd ("further reverse derivatives remain supported",
 /root/reference/docs/api.md:137-139): through the Cauchy matmul and the series
 product against reverse AD of the explicit coefficient sums, and through the norms,
-cross entropy, attention and tanh/sigmoid/silu/gelu_tanh against reverse AD of
-plain-torch jets (tests/jets.py:taylor), at 1e-10 in float64; gelu's erf form
-refuses it.
+cross entropy, attention and tanh/sigmoid/silu/gelu/gelu_tanh against reverse AD
+of plain-torch jets (tests/jets.py:taylor), at 1e-10 in float64.
 """
 
 import math
@@ -362,21 +361,11 @@ def test_second_order_coefficient_autograd_through_attention(causal):
                   Q, degree)
 
 
-@pytest.mark.parametrize("kind", ("tanh", "sigmoid", "silu", "gelu_tanh"))
+@pytest.mark.parametrize("kind", ("tanh", "sigmoid", "silu", "gelu", "gelu_tanh"))
 def test_second_order_coefficient_autograd_through_activations(kind):
     degree = 3
     X = _series_input((4, 5), degree, 35)
-    fn = {"tanh": torch.tanh, "sigmoid": torch.sigmoid, "silu": F.silu,
+    fn = {"tanh": torch.tanh, "sigmoid": torch.sigmoid, "silu": F.silu, "gelu": F.gelu,
           "gelu_tanh": lambda x: F.gelu(x, approximate="tanh")}[kind]
     _second_order(fn, fn, X, degree)
-
-
-def test_second_order_through_gelu_is_refused():
-    # gelu's erf form has no series-product derivative here
-    degree = 2
-    x = [torch.randn(3, 8, dtype=torch.float64, device=DEV).requires_grad_() for _ in range(degree + 1)]
-    with PolyTensor.plain_range(), PolyTensor.coefficient_autograd():
-        out = F.gelu(PolyTensor(tuple(x))).sum()
-    with pytest.raises(NotImplementedError, match="second-order"):
-        torch.autograd.grad(out.coeffs[degree], x[0], create_graph=True)
-
+    _second_order(fn, fn, X, degree, wrt=(2, 1))
