@@ -12,6 +12,8 @@ Inputs are made contiguous first, as the reference's fused path does (:17).
 Half and bfloat16 compute in float32, float64 in float64.
 """
 
+import math
+
 import torch
 
 from . import _complex, _gate, _ops
@@ -21,15 +23,15 @@ _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 BACKWARD_KINDS = ("gelu", "gelu_tanh", "tanh", "sigmoid", "silu")
 
 
-def why_ineligible(*operands, complex_ok=False):
+def why_ineligible(*operands, complex_ok=False, complex_base_ok=False):
     # Reached from __torch_dispatch__ only: autograd above has recorded the native
     # backward operation (gelu_backward, tanh_backward, ...), which routes here too.
     reason = _gate.common_reason(operands, below_autograd=True, complex_ok=complex_ok,
-                                 max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
+                                 complex_base_ok=complex_base_ok, max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
     if reason is not None:
         return reason
     polys = [x for x in operands if isinstance(x, PolyTensor)]
-    dtype = polys[0].dtype
+    dtype = _gate.real_dtype(polys[0].dtype)
     if dtype not in _DTYPES or any(_gate.real_dtype(c.dtype) != dtype for p in polys for c in p.coeffs):
         return "activation series need float16/bfloat16/float32/float64 in every order"
     if any(not isinstance(x, PolyTensor) and (x.dtype != dtype) for x in operands if isinstance(x, torch.Tensor)):
@@ -47,12 +49,102 @@ def _coeffs(x, degree):
     return [base] + [torch.zeros_like(base) for _ in range(degree)]
 
 
+# kinds taken with a complex constant term (gelu's erf has no complex form here)
+COMPLEX_BASE_KINDS = ("exp", "log", "sqrt", "rsqrt", "sin", "cos", "tanh", "sigmoid", "silu", "gelu_tanh")
+
+
+def _mul(a, b):
+    from ._fused_elementwise import binary
+
+    return binary(a, b, "mul")
+
+
+def _div(a, b):
+    from ._fused_elementwise import binary
+
+    return binary(a, b, "div")
+
+
+def _lin(*terms):
+    """sum of scale * series (scale a Python number, real or complex), order by order."""
+    return PolyTensor(tuple(sum(w * x.coeffs[k] for w, x in terms) for k in range(terms[0][1].degree + 1)))
+
+
+def _shift(x, value):
+    """x + value on the constant order."""
+    return PolyTensor((x.coeffs[0] + value,) + tuple(x.coeffs[1:]))
+
+
+def _complex_exp(z):
+    """exp(x + i y) = e^x (cos y + i sin y): the real kernels for exp, cos, sin and the product."""
+    x, y = _complex._split(z)
+    if y is None:
+        return activation(x, "exp")
+    ex = activation(x, "exp")
+    return _complex._join(_mul(ex, activation(y, "cos")), _mul(ex, activation(y, "sin")))
+
+
+def _complex_log(z):
+    """log z = log(x^2 + y^2) / 2 + i arg z. The argument series integrates its derivative along
+    t, (x y' - y x') / (x^2 + y^2) (real products and a quotient), from arg z_0 (torch.atan2: the
+    principal branch, as torch's complex log)."""
+    x, y = _complex._split(z)
+    if y is None:
+        return activation(x, "log")
+    degree = z.degree
+
+    def derivative(s):   # coefficient k: (k + 1) s_{k+1}; the last order has none
+        cs = s.coeffs
+        return PolyTensor(tuple((k + 1) * cs[k + 1] for k in range(degree)) + (torch.zeros_like(cs[0]),))
+
+    r2 = _lin((1.0, _mul(x, x)), (1.0, _mul(y, y)))
+    slope = _div(_lin((1.0, _mul(x, derivative(y))), (-1.0, _mul(y, derivative(x)))), r2)
+    arg = PolyTensor((torch.atan2(y.coeffs[0], x.coeffs[0]),) +
+                     tuple(slope.coeffs[k - 1] / k for k in range(1, degree + 1)))
+    return _complex._join(_lin((0.5, activation(r2, "log"))), arg)
+
+
+def _complex_reciprocal_of(z):
+    """1 / z for a complex series (the complex quotient of the real kernels)."""
+    one = PolyTensor((torch.ones_like(z.coeffs[0]),) + tuple(torch.zeros_like(c) for c in z.coeffs[1:]))
+    return _complex.complex_quotient(_div, _mul, one, z)
+
+
+def _complex_base(z, kind):
+    """``kind`` of a series with a complex constant term, in complex arithmetic over the real
+    kernels (the reference's general rules take complex arithmetic, /root/reference/docs/notes.md:74-77):
+    exp and log as above; sqrt z = exp(log z / 2), rsqrt z = exp(-log z / 2); sin and cos from
+    exp(+-i z); tanh z = 1 - 2 / (exp(2 z) + 1); sigmoid z = 1 / (1 + exp(-z)); silu z = z sigmoid z;
+    gelu_tanh z = z (1 + tanh(c (z + a z^3))) / 2. Principal branches, as torch's."""
+    if kind == "exp":
+        return _complex_exp(z)
+    if kind == "log":
+        return _complex_log(z)
+    if kind in ("sqrt", "rsqrt"):
+        return _complex_exp(_lin((0.5 if kind == "sqrt" else -0.5, _complex_log(z))))
+    if kind in ("sin", "cos"):
+        up, down = _complex_exp(_lin((1j, z))), _complex_exp(_lin((-1j, z)))
+        return _lin((-0.5j, up), (0.5j, down)) if kind == "sin" else _lin((0.5, up), (0.5, down))
+    if kind == "tanh":
+        return _lin((1.0, _shift(_lin((0.0, z)), 1.0)),
+                    (-2.0, _complex_reciprocal_of(_shift(_complex_exp(_lin((2.0, z))), 1.0))))
+    if kind in ("sigmoid", "silu"):
+        sg = _complex_reciprocal_of(_shift(_complex_exp(_lin((-1.0, z))), 1.0))
+        return sg if kind == "sigmoid" else _complex.complex_product(_mul, z, sg)
+    c, a = math.sqrt(2.0 / math.pi), 0.044715   # gelu_tanh
+    cube = _complex.complex_product(_mul, _complex.complex_product(_mul, z, z), z)
+    t = _complex_base(_lin((c, z), (c * a, cube)), "tanh")
+    return _lin((0.5, _complex.complex_product(_mul, z, _shift(t, 1.0))))
+
+
 def activation(x, kind):
     """Series of ``f(x)`` for ``kind`` in gelu, gelu_tanh, tanh, sigmoid, silu, exp, log, sin, cos,
     sqrt, rsqrt."""
-    reason = why_ineligible(x, complex_ok=True)
+    reason = why_ineligible(x, complex_ok=True, complex_base_ok=kind in COMPLEX_BASE_KINDS)
     if reason is not None:
         raise NotImplementedError(f"{kind}: {reason}")
+    if _complex.has_complex_base(x):
+        return _complex_base(x, kind)
     if _complex.has_complex(x):
         return _complex.at_real_nodes_below_autograd(activation, kind, x, kind)
     out = _ops.activation_series(_coeffs(x, x.degree), kind)

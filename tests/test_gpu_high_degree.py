@@ -82,6 +82,41 @@ def test_line_coefficients_match_analytic_derivatives(operation, complex_directi
             torch.testing.assert_close(result.coeffs[order].cpu(), want, rtol=2e-13, atol=1e-28)
 
 
+@pytest.mark.parametrize("degree", (1, 3, 12))
+@pytest.mark.parametrize("operation", ("exp", "log", "rsqrt", "sqrt", "sin", "cos"))
+def test_complex_base_line_coefficients_match_analytic_derivatives(operation, degree):
+    # a complex constant term (the reference's complex arithmetic, docs/notes.md:74-77): the same
+    # closed forms with complex base and direction (principal branches, as torch's)
+    base = torch.tensor([1.7 + 0.4j, 0.6 - 1.1j, -2.9 + 0.8j], dtype=torch.complex128)
+    direction = torch.tensor([0.2 + 0.3j, -0.1 + 0.05j, 0.3 - 0.2j], dtype=torch.complex128)
+    with torch.no_grad(), PolyTensor.plain_range():
+        result = getattr(torch, operation)(_line(base, direction, degree))
+    assert result.degree == degree
+    want0 = getattr(torch, operation)(base)
+    assert rel_err(result.coeffs[0].cpu(), want0) <= 1e-14
+    for order in range(1, degree + 1):
+        assert rel_err(result.coeffs[order].cpu(), _closed_form(operation, base, direction, order)) <= 1e-10, \
+            f"order {order}"
+
+
+@pytest.mark.parametrize("kind", ("tanh", "sigmoid", "silu", "gelu_tanh"))
+def test_complex_base_activations_match_jets(kind):
+    degree = 6
+    g = torch.Generator().manual_seed(960)
+    X = [torch.complex(torch.randn(4, 5, generator=g, dtype=torch.float64),
+                       torch.randn(4, 5, generator=g, dtype=torch.float64)) * 0.5 ** k for k in range(degree + 1)]
+    c, a = math.sqrt(2.0 / math.pi), 0.044715
+    plain = {"tanh": torch.tanh, "sigmoid": torch.sigmoid, "silu": lambda z: z * torch.sigmoid(z),
+             "gelu_tanh": lambda z: 0.5 * z * (1 + torch.tanh(c * (z + a * z ** 3)))}[kind]
+    series = {"tanh": torch.tanh, "sigmoid": torch.sigmoid, "silu": F.silu,
+              "gelu_tanh": lambda z: F.gelu(z, approximate="tanh")}[kind]
+    with torch.no_grad(), PolyTensor.plain_range():
+        out = series(PolyTensor(tuple(x.cuda() for x in X)))
+    want = taylor(plain, [X], degree)
+    for k in range(degree + 1):
+        assert rel_err(out.coeffs[k].cpu(), want[k]) <= 1e-10, f"{kind} order {k}"
+
+
 def test_nonlinear_input_series_round_trips():
     coefficients = tuple(torch.tensor([v, v / 2], dtype=torch.float64)
                          for v in (1.5, 0.2, -0.1, 0.03, 0.0, -0.002))
