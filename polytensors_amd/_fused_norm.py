@@ -23,8 +23,12 @@ from ._tensor import PolyTensor
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 
 
-def why_ineligible(input, normalized_shape, weight=None, bias=None, allow_grad=False):
-    reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad, complex_ok=True)
+def why_ineligible(input, normalized_shape, weight=None, bias=None, allow_grad=False,
+                   max_degree=_gate.MAX_DEGREE):
+    """Why the norm kernel cannot take this call (None if it can); ``max_degree`` the composed
+    path's limit for degrees above the kernel's."""
+    reason = _gate.common_reason((input, weight, bias), allow_plain_grad=allow_grad, complex_ok=True,
+                                 max_degree=max_degree)
     if reason is not None:
         return reason
     if not isinstance(input, torch.Tensor) or input.dtype not in _DTYPES:
@@ -125,7 +129,11 @@ def _composed(input, shape, weight, bias, eps, layer):
 def _run(input, normalized_shape, weight, bias, eps, layer):
     shape = tuple(normalized_shape)
     degree = max((x.degree for x in (input, weight, bias) if isinstance(x, PolyTensor)), default=0)
-    if _gate.MAX_DEGREE < degree <= _gate.MAX_ELEMENTWISE_DEGREE and isinstance(input, PolyTensor):
+    if degree > _gate.MAX_DEGREE and isinstance(input, PolyTensor):
+        reason = why_ineligible(input, shape, weight, bias, allow_grad=_needs_grad(input, weight, bias),
+                                max_degree=_gate.MAX_ELEMENTWISE_DEGREE)
+        if reason is not None:
+            raise NotImplementedError(f"{'layer_norm' if layer else 'rms_norm'}: {reason}")
         return _composed(input, shape, weight, bias, eps, layer)
     grads = _needs_grad(input, weight, bias)
     reason = why_ineligible(input, shape, weight, bias, allow_grad=grads)
