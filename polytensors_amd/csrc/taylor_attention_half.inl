@@ -412,6 +412,19 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 //   so when lane 4j + a of group g addresses V[4g + j][16 db + 4a ..], lane c of
 //   the group receives V[4g + j][16 db + c] for j = 0..3: four keys of its head
 //   dim, the operand slots of the value product.
+// f(integral_constant<int, I>) for I = B .. E-1 in order: indices that are constants from the
+// start, so register arrays indexed by them never go to scratch
+template <int B, int E, typename F>
+__device__ __forceinline__ void attn_static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    attn_static_for<B + 1, E>(f);
+  }
+}
+
+// Used at head dim 128 from degree 3, where both kernels run one wave per SIMD. Elsewhere it
+// measured slower: at d 64, K 4 its 263 registers cost the pipelined kernel's second wave per
+// SIMD (0.54 against 0.38 ms at config 3's other sizes); at d 128, K 1..2 it was 1% slower.
 template <int K, int D>
 struct AttnHalfPipe {
   static constexpr int KB = 32;
@@ -423,7 +436,7 @@ struct AttnHalfPipe {
   static constexpr int RSH = CH >= 16 ? 0 : CH == 8 ? 1 : CH == 4 ? 2 : 3;   // log2(16 / CH)
   static constexpr size_t LDS = 2ull * 2 * (K + 1) * KB * D * 2;
   static constexpr bool split = AttnHalfShape<K, D>::split;
-  static constexpr int R = 4;   // operand ring: reads run three items ahead
+  static constexpr int R = 4;   // the value products' operand ring: reads run three items ahead
   // registers of the accumulators, query tile, scores, probability operands (hi, lo) and ring
   static constexpr int regs =
       (K + 1) * (D / 16 * 4 + (D + 31) / 32 * 4 + 8 + 4) + 4 * R + (split ? 4 * K : 0);
@@ -629,8 +642,11 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
     const int next_kb0 = min(kb0 + KB, last_kb0);
 
     // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T, two 16-key halves ----
-    // Items t = (step, b) in order: one K_b operand (a 16-byte read) feeds the K+1-b products
-    // S_{a+b} += K_b Q_a; the operand reads run R-1 items ahead through a ring of R registers.
+    // Per step (chunk dc, half kh) the K+1 operands K_b (16-byte reads) are read one step ahead,
+    // and the products are grouped by output order, S_k's k+1 products back to back: 2-3% faster
+    // than operand by operand through a ring (K=4 at d=64 0.383 -> 0.373 ms, K=2 at d=128 0.458 ->
+    // 0.448 ms), each accumulator summing in the same order (b ascending). Item t = (step, k)
+    // carries its share of the next block's DMA.
     floatx4 sc[2][K + 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
@@ -648,26 +664,31 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       const u32x4 z = {0u, 0u, 0u, 0u};
       return din ? v : z;
     };
-    u32x4 kring[R];
+    constexpr int NS = 2 * DC;
+    u32x4 kop[2][K + 1];
 #pragma unroll
-    for (int t = 0; t < R - 1 && t < KT; ++t) kring[t] = load_k(t);   // (no item past the block)
+    for (int o = 0; o <= K; ++o) kop[0][o] = load_k(o);
+    attn_static_for<0, NS>([&](auto sc_) __attribute__((always_inline)) {
+      constexpr int st = decltype(sc_)::value;
+      constexpr int dc = st / 2, kh = st % 2;
+      if constexpr (st + 1 < NS) {
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      if (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
-      if constexpr (dma_in_scores) {
-        // evenly over the score products: issued over their first half only, the tile writes
-        // slowed the operand reads more (0.917 -> 0.943 ms at the config-3 shape)
-#pragma unroll
-        for (int i = t * OPS / KT; i < (t + 1) * OPS / KT; ++i)
-          attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, i);
+        for (int o = 0; o <= K; ++o) kop[(st + 1) & 1][o] = load_k((st + 1) * (K + 1) + o);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      const int st = t / (K + 1), bo = t % (K + 1);
-      const int dc = st / 2, kh = st % 2;
+      attn_static_for<0, K + 1>([&](auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        constexpr int t = st * (K + 1) + k;
+        if constexpr (dma_in_scores) {
+          attn_static_for<t * OPS / KT, (t + 1) * OPS / KT>([&](auto ic) __attribute__((always_inline)) {
+            attn_half_issue_op<T, K, D>(nxt, Kp, Vp, head, S, next_kb0, lane, wave, decltype(ic)::value);
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int a = 0; a + bo <= K; ++a) sc[kh][a + bo] = MM::mma(kring[t % R], qreg[a][dc], sc[kh][a + bo]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+        for (int b = 0; b <= k; ++b) sc[kh][k] = MM::mma(kop[st & 1][b], qreg[k - b][dc], sc[kh][k]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
 
     // ---- mask, online maximum of the constant order, exponential series ----
     bool valid[2][4];
@@ -795,23 +816,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 // Buffers: the K tile of block j+2 goes where block j's K tile was (read by the previous
 // iteration's scores), the V tile of block j+1 where block j-1's was; both are issued at the top of
 // iteration j and waited for at the top of iteration j+1.
-// f(integral_constant<int, I>) for I = B .. E-1 in order: indices that are constants from the
-// start, so register arrays indexed by them never go to scratch
-template <int B, int E, typename F>
-__device__ __forceinline__ void attn_static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    attn_static_for<B + 1, E>(f);
-  }
-}
-
-// Used at head dim 128 from degree 3, where both kernels run one wave per SIMD. Elsewhere it
-// measured slower: at d 64, K 4 its 263 registers cost the pipelined kernel's second wave per
-// SIMD (0.54 against 0.38 ms at config 3's other sizes); at d 128, K 1..2 it was 1% slower.
 template <int K, int D>
 struct AttnHalfSw {
   static constexpr bool fits = AttnHalfPipe<K, D>::fits && !AttnHalfPipe<K, D>::split && D == 128 && K >= 3;
-  static constexpr int R = 6;   // operand rings: reads run five items ahead (four: 1% slower at K=4, d=128)
+  static constexpr int R = 6;   // the value products' operand ring: reads run five items ahead
 };
 
 template <typename T, int K, int D, int MASK>
@@ -892,8 +900,12 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   };
 
   // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T of the block in buffer kt, two 16-key halves ----
-  // Items t = (step, b) as in the kernel above; extra(t) runs the other work of item t (DMA
-  // shares and series units) before the item's products, which execute while it issues.
+  // Per step (chunk dc, half kh) the K+1 operands K_b are read one step ahead; the products are
+  // grouped by output order, S_k's k+1 products back to back (0.843 against 0.863 ms at the
+  // config-3 shape with the reference's item order, operand by operand; the same grouping of the
+  // value products measured slower, 0.862 ms). Item t = (step, k) runs extra(t), the other work
+  // of the item (DMA shares and series units), before the order's products, which execute while it
+  // issues. Each accumulator sums its products in the same order either way (b ascending).
   constexpr int R = AttnHalfSw<K, D>::R;
   constexpr int KT = 2 * DC * (K + 1);
   auto scores = [&](Tiles& kt, floatx4 (&s)[2][K + 1], auto&& extra) __attribute__((always_inline)) {
@@ -911,19 +923,25 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       const u32x4 z = {0u, 0u, 0u, 0u};
       return din ? v : z;
     };
-    u32x4 kring[R];
+    constexpr int NS = 2 * DC;
+    u32x4 kop[2][K + 1];
 #pragma unroll
-    for (int t = 0; t < R - 1 && t < KT; ++t) kring[t] = load_k(t);   // (no item past the block)
-    attn_static_for<0, KT>([&](auto tc) __attribute__((always_inline)) {
-      constexpr int t = decltype(tc)::value;
-      if constexpr (t + R - 1 < KT) kring[(t + R - 1) % R] = load_k(t + R - 1);
-      extra(tc);
-      __builtin_amdgcn_sched_barrier(0);
-      constexpr int st = t / (K + 1), bo = t % (K + 1);
+    for (int o = 0; o <= K; ++o) kop[0][o] = load_k(o);
+    attn_static_for<0, NS>([&](auto sc_) __attribute__((always_inline)) {
+      constexpr int st = decltype(sc_)::value;
       constexpr int dc = st / 2, kh = st % 2;
+      if constexpr (st + 1 < NS) {
 #pragma unroll
-      for (int a = 0; a + bo <= K; ++a) s[kh][a + bo] = MM::mma(kring[t % R], qreg[a][dc], s[kh][a + bo]);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int o = 0; o <= K; ++o) kop[(st + 1) & 1][o] = load_k((st + 1) * (K + 1) + o);
+      }
+      attn_static_for<0, K + 1>([&](auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        extra(std::integral_constant<int, st * (K + 1) + k>{});
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b <= k; ++b) s[kh][k] = MM::mma(kop[st & 1][b], qreg[k - b][dc], s[kh][k]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     });
   };
 
