@@ -525,13 +525,16 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
   }
   if constexpr (kAhead) fetch_mask(lo);
 
-  // The P / dS stores of a block go out after its last DMA (both halves' in one 16-byte store per
-  // series and order; where the registers do not allow that, at degree 4 and d 128 with a mask, the
-  // second half's 8-byte stores: 2(K+1) either way), so the next block waits for its DMAs only. A
-  // wave with rows issues all of them (their branch skips only a wave without rows). Per-half stores
-  // also cost the second half a reload of the G rows: the compiler cannot move those loads above
-  // the first half's stores.
-  constexpr bool ONE_STORE = MASK == 0 || K < 4 || D < 128;
+  // The P / dS stores of a block go out after its last DMA, both halves' in one 16-byte store per
+  // series and order (2(K+1)), so the next block waits for its DMAs only. A wave with rows issues
+  // all of them (their branch skips only a wave without rows). Stored half by half (8 bytes), they
+  // also cost the second half a reload of the G rows (the compiler cannot move those loads above
+  // the first half's stores): a padding mask's dQ kernel took 5.48 ms that way at degree 4, d 128.
+  // Where holding the first half's P operands until the store would spill (there, with a mask, whose
+  // values take those registers), they wait in LDS instead, one 8-byte slot per lane and order
+  // (10 KB; the tiles leave 40 KB).
+  constexpr bool STAGE0 = STORE && MASK != 0 && K >= 4 && D >= 128;
+  __shared__ __attribute__((aligned(8))) uint2 pstage[STAGE0 ? kAttnWaves * kWave : 1][K + 1];
   constexpr int kStoresAfterDma = 2 * (K + 1);   // s_waitcnt vmcnt(2(K+1)) expcnt(0) lgkmcnt(0)
   static_assert(!STORE || kStoresAfterDma < 16, "vmcnt field");
   const bool wave_rows = q_block + wave * kAttnQPerWave < L;
@@ -541,7 +544,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     Tile& cur = Kt[j & 1];
     Tile& nxt = Kt[(j + 1) & 1];
     if constexpr (MASK != 0 && !kAhead) fetch_mask(kb0);   // this block's, at its top
-    if (STORE && (ONE_STORE || kAhead) && j > 0 && wave_rows) {
+    if (STORE && j > 0 && wave_rows) {
       // this wave's DMAs of block j have landed; the tile stores of block j-1 that followed its
       // last DMA, its last 2(K+1) vector memory operations (the counter drops in issue order), may
       // still be in flight
@@ -561,9 +564,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
     for (int i = 0; i < OPT; ++i) attn_half_dma_tile<T, K, D>(nxt, Kp, head, S, next_kb0, lane, wave, i);
 
     // ---- per 16-key half: S^T = K Q^T, dP^T = V G^T, then the P and dS series ----
-    // (the P operands of both halves are held for one store where the registers allow; otherwise
-    // each half's are stored as they are formed)
-    u32x4 dsb[K + 1], dsl[NLO], ppk[STORE && ONE_STORE ? K + 1 : 1];
+    // (the P operands of both halves are held for one store: in registers, or the first half's in
+    // LDS where the registers do not allow it)
+    u32x4 dsb[K + 1], dsl[NLO], ppk[STORE ? K + 1 : 1];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       floatx4 sc[K + 1], dp[K + 1];
@@ -620,24 +623,28 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_bwd_q_hal
       attn_half_pack<T, K, SPLIT, NLO>(w, kh, dsb, dsl);
       if constexpr (STORE) {
         static_assert(!SPLIT, "stored tiles hold one 16-bit value per pair");
-        if constexpr (ONE_STORE) {
+        if (STAGE0 && kh == 0) {
+#pragma unroll
+          for (int o = 0; o <= K; ++o)
+            pstage[threadIdx.x][o] = make_uint2(MM::pack2(wp[o][0], wp[o][1]), MM::pack2(wp[o][2], wp[o][3]));
+        } else {
 #pragma unroll
           for (int o = 0; o <= K; ++o) {
             ppk[o][2 * kh] = MM::pack2(wp[o][0], wp[o][1]);
             ppk[o][2 * kh + 1] = MM::pack2(wp[o][2], wp[o][3]);
           }
-        } else if (q_ok) {   // this half's four keys, positions 8 g + 4 (kh ^ q2) .. + 3: an 8-byte store
-          const int64_t at = ((head * (srow / 32) + kb0 / 32) * L + my_q) * 32 + 8 * g + 4 * (kh ^ ((my_q >> 2) & 1));
-#pragma unroll
-          for (int o = 0; o <= K; ++o) {
-            *reinterpret_cast<uint2*>(PT.p[o] + at) =
-                make_uint2(MM::pack2(wp[o][0], wp[o][1]), MM::pack2(wp[o][2], wp[o][3]));
-            *reinterpret_cast<uint2*>(DST.p[o] + at) = make_uint2(dsb[o][2 * kh], dsb[o][2 * kh + 1]);
-          }
         }
       }
     }
-    if constexpr (STORE && ONE_STORE) {
+    if constexpr (STAGE0) {   // the first half's P operands back from LDS (this lane's own slots)
+#pragma unroll
+      for (int o = 0; o <= K; ++o) {
+        const uint2 h0 = pstage[threadIdx.x][o];
+        ppk[o][0] = h0.x;
+        ppk[o][1] = h0.y;
+      }
+    }
+    if constexpr (STORE) {
       // the lane's eight keys (4 g + r and 16 + 4 g + r of the block) of its query, at positions
       // 8 g .. 8 g + 7 of the block's 32: one 16-byte store per series and order, a contiguous
       // kilobyte per wave (plain stores: non-temporal ones measured 8% slower)
