@@ -819,7 +819,6 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
 template <int K, int D>
 struct AttnHalfSw {
   static constexpr bool fits = AttnHalfPipe<K, D>::fits && !AttnHalfPipe<K, D>::split && D == 128 && K >= 3;
-  static constexpr int R = 6;   // the value products' operand ring: reads run five items ahead
 };
 
 template <typename T, int K, int D, int MASK>
@@ -902,11 +901,9 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   // ---- scores S^T_k = sum_{a+b=k} K_b Q_a^T of the block in buffer kt, two 16-key halves ----
   // Per step (chunk dc, half kh) the K+1 operands K_b are read one step ahead; the products are
   // grouped by output order, S_k's k+1 products back to back (0.843 against 0.863 ms at the
-  // config-3 shape with the reference's item order, operand by operand; the same grouping of the
-  // value products measured slower, 0.862 ms). Item t = (step, k) runs extra(t), the other work
-  // of the item (DMA shares and series units), before the order's products, which execute while it
+  // config-3 shape operand by operand). Item t = (step, k) runs extra(t), the other work of the
+  // item (DMA shares and series units), before the order's products, which execute while it
   // issues. Each accumulator sums its products in the same order either way (b ascending).
-  constexpr int R = AttnHalfSw<K, D>::R;
   constexpr int KT = 2 * DC * (K + 1);
   auto scores = [&](Tiles& kt, floatx4 (&s)[2][K + 1], auto&& extra) __attribute__((always_inline)) {
 #pragma unroll
@@ -946,6 +943,10 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
   };
 
   // ---- O^T_k += sum_{a+b=k} V_b^T P_a^T of the block in buffer vt ----
+  // Grouped by output order as the scores, per 16-wide output block db; the next block's K+1
+  // operands (two transpose reads each) are read one per order group, so the reads spread over
+  // the products: 1.3% faster than operand by operand through a ring (read all at the group's
+  // start, they were 2% slower).
   const int tj = c / 4, ta = c % 4;
   auto values = [&](Tiles& vt, const u32x4 (&pb)[K + 1]) __attribute__((always_inline)) {
     auto load_v = [&](int t) {
@@ -956,19 +957,22 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void taylor_attention_fwd_half_
       const int off1 = ((lch ^ P::fs(row1)) * 8) + 4 * (ta % 2);
       return lds_read_tr16x2(&vt[1][o][row0][off0], &vt[1][o][row1][off1]);
     };
-    constexpr int VT = DB * (K + 1);
-    u32x4 vring[R];
+    u32x4 vop[2][K + 1];
 #pragma unroll
-    for (int t = 0; t < R - 1 && t < VT; ++t) vring[t] = load_v(t);
+    for (int o = 0; o <= K; ++o) vop[0][o] = load_v(o);
+    attn_static_for<0, DB>([&](auto dc_) __attribute__((always_inline)) {
+      constexpr int db = decltype(dc_)::value;
+      attn_static_for<0, K + 1>([&](auto kc) __attribute__((always_inline)) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (db + 1 < DB) {   // one operand of the next block db + 1 per order group
+          vop[(db + 1) & 1][k] = load_v((db + 1) * (K + 1) + k);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < VT; ++t) {
-      if (t + R - 1 < VT) vring[(t + R - 1) % R] = load_v(t + R - 1);
-      __builtin_amdgcn_sched_barrier(0);
-      const int db = t / (K + 1), bo = t % (K + 1);
-#pragma unroll
-      for (int a = 0; a + bo <= K; ++a) acc_o[a + bo][db] = MM::mma(vring[t % R], pb[a], acc_o[a + bo][db]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+        for (int b = 0; b <= k; ++b) acc_o[k][db] = MM::mma(vop[db & 1][b], pb[k - b], acc_o[k][db]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
   };
 
   floatx4 scc[2][K + 1], scn[2][K + 1];   // scores of the block in its series, and of the next
